@@ -1,0 +1,329 @@
+#!/usr/bin/env python3
+"""Benchmark of the CKKS evaluation hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+
+Workload (one step): the hoisted rotation set {+-2^k : k = 0..14} (30
+rotations: one shared ModUp, then per rotation the key inner product,
+ModDown and the Galois permutation) applied to one ciphertext at N = 2^16,
+L = 24 limbs, K = 8 special primes, dnum = 3, plus one rescale.  Inputs
+are seeded synthetic ciphertext residues and seeded Galois keys, all
+resident in HBM before the timed region.  `value` is rotations/s.
+
+The same run also times the raw NTT / MAC batch (64 ciphertexts x 2 polys
+x 24 limbs at N = 2^16: forward NTT, plaintext MAC over the 64
+ciphertexts, inverse NTT) and reports NTT HBM GB/s.
+
+Per-kernel times come from HIP events recorded on the library's stream
+around every launch (fhe_profile_begin / fhe_profile_end) over a profiled
+repeat of the timed steps.  The CPU baseline times this build's C
+restatement of the same algorithms (the oracle; OpenFHE is not on this
+host) on a bounded sample, single-threaded for rotations and on all
+available cores for the NTT.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "fhe-mamba_amd"))
+
+METRIC = "rotations/s (N=2^16,L=24,hybrid KS); NTT HBM GB/s; s/token M2-130M"
+HBM_PEAK = 8.0e12  # B/s, MI355X HBM3E
+LOG_N, DEPTH, SCALE_BITS, FIRST_BITS, DNUM = 16, 23, 59, 60, 3
+N = 1 << LOG_N
+LIMB = N * 8  # bytes per limb
+STEPS = [s * (1 << k) for k in range(15) for s in (1, -1)]
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def rotation_bytes(L: int, K: int) -> tuple[int, int, int]:
+    """Algorithmic HBM bytes of one step: ciphertext read once, per hoisted
+    rotation the key ([dnum][2][L+K] limbs) read and the output written,
+    plus the rescale (read 2 x L limbs, write 2 x (L-1))."""
+    ct = 2 * L * LIMB
+    per_rot = DNUM * 2 * (L + K) * LIMB + ct
+    rescale = 2 * L * LIMB + 2 * (L - 1) * LIMB
+    return ct, per_rot, rescale
+
+
+def run_rotations(F, steps: int, warmup: int):
+    import numpy as np
+
+    q, p = F.gen_moduli(LOG_N, DEPTH, SCALE_BITS, FIRST_BITS, DNUM)
+    ctx = F.Context(LOG_N, q, p, DNUM)
+    L, K = ctx.L, ctx.K
+    log(f"rotation context: N=2^{LOG_N} L={L} K={K} dnum={ctx.dnum} alpha={ctx.alpha}")
+    s = ctx.keygen_secret(1)
+    gal = [F.galois_element(r, N) for r in STEPS]
+    keys = [ctx.keygen_galois(s, g, 1000 + i) for i, g in enumerate(gal)]
+    rng = np.random.default_rng(7)
+    ct_host = np.empty((2, L, N), dtype=np.uint64)
+    for j, qj in enumerate(q):
+        ct_host[:, j, :] = rng.integers(0, qj, (2, N), dtype=np.uint64)
+    ct = ctx.upload(ct_host)
+    outs = [ctx.poly(2, L) for _ in STEPS]
+    rs_out = ctx.poly(2, L - 1)
+
+    def step():
+        digits = ctx.rotation_precompute(ct)
+        ctx.rotate_hoisted(ct, digits, keys, gal, outs)
+        ctx.rescale(ct, out=rs_out)
+        digits.close()
+
+    for _ in range(warmup):
+        step()
+    ctx.sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    ctx.sync()
+    elapsed = time.perf_counter() - t0
+    ctx.profile_begin()
+    for _ in range(steps):
+        step()
+    prof = ctx.profile_end()
+    ct_b, rot_b, rs_b = rotation_bytes(L, K)
+    step_bytes = ct_b + len(STEPS) * rot_b + rs_b
+    res = {
+        "elapsed_s": elapsed,
+        "ms_per_step": 1e3 * elapsed / steps,
+        "rotations_per_s": len(STEPS) * steps / elapsed,
+        "step_bytes": step_bytes,
+        "profile": prof,
+        "L": L,
+        "K": K,
+    }
+    for k in keys:
+        k.close()
+    ctx.close()
+    return res
+
+
+def run_ntt_batch(F, steps: int, warmup: int, count: int = 64):
+    import numpy as np
+
+    q = [int(x) for x in ntt_primes(LOG_N, 60, 24)]
+    ctx = F.Context(LOG_N, q, [], 1)
+    L = len(q)
+    rng = np.random.default_rng(11)
+    x = ctx.poly(2 * count, L)
+    w = ctx.poly(count, L)
+    host = np.empty((2 * count, L, N), dtype=np.uint64)
+    for j, qj in enumerate(q):
+        host[:, j, :] = rng.integers(0, qj, (2 * count, N), dtype=np.uint64)
+    x = ctx.upload(host)
+    w = ctx.upload(host[:count].copy())
+    del host
+    acc = ctx.poly(2, L)
+
+    def step():
+        ctx.ntt_forward_dev(x.data_ptr(), 2 * count, L, 0)
+        ctx.mac_dev(x.data_ptr(), w.data_ptr(), count, L, acc.data_ptr())
+        ctx.ntt_inverse_dev(x.data_ptr(), 2 * count, L, 0)
+
+    for _ in range(warmup):
+        step()
+    ctx.sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    ctx.sync()
+    elapsed = time.perf_counter() - t0
+    ctx.profile_begin()
+    for _ in range(steps):
+        step()
+    prof = ctx.profile_end()
+    ntt_bytes = 2 * count * L * LIMB * 2  # read + write the batch once
+    mac_bytes = (2 * count * L + count * L + 2 * L) * LIMB
+    t_fwd = sum(prof.get(k, (0, 0.0))[1] for k in ("ntt_fwd_cols", "ntt_fwd_blocks")) / steps
+    t_inv = sum(prof.get(k, (0, 0.0))[1] for k in ("ntt_inv_cols", "ntt_inv_blocks")) / steps
+    t_mac = prof.get("k_mac", (0, 0.0))[1] / steps
+    ctx.close()
+    return {
+        "elapsed_s": elapsed,
+        "ms_per_step": 1e3 * elapsed / steps,
+        "ntt_gbps": 2 * ntt_bytes / ((t_fwd + t_inv) * 1e-3) / 1e9,
+        "ntt_fwd_ms": t_fwd,
+        "ntt_inv_ms": t_inv,
+        "mac_ms": t_mac,
+        "mac_gbps": mac_bytes / (t_mac * 1e-3) / 1e9 if t_mac else None,
+        "ntt_bytes": ntt_bytes,
+        "profile": prof,
+    }
+
+
+def ntt_primes(log_n: int, bits: int, count: int):
+    """Descending primes q = 1 mod 2N below 2^bits (deterministic)."""
+    from fhemamba_amd.core import gen_moduli  # noqa: F401  (library must load)
+
+    m = 2 << log_n
+    out, c = [], ((1 << bits) // m) * m + 1
+    while len(out) < count:
+        c -= m
+        if _is_prime(c):
+            out.append(c)
+    return out
+
+
+def _is_prime(n: int) -> bool:
+    if n < 2:
+        return False
+    for b in (2, 3, 5, 7, 11, 13, 17, 19, 23, 29, 31, 37):
+        if n % b == 0:
+            return n == b
+    d, s = n - 1, 0
+    while d % 2 == 0:
+        d //= 2
+        s += 1
+    for b in (2, 3, 5, 7, 11, 13, 17, 19, 23, 29, 31, 37):
+        x = pow(b, d, n)
+        if x in (1, n - 1):
+            continue
+        for _ in range(s - 1):
+            x = x * x % n
+            if x == n - 1:
+                break
+        else:
+            return False
+    return True
+
+
+def cpu_baseline(budget_s: float = 20.0):
+    """Oracle (C restatement) on the host: hoisted-set rotations at the
+    benchmark shape, one thread; NTT batch throughput on all cores."""
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    q, p = O.gen_moduli(LOG_N, DEPTH, SCALE_BITS, FIRST_BITS, DNUM)
+    c = O.Ctx(LOG_N, q, p, DNUM)
+    s = c.secret(1)
+    rng = np.random.default_rng(7)
+    ct = np.stack([np.stack([rng.integers(0, qj, N, dtype=np.uint64) for qj in q])
+                   for _ in range(2)])
+    keys = [(O.galois_elt(r, N), None) for r in (1, -1)]
+    keys = [(g, c.galois_key(s, g, 1000 + i)) for i, (g, _) in enumerate(keys)]
+    done, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < budget_s * 0.6 or done < 2:
+        g, k = keys[done % 2]
+        c.rotate(ct, k, g)
+        done += 1
+    rot_rate = done / (time.perf_counter() - t0)
+    cores = min(16, os.cpu_count() or 1)
+    qn = [int(x) for x in ntt_primes(LOG_N, 60, 24)]
+    cn = O.Ctx(LOG_N, qn, [], 1)
+    batch = np.stack([np.stack([rng.integers(0, qj, N, dtype=np.uint64) for qj in qn])
+                      for _ in range(8)])
+    reps, t1 = 0, time.perf_counter()
+    while time.perf_counter() - t1 < budget_s * 0.3 or reps < 1:
+        cn.ntt_fwd_batch(batch, 0, nthreads=cores)
+        reps += 1
+    ntt_rate = reps * batch.size * 8 * 2 / (time.perf_counter() - t1) / 1e9
+    return {
+        "value": rot_rate,
+        "unit": "rotations/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": (f"{done} single (non-hoisted) hybrid key-switched rotations of one "
+                   f"N=2^16, L=24, K=8, dnum=3 ciphertext (steps +1/-1) by the scalar C "
+                   f"oracle; OpenFHE CPU: unavailable on this host"),
+        "ntt_gbps": ntt_rate,
+        "ntt_cores": cores,
+        "ntt_sample": f"{reps} forward NTTs of 8 polys x 24 limbs at N=2^16 on {cores} threads",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--skip-ntt", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (got --gpus {args.gpus}): the path has no "
+              "multi-GPU component in this build; see DESIGN.md for how it would shard.",
+              file=sys.stderr)
+        return 2
+    import fhemamba_amd as F
+
+    log("rotation workload")
+    rot = run_rotations(F, args.steps, args.warmup)
+    ntt = None if args.skip_ntt else (log("ntt batch workload"),
+                                      run_ntt_batch(F, args.steps, args.warmup))[1]
+    prof = rot["profile"]
+    dom = max(prof, key=lambda k: prof[k][1])
+    launches, total_ms = prof[dom]
+    dom_bytes = kernel_bytes(dom, rot["L"], rot["K"])
+    avg_s = total_ms * 1e-3 / launches
+    achieved = dom_bytes / avg_s if dom_bytes else None
+    roofline = {
+        "bound": "hbm",
+        "kernel": dom,
+        "achieved": achieved / 1e9 if achieved else None,
+        "peak": HBM_PEAK / 1e9,
+        "unit": "GB/s",
+        "frac": achieved / HBM_PEAK if achieved else None,
+        "traffic": None,
+        "avg_launch_us": avg_s * 1e6,
+        "step_frac": rot["step_bytes"] / (rot["ms_per_step"] * 1e-3) / HBM_PEAK,
+    }
+    out = {
+        "metric": METRIC,
+        "value": rot["rotations_per_s"],
+        "unit": "rotations/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": rot["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u64",
+        "data": "synthetic (seeded residues, seeded Galois keys)",
+        "config": {
+            "workload": "hoisted rotation set {+-2^k, k<15} (30 rotations) + rescale on one "
+                        "ciphertext, N=2^16, L=24, K=8, dnum=3",
+            "ring_dim": N, "limbs": rot["L"], "special_primes": rot["K"], "dnum": DNUM,
+            "rotations_per_step": len(STEPS), "parallelism": "single GPU",
+        },
+        "roofline": roofline,
+        "kernels_ms_per_step": {k: v[1] / args.steps for k, v in sorted(prof.items())},
+    }
+    if ntt:
+        out["ntt"] = {k: ntt[k] for k in ("ntt_gbps", "ntt_fwd_ms", "ntt_inv_ms", "mac_ms",
+                                          "mac_gbps", "ms_per_step")}
+        out["ntt"]["workload"] = ("64 ciphertexts x 2 polys x 24 limbs, N=2^16: forward NTT, "
+                                  "MAC over 64 plaintexts, inverse NTT")
+        out["ntt"]["frac"] = ntt["ntt_gbps"] * 1e9 / HBM_PEAK
+    if not args.no_cpu_baseline:
+        log("cpu baseline (oracle)")
+        out["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(out))
+    return 0
+
+
+def kernel_bytes(name: str, L: int, K: int):
+    """Algorithmic bytes of one launch of the rotation step's kernels."""
+    ne = L + K
+    if name == "k_ksk_inner":
+        return (DNUM * ne + DNUM * 2 * ne + 2 * ne) * LIMB
+    if name == "k_moddown_combine":
+        return (2 * ne + 2 * L + L + 2 * L) * LIMB  # ext, y, c0 read; out written
+    if name == "k_convert":
+        return None
+    return None
+
+
+if __name__ == "__main__":
+    sys.exit(main())

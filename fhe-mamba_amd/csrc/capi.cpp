@@ -1,0 +1,672 @@
+// extern "C" boundary (include/fhecore.h): handle management, argument and
+// shape validation, and translation of C++ exceptions into status codes plus
+// a thread-local message.  No exception crosses this file's functions.
+#include <cstring>
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "../../include/fhecore.h"
+#include "ops.hpp"
+#include "params.hpp"
+#include "sampling.hpp"
+
+// Every handle shares ownership of its context, so handles may be released
+// in any order (a garbage collector may finalise a context before its polys).
+struct fhe_context {
+  std::shared_ptr<fhe::Context> own;
+  fhe::Context* c;
+};
+
+struct fhe_poly {
+  std::shared_ptr<fhe::Context> own;
+  fhe::Context* c;
+  uint32_t npoly, nlimb;
+  uint64_t* data;
+  size_t bytes;
+};
+
+struct fhe_key {
+  std::shared_ptr<fhe::Context> own;
+  fhe::Context* c;
+  uint64_t* data;  // [dnum][2][L+K][N], Montgomery form
+  size_t bytes;
+};
+
+namespace {
+
+thread_local std::string g_err;
+
+template <typename F>
+int guard(F&& f) {
+  try {
+    f();
+    return FHE_OK;
+  } catch (const fhe::ArgError& e) {
+    g_err = e.what();
+    return FHE_ERR_ARG;
+  } catch (const fhe::HipError& e) {
+    g_err = e.what();
+    return FHE_ERR_HIP;
+  } catch (const std::out_of_range& e) {
+    g_err = e.what();
+    return FHE_ERR_RANGE;
+  } catch (const std::exception& e) {
+    g_err = e.what();
+    return FHE_ERR_INTERNAL;
+  } catch (...) {
+    g_err = "unknown error";
+    return FHE_ERR_INTERNAL;
+  }
+}
+
+void need(bool ok, const char* msg) {
+  if (!ok) throw fhe::ArgError(msg);
+}
+
+size_t words(const fhe::Context& c, uint32_t npoly, uint32_t nlimb) {
+  return (size_t)npoly * nlimb * c.n;
+}
+
+// (Re)shape a poly handle; storage is reused when the size does not change.
+void reshape(fhe_poly* p, uint32_t npoly, uint32_t nlimb) {
+  const size_t bytes = words(*p->c, npoly, nlimb) * 8;
+  if (bytes != p->bytes) {
+    if (p->data) p->c->release(p->data, p->bytes);
+    p->data = bytes ? (uint64_t*)p->c->alloc(bytes) : nullptr;
+    p->bytes = bytes;
+  }
+  p->npoly = npoly;
+  p->nlimb = nlimb;
+}
+
+void same_ctx(const fhe_poly* a, const fhe_poly* b) {
+  need(a && b && a->c == b->c, "polys belong to different contexts");
+}
+
+// Resolve an output handle that may alias an input: the input's storage is
+// read by the launched kernels before (elementwise) or only through scratch.
+void prepare_out(fhe_poly* out, uint32_t npoly, uint32_t nlimb) {
+  if (out->npoly != npoly || out->nlimb != nlimb) reshape(out, npoly, nlimb);
+}
+
+fhe_key* new_key(const std::shared_ptr<fhe::Context>& own) {
+  fhe::Context& c = *own;
+  fhe_key* k = new fhe_key;
+  k->own = own;
+  k->c = &c;
+  k->bytes = (size_t)c.dnum * 2 * (c.L + c.K) * c.n * 8;
+  k->data = (uint64_t*)c.alloc(k->bytes);
+  return k;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* fhe_last_error(void) { return g_err.c_str(); }
+int fhe_abi_version(void) { return 1; }
+
+int fhe_gen_moduli(uint32_t log_n, uint32_t depth, uint32_t scale_bits, uint32_t first_bits,
+                   uint32_t dnum, uint64_t* q_out, uint64_t* p_out, uint32_t p_cap,
+                   uint32_t* num_p) {
+  return guard([&] {
+    need(q_out && p_out && num_p, "null output");
+    need(log_n >= 4 && log_n <= 17, "log_n must be in [4, 17]");
+    need(dnum >= 1 && depth + 1 <= 64, "bad depth or dnum");
+    need(scale_bits >= 20 && scale_bits <= 60 && first_bits >= 20 && first_bits <= 60,
+         "modulus sizes must be in [20, 60] bits");
+    std::vector<uint64_t> p;
+    const std::vector<uint64_t> q = fhe::gen_moduli(log_n, depth, scale_bits, first_bits, dnum, p);
+    need(p.size() <= p_cap, "p_out too small");
+    std::memcpy(q_out, q.data(), q.size() * 8);
+    std::memcpy(p_out, p.data(), p.size() * 8);
+    *num_p = (uint32_t)p.size();
+  });
+}
+
+int fhe_context_create(uint32_t log_n, const uint64_t* q, uint32_t num_q, const uint64_t* p,
+                       uint32_t num_p, uint32_t dnum, int device, fhe_context** out) {
+  return guard([&] {
+    need(q && out && (p || num_p == 0), "null argument");
+    *out = nullptr;
+    std::shared_ptr<fhe::Context> c =
+        std::make_shared<fhe::Context>(log_n, q, num_q, p, num_p, dnum, device);
+    *out = new fhe_context{c, c.get()};
+  });
+}
+
+int fhe_context_destroy(fhe_context* ctx) {
+  return guard([&] {
+    if (!ctx) return;
+    delete ctx;
+  });
+}
+
+int fhe_context_info(const fhe_context* ctx, uint32_t* info5) {
+  return guard([&] {
+    need(ctx && info5, "null argument");
+    const fhe::Context& c = *ctx->c;
+    info5[0] = c.log_n;
+    info5[1] = c.L;
+    info5[2] = c.K;
+    info5[3] = c.dnum;
+    info5[4] = c.alpha;
+  });
+}
+
+int fhe_context_moduli(const fhe_context* ctx, uint64_t* mods, uint64_t* psi) {
+  return guard([&] {
+    need(ctx, "null context");
+    const fhe::Context& c = *ctx->c;
+    if (mods) std::memcpy(mods, c.mods.data(), c.mods.size() * 8);
+    if (psi) std::memcpy(psi, c.psi.data(), c.psi.size() * 8);
+  });
+}
+
+int fhe_context_set_stream(fhe_context* ctx, void* hip_stream) {
+  return guard([&] {
+    need(ctx, "null context");
+    fhe::Context& c = *ctx->c;
+    fhe::hip_check(hipStreamSynchronize(c.stream), "stream switch");
+    hipStream_t s = reinterpret_cast<hipStream_t>(hip_stream);
+    if (!s) {
+      need(c.own_stream, "context has no own stream");
+      return;
+    }
+    if (c.own_stream) {
+      hipStreamDestroy(c.stream);
+      c.own_stream = false;
+    }
+    c.stream = s;
+  });
+}
+
+int fhe_sync(fhe_context* ctx) {
+  return guard([&] {
+    need(ctx, "null context");
+    fhe::hip_check(hipStreamSynchronize(ctx->c->stream), "fhe_sync");
+  });
+}
+
+int fhe_profile_begin(fhe_context* ctx) {
+  return guard([&] {
+    need(ctx, "null context");
+    ctx->c->prof.clear();
+    ctx->c->prof.on = true;
+  });
+}
+
+int fhe_profile_end(fhe_context* ctx, char* buf, size_t cap) {
+  return guard([&] {
+    need(ctx && buf && cap > 2, "null argument");
+    fhe::Context& c = *ctx->c;
+    fhe::hip_check(hipStreamSynchronize(c.stream), "profile sync");
+    std::map<std::string, std::pair<long, double>> agg;
+    for (auto& r : c.prof.recs) {
+      float ms = 0;
+      fhe::hip_check(hipEventElapsedTime(&ms, r.a, r.b), "hipEventElapsedTime");
+      auto& e = agg[r.name];
+      e.first += 1;
+      e.second += ms;
+    }
+    c.prof.clear();
+    c.prof.on = false;
+    std::string js = "{";
+    bool first = true;
+    for (auto& kv : agg) {
+      if (!first) js += ",";
+      first = false;
+      js += "\"" + kv.first + "\":[" + std::to_string(kv.second.first) + "," +
+            std::to_string(kv.second.second) + "]";
+    }
+    js += "}";
+    need(js.size() + 1 <= cap, "profile buffer too small");
+    std::memcpy(buf, js.c_str(), js.size() + 1);
+  });
+}
+
+int fhe_ntt_forward(fhe_context* ctx, uint64_t* data, uint32_t npoly, uint32_t nlimb,
+                    uint32_t limb0) {
+  return guard([&] {
+    need(ctx && data, "null argument");
+    fhe::Context& c = *ctx->c;
+    need(limb0 + nlimb <= c.L + c.K, "limb range exceeds the moduli");
+    fhe::ntt_forward(c, data, npoly, (size_t)nlimb * c.n, nlimb, fhe::LimbMap::contiguous(limb0));
+  });
+}
+
+int fhe_ntt_inverse(fhe_context* ctx, uint64_t* data, uint32_t npoly, uint32_t nlimb,
+                    uint32_t limb0) {
+  return guard([&] {
+    need(ctx && data, "null argument");
+    fhe::Context& c = *ctx->c;
+    need(limb0 + nlimb <= c.L + c.K, "limb range exceeds the moduli");
+    fhe::ntt_inverse(c, data, npoly, (size_t)nlimb * c.n, nlimb, fhe::LimbMap::contiguous(limb0));
+  });
+}
+
+int fhe_mac(fhe_context* ctx, const uint64_t* x, const uint64_t* w, uint32_t n, uint32_t nq,
+            uint64_t* acc) {
+  return guard([&] {
+    need(ctx && x && w && acc, "null argument");
+    need(nq >= 1 && nq <= ctx->c->L, "bad limb count");
+    fhe::poly_mac(*ctx->c, acc, x, w, n, nq);
+  });
+}
+
+int fhe_poly_create(fhe_context* ctx, uint32_t npoly, uint32_t nlimb, fhe_poly** out) {
+  return guard([&] {
+    need(ctx && out, "null argument");
+    need(nlimb <= ctx->c->L + ctx->c->K && npoly <= 65535, "bad poly shape");
+    fhe_poly* p = new fhe_poly{ctx->own, ctx->c, 0, 0, nullptr, 0};
+    try {
+      reshape(p, npoly, nlimb);
+    } catch (...) {
+      delete p;
+      throw;
+    }
+    *out = p;
+  });
+}
+
+int fhe_poly_destroy(fhe_poly* p) {
+  return guard([&] {
+    if (!p) return;
+    if (p->data) p->c->release(p->data, p->bytes);
+    delete p;
+  });
+}
+
+int fhe_poly_shape(const fhe_poly* p, uint32_t* npoly, uint32_t* nlimb) {
+  return guard([&] {
+    need(p && npoly && nlimb, "null argument");
+    *npoly = p->npoly;
+    *nlimb = p->nlimb;
+  });
+}
+
+int fhe_poly_data(const fhe_poly* p, uint64_t** dev) {
+  return guard([&] {
+    need(p && dev, "null argument");
+    *dev = p->data;
+  });
+}
+
+int fhe_poly_upload(fhe_poly* p, const uint64_t* host, uint32_t npoly, uint32_t nlimb) {
+  return guard([&] {
+    need(p && host, "null argument");
+    need(nlimb <= p->c->L + p->c->K, "bad limb count");
+    reshape(p, npoly, nlimb);
+    fhe::hip_check(hipMemcpyAsync(p->data, host, p->bytes, hipMemcpyHostToDevice, p->c->stream),
+                   "upload");
+    fhe::hip_check(hipStreamSynchronize(p->c->stream), "upload sync");
+  });
+}
+
+int fhe_poly_download(const fhe_poly* p, uint64_t* host) {
+  return guard([&] {
+    need(p && host, "null argument");
+    fhe::hip_check(hipMemcpyAsync(host, p->data, p->bytes, hipMemcpyDeviceToHost, p->c->stream),
+                   "download");
+    fhe::hip_check(hipStreamSynchronize(p->c->stream), "download sync");
+  });
+}
+
+int fhe_poly_copy(fhe_poly* dst, const fhe_poly* src) {
+  return guard([&] {
+    same_ctx(dst, src);
+    if (dst == src) return;
+    reshape(dst, src->npoly, src->nlimb);
+    fhe::hip_check(hipMemcpyAsync(dst->data, src->data, src->bytes, hipMemcpyDeviceToDevice,
+                                  src->c->stream),
+                   "copy");
+  });
+}
+
+int fhe_drop_limbs(fhe_poly* out, const fhe_poly* a, uint32_t nlimb) {
+  return guard([&] {
+    same_ctx(out, a);
+    need(nlimb >= 1 && nlimb <= a->nlimb, "can only drop limbs");
+    fhe::Context& c = *a->c;
+    if (out == a) {
+      if (nlimb == a->nlimb) return;
+      fhe::Scratch t(c, words(c, a->npoly, nlimb));
+      fhe::poly_copy_limbs(c, t.p, nlimb, a->data, a->nlimb, a->npoly, nlimb);
+      reshape(out, a->npoly, nlimb);
+      fhe::hip_check(hipMemcpyAsync(out->data, t.p, out->bytes, hipMemcpyDeviceToDevice, c.stream),
+                     "drop");
+      return;
+    }
+    prepare_out(out, a->npoly, nlimb);
+    fhe::poly_copy_limbs(c, out->data, nlimb, a->data, a->nlimb, a->npoly, nlimb);
+  });
+}
+
+static int binary(fhe_poly* out, const fhe_poly* a, const fhe_poly* b, fhe::BinOp op) {
+  return guard([&] {
+    same_ctx(a, b);
+    same_ctx(out, a);
+    need(a->npoly == b->npoly && a->nlimb == b->nlimb, "shape mismatch");
+    prepare_out(out, a->npoly, a->nlimb);
+    fhe::poly_binary(*a->c, op, out->data, a->data, b->data, a->npoly, a->nlimb);
+  });
+}
+
+int fhe_add(fhe_poly* out, const fhe_poly* a, const fhe_poly* b) {
+  return binary(out, a, b, fhe::OP_ADD);
+}
+int fhe_sub(fhe_poly* out, const fhe_poly* a, const fhe_poly* b) {
+  return binary(out, a, b, fhe::OP_SUB);
+}
+
+int fhe_negate(fhe_poly* out, const fhe_poly* a) {
+  return guard([&] {
+    same_ctx(out, a);
+    prepare_out(out, a->npoly, a->nlimb);
+    fhe::poly_negate(*a->c, out->data, a->data, a->npoly, a->nlimb);
+  });
+}
+
+int fhe_mul_plain(fhe_poly* out, const fhe_poly* ct, const fhe_poly* pt) {
+  return guard([&] {
+    same_ctx(ct, pt);
+    same_ctx(out, ct);
+    need(pt->npoly == 1 && pt->nlimb >= ct->nlimb, "plaintext must be one poly at >= limbs");
+    prepare_out(out, ct->npoly, ct->nlimb);
+    fhe::poly_mul_plain(*ct->c, out->data, ct->data, pt->data, ct->npoly, ct->nlimb);
+  });
+}
+
+int fhe_add_plain(fhe_poly* out, const fhe_poly* ct, const fhe_poly* pt) {
+  return guard([&] {
+    same_ctx(ct, pt);
+    same_ctx(out, ct);
+    need(pt->npoly == 1 && pt->nlimb >= ct->nlimb, "plaintext must be one poly at >= limbs");
+    prepare_out(out, ct->npoly, ct->nlimb);
+    fhe::poly_add_plain(*ct->c, out->data, ct->data, pt->data, ct->npoly, ct->nlimb);
+  });
+}
+
+int fhe_mul_const(fhe_poly* out, const fhe_poly* a, const uint64_t* cst) {
+  return guard([&] {
+    same_ctx(out, a);
+    need(cst != nullptr, "null constants");
+    prepare_out(out, a->npoly, a->nlimb);
+    fhe::poly_mul_const(*a->c, out->data, a->data, cst, a->npoly, a->nlimb);
+  });
+}
+
+int fhe_add_const(fhe_poly* out, const fhe_poly* a, const uint64_t* cst) {
+  return guard([&] {
+    same_ctx(out, a);
+    need(cst != nullptr, "null constants");
+    prepare_out(out, a->npoly, a->nlimb);
+    fhe::poly_add_const(*a->c, out->data, a->data, cst, a->npoly, a->nlimb);
+  });
+}
+
+int fhe_mul_int(fhe_poly* out, const fhe_poly* a, int64_t v) {
+  return guard([&] {
+    same_ctx(out, a);
+    std::vector<uint64_t> cst(a->nlimb);
+    for (uint32_t j = 0; j < a->nlimb; ++j) {
+      const uint64_t q = a->c->mods[j];
+      const uint64_t r = (uint64_t)(v < 0 ? -(v + 1) : v) % q;
+      cst[j] = v < 0 ? (q - 1 - r) : r;  // -(|v|) mod q without overflow
+    }
+    prepare_out(out, a->npoly, a->nlimb);
+    fhe::poly_mul_const(*a->c, out->data, a->data, cst.data(), a->npoly, a->nlimb);
+  });
+}
+
+int fhe_rescale(fhe_poly* out, const fhe_poly* a) {
+  return guard([&] {
+    same_ctx(out, a);
+    need(a->nlimb >= 2 && a->nlimb <= a->c->L, "rescale needs 2..L limbs");
+    fhe::Context& c = *a->c;
+    const uint32_t npoly = a->npoly, nq = a->nlimb;
+    if (out == a) {
+      fhe::Scratch t(c, words(c, npoly, nq - 1));
+      fhe::poly_rescale(c, t.p, a->data, npoly, nq);
+      reshape(out, npoly, nq - 1);
+      fhe::hip_check(hipMemcpyAsync(out->data, t.p, out->bytes, hipMemcpyDeviceToDevice, c.stream),
+                     "rescale");
+      return;
+    }
+    prepare_out(out, npoly, nq - 1);
+    fhe::poly_rescale(c, out->data, a->data, npoly, nq);
+  });
+}
+
+int fhe_tensor(fhe_poly* out3, const fhe_poly* a, const fhe_poly* b) {
+  return guard([&] {
+    same_ctx(a, b);
+    same_ctx(out3, a);
+    need(a->npoly == 2 && b->npoly == 2 && a->nlimb == b->nlimb, "tensor needs 2-poly cts");
+    need(out3 != a && out3 != b, "tensor output must not alias an input");
+    prepare_out(out3, 3, a->nlimb);
+    fhe::poly_tensor(*a->c, out3->data, a->data, b->data, a->nlimb);
+  });
+}
+
+int fhe_key_load(fhe_context* ctx, const uint64_t* host, fhe_key** out) {
+  return guard([&] {
+    need(ctx && host && out, "null argument");
+    fhe::Context& c = *ctx->c;
+    fhe_key* k = new_key(ctx->own);
+    fhe::hip_check(hipMemcpyAsync(k->data, host, k->bytes, hipMemcpyHostToDevice, c.stream),
+                   "key upload");
+    fhe::key_to_montgomery(c, k->data);
+    fhe::hip_check(hipStreamSynchronize(c.stream), "key sync");
+    *out = k;
+  });
+}
+
+int fhe_key_destroy(fhe_key* k) {
+  return guard([&] {
+    if (!k) return;
+    k->c->release(k->data, k->bytes);
+    delete k;
+  });
+}
+
+static void check_key(const fhe_poly* p, const fhe_key* k) {
+  need(p && k && p->c == k->c, "key belongs to another context");
+}
+
+int fhe_keyswitch(fhe_poly* out, const fhe_poly* a, const fhe_key* key) {
+  return guard([&] {
+    same_ctx(out, a);
+    check_key(a, key);
+    need(a->npoly == 1 && a->nlimb >= 1 && a->nlimb <= a->c->L, "keyswitch input is one poly");
+    fhe::Context& c = *a->c;
+    const uint32_t nq = a->nlimb, ne = nq + c.K, nd = fhe::num_digits(c, nq);
+    fhe::Scratch dig(c, (size_t)nd * ne * c.n), ext(c, 2 * (size_t)ne * c.n);
+    fhe::modup(c, a->data, nq, dig.p);
+    fhe::ksk_inner(c, dig.p, nq, key->data, ext.p);
+    if (out == a) {
+      fhe::Scratch t(c, words(c, 2, nq));
+      fhe::moddown_pair2(c, ext.p, nq, t.p, nullptr, nullptr, 1);
+      reshape(out, 2, nq);
+      fhe::hip_check(hipMemcpyAsync(out->data, t.p, out->bytes, hipMemcpyDeviceToDevice, c.stream),
+                     "keyswitch");
+      return;
+    }
+    prepare_out(out, 2, nq);
+    fhe::moddown_pair2(c, ext.p, nq, out->data, nullptr, nullptr, 1);
+  });
+}
+
+int fhe_relinearize(fhe_poly* out, const fhe_poly* ct3, const fhe_key* key) {
+  return guard([&] {
+    same_ctx(out, ct3);
+    check_key(ct3, key);
+    need(ct3->npoly == 3 && ct3->nlimb <= ct3->c->L, "relinearize needs a 3-poly tensor");
+    fhe::Context& c = *ct3->c;
+    const uint32_t nq = ct3->nlimb, ne = nq + c.K, nd = fhe::num_digits(c, nq);
+    const size_t pl = (size_t)nq * c.n;
+    fhe::Scratch dig(c, (size_t)nd * ne * c.n), ext(c, 2 * (size_t)ne * c.n), t(c, 2 * pl);
+    fhe::modup(c, ct3->data + 2 * pl, nq, dig.p);
+    fhe::ksk_inner(c, dig.p, nq, key->data, ext.p);
+    fhe::moddown_pair2(c, ext.p, nq, t.p, ct3->data, ct3->data + pl, 1);
+    reshape(out, 2, nq);
+    fhe::hip_check(hipMemcpyAsync(out->data, t.p, out->bytes, hipMemcpyDeviceToDevice, c.stream),
+                   "relinearize");
+  });
+}
+
+int fhe_rotate(fhe_poly* out, const fhe_poly* ct, const fhe_key* key, uint32_t galois) {
+  return guard([&] {
+    same_ctx(out, ct);
+    check_key(ct, key);
+    need(ct->npoly == 2 && ct->nlimb <= ct->c->L, "rotate needs a 2-poly ciphertext");
+    need((galois & 1) && galois < 2 * ct->c->n, "Galois element must be odd and < 2N");
+    fhe::Context& c = *ct->c;
+    const uint32_t nq = ct->nlimb, ne = nq + c.K, nd = fhe::num_digits(c, nq);
+    const size_t pl = (size_t)nq * c.n;
+    fhe::Scratch dig(c, (size_t)nd * ne * c.n), ext(c, 2 * (size_t)ne * c.n), t(c, 2 * pl);
+    fhe::modup(c, ct->data + pl, nq, dig.p);
+    fhe::ksk_inner(c, dig.p, nq, key->data, ext.p);
+    fhe::moddown_pair2(c, ext.p, nq, t.p, ct->data, nullptr, galois);
+    reshape(out, 2, nq);
+    fhe::hip_check(hipMemcpyAsync(out->data, t.p, out->bytes, hipMemcpyDeviceToDevice, c.stream),
+                   "rotate");
+  });
+}
+
+int fhe_rotation_precompute(const fhe_poly* ct, fhe_poly** digits) {
+  return guard([&] {
+    need(ct && digits, "null argument");
+    need(ct->npoly == 2 && ct->nlimb <= ct->c->L, "precompute needs a 2-poly ciphertext");
+    fhe::Context& c = *ct->c;
+    const uint32_t nq = ct->nlimb, nd = fhe::num_digits(c, nq);
+    fhe_poly* d = new fhe_poly{ct->own, &c, 0, 0, nullptr, 0};
+    try {
+      reshape(d, nd, nq + c.K);
+      fhe::modup(c, ct->data + (size_t)nq * c.n, nq, d->data);
+    } catch (...) {
+      fhe_poly_destroy(d);
+      throw;
+    }
+    *digits = d;
+  });
+}
+
+int fhe_rotate_hoisted(const fhe_poly* ct, const fhe_poly* digits, const fhe_key* const* keys,
+                       const uint32_t* galois, uint32_t count, fhe_poly* const* outs) {
+  return guard([&] {
+    need(ct && digits && keys && galois && outs, "null argument");
+    same_ctx(ct, digits);
+    fhe::Context& c = *ct->c;
+    const uint32_t nq = ct->nlimb, ne = nq + c.K;
+    need(ct->npoly == 2 && digits->npoly == fhe::num_digits(c, nq) && digits->nlimb == ne,
+         "digits do not belong to this ciphertext level");
+    for (uint32_t r = 0; r < count; ++r) {
+      check_key(ct, keys[r]);
+      need(outs[r] && outs[r]->c == &c && outs[r] != ct, "bad output handle");
+      need((galois[r] & 1) && galois[r] < 2 * c.n, "Galois element must be odd and < 2N");
+    }
+    fhe::Scratch ext(c, 2 * (size_t)ne * c.n);
+    for (uint32_t r = 0; r < count; ++r) {
+      fhe::ksk_inner(c, digits->data, nq, keys[r]->data, ext.p);
+      prepare_out(outs[r], 2, nq);
+      fhe::moddown_pair2(c, ext.p, nq, outs[r]->data, ct->data, nullptr, galois[r]);
+    }
+  });
+}
+
+int fhe_encode(fhe_context* ctx, const double* re, const double* im, uint32_t count,
+               uint32_t slots, double scale, uint32_t nlimb, fhe_poly* out) {
+  return guard([&] {
+    need(ctx && out && out->c == ctx->c && (re || count == 0), "null argument");
+    fhe::Context& c = *ctx->c;
+    prepare_out(out, 1, nlimb);
+    if (!fhe::encode(c, re, im, count, slots, scale, nlimb, out->data))
+      throw std::out_of_range("encode: a scaled coefficient does not fit in 62 bits");
+  });
+}
+
+int fhe_decode(fhe_context* ctx, const fhe_poly* pt, uint32_t slots, double scale, double* re,
+               double* im) {
+  return guard([&] {
+    need(ctx && pt && re && pt->c == ctx->c, "null argument");
+    need(pt->npoly == 1, "decode takes a one-poly plaintext");
+    fhe::decode(*ctx->c, pt->data, pt->nlimb, slots, scale, re, im);
+  });
+}
+
+int fhe_keygen_secret(fhe_context* ctx, uint64_t seed, int64_t* s_coef) {
+  return guard([&] {
+    need(ctx && s_coef, "null argument");
+    fhe::sample_ternary_host(fhe::stream_key(seed, fhe::TAG_SECRET, 0), s_coef, ctx->c->n);
+  });
+}
+
+int fhe_keygen_public(fhe_context* ctx, const int64_t* s_coef, uint64_t seed, fhe_poly* pk) {
+  return guard([&] {
+    need(ctx && s_coef && pk && pk->c == ctx->c, "null argument");
+    prepare_out(pk, 2, ctx->c->L);
+    fhe::keygen_public(*ctx->c, s_coef, seed, pk->data);
+  });
+}
+
+int fhe_keygen_relin(fhe_context* ctx, const int64_t* s_coef, uint64_t seed, fhe_key** out) {
+  return guard([&] {
+    need(ctx && s_coef && out, "null argument");
+    fhe::Context& c = *ctx->c;
+    fhe_key* k = new_key(ctx->own);
+    try {
+      fhe::keygen_relin(c, s_coef, seed, k->data);
+      fhe::key_to_montgomery(c, k->data);
+      fhe::hip_check(hipStreamSynchronize(c.stream), "keygen");
+    } catch (...) {
+      fhe_key_destroy(k);
+      throw;
+    }
+    *out = k;
+  });
+}
+
+int fhe_keygen_galois(fhe_context* ctx, const int64_t* s_coef, uint32_t galois, uint64_t seed,
+                      fhe_key** out) {
+  return guard([&] {
+    need(ctx && s_coef && out, "null argument");
+    fhe::Context& c = *ctx->c;
+    need((galois & 1) && galois < 2 * c.n, "Galois element must be odd and < 2N");
+    fhe_key* k = new_key(ctx->own);
+    try {
+      fhe::keygen_galois(c, s_coef, galois, seed, k->data);
+      fhe::key_to_montgomery(c, k->data);
+      fhe::hip_check(hipStreamSynchronize(c.stream), "keygen");
+    } catch (...) {
+      fhe_key_destroy(k);
+      throw;
+    }
+    *out = k;
+  });
+}
+
+int fhe_encrypt(fhe_poly* ct, const fhe_poly* pk, const fhe_poly* pt, uint64_t seed) {
+  return guard([&] {
+    same_ctx(pk, pt);
+    same_ctx(ct, pk);
+    need(pk->npoly == 2 && pt->npoly == 1 && pt->nlimb <= pk->nlimb, "bad key or plaintext");
+    need(ct != pt && ct != pk, "ciphertext must not alias an input");
+    prepare_out(ct, 2, pt->nlimb);
+    fhe::encrypt_pk(*pt->c, pk->data, pt->data, pt->nlimb, seed, ct->data);
+  });
+}
+
+int fhe_decrypt(fhe_poly* pt, const fhe_poly* ct, const int64_t* s_coef) {
+  return guard([&] {
+    same_ctx(pt, ct);
+    need(s_coef != nullptr && ct->npoly >= 2 && ct->npoly <= 3, "bad ciphertext");
+    need(pt != ct, "plaintext must not alias the ciphertext");
+    prepare_out(pt, 1, ct->nlimb);
+    fhe::decrypt(*ct->c, ct->data, ct->npoly, ct->nlimb, s_coef, pt->data);
+  });
+}
+
+}  // extern "C"

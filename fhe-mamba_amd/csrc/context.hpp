@@ -1,0 +1,207 @@
+// Device-resident CKKS-RNS context: moduli, transform tables and the basis
+// conversion constants used by key switching and rescaling.
+//
+// Layout conventions (all device arrays are uint64 words):
+//   modulus index m in [0, L+K): q_0..q_{L-1} then p_0..p_{K-1}.
+//   RNS polynomial sets are limb-major: [poly][limb][N].
+//   Transform tables per modulus: tw_fwd[m][k] = (psi^brv(k), Shoup),
+//   tw_inv[m][k] = (psi^-brv(k), Shoup), one 16-byte pair per entry.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <map>
+#include <memory>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "modarith.hpp"
+
+namespace fhe {
+
+struct HipError : std::runtime_error {
+  using std::runtime_error::runtime_error;
+};
+struct ArgError : std::invalid_argument {
+  using std::invalid_argument::invalid_argument;
+};
+
+inline void hip_check(hipError_t e, const char* what) {
+  if (e != hipSuccess) throw HipError(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+// Per-modulus scalar constants, 64-byte aligned record.
+struct ModConst {
+  uint64_t q;
+  uint64_t qinv_neg;   // -q^-1 mod 2^64
+  uint64_t mu64;       // floor(2^64 / q)
+  uint64_t r64;        // 2^64 mod q
+  uint64_t r64_sh;     // Shoup companion of r64
+  uint64_t ninv;       // N^-1 mod q
+  uint64_t ninv_sh;
+  uint64_t r2;         // 2^128 mod q (to Montgomery form via redc)
+};
+
+// x mod q for a 128-bit x = hi * 2^64 + lo (any hi): hi * (2^64 mod q) by
+// Shoup and lo by a one-word Barrett step, both in [0, 2q), then reduce.
+FHE_HD uint64_t reduce128(uint64_t hi, uint64_t lo, const ModConst& m) {
+  const uint64_t a = shoup_lazy(hi, m.r64, m.r64_sh, m.q);
+  const uint64_t b = lo - mulhi64(lo, m.mu64) * m.q;
+  return reduce_4q(a + b, m.q);
+}
+
+FHE_HD uint64_t mul_mod(uint64_t a, uint64_t b, const ModConst& m) {
+  const u128 p = (u128)a * b;
+  return reduce128((uint64_t)(p >> 64), (uint64_t)p, m);
+}
+
+// Basis-conversion plan from a source basis to a target basis:
+//   v_i = x_i * qhat_inv_i (Shoup), y_k = sum_i v_i * qhat_ik mod t_k,
+// with qhat_ik stored in Montgomery form w.r.t. t_k so that one REDC of the
+// 128-bit accumulator gives the standard-domain result.
+struct ConvPlan {
+  uint32_t nsrc = 0, ndst = 0;
+  std::vector<uint32_t> src_idx, dst_idx;  // modulus indices
+  uint64_t* d_qhat_inv = nullptr;          // [nsrc][2]  (value, Shoup)
+  uint64_t* d_qhat_mont = nullptr;         // [nsrc][ndst]
+  uint32_t* d_dst_idx = nullptr;           // [ndst]
+  uint32_t* d_src_idx32 = nullptr;         // [nsrc]
+};
+
+// Optional per-launch timing with HIP events on the context stream
+// (enabled by fhe_profile_begin).  Records (kernel name, start, stop).
+struct Profiler {
+  bool on = false;
+  struct Rec {
+    const char* name;
+    hipEvent_t a, b;
+  };
+  std::vector<Rec> recs;
+  std::vector<hipEvent_t> spare;
+  hipEvent_t get();
+  void clear();
+  ~Profiler();
+};
+
+class Pool {
+ public:
+  explicit Pool(int device) : device_(device) {}
+  ~Pool();
+  void* get(size_t bytes);
+  void put(void* p, size_t bytes);
+  void trim();
+
+ private:
+  int device_;
+  std::mutex mu_;
+  std::multimap<size_t, void*> free_;
+};
+
+struct Context {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  bool own_stream = false;
+  uint32_t log_n = 0, n = 0, L = 0, K = 0, dnum = 0, alpha = 0;
+  std::vector<uint64_t> mods;        // L + K
+  std::vector<uint64_t> psi;         // minimal primitive 2N-th roots
+  std::vector<ModConst> hconst;
+
+  // device tables
+  ModConst* d_const = nullptr;       // [L+K]
+  uint64_t* d_tw_fwd = nullptr;      // [L+K][N][2]
+  uint64_t* d_tw_inv = nullptr;      // [L+K][N][2]
+  // rescale: rs[l][i] = (q_l mod q_i, (q_l)^-1 mod q_i, Shoup) for i < l
+  uint64_t* d_rescale = nullptr;     // [L][L][4]
+  // ModDown: P^-1 mod q_i (value, Shoup)
+  uint64_t* d_pinv_q = nullptr;      // [L][2]
+
+  // Garner CRT inverses g[i][j] = (q_j^-1 mod q_i, Shoup) for j < i (decode).
+  uint64_t* d_garner = nullptr;      // [L][L][2]
+  // Special-FFT twiddles per slot count: (inverse, forward), each [slots-1] x (cos, sin).
+  std::mutex fft_mu;
+  std::map<uint32_t, std::pair<double*, double*>> fft_tables;
+
+  std::unique_ptr<Pool> pool;
+  Profiler prof;
+  std::mutex plan_mu;
+  std::map<std::pair<uint64_t, uint64_t>, std::unique_ptr<ConvPlan>> plans;
+
+  Context(uint32_t log_n, const uint64_t* q, uint32_t num_q, const uint64_t* p,
+          uint32_t num_p, uint32_t dnum, int device);
+  ~Context();
+
+  // Conversion plan for source modulus set [s, e) of Q (or all of P when
+  // s == UINT32_MAX) into target = (Q[0..nq) minus the source) + P, or for
+  // ModDown P -> Q[0..nq).
+  const ConvPlan& modup_plan(uint32_t s, uint32_t e, uint32_t nq);
+  const ConvPlan& moddown_plan(uint32_t nq);
+
+  void* alloc(size_t bytes) { return pool->get(bytes); }
+  void release(void* p, size_t bytes) { pool->put(p, bytes); }
+
+ private:
+  ConvPlan* build_plan(const std::vector<uint32_t>& src, const std::vector<uint32_t>& dst);
+};
+
+// Limb -> modulus index map for a batch of limbs: limb j < split uses
+// modulus base0 + j, limb j >= split uses base1 + (j - split).
+struct LimbMap {
+  uint32_t split, base0, base1;
+  FHE_HD uint32_t operator()(uint32_t j) const {
+    return j < split ? base0 + j : base1 + (j - split);
+  }
+  static LimbMap contiguous(uint32_t limb0) { return LimbMap{0xffffffffu, limb0, 0}; }
+};
+
+// Stream-ordered scratch buffer from the context pool.  Released back to the
+// pool on destruction; later work on the same stream may reuse it, which is
+// safe because all of a context's kernels run in stream order.
+struct Scratch {
+  Context& c;
+  uint64_t* p;
+  size_t bytes;
+  Scratch(Context& ctx, size_t words)
+      : c(ctx), p((uint64_t*)ctx.alloc(words * 8)), bytes(words * 8) {}
+  ~Scratch() { c.release(p, bytes); }
+  Scratch(const Scratch&) = delete;
+  Scratch& operator=(const Scratch&) = delete;
+};
+
+// Scope that brackets one kernel launch with profiling events.
+struct LaunchScope {
+  Context& c;
+  const char* name;
+  hipEvent_t b = nullptr;
+  LaunchScope(Context& ctx, const char* nm) : c(ctx), name(nm) {
+    if (c.prof.on) {
+      hipEvent_t a = c.prof.get();
+      b = c.prof.get();
+      hipEventRecord(a, c.stream);
+      c.prof.recs.push_back({name, a, b});
+    }
+  }
+  ~LaunchScope() {
+    if (b) hipEventRecord(b, c.stream);
+  }
+};
+
+// Launch `kernel` on the context stream under a profiling scope and check
+// the launch status.
+#define FHE_LAUNCH(ctx, name, kernel, grid, block, shmem, ...)                      \
+  do {                                                                              \
+    ::fhe::LaunchScope fhe_scope_((ctx), (name));                                   \
+    hipLaunchKernelGGL(kernel, grid, block, shmem, (ctx).stream, __VA_ARGS__);      \
+    ::fhe::hip_check(hipGetLastError(), name);                                      \
+  } while (0)
+
+// ---- kernel launchers (implemented in the .hip files) ----
+void ntt_forward(Context& c, uint64_t* data, uint32_t npoly, size_t poly_stride,
+                 uint32_t nlimb, LimbMap map);
+void ntt_inverse(Context& c, uint64_t* data, uint32_t npoly, size_t poly_stride,
+                 uint32_t nlimb, LimbMap map);
+
+}  // namespace fhe

@@ -1,0 +1,232 @@
+// CKKS encode / decode on the GPU.
+//
+// Encode = OpenFHE CKKSPackedEncoding::Encode as restated by the
+// reference's GPU encoder (native/fideslib_stage0/src/gpu_special_fft.cu):
+//   special inverse FFT over `slots` values (butterfly order and twiddle
+//   table of gpu_special_fft.cu:12-22, :99-108 and
+//   patches/openfhe-v1.4.2-inverse-fft-plan.patch:18-60), bit reversal,
+//   division by slots, multiplication by the scale, llround (ties away from
+//   zero), placement of the 2*slots real/imaginary coefficients at stride
+//   N / (2 slots), signed RNS lift into each limb
+//   (fideslib_plaintext_rns.cu:11-23), forward NTT.
+// Decode = inverse NTT, centred CRT (balanced mixed-radix / Garner, so no
+// big integers), division by the scale, forward special FFT.
+//
+// All floating-point operations are plain IEEE double add/sub/mul/div; the
+// library is compiled with -ffp-contract=off so none fuse into FMAs, which
+// keeps the encoder's rounding identical to the CPU definition.
+#include <cmath>
+#include <cstring>
+
+#include "ops.hpp"
+
+namespace fhe {
+namespace {
+
+constexpr int TPB = 256;
+
+inline uint32_t ilog2(uint32_t x) {
+  uint32_t l = 0;
+  while ((1u << l) < x) ++l;
+  return l;
+}
+
+// Twiddle (cos, sin) pairs come from one glibc sincos() call per angle: that
+// is what gcc-built OpenFHE evaluates for its (cos(angle), sin(angle))
+// table (gcc fuses the pair), and sincos() differs from separate cos()/sin()
+// in the last bit for a few angles.
+inline void host_sincos(double a, double* s, double* c) { ::sincos(a, s, c); }
+
+std::pair<double*, double*> fft_tables(Context& c, uint32_t slots) {
+  std::lock_guard<std::mutex> g(c.fft_mu);
+  auto it = c.fft_tables.find(slots);
+  if (it != c.fft_tables.end()) return it->second;
+  const uint32_t m = 4 * slots;
+  std::vector<uint32_t> rot(slots);
+  uint32_t p = 1;
+  for (uint32_t j = 0; j < slots; ++j) {
+    rot[j] = p;
+    p = (uint32_t)(((uint64_t)p * 5) % m);
+  }
+  const size_t cnt = slots > 1 ? slots - 1 : 1;
+  std::vector<double> inv(2 * cnt, 0.0), fwd(2 * cnt, 0.0);
+  for (uint32_t len = 2; len <= slots; len <<= 1) {
+    const uint32_t h = len / 2, lenq = 4 * len, gap = m / lenq;
+    for (uint32_t j = 0; j < h; ++j) {
+      const double ai = 2.0 * M_PI * ((lenq - rot[j] % lenq) * gap) / m;
+      const double af = 2.0 * M_PI * ((rot[j] % lenq) * gap) / m;
+      host_sincos(ai, &inv[2 * (h - 1 + j) + 1], &inv[2 * (h - 1 + j)]);
+      host_sincos(af, &fwd[2 * (h - 1 + j) + 1], &fwd[2 * (h - 1 + j)]);
+    }
+  }
+  double *di = nullptr, *df = nullptr;
+  hip_check(hipMalloc(&di, inv.size() * 8), "hipMalloc fft");
+  hip_check(hipMalloc(&df, fwd.size() * 8), "hipMalloc fft");
+  hip_check(hipMemcpy(di, inv.data(), inv.size() * 8, hipMemcpyHostToDevice), "fft table");
+  hip_check(hipMemcpy(df, fwd.data(), fwd.size() * 8, hipMemcpyHostToDevice), "fft table");
+  c.fft_tables[slots] = {di, df};
+  return {di, df};
+}
+
+// One stage of the special inverse FFT: (a, b) -> (a + b, (a - b) * w).
+__global__ void k_fft_inv_stage(double2* v, const double* tw, uint32_t slots, uint32_t len) {
+  const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= slots / 2) return;
+  const uint32_t h = len / 2, j = t % h, i = (t / h) * len + j;
+  const double2 a = v[i], b = v[i + h];
+  const double wr = tw[2 * (h - 1 + j)], wi = tw[2 * (h - 1 + j) + 1];
+  const double vr = a.x - b.x, vi = a.y - b.y;
+  v[i] = make_double2(a.x + b.x, a.y + b.y);
+  v[i + h] = make_double2(vr * wr - vi * wi, vi * wr + vr * wi);
+}
+
+// One stage of the forward special FFT: (u, b) -> (u + b w, u - b w).
+__global__ void k_fft_fwd_stage(double2* v, const double* tw, uint32_t slots, uint32_t len) {
+  const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= slots / 2) return;
+  const uint32_t h = len / 2, j = t % h, i = (t / h) * len + j;
+  const double2 u = v[i], b = v[i + h];
+  const double wr = tw[2 * (h - 1 + j)], wi = tw[2 * (h - 1 + j) + 1];
+  const double vr = b.x * wr - b.y * wi, vi = b.y * wr + b.x * wi;
+  v[i] = make_double2(u.x + vr, u.y + vi);
+  v[i + h] = make_double2(u.x - vr, u.y - vi);
+}
+
+__device__ __forceinline__ uint32_t brev_bits(uint32_t x, uint32_t bits) {
+  return bits ? __brev(x) >> (32 - bits) : 0;
+}
+
+__device__ __forceinline__ uint64_t lift_signed(int64_t x, uint64_t q) {
+  if (x >= 0) return (uint64_t)x % q;
+  const uint64_t r = ((uint64_t)(-x)) % q;
+  return r ? q - r : 0;
+}
+
+// Round slot i of the transformed vector (read through the bit reversal)
+// and scatter its real / imaginary coefficient into every limb.
+__global__ void k_round_lift(const double2* v, uint64_t* out, const ModConst* mc, uint32_t slots,
+                             uint32_t bits, uint32_t gap, uint32_t n, uint32_t nlimb, double scale,
+                             int* status) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= slots) return;
+  const double2 x = v[brev_bits(i, bits)];
+  const double a = (x.x / (double)slots) * scale, b = (x.y / (double)slots) * scale;
+  const double lim = 4611686018427387904.0;  // 2^62
+  if (!isfinite(a) || !isfinite(b) || fabs(a) >= lim || fabs(b) >= lim) {
+    atomicOr(status, 1);
+    return;
+  }
+  const int64_t ra = llround(a), rb = llround(b);
+  for (uint32_t j = 0; j < nlimb; ++j) {
+    const uint64_t q = mc[j].q;
+    out[(size_t)j * n + (size_t)i * gap] = lift_signed(ra, q);
+    out[(size_t)j * n + (size_t)(i + slots) * gap] = lift_signed(rb, q);
+  }
+}
+
+// Balanced Garner reconstruction of coefficient positions i*gap, i < 2 slots,
+// then division by the scale; writes complex slot inputs of the forward FFT
+// at bit-reversed positions.
+template <int MAXL>
+__global__ void k_crt_decode(const uint64_t* coef, double2* v, const ModConst* mc,
+                             const uint64_t* garner, const uint64_t* mods, uint32_t n,
+                             uint32_t nlimb, uint32_t L, uint32_t slots, uint32_t bits,
+                             uint32_t gap, double scale) {
+  const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= 2 * slots) return;
+  const size_t pos = (size_t)t * gap;
+  int64_t a[MAXL];
+  double val = 0.0;
+  for (uint32_t i = 0; i < nlimb; ++i) {
+    const uint64_t q = mc[i].q;
+    uint64_t x = coef[(size_t)i * n + pos];
+    for (uint32_t j = 0; j < i; ++j) {
+      const uint64_t aj = lift_signed(a[j], q);
+      x = shoup(sub_mod(x, aj, q), garner[((size_t)i * L + j) * 2],
+                garner[((size_t)i * L + j) * 2 + 1], q);
+    }
+    a[i] = x > (q >> 1) ? (int64_t)x - (int64_t)q : (int64_t)x;
+  }
+  val = (double)a[nlimb - 1];
+  for (int i = (int)nlimb - 2; i >= 0; --i) val = val * (double)mods[i] + (double)a[i];
+  val = val / scale;
+  const uint32_t slot = t < slots ? t : t - slots;
+  double* dst = reinterpret_cast<double*>(v + brev_bits(slot, bits));
+  dst[t < slots ? 0 : 1] = val;
+}
+
+void run_stages(Context& c, double2* v, const double* tw, uint32_t slots, bool inverse) {
+  if (slots < 2) return;
+  const uint32_t threads = slots / 2 < TPB ? slots / 2 : TPB;
+  const uint32_t blocks = (slots / 2 + threads - 1) / threads;
+  if (inverse) {
+    for (uint32_t len = slots; len >= 2; len >>= 1)
+      FHE_LAUNCH(c, "k_fft_inv_stage", k_fft_inv_stage, dim3(blocks), dim3(threads), 0, v, tw, slots, len);
+  } else {
+    for (uint32_t len = 2; len <= slots; len <<= 1)
+      FHE_LAUNCH(c, "k_fft_fwd_stage", k_fft_fwd_stage, dim3(blocks), dim3(threads), 0, v, tw, slots, len);
+  }
+}
+
+void check_slots(const Context& c, uint32_t slots) {
+  if (slots == 0 || (slots & (slots - 1)) || slots > c.n / 2)
+    throw ArgError("slots must be a power of two <= N/2");
+}
+
+}  // namespace
+
+bool encode(Context& c, const double* re, const double* im, uint32_t count, uint32_t slots,
+            double scale, uint32_t nlimb, uint64_t* out) {
+  check_slots(c, slots);
+  if (count > slots) throw ArgError("more values than slots");
+  if (nlimb == 0 || nlimb > c.L) throw ArgError("bad limb count");
+  if (!(scale > 0) || !std::isfinite(scale)) throw ArgError("scale must be positive");
+  std::vector<double> host(2 * (size_t)slots, 0.0);
+  for (uint32_t j = 0; j < count; ++j) {
+    host[2 * j] = re[j];
+    host[2 * j + 1] = im ? im[j] : 0.0;
+  }
+  const auto tw = fft_tables(c, slots);
+  Scratch v(c, 2 * (size_t)slots), st(c, 1);
+  hip_check(hipMemcpyAsync(v.p, host.data(), host.size() * 8, hipMemcpyHostToDevice, c.stream),
+            "encode upload");
+  hip_check(hipMemsetAsync(st.p, 0, 8, c.stream), "encode status");
+  hip_check(hipMemsetAsync(out, 0, (size_t)nlimb * c.n * 8, c.stream), "encode clear");
+  run_stages(c, reinterpret_cast<double2*>(v.p), tw.first, slots, true);
+  const uint32_t threads = slots < TPB ? slots : TPB;
+  FHE_LAUNCH(c, "k_round_lift", k_round_lift, dim3((slots + threads - 1) / threads), dim3(threads), 0, reinterpret_cast<const double2*>(v.p), out, c.d_const, slots, ilog2(slots), c.n / (2 * slots), c.n, nlimb, scale, reinterpret_cast<int*>(st.p));
+  int status = 0;
+  hip_check(hipMemcpyAsync(&status, st.p, sizeof(int), hipMemcpyDeviceToHost, c.stream),
+            "encode status");
+  hip_check(hipStreamSynchronize(c.stream), "encode sync");
+  if (status) return false;
+  ntt_forward(c, out, 1, 0, nlimb, LimbMap::contiguous(0));
+  return true;
+}
+
+void decode(Context& c, const uint64_t* pt, uint32_t nlimb, uint32_t slots, double scale,
+            double* re, double* im) {
+  check_slots(c, slots);
+  if (nlimb == 0 || nlimb > c.L) throw ArgError("bad limb count");
+  const auto tw = fft_tables(c, slots);
+  Scratch coef(c, (size_t)nlimb * c.n), v(c, 2 * (size_t)slots), mods(c, c.L);
+  hip_check(hipMemcpyAsync(coef.p, pt, (size_t)nlimb * c.n * 8, hipMemcpyDeviceToDevice,
+                           c.stream),
+            "decode copy");
+  hip_check(hipMemcpyAsync(mods.p, c.mods.data(), c.L * 8, hipMemcpyHostToDevice, c.stream),
+            "decode moduli");
+  ntt_inverse(c, coef.p, 1, 0, nlimb, LimbMap::contiguous(0));
+  const uint32_t cnt = 2 * slots, threads = cnt < 64 ? cnt : 64;
+  FHE_LAUNCH(c, "k_crt_decode", (k_crt_decode<64>), dim3((cnt + threads - 1) / threads), dim3(threads), 0, coef.p, reinterpret_cast<double2*>(v.p), c.d_const, c.d_garner, mods.p, c.n, nlimb, c.L, slots, ilog2(slots), c.n / (2 * slots), scale);
+  run_stages(c, reinterpret_cast<double2*>(v.p), tw.second, slots, false);
+  std::vector<double> host(2 * (size_t)slots);
+  hip_check(hipMemcpyAsync(host.data(), v.p, host.size() * 8, hipMemcpyDeviceToHost, c.stream),
+            "decode download");
+  hip_check(hipStreamSynchronize(c.stream), "decode sync");
+  for (uint32_t j = 0; j < slots; ++j) {
+    re[j] = host[2 * j];
+    if (im) im[j] = host[2 * j + 1];
+  }
+}
+
+}  // namespace fhe

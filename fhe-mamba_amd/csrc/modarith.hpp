@@ -1,0 +1,105 @@
+// 64-bit modular arithmetic for primes q < 2^61 on the CDNA4 VALU.
+//
+// gfx950 issues v_mad_u64_u32 / v_mul_lo_u32 / v_mul_hi_u32 at full rate,
+// so every helper here is written to minimise the number of 32-bit
+// multiply instructions the compiler has to emit.  Ranges follow Harvey's
+// lazy-reduction conventions: most helpers return values in [0, 2q) and the
+// callers keep track of the bound (documented at each use).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define FHE_HD __host__ __device__ __forceinline__
+
+namespace fhe {
+
+typedef unsigned __int128 u128;
+
+FHE_HD uint64_t mulhi64(uint64_t a, uint64_t b) {
+  return (uint64_t)(((u128)a * b) >> 64);
+}
+
+// Shoup product with a precomputed companion wp = floor(w * 2^64 / q).
+// For any a < 2^64 and w < q the result is a*w mod q plus 0 or q: [0, 2q).
+FHE_HD uint64_t shoup_lazy(uint64_t a, uint64_t w, uint64_t wp, uint64_t q) {
+  return a * w - mulhi64(a, wp) * q;
+}
+
+FHE_HD uint64_t reduce_2q(uint64_t x, uint64_t q) { return x >= q ? x - q : x; }
+
+FHE_HD uint64_t reduce_4q(uint64_t x, uint64_t q) {
+  x = x >= 2 * q ? x - 2 * q : x;
+  return x >= q ? x - q : x;
+}
+
+FHE_HD uint64_t shoup(uint64_t a, uint64_t w, uint64_t wp, uint64_t q) {
+  return reduce_2q(shoup_lazy(a, w, wp, q), q);
+}
+
+FHE_HD uint64_t add_mod(uint64_t a, uint64_t b, uint64_t q) {
+  uint64_t s = a + b;
+  return s >= q ? s - q : s;
+}
+
+FHE_HD uint64_t sub_mod(uint64_t a, uint64_t b, uint64_t q) {
+  return a >= b ? a - b : a + q - b;
+}
+
+FHE_HD uint64_t neg_mod(uint64_t a, uint64_t q) { return a ? q - a : 0; }
+
+// Montgomery reduction of T = hi*2^64 + lo with T < q * 2^64, qinv_neg =
+// -q^-1 mod 2^64.  Returns T * 2^-64 mod q in [0, q).
+FHE_HD uint64_t redc(uint64_t hi, uint64_t lo, uint64_t q, uint64_t qinv_neg) {
+  const uint64_t m = lo * qinv_neg;
+  const uint64_t t = hi + mulhi64(m, q) + (lo != 0);
+  return t >= q ? t - q : t;
+}
+
+// a * b * 2^-64 mod q for a, b < q (b typically held in Montgomery form,
+// so the product comes out in the standard domain).
+FHE_HD uint64_t mont_mul(uint64_t a, uint64_t b, uint64_t q, uint64_t qinv_neg) {
+  const u128 p = (u128)a * b;
+  return redc((uint64_t)(p >> 64), (uint64_t)p, q, qinv_neg);
+}
+
+// 128-bit accumulator for sums of products that are reduced once.
+struct Acc128 {
+  uint64_t lo, hi;
+  FHE_HD Acc128() : lo(0), hi(0) {}
+  FHE_HD void mac(uint64_t a, uint64_t b) {
+    const u128 p = (u128)a * b;
+    const uint64_t plo = (uint64_t)p;
+    lo += plo;
+    hi += (uint64_t)(p >> 64) + (lo < plo);
+  }
+};
+
+// Host-side helpers for table construction.
+inline uint64_t host_mulmod(uint64_t a, uint64_t b, uint64_t q) {
+  return (uint64_t)(((u128)a * b) % q);
+}
+inline uint64_t host_powmod(uint64_t a, uint64_t e, uint64_t q) {
+  uint64_t r = 1 % q;
+  a %= q;
+  while (e) {
+    if (e & 1) r = host_mulmod(r, a, q);
+    a = host_mulmod(a, a, q);
+    e >>= 1;
+  }
+  return r;
+}
+inline uint64_t host_invmod(uint64_t a, uint64_t q) { return host_powmod(a, q - 2, q); }
+inline uint64_t host_shoup(uint64_t w, uint64_t q) { return (uint64_t)(((u128)w << 64) / q); }
+// -q^-1 mod 2^64 by Newton iteration (q odd).
+inline uint64_t host_qinv_neg(uint64_t q) {
+  uint64_t x = q;  // correct to 3 bits
+  for (int i = 0; i < 6; ++i) x *= 2 - q * x;
+  return ~x + 1;
+}
+// a * 2^64 mod q (Montgomery form).
+inline uint64_t host_to_mont(uint64_t a, uint64_t q) {
+  return (uint64_t)(((u128)(a % q) << 64) % q);
+}
+
+}  // namespace fhe

@@ -1,0 +1,256 @@
+// Negacyclic RNS NTT / inverse NTT for gfx950.
+//
+// Forward transform = OpenFHE's ForwardTransformToBitReverseInPlace (the
+// transform behind every FIDESlib NTT_ launch the reference makes,
+// experiments/ntt_warp_tail/probe.cu:58-66): Cooley-Tukey stages with
+// twiddles psi^brv(m+i), output slot i holding a(psi^(2 brv(i) + 1)).
+// The inverse runs Gentleman-Sande stages with psi^-brv(m+i), then N^-1.
+//
+// Structure.  For N = 2^logN with logN >= 13 the transform is split into
+// two launches over "lines":
+//   COLS   line c in [0, N2): elements c + N2*u, u in [0, N1)  (stages that
+//          pair elements at distance >= N2; S1 = ceil(logN/2) stages)
+//   BLOCKS line b in [0, N1): elements b*N2 + u, u in [0, N2)  (the last
+//          S2 = floor(logN/2) stages)
+// Rings with logN <= 12 use one launch (SINGLE) per limb.  Each thread
+// holds 16 elements in registers and runs 4 stages at a time (radix-16);
+// sub-passes exchange through an LDS tile padded by one word per 16 words,
+// which keeps both the stride-1 and the stride-16 access patterns free of
+// bank conflicts.  Workgroups are 256 threads (4096 elements, ~35 KB LDS).
+//
+// Arithmetic: Harvey lazy butterflies.  Forward values stay in [0, 4q),
+// inverse values in [0, 2q); the final launch reduces to [0, q).  This
+// needs 4q < 2^64, guaranteed by q < 2^61.
+//
+// Grid: (tiles per limb, poly, limb).  The limb index is the slowest grid
+// dimension so consecutive workgroups share one modulus and its twiddle
+// table stays hot in L2.
+#include "context.hpp"
+
+namespace fhe {
+namespace {
+
+constexpr int RHO = 4;
+constexpr int R = 1 << RHO;
+enum Kind { SINGLE = 0, COLS = 1, BLOCKS = 2 };
+
+template <int S>
+struct Geo {
+  static constexpr int TPL = 1 << (S - RHO);  // threads per line
+  static constexpr int LEN = 1 << S;
+  static constexpr int PITCH = LEN + LEN / 16 + 1;
+};
+
+__device__ __forceinline__ uint32_t lds_idx(uint32_t line, uint32_t u, uint32_t pitch) {
+  return line * pitch + u + (u >> 4);
+}
+
+template <int S, int KIND, bool INV>
+__global__ void __launch_bounds__(256)
+    ntt_pass(uint64_t* __restrict__ data, size_t poly_stride, const ModConst* __restrict__ mc,
+             const uint64_t* __restrict__ tw_all, uint32_t log_n, LimbMap map, uint32_t s_other,
+             int last) {
+  using G = Geo<S>;
+  constexpr int LINES = KIND == SINGLE ? 1 : 256 / G::TPL;
+  constexpr int NSP = (S + RHO - 1) / RHO;
+  __shared__ uint64_t lds[LINES * G::PITCH];
+
+  const uint32_t n = 1u << log_n;
+  const uint32_t limb = blockIdx.z;
+  const uint32_t midx = map(limb);
+  const uint64_t q = mc[midx].q, q2 = 2 * q;
+  const uint64_t* __restrict__ tw = tw_all + (size_t)midx * n * 2;
+  uint64_t* __restrict__ base = data + (size_t)blockIdx.y * poly_stride + (size_t)limb * n;
+
+  const uint32_t tid = threadIdx.x;
+  uint32_t line, tau;
+  if (KIND == COLS) {
+    line = tid % LINES;
+    tau = tid / LINES;
+  } else {
+    tau = tid % G::TPL;
+    line = tid / G::TPL;
+  }
+  const uint32_t gline = blockIdx.x * LINES + line;
+  const uint32_t twbase = KIND == BLOCKS ? (1u << s_other) + gline : 1u;
+
+  uint64_t x[R];
+
+#pragma unroll
+  for (int sp = 0; sp < NSP; ++sp) {
+    // Window [w, w + RHO) of line-local index bits held by this thread, and
+    // the stage bits [blo, bhi] processed in this sub-pass.
+    int w, blo, bhi;
+    if (!INV) {
+      const int hi = S - RHO * sp;
+      w = hi >= RHO ? hi - RHO : 0;
+      bhi = hi - 1;
+      blo = w;
+    } else {
+      const int lo = RHO * sp;
+      w = lo + RHO <= S ? lo : S - RHO;
+      blo = lo;
+      bhi = lo + RHO <= S ? lo + RHO - 1 : S - 1;
+    }
+    const uint32_t thi = (tau >> w) << (w + RHO), tlo = tau & ((1u << w) - 1);
+
+    if (sp == 0) {
+#pragma unroll
+      for (int v = 0; v < R; ++v) {
+        const uint32_t u = thi | ((uint32_t)v << w) | tlo;
+        const size_t g = KIND == COLS ? gline + ((size_t)u << s_other) : ((size_t)gline << S) + u;
+        x[v] = base[g];
+      }
+    } else {
+      __syncthreads();
+#pragma unroll
+      for (int v = 0; v < R; ++v) {
+        const uint32_t u = thi | ((uint32_t)v << w) | tlo;
+        x[v] = lds[lds_idx(line, u, G::PITCH)];
+      }
+    }
+
+    if (!INV) {
+#pragma unroll
+      for (int beta = bhi; beta >= blo; --beta) {
+        const int d = 1 << (beta - w);
+#pragma unroll
+        for (int v = 0; v < R; ++v) {
+          if (v & d) continue;
+          const uint32_t u = thi | ((uint32_t)v << w) | tlo;
+          const uint32_t ti = (twbase << (S - 1 - beta)) | (u >> (beta + 1));
+          const uint64_t wv = tw[2 * ti], ws = tw[2 * ti + 1];
+          uint64_t X = x[v];
+          X = X >= q2 ? X - q2 : X;
+          const uint64_t T = shoup_lazy(x[v + d], wv, ws, q);
+          x[v] = X + T;
+          x[v + d] = X + q2 - T;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int beta = blo; beta <= bhi; ++beta) {
+        const int d = 1 << (beta - w);
+#pragma unroll
+        for (int v = 0; v < R; ++v) {
+          if (v & d) continue;
+          const uint32_t u = thi | ((uint32_t)v << w) | tlo;
+          const uint32_t ti = (twbase << (S - 1 - beta)) | (u >> (beta + 1));
+          const uint64_t wv = tw[2 * ti], ws = tw[2 * ti + 1];
+          const uint64_t X = x[v], Y = x[v + d];
+          uint64_t Sx = X + Y;
+          Sx = Sx >= q2 ? Sx - q2 : Sx;
+          x[v + d] = shoup_lazy(X + q2 - Y, wv, ws, q);
+          x[v] = Sx;
+        }
+      }
+    }
+
+    if (sp == NSP - 1) {
+      if (last) {
+        if (!INV) {
+#pragma unroll
+          for (int v = 0; v < R; ++v) x[v] = reduce_4q(x[v], q);
+        } else {
+          const uint64_t ni = mc[midx].ninv, nis = mc[midx].ninv_sh;
+#pragma unroll
+          for (int v = 0; v < R; ++v) x[v] = reduce_2q(shoup_lazy(x[v], ni, nis, q), q);
+        }
+      }
+#pragma unroll
+      for (int v = 0; v < R; ++v) {
+        const uint32_t u = thi | ((uint32_t)v << w) | tlo;
+        const size_t g = KIND == COLS ? gline + ((size_t)u << s_other) : ((size_t)gline << S) + u;
+        base[g] = x[v];
+      }
+    } else {
+      if (sp > 0) __syncthreads();
+#pragma unroll
+      for (int v = 0; v < R; ++v) {
+        const uint32_t u = thi | ((uint32_t)v << w) | tlo;
+        lds[lds_idx(line, u, G::PITCH)] = x[v];
+      }
+    }
+  }
+}
+
+template <int S, int KIND, bool INV>
+void launch_pass(Context& c, uint64_t* data, uint32_t npoly, size_t poly_stride, uint32_t nlimb,
+                 LimbMap map, uint32_t s_other, bool last) {
+  using G = Geo<S>;
+  const uint32_t lines = KIND == SINGLE ? 1 : 256 / G::TPL;
+  const uint32_t threads = KIND == SINGLE ? G::TPL : 256;
+  // COLS has N2 = 2^s_other lines per limb, BLOCKS has N1 = 2^s_other.
+  const uint32_t tiles = KIND == SINGLE ? 1 : (1u << s_other) / lines;
+  dim3 grid(tiles, npoly, nlimb);
+  const char* const PASS_NAME =
+      KIND == SINGLE ? (INV ? "ntt_inv_single" : "ntt_fwd_single")
+      : KIND == COLS ? (INV ? "ntt_inv_cols" : "ntt_fwd_cols")
+                     : (INV ? "ntt_inv_blocks" : "ntt_fwd_blocks");
+  FHE_LAUNCH(c, PASS_NAME, (ntt_pass<S, KIND, INV>), grid, dim3(threads), 0, data, poly_stride, c.d_const, INV ? c.d_tw_inv : c.d_tw_fwd, c.log_n, map, s_other, (int)last);
+}
+
+template <bool INV>
+void launch_single(Context& c, uint64_t* data, uint32_t npoly, size_t ps, uint32_t nlimb, LimbMap map) {
+  switch (c.log_n) {
+#define CASE(S) \
+  case S: launch_pass<S, SINGLE, INV>(c, data, npoly, ps, nlimb, map, 0, true); break;
+    CASE(4) CASE(5) CASE(6) CASE(7) CASE(8) CASE(9) CASE(10) CASE(11) CASE(12)
+#undef CASE
+    default: throw ArgError("unsupported ring dimension");
+  }
+}
+
+template <bool INV>
+void launch_cols(Context& c, uint32_t s1, uint32_t s2, uint64_t* data, uint32_t npoly, size_t ps,
+                 uint32_t nlimb, LimbMap map, bool last) {
+  switch (s1) {
+#define CASE(S) \
+  case S: launch_pass<S, COLS, INV>(c, data, npoly, ps, nlimb, map, s2, last); break;
+    CASE(7) CASE(8) CASE(9)
+#undef CASE
+    default: throw ArgError("unsupported column pass");
+  }
+}
+
+template <bool INV>
+void launch_blocks(Context& c, uint32_t s1, uint32_t s2, uint64_t* data, uint32_t npoly, size_t ps,
+                   uint32_t nlimb, LimbMap map, bool last) {
+  switch (s2) {
+#define CASE(S) \
+  case S: launch_pass<S, BLOCKS, INV>(c, data, npoly, ps, nlimb, map, s1, last); break;
+    CASE(6) CASE(7) CASE(8)
+#undef CASE
+    default: throw ArgError("unsupported block pass");
+  }
+}
+
+}  // namespace
+
+void ntt_forward(Context& c, uint64_t* data, uint32_t npoly, size_t poly_stride, uint32_t nlimb,
+                 LimbMap map) {
+  if (npoly == 0 || nlimb == 0) return;
+  if (npoly > 65535 || nlimb > 65535) throw ArgError("too many polys or limbs in one launch");
+  if (c.log_n <= 12) {
+    launch_single<false>(c, data, npoly, poly_stride, nlimb, map);
+    return;
+  }
+  const uint32_t s1 = (c.log_n + 1) / 2, s2 = c.log_n / 2;
+  launch_cols<false>(c, s1, s2, data, npoly, poly_stride, nlimb, map, false);
+  launch_blocks<false>(c, s1, s2, data, npoly, poly_stride, nlimb, map, true);
+}
+
+void ntt_inverse(Context& c, uint64_t* data, uint32_t npoly, size_t poly_stride, uint32_t nlimb,
+                 LimbMap map) {
+  if (npoly == 0 || nlimb == 0) return;
+  if (npoly > 65535 || nlimb > 65535) throw ArgError("too many polys or limbs in one launch");
+  if (c.log_n <= 12) {
+    launch_single<true>(c, data, npoly, poly_stride, nlimb, map);
+    return;
+  }
+  const uint32_t s1 = (c.log_n + 1) / 2, s2 = c.log_n / 2;
+  launch_blocks<true>(c, s1, s2, data, npoly, poly_stride, nlimb, map, false);
+  launch_cols<true>(c, s1, s2, data, npoly, poly_stride, nlimb, map, true);
+}
+
+}  // namespace fhe

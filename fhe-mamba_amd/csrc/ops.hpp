@@ -1,0 +1,79 @@
+// Device operations on raw limb-major arrays, called by the C ABI layer.
+// Shapes: a poly set is [npoly][nlimb][N]; limb j is reduced mod q_j.
+#pragma once
+
+#include "context.hpp"
+
+namespace fhe {
+
+enum BinOp { OP_ADD = 0, OP_SUB = 1 };
+
+// Elementwise (out may alias an input).
+void poly_binary(Context& c, BinOp op, uint64_t* out, const uint64_t* a, const uint64_t* b,
+                 uint32_t npoly, uint32_t nlimb);
+void poly_negate(Context& c, uint64_t* out, const uint64_t* a, uint32_t npoly, uint32_t nlimb);
+void poly_mul_plain(Context& c, uint64_t* out, const uint64_t* a, const uint64_t* pt,
+                    uint32_t npoly, uint32_t nlimb);
+void poly_add_plain(Context& c, uint64_t* out, const uint64_t* a, const uint64_t* pt,
+                    uint32_t npoly, uint32_t nlimb);
+// Per-limb constants (host array of nlimb values < q_j).
+void poly_mul_const(Context& c, uint64_t* out, const uint64_t* a, const uint64_t* consts,
+                    uint32_t npoly, uint32_t nlimb);
+void poly_add_const(Context& c, uint64_t* out, const uint64_t* a, const uint64_t* consts,
+                    uint32_t npoly, uint32_t nlimb);
+// Copy the first `nlimb` limbs of every poly from a (a_nlimb limbs/poly)
+// into out (out_nlimb limbs/poly).
+void poly_copy_limbs(Context& c, uint64_t* out, uint32_t out_nlimb, const uint64_t* a,
+                     uint32_t a_nlimb, uint32_t npoly, uint32_t nlimb);
+// out3 = (a0 b0, a0 b1 + a1 b0, a1 b1); a == b takes the squaring path.
+void poly_tensor(Context& c, uint64_t* out3, const uint64_t* a, const uint64_t* b,
+                 uint32_t nlimb);
+// acc[2][nq][N] = sum_i x_i (.) w_i for x [n][2][nq][N], w [n][nq][N].
+void poly_mac(Context& c, uint64_t* acc, const uint64_t* x, const uint64_t* w, uint32_t n,
+              uint32_t nq);
+// Drop the last limb with centred division (FLEXIBLEAUTO rescale);
+// out is [npoly][nq-1][N].
+void poly_rescale(Context& c, uint64_t* out, const uint64_t* a, uint32_t npoly, uint32_t nq);
+
+// ---- hybrid key switching (keyswitch.hip) ----
+uint32_t num_digits(const Context& c, uint32_t nq);
+// Digits [nd][nq+K][N] (evaluation form) of a [nq][N].
+void modup(Context& c, const uint64_t* a, uint32_t nq, uint64_t* digits);
+// ext [2][nq+K][N] = sum_j digits_j (.) key_j (key in Montgomery form).
+void ksk_inner(Context& c, const uint64_t* digits, uint32_t nq, const uint64_t* key_mont,
+               uint64_t* ext);
+// out_b = galois-permute((ext_b[Q] - ModDownConv(ext_b[P])) * P^-1 + add_b), b = 0, 1,
+// with addends add0 / add1 ([nq][N], may be null); galois 1 means no permutation.
+void moddown_pair2(Context& c, const uint64_t* ext, uint32_t nq, uint64_t* out,
+                   const uint64_t* add0, const uint64_t* add1, uint32_t galois);
+void moddown_pair(Context& c, const uint64_t* ext, uint32_t nq, uint64_t* out,
+                  const uint64_t* add0, uint32_t galois);
+// Galois permutation X -> X^galois of evaluation-form limbs.
+void automorph(Context& c, uint64_t* out, const uint64_t* in, uint32_t npoly, uint32_t nlimb,
+               uint32_t galois);
+// Convert a standard-form key [dnum][2][L+K][N] to Montgomery form in place.
+void key_to_montgomery(Context& c, uint64_t* key);
+
+// ---- encoding (encode.hip) ----
+// Returns false if a scaled coefficient does not fit.
+bool encode(Context& c, const double* re, const double* im, uint32_t count, uint32_t slots,
+            double scale, uint32_t nlimb, uint64_t* out);
+void decode(Context& c, const uint64_t* pt, uint32_t nlimb, uint32_t slots, double scale,
+            double* re, double* im);
+
+// ---- key material (keygen.hip) ----
+void sample_ternary_host(uint64_t key, int64_t* out, uint32_t n);
+void signed_to_eval(Context& c, const int64_t* coef_host, uint32_t idx0, uint32_t nlimb,
+                    uint64_t* out);
+void keygen_public(Context& c, const int64_t* s_coef, uint64_t seed, uint64_t* pk);
+void keygen_switch(Context& c, const uint64_t* s_old, const uint64_t* s_new, uint64_t seed,
+                   uint64_t tag, uint64_t* key);
+void keygen_relin(Context& c, const int64_t* s_coef, uint64_t seed, uint64_t* key);
+void keygen_galois(Context& c, const int64_t* s_coef, uint32_t galois, uint64_t seed,
+                   uint64_t* key);
+void encrypt_pk(Context& c, const uint64_t* pk, const uint64_t* m, uint32_t nq, uint64_t seed,
+                uint64_t* ct);
+void decrypt(Context& c, const uint64_t* ct, uint32_t npoly, uint32_t nq, const int64_t* s_coef,
+             uint64_t* m);
+
+}  // namespace fhe

@@ -1,0 +1,286 @@
+// Elementwise RNS kernels: add/sub/negate, plaintext and constant products,
+// tensor product, the MAC of a plaintext-ciphertext inner product, and the
+// FLEXIBLEAUTO rescale.  All are HBM-bound; each thread moves two adjacent
+// words with 16-byte accesses and the grid is (N/512, limb, poly) so the
+// modulus constants are uniform per workgroup.
+#include "ops.hpp"
+
+namespace fhe {
+namespace {
+
+constexpr int TPB = 256;  // threads per block, 2 words per thread
+
+struct U2 {
+  uint64_t x, y;
+};
+
+__device__ __forceinline__ U2 ld2(const uint64_t* p) {
+  const ulonglong2 v = *reinterpret_cast<const ulonglong2*>(p);
+  return U2{v.x, v.y};
+}
+__device__ __forceinline__ void st2(uint64_t* p, uint64_t a, uint64_t b) {
+  *reinterpret_cast<ulonglong2*>(p) = make_ulonglong2(a, b);
+}
+
+inline uint32_t tpb_for(const Context& c) { return c.n / 2 < TPB ? c.n / 2 : TPB; }
+inline dim3 grid_for(const Context& c, uint32_t nlimb, uint32_t npoly) {
+  return dim3(c.n / (2 * tpb_for(c)), nlimb, npoly);
+}
+
+// Word pair handled by this thread within its limb.
+__device__ __forceinline__ size_t pair_off() {
+  return 2 * ((size_t)blockIdx.x * blockDim.x + threadIdx.x);
+}
+// blockIdx: x = chunk of N, y = limb, z = poly.
+__device__ __forceinline__ size_t elem_off(uint32_t n, uint32_t nlimb) {
+  return ((size_t)blockIdx.z * nlimb + blockIdx.y) * n + pair_off();
+}
+
+template <int OP>
+__global__ void __launch_bounds__(TPB)
+    k_binary(uint64_t* out, const uint64_t* a, const uint64_t* b, const ModConst* mc, uint32_t n,
+             uint32_t nlimb) {
+  const uint64_t q = mc[blockIdx.y].q;
+  const size_t o = elem_off(n, nlimb);
+  const U2 x = ld2(a + o), y = ld2(b + o);
+  if (OP == OP_ADD)
+    st2(out + o, add_mod(x.x, y.x, q), add_mod(x.y, y.y, q));
+  else
+    st2(out + o, sub_mod(x.x, y.x, q), sub_mod(x.y, y.y, q));
+}
+
+__global__ void __launch_bounds__(TPB)
+    k_negate(uint64_t* out, const uint64_t* a, const ModConst* mc, uint32_t n, uint32_t nlimb) {
+  const uint64_t q = mc[blockIdx.y].q;
+  const size_t o = elem_off(n, nlimb);
+  const U2 x = ld2(a + o);
+  st2(out + o, neg_mod(x.x, q), neg_mod(x.y, q));
+}
+
+__global__ void __launch_bounds__(TPB)
+    k_mul_plain(uint64_t* out, const uint64_t* a, const uint64_t* pt, const ModConst* mc,
+                uint32_t n, uint32_t nlimb) {
+  const ModConst m = mc[blockIdx.y];
+  const size_t o = elem_off(n, nlimb);
+  const size_t po = (size_t)blockIdx.y * n + pair_off();
+  const U2 x = ld2(a + o), w = ld2(pt + po);
+  st2(out + o, mul_mod(x.x, w.x, m), mul_mod(x.y, w.y, m));
+}
+
+__global__ void __launch_bounds__(TPB)
+    k_add_plain(uint64_t* out, const uint64_t* a, const uint64_t* pt, const ModConst* mc,
+                uint32_t n, uint32_t nlimb) {
+  const uint64_t q = mc[blockIdx.y].q;
+  const size_t o = elem_off(n, nlimb);
+  U2 x = ld2(a + o);
+  if (blockIdx.z == 0) {
+    const size_t po = (size_t)blockIdx.y * n + pair_off();
+    const U2 w = ld2(pt + po);
+    x.x = add_mod(x.x, w.x, q);
+    x.y = add_mod(x.y, w.y, q);
+  }
+  st2(out + o, x.x, x.y);
+}
+
+struct LimbConsts {
+  uint64_t v[64][2];  // (value, Shoup companion)
+};
+
+__global__ void __launch_bounds__(TPB)
+    k_mul_const(uint64_t* out, const uint64_t* a, LimbConsts k, const ModConst* mc, uint32_t n,
+                uint32_t nlimb) {
+  const uint64_t q = mc[blockIdx.y].q, w = k.v[blockIdx.y][0], ws = k.v[blockIdx.y][1];
+  const size_t o = elem_off(n, nlimb);
+  const U2 x = ld2(a + o);
+  st2(out + o, shoup(x.x, w, ws, q), shoup(x.y, w, ws, q));
+}
+
+__global__ void __launch_bounds__(TPB)
+    k_add_const(uint64_t* out, const uint64_t* a, LimbConsts k, const ModConst* mc, uint32_t n,
+                uint32_t nlimb) {
+  const uint64_t q = mc[blockIdx.y].q, w = blockIdx.z == 0 ? k.v[blockIdx.y][0] : 0;
+  const size_t o = elem_off(n, nlimb);
+  const U2 x = ld2(a + o);
+  st2(out + o, add_mod(x.x, w, q), add_mod(x.y, w, q));
+}
+
+__global__ void __launch_bounds__(TPB)
+    k_copy_limbs(uint64_t* out, uint32_t out_nlimb, const uint64_t* a, uint32_t a_nlimb,
+                 uint32_t n) {
+  const size_t e = pair_off();
+  const U2 x = ld2(a + ((size_t)blockIdx.z * a_nlimb + blockIdx.y) * n + e);
+  st2(out + ((size_t)blockIdx.z * out_nlimb + blockIdx.y) * n + e, x.x, x.y);
+}
+
+// Tensor: grid (N/512, nlimb, 1).
+template <bool SQUARE>
+__global__ void __launch_bounds__(TPB)
+    k_tensor(uint64_t* out, const uint64_t* a, const uint64_t* b, const ModConst* mc, uint32_t n,
+             uint32_t nlimb) {
+  const ModConst m = mc[blockIdx.y];
+  const size_t pl = (size_t)nlimb * n;
+  const size_t o = (size_t)blockIdx.y * n + pair_off();
+  const U2 a0 = ld2(a + o), a1 = ld2(a + pl + o);
+  if (SQUARE) {
+    const uint64_t c1x = mul_mod(a0.x, a1.x, m), c1y = mul_mod(a0.y, a1.y, m);
+    st2(out + o, mul_mod(a0.x, a0.x, m), mul_mod(a0.y, a0.y, m));
+    st2(out + pl + o, add_mod(c1x, c1x, m.q), add_mod(c1y, c1y, m.q));
+    st2(out + 2 * pl + o, mul_mod(a1.x, a1.x, m), mul_mod(a1.y, a1.y, m));
+  } else {
+    const U2 b0 = ld2(b + o), b1 = ld2(b + pl + o);
+    // The cross term is one reduction of a 128-bit sum of two products.
+    Acc128 sx, sy;
+    sx.mac(a0.x, b1.x);
+    sx.mac(a1.x, b0.x);
+    sy.mac(a0.y, b1.y);
+    sy.mac(a1.y, b0.y);
+    st2(out + o, mul_mod(a0.x, b0.x, m), mul_mod(a0.y, b0.y, m));
+    st2(out + pl + o, reduce128(sx.hi, sx.lo, m), reduce128(sy.hi, sy.lo, m));
+    st2(out + 2 * pl + o, mul_mod(a1.x, b1.x, m), mul_mod(a1.y, b1.y, m));
+  }
+}
+
+// MAC: grid (N/512, nq, 2); each thread accumulates n products per word in
+// 128 bits, folding every 32 terms so the sum never overflows.
+__global__ void __launch_bounds__(TPB)
+    k_mac(uint64_t* acc, const uint64_t* x, const uint64_t* w, const ModConst* mc, uint32_t n,
+          uint32_t nq, uint32_t cnt) {
+  const ModConst m = mc[blockIdx.y];
+  const uint32_t poly = blockIdx.z;
+  const size_t e = pair_off();
+  const size_t limb_off = (size_t)blockIdx.y * n + e;
+  const size_t xs = 2 * (size_t)nq * n, ws = (size_t)nq * n;
+  const uint64_t* xp = x + (size_t)poly * nq * n + limb_off;
+  const uint64_t* wp = w + limb_off;
+  Acc128 s0, s1;
+  uint32_t i = 0;
+  while (i < cnt) {
+    const uint32_t end = i + 32 < cnt ? i + 32 : cnt;
+    for (; i < end; ++i) {
+      const U2 xv = ld2(xp + i * xs), wv = ld2(wp + i * ws);
+      s0.mac(xv.x, wv.x);
+      s1.mac(xv.y, wv.y);
+    }
+    // Fold: keep the reduced value in lo, clear hi.
+    s0.lo = reduce128(s0.hi, s0.lo, m);
+    s0.hi = 0;
+    s1.lo = reduce128(s1.hi, s1.lo, m);
+    s1.hi = 0;
+  }
+  st2(acc + (size_t)poly * nq * n + limb_off, s0.lo, s1.lo);
+}
+
+// Rescale step 1: centred lift of the (inverse-NTT'd) last limb into limbs
+// i < l.  grid (N/512, l, npoly).  last: [npoly][N] coefficient form.
+__global__ void __launch_bounds__(TPB)
+    k_rescale_lift(uint64_t* t, const uint64_t* last, const ModConst* mc, const uint64_t* rs,
+                   uint32_t n, uint32_t l, uint32_t L, uint64_t ql) {
+  const uint32_t i = blockIdx.y;
+  const uint64_t q = mc[i].q;
+  const uint64_t qlm = rs[((size_t)l * L + i) * 4];  // q_l mod q_i
+  const size_t e = pair_off();
+  const U2 v = ld2(last + (size_t)blockIdx.z * n + e);
+  const uint64_t half = ql >> 1;
+  const ModConst m = mc[i];
+  auto lift = [&](uint64_t x) -> uint64_t {
+    // x mod q_i (x < 2^61 may exceed q_i), minus q_l if x is in the upper half.
+    const uint64_t r = reduce_2q(x - mulhi64(x, m.mu64) * q, q);
+    return x > half ? sub_mod(r, qlm, q) : r;
+  };
+  st2(t + ((size_t)blockIdx.z * l + i) * n + e, lift(v.x), lift(v.y));
+}
+
+// Rescale step 2: out_i = (a_i - t_i) * q_l^-1.  grid (N/512, l, npoly).
+__global__ void __launch_bounds__(TPB)
+    k_rescale_combine(uint64_t* out, const uint64_t* a, const uint64_t* t, const ModConst* mc,
+                      const uint64_t* rs, uint32_t n, uint32_t l, uint32_t L) {
+  const uint32_t i = blockIdx.y;
+  const uint64_t q = mc[i].q;
+  const uint64_t inv = rs[((size_t)l * L + i) * 4 + 1], invs = rs[((size_t)l * L + i) * 4 + 2];
+  const size_t e = pair_off();
+  const U2 x = ld2(a + ((size_t)blockIdx.z * (l + 1) + i) * n + e);
+  const U2 y = ld2(t + ((size_t)blockIdx.z * l + i) * n + e);
+  st2(out + ((size_t)blockIdx.z * l + i) * n + e, shoup(x.x + q - y.x, inv, invs, q),
+      shoup(x.y + q - y.y, inv, invs, q));
+}
+
+LimbConsts make_consts(const Context& c, const uint64_t* consts, uint32_t nlimb) {
+  if (nlimb > 64) throw ArgError("at most 64 limbs");
+  LimbConsts k{};
+  for (uint32_t j = 0; j < nlimb; ++j) {
+    const uint64_t q = c.mods[j];
+    if (consts[j] >= q) throw ArgError("constant not reduced mod q_j");
+    k.v[j][0] = consts[j];
+    k.v[j][1] = host_shoup(consts[j], q);
+  }
+  return k;
+}
+
+}  // namespace
+
+void poly_binary(Context& c, BinOp op, uint64_t* out, const uint64_t* a, const uint64_t* b,
+                 uint32_t npoly, uint32_t nlimb) {
+  if (op == OP_ADD)
+    FHE_LAUNCH(c, "k_binary", k_binary<OP_ADD>, grid_for(c, nlimb, npoly), dim3(tpb_for(c)), 0, out, a, b, c.d_const, c.n, nlimb);
+  else
+    FHE_LAUNCH(c, "k_binary", k_binary<OP_SUB>, grid_for(c, nlimb, npoly), dim3(tpb_for(c)), 0, out, a, b, c.d_const, c.n, nlimb);
+}
+
+void poly_negate(Context& c, uint64_t* out, const uint64_t* a, uint32_t npoly, uint32_t nlimb) {
+  FHE_LAUNCH(c, "k_negate", k_negate, grid_for(c, nlimb, npoly), dim3(tpb_for(c)), 0, out, a, c.d_const, c.n, nlimb);
+}
+
+void poly_mul_plain(Context& c, uint64_t* out, const uint64_t* a, const uint64_t* pt,
+                    uint32_t npoly, uint32_t nlimb) {
+  FHE_LAUNCH(c, "k_mul_plain", k_mul_plain, grid_for(c, nlimb, npoly), dim3(tpb_for(c)), 0, out, a, pt, c.d_const, c.n, nlimb);
+}
+
+void poly_add_plain(Context& c, uint64_t* out, const uint64_t* a, const uint64_t* pt,
+                    uint32_t npoly, uint32_t nlimb) {
+  FHE_LAUNCH(c, "k_add_plain", k_add_plain, grid_for(c, nlimb, npoly), dim3(tpb_for(c)), 0, out, a, pt, c.d_const, c.n, nlimb);
+}
+
+void poly_mul_const(Context& c, uint64_t* out, const uint64_t* a, const uint64_t* consts,
+                    uint32_t npoly, uint32_t nlimb) {
+  const LimbConsts k = make_consts(c, consts, nlimb);
+  FHE_LAUNCH(c, "k_mul_const", k_mul_const, grid_for(c, nlimb, npoly), dim3(tpb_for(c)), 0, out, a, k, c.d_const, c.n, nlimb);
+}
+
+void poly_add_const(Context& c, uint64_t* out, const uint64_t* a, const uint64_t* consts,
+                    uint32_t npoly, uint32_t nlimb) {
+  const LimbConsts k = make_consts(c, consts, nlimb);
+  FHE_LAUNCH(c, "k_add_const", k_add_const, grid_for(c, nlimb, npoly), dim3(tpb_for(c)), 0, out, a, k, c.d_const, c.n, nlimb);
+}
+
+void poly_copy_limbs(Context& c, uint64_t* out, uint32_t out_nlimb, const uint64_t* a,
+                     uint32_t a_nlimb, uint32_t npoly, uint32_t nlimb) {
+  if (nlimb == 0 || npoly == 0) return;
+  FHE_LAUNCH(c, "k_copy_limbs", k_copy_limbs, grid_for(c, nlimb, npoly), dim3(tpb_for(c)), 0, out, out_nlimb, a, a_nlimb, c.n);
+}
+
+void poly_tensor(Context& c, uint64_t* out3, const uint64_t* a, const uint64_t* b,
+                 uint32_t nlimb) {
+  if (a == b)
+    FHE_LAUNCH(c, "k_tensor", k_tensor<true>, grid_for(c, nlimb, 1), dim3(tpb_for(c)), 0, out3, a, b, c.d_const, c.n, nlimb);
+  else
+    FHE_LAUNCH(c, "k_tensor", k_tensor<false>, grid_for(c, nlimb, 1), dim3(tpb_for(c)), 0, out3, a, b, c.d_const, c.n, nlimb);
+}
+
+void poly_mac(Context& c, uint64_t* acc, const uint64_t* x, const uint64_t* w, uint32_t n,
+              uint32_t nq) {
+  FHE_LAUNCH(c, "k_mac", k_mac, grid_for(c, nq, 2), dim3(tpb_for(c)), 0, acc, x, w, c.d_const, c.n, nq, n);
+}
+
+void poly_rescale(Context& c, uint64_t* out, const uint64_t* a, uint32_t npoly, uint32_t nq) {
+  if (nq < 2) throw ArgError("rescale needs at least two limbs");
+  const uint32_t l = nq - 1;
+  Scratch last(c, (size_t)npoly * c.n), t(c, (size_t)npoly * l * c.n);
+  // last limb of every poly -> [npoly][N], to coefficient form with q_l
+  FHE_LAUNCH(c, "k_copy_limbs", k_copy_limbs, grid_for(c, 1, npoly), dim3(tpb_for(c)), 0, last.p, 1u, a + (size_t)l * c.n, nq, c.n);
+  ntt_inverse(c, last.p, npoly, c.n, 1, LimbMap::contiguous(l));
+  FHE_LAUNCH(c, "k_rescale_lift", k_rescale_lift, grid_for(c, l, npoly), dim3(tpb_for(c)), 0, t.p, last.p, c.d_const, c.d_rescale, c.n, l, c.L, c.mods[l]);
+  ntt_forward(c, t.p, npoly, (size_t)l * c.n, l, LimbMap::contiguous(0));
+  FHE_LAUNCH(c, "k_rescale_combine", k_rescale_combine, grid_for(c, l, npoly), dim3(tpb_for(c)), 0, out, a, t.p, c.d_const, c.d_rescale, c.n, l, c.L);
+}
+
+}  // namespace fhe

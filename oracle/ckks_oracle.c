@@ -6,6 +6,7 @@
  * site it stands in for.  Nothing here is tuned beyond Shoup twiddles in the
  * transforms; clarity comes first.
  */
+#define _GNU_SOURCE /* sincos */
 #include "ckks_oracle.h"
 
 #include <math.h>
@@ -891,10 +892,14 @@ void orc_decrypt(const orc_ctx *c, const uint64_t *ct, uint32_t npoly,
  * :99-108 and patches/openfhe-v1.4.2-inverse-fft-plan.patch:18-60.
  * Plain IEEE double operations; build with -ffp-contract=off.
  * ====================================================================== */
+/* OpenFHE's table entry is (cos(angle), sin(angle)); gcc at -O2 and above
+ * (how OpenFHE and the reference's host code are built) fuses the pair into
+ * one glibc sincos() call, whose results differ from separate cos()/sin() in
+ * the last bit for a few angles.  sincos() is called explicitly so the
+ * table does not depend on the optimisation level. */
 static void fft_twiddle(uint32_t idx, uint32_t m, double *wr, double *wi) {
   const double angle = 2.0 * M_PI * idx / m;
-  *wr = cos(angle);
-  *wi = sin(angle);
+  sincos(angle, wi, wr);
 }
 
 void orc_fft_special_inv(double *re, double *im, uint32_t slots) {

@@ -1,0 +1,65 @@
+"""CKKS encode/decode and encryption on the GPU vs the CPU oracle."""
+import numpy as np
+import pytest
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+F = pytest.importorskip("fhemamba_amd")
+
+
+@pytest.fixture(scope="module", params=[(12, 5, 40), (13, 7, 50), (16, 3, 59)])
+def pair(request):
+    log_n, depth, sb = request.param
+    q, p = O.gen_moduli(log_n, depth, sb, 60, 2)
+    return F.Context(log_n, q, p, 2), O.Ctx(log_n, q, p, 2)
+
+
+@pytest.mark.parametrize("slots_div", [2, 8, 64])
+def test_encode_bit_exact_and_decode_within_tolerance(pair, slots_div):
+    ctx, orc = pair
+    slots = ctx.n // slots_div
+    rng = np.random.default_rng(slots)
+    z = rng.uniform(-1, 1, slots) + 1j * rng.uniform(-1, 1, slots)
+    scale = float(ctx.q[-1])
+    for nq in (1, ctx.L):
+        got = ctx.encode(z, slots, scale, nq)
+        want = orc.encode(z, slots, scale, nq)
+        assert np.array_equal(got.numpy()[0], want)
+        dec = ctx.decode(got, slots, scale)
+        # decoded slot vectors match within 2^-30 relative to the input range
+        assert np.abs(dec - z).max() < 2.0**-30
+        assert np.abs(dec - orc.decode(want, slots, scale)).max() < 2.0**-40
+
+
+def test_encode_real_partial_and_zero(pair):
+    ctx, orc = pair
+    slots = ctx.n // 2
+    x = np.linspace(-3, 3, 17)
+    scale = 2.0**40
+    assert np.array_equal(ctx.encode(x, slots, scale, 2).numpy()[0],
+                          orc.encode(x, slots, scale, 2))
+    assert not ctx.encode(np.zeros(4), slots, scale, 1).numpy().any()
+
+
+def test_encode_out_of_range_raises(pair):
+    ctx, _ = pair
+    with pytest.raises(OverflowError):
+        ctx.encode([2.0**30], 8, 2.0**40, 1)
+
+
+def test_encrypt_decrypt_match_oracle(pair):
+    ctx, orc = pair
+    s = orc.secret(3)
+    pk = orc.public_key(s, 4)
+    slots = ctx.n // 2
+    x = np.random.default_rng(5).uniform(-1, 1, slots)
+    scale = float(ctx.q[-1])
+    m = orc.encode(x, slots, scale, ctx.L)
+    dpk = ctx.upload(pk)
+    ct = ctx.encrypt(dpk, ctx.upload(m), 6)
+    assert np.array_equal(ct.numpy(), orc.encrypt(pk, m, 6))
+    dm = ctx.decrypt(ct, s)
+    assert np.array_equal(dm.numpy()[0], orc.decrypt(ct.numpy(), s))
+    assert np.abs(ctx.decode(dm, slots, scale).real - x).max() < 1e-6

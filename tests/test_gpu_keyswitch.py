@@ -1,0 +1,130 @@
+"""Hybrid key switching, rotations (single and hoisted), conjugation and
+relinearisation on the GPU, bit-exact against the CPU oracle."""
+import numpy as np
+import pytest
+
+import oracle as O
+from gpu_helpers import residues
+
+pytestmark = pytest.mark.gpu
+
+F = pytest.importorskip("fhemamba_amd")
+
+# (log_n, depth, scale bits, first bits, dnum): config-1-like toy chain and
+# a chain with a partial last digit.
+PARAMS = [(13, 7, 50, 60, 2), (12, 6, 45, 60, 3), (11, 4, 40, 60, 1)]
+
+
+@pytest.fixture(scope="module", params=PARAMS)
+def setup(request):
+    log_n, depth, sb, fb, dnum = request.param
+    q, p = O.gen_moduli(log_n, depth, sb, fb, dnum)
+    ctx, orc = F.Context(log_n, q, p, dnum), O.Ctx(log_n, q, p, dnum)
+    s = orc.secret(11)
+    return ctx, orc, s
+
+
+def test_secret_matches_oracle(setup):
+    ctx, orc, s = setup
+    assert np.array_equal(ctx.keygen_secret(11), s)
+
+
+def test_keyswitch_matches_oracle(setup):
+    ctx, orc, s = setup
+    rng = np.random.default_rng(1)
+    key = orc.relin_key(s, 3)
+    dkey = ctx.load_key(key)
+    for nq in sorted({ctx.L, max(1, ctx.L - 1), ctx.alpha + 1, 1}):
+        a = residues(rng, ctx.q[:nq], (1,), ctx.n)
+        got = ctx.keyswitch(ctx.upload(a), dkey).numpy()
+        assert np.array_equal(got, orc.keyswitch(a[0], key)), nq
+
+
+def test_modup_moddown_pieces_through_keyswitch_in_place(setup):
+    ctx, orc, s = setup
+    rng = np.random.default_rng(2)
+    key = orc.relin_key(s, 4)
+    a = residues(rng, ctx.q, (1,), ctx.n)
+    da = ctx.upload(a)
+    ctx.keyswitch(da, ctx.load_key(key), out=da)
+    assert np.array_equal(da.numpy(), orc.keyswitch(a[0], key))
+
+
+@pytest.mark.parametrize("step", [1, -1, 7, 2, -16])
+def test_rotate_matches_oracle(setup, step):
+    ctx, orc, s = setup
+    g = O.galois_elt(step, ctx.n)
+    assert g == F.galois_element(step, ctx.n)
+    key = orc.galois_key(s, g, 20 + step)
+    rng = np.random.default_rng(30 + step)
+    for nq in (ctx.L, max(1, ctx.L - 2)):
+        ct = residues(rng, ctx.q[:nq], (2,), ctx.n)
+        got = ctx.rotate(ctx.upload(ct), ctx.load_key(key), g).numpy()
+        assert np.array_equal(got, orc.rotate(ct, key, g)), nq
+
+
+def test_conjugate_matches_oracle(setup):
+    ctx, orc, s = setup
+    g = F.conjugation_element(ctx.n)
+    key = orc.galois_key(s, g, 9)
+    ct = residues(np.random.default_rng(9), ctx.q, (2,), ctx.n)
+    got = ctx.rotate(ctx.upload(ct), ctx.load_key(key), g).numpy()
+    assert np.array_equal(got, orc.rotate(ct, key, g))
+
+
+def test_hoisted_rotations_equal_single_rotations(setup):
+    ctx, orc, s = setup
+    steps = [1, -1, 2, -2, 4, 8]
+    gal = [O.galois_elt(r, ctx.n) for r in steps]
+    keys = [orc.galois_key(s, g, 40 + i) for i, g in enumerate(gal)]
+    ct = residues(np.random.default_rng(12), ctx.q, (2,), ctx.n)
+    dct = ctx.upload(ct)
+    digits = ctx.rotation_precompute(dct)
+    assert digits.shape == (orc.num_digits(ctx.L), ctx.L + ctx.K)
+    assert np.array_equal(digits.numpy(), orc.modup(ct[1]))
+    outs = ctx.rotate_hoisted(dct, digits, [ctx.load_key(k) for k in keys], gal)
+    for out, key, g in zip(outs, keys, gal):
+        assert np.array_equal(out.numpy(), orc.rotate(ct, key, g))
+
+
+def test_relinearize_matches_oracle(setup):
+    ctx, orc, s = setup
+    key = orc.relin_key(s, 5)
+    rng = np.random.default_rng(13)
+    a = residues(rng, ctx.q, (2,), ctx.n)
+    b = residues(rng, ctx.q, (2,), ctx.n)
+    t = orc.tensor(a, b)
+    got = ctx.relinearize(ctx.upload(t), ctx.load_key(key)).numpy()
+    assert np.array_equal(got, orc.relinearize(t, key))
+
+
+def test_gpu_keygen_matches_oracle_keys(setup):
+    """GPU-generated keys equal the oracle's: their key switches agree
+    word for word (keys are stored in Montgomery form on the device)."""
+    ctx, orc, s = setup
+    rng = np.random.default_rng(14)
+    a = residues(rng, ctx.q, (1,), ctx.n)
+    da = ctx.upload(a)
+    rk = ctx.keygen_relin(s, 77)
+    assert np.array_equal(ctx.keyswitch(da, rk).numpy(), orc.keyswitch(a[0], orc.relin_key(s, 77)))
+    g = O.galois_elt(3, ctx.n)
+    gk = ctx.keygen_galois(s, g, 78)
+    ct = residues(rng, ctx.q, (2,), ctx.n)
+    assert np.array_equal(ctx.rotate(ctx.upload(ct), gk, g).numpy(),
+                          orc.rotate(ct, orc.galois_key(s, g, 78), g))
+    pk = ctx.keygen_public(s, 79)
+    assert np.array_equal(pk.numpy(), orc.public_key(s, 79))
+
+
+def test_rotation_decrypts_to_rolled_slots(setup):
+    ctx, orc, s = setup
+    slots = ctx.n // 2
+    scale = float(ctx.q[-1])
+    x = np.random.default_rng(15).uniform(-1, 1, slots)
+    pk = ctx.keygen_public(s, 5)
+    ct = ctx.encrypt(pk, ctx.encode(x, slots, scale, ctx.L), 6)
+    for step in (1, -5):
+        g = F.galois_element(step, ctx.n)
+        out = ctx.rotate(ct, ctx.keygen_galois(s, g, 7), g)
+        got = ctx.decode(ctx.decrypt(out, s), slots, scale).real
+        assert np.abs(got - np.roll(x, -step)).max() < 1e-4
