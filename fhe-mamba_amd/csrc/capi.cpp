@@ -1,6 +1,7 @@
 // extern "C" boundary (include/fhecore.h): handle management, argument and
 // shape validation, and translation of C++ exceptions into status codes plus
 // a thread-local message.  No exception crosses this file's functions.
+#include <algorithm>
 #include <cstring>
 #include <map>
 #include <memory>
@@ -568,11 +569,24 @@ int fhe_rotate_hoisted(const fhe_poly* ct, const fhe_poly* digits, const fhe_key
       need(outs[r] && outs[r]->c == &c && outs[r] != ct, "bad output handle");
       need((galois[r] & 1) && galois[r] < 2 * c.n, "Galois element must be odd and < 2N");
     }
-    fhe::Scratch ext(c, 2 * (size_t)ne * c.n);
-    for (uint32_t r = 0; r < count; ++r) {
-      fhe::ksk_inner(c, digits->data, nq, keys[r]->data, ext.p);
-      prepare_out(outs[r], 2, nq);
-      fhe::moddown_pair2(c, ext.p, nq, outs[r]->data, ct->data, nullptr, galois[r]);
+    for (uint32_t r = 0; r < count; ++r) prepare_out(outs[r], 2, nq);
+    // Rotations are processed in batches that share one read of the digits;
+    // the batch keeps its scratch (ext + y, 2(ne + nq) limbs per rotation)
+    // under 2 GiB.
+    const size_t per_rot = 2 * (size_t)(ne + nq) * c.n * 8;
+    uint32_t batch = (uint32_t)std::max<size_t>(1, (size_t(2) << 30) / per_rot);
+    batch = std::min<uint32_t>(batch, fhe::MAX_KS_BATCH);
+    for (uint32_t r0 = 0; r0 < count; r0 += batch) {
+      const uint32_t b = std::min(batch, count - r0);
+      fhe::Scratch ext(c, (size_t)b * 2 * ne * c.n);
+      std::vector<const uint64_t*> kp(b);
+      std::vector<fhe::KeySwitchOut> ko(b);
+      for (uint32_t r = 0; r < b; ++r) {
+        kp[r] = keys[r0 + r]->data;
+        ko[r] = fhe::KeySwitchOut{outs[r0 + r]->data, ct->data, nullptr, galois[r0 + r]};
+      }
+      fhe::ksk_inner_batch(c, digits->data, nq, kp.data(), b, ext.p);
+      fhe::moddown_batch(c, ext.p, nq, b, ko.data());
     }
   });
 }

@@ -178,8 +178,14 @@ Context::Context(uint32_t log_n_, const uint64_t* q, uint32_t num_q, const uint6
     const uint64_t v = host_invmod(pm, qi);
     pinv[2 * i] = v;
     pinv[2 * i + 1] = host_shoup(v, qi);
+    pinv_host.push_back(v);
   }
   d_pinv_q = upload(pinv);
+
+  std::vector<uint64_t> keyfac(nm);
+  for (uint32_t i = 0; i < nm; ++i)
+    keyfac[i] = i < L ? host_mulmod(pinv_host[i], hconst[i].r2, mods[i]) : hconst[i].r2;
+  d_keyfac = upload(keyfac);
 
   std::vector<uint64_t> garner((size_t)L * L * 2, 0);
   for (uint32_t i = 0; i < L; ++i)
@@ -206,6 +212,7 @@ Context::~Context() {
   hipFree(d_tw_inv);
   hipFree(d_rescale);
   hipFree(d_pinv_q);
+  hipFree(d_keyfac);
   hipFree(d_garner);
   for (auto& kv : fft_tables) {
     hipFree(kv.second.first);
@@ -215,7 +222,8 @@ Context::~Context() {
   if (own_stream && stream) hipStreamDestroy(stream);
 }
 
-ConvPlan* Context::build_plan(const std::vector<uint32_t>& src, const std::vector<uint32_t>& dst) {
+ConvPlan* Context::build_plan(const std::vector<uint32_t>& src, const std::vector<uint32_t>& dst,
+                              const std::vector<uint64_t>* factor) {
   std::unique_ptr<ConvPlan> pl(new ConvPlan);
   pl->nsrc = (uint32_t)src.size();
   pl->ndst = (uint32_t)dst.size();
@@ -235,6 +243,7 @@ ConvPlan* Context::build_plan(const std::vector<uint32_t>& src, const std::vecto
       uint64_t hk = 1 % t;
       for (size_t b = 0; b < src.size(); ++b)
         if (b != a) hk = host_mulmod(hk, mods[src[b]] % t, t);
+      if (factor) hk = host_mulmod(hk, (*factor)[k] % t, t);
       qhat_mont[a * dst.size() + k] = host_to_mont(hk, t);
     }
   }
@@ -273,7 +282,10 @@ const ConvPlan& Context::moddown_plan(uint32_t nq) {
   std::vector<uint32_t> src, dst;
   for (uint32_t k = 0; k < K; ++k) src.push_back(L + k);
   for (uint32_t i = 0; i < nq; ++i) dst.push_back(i);
-  ConvPlan* raw = build_plan(src, dst);
+  // ModDown subtracts the conversion and multiplies by P^-1: fold -P^-1 in.
+  std::vector<uint64_t> neg_pinv(nq);
+  for (uint32_t i = 0; i < nq; ++i) neg_pinv[i] = pinv_host[i] ? mods[i] - pinv_host[i] : 0;
+  ConvPlan* raw = build_plan(src, dst, &neg_pinv);
   auto node = plans.extract({(uint64_t)raw, (uint64_t)raw});
   node.key() = {key1, key2};
   plans.insert(std::move(node));

@@ -118,6 +118,11 @@ struct Context {
   uint64_t* d_rescale = nullptr;     // [L][L][4]
   // ModDown: P^-1 mod q_i (value, Shoup)
   uint64_t* d_pinv_q = nullptr;      // [L][2]
+  std::vector<uint64_t> pinv_host;   // [L] P^-1 mod q_i
+  // Key words are stored as k * f_i * 2^-64 with f_i = 2^128 * P^-1 (Q limbs)
+  // or 2^128 (P limbs) mod the limb's modulus: Montgomery form with P^-1
+  // folded into the Q limbs, so the key inner product yields ext * P^-1.
+  uint64_t* d_keyfac = nullptr;      // [L+K]
 
   // Garner CRT inverses g[i][j] = (q_j^-1 mod q_i, Shoup) for j < i (decode).
   uint64_t* d_garner = nullptr;      // [L][L][2]
@@ -144,7 +149,9 @@ struct Context {
   void release(void* p, size_t bytes) { pool->put(p, bytes); }
 
  private:
-  ConvPlan* build_plan(const std::vector<uint32_t>& src, const std::vector<uint32_t>& dst);
+  // factor (optional, per target) multiplies every constant of target k.
+  ConvPlan* build_plan(const std::vector<uint32_t>& src, const std::vector<uint32_t>& dst,
+                       const std::vector<uint64_t>* factor = nullptr);
 };
 
 // Limb -> modulus index map for a batch of limbs: limb j < split uses
@@ -154,7 +161,7 @@ struct LimbMap {
   FHE_HD uint32_t operator()(uint32_t j) const {
     return j < split ? base0 + j : base1 + (j - split);
   }
-  static LimbMap contiguous(uint32_t limb0) { return LimbMap{0xffffffffu, limb0, 0}; }
+  static FHE_HD LimbMap contiguous(uint32_t limb0) { return LimbMap{0xffffffffu, limb0, 0}; }
 };
 
 // Stream-ordered scratch buffer from the context pool.  Released back to the
@@ -198,10 +205,31 @@ struct LaunchScope {
     ::fhe::hip_check(hipGetLastError(), name);                                      \
   } while (0)
 
+// Epilogue of the last forward-NTT pass of a batched ModDown.  Launch poly p
+// is key switch r = p / 2, component b = p % 2.  ext's Q limbs already carry
+// the factor P^-1 (folded into the stored keys) and y carries -P^-1 (folded
+// into the ModDown conversion constants), so
+//   out_r[b][i][d(s)] = ext_r[b][i][s] + y[s] + add_r,b[i][s]
+// equals OpenFHE's (ext - Conv(ext_P)) * P^-1 + add exactly.
+// where d is the inverse of the Galois permutation of element g_r
+// (ginv = g_r^-1 mod 2N; 1 means no permutation).
+constexpr int MAX_KS_BATCH = 32;
+struct ModDownEpi {
+  const uint64_t* ext;                    // [B][2][ne][N]
+  uint64_t* out[MAX_KS_BATCH];            // each [2][nq][N]
+  const uint64_t* add[MAX_KS_BATCH][2];   // [nq][N] or null
+  uint32_t ginv[MAX_KS_BATCH];
+  uint32_t ne, nq;
+};
+
 // ---- kernel launchers (implemented in the .hip files) ----
 void ntt_forward(Context& c, uint64_t* data, uint32_t npoly, size_t poly_stride,
                  uint32_t nlimb, LimbMap map);
 void ntt_inverse(Context& c, uint64_t* data, uint32_t npoly, size_t poly_stride,
                  uint32_t nlimb, LimbMap map);
+// Forward NTT of y [npoly][nq][N] (limb j mod q_j) whose last pass stores
+// through the ModDown epilogue instead of writing y back.
+void ntt_forward_moddown(Context& c, uint64_t* y, uint32_t npoly, uint32_t nq,
+                         const ModDownEpi& epi);
 
 }  // namespace fhe

@@ -72,72 +72,173 @@ __global__ void __launch_bounds__(TPB)
   }
 }
 
-// Key inner product.  grid (N / (2 blockDim), nq + K, 1).
+// Fast basis conversion, specialised for NSRC source limbs and moduli below
+// 2^60.  Operands are split at bit 30 (v = vh 2^30 + vl, c = ch 2^30 + cl,
+// all halves < 2^30), so each 60x60-bit product is four 32x32->64 partial
+// products accumulated with v_mad_u64_u32 and no carries: for NSRC <= 16
+// every partial sum stays below 2^64.  The 128-bit total
+//   T = A0 + (A1a + A1b) 2^30 + A2 2^60 < NSRC * 2^60 * t_k <= t_k * 2^64
+// is reduced by one REDC against the Montgomery-form constants.
+// grid (N / blockDim, ceil(ndst / tch), npoly): each thread converts one
+// coefficient for `tch` consecutive targets.
+template <int NSRC>
 __global__ void __launch_bounds__(TPB)
-    k_ksk_inner(const uint64_t* __restrict__ digits, const uint64_t* __restrict__ key,
-                uint64_t* __restrict__ ext, const ModConst* __restrict__ mc, uint32_t n,
-                uint32_t nq, uint32_t L, uint32_t K, uint32_t nd, uint32_t chunk) {
+    k_convert60(const uint64_t* __restrict__ src, size_t src_ps, uint64_t* __restrict__ out,
+                size_t out_ps, const ModConst* __restrict__ mc,
+                const uint32_t* __restrict__ src_idx, const uint64_t* __restrict__ qhat_inv,
+                const uint64_t* __restrict__ qhat_mont, const uint32_t* __restrict__ dst_idx,
+                uint32_t ndst, uint32_t n, uint32_t L, uint32_t out_nq, uint32_t tch) {
+  constexpr uint32_t M30 = (1u << 30) - 1;
+  const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const uint64_t* s = src + (size_t)blockIdx.z * src_ps;
+  uint64_t* o = out + (size_t)blockIdx.z * out_ps;
+  uint32_t vl[NSRC], vh[NSRC];
+#pragma unroll
+  for (int i = 0; i < NSRC; ++i) {
+    const uint64_t q = mc[src_idx[i]].q;
+    const uint64_t v = shoup(s[(size_t)i * n + e], qhat_inv[2 * i], qhat_inv[2 * i + 1], q);
+    vl[i] = (uint32_t)v & M30;
+    vh[i] = (uint32_t)(v >> 30);
+  }
+  const uint32_t k0 = blockIdx.y * tch, k1 = k0 + tch < ndst ? k0 + tch : ndst;
+  for (uint32_t k = k0; k < k1; ++k) {
+    uint64_t a0 = 0, a1a = 0, a1b = 0, a2 = 0;
+#pragma unroll
+    for (int i = 0; i < NSRC; ++i) {
+      const uint64_t c = qhat_mont[(size_t)i * ndst + k];
+      const uint32_t cl = (uint32_t)c & M30, ch = (uint32_t)(c >> 30);
+      a0 += (uint64_t)vl[i] * cl;
+      a1a += (uint64_t)vl[i] * ch;
+      a1b += (uint64_t)vh[i] * cl;
+      a2 += (uint64_t)vh[i] * ch;
+    }
+    const uint64_t s1 = a1a + a1b;
+    const uint64_t c1 = s1 < a1a;
+    const uint64_t m1 = s1 << 30, m2 = a2 << 60;
+    uint64_t lo = a0 + m1;
+    uint64_t hi = (s1 >> 34) + (c1 << 30) + (a2 >> 4) + (lo < m1);
+    const uint64_t lo2 = lo + m2;
+    hi += lo2 < m2;
+    lo = lo2;
+    const uint32_t dm = dst_idx[k];
+    const uint32_t pos = dm < L ? dm : out_nq + (dm - L);
+    o[(size_t)pos * n + e] = redc(hi, lo, mc[dm].q, mc[dm].qinv_neg);
+  }
+}
+
+// Key inner product for a batch of B key switches sharing one set of
+// digits (a hoisted rotation set): each thread loads its digit words once
+// and reuses them for every key.  grid (N / (2 blockDim), nq + K, 1).
+// ext is [B][2][ne][N].
+constexpr int MAXD = 8;
+struct KeyBatch {
+  const uint64_t* key[MAX_KS_BATCH];
+};
+
+// Specialisation for ND digits whose sum of products fits one REDC
+// (ND * max q < 2^64): rotations are taken two at a time so twelve 16-byte
+// key loads are in flight per thread before any product.
+template <int ND>
+__global__ void __launch_bounds__(TPB)
+    k_ksk_inner_nd(const uint64_t* __restrict__ digits, const KeyBatch kb,
+                   uint64_t* __restrict__ ext, const ModConst* __restrict__ mc, uint32_t n,
+                   uint32_t nq, uint32_t L, uint32_t K, uint32_t batch) {
   const uint32_t i = blockIdx.y, ne = nq + K;
   const uint32_t ki = i < nq ? i : L + (i - nq);
   const uint64_t q = mc[ki].q, qinv = mc[ki].qinv_neg;
   const size_t e = 2 * ((size_t)blockIdx.x * blockDim.x + threadIdx.x);
-  const size_t kl = (size_t)(L + K) * n;  // key limb-set stride
-  uint64_t r0x = 0, r0y = 0, r1x = 0, r1y = 0;
-  uint32_t j0 = 0;
-  while (j0 < nd) {
-    const uint32_t j1 = j0 + chunk < nd ? j0 + chunk : nd;
+  const size_t kl = (size_t)(L + K) * n;
+  ulonglong2 d[ND];
+#pragma unroll
+  for (int j = 0; j < ND; ++j)
+    d[j] = *reinterpret_cast<const ulonglong2*>(digits + ((size_t)j * ne + i) * n + e);
+  auto finish = [&](const ulonglong2 (&kb2)[ND], const ulonglong2 (&ka2)[ND], uint32_t r) {
     Acc128 a0x, a0y, a1x, a1y;
-    for (uint32_t j = j0; j < j1; ++j) {
-      const ulonglong2 d = *reinterpret_cast<const ulonglong2*>(digits + ((size_t)j * ne + i) * n + e);
-      const uint64_t* kb = key + ((size_t)j * 2) * kl + (size_t)ki * n + e;
-      const ulonglong2 b = *reinterpret_cast<const ulonglong2*>(kb);
-      const ulonglong2 a = *reinterpret_cast<const ulonglong2*>(kb + kl);
-      a0x.mac(d.x, b.x);
-      a0y.mac(d.y, b.y);
-      a1x.mac(d.x, a.x);
-      a1y.mac(d.y, a.y);
+#pragma unroll
+    for (int j = 0; j < ND; ++j) {
+      a0x.mac(d[j].x, kb2[j].x);
+      a0y.mac(d[j].y, kb2[j].y);
+      a1x.mac(d[j].x, ka2[j].x);
+      a1y.mac(d[j].y, ka2[j].y);
     }
-    r0x = add_mod(r0x, redc(a0x.hi, a0x.lo, q, qinv), q);
-    r0y = add_mod(r0y, redc(a0y.hi, a0y.lo, q, qinv), q);
-    r1x = add_mod(r1x, redc(a1x.hi, a1x.lo, q, qinv), q);
-    r1y = add_mod(r1y, redc(a1y.hi, a1y.lo, q, qinv), q);
-    j0 = j1;
+    uint64_t* o = ext + (size_t)r * 2 * ne * n;
+    *reinterpret_cast<ulonglong2*>(o + (size_t)i * n + e) =
+        make_ulonglong2(redc(a0x.hi, a0x.lo, q, qinv), redc(a0y.hi, a0y.lo, q, qinv));
+    *reinterpret_cast<ulonglong2*>(o + ((size_t)ne + i) * n + e) =
+        make_ulonglong2(redc(a1x.hi, a1x.lo, q, qinv), redc(a1y.hi, a1y.lo, q, qinv));
+  };
+  uint32_t r = 0;
+  for (; r + 2 <= batch; r += 2) {
+    ulonglong2 b0[ND], a0[ND], b1[ND], a1[ND];
+    const uint64_t* k0 = kb.key[r] + (size_t)ki * n + e;
+    const uint64_t* k1 = kb.key[r + 1] + (size_t)ki * n + e;
+#pragma unroll
+    for (int j = 0; j < ND; ++j) {
+      b0[j] = *reinterpret_cast<const ulonglong2*>(k0 + (size_t)j * 2 * kl);
+      a0[j] = *reinterpret_cast<const ulonglong2*>(k0 + (size_t)j * 2 * kl + kl);
+      b1[j] = *reinterpret_cast<const ulonglong2*>(k1 + (size_t)j * 2 * kl);
+      a1[j] = *reinterpret_cast<const ulonglong2*>(k1 + (size_t)j * 2 * kl + kl);
+    }
+    finish(b0, a0, r);
+    finish(b1, a1, r + 1);
   }
-  *reinterpret_cast<ulonglong2*>(ext + (size_t)i * n + e) = make_ulonglong2(r0x, r0y);
-  *reinterpret_cast<ulonglong2*>(ext + ((size_t)ne + i) * n + e) = make_ulonglong2(r1x, r1y);
+  if (r < batch) {
+    ulonglong2 b0[ND], a0[ND];
+    const uint64_t* k0 = kb.key[r] + (size_t)ki * n + e;
+#pragma unroll
+    for (int j = 0; j < ND; ++j) {
+      b0[j] = *reinterpret_cast<const ulonglong2*>(k0 + (size_t)j * 2 * kl);
+      a0[j] = *reinterpret_cast<const ulonglong2*>(k0 + (size_t)j * 2 * kl + kl);
+    }
+    finish(b0, a0, r);
+  }
+}
+
+__global__ void __launch_bounds__(TPB)
+    k_ksk_inner_batch(const uint64_t* __restrict__ digits, const KeyBatch kb,
+                      uint64_t* __restrict__ ext, const ModConst* __restrict__ mc, uint32_t n,
+                      uint32_t nq, uint32_t L, uint32_t K, uint32_t nd, uint32_t chunk,
+                      uint32_t batch) {
+  const uint32_t i = blockIdx.y, ne = nq + K;
+  const uint32_t ki = i < nq ? i : L + (i - nq);
+  const uint64_t q = mc[ki].q, qinv = mc[ki].qinv_neg;
+  const size_t e = 2 * ((size_t)blockIdx.x * blockDim.x + threadIdx.x);
+  const size_t kl = (size_t)(L + K) * n;
+  ulonglong2 d[MAXD];
+#pragma unroll
+  for (int j = 0; j < MAXD; ++j)
+    if (j < (int)nd) d[j] = *reinterpret_cast<const ulonglong2*>(digits + ((size_t)j * ne + i) * n + e);
+  for (uint32_t r = 0; r < batch; ++r) {
+    const uint64_t* key = kb.key[r] + (size_t)ki * n + e;
+    uint64_t r0x = 0, r0y = 0, r1x = 0, r1y = 0;
+    uint32_t j0 = 0;
+    while (j0 < nd) {
+      const uint32_t j1 = j0 + chunk < nd ? j0 + chunk : nd;
+      Acc128 a0x, a0y, a1x, a1y;
+#pragma unroll
+      for (int j = 0; j < MAXD; ++j) {
+        if (j < (int)j0 || j >= (int)j1) continue;
+        const ulonglong2 b = *reinterpret_cast<const ulonglong2*>(key + (size_t)j * 2 * kl);
+        const ulonglong2 a = *reinterpret_cast<const ulonglong2*>(key + (size_t)j * 2 * kl + kl);
+        a0x.mac(d[j].x, b.x);
+        a0y.mac(d[j].y, b.y);
+        a1x.mac(d[j].x, a.x);
+        a1y.mac(d[j].y, a.y);
+      }
+      r0x = add_mod(r0x, redc(a0x.hi, a0x.lo, q, qinv), q);
+      r0y = add_mod(r0y, redc(a0y.hi, a0y.lo, q, qinv), q);
+      r1x = add_mod(r1x, redc(a1x.hi, a1x.lo, q, qinv), q);
+      r1y = add_mod(r1y, redc(a1y.hi, a1y.lo, q, qinv), q);
+      j0 = j1;
+    }
+    uint64_t* o = ext + (size_t)r * 2 * ne * n;
+    *reinterpret_cast<ulonglong2*>(o + (size_t)i * n + e) = make_ulonglong2(r0x, r0y);
+    *reinterpret_cast<ulonglong2*>(o + ((size_t)ne + i) * n + e) = make_ulonglong2(r1x, r1y);
+  }
 }
 
 __device__ __forceinline__ uint32_t brev_bits(uint32_t x, uint32_t bits) {
   return __brev(x) >> (32 - bits);
-}
-
-// ModDown combine with optional addends and Galois permutation.
-//   out_b[i][x] = ((ext_b[i][s] - y_b[i][s]) * P^-1 + add_b[i][s]) mod q_i,
-//   s = the evaluation slot that X -> X^galois moves to x (s = x if galois
-//   is 1).  grid (N / blockDim, nq, 2).
-__global__ void __launch_bounds__(TPB)
-    k_moddown_combine(uint64_t* __restrict__ out, const uint64_t* __restrict__ ext,
-                      const uint64_t* __restrict__ y, const uint64_t* __restrict__ add0,
-                      const uint64_t* __restrict__ add1, const ModConst* __restrict__ mc,
-                      const uint64_t* __restrict__ pinv, uint32_t n, uint32_t log_n, uint32_t nq,
-                      uint32_t K, uint32_t galois) {
-  const uint32_t i = blockIdx.y, b = blockIdx.z;
-  const uint64_t q = mc[i].q, pi = pinv[2 * i], pis = pinv[2 * i + 1];
-  const uint32_t x = blockIdx.x * blockDim.x + threadIdx.x;
-  uint32_t s = x;
-  if (galois != 1) {
-    const uint32_t j = brev_bits(x, log_n);
-    const uint32_t m2 = 2 * n;
-    const uint32_t ex = (uint32_t)(((2ull * j + 1) * galois) & (m2 - 1));
-    s = brev_bits((ex - 1) >> 1, log_n);
-  }
-  const size_t ne = nq + K;
-  const uint64_t ev = ext[((size_t)b * ne + i) * n + s];
-  const uint64_t yv = y[((size_t)b * nq + i) * n + s];
-  uint64_t r = shoup(ev + q - yv, pi, pis, q);
-  const uint64_t* add = b == 0 ? add0 : add1;
-  if (add) r = add_mod(r, add[(size_t)i * n + s], q);
-  out[((size_t)b * nq + i) * n + x] = r;
 }
 
 // Galois permutation of evaluation-form limbs (no key switching).
@@ -156,11 +257,11 @@ __global__ void __launch_bounds__(TPB)
 // Key words to Montgomery form: k * 2^64 mod q = REDC(k * (2^128 mod q)).
 // grid (N / blockDim, L + K, dnum * 2).
 __global__ void __launch_bounds__(TPB)
-    k_to_mont(uint64_t* key, const ModConst* mc, uint32_t n, uint32_t nm) {
+    k_to_mont(uint64_t* key, const ModConst* mc, const uint64_t* fac, uint32_t n, uint32_t nm) {
   const uint32_t i = blockIdx.y;
   const ModConst m = mc[i];
   const size_t o = ((size_t)blockIdx.z * nm + i) * n + (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  key[o] = mont_mul(key[o], m.r2, m.q, m.qinv_neg);
+  key[o] = mont_mul(key[o], fac[i], m.q, m.qinv_neg);
 }
 
 // Terms per REDC so that terms * max_q < 2^64.
@@ -172,9 +273,34 @@ uint32_t redc_chunk(const Context& c, const std::vector<uint32_t>& idx) {
   return (uint32_t)(ch < 1 ? 1 : ch);
 }
 
+bool below_2_60(const Context& c, const std::vector<uint32_t>& idx) {
+  for (uint32_t i : idx)
+    if (c.mods[i] >= (1ull << 60)) return false;
+  return true;
+}
+
+template <int NSRC>
+void launch_convert60(Context& c, const ConvPlan& pl, const uint64_t* src, size_t src_ps,
+                      uint64_t* out, size_t out_ps, uint32_t out_nq, uint32_t npoly) {
+  const uint32_t tpb = tpb_for(c, 1), tch = 4;
+  FHE_LAUNCH(c, "k_convert", k_convert60<NSRC>, dim3(c.n / tpb, (pl.ndst + tch - 1) / tch, npoly),
+             dim3(tpb), 0, src, src_ps, out, out_ps, c.d_const, pl.d_src_idx32, pl.d_qhat_inv,
+             pl.d_qhat_mont, pl.d_dst_idx, pl.ndst, c.n, c.L, out_nq, tch);
+}
+
 void convert(Context& c, const ConvPlan& pl, const uint64_t* src, size_t src_ps, uint64_t* out,
              size_t out_ps, uint32_t out_nq, uint32_t npoly) {
   if (pl.nsrc > MAXSRC) throw ArgError("basis conversion source larger than 16 limbs");
+  if (below_2_60(c, pl.src_idx) && below_2_60(c, pl.dst_idx)) {
+    switch (pl.nsrc) {
+#define CASE(S) \
+  case S: launch_convert60<S>(c, pl, src, src_ps, out, out_ps, out_nq, npoly); return;
+      CASE(1) CASE(2) CASE(3) CASE(4) CASE(5) CASE(6) CASE(7) CASE(8)
+      CASE(9) CASE(10) CASE(11) CASE(12) CASE(13) CASE(14) CASE(15) CASE(16)
+#undef CASE
+      default: break;
+    }
+  }
   const uint32_t tpb = tpb_for(c, 1);
   FHE_LAUNCH(c, "k_convert", k_convert, dim3(c.n / tpb, 1, npoly), dim3(tpb), 0, src, src_ps, out, out_ps, c.d_const, pl.d_src_idx32, pl.d_qhat_inv, pl.d_qhat_mont, pl.d_dst_idx, pl.nsrc, pl.ndst, c.n, c.L, out_nq, redc_chunk(c, pl.src_idx));
 }
@@ -206,30 +332,79 @@ void modup(Context& c, const uint64_t* a, uint32_t nq, uint64_t* digits) {
   }
 }
 
-void ksk_inner(Context& c, const uint64_t* digits, uint32_t nq, const uint64_t* key_mont,
-               uint64_t* ext) {
+void ksk_inner_batch(Context& c, const uint64_t* digits, uint32_t nq, const uint64_t* const* keys,
+                     uint32_t batch, uint64_t* ext) {
+  if (batch == 0) return;
+  if (batch > MAX_KS_BATCH) throw ArgError("key-switch batch too large");
   const uint32_t nd = num_digits(c, nq);
+  if (nd > MAXD) throw ArgError("more than 8 key-switching digits");
   std::vector<uint32_t> all(c.L + c.K);
   for (uint32_t i = 0; i < c.L + c.K; ++i) all[i] = i;
+  KeyBatch kb{};
+  for (uint32_t r = 0; r < batch; ++r) kb.key[r] = keys[r];
   const uint32_t tpb = tpb_for(c, 2);
-  FHE_LAUNCH(c, "k_ksk_inner", k_ksk_inner, dim3(c.n / (2 * tpb), nq + c.K, 1), dim3(tpb), 0, digits, key_mont, ext, c.d_const, c.n, nq, c.L, c.K, nd, redc_chunk(c, all));
+  const dim3 grid(c.n / (2 * tpb), nq + c.K, 1);
+  if (nd <= redc_chunk(c, all)) {
+    switch (nd) {
+#define CASE(D)                                                                                \
+  case D:                                                                                      \
+    FHE_LAUNCH(c, "k_ksk_inner", k_ksk_inner_nd<D>, grid, dim3(tpb), 0, digits, kb, ext,      \
+               c.d_const, c.n, nq, c.L, c.K, batch);                                           \
+    return;
+      CASE(1) CASE(2) CASE(3) CASE(4) CASE(5) CASE(6) CASE(7) CASE(8)
+#undef CASE
+      default: break;
+    }
+  }
+  FHE_LAUNCH(c, "k_ksk_inner", k_ksk_inner_batch, dim3(c.n / (2 * tpb), nq + c.K, 1), dim3(tpb), 0,
+             digits, kb, ext, c.d_const, c.n, nq, c.L, c.K, nd, redc_chunk(c, all), batch);
 }
 
-void moddown_pair(Context& c, const uint64_t* ext, uint32_t nq, uint64_t* out,
-                  const uint64_t* add0, uint32_t galois) {
-  moddown_pair2(c, ext, nq, out, add0, nullptr, galois);
+uint32_t galois_inverse(const Context& c, uint32_t g) {
+  if (g == 1) return 1;
+  const uint64_t m = 2ull * c.n;
+  for (uint64_t t = 1; t < m; t += 2)
+    if ((t * g) % m == 1) return (uint32_t)t;
+  throw ArgError("Galois element is not a unit mod 2N");
 }
 
-void moddown_pair2(Context& c, const uint64_t* ext, uint32_t nq, uint64_t* out,
-                   const uint64_t* add0, const uint64_t* add1, uint32_t galois) {
+void moddown_batch(Context& c, uint64_t* ext, uint32_t nq, uint32_t batch,
+                   const KeySwitchOut* outs) {
+  if (batch == 0) return;
+  if (batch > MAX_KS_BATCH) throw ArgError("key-switch batch too large");
   const size_t n = c.n, ne = nq + c.K;
-  Scratch pc(c, 2 * (size_t)c.K * n), y(c, 2 * (size_t)nq * n);
-  poly_copy_limbs(c, pc.p, c.K, ext + (size_t)nq * n, (uint32_t)ne, 2, c.K);
-  ntt_inverse(c, pc.p, 2, (size_t)c.K * n, c.K, LimbMap::contiguous(c.L));
-  convert(c, c.moddown_plan(nq), pc.p, (size_t)c.K * n, y.p, (size_t)nq * n, nq, 2);
-  ntt_forward(c, y.p, 2, (size_t)nq * n, nq, LimbMap::contiguous(0));
-  const uint32_t tpb = tpb_for(c, 1);
-  FHE_LAUNCH(c, "k_moddown_combine", k_moddown_combine, dim3(c.n / tpb, nq, 2), dim3(tpb), 0, out, ext, y.p, add0, add1, c.d_const, c.d_pinv_q, c.n, c.log_n, nq, c.K, galois);
+  Scratch y(c, 2 * (size_t)batch * nq * n);
+  // The P limbs of ext are taken to coefficient form in place (ext is scratch).
+  ntt_inverse(c, ext + (size_t)nq * n, 2 * batch, ne * n, c.K, LimbMap::contiguous(c.L));
+  convert(c, c.moddown_plan(nq), ext + (size_t)nq * n, ne * n, y.p, (size_t)nq * n, nq,
+          2 * batch);
+  ModDownEpi epi{};
+  epi.ext = ext;
+  epi.ne = (uint32_t)ne;
+  epi.nq = nq;
+  for (uint32_t r = 0; r < batch; ++r) {
+    epi.out[r] = outs[r].out;
+    epi.add[r][0] = outs[r].add0;
+    epi.add[r][1] = outs[r].add1;
+    epi.ginv[r] = galois_inverse(c, outs[r].galois);
+  }
+  ntt_forward_moddown(c, y.p, 2 * batch, nq, epi);
+}
+
+void ksk_inner(Context& c, const uint64_t* digits, uint32_t nq, const uint64_t* key_mont,
+               uint64_t* ext) {
+  ksk_inner_batch(c, digits, nq, &key_mont, 1, ext);
+}
+
+void moddown_pair2(Context& c, uint64_t* ext, uint32_t nq, uint64_t* out, const uint64_t* add0,
+                   const uint64_t* add1, uint32_t galois) {
+  const KeySwitchOut o{out, add0, add1, galois};
+  moddown_batch(c, ext, nq, 1, &o);
+}
+
+void moddown_pair(Context& c, uint64_t* ext, uint32_t nq, uint64_t* out, const uint64_t* add0,
+                  uint32_t galois) {
+  moddown_pair2(c, ext, nq, out, add0, nullptr, galois);
 }
 
 void automorph(Context& c, uint64_t* out, const uint64_t* in, uint32_t npoly, uint32_t nlimb,
@@ -240,7 +415,7 @@ void automorph(Context& c, uint64_t* out, const uint64_t* in, uint32_t npoly, ui
 
 void key_to_montgomery(Context& c, uint64_t* key) {
   const uint32_t tpb = tpb_for(c, 1);
-  FHE_LAUNCH(c, "k_to_mont", k_to_mont, dim3(c.n / tpb, c.L + c.K, c.dnum * 2), dim3(tpb), 0, key, c.d_const, c.n, c.L + c.K);
+  FHE_LAUNCH(c, "k_to_mont", k_to_mont, dim3(c.n / tpb, c.L + c.K, c.dnum * 2), dim3(tpb), 0, key, c.d_const, c.d_keyfac, c.n, c.L + c.K);
 }
 
 }  // namespace fhe

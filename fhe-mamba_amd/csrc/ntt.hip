@@ -45,11 +45,13 @@ __device__ __forceinline__ uint32_t lds_idx(uint32_t line, uint32_t u, uint32_t 
   return line * pitch + u + (u >> 4);
 }
 
-template <int S, int KIND, bool INV>
-__global__ void __launch_bounds__(256)
-    ntt_pass(uint64_t* __restrict__ data, size_t poly_stride, const ModConst* __restrict__ mc,
-             const uint64_t* __restrict__ tw_all, uint32_t log_n, LimbMap map, uint32_t s_other,
-             int last) {
+// Final stores go through `store(base, offset_in_limb, value, q)`.
+template <int S, int KIND, bool INV, class Store>
+__device__ __forceinline__ void ntt_body(uint64_t* __restrict__ data, size_t poly_stride,
+                                         const ModConst* __restrict__ mc,
+                                         const uint64_t* __restrict__ tw_all, uint32_t log_n,
+                                         LimbMap map, uint32_t s_other, int last,
+                                         const Store& store) {
   using G = Geo<S>;
   constexpr int LINES = KIND == SINGLE ? 1 : 256 / G::TPL;
   constexpr int NSP = (S + RHO - 1) / RHO;
@@ -93,8 +95,25 @@ __global__ void __launch_bounds__(256)
       bhi = lo + RHO <= S ? lo + RHO - 1 : S - 1;
     }
     const uint32_t thi = (tau >> w) << (w + RHO), tlo = tau & ((1u << w) - 1);
+    // In BLOCKS / SINGLE launches a window at bit 0 gives each thread 16
+    // consecutive words; global traffic for such a window goes through LDS
+    // so that lanes touch consecutive addresses.
+    const bool contiguous = KIND != COLS && w == 0;
 
-    if (sp == 0) {
+    if (sp == 0 && contiguous) {
+      const size_t wg0 = ((size_t)blockIdx.x * LINES) << S;
+#pragma unroll
+      for (int k = 0; k < R; ++k) {
+        const uint32_t p = k * blockDim.x + tid;
+        lds[lds_idx(p >> S, p & (G::LEN - 1), G::PITCH)] = base[wg0 + p];
+      }
+      __syncthreads();
+#pragma unroll
+      for (int v = 0; v < R; ++v) {
+        const uint32_t u = thi | ((uint32_t)v << w) | tlo;
+        x[v] = lds[lds_idx(line, u, G::PITCH)];
+      }
+    } else if (sp == 0) {
 #pragma unroll
       for (int v = 0; v < R; ++v) {
         const uint32_t u = thi | ((uint32_t)v << w) | tlo;
@@ -157,14 +176,31 @@ __global__ void __launch_bounds__(256)
           for (int v = 0; v < R; ++v) x[v] = reduce_2q(shoup_lazy(x[v], ni, nis, q), q);
         }
       }
+      if (contiguous) {
+        if (sp > 0 || NSP == 1) __syncthreads();
 #pragma unroll
-      for (int v = 0; v < R; ++v) {
-        const uint32_t u = thi | ((uint32_t)v << w) | tlo;
-        const size_t g = KIND == COLS ? gline + ((size_t)u << s_other) : ((size_t)gline << S) + u;
-        base[g] = x[v];
+        for (int v = 0; v < R; ++v) {
+          const uint32_t u = thi | ((uint32_t)v << w) | tlo;
+          lds[lds_idx(line, u, G::PITCH)] = x[v];
+        }
+        __syncthreads();
+        const size_t wg0 = ((size_t)blockIdx.x * LINES) << S;
+#pragma unroll
+        for (int k = 0; k < R; ++k) {
+          const uint32_t p = k * blockDim.x + tid;
+          store(base, wg0 + p, lds[lds_idx(p >> S, p & (G::LEN - 1), G::PITCH)], q);
+        }
+      } else {
+#pragma unroll
+        for (int v = 0; v < R; ++v) {
+          const uint32_t u = thi | ((uint32_t)v << w) | tlo;
+          const size_t g =
+              KIND == COLS ? gline + ((size_t)u << s_other) : ((size_t)gline << S) + u;
+          store(base, g, x[v], q);
+        }
       }
     } else {
-      if (sp > 0) __syncthreads();
+      if (sp > 0 || (KIND != COLS && INV)) __syncthreads();
 #pragma unroll
       for (int v = 0; v < R; ++v) {
         const uint32_t u = thi | ((uint32_t)v << w) | tlo;
@@ -172,6 +208,58 @@ __global__ void __launch_bounds__(256)
       }
     }
   }
+}
+
+struct PlainStore {
+  __device__ __forceinline__ void operator()(uint64_t* base, size_t g, uint64_t v,
+                                             uint64_t) const {
+    base[g] = v;
+  }
+};
+
+__device__ __forceinline__ uint32_t brev_bits(uint32_t x, uint32_t bits) {
+  return __brev(x) >> (32 - bits);
+}
+
+// ModDown epilogue (see ModDownEpi): the value at evaluation slot s goes to
+// slot d(s) of the output, d being the inverse Galois permutation.
+struct EpiStore {
+  const ModDownEpi& e;
+  uint32_t n, log_n;
+  __device__ __forceinline__ void operator()(uint64_t*, size_t s, uint64_t y, uint64_t q) const {
+    const uint32_t p = blockIdx.y, r = p >> 1, b = p & 1, i = blockIdx.z;
+    const uint64_t ev = e.ext[((size_t)p * e.ne + i) * n + s];
+    uint64_t res = add_mod(ev, y, q);
+    const uint64_t* add = e.add[r][b];
+    if (add) res = add_mod(res, add[(size_t)i * n + s], q);
+    uint32_t d = (uint32_t)s;
+    const uint32_t gi = e.ginv[r];
+    if (gi != 1) {
+      // 32-bit wrap-around is exact here: only the product mod 2N matters.
+      const uint32_t j = brev_bits((uint32_t)s, log_n);
+      const uint32_t ex = ((2u * j + 1u) * gi) & (2u * n - 1u);
+      d = brev_bits((ex - 1u) >> 1, log_n);
+    }
+    e.out[r][((size_t)b * e.nq + i) * n + d] = res;
+  }
+};
+
+template <int S, int KIND, bool INV>
+__global__ void __launch_bounds__(256)
+    ntt_pass(uint64_t* __restrict__ data, size_t poly_stride, const ModConst* __restrict__ mc,
+             const uint64_t* __restrict__ tw_all, uint32_t log_n, LimbMap map, uint32_t s_other,
+             int last) {
+  ntt_body<S, KIND, INV>(data, poly_stride, mc, tw_all, log_n, map, s_other, last, PlainStore{});
+}
+
+// Last forward pass of a batched ModDown (BLOCKS or SINGLE kind).
+template <int S, int KIND>
+__global__ void __launch_bounds__(256)
+    ntt_pass_moddown(uint64_t* __restrict__ data, size_t poly_stride,
+                     const ModConst* __restrict__ mc, const uint64_t* __restrict__ tw_all,
+                     uint32_t log_n, uint32_t s_other, const ModDownEpi epi) {
+  ntt_body<S, KIND, false>(data, poly_stride, mc, tw_all, log_n, LimbMap::contiguous(0), s_other,
+                           1, EpiStore{epi, 1u << log_n, log_n});
 }
 
 template <int S, int KIND, bool INV>
@@ -225,7 +313,43 @@ void launch_blocks(Context& c, uint32_t s1, uint32_t s2, uint64_t* data, uint32_
   }
 }
 
+template <int S, int KIND>
+void launch_moddown(Context& c, uint64_t* y, uint32_t npoly, uint32_t nq, uint32_t s_other,
+                    const ModDownEpi& epi) {
+  using G = Geo<S>;
+  const uint32_t lines = KIND == SINGLE ? 1 : 256 / G::TPL;
+  const uint32_t threads = KIND == SINGLE ? G::TPL : 256;
+  const uint32_t tiles = KIND == SINGLE ? 1 : (1u << s_other) / lines;
+  FHE_LAUNCH(c, KIND == SINGLE ? "ntt_fwd_single_moddown" : "ntt_fwd_blocks_moddown",
+             (ntt_pass_moddown<S, KIND>), dim3(tiles, npoly, nq), dim3(threads), 0, y,
+             (size_t)nq * c.n, c.d_const, c.d_tw_fwd, c.log_n, s_other, epi);
+}
+
 }  // namespace
+
+void ntt_forward_moddown(Context& c, uint64_t* y, uint32_t npoly, uint32_t nq,
+                         const ModDownEpi& epi) {
+  if (npoly == 0 || nq == 0) return;
+  if (npoly > 2 * MAX_KS_BATCH) throw ArgError("ModDown batch too large");
+  if (c.log_n <= 12) {
+    switch (c.log_n) {
+#define CASE(S) \
+  case S: launch_moddown<S, SINGLE>(c, y, npoly, nq, 0, epi); return;
+      CASE(4) CASE(5) CASE(6) CASE(7) CASE(8) CASE(9) CASE(10) CASE(11) CASE(12)
+#undef CASE
+      default: throw ArgError("unsupported ring dimension");
+    }
+  }
+  const uint32_t s1 = (c.log_n + 1) / 2, s2 = c.log_n / 2;
+  launch_cols<false>(c, s1, s2, y, npoly, (size_t)nq * c.n, nq, LimbMap::contiguous(0), false);
+  switch (s2) {
+#define CASE(S) \
+  case S: launch_moddown<S, BLOCKS>(c, y, npoly, nq, s1, epi); return;
+    CASE(6) CASE(7) CASE(8)
+#undef CASE
+    default: throw ArgError("unsupported block pass");
+  }
+}
 
 void ntt_forward(Context& c, uint64_t* data, uint32_t npoly, size_t poly_stride, uint32_t nlimb,
                  LimbMap map) {

@@ -44,10 +44,24 @@ void ksk_inner(Context& c, const uint64_t* digits, uint32_t nq, const uint64_t* 
                uint64_t* ext);
 // out_b = galois-permute((ext_b[Q] - ModDownConv(ext_b[P])) * P^-1 + add_b), b = 0, 1,
 // with addends add0 / add1 ([nq][N], may be null); galois 1 means no permutation.
-void moddown_pair2(Context& c, const uint64_t* ext, uint32_t nq, uint64_t* out,
-                   const uint64_t* add0, const uint64_t* add1, uint32_t galois);
-void moddown_pair(Context& c, const uint64_t* ext, uint32_t nq, uint64_t* out,
-                  const uint64_t* add0, uint32_t galois);
+// The P limbs of ext are overwritten (taken to coefficient form in place).
+void moddown_pair2(Context& c, uint64_t* ext, uint32_t nq, uint64_t* out, const uint64_t* add0,
+                   const uint64_t* add1, uint32_t galois);
+void moddown_pair(Context& c, uint64_t* ext, uint32_t nq, uint64_t* out, const uint64_t* add0,
+                  uint32_t galois);
+// Batched key switching for a hoisted set: ext [B][2][nq+K][N] from one set
+// of digits and B keys, then one ModDown for all B with the combine fused
+// into the last NTT pass.  Output r must not alias its addends.
+struct KeySwitchOut {
+  uint64_t* out;         // [2][nq][N]
+  const uint64_t* add0;  // added to component 0 (or null)
+  const uint64_t* add1;  // added to component 1 (or null)
+  uint32_t galois;       // Galois element applied to the result (1 = none)
+};
+void ksk_inner_batch(Context& c, const uint64_t* digits, uint32_t nq, const uint64_t* const* keys,
+                     uint32_t batch, uint64_t* ext);
+void moddown_batch(Context& c, uint64_t* ext, uint32_t nq, uint32_t batch,
+                   const KeySwitchOut* outs);
 // Galois permutation X -> X^galois of evaluation-form limbs.
 void automorph(Context& c, uint64_t* out, const uint64_t* in, uint32_t npoly, uint32_t nlimb,
                uint32_t galois);

@@ -156,6 +156,20 @@ __global__ void __launch_bounds__(TPB)
   uint32_t i = 0;
   while (i < cnt) {
     const uint32_t end = i + 32 < cnt ? i + 32 : cnt;
+    // Eight independent loads in flight per thread before the products.
+    for (; i + 8 <= end; i += 8) {
+      U2 xv[8], wv[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        xv[u] = ld2(xp + (i + u) * xs);
+        wv[u] = ld2(wp + (i + u) * ws);
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        s0.mac(xv[u].x, wv[u].x);
+        s1.mac(xv[u].y, wv[u].y);
+      }
+    }
     for (; i < end; ++i) {
       const U2 xv = ld2(xp + i * xs), wv = ld2(wp + i * ws);
       s0.mac(xv.x, wv.x);
