@@ -34,6 +34,11 @@ sys.path.insert(0, os.path.join(ROOT, "fhe-mamba_amd"))
 
 METRIC = "rotations/s (N=2^16,L=24,hybrid KS); NTT HBM GB/s; s/token M2-130M"
 HBM_PEAK = 8.0e12  # B/s, MI355X HBM3E
+# HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE and
+# WRITE_SIZE on this workload (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0, the factors
+# a plain copy of known size reads back); recorded in
+# profiles/rotation_step_n65536_l24.md together with the commands.
+MEASURED_TRAFFIC = {"k_ksk_inner": 3_070_409_523 + 1_006_632_960}
 LOG_N, DEPTH, SCALE_BITS, FIRST_BITS, DNUM = 16, 23, 59, 60, 3
 N = 1 << LOG_N
 LIMB = N * 8  # bytes per limb
@@ -249,6 +254,10 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--skip-ntt", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="after the workloads, run one plain limb copy (k_copy_limbs) of "
+                         f"{COPY_PROBE_BYTES} bytes read and the same written, untimed, as "
+                         "the reference point for hardware byte counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (got --gpus {args.gpus}): the path has no "
@@ -262,11 +271,12 @@ def main() -> int:
     ntt = None if args.skip_ntt else (log("ntt batch workload"),
                                       run_ntt_batch(F, args.steps, args.warmup))[1]
     prof = rot["profile"]
+    model = step_kernel_bytes(rot["L"], rot["K"], len(STEPS))
     dom = max(prof, key=lambda k: prof[k][1])
     launches, total_ms = prof[dom]
-    dom_bytes = kernel_bytes(dom, rot["L"], rot["K"])
     avg_s = total_ms * 1e-3 / launches
-    achieved = dom_bytes / avg_s if dom_bytes else None
+    per_launch = model[dom] * args.steps / launches if dom in model else None
+    achieved = per_launch / avg_s if per_launch else None
     roofline = {
         "bound": "hbm",
         "kernel": dom,
@@ -274,10 +284,13 @@ def main() -> int:
         "peak": HBM_PEAK / 1e9,
         "unit": "GB/s",
         "frac": achieved / HBM_PEAK if achieved else None,
-        "traffic": None,
+        "traffic": MEASURED_TRAFFIC.get(dom),
+        "bytes_per_launch": per_launch,
         "avg_launch_us": avg_s * 1e6,
         "step_frac": rot["step_bytes"] / (rot["ms_per_step"] * 1e-3) / HBM_PEAK,
     }
+    kernel_gbps = {k: model[k] * args.steps / (prof[k][1] * 1e-3) / 1e9
+                   for k in sorted(prof) if k in model and prof[k][1] > 0}
     out = {
         "metric": METRIC,
         "value": rot["rotations_per_s"],
@@ -299,6 +312,7 @@ def main() -> int:
         },
         "roofline": roofline,
         "kernels_ms_per_step": {k: v[1] / args.steps for k, v in sorted(prof.items())},
+        "kernels_gbps": kernel_gbps,
     }
     if ntt:
         out["ntt"] = {k: ntt[k] for k in ("ntt_gbps", "ntt_fwd_ms", "ntt_inv_ms", "mac_ms",
@@ -306,6 +320,9 @@ def main() -> int:
         out["ntt"]["workload"] = ("64 ciphertexts x 2 polys x 24 limbs, N=2^16: forward NTT, "
                                   "MAC over 64 plaintexts, inverse NTT")
         out["ntt"]["frac"] = ntt["ntt_gbps"] * 1e9 / HBM_PEAK
+    if args.copy_probe:
+        log("copy probe")
+        copy_probe(F)
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle)")
         out["cpu_baseline"] = cpu_baseline()
@@ -313,16 +330,46 @@ def main() -> int:
     return 0
 
 
-def kernel_bytes(name: str, L: int, K: int):
-    """Algorithmic bytes of one launch of the rotation step's kernels."""
+COPY_PROBE_POLYS, COPY_PROBE_LIMBS = 16, 24
+COPY_PROBE_BYTES = COPY_PROBE_POLYS * COPY_PROBE_LIMBS * LIMB
+
+
+def copy_probe(F) -> None:
+    """One k_copy_limbs launch over 16 x 24 limbs (read once, written once)."""
+    q = [int(x) for x in ntt_primes(LOG_N, 60, COPY_PROBE_LIMBS)]
+    ctx = F.Context(LOG_N, q, [], 1)
+    src = ctx.poly(COPY_PROBE_POLYS, COPY_PROBE_LIMBS)
+    dst = ctx.poly(COPY_PROBE_POLYS, COPY_PROBE_LIMBS)
+    ctx.drop_limbs(src, COPY_PROBE_LIMBS, out=dst)
+    ctx.sync()
+    ctx.close()
+
+
+def step_kernel_bytes(L: int, K: int, R: int) -> dict:
+    """Bytes each kernel of one rotation step must move (read + write once),
+    summed over its launches in the step.  R hoisted rotations, ne = L + K
+    extended limbs, alpha = ceil(L / dnum) limbs per digit:
+      k_ksk_inner             digits dnum*ne once per batch, per rotation the
+                              key dnum*2*ne read and ext 2*ne written;
+      ntt_fwd_blocks_moddown  per rotation y 2L + ext(Q) 2L + c0 L read,
+                              output 2L written;
+      k_convert               ModUp: dnum*ne (alpha read, ne-alpha written per
+                              digit); ModDown: per rotation 2K read, 2L written;
+      ntt_{fwd,inv}_{cols,blocks}  read + write of every limb of the pass:
+                              forward ModUp dnum*(ne-alpha) + ModDown R*2L
+                              (cols only), inverse ModUp L + ModDown R*2K."""
     ne = L + K
-    if name == "k_ksk_inner":
-        return (DNUM * ne + DNUM * 2 * ne + 2 * ne) * LIMB
-    if name == "k_moddown_combine":
-        return (2 * ne + 2 * L + L + 2 * L) * LIMB  # ext, y, c0 read; out written
-    if name == "k_convert":
-        return None
-    return None
+    alpha = -(-L // DNUM)
+    modup_fwd = DNUM * (ne - alpha)
+    return {k: v * LIMB for k, v in {
+        "k_ksk_inner": DNUM * ne + R * (DNUM * 2 * ne + 2 * ne),
+        "ntt_fwd_blocks_moddown": R * 7 * L,
+        "k_convert": DNUM * ne + R * 2 * (K + L),
+        "ntt_fwd_cols": 2 * (modup_fwd + R * 2 * L),
+        "ntt_fwd_blocks": 2 * modup_fwd,
+        "ntt_inv_cols": 2 * (L + R * 2 * K),
+        "ntt_inv_blocks": 2 * (L + R * 2 * K),
+    }.items()}
 
 
 if __name__ == "__main__":
