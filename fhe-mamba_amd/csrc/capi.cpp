@@ -473,6 +473,24 @@ int fhe_key_destroy(fhe_key* k) {
   });
 }
 
+// Key inner products and ModDowns of `count` hoisted rotations of one
+// ciphertext, in batches that share one read of the digits; a batch keeps
+// its scratch (ext + y, 2(ne + nq) limbs per rotation) under 2 GiB.
+static void hoisted_batches(fhe::Context& c, const uint64_t* digits, uint32_t nq,
+                            const uint64_t* const* keys, const fhe::KeySwitchOut* outs,
+                            uint32_t count) {
+  const size_t ne = nq + c.K, ext_words = 2 * ne * c.n;
+  const size_t per_rot = (ext_words + 2 * (size_t)nq * c.n) * 8;
+  uint32_t batch = (uint32_t)std::max<size_t>(1, (size_t(2) << 30) / per_rot);
+  batch = std::min<uint32_t>(batch, fhe::MAX_KS_BATCH);
+  for (uint32_t r0 = 0; r0 < count; r0 += batch) {
+    const uint32_t b = std::min(batch, count - r0);
+    fhe::Scratch ext(c, b * ext_words);
+    fhe::ksk_inner_batch(c, digits, nq, keys + r0, b, ext.p);
+    fhe::moddown_batch(c, ext.p, nq, b, outs + r0);
+  }
+}
+
 static void check_key(const fhe_poly* p, const fhe_key* k) {
   need(p && k && p->c == k->c, "key belongs to another context");
 }
@@ -570,24 +588,13 @@ int fhe_rotate_hoisted(const fhe_poly* ct, const fhe_poly* digits, const fhe_key
       need((galois[r] & 1) && galois[r] < 2 * c.n, "Galois element must be odd and < 2N");
     }
     for (uint32_t r = 0; r < count; ++r) prepare_out(outs[r], 2, nq);
-    // Rotations are processed in batches that share one read of the digits;
-    // the batch keeps its scratch (ext + y, 2(ne + nq) limbs per rotation)
-    // under 2 GiB.
-    const size_t per_rot = 2 * (size_t)(ne + nq) * c.n * 8;
-    uint32_t batch = (uint32_t)std::max<size_t>(1, (size_t(2) << 30) / per_rot);
-    batch = std::min<uint32_t>(batch, fhe::MAX_KS_BATCH);
-    for (uint32_t r0 = 0; r0 < count; r0 += batch) {
-      const uint32_t b = std::min(batch, count - r0);
-      fhe::Scratch ext(c, (size_t)b * 2 * ne * c.n);
-      std::vector<const uint64_t*> kp(b);
-      std::vector<fhe::KeySwitchOut> ko(b);
-      for (uint32_t r = 0; r < b; ++r) {
-        kp[r] = keys[r0 + r]->data;
-        ko[r] = fhe::KeySwitchOut{outs[r0 + r]->data, ct->data, nullptr, galois[r0 + r]};
-      }
-      fhe::ksk_inner_batch(c, digits->data, nq, kp.data(), b, ext.p);
-      fhe::moddown_batch(c, ext.p, nq, b, ko.data());
+    std::vector<const uint64_t*> kp(count);
+    std::vector<fhe::KeySwitchOut> ko(count);
+    for (uint32_t r = 0; r < count; ++r) {
+      kp[r] = keys[r]->data;
+      ko[r] = fhe::KeySwitchOut{outs[r]->data, ct->data, nullptr, galois[r]};
     }
+    hoisted_batches(c, digits->data, nq, kp.data(), ko.data(), count);
   });
 }
 

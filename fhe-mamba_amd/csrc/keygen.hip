@@ -93,13 +93,6 @@ __global__ void k_square(uint64_t* out, const uint64_t* a, const ModConst* mc, u
   out[o] = mul_mod(a[o], a[o], mc[i]);
 }
 
-uint32_t galois_inverse(uint32_t g, uint32_t n) {
-  const uint64_t m = 2ull * n;
-  for (uint64_t t = 1; t < m; t += 2)
-    if ((t * g) % m == 1) return (uint32_t)t;
-  throw ArgError("Galois element is not a unit mod 2N");
-}
-
 void signed_small_to_eval(Context& c, const std::vector<int64_t>& coef, uint32_t idx0,
                           uint32_t nlimb, uint64_t* out) {
   Scratch d(c, c.n);

@@ -360,12 +360,14 @@ void ksk_inner_batch(Context& c, const uint64_t* digits, uint32_t nq, const uint
              digits, kb, ext, c.d_const, c.n, nq, c.L, c.K, nd, redc_chunk(c, all), batch);
 }
 
-uint32_t galois_inverse(const Context& c, uint32_t g) {
-  if (g == 1) return 1;
-  const uint64_t m = 2ull * c.n;
-  for (uint64_t t = 1; t < m; t += 2)
-    if ((t * g) % m == 1) return (uint32_t)t;
-  throw ArgError("Galois element is not a unit mod 2N");
+uint32_t galois_inverse(uint32_t g, uint32_t n) {
+  // The odd residues mod 2N form a group of order N, so g^-1 = g^(N-1).
+  const uint64_t m = 2ull * n;
+  if (!(g & 1) || g >= m) throw ArgError("Galois element is not a unit mod 2N");
+  uint64_t r = 1, b = g;
+  for (uint64_t e = n - 1; e; e >>= 1, b = b * b % m)
+    if (e & 1) r = r * b % m;
+  return (uint32_t)r;
 }
 
 void moddown_batch(Context& c, uint64_t* ext, uint32_t nq, uint32_t batch,
@@ -386,7 +388,7 @@ void moddown_batch(Context& c, uint64_t* ext, uint32_t nq, uint32_t batch,
     epi.out[r] = outs[r].out;
     epi.add[r][0] = outs[r].add0;
     epi.add[r][1] = outs[r].add1;
-    epi.ginv[r] = galois_inverse(c, outs[r].galois);
+    epi.ginv[r] = galois_inverse(outs[r].galois, c.n);
   }
   ntt_forward_moddown(c, y.p, 2 * batch, nq, epi);
 }

@@ -62,6 +62,8 @@ void ksk_inner_batch(Context& c, const uint64_t* digits, uint32_t nq, const uint
                      uint32_t batch, uint64_t* ext);
 void moddown_batch(Context& c, uint64_t* ext, uint32_t nq, uint32_t batch,
                    const KeySwitchOut* outs);
+// g^-1 mod 2N for an odd Galois element g < 2N.
+uint32_t galois_inverse(uint32_t g, uint32_t n);
 // Galois permutation X -> X^galois of evaluation-form limbs.
 void automorph(Context& c, uint64_t* out, const uint64_t* in, uint32_t npoly, uint32_t nlimb,
                uint32_t galois);

@@ -87,6 +87,31 @@ def test_hoisted_rotations_equal_single_rotations(setup):
         assert np.array_equal(out.numpy(), orc.rotate(ct, key, g))
 
 
+def test_hoisted_pipelined_set_matches_oracle(setup):
+    """15 rotations (more than one pipeline chunk, with a partial last
+    chunk; repeated and conjugation elements included): every output equals
+    the oracle's single rotation, and the input and digits are untouched."""
+    ctx, orc, s = setup
+    steps = [1, -1, 2, -2, 3, 5, 7, -7, 16, 1, -3, 9, 11, -16, 6]
+    gal = [O.galois_elt(r, ctx.n) for r in steps]
+    gal[7] = 2 * ctx.n - 1
+    keys = {g: orc.galois_key(s, g, 60 + i) for i, g in enumerate(dict.fromkeys(gal))}
+    dkeys = {g: ctx.load_key(k) for g, k in keys.items()}
+    ct = residues(np.random.default_rng(15), ctx.q, (2,), ctx.n)
+    dct = ctx.upload(ct)
+    digits = ctx.rotation_precompute(dct)
+    before = digits.numpy()
+    outs = ctx.rotate_hoisted(dct, digits, [dkeys[g] for g in gal], gal)
+    for out, g in zip(outs, gal):
+        assert np.array_equal(out.numpy(), orc.rotate(ct, keys[g], g))
+    assert np.array_equal(dct.numpy(), ct)
+    assert np.array_equal(digits.numpy(), before)
+    # a second call reusing the outputs gives the same words
+    again = ctx.rotate_hoisted(dct, digits, [dkeys[g] for g in gal], gal, outs=outs)
+    for out, g in zip(again, gal):
+        assert np.array_equal(out.numpy(), orc.rotate(ct, keys[g], g))
+
+
 def test_relinearize_matches_oracle(setup):
     ctx, orc, s = setup
     key = orc.relin_key(s, 5)
