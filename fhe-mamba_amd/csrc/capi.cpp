@@ -473,24 +473,6 @@ int fhe_key_destroy(fhe_key* k) {
   });
 }
 
-// Key inner products and ModDowns of `count` hoisted rotations of one
-// ciphertext, in batches that share one read of the digits; a batch keeps
-// its scratch (ext + y, 2(ne + nq) limbs per rotation) under 2 GiB.
-static void hoisted_batches(fhe::Context& c, const uint64_t* digits, uint32_t nq,
-                            const uint64_t* const* keys, const fhe::KeySwitchOut* outs,
-                            uint32_t count) {
-  const size_t ne = nq + c.K, ext_words = 2 * ne * c.n;
-  const size_t per_rot = (ext_words + 2 * (size_t)nq * c.n) * 8;
-  uint32_t batch = (uint32_t)std::max<size_t>(1, (size_t(2) << 30) / per_rot);
-  batch = std::min<uint32_t>(batch, fhe::MAX_KS_BATCH);
-  for (uint32_t r0 = 0; r0 < count; r0 += batch) {
-    const uint32_t b = std::min(batch, count - r0);
-    fhe::Scratch ext(c, b * ext_words);
-    fhe::ksk_inner_batch(c, digits, nq, keys + r0, b, ext.p);
-    fhe::moddown_batch(c, ext.p, nq, b, outs + r0);
-  }
-}
-
 static void check_key(const fhe_poly* p, const fhe_key* k) {
   need(p && k && p->c == k->c, "key belongs to another context");
 }
@@ -594,7 +576,48 @@ int fhe_rotate_hoisted(const fhe_poly* ct, const fhe_poly* digits, const fhe_key
       kp[r] = keys[r]->data;
       ko[r] = fhe::KeySwitchOut{outs[r]->data, ct->data, nullptr, galois[r]};
     }
-    hoisted_batches(c, digits->data, nq, kp.data(), ko.data(), count);
+    fhe::keyswitch_hoisted(c, digits->data, nq, kp.data(), ko.data(), count);
+  });
+}
+
+int fhe_linear_transform(fhe_poly* out, const fhe_poly* ct, const fhe_poly* const* pts,
+                         uint32_t count, uint32_t bstep, const fhe_key* const* baby_keys,
+                         const uint32_t* baby_galois, const fhe_key* giant_key,
+                         uint32_t giant_galois) {
+  return guard([&] {
+    need(ct && pts && (bstep <= 1 || (baby_keys && baby_galois)), "null argument");
+    same_ctx(out, ct);
+    fhe::Context& c = *ct->c;
+    need(ct->npoly == 2 && ct->nlimb <= c.L, "linear transform needs a 2-poly ciphertext");
+    need(count >= 1 && bstep >= 1 && bstep <= fhe::MAC_TABLE,
+         "need count >= 1 and 1 <= bstep <= 64");
+    const uint32_t nq = ct->nlimb, giants = (count + bstep - 1) / bstep;
+    std::vector<const uint64_t*> pp(count, nullptr);
+    bool any = false;
+    for (uint32_t k = 0; k < count; ++k) {
+      if (!pts[k]) continue;
+      need(pts[k]->c == &c && pts[k]->npoly == 1 && pts[k]->nlimb >= nq,
+           "diagonal must be a one-poly plaintext with at least the ciphertext's limbs");
+      pp[k] = pts[k]->data;
+      any = true;
+    }
+    need(any, "linear transform has no nonzero diagonal");
+    const uint32_t nb = std::min(bstep, count);
+    std::vector<const uint64_t*> bk(nb > 1 ? nb - 1 : 1, nullptr);
+    for (uint32_t b = 1; b < nb; ++b) {
+      if (!baby_keys[b - 1]) continue;
+      check_key(ct, baby_keys[b - 1]);
+      need((baby_galois[b - 1] & 1) && baby_galois[b - 1] < 2 * c.n, "bad Galois element");
+      bk[b - 1] = baby_keys[b - 1]->data;
+    }
+    if (giants > 1) {
+      need(giant_key != nullptr, "giant-step key required when count > bstep");
+      check_key(ct, giant_key);
+      need((giant_galois & 1) && giant_galois < 2 * c.n, "bad Galois element");
+    }
+    prepare_out(out, 2, nq);
+    fhe::linear_transform(c, out->data, ct->data, nq, pp.data(), count, bstep, bk.data(),
+                          baby_galois, giants > 1 ? giant_key->data : nullptr, giant_galois);
   });
 }
 

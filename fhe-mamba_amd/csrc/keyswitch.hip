@@ -18,6 +18,9 @@
 // [Qhat_i * 2^64]_{t_k}), one reduction per output word.  That needs the sum
 // to stay below t_k * 2^64, i.e. (terms per REDC) * max source modulus <
 // 2^64; the kernel reduces in chunks of `chunk` terms chosen on the host.
+#include <algorithm>
+#include <vector>
+
 #include "ops.hpp"
 
 namespace fhe {
@@ -407,6 +410,88 @@ void moddown_pair2(Context& c, uint64_t* ext, uint32_t nq, uint64_t* out, const 
 void moddown_pair(Context& c, uint64_t* ext, uint32_t nq, uint64_t* out, const uint64_t* add0,
                   uint32_t galois) {
   moddown_pair2(c, ext, nq, out, add0, nullptr, galois);
+}
+
+void keyswitch_hoisted(Context& c, const uint64_t* digits, uint32_t nq,
+                       const uint64_t* const* keys, const KeySwitchOut* outs, uint32_t count) {
+  const size_t ext_words = 2 * (size_t)(nq + c.K) * c.n;
+  const size_t per_rot = (ext_words + 2 * (size_t)nq * c.n) * 8;
+  uint32_t batch = (uint32_t)std::max<size_t>(1, (size_t(2) << 30) / per_rot);
+  batch = std::min<uint32_t>(batch, MAX_KS_BATCH);
+  for (uint32_t r0 = 0; r0 < count; r0 += batch) {
+    const uint32_t b = std::min(batch, count - r0);
+    Scratch ext(c, b * ext_words);
+    ksk_inner_batch(c, digits, nq, keys + r0, b, ext.p);
+    moddown_batch(c, ext.p, nq, b, outs + r0);
+  }
+}
+
+void rotate(Context& c, uint64_t* out, const uint64_t* ct, uint32_t nq, const uint64_t* key,
+            uint32_t galois) {
+  const size_t ne = nq + c.K;
+  Scratch dig(c, num_digits(c, nq) * ne * c.n), ext(c, 2 * ne * c.n);
+  modup(c, ct + (size_t)nq * c.n, nq, dig.p);
+  ksk_inner(c, dig.p, nq, key, ext.p);
+  moddown_pair(c, ext.p, nq, out, ct, galois);
+}
+
+void linear_transform(Context& c, uint64_t* out, const uint64_t* ct, uint32_t nq,
+                      const uint64_t* const* pts, uint32_t count, uint32_t bstep,
+                      const uint64_t* const* baby_keys, const uint32_t* baby_galois,
+                      const uint64_t* giant_key, uint32_t giant_galois) {
+  if (count == 0 || bstep == 0) throw ArgError("linear transform: no diagonals");
+  const size_t n = c.n, ne = nq + c.K, pl = 2 * (size_t)nq * n;
+  const uint32_t giants = (count + bstep - 1) / bstep, nb = std::min(bstep, count);
+  if (giants > 1 && !giant_key) throw ArgError("linear transform: giant-step key missing");
+  std::vector<uint8_t> used(nb, 0);
+  for (uint32_t k = 0; k < count; ++k)
+    if (pts[k]) used[k % bstep] = 1;
+  // Babies rot_b(ct) for the b some diagonal uses, from one ModUp.
+  std::vector<const uint64_t*> baby(nb, nullptr);
+  baby[0] = ct;
+  Scratch babies(c, std::max<size_t>(1, (nb - 1) * pl));
+  Scratch dig(c, num_digits(c, nq) * ne * n);
+  std::vector<const uint64_t*> keys;
+  std::vector<KeySwitchOut> outs;
+  for (uint32_t b = 1; b < nb; ++b) {
+    if (!used[b]) continue;
+    if (!baby_keys[b - 1]) throw ArgError("linear transform: baby-step key missing");
+    uint64_t* dst = babies.p + (b - 1) * pl;
+    baby[b] = dst;
+    keys.push_back(baby_keys[b - 1]);
+    outs.push_back(KeySwitchOut{dst, ct, nullptr, baby_galois[b - 1]});
+  }
+  if (!keys.empty()) {
+    modup(c, ct + (size_t)nq * n, nq, dig.p);
+    keyswitch_hoisted(c, dig.p, nq, keys.data(), outs.data(), (uint32_t)keys.size());
+  }
+  // Giant steps by Horner's rule: acc = inner_{G-1}; acc = inner_g + rot(acc).
+  Scratch acc0(c, pl), acc1(c, pl), ext(c, 2 * ne * n);
+  uint64_t* cur = acc0.p;
+  uint64_t* nxt = acc1.p;
+  std::vector<const uint64_t*> xs, ws;
+  auto inner = [&](uint32_t g, uint64_t* acc, bool accumulate) {
+    xs.clear();
+    ws.clear();
+    for (uint32_t b = 0; b < bstep; ++b) {
+      const uint32_t k = g * bstep + b;
+      if (k < count && pts[k]) {
+        xs.push_back(baby[b]);
+        ws.push_back(pts[k]);
+      }
+    }
+    poly_mac_table(c, acc, xs.data(), ws.data(), (uint32_t)xs.size(), nq, accumulate);
+  };
+  inner(giants - 1, cur, false);
+  for (int g = (int)giants - 2; g >= 0; --g) {
+    modup(c, cur + (size_t)nq * n, nq, dig.p);
+    ksk_inner(c, dig.p, nq, giant_key, ext.p);
+    moddown_pair(c, ext.p, nq, nxt, cur, giant_galois);
+    inner((uint32_t)g, nxt, true);
+    std::swap(cur, nxt);
+  }
+  hip_check(hipMemcpyAsync(out, cur, pl * 8, hipMemcpyDeviceToDevice, c.stream),
+            "linear transform");
 }
 
 void automorph(Context& c, uint64_t* out, const uint64_t* in, uint32_t npoly, uint32_t nlimb,

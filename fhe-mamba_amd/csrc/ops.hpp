@@ -31,6 +31,15 @@ void poly_tensor(Context& c, uint64_t* out3, const uint64_t* a, const uint64_t* 
 // acc[2][nq][N] = sum_i x_i (.) w_i for x [n][2][nq][N], w [n][nq][N].
 void poly_mac(Context& c, uint64_t* acc, const uint64_t* x, const uint64_t* w, uint32_t n,
               uint32_t nq);
+// acc [2][nq][N] (+)= sum_i x[i] (.) w[i] for ciphertexts x[i] [2][nq][N] and
+// plaintexts w[i] (first nq limbs used) given by address; cnt may be 0.
+constexpr uint32_t MAC_TABLE = 64;
+struct MacTable {
+  const uint64_t* x[MAC_TABLE];
+  const uint64_t* w[MAC_TABLE];
+};
+void poly_mac_table(Context& c, uint64_t* acc, const uint64_t* const* x,
+                    const uint64_t* const* w, uint32_t cnt, uint32_t nq, bool accumulate);
 // Drop the last limb with centred division (FLEXIBLEAUTO rescale);
 // out is [npoly][nq-1][N].
 void poly_rescale(Context& c, uint64_t* out, const uint64_t* a, uint32_t npoly, uint32_t nq);
@@ -62,6 +71,23 @@ void ksk_inner_batch(Context& c, const uint64_t* digits, uint32_t nq, const uint
                      uint32_t batch, uint64_t* ext);
 void moddown_batch(Context& c, uint64_t* ext, uint32_t nq, uint32_t batch,
                    const KeySwitchOut* outs);
+// `count` key switches of one set of digits (keys[r] in Montgomery form), in
+// batches that share one read of the digits (scratch per batch <= 2 GiB).
+void keyswitch_hoisted(Context& c, const uint64_t* digits, uint32_t nq,
+                       const uint64_t* const* keys, const KeySwitchOut* outs, uint32_t count);
+// Rotate ct [2][nq][N] by one key: out = galois-permute(KS(c1) + (c0, 0)).
+// out must not alias ct.
+void rotate(Context& c, uint64_t* out, const uint64_t* ct, uint32_t nq, const uint64_t* key,
+            uint32_t galois);
+// Baby-step giant-step plaintext linear transform of ct [2][nq][N]:
+//   out = sum_{g < G} rot_giant^g( sum_{b < bstep} pts[g*bstep + b] (.) rot_b(ct) ),
+// G = ceil(count / bstep), rot_b by baby_keys[b - 1] (b >= 1; rot_0 = id, all
+// babies from one ModUp), the giant sum evaluated by Horner's rule with the
+// one giant key.  Null pts are skipped.  out may alias ct.
+void linear_transform(Context& c, uint64_t* out, const uint64_t* ct, uint32_t nq,
+                      const uint64_t* const* pts, uint32_t count, uint32_t bstep,
+                      const uint64_t* const* baby_keys, const uint32_t* baby_galois,
+                      const uint64_t* giant_key, uint32_t giant_galois);
 // g^-1 mod 2N for an odd Galois element g < 2N.
 uint32_t galois_inverse(uint32_t g, uint32_t n);
 // Galois permutation X -> X^galois of evaluation-form limbs.

@@ -184,6 +184,51 @@ __global__ void __launch_bounds__(TPB)
   st2(acc + (size_t)poly * nq * n + limb_off, s0.lo, s1.lo);
 }
 
+// acc[p][j] = (acc[p][j] if accumulate) + sum_i x_i[p][j] * w_i[j] mod q_j for
+// ciphertexts x_i [2][nq][N] and plaintexts w_i (limb j at w_i + j * N)
+// given by address; same 128-bit accumulation as k_mac.
+__global__ void __launch_bounds__(TPB)
+    k_mac_table(uint64_t* acc, const MacTable t, const ModConst* mc, uint32_t n, uint32_t nq,
+                uint32_t cnt, uint32_t accumulate) {
+  const ModConst m = mc[blockIdx.y];
+  const size_t limb_off = (size_t)blockIdx.y * n + pair_off();
+  const size_t xoff = (size_t)blockIdx.z * nq * n + limb_off;
+  Acc128 s0, s1;
+  uint32_t i = 0;
+  while (i < cnt) {
+    const uint32_t end = i + 32 < cnt ? i + 32 : cnt;
+    for (; i + 4 <= end; i += 4) {
+      U2 xv[4], wv[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        xv[u] = ld2(t.x[i + u] + xoff);
+        wv[u] = ld2(t.w[i + u] + limb_off);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        s0.mac(xv[u].x, wv[u].x);
+        s1.mac(xv[u].y, wv[u].y);
+      }
+    }
+    for (; i < end; ++i) {
+      const U2 xv = ld2(t.x[i] + xoff), wv = ld2(t.w[i] + limb_off);
+      s0.mac(xv.x, wv.x);
+      s1.mac(xv.y, wv.y);
+    }
+    s0.lo = reduce128(s0.hi, s0.lo, m);
+    s0.hi = 0;
+    s1.lo = reduce128(s1.hi, s1.lo, m);
+    s1.hi = 0;
+  }
+  uint64_t* ap = acc + xoff;
+  if (accumulate) {
+    const U2 a = ld2(ap);
+    s0.lo = add_mod(s0.lo, a.x, m.q);
+    s1.lo = add_mod(s1.lo, a.y, m.q);
+  }
+  st2(ap, s0.lo, s1.lo);
+}
+
 // Rescale step 1: centred lift of the (inverse-NTT'd) last limb into limbs
 // i < l.  grid (N/512, l, npoly).  last: [npoly][N] coefficient form.
 __global__ void __launch_bounds__(TPB)
@@ -283,6 +328,22 @@ void poly_tensor(Context& c, uint64_t* out3, const uint64_t* a, const uint64_t* 
 void poly_mac(Context& c, uint64_t* acc, const uint64_t* x, const uint64_t* w, uint32_t n,
               uint32_t nq) {
   FHE_LAUNCH(c, "k_mac", k_mac, grid_for(c, nq, 2), dim3(tpb_for(c)), 0, acc, x, w, c.d_const, c.n, nq, n);
+}
+
+void poly_mac_table(Context& c, uint64_t* acc, const uint64_t* const* x,
+                    const uint64_t* const* w, uint32_t cnt, uint32_t nq, bool accumulate) {
+  uint32_t i = 0;
+  do {
+    const uint32_t k = cnt - i < MAC_TABLE ? cnt - i : MAC_TABLE;
+    MacTable t{};
+    for (uint32_t j = 0; j < k; ++j) {
+      t.x[j] = x[i + j];
+      t.w[j] = w[i + j];
+    }
+    const uint32_t acc_flag = (accumulate || i > 0) ? 1u : 0u;
+    FHE_LAUNCH(c, "k_mac_table", k_mac_table, grid_for(c, nq, 2), dim3(tpb_for(c)), 0, acc, t, c.d_const, c.n, nq, k, acc_flag);
+    i += k;
+  } while (i < cnt);
 }
 
 void poly_rescale(Context& c, uint64_t* out, const uint64_t* a, uint32_t npoly, uint32_t nq) {

@@ -209,6 +209,26 @@ class Context:
         call("fhe_rotate_hoisted", ct.handle, digits.handle, kh, _ptr(ga), count, oh)
         return outs
 
+    def linear_transform(self, ct, pts, bstep: int, baby_keys, baby_galois, giant_key=None,
+                         giant_galois: int = 1, out=None):
+        """BSGS transform: sum_g rot_giant^g(sum_b pts[g*bstep+b] * rot_b(ct)).
+
+        pts: list of one-poly plaintexts or None (zero diagonal), already
+        pre-rotated for their giant step; baby_keys / baby_galois: bstep - 1
+        entries (None where unused); giant_key rotates by bstep strides."""
+        count = len(pts)
+        out = self._out(out, 2, ct.nlimb)
+        ph = (ctypes.c_void_p * count)(*[p.handle.value if p is not None else None
+                                         for p in pts])
+        nb = max(1, bstep - 1)
+        bk = (ctypes.c_void_p * nb)(*([k.handle.value if k is not None else None
+                                       for k in baby_keys] + [None] * (nb - len(baby_keys))))
+        bg = np.zeros(nb, dtype=np.uint32)
+        bg[: len(baby_galois)] = baby_galois
+        call("fhe_linear_transform", out.handle, ct.handle, ph, count, bstep, bk, _ptr(bg),
+             giant_key.handle if giant_key is not None else None, giant_galois)
+        return out
+
     # -------------------------------------------------------------- encoding
     def encode(self, values, slots: int, scale: float, nlimb: int, out=None) -> "Poly":
         v = np.asarray(values)

@@ -165,6 +165,23 @@ int fhe_rotation_precompute(const fhe_poly *ct, fhe_poly **digits);
 int fhe_rotate_hoisted(const fhe_poly *ct, const fhe_poly *digits,
                        const fhe_key *const *keys, const uint32_t *galois,
                        uint32_t count, fhe_poly *const *outs);
+/* LinearTransformInPlace(ct, rowSize = count, bStep = bstep, pts)
+ * (native/fideslib_stage0/patches/fideslib-v2.1.0-linear-transform-api.patch:21-38,
+ *  called at src/stage1_mamba2_decode_fideslib.cpp:3517-3531; unfused form
+ *  src/packed_fideslib.cpp:447-516):
+ *   out = sum_g rot_giant^g( sum_b pts[g*bstep + b] (.) rot_b(ct) )
+ * with pts already pre-rotated by the caller for their giant step.
+ * baby_keys[b-1] / baby_galois[b-1] rotate by b strides (b = 1..bstep-1; a
+ * key may be null when no diagonal uses that baby), all babies from one
+ * ModUp; giant_key rotates by bstep strides and is applied by Horner's rule
+ * (required when count > bstep).  pts[k] may be null (zero diagonal); at
+ * least one must be present.  Plaintexts are one-poly with at least the
+ * ciphertext's limbs.  out may be ct. */
+int fhe_linear_transform(fhe_poly *out, const fhe_poly *ct,
+                         const fhe_poly *const *pts, uint32_t count,
+                         uint32_t bstep, const fhe_key *const *baby_keys,
+                         const uint32_t *baby_galois, const fhe_key *giant_key,
+                         uint32_t giant_galois);
 
 /* ---- encoding -----------------------------------------------------------
  * MakeCKKSPackedPlaintext (packed_fideslib.cpp:204): special inverse FFT of

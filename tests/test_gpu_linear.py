@@ -1,0 +1,107 @@
+"""BSGS plaintext linear transform on the GPU, bit-exact against the same
+composition of oracle rotations, plaintext MACs and additions (babies from
+one ModUp, giant steps by Horner's rule with one giant key)."""
+import numpy as np
+import pytest
+
+import oracle as O
+from gpu_helpers import residues
+
+pytestmark = pytest.mark.gpu
+
+F = pytest.importorskip("fhemamba_amd")
+
+PARAMS = [(12, 5, 45, 60, 2), (11, 4, 40, 60, 3)]
+
+
+@pytest.fixture(scope="module", params=PARAMS)
+def setup(request):
+    log_n, depth, sb, fb, dnum = request.param
+    q, p = O.gen_moduli(log_n, depth, sb, fb, dnum)
+    ctx, orc = F.Context(log_n, q, p, dnum), O.Ctx(log_n, q, p, dnum)
+    s = orc.secret(21)
+    return ctx, orc, s, {}
+
+
+def _key(setup, step):
+    ctx, orc, s, cache = setup
+    if step not in cache:
+        g = O.galois_elt(step, ctx.n)
+        k = orc.galois_key(s, g, 300 + len(cache))
+        cache[step] = (g, k, ctx.load_key(k))
+    return cache[step]
+
+
+def oracle_transform(orc, q, ct, pts, bstep, baby, giant):
+    count, nq = len(pts), ct.shape[1]
+    qa = np.array(q[:nq], dtype=np.uint64)[None, :, None]
+    used = {k % bstep for k in range(count) if pts[k] is not None}
+    babies = {0: ct}
+    for b in range(1, min(bstep, count)):
+        if b in used:
+            g, k = baby[b]
+            babies[b] = orc.rotate(ct, k, g)
+
+    def inner(g):
+        xs, ws = [], []
+        for b in range(bstep):
+            k = g * bstep + b
+            if k < count and pts[k] is not None:
+                xs.append(babies[b])
+                ws.append(pts[k][:nq])
+        if not xs:
+            return np.zeros_like(ct)
+        return orc.mac(np.stack(xs), np.stack(ws))
+
+    giants = -(-count // bstep)
+    acc = inner(giants - 1)
+    for g in range(giants - 2, -1, -1):
+        r = orc.rotate(acc, giant[1], giant[0])
+        acc = (r + inner(g)) % qa
+    return acc
+
+
+CASES = [
+    # (count, bstep, stride, null diagonals, in place)
+    (7, 3, 1, (4,), False),
+    (4, 4, 2, (), False),
+    (5, 1, 1, (), False),
+    (9, 4, 1, (1, 5, 8), True),
+    (1, 1, 1, (), False),
+]
+
+
+@pytest.mark.parametrize("count,bstep,stride,nulls,inplace", CASES)
+def test_linear_transform_matches_oracle(setup, count, bstep, stride, nulls, inplace):
+    ctx, orc, s, _ = setup
+    rng = np.random.default_rng(100 + count * 7 + bstep)
+    nq = ctx.L - 1  # one level down: keys and plaintexts carry more limbs
+    ct = residues(rng, ctx.q[:nq], (2,), ctx.n)
+    pts_host = [None if k in nulls else residues(rng, ctx.q, (), ctx.n)
+                for k in range(count)]
+    pts_dev = [None if p is None else ctx.upload(p[None]) for p in pts_host]
+    baby = {b: _key(setup, b * stride)[:2] for b in range(1, min(bstep, count))}
+    baby_dev = [_key(setup, b * stride)[2] for b in range(1, min(bstep, count))]
+    baby_gal = [baby[b][0] for b in range(1, min(bstep, count))]
+    gk = _key(setup, bstep * stride) if count > bstep else None
+    dct = ctx.upload(ct)
+    out = dct if inplace else None
+    got = ctx.linear_transform(dct, pts_dev, bstep, baby_dev, baby_gal,
+                               gk[2] if gk else None, gk[0] if gk else 1, out=out).numpy()
+    want = oracle_transform(orc, ctx.q, ct, pts_host, bstep, baby,
+                            gk[:2] if gk else None)
+    assert np.array_equal(got, want)
+
+
+def test_linear_transform_rejects_bad_arguments(setup):
+    ctx, orc, s, _ = setup
+    rng = np.random.default_rng(5)
+    ct = ctx.upload(residues(rng, ctx.q, (2,), ctx.n))
+    pt = ctx.upload(residues(rng, ctx.q, (1,), ctx.n))
+    with pytest.raises(ValueError):  # every diagonal null
+        ctx.linear_transform(ct, [None, None], 2, [None], [1])
+    with pytest.raises(ValueError):  # giant key missing
+        ctx.linear_transform(ct, [pt, pt, pt], 2, [_key(setup, 1)[2]], [_key(setup, 1)[0]])
+    short = ctx.upload(residues(rng, ctx.q[:2], (1,), ctx.n))
+    with pytest.raises(ValueError):  # plaintext with fewer limbs than ct
+        ctx.linear_transform(ct, [short], 1, [], [])
