@@ -1,0 +1,207 @@
+"""CKKS circuit helpers with the interface of src/fhemamba/ckks_probes.py.
+
+CkksPrimitives drives any object with the OpenFHE CryptoContext surface
+(by default this package's fhemamba_amd.ckks on the GPU); the helpers below
+follow src/fhemamba/ckks_probes.py:10-164 so that the same circuits issue
+the same sequence of homomorphic operations:
+  * floor_coeffs / affine / cheb_eval64 / ceil_log2 (:13-31);
+  * cheb_baby_size: 2^ceil(levels / 2), levels = max(1, ceil(log2(d + 1)))
+    (:34-36);
+  * cheb_ps_depth: the level ledger of the Paterson-Stockmeyer recursion
+    (:39-66);
+  * eval_chebyshev: Paterson-Stockmeyer over Chebyshev polynomials with
+    T_2i = 2 T_i^2 - 1, T_2i+1 = 2 T_i+1 T_i - T_1 and the split
+    p = a' + T_k * b~ (:107-155);
+  * newton_refine: y <- 1.5 y + (-v/2) y^3 (:157-164);
+  * build_toy_context (:167-201), TOY security (HEStd_NotSet).
+"""
+from __future__ import annotations
+
+from typing import Sequence
+
+import numpy as np
+
+CHEB_COEFF_FLOOR = 1e-12
+
+
+def floor_coeffs(coeffs, threshold: float = CHEB_COEFF_FLOOR) -> list[float]:
+    """Zero every coefficient below the floor (in magnitude)."""
+    return [float(c) if abs(float(c)) >= threshold else 0.0 for c in coeffs]
+
+
+def affine(lo: float, hi: float) -> tuple[float, float]:
+    """(a, b) such that a * x + b maps [lo, hi] onto [-1, 1]."""
+    width = hi - lo
+    return 2.0 / width, -(hi + lo) / width
+
+
+def cheb_eval64(coeffs: Sequence[float], u: np.ndarray) -> np.ndarray:
+    return np.polynomial.chebyshev.chebval(u, np.asarray(coeffs, dtype=np.float64))
+
+
+def ceil_log2(value: int) -> int:
+    """Smallest e >= 0 with 2^e >= value."""
+    e = 0
+    while (1 << e) < value:
+        e += 1
+    return e
+
+
+def cheb_baby_size(degree: int) -> int:
+    levels = max(1, ceil_log2(degree + 1))
+    return 1 << ((levels + 1) // 2)
+
+
+def _giant_split(n: int, m: int) -> int:
+    """Smallest k = m * 2^j with 2k - 1 >= n."""
+    k = m
+    while 2 * k - 1 < n:
+        k *= 2
+    return k
+
+
+def cheb_ps_depth(degree: int) -> int:
+    """Multiplicative depth the Paterson-Stockmeyer evaluation spends."""
+    m = cheb_baby_size(degree)
+    memo: dict[int, int] = {}
+
+    def t_depth(i: int) -> int:
+        if i <= 1:
+            return 0
+        if i not in memo:
+            if i % 2 == 0:
+                memo[i] = t_depth(i // 2) + 1
+            else:
+                memo[i] = max(t_depth(i // 2), t_depth(i // 2 + 1)) + 1
+        return memo[i]
+
+    def depth(n: int) -> int:
+        if n == 0:
+            return 0
+        if n < m:
+            return 1 + max(t_depth(i) for i in range(1, n + 1))
+        k = _giant_split(n, m)
+        return max(depth(k - 1), 1 + max(t_depth(k), depth(n - k)))
+
+    return depth(degree)
+
+
+class CkksPrimitives:
+    """Elementary encrypted helpers over an OpenFHE-shaped context."""
+
+    def __init__(self, cc, keys, *, batch: int,
+                 coefficient_floor: float = CHEB_COEFF_FLOOR) -> None:
+        self.cc = cc
+        self.keys = keys
+        self.batch = batch
+        self.coefficient_floor = coefficient_floor
+        # Constants are produced from an encrypted all-ones vector.
+        self.ones_ct = self.encrypt(np.ones(batch))
+
+    def encrypt(self, values: np.ndarray, fill: float = 0.0):
+        """Encrypt `values`, padding the unused slots with `fill`."""
+        slots = np.full(self.batch, float(fill))
+        slots[: len(values)] = values
+        pt = self.cc.MakeCKKSPackedPlaintext([float(x) for x in slots])
+        return self.cc.Encrypt(self.keys.publicKey, pt)
+
+    def decrypt(self, ct, n: int | None = None) -> np.ndarray:
+        pt = self.cc.Decrypt(ct, self.keys.secretKey)
+        pt.SetLength(self.batch)
+        return np.asarray(pt.GetRealPackedValue(), dtype=np.float64)[:n]
+
+    def mask_mult(self, ct, mask: np.ndarray):
+        return self.cc.EvalMult(ct, self.cc.MakeCKKSPackedPlaintext([float(x) for x in mask]))
+
+    def const_ct(self, value: float):
+        return self.cc.EvalMult(self.ones_ct, float(value))
+
+    def affine_ct(self, ct, a: float, b: float):
+        """a * ct + b (one level)."""
+        return self.cc.EvalAdd(self.cc.EvalMult(ct, float(a)), float(b))
+
+    def eval_chebyshev(self, u, coeffs: Sequence[float]):
+        """sum_i coeffs[i] T_i(u) by Paterson-Stockmeyer."""
+        degree = len(coeffs) - 1
+        if degree < 1:
+            return self.const_ct(coeffs[0] if len(coeffs) else 0.0)
+        cc = self.cc
+        m = cheb_baby_size(degree)
+        cache = {1: u}
+
+        def cheb(i: int):
+            if i not in cache:
+                if i % 2 == 0:
+                    h = cheb(i // 2)
+                    sq = cc.EvalMult(h, h)
+                    cache[i] = cc.EvalSub(cc.EvalAdd(sq, sq), 1.0)
+                else:
+                    pr = cc.EvalMult(cheb(i // 2 + 1), cheb(i // 2))
+                    cache[i] = cc.EvalSub(cc.EvalAdd(pr, pr), u)
+            return cache[i]
+
+        def evaluate(c: list[float]):
+            n = len(c) - 1
+            if n < m:
+                acc = None
+                for i in range(1, n + 1):
+                    if abs(c[i]) < self.coefficient_floor:
+                        continue
+                    term = cc.EvalMult(cheb(i), c[i])
+                    acc = term if acc is None else cc.EvalAdd(acc, term)
+                if acc is None:
+                    return self.const_ct(c[0])
+                if abs(c[0]) >= self.coefficient_floor:
+                    acc = cc.EvalAdd(acc, c[0])
+                return acc
+            # p = a' + T_k * b~ using T_k T_j = (T_{k+j} + T_{k-j}) / 2.
+            k = _giant_split(n, m)
+            quot = [c[k]] + [2.0 * c[k + j] for j in range(1, n - k + 1)]
+            rem = list(c[:k])
+            for i in range(k + 1, n + 1):
+                rem[2 * k - i] -= c[i]
+            giant = cc.EvalMult(cheb(k), evaluate(quot))
+            return cc.EvalAdd(evaluate(rem), giant)
+
+        return evaluate(list(coeffs))
+
+    def newton_refine(self, y, v_neg_half, iterations: int):
+        """Newton steps for 1/sqrt(v): y <- 1.5 y + (-v/2) * y * y^2."""
+        cc = self.cc
+        for _ in range(iterations):
+            y_sq = cc.EvalMult(y, y)
+            vy = cc.EvalMult(v_neg_half, y)
+            cube = cc.EvalMult(vy, y_sq)
+            y = cc.EvalAdd(cc.EvalMult(y, 1.5), cube)
+        return y
+
+
+def build_toy_context(*, ring_dimension, batch, depth, scale_bits, first_mod_bits,
+                      rotations=(), backend=None, seed=None):
+    """CKKS context with TOY security for probes: uniform-ternary secret,
+    FLEXIBLEAUTO, HYBRID, explicit ring dimension and batch; keys for
+    multiplication and the given rotations.  `backend` is any module with
+    the OpenFHE names (default: fhemamba_amd.ckks)."""
+    if backend is None:
+        from . import ckks as backend
+    params = backend.CCParamsCKKSRNS()
+    params.SetSecretKeyDist(backend.SecretKeyDist.UNIFORM_TERNARY)
+    params.SetSecurityLevel(backend.SecurityLevel.HEStd_NotSet)
+    params.SetRingDim(ring_dimension)
+    params.SetScalingTechnique(backend.ScalingTechnique.FLEXIBLEAUTO)
+    params.SetFirstModSize(first_mod_bits)
+    params.SetScalingModSize(scale_bits)
+    params.SetKeySwitchTechnique(backend.KeySwitchTechnique.HYBRID)
+    params.SetMultiplicativeDepth(depth)
+    params.SetBatchSize(batch)
+    cc = backend.GenCryptoContext(params) if seed is None else \
+        backend.GenCryptoContext(params, seed=seed)
+    features = backend.PKESchemeFeature
+    for f in (features.PKE, features.KEYSWITCH, features.LEVELEDSHE, features.ADVANCEDSHE,
+              features.FHE):
+        cc.Enable(f)
+    keys = cc.KeyGen()
+    cc.EvalMultKeyGen(keys.secretKey)
+    if rotations:
+        cc.EvalRotateKeyGen(keys.secretKey, list(rotations))
+    return cc, keys
