@@ -38,7 +38,7 @@ HBM_PEAK = 8.0e12  # B/s, MI355X HBM3E
 # WRITE_SIZE on this workload (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0, the factors
 # a plain copy of known size reads back); recorded in
 # profiles/rotation_step_n65536_l24.md together with the commands.
-MEASURED_TRAFFIC = {"k_ksk_inner": 3_070_409_523 + 1_006_632_960}
+MEASURED_TRAFFIC: dict = {}
 LOG_N, DEPTH, SCALE_BITS, FIRST_BITS, DNUM = 16, 23, 59, 60, 3
 N = 1 << LOG_N
 LIMB = N * 8  # bytes per limb
@@ -349,10 +349,13 @@ def step_kernel_bytes(L: int, K: int, R: int) -> dict:
     """Bytes each kernel of one rotation step must move (read + write once),
     summed over its launches in the step.  R hoisted rotations, ne = L + K
     extended limbs, alpha = ceil(L / dnum) limbs per digit:
-      k_ksk_inner             digits dnum*ne once per batch, per rotation the
-                              key dnum*2*ne read and ext 2*ne written;
-      ntt_fwd_blocks_moddown  per rotation y 2L + ext(Q) 2L + c0 L read,
-                              output 2L written;
+      k_ksk_inner             P limbs of the key inner product: digits dnum*K
+                              once per batch, per rotation the key's P limbs
+                              dnum*2*K read and 2*K written;
+      ntt_fwd_blocks_moddown  last ModDown pass with the Q-limb inner product:
+                              digits dnum*L and c0 L once per batch, per
+                              rotation y 2L and the key's Q limbs dnum*2*L
+                              read, output 2L written;
       k_convert               ModUp: dnum*ne (alpha read, ne-alpha written per
                               digit); ModDown: per rotation 2K read, 2L written;
       ntt_{fwd,inv}_{cols,blocks}  read + write of every limb of the pass:
@@ -362,8 +365,8 @@ def step_kernel_bytes(L: int, K: int, R: int) -> dict:
     alpha = -(-L // DNUM)
     modup_fwd = DNUM * (ne - alpha)
     return {k: v * LIMB for k, v in {
-        "k_ksk_inner": DNUM * ne + R * (DNUM * 2 * ne + 2 * ne),
-        "ntt_fwd_blocks_moddown": R * 7 * L,
+        "k_ksk_inner": DNUM * K + R * (DNUM * 2 * K + 2 * K),
+        "ntt_fwd_blocks_moddown": DNUM * L + L + R * (2 * L + DNUM * 2 * L + 2 * L),
         "k_convert": DNUM * ne + R * 2 * (K + L),
         "ntt_fwd_cols": 2 * (modup_fwd + R * 2 * L),
         "ntt_fwd_blocks": 2 * modup_fwd,

@@ -483,20 +483,17 @@ int fhe_keyswitch(fhe_poly* out, const fhe_poly* a, const fhe_key* key) {
     check_key(a, key);
     need(a->npoly == 1 && a->nlimb >= 1 && a->nlimb <= a->c->L, "keyswitch input is one poly");
     fhe::Context& c = *a->c;
-    const uint32_t nq = a->nlimb, ne = nq + c.K, nd = fhe::num_digits(c, nq);
-    fhe::Scratch dig(c, (size_t)nd * ne * c.n), ext(c, 2 * (size_t)ne * c.n);
-    fhe::modup(c, a->data, nq, dig.p);
-    fhe::ksk_inner(c, dig.p, nq, key->data, ext.p);
+    const uint32_t nq = a->nlimb;
     if (out == a) {
       fhe::Scratch t(c, words(c, 2, nq));
-      fhe::moddown_pair2(c, ext.p, nq, t.p, nullptr, nullptr, 1);
+      fhe::keyswitch(c, a->data, nq, key->data, fhe::KeySwitchOut{t.p, nullptr, nullptr, 1});
       reshape(out, 2, nq);
       fhe::hip_check(hipMemcpyAsync(out->data, t.p, out->bytes, hipMemcpyDeviceToDevice, c.stream),
                      "keyswitch");
       return;
     }
     prepare_out(out, 2, nq);
-    fhe::moddown_pair2(c, ext.p, nq, out->data, nullptr, nullptr, 1);
+    fhe::keyswitch(c, a->data, nq, key->data, fhe::KeySwitchOut{out->data, nullptr, nullptr, 1});
   });
 }
 
@@ -506,12 +503,11 @@ int fhe_relinearize(fhe_poly* out, const fhe_poly* ct3, const fhe_key* key) {
     check_key(ct3, key);
     need(ct3->npoly == 3 && ct3->nlimb <= ct3->c->L, "relinearize needs a 3-poly tensor");
     fhe::Context& c = *ct3->c;
-    const uint32_t nq = ct3->nlimb, ne = nq + c.K, nd = fhe::num_digits(c, nq);
+    const uint32_t nq = ct3->nlimb;
     const size_t pl = (size_t)nq * c.n;
-    fhe::Scratch dig(c, (size_t)nd * ne * c.n), ext(c, 2 * (size_t)ne * c.n), t(c, 2 * pl);
-    fhe::modup(c, ct3->data + 2 * pl, nq, dig.p);
-    fhe::ksk_inner(c, dig.p, nq, key->data, ext.p);
-    fhe::moddown_pair2(c, ext.p, nq, t.p, ct3->data, ct3->data + pl, 1);
+    fhe::Scratch t(c, 2 * pl);
+    fhe::keyswitch(c, ct3->data + 2 * pl, nq, key->data,
+                   fhe::KeySwitchOut{t.p, ct3->data, ct3->data + pl, 1});
     reshape(out, 2, nq);
     fhe::hip_check(hipMemcpyAsync(out->data, t.p, out->bytes, hipMemcpyDeviceToDevice, c.stream),
                    "relinearize");
@@ -525,12 +521,9 @@ int fhe_rotate(fhe_poly* out, const fhe_poly* ct, const fhe_key* key, uint32_t g
     need(ct->npoly == 2 && ct->nlimb <= ct->c->L, "rotate needs a 2-poly ciphertext");
     need((galois & 1) && galois < 2 * ct->c->n, "Galois element must be odd and < 2N");
     fhe::Context& c = *ct->c;
-    const uint32_t nq = ct->nlimb, ne = nq + c.K, nd = fhe::num_digits(c, nq);
-    const size_t pl = (size_t)nq * c.n;
-    fhe::Scratch dig(c, (size_t)nd * ne * c.n), ext(c, 2 * (size_t)ne * c.n), t(c, 2 * pl);
-    fhe::modup(c, ct->data + pl, nq, dig.p);
-    fhe::ksk_inner(c, dig.p, nq, key->data, ext.p);
-    fhe::moddown_pair2(c, ext.p, nq, t.p, ct->data, nullptr, galois);
+    const uint32_t nq = ct->nlimb;
+    fhe::Scratch t(c, 2 * (size_t)nq * c.n);
+    fhe::rotate(c, t.p, ct->data, nq, key->data, galois);
     reshape(out, 2, nq);
     fhe::hip_check(hipMemcpyAsync(out->data, t.p, out->bytes, hipMemcpyDeviceToDevice, c.stream),
                    "rotate");

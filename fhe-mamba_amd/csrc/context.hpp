@@ -206,20 +206,25 @@ struct LaunchScope {
   } while (0)
 
 // Epilogue of the last forward-NTT pass of a batched ModDown.  Launch poly p
-// is key switch r = p / 2, component b = p % 2.  ext's Q limbs already carry
-// the factor P^-1 (folded into the stored keys) and y carries -P^-1 (folded
-// into the ModDown conversion constants), so
+// is key switch r = p / 2, component b = p % 2.  The Q-limb key inner
+// product is formed here,
+//   ext_r[b][i][s] = REDC(sum_j digits[j][i][s] * key_r[j][b][i][s]),
+// and carries the factor P^-1 (folded into the stored keys); y carries -P^-1
+// (folded into the ModDown conversion constants), so
 //   out_r[b][i][d(s)] = ext_r[b][i][s] + y[s] + add_r,b[i][s]
-// equals OpenFHE's (ext - Conv(ext_P)) * P^-1 + add exactly.
-// where d is the inverse of the Galois permutation of element g_r
-// (ginv = g_r^-1 mod 2N; 1 means no permutation).
+// equals OpenFHE's (ext - Conv(ext_P)) * P^-1 + add exactly, where d is the
+// inverse of the Galois permutation of element g_r (ginv = g_r^-1 mod 2N;
+// 1 means no permutation).  One REDC suffices while nd * q_i < 2^64.
 constexpr int MAX_KS_BATCH = 32;
 struct ModDownEpi {
-  const uint64_t* ext;                    // [B][2][ne][N]
+  const uint64_t* digits;                 // [nd][ne][N]
+  const ModConst* mc;
+  const uint64_t* key[MAX_KS_BATCH];      // each [nd][2][L+K][N], Montgomery form
   uint64_t* out[MAX_KS_BATCH];            // each [2][nq][N]
   const uint64_t* add[MAX_KS_BATCH][2];   // [nq][N] or null
   uint32_t ginv[MAX_KS_BATCH];
-  uint32_t ne, nq;
+  size_t kl;                              // words per key component, (L+K) N
+  uint32_t nd, ne, nq;
 };
 
 // ---- kernel launchers (implemented in the .hip files) ----

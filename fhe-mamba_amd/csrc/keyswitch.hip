@@ -131,8 +131,9 @@ __global__ void __launch_bounds__(TPB)
 
 // Key inner product for a batch of B key switches sharing one set of
 // digits (a hoisted rotation set): each thread loads its digit words once
-// and reuses them for every key.  grid (N / (2 blockDim), nq + K, 1).
-// ext is [B][2][ne][N].
+// and reuses them for every key.  grid (N / (2 blockDim), nout, 1) covers
+// extended limbs [limb0, limb0 + nout) (ModDown asks for the P limbs only:
+// the Q limbs are formed in its last NTT pass); ext is [B][2][nout][N].
 constexpr int MAXD = 8;
 struct KeyBatch {
   const uint64_t* key[MAX_KS_BATCH];
@@ -145,8 +146,9 @@ template <int ND>
 __global__ void __launch_bounds__(TPB)
     k_ksk_inner_nd(const uint64_t* __restrict__ digits, const KeyBatch kb,
                    uint64_t* __restrict__ ext, const ModConst* __restrict__ mc, uint32_t n,
-                   uint32_t nq, uint32_t L, uint32_t K, uint32_t batch) {
-  const uint32_t i = blockIdx.y, ne = nq + K;
+                   uint32_t nq, uint32_t L, uint32_t K, uint32_t batch, uint32_t limb0,
+                   uint32_t nout) {
+  const uint32_t i = limb0 + blockIdx.y, ne = nq + K, io = blockIdx.y;
   const uint32_t ki = i < nq ? i : L + (i - nq);
   const uint64_t q = mc[ki].q, qinv = mc[ki].qinv_neg;
   const size_t e = 2 * ((size_t)blockIdx.x * blockDim.x + threadIdx.x);
@@ -164,10 +166,10 @@ __global__ void __launch_bounds__(TPB)
       a1x.mac(d[j].x, ka2[j].x);
       a1y.mac(d[j].y, ka2[j].y);
     }
-    uint64_t* o = ext + (size_t)r * 2 * ne * n;
-    *reinterpret_cast<ulonglong2*>(o + (size_t)i * n + e) =
+    uint64_t* o = ext + (size_t)r * 2 * nout * n;
+    *reinterpret_cast<ulonglong2*>(o + (size_t)io * n + e) =
         make_ulonglong2(redc(a0x.hi, a0x.lo, q, qinv), redc(a0y.hi, a0y.lo, q, qinv));
-    *reinterpret_cast<ulonglong2*>(o + ((size_t)ne + i) * n + e) =
+    *reinterpret_cast<ulonglong2*>(o + ((size_t)nout + io) * n + e) =
         make_ulonglong2(redc(a1x.hi, a1x.lo, q, qinv), redc(a1y.hi, a1y.lo, q, qinv));
   };
   uint32_t r = 0;
@@ -201,8 +203,8 @@ __global__ void __launch_bounds__(TPB)
     k_ksk_inner_batch(const uint64_t* __restrict__ digits, const KeyBatch kb,
                       uint64_t* __restrict__ ext, const ModConst* __restrict__ mc, uint32_t n,
                       uint32_t nq, uint32_t L, uint32_t K, uint32_t nd, uint32_t chunk,
-                      uint32_t batch) {
-  const uint32_t i = blockIdx.y, ne = nq + K;
+                      uint32_t batch, uint32_t limb0, uint32_t nout) {
+  const uint32_t i = limb0 + blockIdx.y, ne = nq + K, io = blockIdx.y;
   const uint32_t ki = i < nq ? i : L + (i - nq);
   const uint64_t q = mc[ki].q, qinv = mc[ki].qinv_neg;
   const size_t e = 2 * ((size_t)blockIdx.x * blockDim.x + threadIdx.x);
@@ -234,9 +236,9 @@ __global__ void __launch_bounds__(TPB)
       r1y = add_mod(r1y, redc(a1y.hi, a1y.lo, q, qinv), q);
       j0 = j1;
     }
-    uint64_t* o = ext + (size_t)r * 2 * ne * n;
-    *reinterpret_cast<ulonglong2*>(o + (size_t)i * n + e) = make_ulonglong2(r0x, r0y);
-    *reinterpret_cast<ulonglong2*>(o + ((size_t)ne + i) * n + e) = make_ulonglong2(r1x, r1y);
+    uint64_t* o = ext + (size_t)r * 2 * nout * n;
+    *reinterpret_cast<ulonglong2*>(o + (size_t)io * n + e) = make_ulonglong2(r0x, r0y);
+    *reinterpret_cast<ulonglong2*>(o + ((size_t)nout + io) * n + e) = make_ulonglong2(r1x, r1y);
   }
 }
 
@@ -336,9 +338,10 @@ void modup(Context& c, const uint64_t* a, uint32_t nq, uint64_t* digits) {
 }
 
 void ksk_inner_batch(Context& c, const uint64_t* digits, uint32_t nq, const uint64_t* const* keys,
-                     uint32_t batch, uint64_t* ext) {
-  if (batch == 0) return;
+                     uint32_t batch, uint64_t* ext, uint32_t limb0, uint32_t nout) {
+  if (batch == 0 || nout == 0) return;
   if (batch > MAX_KS_BATCH) throw ArgError("key-switch batch too large");
+  if (limb0 + nout > nq + c.K) throw ArgError("inner product limbs out of range");
   const uint32_t nd = num_digits(c, nq);
   if (nd > MAXD) throw ArgError("more than 8 key-switching digits");
   std::vector<uint32_t> all(c.L + c.K);
@@ -346,21 +349,21 @@ void ksk_inner_batch(Context& c, const uint64_t* digits, uint32_t nq, const uint
   KeyBatch kb{};
   for (uint32_t r = 0; r < batch; ++r) kb.key[r] = keys[r];
   const uint32_t tpb = tpb_for(c, 2);
-  const dim3 grid(c.n / (2 * tpb), nq + c.K, 1);
+  const dim3 grid(c.n / (2 * tpb), nout, 1);
   if (nd <= redc_chunk(c, all)) {
     switch (nd) {
 #define CASE(D)                                                                                \
   case D:                                                                                      \
     FHE_LAUNCH(c, "k_ksk_inner", k_ksk_inner_nd<D>, grid, dim3(tpb), 0, digits, kb, ext,      \
-               c.d_const, c.n, nq, c.L, c.K, batch);                                           \
+               c.d_const, c.n, nq, c.L, c.K, batch, limb0, nout);                              \
     return;
       CASE(1) CASE(2) CASE(3) CASE(4) CASE(5) CASE(6) CASE(7) CASE(8)
 #undef CASE
       default: break;
     }
   }
-  FHE_LAUNCH(c, "k_ksk_inner", k_ksk_inner_batch, dim3(c.n / (2 * tpb), nq + c.K, 1), dim3(tpb), 0,
-             digits, kb, ext, c.d_const, c.n, nq, c.L, c.K, nd, redc_chunk(c, all), batch);
+  FHE_LAUNCH(c, "k_ksk_inner", k_ksk_inner_batch, grid, dim3(tpb), 0, digits, kb, ext, c.d_const,
+             c.n, nq, c.L, c.K, nd, redc_chunk(c, all), batch, limb0, nout);
 }
 
 uint32_t galois_inverse(uint32_t g, uint32_t n) {
@@ -373,21 +376,30 @@ uint32_t galois_inverse(uint32_t g, uint32_t n) {
   return (uint32_t)r;
 }
 
-void moddown_batch(Context& c, uint64_t* ext, uint32_t nq, uint32_t batch,
-                   const KeySwitchOut* outs) {
+void keyswitch_batch(Context& c, const uint64_t* digits, uint32_t nq,
+                     const uint64_t* const* keys, uint32_t batch, const KeySwitchOut* outs) {
   if (batch == 0) return;
   if (batch > MAX_KS_BATCH) throw ArgError("key-switch batch too large");
-  const size_t n = c.n, ne = nq + c.K;
-  Scratch y(c, 2 * (size_t)batch * nq * n);
-  // The P limbs of ext are taken to coefficient form in place (ext is scratch).
-  ntt_inverse(c, ext + (size_t)nq * n, 2 * batch, ne * n, c.K, LimbMap::contiguous(c.L));
-  convert(c, c.moddown_plan(nq), ext + (size_t)nq * n, ne * n, y.p, (size_t)nq * n, nq,
-          2 * batch);
+  if (c.K == 0) throw ArgError("key switching needs special primes");
+  const uint32_t nd = num_digits(c, nq);
+  if (nd > MAXD) throw ArgError("more than 8 key-switching digits");
+  const size_t n = c.n, ne = nq + c.K, kw = (size_t)c.K * n;
+  // The fused Q-limb products are reduced once: nd * q_i < 2^64 holds for
+  // nd <= 8 and q_i < 2^61.
+  Scratch ext(c, 2 * (size_t)batch * kw), y(c, 2 * (size_t)batch * nq * n);
+  // P limbs of the inner product, to coefficient form, converted to Q.
+  ksk_inner_batch(c, digits, nq, keys, batch, ext.p, nq, c.K);
+  ntt_inverse(c, ext.p, 2 * batch, kw, c.K, LimbMap::contiguous(c.L));
+  convert(c, c.moddown_plan(nq), ext.p, kw, y.p, (size_t)nq * n, nq, 2 * batch);
   ModDownEpi epi{};
-  epi.ext = ext;
+  epi.digits = digits;
+  epi.mc = c.d_const;
+  epi.kl = (size_t)(c.L + c.K) * n;
+  epi.nd = nd;
   epi.ne = (uint32_t)ne;
   epi.nq = nq;
   for (uint32_t r = 0; r < batch; ++r) {
+    epi.key[r] = keys[r];
     epi.out[r] = outs[r].out;
     epi.add[r][0] = outs[r].add0;
     epi.add[r][1] = outs[r].add1;
@@ -396,43 +408,25 @@ void moddown_batch(Context& c, uint64_t* ext, uint32_t nq, uint32_t batch,
   ntt_forward_moddown(c, y.p, 2 * batch, nq, epi);
 }
 
-void ksk_inner(Context& c, const uint64_t* digits, uint32_t nq, const uint64_t* key_mont,
-               uint64_t* ext) {
-  ksk_inner_batch(c, digits, nq, &key_mont, 1, ext);
-}
-
-void moddown_pair2(Context& c, uint64_t* ext, uint32_t nq, uint64_t* out, const uint64_t* add0,
-                   const uint64_t* add1, uint32_t galois) {
-  const KeySwitchOut o{out, add0, add1, galois};
-  moddown_batch(c, ext, nq, 1, &o);
-}
-
-void moddown_pair(Context& c, uint64_t* ext, uint32_t nq, uint64_t* out, const uint64_t* add0,
-                  uint32_t galois) {
-  moddown_pair2(c, ext, nq, out, add0, nullptr, galois);
-}
-
 void keyswitch_hoisted(Context& c, const uint64_t* digits, uint32_t nq,
                        const uint64_t* const* keys, const KeySwitchOut* outs, uint32_t count) {
-  const size_t ext_words = 2 * (size_t)(nq + c.K) * c.n;
-  const size_t per_rot = (ext_words + 2 * (size_t)nq * c.n) * 8;
+  const size_t per_rot = 2 * (size_t)(c.K + nq) * c.n * 8;
   uint32_t batch = (uint32_t)std::max<size_t>(1, (size_t(2) << 30) / per_rot);
   batch = std::min<uint32_t>(batch, MAX_KS_BATCH);
-  for (uint32_t r0 = 0; r0 < count; r0 += batch) {
-    const uint32_t b = std::min(batch, count - r0);
-    Scratch ext(c, b * ext_words);
-    ksk_inner_batch(c, digits, nq, keys + r0, b, ext.p);
-    moddown_batch(c, ext.p, nq, b, outs + r0);
-  }
+  for (uint32_t r0 = 0; r0 < count; r0 += batch)
+    keyswitch_batch(c, digits, nq, keys + r0, std::min(batch, count - r0), outs + r0);
+}
+
+void keyswitch(Context& c, const uint64_t* a, uint32_t nq, const uint64_t* key,
+               const KeySwitchOut& out) {
+  Scratch dig(c, num_digits(c, nq) * (size_t)(nq + c.K) * c.n);
+  modup(c, a, nq, dig.p);
+  keyswitch_batch(c, dig.p, nq, &key, 1, &out);
 }
 
 void rotate(Context& c, uint64_t* out, const uint64_t* ct, uint32_t nq, const uint64_t* key,
             uint32_t galois) {
-  const size_t ne = nq + c.K;
-  Scratch dig(c, num_digits(c, nq) * ne * c.n), ext(c, 2 * ne * c.n);
-  modup(c, ct + (size_t)nq * c.n, nq, dig.p);
-  ksk_inner(c, dig.p, nq, key, ext.p);
-  moddown_pair(c, ext.p, nq, out, ct, galois);
+  keyswitch(c, ct + (size_t)nq * c.n, nq, key, KeySwitchOut{out, ct, nullptr, galois});
 }
 
 void linear_transform(Context& c, uint64_t* out, const uint64_t* ct, uint32_t nq,
@@ -466,7 +460,7 @@ void linear_transform(Context& c, uint64_t* out, const uint64_t* ct, uint32_t nq
     keyswitch_hoisted(c, dig.p, nq, keys.data(), outs.data(), (uint32_t)keys.size());
   }
   // Giant steps by Horner's rule: acc = inner_{G-1}; acc = inner_g + rot(acc).
-  Scratch acc0(c, pl), acc1(c, pl), ext(c, 2 * ne * n);
+  Scratch acc0(c, pl), acc1(c, pl);
   uint64_t* cur = acc0.p;
   uint64_t* nxt = acc1.p;
   std::vector<const uint64_t*> xs, ws;
@@ -485,8 +479,8 @@ void linear_transform(Context& c, uint64_t* out, const uint64_t* ct, uint32_t nq
   inner(giants - 1, cur, false);
   for (int g = (int)giants - 2; g >= 0; --g) {
     modup(c, cur + (size_t)nq * n, nq, dig.p);
-    ksk_inner(c, dig.p, nq, giant_key, ext.p);
-    moddown_pair(c, ext.p, nq, nxt, cur, giant_galois);
+    const KeySwitchOut ko{nxt, cur, nullptr, giant_galois};
+    keyswitch_batch(c, dig.p, nq, &giant_key, 1, &ko);
     inner((uint32_t)g, nxt, true);
     std::swap(cur, nxt);
   }

@@ -45,7 +45,8 @@ __device__ __forceinline__ uint32_t lds_idx(uint32_t line, uint32_t u, uint32_t 
   return line * pitch + u + (u >> 4);
 }
 
-// Final stores go through `store(base, offset_in_limb, value, q)`.
+// Final stores go through `store.fin(base, offset_in_limb, value, t, q)`,
+// with t = store.pre(offset_in_limb, q) when Store::kPre.
 template <int S, int KIND, bool INV, class Store>
 __device__ __forceinline__ void ntt_body(uint64_t* __restrict__ data, size_t poly_stride,
                                          const ModConst* __restrict__ mc,
@@ -77,6 +78,7 @@ __device__ __forceinline__ void ntt_body(uint64_t* __restrict__ data, size_t pol
   const uint32_t twbase = KIND == BLOCKS ? (1u << s_other) + gline : 1u;
 
   uint64_t x[R];
+  uint64_t pre[Store::kPre ? R : 1];
 
 #pragma unroll
   for (int sp = 0; sp < NSP; ++sp) {
@@ -126,6 +128,22 @@ __device__ __forceinline__ void ntt_body(uint64_t* __restrict__ data, size_t pol
       for (int v = 0; v < R; ++v) {
         const uint32_t u = thi | ((uint32_t)v << w) | tlo;
         x[v] = lds[lds_idx(line, u, G::PITCH)];
+      }
+    }
+    // Store-side terms for this thread's final positions, loaded ahead of the
+    // butterflies: with the first sub-pass when the final window is
+    // contiguous (staged positions do not depend on the window), else with
+    // the last one.
+    constexpr bool kFinalContig = !INV && KIND != COLS;
+    if (Store::kPre && last && sp == (kFinalContig ? 0 : NSP - 1)) {
+      const size_t wg0 = ((size_t)blockIdx.x * LINES) << S;
+#pragma unroll
+      for (int k = 0; k < R; ++k) {
+        const uint32_t u = thi | ((uint32_t)k << w) | tlo;
+        const size_t g = kFinalContig ? wg0 + (size_t)k * blockDim.x + tid
+                         : KIND == COLS ? gline + ((size_t)u << s_other)
+                                        : ((size_t)gline << S) + u;
+        pre[Store::kPre ? k : 0] = store.pre(g, q);
       }
     }
 
@@ -188,7 +206,8 @@ __device__ __forceinline__ void ntt_body(uint64_t* __restrict__ data, size_t pol
 #pragma unroll
         for (int k = 0; k < R; ++k) {
           const uint32_t p = k * blockDim.x + tid;
-          store(base, wg0 + p, lds[lds_idx(p >> S, p & (G::LEN - 1), G::PITCH)], q);
+          store.fin(base, wg0 + p, lds[lds_idx(p >> S, p & (G::LEN - 1), G::PITCH)],
+                    pre[Store::kPre ? k : 0], q);
         }
       } else {
 #pragma unroll
@@ -196,7 +215,7 @@ __device__ __forceinline__ void ntt_body(uint64_t* __restrict__ data, size_t pol
           const uint32_t u = thi | ((uint32_t)v << w) | tlo;
           const size_t g =
               KIND == COLS ? gline + ((size_t)u << s_other) : ((size_t)gline << S) + u;
-          store(base, g, x[v], q);
+          store.fin(base, g, x[v], pre[Store::kPre ? v : 0], q);
         }
       }
     } else {
@@ -210,9 +229,15 @@ __device__ __forceinline__ void ntt_body(uint64_t* __restrict__ data, size_t pol
   }
 }
 
+// Store functors of the last pass.  kPre: the store adds a term t(s) that
+// does not depend on the transform (pre), loaded for all of a thread's
+// positions before the last sub-pass so its global loads overlap the
+// butterflies; fin then writes f(y, t).
 struct PlainStore {
-  __device__ __forceinline__ void operator()(uint64_t* base, size_t g, uint64_t v,
-                                             uint64_t) const {
+  static constexpr bool kPre = false;
+  __device__ __forceinline__ uint64_t pre(size_t, uint64_t) const { return 0; }
+  __device__ __forceinline__ void fin(uint64_t* base, size_t g, uint64_t v, uint64_t,
+                                      uint64_t) const {
     base[g] = v;
   }
 };
@@ -224,14 +249,28 @@ __device__ __forceinline__ uint32_t brev_bits(uint32_t x, uint32_t bits) {
 // ModDown epilogue (see ModDownEpi): the value at evaluation slot s goes to
 // slot d(s) of the output, d being the inverse Galois permutation.
 struct EpiStore {
+  static constexpr bool kPre = true;
   const ModDownEpi& e;
   uint32_t n, log_n;
-  __device__ __forceinline__ void operator()(uint64_t*, size_t s, uint64_t y, uint64_t q) const {
+  // Q-limb key inner product plus the addend at position s.
+  __device__ __forceinline__ uint64_t pre(size_t s, uint64_t q) const {
     const uint32_t p = blockIdx.y, r = p >> 1, b = p & 1, i = blockIdx.z;
-    const uint64_t ev = e.ext[((size_t)p * e.ne + i) * n + s];
-    uint64_t res = add_mod(ev, y, q);
+    const uint64_t* dg = e.digits + (size_t)i * n + s;
+    const uint64_t* kr = e.key[r] + (size_t)b * e.kl + (size_t)i * n + s;
+    const size_t dstride = (size_t)e.ne * n, kstride = 2 * e.kl;
+    Acc128 acc;
+#pragma unroll
+    for (uint32_t j = 0; j < 8; ++j)
+      if (j < e.nd) acc.mac(dg[j * dstride], kr[j * kstride]);
+    uint64_t t = redc(acc.hi, acc.lo, q, e.mc[i].qinv_neg);
     const uint64_t* add = e.add[r][b];
-    if (add) res = add_mod(res, add[(size_t)i * n + s], q);
+    if (add) t = add_mod(t, add[(size_t)i * n + s], q);
+    return t;
+  }
+  __device__ __forceinline__ void fin(uint64_t*, size_t s, uint64_t y, uint64_t t,
+                                      uint64_t q) const {
+    const uint32_t p = blockIdx.y, r = p >> 1, b = p & 1, i = blockIdx.z;
+    const uint64_t res = add_mod(t, y, q);
     uint32_t d = (uint32_t)s;
     const uint32_t gi = e.ginv[r];
     if (gi != 1) {

@@ -48,29 +48,29 @@ void poly_rescale(Context& c, uint64_t* out, const uint64_t* a, uint32_t npoly, 
 uint32_t num_digits(const Context& c, uint32_t nq);
 // Digits [nd][nq+K][N] (evaluation form) of a [nq][N].
 void modup(Context& c, const uint64_t* a, uint32_t nq, uint64_t* digits);
-// ext [2][nq+K][N] = sum_j digits_j (.) key_j (key in Montgomery form).
-void ksk_inner(Context& c, const uint64_t* digits, uint32_t nq, const uint64_t* key_mont,
-               uint64_t* ext);
-// out_b = galois-permute((ext_b[Q] - ModDownConv(ext_b[P])) * P^-1 + add_b), b = 0, 1,
-// with addends add0 / add1 ([nq][N], may be null); galois 1 means no permutation.
-// The P limbs of ext are overwritten (taken to coefficient form in place).
-void moddown_pair2(Context& c, uint64_t* ext, uint32_t nq, uint64_t* out, const uint64_t* add0,
-                   const uint64_t* add1, uint32_t galois);
-void moddown_pair(Context& c, uint64_t* ext, uint32_t nq, uint64_t* out, const uint64_t* add0,
-                  uint32_t galois);
-// Batched key switching for a hoisted set: ext [B][2][nq+K][N] from one set
-// of digits and B keys, then one ModDown for all B with the combine fused
-// into the last NTT pass.  Output r must not alias its addends.
+// Result of one key switch r of a batch:
+//   out_b = galois-permute((ext_b[Q] - ModDownConv(ext_b[P])) * P^-1 + add_b),
+// b = 0, 1, with ext_b = sum_j digits_j (.) key_r,j,b over Q_l + P, addends
+// add0 / add1 ([nq][N], may be null) and galois 1 meaning no permutation.
+// out must not alias its addends.
 struct KeySwitchOut {
   uint64_t* out;         // [2][nq][N]
   const uint64_t* add0;  // added to component 0 (or null)
   const uint64_t* add1;  // added to component 1 (or null)
   uint32_t galois;       // Galois element applied to the result (1 = none)
 };
+// Key inner product over extended limbs [limb0, limb0 + nout) (keys in
+// Montgomery form) into ext [B][2][nout][N].
 void ksk_inner_batch(Context& c, const uint64_t* digits, uint32_t nq, const uint64_t* const* keys,
-                     uint32_t batch, uint64_t* ext);
-void moddown_batch(Context& c, uint64_t* ext, uint32_t nq, uint32_t batch,
-                   const KeySwitchOut* outs);
+                     uint32_t batch, uint64_t* ext, uint32_t limb0, uint32_t nout);
+// B <= MAX_KS_BATCH key switches of one set of digits: the P limbs of the
+// inner product, one batched ModDown, and the Q-limb products, combine and
+// Galois permutation in its last NTT pass.
+void keyswitch_batch(Context& c, const uint64_t* digits, uint32_t nq,
+                     const uint64_t* const* keys, uint32_t batch, const KeySwitchOut* outs);
+// ModUp of a [nq][N] (evaluation form) and one key switch.
+void keyswitch(Context& c, const uint64_t* a, uint32_t nq, const uint64_t* key,
+               const KeySwitchOut& out);
 // `count` key switches of one set of digits (keys[r] in Montgomery form), in
 // batches that share one read of the digits (scratch per batch <= 2 GiB).
 void keyswitch_hoisted(Context& c, const uint64_t* digits, uint32_t nq,
