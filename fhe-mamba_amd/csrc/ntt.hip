@@ -13,7 +13,8 @@
 //   BLOCKS line b in [0, N1): elements b*N2 + u, u in [0, N2)  (the last
 //          S2 = floor(logN/2) stages)
 // Rings with logN <= 12 use one launch (SINGLE) per limb.  Each thread
-// holds 16 elements in registers and runs 4 stages at a time (radix-16);
+// holds 16 elements in registers and runs 4 stages at a time (radix-16;
+// the ModDown epilogue pass holds 8 and runs 3, see RHO_EPILOGUE);
 // sub-passes exchange through an LDS tile padded by one word per 16 words,
 // which keeps both the stride-1 and the stride-16 access patterns free of
 // bank conflicts.  Workgroups are 256 threads (4096 elements, ~35 KB LDS).
@@ -30,12 +31,17 @@
 namespace fhe {
 namespace {
 
-constexpr int RHO = 4;
-constexpr int R = 1 << RHO;
 enum Kind { SINGLE = 0, COLS = 1, BLOCKS = 2 };
 
-template <int S>
+// RHO stages per sub-pass, radix 2^RHO per thread.  Plain passes are
+// ALU-bound and use radix 16 (two sub-passes for 8 stages); the ModDown
+// epilogue pass uses radix 8 in its two-launch form: half the LDS and
+// registers per wave, so twice the waves to cover its extra global loads.
+constexpr int RHO_PLAIN = 4, RHO_EPILOGUE = 3;
+
+template <int S, int RHO_>
 struct Geo {
+  static constexpr int RHO = RHO_;
   static constexpr int TPL = 1 << (S - RHO);  // threads per line
   static constexpr int LEN = 1 << S;
   static constexpr int PITCH = LEN + LEN / 16 + 1;
@@ -47,13 +53,15 @@ __device__ __forceinline__ uint32_t lds_idx(uint32_t line, uint32_t u, uint32_t 
 
 // Final stores go through `store.fin(base, offset_in_limb, value, t, q)`,
 // with t = store.pre(offset_in_limb, q) when Store::kPre.
-template <int S, int KIND, bool INV, class Store>
+template <int S, int KIND, bool INV, int RHO_, class Store>
 __device__ __forceinline__ void ntt_body(uint64_t* __restrict__ data, size_t poly_stride,
                                          const ModConst* __restrict__ mc,
                                          const uint64_t* __restrict__ tw_all, uint32_t log_n,
                                          LimbMap map, uint32_t s_other, int last,
                                          const Store& store) {
-  using G = Geo<S>;
+  using G = Geo<S, RHO_>;
+  constexpr int RHO = G::RHO;
+  constexpr int R = 1 << RHO;
   constexpr int LINES = KIND == SINGLE ? 1 : 256 / G::TPL;
   constexpr int NSP = (S + RHO - 1) / RHO;
   __shared__ uint64_t lds[LINES * G::PITCH];
@@ -247,7 +255,9 @@ __device__ __forceinline__ uint32_t brev_bits(uint32_t x, uint32_t bits) {
 }
 
 // ModDown epilogue (see ModDownEpi): the value at evaluation slot s goes to
-// slot d(s) of the output, d being the inverse Galois permutation.
+// slot d(s) of the output, d being the inverse Galois permutation.  ND > 0
+// fixes the digit count at compile time (ND = 0: e.nd at run time).
+template <int ND>
 struct EpiStore {
   static constexpr bool kPre = true;
   const ModDownEpi& e;
@@ -259,9 +269,12 @@ struct EpiStore {
     const uint64_t* kr = e.key[r] + (size_t)b * e.kl + (size_t)i * n + s;
     const size_t dstride = (size_t)e.ne * n, kstride = 2 * e.kl;
     Acc128 acc;
+    if (ND > 0) {
 #pragma unroll
-    for (uint32_t j = 0; j < 8; ++j)
-      if (j < e.nd) acc.mac(dg[j * dstride], kr[j * kstride]);
+      for (int j = 0; j < ND; ++j) acc.mac(dg[j * dstride], kr[j * kstride]);
+    } else {
+      for (uint32_t j = 0; j < e.nd; ++j) acc.mac(dg[j * dstride], kr[j * kstride]);
+    }
     uint64_t t = redc(acc.hi, acc.lo, q, e.mc[i].qinv_neg);
     const uint64_t* add = e.add[r][b];
     if (add) t = add_mod(t, add[(size_t)i * n + s], q);
@@ -288,23 +301,30 @@ __global__ void __launch_bounds__(256)
     ntt_pass(uint64_t* __restrict__ data, size_t poly_stride, const ModConst* __restrict__ mc,
              const uint64_t* __restrict__ tw_all, uint32_t log_n, LimbMap map, uint32_t s_other,
              int last) {
-  ntt_body<S, KIND, INV>(data, poly_stride, mc, tw_all, log_n, map, s_other, last, PlainStore{});
+  ntt_body<S, KIND, INV, RHO_PLAIN>(data, poly_stride, mc, tw_all, log_n, map, s_other, last,
+                                    PlainStore{});
 }
 
 // Last forward pass of a batched ModDown (BLOCKS or SINGLE kind).
 template <int S, int KIND>
+constexpr int epilogue_rho() {
+  return KIND == SINGLE ? RHO_PLAIN : RHO_EPILOGUE;
+}
+
+template <int S, int KIND, int ND>
 __global__ void __launch_bounds__(256)
     ntt_pass_moddown(uint64_t* __restrict__ data, size_t poly_stride,
                      const ModConst* __restrict__ mc, const uint64_t* __restrict__ tw_all,
                      uint32_t log_n, uint32_t s_other, const ModDownEpi epi) {
-  ntt_body<S, KIND, false>(data, poly_stride, mc, tw_all, log_n, LimbMap::contiguous(0), s_other,
-                           1, EpiStore{epi, 1u << log_n, log_n});
+  ntt_body<S, KIND, false, epilogue_rho<S, KIND>()>(data, poly_stride, mc, tw_all, log_n,
+                                                    LimbMap::contiguous(0), s_other, 1,
+                                                    EpiStore<ND>{epi, 1u << log_n, log_n});
 }
 
 template <int S, int KIND, bool INV>
 void launch_pass(Context& c, uint64_t* data, uint32_t npoly, size_t poly_stride, uint32_t nlimb,
                  LimbMap map, uint32_t s_other, bool last) {
-  using G = Geo<S>;
+  using G = Geo<S, RHO_PLAIN>;
   const uint32_t lines = KIND == SINGLE ? 1 : 256 / G::TPL;
   const uint32_t threads = KIND == SINGLE ? G::TPL : 256;
   // COLS has N2 = 2^s_other lines per limb, BLOCKS has N1 = 2^s_other.
@@ -355,13 +375,23 @@ void launch_blocks(Context& c, uint32_t s1, uint32_t s2, uint64_t* data, uint32_
 template <int S, int KIND>
 void launch_moddown(Context& c, uint64_t* y, uint32_t npoly, uint32_t nq, uint32_t s_other,
                     const ModDownEpi& epi) {
-  using G = Geo<S>;
+  using G = Geo<S, epilogue_rho<S, KIND>()>;
   const uint32_t lines = KIND == SINGLE ? 1 : 256 / G::TPL;
   const uint32_t threads = KIND == SINGLE ? G::TPL : 256;
   const uint32_t tiles = KIND == SINGLE ? 1 : (1u << s_other) / lines;
-  FHE_LAUNCH(c, KIND == SINGLE ? "ntt_fwd_single_moddown" : "ntt_fwd_blocks_moddown",
-             (ntt_pass_moddown<S, KIND>), dim3(tiles, npoly, nq), dim3(threads), 0, y,
-             (size_t)nq * c.n, c.d_const, c.d_tw_fwd, c.log_n, s_other, epi);
+  const char* name = KIND == SINGLE ? "ntt_fwd_single_moddown" : "ntt_fwd_blocks_moddown";
+  switch (epi.nd) {
+#define CASE(D)                                                                               \
+  case D:                                                                                     \
+    FHE_LAUNCH(c, name, (ntt_pass_moddown<S, KIND, D>), dim3(tiles, npoly, nq), dim3(threads), \
+               0, y, (size_t)nq * c.n, c.d_const, c.d_tw_fwd, c.log_n, s_other, epi);         \
+    return;
+    CASE(1) CASE(2) CASE(3)
+#undef CASE
+    default:
+      FHE_LAUNCH(c, name, (ntt_pass_moddown<S, KIND, 0>), dim3(tiles, npoly, nq), dim3(threads), 0,
+                 y, (size_t)nq * c.n, c.d_const, c.d_tw_fwd, c.log_n, s_other, epi);
+  }
 }
 
 }  // namespace
