@@ -349,9 +349,10 @@ def step_kernel_bytes(L: int, K: int, R: int) -> dict:
     """Bytes each kernel of one rotation step must move (read + write once),
     summed over its launches in the step.  R hoisted rotations, ne = L + K
     extended limbs, alpha = ceil(L / dnum) limbs per digit:
-      k_ksk_inner             P limbs of the key inner product: digits dnum*K
-                              once per batch, per rotation the key's P limbs
-                              dnum*2*K read and 2*K written;
+      ntt_inv_blocks_ksk      first inverse ModDown pass, fed by the P-limb
+                              key inner product: digits dnum*K once per batch,
+                              per rotation the key's P limbs dnum*2*K read and
+                              2*K written;
       ntt_fwd_blocks_moddown  last ModDown pass with the Q-limb inner product:
                               digits dnum*L and c0 L once per batch, per
                               rotation y 2L and the key's Q limbs dnum*2*L
@@ -360,18 +361,19 @@ def step_kernel_bytes(L: int, K: int, R: int) -> dict:
                               digit); ModDown: per rotation 2K read, 2L written;
       ntt_{fwd,inv}_{cols,blocks}  read + write of every limb of the pass:
                               forward ModUp dnum*(ne-alpha) + ModDown R*2L
-                              (cols only), inverse ModUp L + ModDown R*2K."""
+                              (cols only), inverse blocks ModUp L, inverse
+                              cols ModUp L + ModDown R*2K."""
     ne = L + K
     alpha = -(-L // DNUM)
     modup_fwd = DNUM * (ne - alpha)
     return {k: v * LIMB for k, v in {
-        "k_ksk_inner": DNUM * K + R * (DNUM * 2 * K + 2 * K),
+        "ntt_inv_blocks_ksk": DNUM * K + R * (DNUM * 2 * K + 2 * K),
         "ntt_fwd_blocks_moddown": DNUM * L + L + R * (2 * L + DNUM * 2 * L + 2 * L),
         "k_convert": DNUM * ne + R * 2 * (K + L),
         "ntt_fwd_cols": 2 * (modup_fwd + R * 2 * L),
         "ntt_fwd_blocks": 2 * modup_fwd,
         "ntt_inv_cols": 2 * (L + R * 2 * K),
-        "ntt_inv_blocks": 2 * (L + R * 2 * K),
+        "ntt_inv_blocks": 2 * L,
     }.items()}
 
 

@@ -162,6 +162,27 @@ struct LimbMap {
     return j < split ? base0 + j : base1 + (j - split);
   }
   static FHE_HD LimbMap contiguous(uint32_t limb0) { return LimbMap{0xffffffffu, limb0, 0}; }
+  // Launch slot j of any poly: limb position j, modulus (*this)(j).
+  FHE_HD bool resolve(uint32_t, uint32_t j, uint32_t& pos, uint32_t& mod) const {
+    pos = j;
+    mod = (*this)(j);
+    return true;
+  }
+};
+
+// The converted limbs of ModUp digits [nd][ne][N]: digit (poly) d keeps its
+// own limbs [d*alpha, min((d+1)*alpha, nq)) of Q; slot t walks the other
+// limbs of Q_l + P in order (position pos, modulus pos < nq ? pos :
+// L + pos - nq).  Slots past the digit's count are not launched work.
+struct DigitMap {
+  uint32_t alpha, nq, L, ne;
+  FHE_HD bool resolve(uint32_t d, uint32_t t, uint32_t& pos, uint32_t& mod) const {
+    const uint32_t s = d * alpha, e = s + alpha < nq ? s + alpha : nq, w = e - s;
+    if (t + w >= ne) return false;
+    pos = t < s ? t : t + w;
+    mod = pos < nq ? pos : L + (pos - nq);
+    return true;
+  }
 };
 
 // Stream-ordered scratch buffer from the context pool.  Released back to the
@@ -224,7 +245,7 @@ struct ModDownEpi {
   const uint64_t* add[MAX_KS_BATCH][2];   // [nq][N] or null
   uint32_t ginv[MAX_KS_BATCH];
   size_t kl;                              // words per key component, (L+K) N
-  uint32_t nd, ne, nq;
+  uint32_t nd, ne, nq, L;
 };
 
 // ---- kernel launchers (implemented in the .hip files) ----
@@ -236,5 +257,12 @@ void ntt_inverse(Context& c, uint64_t* data, uint32_t npoly, size_t poly_stride,
 // through the ModDown epilogue instead of writing y back.
 void ntt_forward_moddown(Context& c, uint64_t* y, uint32_t npoly, uint32_t nq,
                          const ModDownEpi& epi);
+// Inverse NTT into ext_p [2B][K][N] of the P-limb key inner products
+//   ext_p[2r+b][t][s] = REDC(sum_j digits[j][nq+t][s] * key_r[j][b][L+t][s]),
+// formed while the first pass loads its input (epi.digits / key / mc / kl /
+// nd / ne / nq / L are used; the output fields are not).
+void ntt_inverse_ksk(Context& c, uint64_t* ext_p, uint32_t npoly, const ModDownEpi& epi);
+// Forward NTT of the converted limbs of all nd ModUp digits [nd][nq+K][N].
+void ntt_forward_digits(Context& c, uint64_t* digits, uint32_t nd, uint32_t nq);
 
 }  // namespace fhe

@@ -85,16 +85,13 @@ __global__ void __launch_bounds__(TPB)
 // grid (N / blockDim, ceil(ndst / tch), npoly): each thread converts one
 // coefficient for `tch` consecutive targets.
 template <int NSRC>
-__global__ void __launch_bounds__(TPB)
-    k_convert60(const uint64_t* __restrict__ src, size_t src_ps, uint64_t* __restrict__ out,
-                size_t out_ps, const ModConst* __restrict__ mc,
-                const uint32_t* __restrict__ src_idx, const uint64_t* __restrict__ qhat_inv,
-                const uint64_t* __restrict__ qhat_mont, const uint32_t* __restrict__ dst_idx,
-                uint32_t ndst, uint32_t n, uint32_t L, uint32_t out_nq, uint32_t tch) {
+__device__ __forceinline__ void convert60_body(
+    const uint64_t* __restrict__ s, uint64_t* __restrict__ o, const ModConst* __restrict__ mc,
+    const uint32_t* __restrict__ src_idx, const uint64_t* __restrict__ qhat_inv,
+    const uint64_t* __restrict__ qhat_mont, const uint32_t* __restrict__ dst_idx, uint32_t ndst,
+    uint32_t n, uint32_t L, uint32_t out_nq, uint32_t tch) {
   constexpr uint32_t M30 = (1u << 30) - 1;
   const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const uint64_t* s = src + (size_t)blockIdx.z * src_ps;
-  uint64_t* o = out + (size_t)blockIdx.z * out_ps;
   uint32_t vl[NSRC], vh[NSRC];
 #pragma unroll
   for (int i = 0; i < NSRC; ++i) {
@@ -129,118 +126,46 @@ __global__ void __launch_bounds__(TPB)
   }
 }
 
-// Key inner product for a batch of B key switches sharing one set of
-// digits (a hoisted rotation set): each thread loads its digit words once
-// and reuses them for every key.  grid (N / (2 blockDim), nout, 1) covers
-// extended limbs [limb0, limb0 + nout) (ModDown asks for the P limbs only:
-// the Q limbs are formed in its last NTT pass); ext is [B][2][nout][N].
+// grid (N / blockDim, ceil(ndst / tch), npoly): each thread converts one
+// coefficient of poly blockIdx.z for `tch` consecutive targets.
+template <int NSRC>
+__global__ void __launch_bounds__(TPB)
+    k_convert60(const uint64_t* __restrict__ src, size_t src_ps, uint64_t* __restrict__ out,
+                size_t out_ps, const ModConst* __restrict__ mc,
+                const uint32_t* __restrict__ src_idx, const uint64_t* __restrict__ qhat_inv,
+                const uint64_t* __restrict__ qhat_mont, const uint32_t* __restrict__ dst_idx,
+                uint32_t ndst, uint32_t n, uint32_t L, uint32_t out_nq, uint32_t tch) {
+  convert60_body<NSRC>(src + (size_t)blockIdx.z * src_ps, out + (size_t)blockIdx.z * out_ps, mc,
+                       src_idx, qhat_inv, qhat_mont, dst_idx, ndst, n, L, out_nq, tch);
+}
+
+// ModUp conversion of several digits in one launch: digit d = blockIdx.z
+// converts its limbs coef[src_off[d] ..) with its own plan into digits[d].
 constexpr int MAXD = 8;
-struct KeyBatch {
-  const uint64_t* key[MAX_KS_BATCH];
+struct DigitPlans {
+  const uint32_t* src_idx[MAXD];
+  const uint64_t* qhat_inv[MAXD];
+  const uint64_t* qhat_mont[MAXD];
+  const uint32_t* dst_idx[MAXD];
+  uint32_t ndst[MAXD];
+  uint32_t src_limb[MAXD];
 };
 
-// Specialisation for ND digits whose sum of products fits one REDC
-// (ND * max q < 2^64): rotations are taken two at a time so twelve 16-byte
-// key loads are in flight per thread before any product.
-template <int ND>
+template <int NSRC>
 __global__ void __launch_bounds__(TPB)
-    k_ksk_inner_nd(const uint64_t* __restrict__ digits, const KeyBatch kb,
-                   uint64_t* __restrict__ ext, const ModConst* __restrict__ mc, uint32_t n,
-                   uint32_t nq, uint32_t L, uint32_t K, uint32_t batch, uint32_t limb0,
-                   uint32_t nout) {
-  const uint32_t i = limb0 + blockIdx.y, ne = nq + K, io = blockIdx.y;
-  const uint32_t ki = i < nq ? i : L + (i - nq);
-  const uint64_t q = mc[ki].q, qinv = mc[ki].qinv_neg;
-  const size_t e = 2 * ((size_t)blockIdx.x * blockDim.x + threadIdx.x);
-  const size_t kl = (size_t)(L + K) * n;
-  ulonglong2 d[ND];
-#pragma unroll
-  for (int j = 0; j < ND; ++j)
-    d[j] = *reinterpret_cast<const ulonglong2*>(digits + ((size_t)j * ne + i) * n + e);
-  auto finish = [&](const ulonglong2 (&kb2)[ND], const ulonglong2 (&ka2)[ND], uint32_t r) {
-    Acc128 a0x, a0y, a1x, a1y;
-#pragma unroll
-    for (int j = 0; j < ND; ++j) {
-      a0x.mac(d[j].x, kb2[j].x);
-      a0y.mac(d[j].y, kb2[j].y);
-      a1x.mac(d[j].x, ka2[j].x);
-      a1y.mac(d[j].y, ka2[j].y);
-    }
-    uint64_t* o = ext + (size_t)r * 2 * nout * n;
-    *reinterpret_cast<ulonglong2*>(o + (size_t)io * n + e) =
-        make_ulonglong2(redc(a0x.hi, a0x.lo, q, qinv), redc(a0y.hi, a0y.lo, q, qinv));
-    *reinterpret_cast<ulonglong2*>(o + ((size_t)nout + io) * n + e) =
-        make_ulonglong2(redc(a1x.hi, a1x.lo, q, qinv), redc(a1y.hi, a1y.lo, q, qinv));
-  };
-  uint32_t r = 0;
-  for (; r + 2 <= batch; r += 2) {
-    ulonglong2 b0[ND], a0[ND], b1[ND], a1[ND];
-    const uint64_t* k0 = kb.key[r] + (size_t)ki * n + e;
-    const uint64_t* k1 = kb.key[r + 1] + (size_t)ki * n + e;
-#pragma unroll
-    for (int j = 0; j < ND; ++j) {
-      b0[j] = *reinterpret_cast<const ulonglong2*>(k0 + (size_t)j * 2 * kl);
-      a0[j] = *reinterpret_cast<const ulonglong2*>(k0 + (size_t)j * 2 * kl + kl);
-      b1[j] = *reinterpret_cast<const ulonglong2*>(k1 + (size_t)j * 2 * kl);
-      a1[j] = *reinterpret_cast<const ulonglong2*>(k1 + (size_t)j * 2 * kl + kl);
-    }
-    finish(b0, a0, r);
-    finish(b1, a1, r + 1);
-  }
-  if (r < batch) {
-    ulonglong2 b0[ND], a0[ND];
-    const uint64_t* k0 = kb.key[r] + (size_t)ki * n + e;
-#pragma unroll
-    for (int j = 0; j < ND; ++j) {
-      b0[j] = *reinterpret_cast<const ulonglong2*>(k0 + (size_t)j * 2 * kl);
-      a0[j] = *reinterpret_cast<const ulonglong2*>(k0 + (size_t)j * 2 * kl + kl);
-    }
-    finish(b0, a0, r);
-  }
+    k_convert60_digits(const uint64_t* __restrict__ coef, uint64_t* __restrict__ digits,
+                       size_t digit_words, const ModConst* __restrict__ mc, const DigitPlans P,
+                       uint32_t n, uint32_t L, uint32_t nq, uint32_t tch) {
+  const uint32_t d = blockIdx.z;
+  if (blockIdx.y * tch >= P.ndst[d]) return;
+  convert60_body<NSRC>(coef + (size_t)P.src_limb[d] * n, digits + (size_t)d * digit_words, mc,
+                       P.src_idx[d], P.qhat_inv[d], P.qhat_mont[d], P.dst_idx[d], P.ndst[d], n,
+                       L, nq, tch);
 }
 
-__global__ void __launch_bounds__(TPB)
-    k_ksk_inner_batch(const uint64_t* __restrict__ digits, const KeyBatch kb,
-                      uint64_t* __restrict__ ext, const ModConst* __restrict__ mc, uint32_t n,
-                      uint32_t nq, uint32_t L, uint32_t K, uint32_t nd, uint32_t chunk,
-                      uint32_t batch, uint32_t limb0, uint32_t nout) {
-  const uint32_t i = limb0 + blockIdx.y, ne = nq + K, io = blockIdx.y;
-  const uint32_t ki = i < nq ? i : L + (i - nq);
-  const uint64_t q = mc[ki].q, qinv = mc[ki].qinv_neg;
-  const size_t e = 2 * ((size_t)blockIdx.x * blockDim.x + threadIdx.x);
-  const size_t kl = (size_t)(L + K) * n;
-  ulonglong2 d[MAXD];
-#pragma unroll
-  for (int j = 0; j < MAXD; ++j)
-    if (j < (int)nd) d[j] = *reinterpret_cast<const ulonglong2*>(digits + ((size_t)j * ne + i) * n + e);
-  for (uint32_t r = 0; r < batch; ++r) {
-    const uint64_t* key = kb.key[r] + (size_t)ki * n + e;
-    uint64_t r0x = 0, r0y = 0, r1x = 0, r1y = 0;
-    uint32_t j0 = 0;
-    while (j0 < nd) {
-      const uint32_t j1 = j0 + chunk < nd ? j0 + chunk : nd;
-      Acc128 a0x, a0y, a1x, a1y;
-#pragma unroll
-      for (int j = 0; j < MAXD; ++j) {
-        if (j < (int)j0 || j >= (int)j1) continue;
-        const ulonglong2 b = *reinterpret_cast<const ulonglong2*>(key + (size_t)j * 2 * kl);
-        const ulonglong2 a = *reinterpret_cast<const ulonglong2*>(key + (size_t)j * 2 * kl + kl);
-        a0x.mac(d[j].x, b.x);
-        a0y.mac(d[j].y, b.y);
-        a1x.mac(d[j].x, a.x);
-        a1y.mac(d[j].y, a.y);
-      }
-      r0x = add_mod(r0x, redc(a0x.hi, a0x.lo, q, qinv), q);
-      r0y = add_mod(r0y, redc(a0y.hi, a0y.lo, q, qinv), q);
-      r1x = add_mod(r1x, redc(a1x.hi, a1x.lo, q, qinv), q);
-      r1y = add_mod(r1y, redc(a1y.hi, a1y.lo, q, qinv), q);
-      j0 = j1;
-    }
-    uint64_t* o = ext + (size_t)r * 2 * nout * n;
-    *reinterpret_cast<ulonglong2*>(o + (size_t)io * n + e) = make_ulonglong2(r0x, r0y);
-    *reinterpret_cast<ulonglong2*>(o + ((size_t)nout + io) * n + e) = make_ulonglong2(r1x, r1y);
-  }
-}
+// The key inner product has no kernel of its own: its P limbs feed the
+// first pass of ModDown's inverse NTT and its Q limbs the last pass of the
+// forward NTT (ntt.hip, KskLoad / EpiStore).  Up to MAXD digits.
 
 __device__ __forceinline__ uint32_t brev_bits(uint32_t x, uint32_t bits) {
   return __brev(x) >> (32 - bits);
@@ -325,45 +250,60 @@ void modup(Context& c, const uint64_t* a, uint32_t nq, uint64_t* digits) {
             "modup copy");
   ntt_inverse(c, coef.p, 1, 0, nq, LimbMap::contiguous(0));
   const uint32_t nd = num_digits(c, nq);
+  if (nd > MAXD) throw ArgError("more than 8 key-switching digits");
+  // Conversions: the full-width digits in one launch when the 30-bit split
+  // applies, any other digit on its own.
+  std::vector<const ConvPlan*> plans(nd);
   for (uint32_t j = 0; j < nd; ++j) {
     const uint32_t s = j * c.alpha, e = s + c.alpha < nq ? s + c.alpha : nq;
-    uint64_t* dj = digits + (size_t)j * ne * n;
-    convert(c, c.modup_plan(s, e, nq), coef.p + (size_t)s * n, 0, dj, 0, nq, 1);
-    if (s > 0) ntt_forward(c, dj, 1, 0, s, LimbMap::contiguous(0));
-    ntt_forward(c, dj + (size_t)e * n, 1, 0, (uint32_t)(ne - e), LimbMap{nq - e, e, c.L});
-    hip_check(hipMemcpyAsync(dj + (size_t)s * n, a + (size_t)s * n, (size_t)(e - s) * n * 8,
-                             hipMemcpyDeviceToDevice, c.stream),
+    plans[j] = &c.modup_plan(s, e, nq);
+  }
+  uint32_t batched = 0;
+  if (c.alpha <= MAXSRC) {
+    while (batched < nd && plans[batched]->nsrc == c.alpha &&
+           below_2_60(c, plans[batched]->src_idx) && below_2_60(c, plans[batched]->dst_idx))
+      ++batched;
+  }
+  if (batched > 1) {
+    DigitPlans P{};
+    uint32_t ndst = 0;
+    for (uint32_t j = 0; j < batched; ++j) {
+      P.src_idx[j] = plans[j]->d_src_idx32;
+      P.qhat_inv[j] = plans[j]->d_qhat_inv;
+      P.qhat_mont[j] = plans[j]->d_qhat_mont;
+      P.dst_idx[j] = plans[j]->d_dst_idx;
+      P.ndst[j] = plans[j]->ndst;
+      P.src_limb[j] = j * c.alpha;
+      ndst = std::max(ndst, plans[j]->ndst);
+    }
+    const uint32_t tpb = tpb_for(c, 1), tch = 4;
+    const dim3 grid(c.n / tpb, (ndst + tch - 1) / tch, batched);
+    switch (c.alpha) {
+#define CASE(S)                                                                                \
+  case S:                                                                                      \
+    FHE_LAUNCH(c, "k_convert", k_convert60_digits<S>, grid, dim3(tpb), 0, coef.p, digits,     \
+               ne * n, c.d_const, P, c.n, c.L, nq, tch);                                       \
+    break;
+      CASE(1) CASE(2) CASE(3) CASE(4) CASE(5) CASE(6) CASE(7) CASE(8)
+      CASE(9) CASE(10) CASE(11) CASE(12) CASE(13) CASE(14) CASE(15) CASE(16)
+#undef CASE
+      default: throw ArgError("digit width above 16 limbs");
+    }
+  } else {
+    batched = 0;
+  }
+  for (uint32_t j = batched; j < nd; ++j)
+    convert(c, *plans[j], coef.p + (size_t)j * c.alpha * n, 0, digits + (size_t)j * ne * n, 0,
+            nq, 1);
+  // Forward NTT of every digit's converted limbs in one two-pass launch,
+  // then each digit's own limbs copied in evaluation form.
+  ntt_forward_digits(c, digits, nd, nq);
+  for (uint32_t j = 0; j < nd; ++j) {
+    const uint32_t s = j * c.alpha, e = s + c.alpha < nq ? s + c.alpha : nq;
+    hip_check(hipMemcpyAsync(digits + ((size_t)j * ne + s) * n, a + (size_t)s * n,
+                             (size_t)(e - s) * n * 8, hipMemcpyDeviceToDevice, c.stream),
               "modup digit copy");
   }
-}
-
-void ksk_inner_batch(Context& c, const uint64_t* digits, uint32_t nq, const uint64_t* const* keys,
-                     uint32_t batch, uint64_t* ext, uint32_t limb0, uint32_t nout) {
-  if (batch == 0 || nout == 0) return;
-  if (batch > MAX_KS_BATCH) throw ArgError("key-switch batch too large");
-  if (limb0 + nout > nq + c.K) throw ArgError("inner product limbs out of range");
-  const uint32_t nd = num_digits(c, nq);
-  if (nd > MAXD) throw ArgError("more than 8 key-switching digits");
-  std::vector<uint32_t> all(c.L + c.K);
-  for (uint32_t i = 0; i < c.L + c.K; ++i) all[i] = i;
-  KeyBatch kb{};
-  for (uint32_t r = 0; r < batch; ++r) kb.key[r] = keys[r];
-  const uint32_t tpb = tpb_for(c, 2);
-  const dim3 grid(c.n / (2 * tpb), nout, 1);
-  if (nd <= redc_chunk(c, all)) {
-    switch (nd) {
-#define CASE(D)                                                                                \
-  case D:                                                                                      \
-    FHE_LAUNCH(c, "k_ksk_inner", k_ksk_inner_nd<D>, grid, dim3(tpb), 0, digits, kb, ext,      \
-               c.d_const, c.n, nq, c.L, c.K, batch, limb0, nout);                              \
-    return;
-      CASE(1) CASE(2) CASE(3) CASE(4) CASE(5) CASE(6) CASE(7) CASE(8)
-#undef CASE
-      default: break;
-    }
-  }
-  FHE_LAUNCH(c, "k_ksk_inner", k_ksk_inner_batch, grid, dim3(tpb), 0, digits, kb, ext, c.d_const,
-             c.n, nq, c.L, c.K, nd, redc_chunk(c, all), batch, limb0, nout);
 }
 
 uint32_t galois_inverse(uint32_t g, uint32_t n) {
@@ -387,10 +327,6 @@ void keyswitch_batch(Context& c, const uint64_t* digits, uint32_t nq,
   // The fused Q-limb products are reduced once: nd * q_i < 2^64 holds for
   // nd <= 8 and q_i < 2^61.
   Scratch ext(c, 2 * (size_t)batch * kw), y(c, 2 * (size_t)batch * nq * n);
-  // P limbs of the inner product, to coefficient form, converted to Q.
-  ksk_inner_batch(c, digits, nq, keys, batch, ext.p, nq, c.K);
-  ntt_inverse(c, ext.p, 2 * batch, kw, c.K, LimbMap::contiguous(c.L));
-  convert(c, c.moddown_plan(nq), ext.p, kw, y.p, (size_t)nq * n, nq, 2 * batch);
   ModDownEpi epi{};
   epi.digits = digits;
   epi.mc = c.d_const;
@@ -398,6 +334,7 @@ void keyswitch_batch(Context& c, const uint64_t* digits, uint32_t nq,
   epi.nd = nd;
   epi.ne = (uint32_t)ne;
   epi.nq = nq;
+  epi.L = c.L;
   for (uint32_t r = 0; r < batch; ++r) {
     epi.key[r] = keys[r];
     epi.out[r] = outs[r].out;
@@ -405,6 +342,11 @@ void keyswitch_batch(Context& c, const uint64_t* digits, uint32_t nq,
     epi.add[r][1] = outs[r].add1;
     epi.ginv[r] = galois_inverse(outs[r].galois, c.n);
   }
+  // P limbs of the inner product (formed by the inverse NTT's first pass),
+  // to coefficient form, converted to Q; then the forward NTT with the
+  // Q-limb products and the combine in its last pass.
+  ntt_inverse_ksk(c, ext.p, 2 * batch, epi);
+  convert(c, c.moddown_plan(nq), ext.p, kw, y.p, (size_t)nq * n, nq, 2 * batch);
   ntt_forward_moddown(c, y.p, 2 * batch, nq, epi);
 }
 

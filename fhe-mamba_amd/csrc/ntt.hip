@@ -53,12 +53,20 @@ __device__ __forceinline__ uint32_t lds_idx(uint32_t line, uint32_t u, uint32_t 
 
 // Final stores go through `store.fin(base, offset_in_limb, value, t, q)`,
 // with t = store.pre(offset_in_limb, q) when Store::kPre.
-template <int S, int KIND, bool INV, int RHO_, class Store>
+// The first pass's input comes from `load.get(offset_in_limb, q)` instead
+// of data when Load::kLoad.
+struct PlainLoad {
+  static constexpr bool kLoad = false;
+  __device__ __forceinline__ uint64_t get(size_t, uint64_t) const { return 0; }
+};
+
+template <int S, int KIND, bool INV, int RHO_, class Store, class Load = PlainLoad,
+          class Map = LimbMap>
 __device__ __forceinline__ void ntt_body(uint64_t* __restrict__ data, size_t poly_stride,
                                          const ModConst* __restrict__ mc,
                                          const uint64_t* __restrict__ tw_all, uint32_t log_n,
-                                         LimbMap map, uint32_t s_other, int last,
-                                         const Store& store) {
+                                         Map map, uint32_t s_other, int last,
+                                         const Store& store, const Load& load = Load{}) {
   using G = Geo<S, RHO_>;
   constexpr int RHO = G::RHO;
   constexpr int R = 1 << RHO;
@@ -67,11 +75,12 @@ __device__ __forceinline__ void ntt_body(uint64_t* __restrict__ data, size_t pol
   __shared__ uint64_t lds[LINES * G::PITCH];
 
   const uint32_t n = 1u << log_n;
-  const uint32_t limb = blockIdx.z;
-  const uint32_t midx = map(limb);
+  // Workgroup-uniform: a slot without work exits before any barrier.
+  uint32_t pos, midx;
+  if (!map.resolve(blockIdx.y, blockIdx.z, pos, midx)) return;
   const uint64_t q = mc[midx].q, q2 = 2 * q;
   const uint64_t* __restrict__ tw = tw_all + (size_t)midx * n * 2;
-  uint64_t* __restrict__ base = data + (size_t)blockIdx.y * poly_stride + (size_t)limb * n;
+  uint64_t* __restrict__ base = data + (size_t)blockIdx.y * poly_stride + (size_t)pos * n;
 
   const uint32_t tid = threadIdx.x;
   uint32_t line, tau;
@@ -115,7 +124,8 @@ __device__ __forceinline__ void ntt_body(uint64_t* __restrict__ data, size_t pol
 #pragma unroll
       for (int k = 0; k < R; ++k) {
         const uint32_t p = k * blockDim.x + tid;
-        lds[lds_idx(p >> S, p & (G::LEN - 1), G::PITCH)] = base[wg0 + p];
+        lds[lds_idx(p >> S, p & (G::LEN - 1), G::PITCH)] =
+            Load::kLoad ? load.get(wg0 + p, q) : base[wg0 + p];
       }
       __syncthreads();
 #pragma unroll
@@ -128,7 +138,7 @@ __device__ __forceinline__ void ntt_body(uint64_t* __restrict__ data, size_t pol
       for (int v = 0; v < R; ++v) {
         const uint32_t u = thi | ((uint32_t)v << w) | tlo;
         const size_t g = KIND == COLS ? gline + ((size_t)u << s_other) : ((size_t)gline << S) + u;
-        x[v] = base[g];
+        x[v] = Load::kLoad ? load.get(g, q) : base[g];
       }
     } else {
       __syncthreads();
@@ -296,19 +306,53 @@ struct EpiStore {
   }
 };
 
-template <int S, int KIND, bool INV>
+template <int S, int KIND, bool INV, class Map>
 __global__ void __launch_bounds__(256)
     ntt_pass(uint64_t* __restrict__ data, size_t poly_stride, const ModConst* __restrict__ mc,
-             const uint64_t* __restrict__ tw_all, uint32_t log_n, LimbMap map, uint32_t s_other,
+             const uint64_t* __restrict__ tw_all, uint32_t log_n, Map map, uint32_t s_other,
              int last) {
-  ntt_body<S, KIND, INV, RHO_PLAIN>(data, poly_stride, mc, tw_all, log_n, map, s_other, last,
-                                    PlainStore{});
+  ntt_body<S, KIND, INV, RHO_PLAIN, PlainStore, PlainLoad, Map>(
+      data, poly_stride, mc, tw_all, log_n, map, s_other, last, PlainStore{});
 }
 
 // Last forward pass of a batched ModDown (BLOCKS or SINGLE kind).
 template <int S, int KIND>
 constexpr int epilogue_rho() {
   return KIND == SINGLE ? RHO_PLAIN : RHO_EPILOGUE;
+}
+
+// P-limb key inner product as the input of ModDown's inverse NTT: launch
+// poly p is key switch r = p / 2, component b = p % 2, limb t is P limb t.
+template <int ND>
+struct KskLoad {
+  static constexpr bool kLoad = true;
+  const ModDownEpi& e;
+  uint32_t n;
+  __device__ __forceinline__ uint64_t get(size_t s, uint64_t q) const {
+    const uint32_t p = blockIdx.y, r = p >> 1, b = p & 1, t = blockIdx.z;
+    const uint64_t* dg = e.digits + (size_t)(e.nq + t) * n + s;
+    const uint64_t* kr = e.key[r] + (size_t)b * e.kl + (size_t)(e.L + t) * n + s;
+    const size_t dstride = (size_t)e.ne * n, kstride = 2 * e.kl;
+    Acc128 acc;
+    if (ND > 0) {
+#pragma unroll
+      for (int j = 0; j < ND; ++j) acc.mac(dg[j * dstride], kr[j * kstride]);
+    } else {
+      for (uint32_t j = 0; j < e.nd; ++j) acc.mac(dg[j * dstride], kr[j * kstride]);
+    }
+    return redc(acc.hi, acc.lo, q, e.mc[e.L + t].qinv_neg);
+  }
+};
+
+// First inverse pass of ModDown (BLOCKS or SINGLE kind) fed by KskLoad.
+template <int S, int KIND, int ND>
+__global__ void __launch_bounds__(256)
+    ntt_pass_ksk(uint64_t* __restrict__ data, size_t poly_stride, const ModConst* __restrict__ mc,
+                 const uint64_t* __restrict__ tw_all, uint32_t log_n, uint32_t s_other,
+                 int last, const ModDownEpi epi) {
+  ntt_body<S, KIND, true, epilogue_rho<S, KIND>()>(
+      data, poly_stride, mc, tw_all, log_n, LimbMap::contiguous(epi.L), s_other, last,
+      PlainStore{}, KskLoad<ND>{epi, 1u << log_n});
 }
 
 template <int S, int KIND, int ND>
@@ -321,9 +365,9 @@ __global__ void __launch_bounds__(256)
                                                     EpiStore<ND>{epi, 1u << log_n, log_n});
 }
 
-template <int S, int KIND, bool INV>
+template <int S, int KIND, bool INV, class Map>
 void launch_pass(Context& c, uint64_t* data, uint32_t npoly, size_t poly_stride, uint32_t nlimb,
-                 LimbMap map, uint32_t s_other, bool last) {
+                 Map map, uint32_t s_other, bool last) {
   using G = Geo<S, RHO_PLAIN>;
   const uint32_t lines = KIND == SINGLE ? 1 : 256 / G::TPL;
   const uint32_t threads = KIND == SINGLE ? G::TPL : 256;
@@ -334,11 +378,11 @@ void launch_pass(Context& c, uint64_t* data, uint32_t npoly, size_t poly_stride,
       KIND == SINGLE ? (INV ? "ntt_inv_single" : "ntt_fwd_single")
       : KIND == COLS ? (INV ? "ntt_inv_cols" : "ntt_fwd_cols")
                      : (INV ? "ntt_inv_blocks" : "ntt_fwd_blocks");
-  FHE_LAUNCH(c, PASS_NAME, (ntt_pass<S, KIND, INV>), grid, dim3(threads), 0, data, poly_stride, c.d_const, INV ? c.d_tw_inv : c.d_tw_fwd, c.log_n, map, s_other, (int)last);
+  FHE_LAUNCH(c, PASS_NAME, (ntt_pass<S, KIND, INV, Map>), grid, dim3(threads), 0, data, poly_stride, c.d_const, INV ? c.d_tw_inv : c.d_tw_fwd, c.log_n, map, s_other, (int)last);
 }
 
-template <bool INV>
-void launch_single(Context& c, uint64_t* data, uint32_t npoly, size_t ps, uint32_t nlimb, LimbMap map) {
+template <bool INV, class Map = LimbMap>
+void launch_single(Context& c, uint64_t* data, uint32_t npoly, size_t ps, uint32_t nlimb, Map map) {
   switch (c.log_n) {
 #define CASE(S) \
   case S: launch_pass<S, SINGLE, INV>(c, data, npoly, ps, nlimb, map, 0, true); break;
@@ -348,9 +392,9 @@ void launch_single(Context& c, uint64_t* data, uint32_t npoly, size_t ps, uint32
   }
 }
 
-template <bool INV>
+template <bool INV, class Map = LimbMap>
 void launch_cols(Context& c, uint32_t s1, uint32_t s2, uint64_t* data, uint32_t npoly, size_t ps,
-                 uint32_t nlimb, LimbMap map, bool last) {
+                 uint32_t nlimb, Map map, bool last) {
   switch (s1) {
 #define CASE(S) \
   case S: launch_pass<S, COLS, INV>(c, data, npoly, ps, nlimb, map, s2, last); break;
@@ -360,9 +404,9 @@ void launch_cols(Context& c, uint32_t s1, uint32_t s2, uint64_t* data, uint32_t 
   }
 }
 
-template <bool INV>
+template <bool INV, class Map = LimbMap>
 void launch_blocks(Context& c, uint32_t s1, uint32_t s2, uint64_t* data, uint32_t npoly, size_t ps,
-                   uint32_t nlimb, LimbMap map, bool last) {
+                   uint32_t nlimb, Map map, bool last) {
   switch (s2) {
 #define CASE(S) \
   case S: launch_pass<S, BLOCKS, INV>(c, data, npoly, ps, nlimb, map, s1, last); break;
@@ -394,7 +438,73 @@ void launch_moddown(Context& c, uint64_t* y, uint32_t npoly, uint32_t nq, uint32
   }
 }
 
+template <int S, int KIND>
+void launch_ksk(Context& c, uint64_t* ext, uint32_t npoly, uint32_t s_other, bool last,
+                const ModDownEpi& epi) {
+  using G = Geo<S, epilogue_rho<S, KIND>()>;
+  const uint32_t lines = KIND == SINGLE ? 1 : 256 / G::TPL;
+  const uint32_t threads = KIND == SINGLE ? G::TPL : 256;
+  const uint32_t tiles = KIND == SINGLE ? 1 : (1u << s_other) / lines;
+  const char* name = KIND == SINGLE ? "ntt_inv_single_ksk" : "ntt_inv_blocks_ksk";
+  const dim3 grid(tiles, npoly, c.K);
+  const size_t ps = (size_t)c.K * c.n;
+  switch (epi.nd) {
+#define CASE(D)                                                                         \
+  case D:                                                                               \
+    FHE_LAUNCH(c, name, (ntt_pass_ksk<S, KIND, D>), grid, dim3(threads), 0, ext, ps,     \
+               c.d_const, c.d_tw_inv, c.log_n, s_other, (int)last, epi);                \
+    return;
+    CASE(1) CASE(2) CASE(3)
+#undef CASE
+    default:
+      FHE_LAUNCH(c, name, (ntt_pass_ksk<S, KIND, 0>), grid, dim3(threads), 0, ext, ps, c.d_const,
+                 c.d_tw_inv, c.log_n, s_other, (int)last, epi);
+  }
+}
+
 }  // namespace
+
+void ntt_forward_digits(Context& c, uint64_t* digits, uint32_t nd, uint32_t nq) {
+  if (nd == 0 || nq == 0) return;
+  if (nq > c.L) throw ArgError("ModUp level out of range");
+  const uint32_t ne = nq + c.K;
+  // The last digit is the narrowest and so has the most converted limbs.
+  const uint32_t w_last = nq - (nd - 1) * c.alpha;
+  const uint32_t slots = ne - w_last;
+  const DigitMap map{c.alpha, nq, c.L, ne};
+  const size_t ps = (size_t)ne * c.n;
+  if (c.log_n <= 12) {
+    launch_single<false>(c, digits, nd, ps, slots, map);
+    return;
+  }
+  const uint32_t s1 = (c.log_n + 1) / 2, s2 = c.log_n / 2;
+  launch_cols<false>(c, s1, s2, digits, nd, ps, slots, map, false);
+  launch_blocks<false>(c, s1, s2, digits, nd, ps, slots, map, true);
+}
+
+void ntt_inverse_ksk(Context& c, uint64_t* ext_p, uint32_t npoly, const ModDownEpi& epi) {
+  if (npoly == 0 || c.K == 0) return;
+  if (npoly > 2 * MAX_KS_BATCH) throw ArgError("key-switch batch too large");
+  if (c.log_n <= 12) {
+    switch (c.log_n) {
+#define CASE(S) \
+  case S: launch_ksk<S, SINGLE>(c, ext_p, npoly, 0, true, epi); return;
+      CASE(4) CASE(5) CASE(6) CASE(7) CASE(8) CASE(9) CASE(10) CASE(11) CASE(12)
+#undef CASE
+      default: throw ArgError("unsupported ring dimension");
+    }
+  }
+  const uint32_t s1 = (c.log_n + 1) / 2, s2 = c.log_n / 2;
+  switch (s2) {
+#define CASE(S) \
+  case S: launch_ksk<S, BLOCKS>(c, ext_p, npoly, s1, false, epi); break;
+    CASE(6) CASE(7) CASE(8)
+#undef CASE
+    default: throw ArgError("unsupported block pass");
+  }
+  launch_cols<true>(c, s1, s2, ext_p, npoly, (size_t)c.K * c.n, c.K, LimbMap::contiguous(c.L),
+                    true);
+}
 
 void ntt_forward_moddown(Context& c, uint64_t* y, uint32_t npoly, uint32_t nq,
                          const ModDownEpi& epi) {

@@ -59,13 +59,10 @@ struct KeySwitchOut {
   const uint64_t* add1;  // added to component 1 (or null)
   uint32_t galois;       // Galois element applied to the result (1 = none)
 };
-// Key inner product over extended limbs [limb0, limb0 + nout) (keys in
-// Montgomery form) into ext [B][2][nout][N].
-void ksk_inner_batch(Context& c, const uint64_t* digits, uint32_t nq, const uint64_t* const* keys,
-                     uint32_t batch, uint64_t* ext, uint32_t limb0, uint32_t nout);
-// B <= MAX_KS_BATCH key switches of one set of digits: the P limbs of the
-// inner product, one batched ModDown, and the Q-limb products, combine and
-// Galois permutation in its last NTT pass.
+// B <= MAX_KS_BATCH key switches of one set of digits (keys in Montgomery
+// form): one batched ModDown whose inverse NTT forms the P limbs of the
+// inner product as it loads, and whose forward NTT's last pass forms the Q
+// limbs and applies the combine and the Galois permutation.
 void keyswitch_batch(Context& c, const uint64_t* digits, uint32_t nq,
                      const uint64_t* const* keys, uint32_t batch, const KeySwitchOut* outs);
 // ModUp of a [nq][N] (evaluation form) and one key switch.
