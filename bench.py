@@ -95,12 +95,23 @@ def run_rotations(F, steps: int, warmup: int):
     for _ in range(steps):
         step()
     prof = ctx.profile_end()
+    # Non-hoisted rotations (each with its own ModUp), same keys and input.
+    single = ctx.poly(2, L)
+    for k, g in zip(keys[:4], gal[:4]):
+        ctx.rotate(ct, k, g, out=single)
+    ctx.sync()
+    t1 = time.perf_counter()
+    for k, g in zip(keys, gal):
+        ctx.rotate(ct, k, g, out=single)
+    ctx.sync()
+    single_s = time.perf_counter() - t1
     ct_b, rot_b, rs_b = rotation_bytes(L, K)
     step_bytes = ct_b + len(STEPS) * rot_b + rs_b
     res = {
         "elapsed_s": elapsed,
         "ms_per_step": 1e3 * elapsed / steps,
         "rotations_per_s": len(STEPS) * steps / elapsed,
+        "single_rotations_per_s": len(keys) / single_s,
         "step_bytes": step_bytes,
         "profile": prof,
         "L": L,
@@ -313,6 +324,11 @@ def main() -> int:
         "roofline": roofline,
         "kernels_ms_per_step": {k: v[1] / args.steps for k, v in sorted(prof.items())},
         "kernels_gbps": kernel_gbps,
+        "single_rotation": {
+            "rotations_per_s": rot["single_rotations_per_s"],
+            "workload": "the same 30 rotations, each a full EvalRotate (own ModUp)",
+            "frac": rot["single_rotations_per_s"] * 150_994_944 / HBM_PEAK,
+        },
     }
     if ntt:
         out["ntt"] = {k: ntt[k] for k in ("ntt_gbps", "ntt_fwd_ms", "ntt_inv_ms", "mac_ms",

@@ -209,10 +209,20 @@ bool below_2_60(const Context& c, const std::vector<uint32_t>& idx) {
   return true;
 }
 
+// Targets per thread: as many as possible (each thread's source words and
+// their Shoup products are reused for every target it covers) while the
+// launch still has >= 4096 workgroups; at least 4.
+inline uint32_t convert_tch(const Context& c, uint32_t ndst, uint32_t npoly) {
+  const uint64_t per = (uint64_t)(c.n / tpb_for(c, 1)) * npoly;
+  uint32_t tch = ndst;
+  while (tch > 4 && per * ((ndst + tch - 1) / tch) < 4096) tch = (tch + 1) / 2;
+  return tch < 4 ? 4 : tch;
+}
+
 template <int NSRC>
 void launch_convert60(Context& c, const ConvPlan& pl, const uint64_t* src, size_t src_ps,
                       uint64_t* out, size_t out_ps, uint32_t out_nq, uint32_t npoly) {
-  const uint32_t tpb = tpb_for(c, 1), tch = 4;
+  const uint32_t tpb = tpb_for(c, 1), tch = convert_tch(c, pl.ndst, npoly);
   FHE_LAUNCH(c, "k_convert", k_convert60<NSRC>, dim3(c.n / tpb, (pl.ndst + tch - 1) / tch, npoly),
              dim3(tpb), 0, src, src_ps, out, out_ps, c.d_const, pl.d_src_idx32, pl.d_qhat_inv,
              pl.d_qhat_mont, pl.d_dst_idx, pl.ndst, c.n, c.L, out_nq, tch);
@@ -276,7 +286,7 @@ void modup(Context& c, const uint64_t* a, uint32_t nq, uint64_t* digits) {
       P.src_limb[j] = j * c.alpha;
       ndst = std::max(ndst, plans[j]->ndst);
     }
-    const uint32_t tpb = tpb_for(c, 1), tch = 4;
+    const uint32_t tpb = tpb_for(c, 1), tch = convert_tch(c, ndst, batched);
     const dim3 grid(c.n / tpb, (ndst + tch - 1) / tch, batched);
     switch (c.alpha) {
 #define CASE(S)                                                                                \
