@@ -573,6 +573,50 @@ int fhe_rotate_hoisted(const fhe_poly* ct, const fhe_poly* digits, const fhe_key
   });
 }
 
+int fhe_rotate_many(fhe_poly* const* outs, const fhe_poly* const* cts, const fhe_key* const* keys,
+                    const uint32_t* galois, uint32_t count) {
+  return guard([&] {
+    need(outs && cts && keys && galois, "null argument");
+    if (count == 0) return;
+    need(cts[0] != nullptr, "null ciphertext");
+    fhe::Context& c = *cts[0]->c;
+    const uint32_t nq = cts[0]->nlimb;
+    for (uint32_t r = 0; r < count; ++r) {
+      need(cts[r] && outs[r], "null handle");
+      same_ctx(outs[r], cts[r]);
+      need(cts[r]->c == &c && cts[r]->npoly == 2 && cts[r]->nlimb == nq && nq <= c.L,
+           "rotate_many needs 2-poly ciphertexts of one context and level");
+      check_key(cts[r], keys[r]);
+      need((galois[r] & 1) && galois[r] < 2 * c.n, "Galois element must be odd and < 2N");
+      for (uint32_t s = 0; s < r; ++s) need(outs[s] != outs[r], "outputs must be distinct");
+    }
+    // Outputs that alias an input are written to scratch and copied after.
+    const size_t pl = 2 * (size_t)nq * c.n;
+    std::vector<uint8_t> alias(count, 0);
+    uint32_t naliased = 0;
+    for (uint32_t r = 0; r < count; ++r)
+      for (uint32_t s = 0; s < count; ++s)
+        if (outs[r] == cts[s]) alias[r] = 1;
+    for (uint32_t r = 0; r < count; ++r) naliased += alias[r];
+    fhe::Scratch tmp(c, std::max<size_t>(1, naliased * pl));
+    std::vector<uint64_t*> dst(count);
+    std::vector<const uint64_t*> src(count), kp(count);
+    for (uint32_t r = 0, t = 0; r < count; ++r) {
+      if (!alias[r]) prepare_out(outs[r], 2, nq);
+      dst[r] = alias[r] ? tmp.p + (t++) * pl : outs[r]->data;
+      src[r] = cts[r]->data;
+      kp[r] = keys[r]->data;
+    }
+    fhe::rotate_many(c, dst.data(), src.data(), nq, kp.data(), galois, count);
+    for (uint32_t r = 0; r < count; ++r) {
+      if (!alias[r]) continue;  // an input handle: already [2][nq]
+      fhe::hip_check(hipMemcpyAsync(outs[r]->data, dst[r], pl * 8, hipMemcpyDeviceToDevice,
+                                    c.stream),
+                     "rotate_many");
+    }
+  });
+}
+
 int fhe_linear_transform(fhe_poly* out, const fhe_poly* ct, const fhe_poly* const* pts,
                          uint32_t count, uint32_t bstep, const fhe_key* const* baby_keys,
                          const uint32_t* baby_galois, const fhe_key* giant_key,

@@ -175,8 +175,9 @@ struct LimbMap {
 // limbs of Q_l + P in order (position pos, modulus pos < nq ? pos :
 // L + pos - nq).  Slots past the digit's count are not launched work.
 struct DigitMap {
-  uint32_t alpha, nq, L, ne;
-  FHE_HD bool resolve(uint32_t d, uint32_t t, uint32_t& pos, uint32_t& mod) const {
+  uint32_t alpha, nq, L, ne, nd;  // poly = ciphertext * nd + digit
+  FHE_HD bool resolve(uint32_t poly, uint32_t t, uint32_t& pos, uint32_t& mod) const {
+    const uint32_t d = poly % nd;
     const uint32_t s = d * alpha, e = s + alpha < nq ? s + alpha : nq, w = e - s;
     if (t + w >= ne) return false;
     pos = t < s ? t : t + w;
@@ -229,7 +230,7 @@ struct LaunchScope {
 // Epilogue of the last forward-NTT pass of a batched ModDown.  Launch poly p
 // is key switch r = p / 2, component b = p % 2.  The Q-limb key inner
 // product is formed here,
-//   ext_r[b][i][s] = REDC(sum_j digits[j][i][s] * key_r[j][b][i][s]),
+//   ext_r[b][i][s] = REDC(sum_j digits_r[j][i][s] * key_r[j][b][i][s]),
 // and carries the factor P^-1 (folded into the stored keys); y carries -P^-1
 // (folded into the ModDown conversion constants), so
 //   out_r[b][i][d(s)] = ext_r[b][i][s] + y[s] + add_r,b[i][s]
@@ -238,7 +239,7 @@ struct LaunchScope {
 // 1 means no permutation).  One REDC suffices while nd * q_i < 2^64.
 constexpr int MAX_KS_BATCH = 32;
 struct ModDownEpi {
-  const uint64_t* digits;                 // [nd][ne][N]
+  const uint64_t* digits[MAX_KS_BATCH];   // each [nd][ne][N]
   const ModConst* mc;
   const uint64_t* key[MAX_KS_BATCH];      // each [nd][2][L+K][N], Montgomery form
   uint64_t* out[MAX_KS_BATCH];            // each [2][nq][N]
@@ -262,7 +263,8 @@ void ntt_forward_moddown(Context& c, uint64_t* y, uint32_t npoly, uint32_t nq,
 // formed while the first pass loads its input (epi.digits / key / mc / kl /
 // nd / ne / nq / L are used; the output fields are not).
 void ntt_inverse_ksk(Context& c, uint64_t* ext_p, uint32_t npoly, const ModDownEpi& epi);
-// Forward NTT of the converted limbs of all nd ModUp digits [nd][nq+K][N].
-void ntt_forward_digits(Context& c, uint64_t* digits, uint32_t nd, uint32_t nq);
+// Forward NTT of the converted limbs of the ModUp digits of `count`
+// ciphertexts, [count][nd][nq+K][N].
+void ntt_forward_digits(Context& c, uint64_t* digits, uint32_t count, uint32_t nd, uint32_t nq);
 
 }  // namespace fhe

@@ -139,8 +139,9 @@ __global__ void __launch_bounds__(TPB)
                        src_idx, qhat_inv, qhat_mont, dst_idx, ndst, n, L, out_nq, tch);
 }
 
-// ModUp conversion of several digits in one launch: digit d = blockIdx.z
-// converts its limbs coef[src_off[d] ..) with its own plan into digits[d].
+// ModUp conversion of several digits of several ciphertexts in one launch:
+// blockIdx.z = ciphertext * ndig + digit d; digit d converts its limbs
+// coef[ct][src_limb[d] ..) with its own plan into digits[ct][d].
 constexpr int MAXD = 8;
 struct DigitPlans {
   const uint32_t* src_idx[MAXD];
@@ -155,12 +156,13 @@ template <int NSRC>
 __global__ void __launch_bounds__(TPB)
     k_convert60_digits(const uint64_t* __restrict__ coef, uint64_t* __restrict__ digits,
                        size_t digit_words, const ModConst* __restrict__ mc, const DigitPlans P,
-                       uint32_t n, uint32_t L, uint32_t nq, uint32_t tch) {
-  const uint32_t d = blockIdx.z;
+                       uint32_t n, uint32_t L, uint32_t nq, uint32_t tch, uint32_t ndig,
+                       uint32_t nd) {
+  const uint32_t ct = blockIdx.z / ndig, d = blockIdx.z % ndig;
   if (blockIdx.y * tch >= P.ndst[d]) return;
-  convert60_body<NSRC>(coef + (size_t)P.src_limb[d] * n, digits + (size_t)d * digit_words, mc,
-                       P.src_idx[d], P.qhat_inv[d], P.qhat_mont[d], P.dst_idx[d], P.ndst[d], n,
-                       L, nq, tch);
+  convert60_body<NSRC>(coef + ((size_t)ct * nq + P.src_limb[d]) * n,
+                       digits + ((size_t)ct * nd + d) * digit_words, mc, P.src_idx[d],
+                       P.qhat_inv[d], P.qhat_mont[d], P.dst_idx[d], P.ndst[d], n, L, nq, tch);
 }
 
 // The key inner product has no kernel of its own: its P limbs feed the
@@ -253,13 +255,21 @@ uint32_t num_digits(const Context& c, uint32_t nq) {
 }
 
 void modup(Context& c, const uint64_t* a, uint32_t nq, uint64_t* digits) {
+  modup_batch(c, &a, 1, nq, digits);
+}
+
+void modup_batch(Context& c, const uint64_t* const* as, uint32_t count, uint32_t nq,
+                 uint64_t* digits) {
   if (nq == 0 || nq > c.L) throw ArgError("modup: bad level");
-  const size_t n = c.n, ne = nq + c.K;
-  Scratch coef(c, (size_t)nq * n);
-  hip_check(hipMemcpyAsync(coef.p, a, (size_t)nq * n * 8, hipMemcpyDeviceToDevice, c.stream),
-            "modup copy");
-  ntt_inverse(c, coef.p, 1, 0, nq, LimbMap::contiguous(0));
+  if (count == 0) return;
+  const size_t n = c.n, ne = nq + c.K, pl = (size_t)nq * n;
   const uint32_t nd = num_digits(c, nq);
+  const size_t ct_words = (size_t)nd * ne * n;
+  Scratch coef(c, count * pl);
+  for (uint32_t i = 0; i < count; ++i)
+    hip_check(hipMemcpyAsync(coef.p + i * pl, as[i], pl * 8, hipMemcpyDeviceToDevice, c.stream),
+              "modup copy");
+  ntt_inverse(c, coef.p, count, pl, nq, LimbMap::contiguous(0));
   if (nd > MAXD) throw ArgError("more than 8 key-switching digits");
   // Conversions: the full-width digits in one launch when the 30-bit split
   // applies, any other digit on its own.
@@ -286,13 +296,13 @@ void modup(Context& c, const uint64_t* a, uint32_t nq, uint64_t* digits) {
       P.src_limb[j] = j * c.alpha;
       ndst = std::max(ndst, plans[j]->ndst);
     }
-    const uint32_t tpb = tpb_for(c, 1), tch = convert_tch(c, ndst, batched);
-    const dim3 grid(c.n / tpb, (ndst + tch - 1) / tch, batched);
+    const uint32_t tpb = tpb_for(c, 1), tch = convert_tch(c, ndst, batched * count);
+    const dim3 grid(c.n / tpb, (ndst + tch - 1) / tch, batched * count);
     switch (c.alpha) {
 #define CASE(S)                                                                                \
   case S:                                                                                      \
     FHE_LAUNCH(c, "k_convert", k_convert60_digits<S>, grid, dim3(tpb), 0, coef.p, digits,     \
-               ne * n, c.d_const, P, c.n, c.L, nq, tch);                                       \
+               ne * n, c.d_const, P, c.n, c.L, nq, tch, batched, nd);                          \
     break;
       CASE(1) CASE(2) CASE(3) CASE(4) CASE(5) CASE(6) CASE(7) CASE(8)
       CASE(9) CASE(10) CASE(11) CASE(12) CASE(13) CASE(14) CASE(15) CASE(16)
@@ -303,17 +313,19 @@ void modup(Context& c, const uint64_t* a, uint32_t nq, uint64_t* digits) {
     batched = 0;
   }
   for (uint32_t j = batched; j < nd; ++j)
-    convert(c, *plans[j], coef.p + (size_t)j * c.alpha * n, 0, digits + (size_t)j * ne * n, 0,
-            nq, 1);
+    convert(c, *plans[j], coef.p + (size_t)j * c.alpha * n, pl, digits + (size_t)j * ne * n,
+            ct_words, nq, count);
   // Forward NTT of every digit's converted limbs in one two-pass launch,
   // then each digit's own limbs copied in evaluation form.
-  ntt_forward_digits(c, digits, nd, nq);
-  for (uint32_t j = 0; j < nd; ++j) {
-    const uint32_t s = j * c.alpha, e = s + c.alpha < nq ? s + c.alpha : nq;
-    hip_check(hipMemcpyAsync(digits + ((size_t)j * ne + s) * n, a + (size_t)s * n,
-                             (size_t)(e - s) * n * 8, hipMemcpyDeviceToDevice, c.stream),
-              "modup digit copy");
-  }
+  ntt_forward_digits(c, digits, count, nd, nq);
+  for (uint32_t i = 0; i < count; ++i)
+    for (uint32_t j = 0; j < nd; ++j) {
+      const uint32_t s = j * c.alpha, e = s + c.alpha < nq ? s + c.alpha : nq;
+      hip_check(hipMemcpyAsync(digits + i * ct_words + ((size_t)j * ne + s) * n,
+                               as[i] + (size_t)s * n, (size_t)(e - s) * n * 8,
+                               hipMemcpyDeviceToDevice, c.stream),
+                "modup digit copy");
+    }
 }
 
 uint32_t galois_inverse(uint32_t g, uint32_t n) {
@@ -328,6 +340,14 @@ uint32_t galois_inverse(uint32_t g, uint32_t n) {
 
 void keyswitch_batch(Context& c, const uint64_t* digits, uint32_t nq,
                      const uint64_t* const* keys, uint32_t batch, const KeySwitchOut* outs) {
+  if (batch > MAX_KS_BATCH) throw ArgError("key-switch batch too large");
+  const uint64_t* dg[MAX_KS_BATCH];
+  for (uint32_t r = 0; r < batch; ++r) dg[r] = digits;
+  keyswitch_batch(c, dg, nq, keys, batch, outs);
+}
+
+void keyswitch_batch(Context& c, const uint64_t* const* digits, uint32_t nq,
+                     const uint64_t* const* keys, uint32_t batch, const KeySwitchOut* outs) {
   if (batch == 0) return;
   if (batch > MAX_KS_BATCH) throw ArgError("key-switch batch too large");
   if (c.K == 0) throw ArgError("key switching needs special primes");
@@ -338,7 +358,6 @@ void keyswitch_batch(Context& c, const uint64_t* digits, uint32_t nq,
   // nd <= 8 and q_i < 2^61.
   Scratch ext(c, 2 * (size_t)batch * kw), y(c, 2 * (size_t)batch * nq * n);
   ModDownEpi epi{};
-  epi.digits = digits;
   epi.mc = c.d_const;
   epi.kl = (size_t)(c.L + c.K) * n;
   epi.nd = nd;
@@ -346,6 +365,7 @@ void keyswitch_batch(Context& c, const uint64_t* digits, uint32_t nq,
   epi.nq = nq;
   epi.L = c.L;
   for (uint32_t r = 0; r < batch; ++r) {
+    epi.digits[r] = digits[r];
     epi.key[r] = keys[r];
     epi.out[r] = outs[r].out;
     epi.add[r][0] = outs[r].add0;
@@ -379,6 +399,30 @@ void keyswitch(Context& c, const uint64_t* a, uint32_t nq, const uint64_t* key,
 void rotate(Context& c, uint64_t* out, const uint64_t* ct, uint32_t nq, const uint64_t* key,
             uint32_t galois) {
   keyswitch(c, ct + (size_t)nq * c.n, nq, key, KeySwitchOut{out, ct, nullptr, galois});
+}
+
+void rotate_many(Context& c, uint64_t* const* outs, const uint64_t* const* cts, uint32_t nq,
+                 const uint64_t* const* keys, const uint32_t* galois, uint32_t count) {
+  const size_t n = c.n, ne = nq + c.K;
+  const uint32_t nd = num_digits(c, nq);
+  const size_t ct_words = (size_t)nd * ne * n;
+  // Per rotation: digits + ext (P limbs) + y, kept under 2 GiB per batch.
+  const size_t per_rot = (ct_words + 2 * (size_t)(c.K + nq) * n) * 8;
+  uint32_t batch = (uint32_t)std::max<size_t>(1, (size_t(2) << 30) / per_rot);
+  batch = std::min<uint32_t>(batch, MAX_KS_BATCH);
+  for (uint32_t r0 = 0; r0 < count; r0 += batch) {
+    const uint32_t b = std::min(batch, count - r0);
+    Scratch dig(c, b * ct_words);
+    std::vector<const uint64_t*> c1(b), dg(b);
+    std::vector<KeySwitchOut> ko(b);
+    for (uint32_t r = 0; r < b; ++r) {
+      c1[r] = cts[r0 + r] + (size_t)nq * n;
+      dg[r] = dig.p + r * ct_words;
+      ko[r] = KeySwitchOut{outs[r0 + r], cts[r0 + r], nullptr, galois[r0 + r]};
+    }
+    modup_batch(c, c1.data(), b, nq, dig.p);
+    keyswitch_batch(c, dg.data(), nq, keys + r0, b, ko.data());
+  }
 }
 
 void linear_transform(Context& c, uint64_t* out, const uint64_t* ct, uint32_t nq,

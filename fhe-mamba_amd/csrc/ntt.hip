@@ -275,7 +275,7 @@ struct EpiStore {
   // Q-limb key inner product plus the addend at position s.
   __device__ __forceinline__ uint64_t pre(size_t s, uint64_t q) const {
     const uint32_t p = blockIdx.y, r = p >> 1, b = p & 1, i = blockIdx.z;
-    const uint64_t* dg = e.digits + (size_t)i * n + s;
+    const uint64_t* dg = e.digits[r] + (size_t)i * n + s;
     const uint64_t* kr = e.key[r] + (size_t)b * e.kl + (size_t)i * n + s;
     const size_t dstride = (size_t)e.ne * n, kstride = 2 * e.kl;
     Acc128 acc;
@@ -330,7 +330,7 @@ struct KskLoad {
   uint32_t n;
   __device__ __forceinline__ uint64_t get(size_t s, uint64_t q) const {
     const uint32_t p = blockIdx.y, r = p >> 1, b = p & 1, t = blockIdx.z;
-    const uint64_t* dg = e.digits + (size_t)(e.nq + t) * n + s;
+    const uint64_t* dg = e.digits[r] + (size_t)(e.nq + t) * n + s;
     const uint64_t* kr = e.key[r] + (size_t)b * e.kl + (size_t)(e.L + t) * n + s;
     const size_t dstride = (size_t)e.ne * n, kstride = 2 * e.kl;
     Acc128 acc;
@@ -464,22 +464,25 @@ void launch_ksk(Context& c, uint64_t* ext, uint32_t npoly, uint32_t s_other, boo
 
 }  // namespace
 
-void ntt_forward_digits(Context& c, uint64_t* digits, uint32_t nd, uint32_t nq) {
-  if (nd == 0 || nq == 0) return;
+void ntt_forward_digits(Context& c, uint64_t* digits, uint32_t count, uint32_t nd,
+                        uint32_t nq) {
+  if (count == 0 || nd == 0 || nq == 0) return;
   if (nq > c.L) throw ArgError("ModUp level out of range");
+  if ((uint64_t)count * nd > 65535) throw ArgError("too many digits in one launch");
   const uint32_t ne = nq + c.K;
   // The last digit is the narrowest and so has the most converted limbs.
   const uint32_t w_last = nq - (nd - 1) * c.alpha;
   const uint32_t slots = ne - w_last;
-  const DigitMap map{c.alpha, nq, c.L, ne};
+  const DigitMap map{c.alpha, nq, c.L, ne, nd};
   const size_t ps = (size_t)ne * c.n;
+  const uint32_t npoly = count * nd;
   if (c.log_n <= 12) {
-    launch_single<false>(c, digits, nd, ps, slots, map);
+    launch_single<false>(c, digits, npoly, ps, slots, map);
     return;
   }
   const uint32_t s1 = (c.log_n + 1) / 2, s2 = c.log_n / 2;
-  launch_cols<false>(c, s1, s2, digits, nd, ps, slots, map, false);
-  launch_blocks<false>(c, s1, s2, digits, nd, ps, slots, map, true);
+  launch_cols<false>(c, s1, s2, digits, npoly, ps, slots, map, false);
+  launch_blocks<false>(c, s1, s2, digits, npoly, ps, slots, map, true);
 }
 
 void ntt_inverse_ksk(Context& c, uint64_t* ext_p, uint32_t npoly, const ModDownEpi& epi) {

@@ -48,6 +48,9 @@ void poly_rescale(Context& c, uint64_t* out, const uint64_t* a, uint32_t npoly, 
 uint32_t num_digits(const Context& c, uint32_t nq);
 // Digits [nd][nq+K][N] (evaluation form) of a [nq][N].
 void modup(Context& c, const uint64_t* a, uint32_t nq, uint64_t* digits);
+// ModUp of `count` inputs as[i] [nq][N] into digits [count][nd][nq+K][N].
+void modup_batch(Context& c, const uint64_t* const* as, uint32_t count, uint32_t nq,
+                 uint64_t* digits);
 // Result of one key switch r of a batch:
 //   out_b = galois-permute((ext_b[Q] - ModDownConv(ext_b[P])) * P^-1 + add_b),
 // b = 0, 1, with ext_b = sum_j digits_j (.) key_r,j,b over Q_l + P, addends
@@ -65,6 +68,9 @@ struct KeySwitchOut {
 // limbs and applies the combine and the Galois permutation.
 void keyswitch_batch(Context& c, const uint64_t* digits, uint32_t nq,
                      const uint64_t* const* keys, uint32_t batch, const KeySwitchOut* outs);
+// The same with digits[r] ([nd][nq+K][N]) per key switch.
+void keyswitch_batch(Context& c, const uint64_t* const* digits, uint32_t nq,
+                     const uint64_t* const* keys, uint32_t batch, const KeySwitchOut* outs);
 // ModUp of a [nq][N] (evaluation form) and one key switch.
 void keyswitch(Context& c, const uint64_t* a, uint32_t nq, const uint64_t* key,
                const KeySwitchOut& out);
@@ -76,6 +82,10 @@ void keyswitch_hoisted(Context& c, const uint64_t* digits, uint32_t nq,
 // out must not alias ct.
 void rotate(Context& c, uint64_t* out, const uint64_t* ct, uint32_t nq, const uint64_t* key,
             uint32_t galois);
+// Rotations of `count` different ciphertexts cts[r] [2][nq][N] by keys[r]:
+// batched ModUps and batched ModDowns.  outs[r] must not alias any cts[.].
+void rotate_many(Context& c, uint64_t* const* outs, const uint64_t* const* cts, uint32_t nq,
+                 const uint64_t* const* keys, const uint32_t* galois, uint32_t count);
 // Baby-step giant-step plaintext linear transform of ct [2][nq][N]:
 //   out = sum_{g < G} rot_giant^g( sum_{b < bstep} pts[g*bstep + b] (.) rot_b(ct) ),
 // G = ceil(count / bstep), rot_b by baby_keys[b - 1] (b >= 1; rot_0 = id, all

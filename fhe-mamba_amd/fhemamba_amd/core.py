@@ -209,6 +209,17 @@ class Context:
         call("fhe_rotate_hoisted", ct.handle, digits.handle, kh, _ptr(ga), count, oh)
         return outs
 
+    def rotate_many(self, cts, keys, galois, outs=None):
+        """Rotate cts[r] by keys[r] / galois[r] in one batched key switch."""
+        count = len(cts)
+        outs = outs if outs is not None else [Poly(self, 2, c.nlimb) for c in cts]
+        ch = (ctypes.c_void_p * count)(*[c.handle.value for c in cts])
+        kh = (ctypes.c_void_p * count)(*[k.handle.value for k in keys])
+        oh = (ctypes.c_void_p * count)(*[o.handle.value for o in outs])
+        ga = np.ascontiguousarray(galois, dtype=np.uint32)
+        call("fhe_rotate_many", oh, ch, kh, _ptr(ga), count)
+        return outs
+
     def linear_transform(self, ct, pts, bstep: int, baby_keys, baby_galois, giant_key=None,
                          giant_galois: int = 1, out=None):
         """BSGS transform: sum_g rot_giant^g(sum_b pts[g*bstep+b] * rot_b(ct)).

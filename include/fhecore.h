@@ -165,6 +165,15 @@ int fhe_rotation_precompute(const fhe_poly *ct, fhe_poly **digits);
 int fhe_rotate_hoisted(const fhe_poly *ct, const fhe_poly *digits,
                        const fhe_key *const *keys, const uint32_t *galois,
                        uint32_t count, fhe_poly *const *outs);
+/* EvalRotate over `count` different ciphertexts of one level at once
+ * (cts[r] by keys[r] / galois[r] into outs[r]): the per-stream rotations
+ * of the reference's Mamba-2 step (src/stage1_mamba2_decode_fideslib.cpp:
+ * 3865-3890, 4047-4052: the same rotate-sum step on every state group) as
+ * one batched ModUp and one batched ModDown.  Outputs must be distinct; an
+ * output may be one of the inputs. */
+int fhe_rotate_many(fhe_poly *const *outs, const fhe_poly *const *cts,
+                    const fhe_key *const *keys, const uint32_t *galois,
+                    uint32_t count);
 /* LinearTransformInPlace(ct, rowSize = count, bStep = bstep, pts)
  * (native/fideslib_stage0/patches/fideslib-v2.1.0-linear-transform-api.patch:21-38,
  *  called at src/stage1_mamba2_decode_fideslib.cpp:3517-3531; unfused form

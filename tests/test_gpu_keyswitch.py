@@ -112,6 +112,27 @@ def test_hoisted_pipelined_set_matches_oracle(setup):
         assert np.array_equal(out.numpy(), orc.rotate(ct, keys[g], g))
 
 
+def test_rotate_many_matches_single_rotations(setup):
+    """Five different ciphertexts (one level down), mixed keys, one output
+    written over its own input and one over another's: each equals the
+    oracle's rotation of the original input."""
+    ctx, orc, s = setup
+    rng = np.random.default_rng(16)
+    nq = ctx.L - 1
+    steps = [1, -1, 3, 1, 2 * ctx.n - 1]
+    gal = [O.galois_elt(r, ctx.n) for r in steps[:4]] + [steps[4]]
+    keys = {g: orc.galois_key(s, g, 80 + i) for i, g in enumerate(dict.fromkeys(gal))}
+    dkeys = {g: ctx.load_key(k) for g, k in keys.items()}
+    cts = [residues(rng, ctx.q[:nq], (2,), ctx.n) for _ in steps]
+    dcts = [ctx.upload(c) for c in cts]
+    outs = [ctx.poly(2, nq) for _ in steps]
+    outs[1] = dcts[1]          # in place
+    outs[3] = dcts[0]          # over another rotation's input
+    got = ctx.rotate_many(dcts, [dkeys[g] for g in gal], gal, outs=outs)
+    for r, (g, c) in enumerate(zip(gal, cts)):
+        assert np.array_equal(got[r].numpy(), orc.rotate(c, keys[g], g)), r
+
+
 def test_relinearize_matches_oracle(setup):
     ctx, orc, s = setup
     key = orc.relin_key(s, 5)
