@@ -543,6 +543,29 @@ class CryptoContext:
     def EvalRotateInPlace(self, a: "Ciphertext", index: int) -> None:  # noqa: N802
         a._assign(self.EvalRotate(a, index))
 
+    def EvalRotateMany(self, cts: Sequence["Ciphertext"], index) -> list:  # noqa: N802
+        """Rotate several ciphertexts (one index for all, or one each) in one
+        batched key switch; ciphertexts at different levels are grouped."""
+        idx = list(index) if isinstance(index, (list, tuple, np.ndarray)) else [index] * len(cts)
+        if len(idx) != len(cts):
+            raise ValueError("one rotation index per ciphertext")
+        outs: list = [None] * len(cts)
+        by_level: dict = {}
+        for j, (c, i) in enumerate(zip(cts, idx)):
+            g = galois_element(int(i), self.n)
+            if g == 1:
+                outs[j] = c.Clone()
+            else:
+                by_level.setdefault(c.level, []).append((j, g))
+        for level, items in by_level.items():
+            polys = self._ctx.rotate_many([cts[j].poly for j, _ in items],
+                                          [self._key_for(g) for _, g in items],
+                                          [g for _, g in items])
+            for (j, _), p in zip(items, polys):
+                c = cts[j]
+                outs[j] = self._wrap(p, c.level, c.deg, c.scale, c.slots)
+        return outs
+
     def EvalConjugate(self, a: "Ciphertext") -> "Ciphertext":  # noqa: N802
         g = conjugation_element(self.n)
         poly = self._ctx.rotate(a.poly, self._key_for(g), g)
