@@ -176,6 +176,68 @@ def run_ntt_batch(F, steps: int, warmup: int, count: int = 64):
     }
 
 
+def run_ssm_step(steps: int = 2, warmup: int = 1):
+    """One encrypted Mamba-2 SSM layer step at the 130M shape (24 heads x 64
+    channels x 128 states in six 32768-slot state ciphertexts) at N=2^16,
+    24 limbs: decay exp(dt A), state update, rotate-sum readout, D x.  Inputs
+    are seeded synthetic values with the model's distributions, encrypted
+    before timing; the result is decrypted after timing and compared with
+    the float64 reference."""
+    import numpy as np
+    from fhemamba_amd.ckks_probes import build_toy_context
+    from fhemamba_amd.mamba2 import (DecayPolynomial, EncryptedSSMStep, SSMShape,
+                                     expand_channels, expand_heads, expand_states, pack_state,
+                                     ssm_step_reference, unpack_state)
+
+    s = SSMShape()
+    rng = np.random.default_rng(5)
+    h = rng.normal(0, 0.5, (s.nheads, s.headdim, s.d_state))
+    x = np.clip(rng.normal(0, 1, (s.nheads, s.headdim)), -8, 8)
+    dt = np.clip(np.log1p(np.exp(rng.normal(0, 1, s.nheads))), 0.0, 6.0)
+    A = -np.exp(rng.uniform(0, np.log(16), s.nheads))
+    B, C = rng.normal(0, 0.3, s.d_state), rng.normal(0, 0.3, s.d_state)
+    D = rng.normal(0, 1, s.nheads)
+    cc, keys = build_toy_context(ring_dimension=N, batch=s.slots, depth=DEPTH,
+                                 scale_bits=SCALE_BITS, first_mod_bits=FIRST_BITS, seed=11)
+    step = EncryptedSSMStep(cc, keys, s, A, D, DecayPolynomial(amax=96.0, squarings=5,
+                                                               degree=13))
+    cc.EvalRotateKeyGen(keys.secretKey, step.rotation_indices())
+
+    def enc(v):
+        return cc.Encrypt(keys.publicKey, cc.MakeCKKSPackedPlaintext(list(v)))
+
+    xc = np.zeros(s.slots)
+    xc[: s.d_inner] = x.reshape(-1)
+    inputs = ([enc(v) for v in pack_state(h, s)], [enc(v) for v in expand_channels(x, s)],
+              [enc(v) for v in expand_heads(dt, s)], enc(expand_states(B, s)),
+              enc(expand_states(C, s)), enc(xc))
+    for _ in range(warmup):
+        step(*inputs)
+    cc.device.sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        new_state, y = step(*inputs)
+    cc.device.sync()
+    per_step = (time.perf_counter() - t0) / steps
+
+    def dec(ct):
+        pt = cc.Decrypt(ct, keys.secretKey)
+        pt.SetLength(s.slots)
+        return np.asarray(pt.GetRealPackedValue())
+
+    h2, y_ref = ssm_step_reference(h, x, dt, A, B, C, D)
+    err_h = float(np.max(np.abs(unpack_state([dec(c) for c in new_state], s) - h2)))
+    err_y = float(np.max(np.abs(dec(y)[: s.d_inner].reshape(s.nheads, s.headdim) - y_ref)))
+    return {
+        "s_per_layer_step": per_step,
+        "max_abs_err_state": err_h,
+        "max_abs_err_y": err_y,
+        "levels_used": int(y.GetLevel()),
+        "workload": ("Mamba-2-130M SSM layer step (24 heads x 64 x 128 states, six 32768-slot "
+                     "state ciphertexts), N=2^16, 24 limbs, synthetic seeded inputs"),
+    }
+
+
 def ntt_primes(log_n: int, bits: int, count: int):
     """Descending primes q = 1 mod 2N below 2^bits (deterministic)."""
     from fhemamba_amd.core import gen_moduli  # noqa: F401  (library must load)
@@ -265,6 +327,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--skip-ntt", action="store_true")
+    ap.add_argument("--skip-ssm", action="store_true")
     ap.add_argument("--copy-probe", action="store_true",
                     help="after the workloads, run one plain limb copy (k_copy_limbs) of "
                          f"{COPY_PROBE_BYTES} bytes read and the same written, untimed, as "
@@ -336,6 +399,9 @@ def main() -> int:
         out["ntt"]["workload"] = ("64 ciphertexts x 2 polys x 24 limbs, N=2^16: forward NTT, "
                                   "MAC over 64 plaintexts, inverse NTT")
         out["ntt"]["frac"] = ntt["ntt_gbps"] * 1e9 / HBM_PEAK
+    if not args.skip_ssm:
+        log("ssm layer step workload")
+        out["ssm_layer_step"] = run_ssm_step()
     if args.copy_probe:
         log("copy probe")
         copy_probe(F)
