@@ -38,7 +38,7 @@ HBM_PEAK = 8.0e12  # B/s, MI355X HBM3E
 # WRITE_SIZE on this workload (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0, the factors
 # a plain copy of known size reads back); recorded in
 # profiles/rotation_step_n65536_l24.md together with the commands.
-MEASURED_TRAFFIC: dict = {}
+MEASURED_TRAFFIC = {"ntt_fwd_blocks_moddown": 3_102_681_498 + 754_974_720}
 LOG_N, DEPTH, SCALE_BITS, FIRST_BITS, DNUM = 16, 23, 59, 60, 3
 N = 1 << LOG_N
 LIMB = N * 8  # bytes per limb
