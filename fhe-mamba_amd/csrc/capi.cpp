@@ -422,6 +422,21 @@ int fhe_mul_int(fhe_poly* out, const fhe_poly* a, int64_t v) {
   });
 }
 
+int fhe_mod_raise(fhe_poly* out, const fhe_poly* a, uint32_t nlimb) {
+  return guard([&] {
+    same_ctx(out, a);
+    need(a->nlimb >= 1 && a->npoly >= 1, "ModRaise needs at least one limb");
+    need(nlimb >= 1 && nlimb <= a->c->L, "ModRaise output must have 1..L limbs");
+    fhe::Context& c = *a->c;
+    const uint32_t npoly = a->npoly;
+    fhe::Scratch t(c, words(c, npoly, nlimb));
+    fhe::poly_mod_raise(c, t.p, nlimb, a->data, a->nlimb, npoly);
+    reshape(out, npoly, nlimb);
+    fhe::hip_check(hipMemcpyAsync(out->data, t.p, out->bytes, hipMemcpyDeviceToDevice, c.stream),
+                   "mod raise");
+  });
+}
+
 int fhe_rescale(fhe_poly* out, const fhe_poly* a) {
   return guard([&] {
     same_ctx(out, a);

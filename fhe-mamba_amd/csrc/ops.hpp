@@ -40,6 +40,11 @@ struct MacTable {
 };
 void poly_mac_table(Context& c, uint64_t* acc, const uint64_t* const* x,
                     const uint64_t* const* w, uint32_t cnt, uint32_t nq, bool accumulate);
+// ModRaise: limb 0 of each of npoly polys of a ([npoly][a_nlimb][N],
+// evaluation form mod q0) to coefficient form, centred, lifted to
+// q_0..q_{nq_out-1} and back to evaluation form in out [npoly][nq_out][N].
+void poly_mod_raise(Context& c, uint64_t* out, uint32_t nq_out, const uint64_t* a,
+                    uint32_t a_nlimb, uint32_t npoly);
 // Drop the last limb with centred division (FLEXIBLEAUTO rescale);
 // out is [npoly][nq-1][N].
 void poly_rescale(Context& c, uint64_t* out, const uint64_t* a, uint32_t npoly, uint32_t nq);

@@ -249,6 +249,25 @@ __global__ void __launch_bounds__(TPB)
   st2(t + ((size_t)blockIdx.z * l + i) * n + e, lift(v.x), lift(v.y));
 }
 
+// ModRaise lift: x [npoly][N] in coefficient form mod q0 -> out[p][j] =
+// (x centred mod q0) mod q_j for j < nq.  grid (N/512, nq, npoly).
+__global__ void __launch_bounds__(TPB)
+    k_mod_raise_lift(uint64_t* out, const uint64_t* x, const ModConst* mc, uint32_t n, uint32_t nq,
+                     uint64_t q0) {
+  const uint32_t j = blockIdx.y;
+  const ModConst m = mc[j];
+  const uint64_t q = m.q;
+  auto red = [&](uint64_t v) -> uint64_t { return reduce_2q(v - mulhi64(v, m.mu64) * q, q); };
+  const uint64_t q0m = red(q0), half = q0 >> 1;
+  const size_t e = pair_off();
+  const U2 v = ld2(x + (size_t)blockIdx.z * n + e);
+  auto lift = [&](uint64_t a) -> uint64_t {
+    const uint64_t r = red(a);
+    return a > half ? sub_mod(r, q0m, q) : r;
+  };
+  st2(out + ((size_t)blockIdx.z * nq + j) * n + e, lift(v.x), lift(v.y));
+}
+
 // Rescale step 2: out_i = (a_i - t_i) * q_l^-1.  grid (N/512, l, npoly).
 __global__ void __launch_bounds__(TPB)
     k_rescale_combine(uint64_t* out, const uint64_t* a, const uint64_t* t, const ModConst* mc,
@@ -344,6 +363,16 @@ void poly_mac_table(Context& c, uint64_t* acc, const uint64_t* const* x,
     FHE_LAUNCH(c, "k_mac_table", k_mac_table, grid_for(c, nq, 2), dim3(tpb_for(c)), 0, acc, t, c.d_const, c.n, nq, k, acc_flag);
     i += k;
   } while (i < cnt);
+}
+
+void poly_mod_raise(Context& c, uint64_t* out, uint32_t nq_out, const uint64_t* a,
+                    uint32_t a_nlimb, uint32_t npoly) {
+  if (nq_out == 0 || nq_out > c.L) throw ArgError("ModRaise: bad output level");
+  Scratch low(c, (size_t)npoly * c.n);
+  FHE_LAUNCH(c, "k_copy_limbs", k_copy_limbs, grid_for(c, 1, npoly), dim3(tpb_for(c)), 0, low.p, 1u, a, a_nlimb, c.n);
+  ntt_inverse(c, low.p, npoly, c.n, 1, LimbMap::contiguous(0));
+  FHE_LAUNCH(c, "k_mod_raise_lift", k_mod_raise_lift, grid_for(c, nq_out, npoly), dim3(tpb_for(c)), 0, out, low.p, c.d_const, c.n, nq_out, c.mods[0]);
+  ntt_forward(c, out, npoly, (size_t)nq_out * c.n, nq_out, LimbMap::contiguous(0));
 }
 
 void poly_rescale(Context& c, uint64_t* out, const uint64_t* a, uint32_t npoly, uint32_t nq) {

@@ -170,6 +170,12 @@ class Context:
         call("fhe_drop_limbs", out.handle, a.handle, nlimb)
         return out
 
+    def mod_raise(self, a, nlimb: int, out=None):
+        """Limb 0 of every poly, centred mod q0, lifted to nlimb limbs."""
+        out = self._out(out, a.npoly, nlimb)
+        call("fhe_mod_raise", out.handle, a.handle, nlimb)
+        return out
+
     def rescale(self, a, out=None):
         out = self._out(out, a.npoly, a.nlimb - 1)
         call("fhe_rescale", out.handle, a.handle)

@@ -133,6 +133,10 @@ int fhe_mul_int(fhe_poly *out, const fhe_poly *a, int64_t c);
 /* RescaleInPlace, FLEXIBLEAUTO (packed_fideslib.cpp:236): drop the last limb
  * with division by its prime and centred rounding. */
 int fhe_rescale(fhe_poly *out, const fhe_poly *a);
+/* ModRaise, the first step of EvalBootstrap (packed_fideslib.cpp:235-270,
+ * stage1_mamba2_decode_fideslib.cpp:2127): limb 0 (mod q0) of every poly
+ * of a, centred, lifted to q_0..q_{nlimb-1}; out is [npoly][nlimb]. */
+int fhe_mod_raise(fhe_poly *out, const fhe_poly *a, uint32_t nlimb);
 /* Tensor product of two 2-poly ciphertexts -> 3 polys (EvalMult core);
  * a == b gives the 3-product square (EvalSquareInPlace,
  * native/fideslib_stage0/src/fideslib_owned_arithmetic.hpp:10-19). */

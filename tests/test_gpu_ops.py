@@ -100,6 +100,39 @@ def test_rescale(pair, npoly):
     assert np.array_equal(da.numpy(), orc.rescale(a))
 
 
+def oracle_mod_raise(orc, q, a, nlimb):
+    """Limb 0 to coefficients (oracle iNTT), centred mod q0, reduced mod
+    each q_j and back through the oracle NTT."""
+    out = np.empty((a.shape[0], nlimb, a.shape[2]), dtype=np.uint64)
+    for p in range(a.shape[0]):
+        c = orc.ntt_inv(a[p, 0].copy(), 0).astype(object)
+        c = np.where(c > q[0] // 2, c - q[0], c)
+        for j in range(nlimb):
+            out[p, j] = orc.ntt_fwd(np.array([int(v) % q[j] for v in c], dtype=np.uint64), j)
+    return out
+
+
+def test_mod_raise(pair):
+    ctx, orc = pair
+    rng = np.random.default_rng(17)
+    for src_limbs, nlimb in ((1, ctx.L), (3, ctx.L - 1), (1, 1)):
+        a = residues(rng, ctx.q[:src_limbs], (2,), ctx.n)
+        got = ctx.mod_raise(ctx.upload(a), nlimb).numpy()
+        assert np.array_equal(got, oracle_mod_raise(orc, ctx.q, a, nlimb))
+    # in place, and the centring at the edges (0, q0 // 2, q0 // 2 + 1, q0 - 1)
+    c = np.zeros(ctx.n, dtype=np.uint64)
+    c[:4] = [0, ctx.q[0] // 2, ctx.q[0] // 2 + 1, ctx.q[0] - 1]
+    a = orc.ntt_fwd(c.copy(), 0)[None, None, :].copy()
+    da = ctx.upload(a)
+    ctx.mod_raise(da, ctx.L, out=da)
+    want = oracle_mod_raise(orc, ctx.q, a, ctx.L)
+    assert np.array_equal(da.numpy(), want)
+    # centred values 0, (q0-1)/2, -(q0-1)/2, -1 reduced mod q1 (q1 < q0/2 here)
+    coef = orc.ntt_inv(want[0, 1].copy(), 1)
+    q0, q1 = ctx.q[0], ctx.q[1]
+    assert [int(x) for x in coef[:4]] == [0, (q0 // 2) % q1, (q0 // 2 + 1 - q0) % q1, q1 - 1]
+
+
 @pytest.mark.parametrize("count", [1, 5, 40])
 def test_mac(pair, count):
     ctx, orc = pair
