@@ -1,0 +1,356 @@
+"""CKKS bootstrapping (full packing, slots = N/2) over the CKKS interface.
+
+Pipeline of EvalBootstrap as the reference drives it
+(native/fideslib_stage0/src/packed_fideslib.cpp:235-270,
+src/stage1_mamba2_decode_fideslib.cpp:2127-2297):
+  1. scale the input down by 2^-c (the correction that keeps the message
+     small against q0) and drop it to one limb;
+  2. ModRaise (fhe_mod_raise): the decryption becomes t = P + q0 I;
+  3. CoeffToSlot: the inverse special FFT (the encoder's, without its final
+     bit reversal), so slot s holds (t_j + i t_{j+n}) / q0 for j =
+     brv(s), scaled by 1/(2K);
+  4. EvalMod on the real and imaginary parts (split by conjugation):
+     sin(2 pi u) / (2 pi) ~ u - round(u) from a Chebyshev interpolant of
+     cos(2 pi (u - 1/4) / 2^r) on [-K, K] and r double-angle steps;
+  5. SlotToCoeff: the forward special FFT stages on the bit-reversed input,
+     scaled back by 2 pi q0 2^c / scale.
+The FFTs are factored into their radix-2 stages, grouped by the level
+budget; each group is one baby-step giant-step linear transform over the
+diagonals of the group's product (LinearTransformInPlace).
+
+The stage structure follows the encoder's special FFT (oracle/ckks_oracle.c
+fft_special / fft_special_inv: roots zeta^(5^j) of order 4 * slots).
+OpenFHE's exact bootstrapping (its level-budget split of the FFT, its sine
+approximation and scaling constants, the sparse-secret key) is not
+reproduced: the result is checked by decryption, not residue by residue.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from .ckks_probes import cheb_ps_depth, chebyshev_ps
+
+Diag = dict  # rotation offset -> complex diagonal vector
+
+
+# ----------------------------------------------------------------- FFT stages
+def _rot_group(n: int) -> np.ndarray:
+    m = 4 * n
+    out = np.empty(n, dtype=np.int64)
+    p = 1
+    for j in range(n):
+        out[j] = p
+        p = p * 5 % m
+    return out
+
+
+def _twiddle(k: int, m: int) -> complex:
+    a = 2.0 * math.pi * k / m
+    return complex(math.cos(a), math.sin(a))
+
+
+def forward_stage(n: int, length: int) -> Diag:
+    """Stage `length` of the decode FFT: for each block and j < h,
+    out[x] = a[x] + w_j a[x+h], out[x+h] = a[x] - w_j a[x+h]."""
+    m, h = 4 * n, length // 2
+    lenq, rot = 4 * length, _rot_group(n)
+    gap = m // lenq
+    w = np.array([_twiddle(int(rot[j] % lenq) * gap, m) for j in range(h)])
+    x = np.arange(n)
+    j = x % length
+    top = j < h
+    d0 = np.where(top, 1.0 + 0j, -w[np.where(top, 0, j - h)])
+    dp = np.where(top, w[np.where(top, j, 0)], 0j)
+    dm = np.where(top, 0j, 1.0 + 0j)
+    return _merge({0: d0, h % n: dp}, {(-h) % n: dm})
+
+
+def inverse_stage(n: int, length: int) -> Diag:
+    """Stage `length` of the encode FFT: out[x] = a[x] + a[x+h],
+    out[x+h] = conj(w_j) (a[x] - a[x+h])."""
+    m, h = 4 * n, length // 2
+    lenq, rot = 4 * length, _rot_group(n)
+    gap = m // lenq
+    wc = np.array([_twiddle(int((lenq - rot[j] % lenq) * gap), m) for j in range(h)])
+    x = np.arange(n)
+    j = x % length
+    top = j < h
+    wb = wc[np.where(top, 0, j - h)]
+    d0 = np.where(top, 1.0 + 0j, -wb)
+    dp = np.where(top, 1.0 + 0j, 0j)
+    dm = np.where(top, 0j, wb)
+    return _merge({0: d0, h % n: dp}, {(-h) % n: dm})
+
+
+def _merge(a: Diag, b: Diag) -> Diag:
+    out = {k: v.copy() for k, v in a.items()}
+    for k, v in b.items():
+        out[k] = out[k] + v if k in out else v.copy()
+    return out
+
+
+def compose(A: Diag, B: Diag, n: int) -> Diag:
+    """Diagonals of A(B(.)): sum over k + m = s of A_k * rot(B_m, k)."""
+    out: Diag = {}
+    for k, da in A.items():
+        for mo, db in B.items():
+            s = (k + mo) % n
+            term = da * np.roll(db, -k)
+            out[s] = out[s] + term if s in out else term
+    return out
+
+
+def apply_diags(D: Diag, a: np.ndarray) -> np.ndarray:
+    out = np.zeros_like(a, dtype=complex)
+    for k, d in D.items():
+        out += d * np.roll(a, -k)
+    return out
+
+
+def split_budget(stages: int, budget: int) -> list[int]:
+    """Stage counts per group, as even as possible, larger groups first."""
+    budget = max(1, min(budget, stages))
+    base, extra = divmod(stages, budget)
+    return [base + (1 if i < extra else 0) for i in range(budget)]
+
+
+def fft_groups(n: int, budget: int, inverse: bool) -> list[Diag]:
+    """The encode (inverse=True: stages n..2) or decode (stages 2..n) FFT
+    without bit reversal, as `budget` composed groups in application order."""
+    lengths = [1 << k for k in range(1, int(math.log2(n)) + 1)]
+    if inverse:
+        lengths = lengths[::-1]
+    stages = [inverse_stage(n, L) if inverse else forward_stage(n, L) for L in lengths]
+    groups, i = [], 0
+    for size in split_budget(len(stages), budget):
+        D = stages[i]
+        for s in stages[i + 1:i + size]:
+            D = compose(s, D, n)
+        groups.append(D)
+        i += size
+    return groups
+
+
+@dataclass
+class GroupPlan:
+    """One linear transform: out = sum_k pts[k] (.) rot(in, offset + k stride)."""
+    offset: int
+    stride: int
+    diags: list            # complex vectors (None for zero), index k
+    bstep: int
+
+    @property
+    def rows(self) -> int:
+        return len(self.diags)
+
+    def rotations(self) -> list[int]:
+        out = [b * self.stride for b in range(1, min(self.bstep, self.rows))]
+        if self.rows > self.bstep:
+            out.append(self.bstep * self.stride)
+        if self.offset:
+            out.append(self.offset)
+        return out
+
+    def prerotated(self) -> list:
+        """pts[k] rotated by -(k // bstep) * bstep * stride (LinearTransformInPlace)."""
+        out = []
+        for k, d in enumerate(self.diags):
+            if d is None:
+                out.append(None)
+            else:
+                out.append(np.roll(d, (k // self.bstep) * self.bstep * self.stride))
+        return out
+
+
+def plan_group(D: Diag, n: int, tol: float = 1e-12) -> GroupPlan:
+    """Lay a group's nonzero diagonals on an arithmetic progression of
+    rotation offsets (symmetric offsets -r..r of the smallest stride)."""
+    offs = [k for k, v in D.items() if np.max(np.abs(v)) > tol]
+    signed = sorted(((k + n // 2) % n) - n // 2 for k in offs)
+    nz = [abs(s) for s in signed if s]
+    stride = min(nz) if nz else 1
+    lo, hi = signed[0], signed[-1]
+    rows = (hi - lo) // stride + 1
+    diags = [None] * rows
+    for k in offs:
+        s = ((k + n // 2) % n) - n // 2
+        idx = (s - lo) // stride
+        diags[idx] = D[k] if diags[idx] is None else diags[idx] + D[k]
+    bstep = max(1, 1 << int(math.ceil(math.log2(max(1, math.isqrt(rows))))))
+    return GroupPlan(offset=lo, stride=stride, diags=diags, bstep=bstep)
+
+
+# ----------------------------------------------------------------- EvalMod
+@dataclass(frozen=True)
+class SineApprox:
+    """sin(2 pi u) for u in [-K, K] as cos(2 pi (u - 1/4) / 2^r) (Chebyshev
+    interpolant of degree `degree` in v = u / K) and r double-angle steps
+    cos(2x) = 2 cos(x)^2 - 1."""
+    K: float
+    r: int
+    degree: int
+
+    @property
+    def coeffs(self) -> list[float]:
+        f = lambda v: np.cos(2 * np.pi * (v * self.K - 0.25) / 2 ** self.r)  # noqa: E731
+        return [float(c) for c in np.polynomial.chebyshev.chebinterpolate(f, self.degree)]
+
+    def plain(self, u: np.ndarray) -> np.ndarray:
+        c = np.polynomial.chebyshev.chebval(np.asarray(u) / self.K, self.coeffs)
+        for _ in range(self.r):
+            c = 2 * c * c - 1
+        return c
+
+    def depth(self) -> int:
+        return cheb_ps_depth(self.degree) + self.r
+
+
+def uniform_ternary_bound(ring_dim: int) -> float:
+    """Power of two K bounding |I| in t = m + q0 I after ModRaise for a
+    uniform-ternary secret: each coefficient of I is a sum of about 2N/3 + 1
+    terms uniform in [-1/2, 1/2] (standard deviation sqrt(N / 18)); K covers
+    8 standard deviations."""
+    return float(1 << math.ceil(math.log2(8.0 * math.sqrt(ring_dim / 18.0))))
+
+
+NOISE_MODEL_OFFSET_BITS = 4.0
+
+
+def correction_bits_for(ring_dim: int, sine: SineApprox, in_scale: float, q0: float,
+                        scale: float) -> int:
+    """Scale-down c (the message enters ModRaise times 2^-c) balancing the
+    two errors of one bootstrap, in message units for a coefficient of size 1:
+      * noise: rescale / key-switch rounding of about N / sqrt(18) per
+        coefficient (uniform ternary secret) at the working scale, times K
+        (v = u / K), 2^r (double angles), sqrt(N / 2) (SlotToCoeff gain) and
+        q0 / (2 pi in_scale) (the way back), all times 2^c; the offset
+        NOISE_MODEL_OFFSET_BITS is measured (N = 2^12 and 2^16, 59-bit scale);
+      * the sine's cubic term: (2 pi a)^2 / 6 relative, a = 2^-c in_scale / q0.
+    Equal at 3c = log2((2 pi rho)^2 / 6) - e0, rho = in_scale / q0."""
+    rho = in_scale / q0
+    e0 = (math.log2(ring_dim / math.sqrt(18.0) / scale) + math.log2(sine.K) + sine.r
+          + 0.5 * math.log2(ring_dim / 2) + math.log2(q0 / (2 * math.pi * in_scale))
+          + NOISE_MODEL_OFFSET_BITS)
+    c = (math.log2((2 * math.pi * rho) ** 2 / 6.0) - e0) / 3.0
+    return max(0, min(30, int(round(c))))
+
+
+@dataclass
+class BootstrapConfig:
+    level_budget: tuple = (3, 3)
+    correction_bits: int = 0            # 0: chosen by correction_bits_for()
+    sine: SineApprox = field(default_factory=lambda: SineApprox(K=128.0, r=5, degree=59))
+
+    @classmethod
+    def for_ring(cls, ring_dim: int, level_budget=(3, 3), correction_bits: int = 0):
+        """K from the secret's bound; r double angles bring the interpolated
+        cosine down to K / 2^r = 4 periods over [-K, K] (degree 59) or 8
+        (degree 89) for the larger rings."""
+        K = uniform_ternary_bound(ring_dim)
+        if K <= 128:
+            sine = SineApprox(K=K, r=max(0, int(math.log2(K)) - 2), degree=59)
+        else:
+            sine = SineApprox(K=K, r=int(math.log2(K)) - 3, degree=89)
+        return cls(level_budget=tuple(level_budget), correction_bits=int(correction_bits),
+                   sine=sine)
+
+
+class CKKSBootstrapper:
+    """Full-packing bootstrapping for a CryptoContext of this package
+    (driven by CryptoContext.EvalBootstrapSetup / EvalBootstrap)."""
+
+    def __init__(self, cc, config: BootstrapConfig | None = None):
+        self.cc = cc
+        self.cfg = config or BootstrapConfig.for_ring(cc.GetRingDimension())
+        self.N = cc.GetRingDimension()
+        self.n = self.N // 2
+        self.c2s = [plan_group(D, self.n) for D in
+                    fft_groups(self.n, self.cfg.level_budget[0], inverse=True)]
+        self.s2c = [plan_group(D, self.n) for D in
+                    fft_groups(self.n, self.cfg.level_budget[1], inverse=False)]
+        self._coeffs = self.cfg.sine.coeffs
+        self._pts: dict = {}
+
+    def rotation_indices(self) -> list[int]:
+        out = set()
+        for g in self.c2s + self.s2c:
+            out.update(i % self.n for i in g.rotations())
+        return sorted(i for i in out if i)
+
+    def depth(self) -> int:
+        """Levels from ModRaise (level 0) to the output."""
+        return len(self.c2s) + self.cfg.sine.depth() + len(self.s2c)
+
+    def correction_bits(self, in_scale: float, q0: float, scale: float) -> int:
+        if self.cfg.correction_bits:
+            return self.cfg.correction_bits
+        return correction_bits_for(self.N, self.cfg.sine, in_scale, q0, scale)
+
+    # --------------------------------------------------------------- helpers
+    def _group_pts(self, which: str, idx: int, plan: GroupPlan, level: int, factor: float):
+        key = (which, idx, level, factor)
+        if key not in self._pts:
+            self._pts[key] = [None if d is None else
+                              self.cc.MakeCKKSPackedPlaintext(d * factor, 1, level)
+                              for d in plan.prerotated()]
+        return self._pts[key]
+
+    def _transform(self, ct, plans: list, which: str, total: float):
+        """Apply the groups in order; the constant `total` is spread evenly
+        over them (each diagonal set scaled by total^(1/groups))."""
+        factor = abs(total) ** (1.0 / len(plans))
+        sign = -1.0 if total < 0 else 1.0
+        for idx, plan in enumerate(plans):
+            if ct.GetNoiseScaleDeg() >= 2:
+                self.cc.RescaleInPlace(ct)
+            f = factor * (sign if idx == 0 else 1.0)
+            pts = self._group_pts(which, idx, plan, ct.GetLevel(), f)
+            self.cc.LinearTransformInPlace(ct, plan.rows, plan.bstep, pts, plan.stride,
+                                           plan.offset)
+        self.cc.RescaleInPlace(ct)
+        return ct
+
+    def _eval_mod(self, v):
+        c = chebyshev_ps(self.cc, v, self._coeffs, floor=1e-14)
+        for _ in range(self.cfg.sine.r):
+            sq = self.cc.EvalSquare(c)
+            c = self.cc.EvalSub(self.cc.EvalAdd(sq, sq), 1.0)
+        return c
+
+    # --------------------------------------------------------------- bootstrap
+    def bootstrap(self, ct, pre: float = 1.0, post: float = 1.0):
+        """Refresh ct; the slots are multiplied by `pre` on the way in (in
+        the scale-down step) and by `post` on the way out (in SlotToCoeff),
+        so a residual pass spends no extra level."""
+        cc, n, N = self.cc, self.n, self.N
+        L = len(cc.GetModuli()[0])
+        q0 = float(cc.GetModuli()[0][0])
+        x = ct.Clone()
+        cc.RescaleInPlace(x)
+        if x.GetLevel() > L - 2:
+            raise ValueError(f"EvalBootstrap needs the input at level <= {L - 2}")
+        x.SetLevel(L - 2)
+        c = self.correction_bits(cc.GetScalingFactorReal(L - 1), q0,
+                                 cc.GetScalingFactorReal(0))
+        x = cc.EvalMult(x, pre * 2.0 ** -c)
+        cc.RescaleInPlace(x)                                  # one limb left
+        in_scale = x.GetScalingFactor()
+        raised = cc.ModRaise(x)                               # decrypts to t = P + q0 I
+        # Slots of `raised` are Decode(t) / sf0; the encode stages map them
+        # to n * (t_j + i t_{j+n}) / sf0 at slot brv(j).  Scaled so that each
+        # part of u = (t_j + i t_{j+n}) / q0 arrives divided by 2K.
+        K = self.cfg.sine.K
+        y = self._transform(raised, self.c2s, "c2s",
+                            raised.GetScalingFactor() / (q0 * n * 2 * K))
+        yc = cc.EvalConjugate(y)
+        re = cc.EvalAdd(y, yc)                                # Re(u) / K
+        im = cc.MultByMonomial(cc.EvalSub(y, yc), 3 * N // 2)  # (2i Im(u) / 2K) * -i
+        re_m, im_m = self._eval_mod(re), self._eval_mod(im)   # sin(2 pi u) ~ 2 pi P / q0
+        w = cc.EvalAdd(re_m, cc.MultByMonomial(im_m, N // 2))
+        # The decode stages of (P_j + i P_{j+n}) / in_scale at slot brv(j)
+        # give the message times 2^-c.
+        back = q0 / (2 * math.pi * in_scale) * 2.0 ** c * post
+        return self._transform(w, self.s2c, "s2c", back)

@@ -219,6 +219,8 @@ class CryptoContext:
         self._galois: dict = {}
         self._seed = int.from_bytes(os.urandom(8), "little") if seed is None else int(seed)
         self._draws = 0
+        self._cache: dict = {}
+        self._boot = None
 
     # ------------------------------------------------------------ set-up
     def _next_seed(self) -> int:
@@ -642,6 +644,86 @@ class CryptoContext:
         poly = self._ctx.linear_transform(ct.poly, [None if p is None else p.poly for p in pts],
                                           bstep, baby_keys, baby_gal, gk, gg)
         ct._assign(self._wrap(poly, ct.level, ct.deg + deg, ct.scale * scale, ct.slots))
+
+    # ------------------------------------------------------------ bootstrapping
+    def _monomial(self, power: int, nq: int) -> Poly:
+        """X^power (power mod 2N) in evaluation form on nq limbs."""
+        key = ("monomial", power, nq)
+        if key not in self._cache:
+            n, q = self.n, self._ctx.q[:nq]
+            coef = np.zeros((1, nq, n), dtype=np.uint64)
+            k = power % (2 * n)
+            for j, qj in enumerate(q):
+                coef[0, j, k % n] = 1 if k < n else qj - 1
+            poly = self._ctx.upload(coef)
+            self._ctx.ntt_forward_dev(poly.data_ptr(), 1, nq, 0)
+            self._cache[key] = poly
+        return self._cache[key]
+
+    def MultByMonomial(self, a: "Ciphertext", power: int) -> "Ciphertext":  # noqa: N802
+        """a * X^power.  Slot j is multiplied by zeta^(power * 5^j) for the
+        primitive 2N-th root zeta; X^(N/2) multiplies every slot by i and
+        X^(3N/2) by -i.  Exact: no level, scale or noise change."""
+        poly = self._ctx.mul_plain(a.poly, self._monomial(int(power), a.poly.nlimb))
+        return self._wrap(poly, a.level, a.deg, a.scale, a.slots)
+
+    def ModRaise(self, a: "Ciphertext") -> "Ciphertext":  # noqa: N802
+        """Lift a one-limb ciphertext to every limb (level 0).  It then
+        decrypts to t = m + q0 * I with small integer I; its scale is set to
+        sf[0], so its slots decode to Decode(t) / sf[0]."""
+        if a.deg >= 2:
+            a = self._rescaled(a)
+        if a.poly.nlimb != 1:
+            raise ValueError("ModRaise needs a ciphertext with one limb left")
+        poly = self._ctx.mod_raise(a.poly, self.L)
+        return self._wrap(poly, 0, 1, self._sf[0], a.slots)
+
+    def EvalBootstrapSetup(self, levelBudget=(5, 5), dim1=(0, 0), slots: int = 0,  # noqa: N802,N803
+                           correctionFactor: int = 0, precompute: bool = True) -> None:
+        """Plan CoeffToSlot / SlotToCoeff for `slots` (full packing) with
+        levelBudget = (levels for CoeffToSlot, levels for SlotToCoeff).
+        correctionFactor 0 picks the message scale-down automatically."""
+        from .bootstrap import BootstrapConfig, CKKSBootstrapper
+        slots = int(slots) or self._slots
+        if slots != self.n // 2:
+            raise NotImplementedError("bootstrapping is implemented for full packing "
+                                      f"(slots = {self.n // 2})")
+        cfg = BootstrapConfig.for_ring(self.n, tuple(int(b) for b in levelBudget),
+                                       int(correctionFactor))
+        self._boot = CKKSBootstrapper(self, cfg)
+
+    def _bootstrapper(self):
+        if self._boot is None:
+            raise RuntimeError("call EvalBootstrapSetup first")
+        return self._boot
+
+    def EvalBootstrapKeyGen(self, secretKey: "PrivateKey", slots: int = 0) -> None:  # noqa: N802,N803
+        """Rotation keys of the CoeffToSlot / SlotToCoeff plans and the
+        conjugation key."""
+        boot = self._bootstrapper()
+        self.EvalRotateKeyGen(secretKey, boot.rotation_indices())
+        self.EvalConjugateKeyGen(secretKey)
+
+    def GetBootstrapDepth(self) -> int:  # noqa: N802
+        """Levels one EvalBootstrap consumes after ModRaise."""
+        return self._bootstrapper().depth()
+
+    def EvalBootstrap(self, ct: "Ciphertext", numIterations: int = 1,  # noqa: N802,N803
+                      precision: int = 0) -> "Ciphertext":
+        """Refresh `ct` to level GetBootstrapDepth() (slot values kept to
+        bootstrapping precision).  numIterations = 2 runs a second pass on
+        the scaled residual of the first (precision = log2 of that scale;
+        0 picks 12)."""
+        boot = self._bootstrapper()
+        out = boot.bootstrap(ct)
+        if int(numIterations) <= 1:
+            return out
+        if int(numIterations) != 2:
+            raise ValueError("numIterations must be 1 or 2")
+        bits = int(precision) or 12
+        residual = self.EvalSub(ct, out)
+        fix = boot.bootstrap(residual, pre=2.0 ** bits, post=2.0 ** -bits)
+        return self.EvalAdd(out, fix)
 
 
 class FastRotationPrecompute:

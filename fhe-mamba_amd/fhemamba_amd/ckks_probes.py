@@ -86,6 +86,59 @@ def cheb_ps_depth(degree: int) -> int:
     return depth(degree)
 
 
+def chebyshev_ps(cc, u, coeffs: Sequence[float], floor: float = CHEB_COEFF_FLOOR,
+                 const_ct=None):
+    """sum_i coeffs[i] T_i(u) by Paterson-Stockmeyer
+    (src/fhemamba/ckks_probes.py:108-155).  `const_ct(value)` supplies a
+    constant ciphertext when no term survives the coefficient floor."""
+    def constant(value: float):
+        if const_ct is None:
+            raise ValueError("Chebyshev series has no term above the coefficient floor")
+        return const_ct(value)
+
+    degree = len(coeffs) - 1
+    if degree < 1:
+        return constant(coeffs[0] if len(coeffs) else 0.0)
+    m = cheb_baby_size(degree)
+    cache = {1: u}
+
+    def cheb(i: int):
+        if i not in cache:
+            if i % 2 == 0:
+                h = cheb(i // 2)
+                sq = cc.EvalMult(h, h)
+                cache[i] = cc.EvalSub(cc.EvalAdd(sq, sq), 1.0)
+            else:
+                pr = cc.EvalMult(cheb(i // 2 + 1), cheb(i // 2))
+                cache[i] = cc.EvalSub(cc.EvalAdd(pr, pr), u)
+        return cache[i]
+
+    def evaluate(c: list[float]):
+        n = len(c) - 1
+        if n < m:
+            acc = None
+            for i in range(1, n + 1):
+                if abs(c[i]) < floor:
+                    continue
+                term = cc.EvalMult(cheb(i), c[i])
+                acc = term if acc is None else cc.EvalAdd(acc, term)
+            if acc is None:
+                return constant(c[0])
+            if abs(c[0]) >= floor:
+                acc = cc.EvalAdd(acc, c[0])
+            return acc
+        # p = a' + T_k * b~ using T_k T_j = (T_{k+j} + T_{k-j}) / 2.
+        k = _giant_split(n, m)
+        quot = [c[k]] + [2.0 * c[k + j] for j in range(1, n - k + 1)]
+        rem = list(c[:k])
+        for i in range(k + 1, n + 1):
+            rem[2 * k - i] -= c[i]
+        giant = cc.EvalMult(cheb(k), evaluate(quot))
+        return cc.EvalAdd(evaluate(rem), giant)
+
+    return evaluate(list(coeffs))
+
+
 class CkksPrimitives:
     """Elementary encrypted helpers over an OpenFHE-shaped context."""
 
@@ -122,48 +175,7 @@ class CkksPrimitives:
 
     def eval_chebyshev(self, u, coeffs: Sequence[float]):
         """sum_i coeffs[i] T_i(u) by Paterson-Stockmeyer."""
-        degree = len(coeffs) - 1
-        if degree < 1:
-            return self.const_ct(coeffs[0] if len(coeffs) else 0.0)
-        cc = self.cc
-        m = cheb_baby_size(degree)
-        cache = {1: u}
-
-        def cheb(i: int):
-            if i not in cache:
-                if i % 2 == 0:
-                    h = cheb(i // 2)
-                    sq = cc.EvalMult(h, h)
-                    cache[i] = cc.EvalSub(cc.EvalAdd(sq, sq), 1.0)
-                else:
-                    pr = cc.EvalMult(cheb(i // 2 + 1), cheb(i // 2))
-                    cache[i] = cc.EvalSub(cc.EvalAdd(pr, pr), u)
-            return cache[i]
-
-        def evaluate(c: list[float]):
-            n = len(c) - 1
-            if n < m:
-                acc = None
-                for i in range(1, n + 1):
-                    if abs(c[i]) < self.coefficient_floor:
-                        continue
-                    term = cc.EvalMult(cheb(i), c[i])
-                    acc = term if acc is None else cc.EvalAdd(acc, term)
-                if acc is None:
-                    return self.const_ct(c[0])
-                if abs(c[0]) >= self.coefficient_floor:
-                    acc = cc.EvalAdd(acc, c[0])
-                return acc
-            # p = a' + T_k * b~ using T_k T_j = (T_{k+j} + T_{k-j}) / 2.
-            k = _giant_split(n, m)
-            quot = [c[k]] + [2.0 * c[k + j] for j in range(1, n - k + 1)]
-            rem = list(c[:k])
-            for i in range(k + 1, n + 1):
-                rem[2 * k - i] -= c[i]
-            giant = cc.EvalMult(cheb(k), evaluate(quot))
-            return cc.EvalAdd(evaluate(rem), giant)
-
-        return evaluate(list(coeffs))
+        return chebyshev_ps(self.cc, u, coeffs, self.coefficient_floor, self.const_ct)
 
     def newton_refine(self, y, v_neg_half, iterations: int):
         """Newton steps for 1/sqrt(v): y <- 1.5 y + (-v/2) * y * y^2."""

@@ -1,0 +1,236 @@
+"""Bootstrapping plan on the CPU: the factored special FFT against the
+oracle's encode / decode FFT, the baby-step giant-step layout of each group,
+the sine approximation, and the whole circuit on a slot-level simulation
+(ModRaise simulated through the oracle's coefficient encoding)."""
+import math
+
+import numpy as np
+import pytest
+
+import oracle as O
+from fhemamba_amd import bootstrap as B
+
+
+def brv_perm(n):
+    bits = n.bit_length() - 1
+    return np.array([int(format(i, f"0{bits}b")[::-1], 2) if bits else 0 for i in range(n)])
+
+
+@pytest.mark.parametrize("n", [2, 4, 16, 128, 1024])
+@pytest.mark.parametrize("budget", [1, 2, 3, 4])
+def test_fft_groups_match_oracle_fft(n, budget):
+    rng = np.random.default_rng(n + budget)
+    z = rng.normal(size=n) + 1j * rng.normal(size=n)
+    coef = np.array(O.fft_special_inv(z))           # encode FFT (with its 1/n and bitrev)
+    # encode stages without bit reversal: n * coef at slot brv(j)
+    y = z.copy()
+    for g in B.fft_groups(n, budget, inverse=True):
+        y = B.apply_diags(g, y)
+    assert np.max(np.abs(y - n * coef[brv_perm(n)])) < 1e-12 * n
+    # decode stages on bit-reversed input give back the slots
+    w = coef[brv_perm(n)].copy()
+    for g in B.fft_groups(n, budget, inverse=False):
+        w = B.apply_diags(g, w)
+    assert np.max(np.abs(w - z)) < 1e-12 * n
+    assert np.allclose(np.array(O.fft_special(coef)), z)
+
+
+def test_stage_diagonals_are_sparse():
+    n = 64
+    for L in (2, 4, 64):
+        for D in (B.forward_stage(n, L), B.inverse_stage(n, L)):
+            assert sorted(D) == sorted({0, L // 2 % n, (-L // 2) % n})
+
+
+def test_split_budget():
+    assert B.split_budget(15, 4) == [4, 4, 4, 3]
+    assert B.split_budget(15, 1) == [15]
+    assert B.split_budget(3, 5) == [1, 1, 1]
+    assert sum(B.split_budget(11, 3)) == 11
+
+
+def simulate_linear_transform(ct, plan):
+    """LinearTransformInPlace semantics: rotate by offset, then
+    sum_g rot(sum_b pts[g*bs+b] * rot(ct, b*stride), g*bs*stride)."""
+    rot = lambda v, k: np.roll(v, -k)  # noqa: E731
+    x = rot(ct, plan.offset)
+    pts = plan.prerotated()
+    out = np.zeros_like(x)
+    for g in range((plan.rows + plan.bstep - 1) // plan.bstep):
+        inner = np.zeros_like(x)
+        for b in range(plan.bstep):
+            k = g * plan.bstep + b
+            if k < plan.rows and pts[k] is not None:
+                inner += pts[k] * rot(x, b * plan.stride)
+        out += rot(inner, g * plan.bstep * plan.stride)
+    return out
+
+
+@pytest.mark.parametrize("n,budget", [(256, 3), (1024, 4), (2048, 3), (32768, 4)])
+def test_group_plans_reproduce_groups(n, budget):
+    rng = np.random.default_rng(7)
+    x = rng.normal(size=n) + 1j * rng.normal(size=n)
+    for inverse in (True, False):
+        groups = B.fft_groups(n, budget, inverse) if n <= 2048 else \
+            B.fft_groups(n, budget, inverse)[:1]
+        for D in groups:
+            plan = B.plan_group(D, n)
+            assert plan.rows <= 2 ** (max(B.split_budget(int(math.log2(n)), budget)) + 1) - 1
+            assert np.max(np.abs(simulate_linear_transform(x, plan) - B.apply_diags(D, x))) \
+                < 1e-9
+            # every rotation the transform makes is in its key list
+            assert all(r % n for r in plan.rotations())
+
+
+def test_uniform_ternary_bound():
+    assert B.uniform_ternary_bound(2 ** 12) == 128
+    assert B.uniform_ternary_bound(2 ** 16) == 512
+
+
+@pytest.mark.parametrize("ring", [2 ** 10, 2 ** 12, 2 ** 16])
+def test_sine_approximation(ring):
+    s = B.BootstrapConfig.for_ring(ring).sine
+    K = int(s.K)
+    u = (np.arange(-K + 1, K)[:, None] + np.linspace(-2 ** -10, 2 ** -10, 17)[None, :]).ravel()
+    assert np.max(np.abs(s.plain(u) - np.sin(2 * np.pi * u))) < 1e-9
+    # the interpolant stays inside [-1, 1] (T_i stay bounded)
+    v = np.linspace(-1, 1, 20001)
+    assert np.max(np.abs(np.polynomial.chebyshev.chebval(v, s.coeffs))) <= 1 + 1e-9
+
+
+# ---------------------------------------------------------------- slot simulation
+class SimCt:
+    def __init__(self, z, level, deg=1):
+        self.z, self.level, self.deg = np.asarray(z, dtype=complex), level, deg
+
+    def Clone(self):  # noqa: N802
+        return SimCt(self.z.copy(), self.level, self.deg)
+
+    def GetLevel(self):  # noqa: N802
+        return self.level
+
+    def SetLevel(self, level):  # noqa: N802
+        self.level = level
+
+    def GetNoiseScaleDeg(self):  # noqa: N802
+        return self.deg
+
+
+class SimCC:
+    """Slot vectors in place of ciphertexts.  ModRaise goes through the
+    oracle's encoding: the coefficients t = Encode(z) * scale gain q0 * I for
+    random integers |I| < K / 2 and are decoded at scale sf0."""
+
+    def __init__(self, log_n, L, q0_bits=60, sf_bits=59, seed=0):
+        self.N, self.L = 1 << log_n, L
+        self.q0 = float(2 ** q0_bits - 2 ** 20 + 1)
+        self.sf = [2.0 ** sf_bits] * L
+        self.rng = np.random.default_rng(seed)
+        self.ibound = 0
+
+    def GetRingDimension(self):  # noqa: N802
+        return self.N
+
+    def GetModuli(self):  # noqa: N802
+        return [int(self.q0)] + [1] * (self.L - 1), []
+
+    def GetScalingFactorReal(self, level):  # noqa: N802
+        return self.sf[level]
+
+    def RescaleInPlace(self, ct):  # noqa: N802
+        while ct.deg >= 2:
+            ct.deg -= 1
+            ct.level += 1
+        assert ct.level < self.L
+
+    @staticmethod
+    def _val(x):
+        return x.z if isinstance(x, SimCt) else x
+
+    def _bin(self, a, b, f, deg_add):
+        level = max(a.level, b.level) if isinstance(b, SimCt) else a.level
+        deg = a.deg + (b.deg if isinstance(b, SimCt) else 1) if deg_add else a.deg
+        return SimCt(f(a.z, self._val(b)), level, deg)
+
+    def EvalAdd(self, a, b):  # noqa: N802
+        return self._bin(a, b, np.add, False)
+
+    def EvalSub(self, a, b):  # noqa: N802
+        return self._bin(a, b, np.subtract, False)
+
+    def EvalMult(self, a, b):  # noqa: N802
+        a = a.Clone()
+        self.RescaleInPlace(a)
+        if isinstance(b, SimCt):
+            b = b.Clone()
+            self.RescaleInPlace(b)
+        return self._bin(a, b, np.multiply, True)
+
+    def EvalSquare(self, a):  # noqa: N802
+        return self.EvalMult(a, a)
+
+    def EvalConjugate(self, a):  # noqa: N802
+        return SimCt(np.conj(a.z), a.level, a.deg)
+
+    def MultByMonomial(self, a, power):  # noqa: N802
+        n = self.N // 2
+        rot = np.array([pow(5, j, 2 * self.N) for j in range(n)], dtype=object)
+        e = np.array([int(power * r % (2 * self.N)) for r in rot], dtype=float)
+        return SimCt(a.z * np.exp(1j * np.pi * e / self.N), a.level, a.deg)
+
+    def MakeCKKSPackedPlaintext(self, values, deg=1, level=0):  # noqa: N802
+        return np.asarray(values, dtype=complex)
+
+    def LinearTransformInPlace(self, ct, rows, bstep, pts, stride, offset):  # noqa: N802
+        plan = B.GroupPlan(offset=offset, stride=stride, diags=[None] * rows, bstep=bstep)
+        plan.prerotated = lambda: pts
+        self.RescaleInPlace(ct)
+        ct.z = simulate_linear_transform(ct.z, plan)
+        ct.deg += 1
+
+    def ModRaise(self, x):  # noqa: N802
+        assert x.level == self.L - 1
+        coef = np.array(O.fft_special_inv(x.z))          # t / scale as complex pairs
+        t = np.round(coef * self.sf[self.L - 1])
+        I = self.rng.integers(-self.ibound, self.ibound + 1, size=(2, len(t)))
+        t = t + self.q0 * (I[0] + 1j * I[1])
+        return SimCt(np.array(O.fft_special(t / self.sf[0])), 0)
+
+    def GetScalingFactor(self, ct):
+        return self.sf[ct.level]
+
+
+SimCt.GetScalingFactor = lambda self: 2.0 ** 59
+
+
+@pytest.mark.parametrize("log_n,budget", [(8, (2, 2)), (10, (3, 3)), (11, (4, 2))])
+def test_bootstrap_circuit_on_slots(log_n, budget):
+    cc = SimCC(log_n, L=40)
+    cfg = B.BootstrapConfig.for_ring(1 << log_n, budget)
+    cc.ibound = int(cfg.sine.K) // 2
+    boot = B.CKKSBootstrapper(cc, cfg)
+    n = cc.N // 2
+    rng = np.random.default_rng(log_n)
+    m = rng.uniform(-1, 1, n) + 1j * rng.uniform(-1, 1, n)
+    out = boot.bootstrap(SimCt(m, 5))
+    assert out.level == boot.depth()
+    err = np.max(np.abs(out.z - m))
+    # noise-free: the sine's cubic term at |P / q0| <= 2^-(c+1) bounds the error
+    c = boot.correction_bits(2.0 ** 59, cc.q0, 2.0 ** 59)
+    assert c == B.correction_bits_for(cc.N, cfg.sine, 2.0 ** 59, cc.q0, 2.0 ** 59) >= 9
+    assert err < 1e-5, err
+
+
+def test_correction_bits_model():
+    """c grows with the room the noise leaves: 10 at N = 2^12 and 7 at
+    N = 2^16 for a 59-bit scale over a 60-bit q0; 0 at a 50-bit scale."""
+    for ring, sbits, want in ((2 ** 12, 59, 10), (2 ** 16, 59, 7), (2 ** 12, 50, 0)):
+        sine = B.BootstrapConfig.for_ring(ring).sine
+        assert B.correction_bits_for(ring, sine, 2.0 ** sbits, 2.0 ** 60, 2.0 ** sbits) == want
+
+
+def test_bootstrap_rejects_a_fresh_top_level_input():
+    cc = SimCC(8, L=30)
+    boot = B.CKKSBootstrapper(cc, B.BootstrapConfig.for_ring(256, (2, 2)))
+    with pytest.raises(ValueError):
+        boot.bootstrap(SimCt(np.zeros(128), 29))

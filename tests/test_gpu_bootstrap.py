@@ -1,0 +1,99 @@
+"""CKKS bootstrapping end to end on the GPU (EvalBootstrapSetup /
+EvalBootstrapKeyGen / EvalBootstrap as native/fideslib_stage0/src/
+packed_fideslib.cpp:235-270 drives them), checked by decryption against the
+input slots.  Tolerances: one pass keeps about 2^-18 absolute on values in
+[-1, 1] at these toy parameters (N = 2^12, uniform-ternary secret, K = 128,
+59-bit scale over a 60-bit q0, as the reference's bootstrapped chains use);
+the test allows 2^-16.  Two passes allow 2^-24."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+F = pytest.importorskip("fhemamba_amd")
+from fhemamba_amd.ckks_probes import build_toy_context  # noqa: E402
+
+LOG_N = 12
+SLOTS = 1 << (LOG_N - 1)
+ONE_PASS_TOL = 2.0 ** -16
+TWO_PASS_TOL = 2.0 ** -24
+
+
+@pytest.fixture(scope="module")
+def env():
+    cc, keys = build_toy_context(ring_dimension=1 << LOG_N, batch=SLOTS, depth=44,
+                                 scale_bits=59, first_mod_bits=60, seed=99)
+    cc.EvalBootstrapSetup([3, 3], [0, 0], SLOTS)
+    cc.EvalBootstrapKeyGen(keys.secretKey, SLOTS)
+    return cc, keys
+
+
+def enc_at(cc, keys, v, level):
+    ct = cc.Encrypt(keys.publicKey, cc.MakeCKKSPackedPlaintext(list(v)))
+    ct.SetLevel(level)
+    return ct
+
+
+def dec(cc, keys, ct, complex_=False):
+    pt = cc.Decrypt(ct, keys.secretKey)
+    pt.SetLength(SLOTS)
+    return np.asarray(pt.GetCKKSPackedValue() if complex_ else pt.GetRealPackedValue())
+
+
+def test_bootstrap_refreshes_real_slots(env):
+    cc, keys = env
+    L = len(cc.GetModuli()[0])
+    x = np.random.default_rng(1).uniform(-1, 1, SLOTS)
+    ct = enc_at(cc, keys, x, L - 2)
+    out = cc.EvalBootstrap(ct)
+    assert out.GetLevel() == cc.GetBootstrapDepth() < L - 2
+    err = np.max(np.abs(dec(cc, keys, out) - x))
+    print(f"one-pass bootstrap error 2^{np.log2(err):.1f}", flush=True)
+    assert err < ONE_PASS_TOL
+    # the refreshed ciphertext multiplies on
+    sq = cc.EvalMult(out, out)
+    assert np.max(np.abs(dec(cc, keys, sq) - x * x)) < 4 * ONE_PASS_TOL
+
+
+def test_bootstrap_complex_slots_and_lower_input_levels(env):
+    cc, keys = env
+    L = len(cc.GetModuli()[0])
+    rng = np.random.default_rng(2)
+    z = rng.uniform(-1, 1, SLOTS) + 1j * rng.uniform(-1, 1, SLOTS)
+    for level in (L - 2, L - 5):
+        ct = enc_at(cc, keys, z, level)
+        out = cc.EvalBootstrap(ct)
+        err = np.max(np.abs(dec(cc, keys, out, complex_=True) - z))
+        assert err < ONE_PASS_TOL, (level, err)
+
+
+def test_bootstrap_after_a_multiplication(env):
+    """A degree-2 input (unrescaled product) is rescaled first."""
+    cc, keys = env
+    L = len(cc.GetModuli()[0])
+    x = np.random.default_rng(3).uniform(-1, 1, SLOTS)
+    ct = enc_at(cc, keys, x, L - 4)
+    prod = cc.EvalMult(ct, ct)
+    assert prod.GetNoiseScaleDeg() == 2
+    out = cc.EvalBootstrap(prod)
+    assert np.max(np.abs(dec(cc, keys, out) - x * x)) < ONE_PASS_TOL
+
+
+def test_two_pass_bootstrap(env):
+    cc, keys = env
+    L = len(cc.GetModuli()[0])
+    x = np.random.default_rng(4).uniform(-1, 1, SLOTS)
+    ct = enc_at(cc, keys, x, L - 2)
+    out = cc.EvalBootstrap(ct, 2, 15)
+    err = np.max(np.abs(dec(cc, keys, out) - x))
+    print(f"two-pass bootstrap error 2^{np.log2(err):.1f}", flush=True)
+    assert err < TWO_PASS_TOL
+
+
+def test_bootstrap_input_checks(env):
+    cc, keys = env
+    x = np.zeros(SLOTS)
+    with pytest.raises(ValueError):
+        cc.EvalBootstrap(enc_at(cc, keys, x, len(cc.GetModuli()[0]) - 1))
+    with pytest.raises(NotImplementedError):
+        cc.EvalBootstrapSetup([3, 3], [0, 0], SLOTS // 2)
