@@ -12,7 +12,9 @@ resident in HBM before the timed region.  `value` is rotations/s.
 
 The same run also times the raw NTT / MAC batch (64 ciphertexts x 2 polys
 x 24 limbs at N = 2^16: forward NTT, plaintext MAC over the 64
-ciphertexts, inverse NTT) and reports NTT HBM GB/s.
+ciphertexts, inverse NTT) and reports NTT HBM GB/s, one encrypted Mamba-2
+SSM layer step at the 130M shape, and EvalBootstrap at N = 2^16 (one pass
+and the two-pass refresh, 45 limbs).
 
 Per-kernel times come from HIP events recorded on the library's stream
 around every launch (fhe_profile_begin / fhe_profile_end) over a profiled
@@ -238,6 +240,59 @@ def run_ssm_step(steps: int = 2, warmup: int = 1):
     }
 
 
+BOOT_DEPTH, BOOT_BUDGET = 44, (4, 4)
+# 1,083.2 s of bootstrapping over 2,187 EvalBootstrap calls in the reference's
+# Mamba-2-130M decode on GB10 (results/dgx/2026-09-24/owned-arithmetic/
+# m2-full-candidate/native.json, `timing` and `operation_counts`).
+REF_BOOTSTRAP_S = 1083.2 / 2187
+
+
+def run_bootstrap(steps: int = 3, warmup: int = 1):
+    """EvalBootstrap of one full-packing ciphertext (32768 slots) at N=2^16,
+    45 limbs (multiplicative depth 44, 59-bit scale, 60-bit q0), dnum 3,
+    level budget (4, 4): one pass and the two-pass refresh.  The input is a
+    seeded uniform vector in [-1, 1], encrypted and brought to the last
+    level but one before timing; errors are measured after timing."""
+    import numpy as np
+    from fhemamba_amd.ckks_probes import build_toy_context
+
+    slots = N // 2
+    cc, keys = build_toy_context(ring_dimension=N, batch=slots, depth=BOOT_DEPTH,
+                                 scale_bits=SCALE_BITS, first_mod_bits=FIRST_BITS, seed=21)
+    cc.EvalBootstrapSetup(list(BOOT_BUDGET), [0, 0], slots)
+    cc.EvalBootstrapKeyGen(keys.secretKey, slots)
+    L = len(cc.GetModuli()[0])
+    x = np.random.default_rng(8).uniform(-1, 1, slots)
+    ct = cc.Encrypt(keys.publicKey, cc.MakeCKKSPackedPlaintext(list(x)))
+    ct.SetLevel(L - 2)
+    res = {}
+    for passes in (1, 2):
+        for _ in range(warmup):
+            cc.EvalBootstrap(ct, passes)
+        cc.device.sync()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            out = cc.EvalBootstrap(ct, passes)
+        cc.device.sync()
+        sec = (time.perf_counter() - t0) / steps
+        pt = cc.Decrypt(out, keys.secretKey)
+        pt.SetLength(slots)
+        err = float(np.max(np.abs(np.asarray(pt.GetRealPackedValue()) - x)))
+        res[f"{'one' if passes == 1 else 'two'}_pass"] = {
+            "ms": sec * 1e3, "max_abs_err": err, "log2_err": float(np.log2(err))}
+    res.update({
+        "levels_consumed": cc.GetBootstrapDepth(),
+        "output_level": int(out.GetLevel()),
+        "rotation_keys": len(cc._boot.rotation_indices()),
+        "reference_gb10_ms_per_bootstrap": REF_BOOTSTRAP_S * 1e3,
+        "speedup_vs_reference_one_pass": REF_BOOTSTRAP_S / (res["one_pass"]["ms"] * 1e-3),
+        "workload": ("EvalBootstrap, 32768 slots, N=2^16, 45 limbs (depth 44, scale 2^59), "
+                     "dnum 3, level budget (4,4), uniform ternary secret (K=512); the "
+                     "reference figure is its GB10 mean over a full decode (sparse secret)"),
+    })
+    return res
+
+
 def ntt_primes(log_n: int, bits: int, count: int):
     """Descending primes q = 1 mod 2N below 2^bits (deterministic)."""
     from fhemamba_amd.core import gen_moduli  # noqa: F401  (library must load)
@@ -328,6 +383,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--skip-ntt", action="store_true")
     ap.add_argument("--skip-ssm", action="store_true")
+    ap.add_argument("--skip-bootstrap", action="store_true")
     ap.add_argument("--copy-probe", action="store_true",
                     help="after the workloads, run one plain limb copy (k_copy_limbs) of "
                          f"{COPY_PROBE_BYTES} bytes read and the same written, untimed, as "
@@ -402,6 +458,9 @@ def main() -> int:
     if not args.skip_ssm:
         log("ssm layer step workload")
         out["ssm_layer_step"] = run_ssm_step()
+    if not args.skip_bootstrap:
+        log("bootstrap workload")
+        out["bootstrap"] = run_bootstrap()
     if args.copy_probe:
         log("copy probe")
         copy_probe(F)
