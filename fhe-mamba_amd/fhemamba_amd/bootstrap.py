@@ -1,4 +1,4 @@
-"""CKKS bootstrapping (full packing, slots = N/2) over the CKKS interface.
+"""CKKS bootstrapping (full and sparse packing) over the CKKS interface.
 
 Pipeline of EvalBootstrap as the reference drives it
 (native/fideslib_stage0/src/packed_fideslib.cpp:235-270,
@@ -13,7 +13,7 @@ src/stage1_mamba2_decode_fideslib.cpp:2127-2297):
      sin(2 pi u) / (2 pi) ~ u - round(u) from a Chebyshev interpolant of
      cos(2 pi (u - 1/4) / 2^r) on [-K, K] and r double-angle steps;
   5. SlotToCoeff: the forward special FFT stages on the bit-reversed input,
-     scaled back by 2 pi q0 2^c / scale.
+     scaled back by q0 2^c / (2 pi scale).
 The FFTs are factored into their radix-2 stages, grouped by the level
 budget; each group is one baby-step giant-step linear transform over the
 diagonals of the group's product (LinearTransformInPlace).
@@ -220,19 +220,20 @@ NOISE_MODEL_OFFSET_BITS = 4.0
 
 
 def correction_bits_for(ring_dim: int, sine: SineApprox, in_scale: float, q0: float,
-                        scale: float) -> int:
+                        scale: float, slots: int = 0) -> int:
     """Scale-down c (the message enters ModRaise times 2^-c) balancing the
     two errors of one bootstrap, in message units for a coefficient of size 1:
       * noise: rescale / key-switch rounding of about N / sqrt(18) per
         coefficient (uniform ternary secret) at the working scale, times K
-        (v = u / K), 2^r (double angles), sqrt(N / 2) (SlotToCoeff gain) and
+        (v = u / K), 2^r (double angles), sqrt(slots) (SlotToCoeff gain) and
         q0 / (2 pi in_scale) (the way back), all times 2^c; the offset
         NOISE_MODEL_OFFSET_BITS is measured (N = 2^12 and 2^16, 59-bit scale);
       * the sine's cubic term: (2 pi a)^2 / 6 relative, a = 2^-c in_scale / q0.
     Equal at 3c = log2((2 pi rho)^2 / 6) - e0, rho = in_scale / q0."""
     rho = in_scale / q0
     e0 = (math.log2(ring_dim / math.sqrt(18.0) / scale) + math.log2(sine.K) + sine.r
-          + 0.5 * math.log2(ring_dim / 2) + math.log2(q0 / (2 * math.pi * in_scale))
+          + 0.5 * math.log2(slots or ring_dim // 2)
+          + math.log2(q0 / (2 * math.pi * in_scale))
           + NOISE_MODEL_OFFSET_BITS)
     c = (math.log2((2 * math.pi * rho) ** 2 / 6.0) - e0) / 3.0
     return max(0, min(30, int(round(c))))
@@ -259,14 +260,25 @@ class BootstrapConfig:
 
 
 class CKKSBootstrapper:
-    """Full-packing bootstrapping for a CryptoContext of this package
-    (driven by CryptoContext.EvalBootstrapSetup / EvalBootstrap)."""
+    """Bootstrapping of `slots`-slot ciphertexts for a CryptoContext of this
+    package (driven by CryptoContext.EvalBootstrapSetup / EvalBootstrap).
 
-    def __init__(self, cc, config: BootstrapConfig | None = None):
+    Sparse packing (slots n < N/2): the message lies in the subring of
+    X^(N/2n) and its slots repeat with period n over the N/2 evaluation
+    points.  After ModRaise the sum of rotations by n, 2n, ..., N/4 (the
+    trace onto that subring) turns t = m + q0 I into R (m + q0 I'), R =
+    N / 2n, where I' keeps I's coefficients at multiples of N/2n; the n-point
+    transforms then act on the n slots as they do at full packing, and 1/R
+    joins the CoeffToSlot constant."""
+
+    def __init__(self, cc, config: BootstrapConfig | None = None, slots: int = 0):
         self.cc = cc
         self.cfg = config or BootstrapConfig.for_ring(cc.GetRingDimension())
         self.N = cc.GetRingDimension()
-        self.n = self.N // 2
+        self.n = int(slots) or self.N // 2
+        if self.n < 2 or self.n & (self.n - 1) or self.n > self.N // 2:
+            raise ValueError(f"bootstrapping slots must be a power of two in [2, {self.N // 2}]")
+        self.R = self.N // (2 * self.n)
         self.c2s = [plan_group(D, self.n) for D in
                     fft_groups(self.n, self.cfg.level_budget[0], inverse=True)]
         self.s2c = [plan_group(D, self.n) for D in
@@ -274,11 +286,15 @@ class CKKSBootstrapper:
         self._coeffs = self.cfg.sine.coeffs
         self._pts: dict = {}
 
+    def trace_rotations(self) -> list[int]:
+        """Rotations n, 2n, ..., N/4 of the subring trace (empty at full packing)."""
+        return [self.n << k for k in range(int(math.log2(self.R)))]
+
     def rotation_indices(self) -> list[int]:
         out = set()
         for g in self.c2s + self.s2c:
             out.update(i % self.n for i in g.rotations())
-        return sorted(i for i in out if i)
+        return sorted(i for i in out if i) + self.trace_rotations()
 
     def depth(self) -> int:
         """Levels from ModRaise (level 0) to the output."""
@@ -287,14 +303,15 @@ class CKKSBootstrapper:
     def correction_bits(self, in_scale: float, q0: float, scale: float) -> int:
         if self.cfg.correction_bits:
             return self.cfg.correction_bits
-        return correction_bits_for(self.N, self.cfg.sine, in_scale, q0, scale)
+        return correction_bits_for(self.N, self.cfg.sine, in_scale, q0, scale, self.n)
 
     # --------------------------------------------------------------- helpers
     def _group_pts(self, which: str, idx: int, plan: GroupPlan, level: int, factor: float):
         key = (which, idx, level, factor)
         if key not in self._pts:
             self._pts[key] = [None if d is None else
-                              self.cc.MakeCKKSPackedPlaintext(d * factor, 1, level)
+                              self.cc.MakeCKKSPackedPlaintext(d * factor, 1, level,
+                                                              slots=self.n)
                               for d in plan.prerotated()]
         return self._pts[key]
 
@@ -308,16 +325,27 @@ class CKKSBootstrapper:
                 self.cc.RescaleInPlace(ct)
             f = factor * (sign if idx == 0 else 1.0)
             pts = self._group_pts(which, idx, plan, ct.GetLevel(), f)
+            # offsets mod n: rotations act on the n slots (5^-h and 5^(n-h)
+            # differ as automorphisms once n < N/2)
             self.cc.LinearTransformInPlace(ct, plan.rows, plan.bstep, pts, plan.stride,
-                                           plan.offset)
+                                           plan.offset % self.n)
         self.cc.RescaleInPlace(ct)
         return ct
 
-    def _eval_mod(self, v):
+    def _eval_mod(self, v, gain: int = 1):
+        """sin(2 pi u) * gain for v = u / K; the integer gain rides on the
+        last double angle (gain (2 y^2 - 1) = (2 gain) y^2 - gain by an
+        integer product, no level)."""
         c = chebyshev_ps(self.cc, v, self._coeffs, floor=1e-14)
-        for _ in range(self.cfg.sine.r):
+        r = self.cfg.sine.r
+        for step in range(r):
             sq = self.cc.EvalSquare(c)
-            c = self.cc.EvalSub(self.cc.EvalAdd(sq, sq), 1.0)
+            if step == r - 1 and gain != 1:
+                c = self.cc.EvalSub(self.cc.MultByInteger(sq, 2 * gain), float(gain))
+            else:
+                c = self.cc.EvalSub(self.cc.EvalAdd(sq, sq), 1.0)
+        if r == 0 and gain != 1:
+            c = self.cc.MultByInteger(c, gain)
         return c
 
     # --------------------------------------------------------------- bootstrap
@@ -339,18 +367,25 @@ class CKKSBootstrapper:
         cc.RescaleInPlace(x)                                  # one limb left
         in_scale = x.GetScalingFactor()
         raised = cc.ModRaise(x)                               # decrypts to t = P + q0 I
+        for r in self.trace_rotations():                      # sparse: R (P + q0 I')
+            raised = cc.EvalAdd(raised, cc.EvalRotate(raised, r))
         # Slots of `raised` are Decode(t) / sf0; the encode stages map them
-        # to n * (t_j + i t_{j+n}) / sf0 at slot brv(j).  Scaled so that each
-        # part of u = (t_j + i t_{j+n}) / q0 arrives divided by 2K.
+        # to n * (t_j + i t_{j+n}) / sf0 at slot brv(j) (coefficient index
+        # j N/2n under sparse packing).  Scaled so that each part of
+        # u = (t_j + i t_{j+n}) / q0 arrives divided by 2K.
         K = self.cfg.sine.K
         y = self._transform(raised, self.c2s, "c2s",
-                            raised.GetScalingFactor() / (q0 * n * 2 * K))
+                            raised.GetScalingFactor() / (q0 * n * 2 * K * self.R))
         yc = cc.EvalConjugate(y)
         re = cc.EvalAdd(y, yc)                                # Re(u) / K
         im = cc.MultByMonomial(cc.EvalSub(y, yc), 3 * N // 2)  # (2i Im(u) / 2K) * -i
-        re_m, im_m = self._eval_mod(re), self._eval_mod(im)   # sin(2 pi u) ~ 2 pi P / q0
-        w = cc.EvalAdd(re_m, cc.MultByMonomial(im_m, N // 2))
         # The decode stages of (P_j + i P_{j+n}) / in_scale at slot brv(j)
-        # give the message times 2^-c.
+        # give the message times 2^-c.  A power of two of the way-back factor
+        # moves into EvalMod so that each SlotToCoeff group's diagonals stay
+        # within 2 (times the scale) of the 62-bit encoding limit.
         back = q0 / (2 * math.pi * in_scale) * 2.0 ** c * post
-        return self._transform(w, self.s2c, "s2c", back)
+        gain = 1 << max(0, math.ceil(math.log2(max(back, 1.0))) - len(self.s2c))
+        re_m = self._eval_mod(re, gain)                       # gain sin(2 pi u)
+        im_m = self._eval_mod(im, gain)                       #   ~ gain 2 pi P / q0
+        w = cc.EvalAdd(re_m, cc.MultByMonomial(im_m, N // 2))
+        return self._transform(w, self.s2c, "s2c", back / gain)

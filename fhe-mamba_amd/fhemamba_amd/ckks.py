@@ -680,17 +680,15 @@ class CryptoContext:
 
     def EvalBootstrapSetup(self, levelBudget=(5, 5), dim1=(0, 0), slots: int = 0,  # noqa: N802,N803
                            correctionFactor: int = 0, precompute: bool = True) -> None:
-        """Plan CoeffToSlot / SlotToCoeff for `slots` (full packing) with
-        levelBudget = (levels for CoeffToSlot, levels for SlotToCoeff).
-        correctionFactor 0 picks the message scale-down automatically."""
+        """Plan CoeffToSlot / SlotToCoeff for `slots`-slot ciphertexts (full
+        or sparse packing) with levelBudget = (levels for CoeffToSlot, levels
+        for SlotToCoeff).  correctionFactor 0 picks the message scale-down
+        automatically."""
         from .bootstrap import BootstrapConfig, CKKSBootstrapper
         slots = int(slots) or self._slots
-        if slots != self.n // 2:
-            raise NotImplementedError("bootstrapping is implemented for full packing "
-                                      f"(slots = {self.n // 2})")
         cfg = BootstrapConfig.for_ring(self.n, tuple(int(b) for b in levelBudget),
                                        int(correctionFactor))
-        self._boot = CKKSBootstrapper(self, cfg)
+        self._boot = CKKSBootstrapper(self, cfg, slots)
 
     def _bootstrapper(self):
         if self._boot is None:

@@ -117,9 +117,11 @@ class SimCt:
 
 
 class SimCC:
-    """Slot vectors in place of ciphertexts.  ModRaise goes through the
-    oracle's encoding: the coefficients t = Encode(z) * scale gain q0 * I for
-    random integers |I| < K / 2 and are decoded at scale sf0."""
+    """Slot vectors (all N/2 evaluation points) in place of ciphertexts.
+    ModRaise goes through the oracle's encoding: the coefficients
+    t = Encode(z) * scale gain q0 * I for random integers |I| < K / 2 (at
+    every coefficient, also outside a sparse message's subring) and are
+    decoded at scale sf0."""
 
     def __init__(self, log_n, L, q0_bits=60, sf_bits=59, seed=0):
         self.N, self.L = 1 << log_n, L
@@ -169,6 +171,9 @@ class SimCC:
     def EvalSquare(self, a):  # noqa: N802
         return self.EvalMult(a, a)
 
+    def MultByInteger(self, a, value):  # noqa: N802
+        return SimCt(a.z * int(value), a.level, a.deg)
+
     def EvalConjugate(self, a):  # noqa: N802
         return SimCt(np.conj(a.z), a.level, a.deg)
 
@@ -178,8 +183,12 @@ class SimCC:
         e = np.array([int(power * r % (2 * self.N)) for r in rot], dtype=float)
         return SimCt(a.z * np.exp(1j * np.pi * e / self.N), a.level, a.deg)
 
-    def MakeCKKSPackedPlaintext(self, values, deg=1, level=0):  # noqa: N802
-        return np.asarray(values, dtype=complex)
+    def MakeCKKSPackedPlaintext(self, values, deg=1, level=0, slots=0):  # noqa: N802
+        v = np.asarray(values, dtype=complex)
+        return np.tile(v, (self.N // 2) // len(v))         # sparse slots repeat
+
+    def EvalRotate(self, a, k):  # noqa: N802
+        return SimCt(np.roll(a.z, -k), a.level, a.deg)
 
     def LinearTransformInPlace(self, ct, rows, bstep, pts, stride, offset):  # noqa: N802
         plan = B.GroupPlan(offset=offset, stride=stride, diags=[None] * rows, bstep=bstep)
@@ -227,6 +236,23 @@ def test_correction_bits_model():
     for ring, sbits, want in ((2 ** 12, 59, 10), (2 ** 16, 59, 7), (2 ** 12, 50, 0)):
         sine = B.BootstrapConfig.for_ring(ring).sine
         assert B.correction_bits_for(ring, sine, 2.0 ** sbits, 2.0 ** 60, 2.0 ** sbits) == want
+
+
+@pytest.mark.parametrize("log_n,slots", [(10, 64), (11, 8), (11, 512)])
+def test_sparse_bootstrap_circuit_on_slots(log_n, slots):
+    """Sparse packing: the trace after ModRaise removes I's coefficients
+    outside the subring, so only the n slots' own coefficients reach EvalMod."""
+    cc = SimCC(log_n, L=40, seed=slots)
+    cfg = B.BootstrapConfig.for_ring(1 << log_n, (2, 2))
+    cc.ibound = int(cfg.sine.K) // 2
+    boot = B.CKKSBootstrapper(cc, cfg, slots)
+    assert boot.trace_rotations() == [slots << k for k in range(int(math.log2(boot.R)))]
+    rng = np.random.default_rng(slots)
+    m = rng.uniform(-1, 1, slots) + 1j * rng.uniform(-1, 1, slots)
+    out = boot.bootstrap(SimCt(np.tile(m, boot.R), 5))
+    assert np.max(np.abs(out.z - np.tile(m, boot.R))) < 1e-5
+    with pytest.raises(ValueError):
+        B.CKKSBootstrapper(cc, cfg, 3)
 
 
 def test_bootstrap_rejects_a_fresh_top_level_input():

@@ -95,5 +95,26 @@ def test_bootstrap_input_checks(env):
     x = np.zeros(SLOTS)
     with pytest.raises(ValueError):
         cc.EvalBootstrap(enc_at(cc, keys, x, len(cc.GetModuli()[0]) - 1))
-    with pytest.raises(NotImplementedError):
-        cc.EvalBootstrapSetup([3, 3], [0, 0], SLOTS // 2)
+    with pytest.raises(ValueError):
+        cc.EvalBootstrapSetup([3, 3], [0, 0], 3)
+
+
+@pytest.mark.parametrize("slots", [8, 256])
+def test_sparse_packing_bootstrap(slots):
+    """Sparse packing (slots < N/2), as the reference's packed programs use
+    it (batch size = program slots on a larger ring)."""
+    cc, keys = build_toy_context(ring_dimension=1 << LOG_N, batch=slots, depth=44,
+                                 scale_bits=59, first_mod_bits=60, seed=7 + slots)
+    cc.EvalBootstrapSetup([2, 2], [0, 0], slots)
+    cc.EvalBootstrapKeyGen(keys.secretKey, slots)
+    L = len(cc.GetModuli()[0])
+    x = np.random.default_rng(slots).uniform(-1, 1, slots)
+    ct = cc.Encrypt(keys.publicKey, cc.MakeCKKSPackedPlaintext(list(x)))
+    ct.SetLevel(L - 2)
+    for passes, tol in ((1, ONE_PASS_TOL), (2, TWO_PASS_TOL)):
+        out = cc.EvalBootstrap(ct, passes, 15)
+        pt = cc.Decrypt(out, keys.secretKey)
+        pt.SetLength(slots)
+        err = np.max(np.abs(np.asarray(pt.GetRealPackedValue()) - x))
+        print(f"sparse {slots} slots, {passes} pass(es): error 2^{np.log2(err):.1f}", flush=True)
+        assert err < tol
