@@ -1,0 +1,278 @@
+"""Packed-program executor on the CPU: the reader against the reference's
+own parser cases (native/fideslib_stage0/tests/test_packed_program.cpp),
+output errors, the rotation-sum schedule, the replicated matrix layout and
+monotone routing against numpy, and every node kind through the executor
+on a slot-level stand-in for the CKKS context."""
+import math
+
+import numpy as np
+import pytest
+
+from fhemamba_amd import packed as P
+from packed_builder import ProgramBuilder, SlotContext, SlotKeys
+
+VALID = "fhemamba-packed-v1 8 64 2 1\ninput 2 0 2 1 2\ngather 2 1 0 2 1 0\n1 2 2 1 2 1\n"
+EXTENDED = ("fhemamba-packed-v2 8 64 4 1\n"
+            "input 2 8 0 2 1 2\nlinear 2 16 1 0 4 1 0 0 1\n"
+            "linear_ref 2 16 1 0 1 1\nfeedback 2 8 1 2 0\n2 2 1 2 1 2\n")
+
+
+def test_reader_accepts_the_reference_cases():
+    p = P.read_packed_program(VALID)
+    assert p.slots == 8 and len(p.nodes) == 2 and p.outputs[0].exact[0] == 2
+    e = P.packed_output_errors([2.0005, 1], p.outputs[0])
+    assert e.passes(.001, .001) and not e.passes(.0001, .001) and not e.passes(.001, .0001)
+    assert not e.passes(math.inf, .001)
+    nf = P.packed_output_errors([math.nan, 1], p.outputs[0])
+    assert nf.non_finite == 1 and not nf.passes(.001, .001)
+    with pytest.raises(ValueError):
+        P.packed_output_errors([2], p.outputs[0])
+    v2 = P.read_packed_program(EXTENDED)
+    assert v2.nodes[2].operation == "linear_ref" and v2.nodes[2].bound == 16
+    assert v2.nodes[3].operation == "feedback" and len(v2.nodes[3].data) == 0
+
+
+def test_reader_parses_a_long_chain():
+    n = 20000
+    lines = [f"fhemamba-packed-v2 8 64 {n} 1", "input 1 8 0 1 1"]
+    lines += [f"addp 1 8 1 {i - 1} 1 0" for i in range(1, n)]
+    lines.append(f"{n - 1} 1 1 1")
+    p = P.read_packed_program("\n".join(lines))
+    assert len(p.nodes) == n and p.outputs[0].node == n - 1
+
+
+@pytest.mark.parametrize("text", [
+    "fhemamba-packed-v1 3 64 1 1",                                   # non-power-of-two slots
+    "fhemamba-packed-v2 8 64 1000001 1",                             # node count bound
+    "fhemamba-packed-v1 8 64 1 1 input 2 0 2 1 nan",                 # invalid constant
+    "fhemamba-packed-v1 8 64 1 1 add 2 2 0 0 0",                     # future dependency
+    "fhemamba-packed-v1 8 64 2 1 input 2 0 2 1 2 gather 1 1 0 1 2",  # index overflow
+    VALID + "trailing",
+    "fhemamba-packed-v2 8 64 1 1 input 2 65 0 2 1 2",                # bound above the header's
+    "fhemamba-packed-v2 8 64 2 1 input 2 8 0 2 1 2 linear_ref 2 8 1 0 1 0",  # not a weight
+    "fhemamba-packed-v2 8 64 2 1 input 2 8 0 2 1 2 feedback 3 8 1 0 0",      # width change
+    "fhemamba-packed-v1 8 64 2 1 input 2 0 2 1 2 feedback 2 1 0 0",  # v2-only operation
+    "fhemamba-packed-v1 8 64 2 1 input 4 0 4 1 2 3 4 repeat 12 1 0 3 1 4 3",  # v1 repeat 3
+    "fhemamba-packed-v1 8 64 2 1 input 4 0 4 1 2 3 4 sum 1 1 0 1 3",  # width not 2^k
+    "fhemamba-packed-v1 8 64 2 1 input 2 0 2 1 2 scatter 4 1 0 2 1 1",  # repeated target
+    "fhemamba-packed-v1 8 64 2 1 input 2 0 2 1 2 cheb 2 1 0 4 1 0 1 1",  # lo >= hi
+])
+def test_reader_rejects(text):
+    with pytest.raises(ValueError):
+        P.read_packed_program(text)
+
+
+@pytest.mark.parametrize("count", list(range(1, 41)) + [127, 128, 1000])
+def test_rotation_sum_schedule_covers_every_shift_once(count):
+    terms = {0: 1}       # shift -> multiplicity in the running sum
+    for off, acc in P.rotation_sum_schedule(count):
+        src = dict(terms) if acc else {0: 1}
+        for k, c in src.items():
+            terms[k + off] = terms.get(k + off, 0) + c
+    assert terms == {k: 1 for k in range(count)}
+
+
+def replicated_numpy(W, x, slots):
+    """The replicated layout evaluated with numpy rotations."""
+    m, n = W.shape
+    s = P.replicated_shape(m, n, slots)
+    rot = lambda v, k: np.roll(v, -k)  # noqa: E731
+    v = np.zeros(slots)
+    v[:n] = x
+
+    def rsum(a, count, stride):
+        out = a
+        for off, acc in P.rotation_sum_schedule(count):
+            out = out + rot(out if acc else a, off * stride)
+        return out
+
+    rep = rsum(rsum(v, s.reps, -n), s.replicas + s.guard, -s.window)
+    out = np.zeros(slots)
+    for k in range(s.per_replica):
+        out += P.replicated_mask(W, k, s, slots) * rot(rep, k * s.replicas)
+    out = rsum(out, s.replicas, s.window + 1)
+    return out[:m], s
+
+
+@pytest.mark.parametrize("m,n,slots", [(4, 4, 64), (8, 3, 64), (16, 24, 256), (48, 24, 1024),
+                                       (100, 7, 1024), (1536, 768, 32768)])
+def test_replicated_layout_computes_the_product(m, n, slots):
+    rng = np.random.default_rng(m * n)
+    W = rng.normal(size=(m, n))
+    x = rng.normal(size=n)
+    got, s = replicated_numpy(W, x, slots)
+    assert s.replicas > 1
+    assert (s.replicas + s.guard) * s.window <= slots and s.window % n == 0
+    assert np.allclose(got, W @ x)
+
+
+def test_replicated_shape_falls_back_when_nothing_fits():
+    assert P.replicated_shape(60, 60, 64).replicas == 1
+    s = P.replicated_shape(1536, 768, 32768)
+    assert (s.replicas, s.window, s.per_replica) == (13, 2304, 60)
+
+
+def route_numpy(x, idx, scatter, slots):
+    rot = lambda v, k: np.roll(v, -k)  # noqa: E731
+    v = np.zeros(slots)
+    v[: len(x)] = x
+    for stage in P.monotone_routing(idx, scatter):
+        nxt = np.zeros(slots)
+        for off, positions in stage.items():
+            sel = np.zeros(slots)
+            sel[positions] = 1
+            nxt += rot(v * sel, off)
+        v = nxt
+    return v
+
+
+def test_monotone_routing_gathers_and_scatters():
+    rng = np.random.default_rng(3)
+    slots = 4096
+    idx = np.sort(rng.choice(3000, 200, replace=False))
+    x = rng.normal(size=3000)
+    g = route_numpy(x, idx, False, slots)
+    assert np.allclose(g[:200], x[idx]) and np.allclose(g[200:], 0)
+    y = rng.normal(size=200)
+    sc = route_numpy(y, idx, True, slots)
+    want = np.zeros(slots)
+    want[idx] = y
+    assert np.allclose(sc, want)
+    with pytest.raises(ValueError):
+        P.monotone_routing([3, 2], False)
+
+
+# ---------------------------------------------------------------- executor
+def run_slots(builder, **kw):
+    program = P.read_packed_program(builder.text())
+    cc = SlotContext(program.slots)
+    ev = P.PackedEvaluator(cc, SlotKeys(), program.slots, **kw)
+    outs = ev.evaluate(program)
+    return program, ev, [ev.decrypt(ct, len(o.polynomial)) for o, ct in zip(program.outputs, outs)]
+
+
+def check(builder, tol=1e-9, **kw):
+    program, ev, values = run_slots(builder, **kw)
+    for o, v in zip(program.outputs, values):
+        e = P.packed_output_errors(v, o)
+        assert e.passes(tol, tol), (e, o.node, program.nodes[o.node].operation)
+    return ev
+
+
+def test_every_node_kind_on_slots():
+    rng = np.random.default_rng(5)
+    b = ProgramBuilder(256, bound=64.0, extended=True)
+    x = b.input(rng.uniform(-1, 1, 16))
+    c = b.public(rng.uniform(-1, 1, 16))
+    s = b.add(x, c)
+    m = b.mul(s, x)
+    sq = b.mul(m, m)
+    ap = b.addp(sq, rng.uniform(-1, 1, 16))
+    mp = b.mulp(ap, rng.uniform(-1, 1, 16))
+    W = rng.normal(size=(24, 16)) * 0.3
+    lin = b.linear(mp, W)
+    lr = b.linear_ref(x, lin)                  # shared weight table
+    g = b.gather(lin, [3, 1, 4, 1, 5, 9, 2, 6])   # non-monotone
+    sc = b.scatter(g, [0, 2, 4, 6, 8, 10, 12, 14], 16)
+    rp = b.repeat(sc, 2, 8, 3)
+    sm = b.sum(b.addp(rp, np.zeros(48)), 16)
+    ch = b.cheb(x, -1.5, 1.5, [0.1, 0.5, -0.2, 0.05, 0.01, -0.003])
+    for node in (s, m, sq, ap, mp, lin, lr, g, sc, rp, sm, ch):
+        b.output(node)
+    ev = check(b)
+    assert ev.stats["rotations"] > 0 and ev.stats["logical_refreshes"] == 0
+
+
+def test_direct_linear_matches_replicated():
+    rng = np.random.default_rng(6)
+    b = ProgramBuilder(512)
+    x = b.input(rng.uniform(-1, 1, 32))
+    b.output(b.linear(x, rng.normal(size=(40, 32))))
+    check(b, replicated_linear=False)
+    check(b, replicated_linear=True)
+
+
+def test_large_monotone_gather_uses_routing_stages():
+    rng = np.random.default_rng(7)
+    b = ProgramBuilder(4096)
+    x = b.input(rng.uniform(-1, 1, 3000))
+    idx = np.sort(rng.choice(3000, 300, replace=False))
+    g = b.gather(x, idx)
+    b.output(g)
+    b.output(b.scatter(g, idx, 3000))
+    check(b)
+
+
+def test_deep_chain_is_refreshed():
+    """Eighty levels of products pass the ceiling several times."""
+    rng = np.random.default_rng(8)
+    b = ProgramBuilder(64, bound=4.0)
+    v = b.input(rng.uniform(0.5, 1.5, 8))
+    w = b.input(np.ones(8))
+    for _ in range(40):                     # v <- (v * w) * 1: two levels, same value,
+        v = b.mulp(b.mul(v, w), np.ones(8))  # errors add (no amplification)
+    b.output(v)
+    program, ev, values = run_slots(b)
+    assert ev.stats["logical_refreshes"] >= 3
+    assert ev.stats["bootstraps"] == 2 * ev.stats["logical_refreshes"]
+    assert np.allclose(values[0], b.values[v])
+
+
+def test_feedback_uses_the_client():
+    rng = np.random.default_rng(9)
+    b = ProgramBuilder(64, extended=True)
+    h = b.input(rng.uniform(-1, 1, 4))
+    fb = b.feedback(h, np.zeros(4))
+    b.output(h)
+    b.output(fb, np.full(4, 7.0))
+    program = P.read_packed_program(b.text())
+    calls = []
+
+    def client(ev, node, hidden):
+        calls.append(node)
+        return np.full(4, 7.0)
+
+    ev = P.PackedEvaluator(SlotContext(64), SlotKeys(), 64, client=client)
+    outs = ev.evaluate(program)
+    assert calls == [1] and np.allclose(ev.decrypt(outs[1], 4), 7.0)
+    with pytest.raises(RuntimeError):
+        P.PackedEvaluator(SlotContext(64), SlotKeys(), 64).evaluate(program)
+
+
+def test_command_line_options():
+    o = P.parse_args(["p.txt", "r.json", "1e-3", "1e-2", "--bootstrap-passes", "1",
+                      "--cache-plaintexts", "--prefetch-workers", "2", "--direct-linear"])
+    assert o["bootstrap_passes"] == 1 and o["direct_linear"] and o["exact_tol"] == 1e-2
+    assert o["accepted"] == ["--cache-plaintexts", "--prefetch-workers 2"]
+    for bad in (["p", "r", "1"], ["p", "r", "0", "1"], ["p", "r", "1", "1", "--bogus"],
+                ["p", "r", "1", "1", "--bootstrap-passes", "3"],
+                ["p", "r", "1", "1", "--security", "256"],
+                ["p", "r", "1", "1", "--s2c-first"]):
+        with pytest.raises(ValueError):
+            P.parse_args(bad)
+
+
+def test_client_head_reader(tmp_path):
+    rng = np.random.default_rng(10)
+    w = rng.normal(size=(5, 4)).astype("<f4")
+    path = tmp_path / "head.f32"
+    path.write_bytes(np.array([5, 4], dtype="<u4").tobytes() + w.tobytes())
+    c = P.GenerationClient(str(path))
+    h = rng.normal(size=4)
+    emb = c.select(h)
+    best = int(np.argmax(w.astype(np.float64) @ h))
+    assert c.tokens == [best] and np.allclose(emb, w[best])
+    path.write_bytes(np.array([5, 4], dtype="<u4").tobytes() + w.tobytes()[:-4])
+    with pytest.raises(ValueError):
+        P.GenerationClient(str(path))
+
+
+def test_launcher_reports_bad_arguments_with_exit_code_2():
+    import os
+    import subprocess
+    import sys
+    launcher = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                            "fhe-mamba_amd", "packed_fhemamba")
+    r = subprocess.run([sys.executable, launcher, "p.txt", "r.json", "1e-3"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 2 and "usage" in r.stderr
