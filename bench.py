@@ -14,7 +14,8 @@ The same run also times the raw NTT / MAC batch (64 ciphertexts x 2 polys
 x 24 limbs at N = 2^16: forward NTT, plaintext MAC over the 64
 ciphertexts, inverse NTT) and reports NTT HBM GB/s, one encrypted Mamba-2
 SSM layer step at the 130M shape, and EvalBootstrap at N = 2^16 (one pass
-and the two-pass refresh, 45 limbs).
+and the two-pass refresh, 45 limbs), and a 24-layer encrypted Mamba-2 decode
+(s/token, first and carried-state token).
 
 Per-kernel times come from HIP events recorded on the library's stream
 around every launch (fhe_profile_begin / fhe_profile_end) over a profiled
@@ -293,6 +294,39 @@ def run_bootstrap(steps: int = 3, warmup: int = 1):
     return res
 
 
+# 396.6 s per carried-state token (mean of 4) and 356.4 s for the first, the
+# reference's Mamba-2-130M encrypted decode on GB10 (results/dgx/2026-09-24/
+# owned-arithmetic/m2-full-candidate/native.json, `timing`).
+REF_TOKEN_S = 396.6
+
+
+def run_decode(tokens: int = 2):
+    """Encrypted Mamba-2 decode of a seeded random-init 24-layer payload at
+    the 130M shape (d_model 768, d_inner 1536, 24 heads x 64, state 128,
+    conv 4): N=2^16, 32768 slots, depth 44, 59-bit scale; the first token
+    from zero state, then carried-state tokens.  Errors against the
+    payload's polynomial circuit after decryption."""
+    import tempfile
+    from fhemamba_amd import mamba2_decode as D
+    from fhemamba_amd import mamba2_payload as M
+    with tempfile.TemporaryDirectory() as d:
+        M.synthetic_chain(d, n_layers=24, n_test_tokens=tokens, seed=13)
+        rep = D.run_payload(d, seed=14, log=lambda m: None)
+    carried = rep["carried_token_seconds"]
+    return {
+        "s_per_token_first": rep["first_token_seconds"],
+        "s_per_token_carried": carried,
+        "max_abs_err_vs_polynomial": rep["max_abs_error_vs_polynomial"],
+        "bootstraps_per_token": rep["bootstraps"] / tokens,
+        "rotations_per_token": rep["rotations"] / tokens,
+        "reference_gb10_s_per_token": REF_TOKEN_S,
+        "speedup_vs_reference": REF_TOKEN_S / carried if carried else None,
+        "workload": ("encrypted Mamba-2-130M-shaped decode, 24 layers (seeded random-init "
+                     "weights and calibrated polynomials, synthetic payload), N=2^16, "
+                     "depth 44; first token from zero state, then carried state"),
+    }
+
+
 def ntt_primes(log_n: int, bits: int, count: int):
     """Descending primes q = 1 mod 2N below 2^bits (deterministic)."""
     from fhemamba_amd.core import gen_moduli  # noqa: F401  (library must load)
@@ -384,6 +418,7 @@ def main() -> int:
     ap.add_argument("--skip-ntt", action="store_true")
     ap.add_argument("--skip-ssm", action="store_true")
     ap.add_argument("--skip-bootstrap", action="store_true")
+    ap.add_argument("--skip-decode", action="store_true")
     ap.add_argument("--copy-probe", action="store_true",
                     help="after the workloads, run one plain limb copy (k_copy_limbs) of "
                          f"{COPY_PROBE_BYTES} bytes read and the same written, untimed, as "
@@ -461,6 +496,9 @@ def main() -> int:
     if not args.skip_bootstrap:
         log("bootstrap workload")
         out["bootstrap"] = run_bootstrap()
+    if not args.skip_decode:
+        log("mamba-2 decode workload")
+        out["mamba2_decode"] = run_decode()
     if args.copy_probe:
         log("copy probe")
         copy_probe(F)

@@ -509,6 +509,34 @@ class CryptoContext:
     def EvalSquareInPlace(self, a: "Ciphertext") -> None:  # noqa: N802
         a._assign(self._mult_ct(a, a))
 
+    def EvalLinearWSum(self, cts: Sequence["Ciphertext"], weights) -> "Ciphertext":  # noqa: N802
+        """sum_i weights[i] * cts[i] as one degree-2 ciphertext at the
+        deepest input level with scale sf[t]^2 (so that its rescale lands
+        on the FLEXIBLEAUTO table): each input is rescaled if needed, has
+        limbs dropped to level t (free) and is multiplied by the integer
+        round(w_i sf[t]^2 / scale_i), so every product carries the same
+        scale and the sum needs no alignment products."""
+        items = [(c if c.deg < 2 else self._rescaled(c), float(w))
+                 for c, w in zip(cts, weights)]
+        if not items:
+            raise ValueError("EvalLinearWSum needs at least one ciphertext")
+        t = max(c.level for c, _ in items)
+        target = self._sf[t] * self._sf[t]
+        nq = self.L - t
+        acc = None
+        for c, w in items:
+            m = int(round(w * target / c.scale))
+            if m == 0:
+                continue
+            x = c.poly if c.level == t else self._ctx.drop_limbs(c.poly, nq)
+            term = self._ctx.mul_const(x, self._const_residues(m, nq))
+            acc = term if acc is None else self._ctx.add(acc, term, out=acc)
+        if acc is None:
+            c0 = items[0][0]
+            x = c0.poly if c0.level == t else self._ctx.drop_limbs(c0.poly, nq)
+            acc = self._ctx.mul_const(x, self._const_residues(0, nq))
+        return self._wrap(acc, t, 2, target, items[0][0].slots)
+
     def MultByInteger(self, a: "Ciphertext", value: int) -> "Ciphertext":  # noqa: N802
         """Multiply by a small integer without changing the scale
         (multIntScalar, native/fideslib_stage0/src/fideslib_refresh_correction.hpp:37)."""

@@ -100,6 +100,12 @@ def chebyshev_ps(cc, u, coeffs: Sequence[float], floor: float = CHEB_COEFF_FLOOR
     if degree < 1:
         return constant(coeffs[0] if len(coeffs) else 0.0)
     m = cheb_baby_size(degree)
+    # Backends with Rescale keep each basis polynomial rescaled once (it is
+    # multiplied many times); with EvalLinearWSum a leaf's sum of c_i T_i is
+    # one weighted sum at the deepest T_i level instead of products aligned
+    # pairwise.  Both leave the result's value unchanged.
+    settle = getattr(cc, "Rescale", None) or (lambda ct: ct)
+    wsum = getattr(cc, "EvalLinearWSum", None)
     cache = {1: u}
 
     def cheb(i: int):
@@ -107,21 +113,23 @@ def chebyshev_ps(cc, u, coeffs: Sequence[float], floor: float = CHEB_COEFF_FLOOR
             if i % 2 == 0:
                 h = cheb(i // 2)
                 sq = cc.EvalMult(h, h)
-                cache[i] = cc.EvalSub(cc.EvalAdd(sq, sq), 1.0)
+                cache[i] = settle(cc.EvalSub(cc.EvalAdd(sq, sq), 1.0))
             else:
                 pr = cc.EvalMult(cheb(i // 2 + 1), cheb(i // 2))
-                cache[i] = cc.EvalSub(cc.EvalAdd(pr, pr), u)
+                cache[i] = settle(cc.EvalSub(cc.EvalAdd(pr, pr), u))
         return cache[i]
 
     def evaluate(c: list[float]):
         n = len(c) - 1
         if n < m:
+            idx = [i for i in range(1, n + 1) if abs(c[i]) >= floor]
             acc = None
-            for i in range(1, n + 1):
-                if abs(c[i]) < floor:
-                    continue
-                term = cc.EvalMult(cheb(i), c[i])
-                acc = term if acc is None else cc.EvalAdd(acc, term)
+            if idx and wsum is not None:
+                acc = wsum([cheb(i) for i in idx], [c[i] for i in idx])
+            else:
+                for i in idx:
+                    term = cc.EvalMult(cheb(i), c[i])
+                    acc = term if acc is None else cc.EvalAdd(acc, term)
             if acc is None:
                 return constant(c[0])
             if abs(c[0]) >= floor:

@@ -1,0 +1,429 @@
+"""Encrypted Mamba-2 decode from a chain payload: a drop-in for the token
+and layer loops of native/fideslib_stage0/src/stage1_mamba2_decode_fideslib.cpp
+(run_layer :3634-4232, token loop :4287, layer loop :4388) over this
+package's CKKS interface on the GPU.
+
+Per layer (semantics of fhemamba_amd.mamba2_payload.layer_step, the payload's
+polynomial circuit), all ciphertexts of `slots` = N/2 slots:
+  * block norm: hidden^2 summed over every slot by rotate-adds (zero padding
+    makes the total land in every slot), v = total / d_model + eps,
+    inverse square root by the payload's Chebyshev guess + Newton steps;
+    normed = hidden * inv;
+  * in_proj by the replicated baby-step giant-step matvec (block_norm_w
+    folded into the weights); proj holds z | xBC | dt at slots
+    [0, d_inner) | [d_inner, d_inner + conv_dim) | the rest;
+  * conv: the FIFO keeps the last conv_kernel - 1 proj ciphertexts; taps
+    and bias are plaintext vectors on the xBC slots (the reference's "taps
+    multiply xBC slots of the raw proj ciphertexts", :3741-3760); SiLU by
+    the payload's Chebyshev series;
+  * gates: SiLU(z); dt = (Chebyshev sqrt-softplus)^2 on dt + dt_bias;
+    decay = exp(dt A) by Chebyshev and squarings, times the head mask;
+  * SSM in the reference's packing (:23-27): state group g holds heads
+    heads_per_ct g ... at slot n * group_block + h_local * head_dim + p;
+    x, dt and decay are expanded to it (a rotation, a mask, a rotate-sum
+    over n), B and C replicated (a one-level diagonal scatter of B[n] to
+    n * group_block, then a rotate-sum over the block); h' = decay h +
+    (dt x) B; readout h' C rotate-summed over n, masked and placed; + D x;
+  * gated norm of y * SiLU(z) with the payload's squared-guess Newton
+    inverse square root; out_proj (gated_norm_w folded); residual add.
+The final hidden goes through RMSNorm with final_norm_w.
+
+Refresh: before each phase every input ciphertext whose level plus the
+phase's level need would pass the ceiling is scaled into [-1, 1] by a
+public bound, bootstrapped (two passes) and scaled back, as the reference's
+maybe_bootstrap checkpoints do (:2127-2297).  Bounds are public calibration
+maxima (payload `carried_bounds`, else the defaults below), never values
+read from ciphertexts.
+"""
+from __future__ import annotations
+
+import math
+import time
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from .ckks_probes import cheb_ps_depth, chebyshev_ps
+from .mamba2_payload import ChainPayload, LayerPayload, PolySpec
+from .packed import PackedEvaluator, replicated_shape
+
+# Refresh bounds by checkpoint where a payload carries no calibration maxima
+# (with maxima: BOUND_MARGIN times the payload's value).
+DEFAULT_BOUNDS = {"residual": 64.0, "variance": 64.0, "inv": 64.0, "proj_raw": 64.0,
+                  "proj": 16.0, "conv": 16.0, "act": 16.0, "gate": 16.0, "dt": 16.0,
+                  "decay": 1.0, "state": 64.0, "y": 64.0, "gated": 64.0,
+                  "gated_variance": 64.0, "gated_inv": 64.0, "out_raw": 64.0,
+                  "output": 64.0, "out_residual": 64.0, "out_variance": 64.0,
+                  "out_inv": 64.0}
+BOUND_MARGIN = 2.0
+
+
+@dataclass
+class LayerCtState:
+    ssm: list | None = None            # state group ciphertexts (None: zero)
+    fifo: list = field(default_factory=list)   # previous proj ciphertexts, oldest first
+
+
+class EncryptedMamba2Decoder:
+    def __init__(self, cc, keys, chain: ChainPayload, *, bootstrap_passes: int = 2,
+                 refresh_ceiling: int = 39, bounds: dict | None = None, log=None):
+        first = chain.layers[0]
+        self.chain, self.cc = chain, cc
+        self.slots = cc.GetBatchSize()
+        self.log = log or (lambda m: None)
+        self.ev = PackedEvaluator(cc, keys, self.slots, bootstrap_passes=bootstrap_passes,
+                                  refresh_ceiling=refresh_ceiling, log=self.log)
+        self.bounds = [self._layer_bounds(lay, bounds) for lay in chain.layers]
+        self.d, self.di, self.ns = first.d_model, first.d_inner, first.state_size
+        self.nh, self.hd, self.kc = first.num_heads, first.head_dim, first.conv_kernel
+        self.cd = first.conv_dim
+        per = self.hd * self.ns
+        if self.slots % per or self.nh % (self.slots // per):
+            raise ValueError("slots must hold whole heads and the heads whole ciphertexts")
+        self.hp = self.slots // per                    # heads per state ciphertext
+        self.gb = self.hp * self.hd                    # group block
+        self.groups = self.nh // self.hp
+        if first.proj_dim > self.slots or self.d > self.slots:
+            raise ValueError("the projection does not fit one ciphertext")
+        self.stats = dict(tokens=0, layers=0)
+
+    # ------------------------------------------------------------ helpers
+    def _vec(self, entries: dict) -> np.ndarray:
+        v = np.zeros(self.slots)
+        for start, values in entries.items():
+            values = np.atleast_1d(np.asarray(values, dtype=np.float64))
+            v[start:start + len(values)] = values
+        return v
+
+    def _support(self, start: int, size: int) -> np.ndarray:
+        return self._vec({start: np.ones(size)})
+
+    @staticmethod
+    def _layer_bounds(lay: LayerPayload, override) -> dict:
+        b = dict(DEFAULT_BOUNDS)
+        for k, v in lay.bounds.items():
+            b[k] = max(BOUND_MARGIN * float(v), 1e-12)
+        b.update(override or {})
+        return b
+
+    def ready(self, ct, need: int, bound: float, support=None):
+        """Refresh ct (masked to `support`) if `need` more levels would pass
+        the ceiling."""
+        if self.ev._level(ct) + need > self.ev.refresh_ceiling:
+            return self.ev.refresh(ct, bound, support if support is not None else self.slots)
+        return ct
+
+    def full_sum(self, ct):
+        """Every slot gets the sum over all slots (rotate-adds)."""
+        step = 1
+        while step < self.slots:
+            ct = self.ev.add(ct, self.ev.rotate(ct, step))
+            step *= 2
+        return ct
+
+    def cheb(self, x, spec: PolySpec, support: np.ndarray, squarings_scale: int = 0):
+        """Chebyshev series of `spec` on the supported slots (domain scaled
+        by 2^squarings_scale for the range-reduced exp)."""
+        lo, hi = spec.lo * 2 ** squarings_scale, spec.hi * 2 ** squarings_scale
+        u = self.ev.plain(x, support * (2.0 / (hi - lo)), True)
+        u = self.ev.plain(u, support * (-(lo + hi) / (hi - lo)), False)
+        return chebyshev_ps(self.cc, u, [float(c) for c in spec.coeffs], 1e-14,
+                            lambda v: self.ev.scale(u, 0.0))
+
+    def cheb_need(self, spec: PolySpec) -> int:
+        return 1 + cheb_ps_depth(len(spec.coeffs) - 1) + 1
+
+    def inv_sqrt(self, v, spec: PolySpec, vbound: float, ibound: float):
+        """The payload's Newton inverse square root of v (v in every slot,
+        so refreshes need no mask)."""
+        v = self.ready(v, self.cheb_need(spec) + 2, vbound)
+        q = self.cheb(v, spec, np.ones(self.slots))
+        if spec.kind == "poly-newton":
+            y = self.ev.scale(q, 0.9)
+        elif spec.kind == "sq-poly-newton":
+            y = self.ev.scale(self.ev.mul(q, q), spec.damping)
+        else:
+            raise ValueError(f"inverse square root of kind {spec.kind}")
+        vh = self.ev.scale(v, -0.5)
+        for _ in range(spec.iterations):
+            y = self.ready(y, 3, ibound)
+            vh = self.ready(vh, 3, vbound)
+            t = self.ev.mul(vh, self.ev.mul(y, y))
+            y = self.ev.mul(y, self.cc.EvalAdd(t, 1.5))
+        return y
+
+    def rms_scale(self, x, width: int, eps: float, spec: PolySpec, xbound: float,
+                  vbound: float, ibound: float):
+        """inv_sqrt(mean(x^2) + eps) of the first `width` slots, in every slot
+        (a broadcast scalar: it commutes with a following matvec)."""
+        x = self.ready(x, 3, xbound, self._support(0, width))
+        tot = self.full_sum(self.ev.mul(x, x))
+        v = self.cc.EvalAdd(self.ev.scale(tot, 1.0 / width), float(eps))
+        return self.inv_sqrt(v, spec, vbound, ibound)
+
+    def times_scale(self, x, inv, bound: float, support, ibound: float):
+        x = self.ready(x, 1, bound, support)
+        inv = self.ready(inv, 1, ibound)
+        return self.ev.mul(x, inv)
+
+    def expand_compact(self, ct, start: int):
+        """Slots [start + g gb, start + (g+1) gb) of ct -> per group g, that
+        block at every n (slot n gb + j)."""
+        offs = [start + g * self.gb for g in range(self.groups)]
+        rots = self.ev.rotate_hoisted(ct, offs)
+        sup = self._support(0, self.gb)
+        out = []
+        for r in rots:
+            m = self.ev.plain(r, sup, True, key=("blk", self.gb))
+            out.append(self.ev.rotation_sum(m, self.ns, -self.gb))
+        return out
+
+    def spread_heads(self, ct, start: int):
+        """Per-head values at slots [start, start + nh) -> compact channel
+        layout (value of head h at h hd + p)."""
+        masks: dict = {}
+        for h in range(self.nh):
+            off = start + h - h * self.hd          # rot(x, off)[h hd] = x[start + h]
+            masks.setdefault(off, np.zeros(self.slots))[h * self.hd] = 1.0
+        lone = self.ev.transform(ct, masks)
+        return self.ev.rotation_sum(lone, self.hd, -1)
+
+    def replicate_states(self, ct, start: int):
+        """B[n] at slot start + n -> B[n] at every slot of block n (n gb + j)."""
+        masks: dict = {}
+        for n in range(self.ns):
+            off = start + n - n * self.gb
+            masks.setdefault(off, np.zeros(self.slots))[n * self.gb] = 1.0
+        lone = self.ev.transform(ct, masks)
+        return self.ev.rotation_sum(lone, self.gb, -1)
+
+    # ------------------------------------------------------------ layer
+    def layer(self, li: int, hidden, st: LayerCtState):
+        lay: LayerPayload = self.chain.layers[li]
+        ev, cc, B = self.ev, self.cc, self.bounds[li]
+        di, cd, ns, gb = self.di, self.cd, self.ns, self.gb
+        t = lay.t
+        # block norm: in_proj(hidden * inv) = in_proj(hidden) * inv, so the
+        # matvec runs on the shallow residual (block_norm_w folded in)
+        inv = self.rms_scale(hidden, self.d, lay.eps_block, lay.polys["rms_invsqrt"],
+                             B["residual"], B["variance"], B["inv"])
+        w_in = t("in_proj_w") * t("block_norm_w")[None, :]
+        hin = self.ready(hidden, 4, B["residual"], self._support(0, self.d))
+        psup = self._support(0, lay.proj_dim)
+        proj = self.times_scale(ev.linear(hin, w_in, ("in_proj", li)), inv, B["proj_raw"],
+                                psup, B["inv"])
+        # one refresh serves every consumer of proj (conv, gate, dt, FIFO)
+        need = max(2, self.cheb_need(lay.polys["gate_silu"]),
+                   self.cheb_need(lay.polys["dt_softplus"]) + 2)
+        proj = self.ready(proj, need, B["proj"], psup)
+        # conv over the FIFO of raw proj ciphertexts (taps on the xBC slots)
+        window = list(st.fifo) + [proj]
+        xs = self._support(di, cd)
+        pad = self.kc - len(window)
+        conv = None
+        for k, ct in enumerate(window):
+            ct = self.ready(ct, 2, B["proj"], psup)
+            term = ev.plain(ct, self._vec({di: t("conv_w")[:, pad + k]}), True)
+            conv = term if conv is None else ev.add(conv, term)
+        conv = ev.plain(conv, self._vec({di: t("conv_b")}), False)
+        conv = self.ready(conv, self.cheb_need(lay.polys["conv_silu"]), B["conv"], xs)
+        act = ev.plain(self.cheb(conv, lay.polys["conv_silu"], xs), xs, True,
+                       key=("xbc", di, cd))
+        # gates: SiLU(z), dt, decay
+        zs = self._support(0, di)
+        gate = ev.plain(self.cheb(proj, lay.polys["gate_silu"], zs), zs, True, key=("z", di))
+        d0 = di + cd
+        ds = self._support(d0, self.nh)
+        sp = lay.polys["dt_softplus"]
+        dtin = ev.plain(proj, self._vec({d0: t("dt_bias")}), False)
+        q = self.cheb(dtin, sp, ds)
+        dt = ev.plain(ev.mul(q, q), ds, True, key=("dt", d0))
+        dec = lay.polys["decay_exp"]
+        A = -np.exp(t("a_log"))
+        dt = self.ready(dt, self.cheb_need(dec) + dec.squarings + 2, B["dt"], ds)
+        e = self.cheb(ev.plain(dt, self._vec({d0: A}), True), dec, ds, dec.squarings)
+        for _ in range(dec.squarings):
+            e = self.ev.mul(e, e)
+        hm = dec.head_mask if dec.head_mask is not None else np.ones(self.nh)
+        decay = ev.plain(e, self._vec({d0: hm}), True)
+        # expansions into the state packing
+        # compact values refreshed with room for the expansions and the
+        # state update, so the expanded ciphertexts need no refresh
+        act = self.ready(act, 7, B["act"], xs)
+        x_groups = self.expand_compact(act, di)
+        b_rep = self.replicate_states(act, di + di)
+        c_rep = self.replicate_states(act, di + di + ns)
+        dt = self.ready(dt, 6, B["dt"], ds)
+        dt_groups = self.expand_compact(self.spread_heads(dt, d0), 0)
+        decay = self.ready(decay, 5, B["decay"], ds)
+        decay_groups = self.expand_compact(self.spread_heads(decay, d0), 0)
+        # state update and readout
+        new_ssm, reads = [], []
+        for g in range(self.groups):
+            xg = self.ready(x_groups[g], 4, B["act"])
+            dg = self.ready(dt_groups[g], 4, B["dt"])
+            br = self.ready(b_rep, 3, B["act"])
+            write = ev.mul(ev.mul(xg, dg), br)
+            if st.ssm is not None:
+                eg = self.ready(decay_groups[g], 2, B["decay"])
+                hg = self.ready(st.ssm[g], 2, B["state"])
+                h2 = ev.add(ev.mul(eg, hg), write)
+            else:
+                h2 = write
+            h2 = self.ready(h2, 3, B["state"])
+            new_ssm.append(h2)
+            cr = self.ready(c_rep, 3, B["act"])
+            reads.append(ev.mul(h2, cr))
+        k = gb
+        while k < self.slots:
+            ev._ensure_keys([k])
+            ev.stats["rotations"] += len(reads)
+            rot = self.cc.EvalRotateMany(reads, k) if hasattr(self.cc, "EvalRotateMany") \
+                else [self.cc.EvalRotate(r, k) for r in reads]
+            reads = [ev.add(a, b) for a, b in zip(reads, rot)]
+            k *= 2
+        y = None
+        for g, r in enumerate(reads):
+            m = ev.plain(r, self._support(0, gb), True, key=("blk", gb))
+            m = ev.rotate(m, -g * gb)
+            y = m if y is None else ev.add(y, m)
+        xc = ev.rotate(act, di)                                   # x at [0, di)
+        skip = ev.plain(xc, self._vec({0: np.repeat(t("d_skip"), self.hd)}), True)
+        y = ev.add(y, skip)
+        # gated norm, out_proj, residual
+        y = self.ready(y, 2, B["y"], zs)
+        gate = self.ready(gate, 2, B["gate"], zs)
+        gated = ev.mul(y, gate)
+        # gated norm: out_proj(gated * inv2) = out_proj(gated) * inv2
+        inv2 = self.rms_scale(gated, di, lay.eps_gated, lay.polys["gated_rms_invsqrt"],
+                              B["gated"], B["gated_variance"], B["gated_inv"])
+        w_out = t("out_proj_w") * t("gated_norm_w")[None, :]
+        gin = self.ready(gated, 4, B["gated"], zs)
+        dsup = self._support(0, self.d)
+        out = self.times_scale(ev.linear(gin, w_out, ("out_proj", li)), inv2, B["out_raw"],
+                               dsup, B["gated_inv"])
+        hidden = self.ready(hidden, 1, B["residual"], dsup)
+        new_hidden = ev.add(hidden, out)
+        fifo = (list(st.fifo) + [proj])[-(self.kc - 1):] if self.kc > 1 else []
+        self.stats["layers"] += 1
+        return new_hidden, LayerCtState(new_ssm, fifo)
+
+    # ------------------------------------------------------------ token
+    def initial_states(self) -> list:
+        return [LayerCtState() for _ in self.chain.layers]
+
+    def step(self, embedding, states: list):
+        """One token: encrypt the embedding (client side), run every layer,
+        final RMSNorm; returns (final ciphertext, new states)."""
+        h = self.ev.encrypt(np.asarray(embedding, dtype=np.float64))
+        new_states = []
+        for li, st in enumerate(states):
+            t0 = time.perf_counter()
+            h, ns_ = self.layer(li, h, st)
+            new_states.append(ns_)
+            self.log(f"layer {li}: {time.perf_counter() - t0:.3f}s level {h.GetLevel()} "
+                     f"bootstraps {self.ev.stats['bootstraps']}")
+        last = self.chain.layers[-1]
+        B = self.bounds[-1]
+        inv = self.rms_scale(h, self.d, self.chain.final_norm_eps, last.polys["rms_invsqrt"],
+                             B["out_residual"], B["out_variance"], B["out_inv"])
+        h = self.ready(h, 2, B["out_residual"], self._support(0, self.d))
+        final = self.ev.plain(h, self._vec({0: self.chain.final_norm_w}), True)
+        final = self.times_scale(final, inv, B["out_residual"] * float(
+            np.max(np.abs(self.chain.final_norm_w))), self._support(0, self.d), B["out_inv"])
+        self.stats["tokens"] += 1
+        return final, new_states
+
+    def decrypt(self, ct) -> np.ndarray:
+        return self.ev.decrypt(ct, self.d)
+
+
+def expected_rotation_count(lay: LayerPayload, slots: int) -> dict:
+    """Replicated shapes of the two projections (plaintext count per layer)."""
+    s_in = replicated_shape(lay.proj_dim, lay.d_model, slots)
+    s_out = replicated_shape(lay.d_model, lay.d_inner, slots)
+    return {"in_proj_masks": s_in.per_replica, "out_proj_masks": s_out.per_replica}
+
+
+# ----------------------------------------------------------------- command line
+def run_payload(payload_dir: str, *, tokens: int = 0, bootstrap_passes: int = 2, seed=None,
+                log=print) -> dict:
+    """Decode the payload's test embeddings in turn (carried state) and
+    compare the decrypted outputs with its polynomial-circuit and exact
+    references; returns the report."""
+    from .mamba2_payload import read_chain_payload
+    from .packed import build_context
+    chain = read_chain_payload(payload_dir)
+    n_tok = tokens or chain.n_test_tokens
+    slots = 32768
+    t0 = time.perf_counter()
+    cc, keys = build_context(slots, seed=seed)
+    dec = EncryptedMamba2Decoder(cc, keys, chain, bootstrap_passes=bootstrap_passes, log=log)
+    setup = time.perf_counter() - t0
+    states = dec.initial_states()
+    per_token, errs_poly, errs_exact = [], [], []
+    for k in range(n_tok):
+        cc.device.sync()
+        t = time.perf_counter()
+        ct, states = dec.step(chain.input_embeddings[k], states)
+        cc.device.sync()
+        per_token.append(time.perf_counter() - t)
+        got = dec.decrypt(ct)
+        if chain.expected_poly_final is not None:
+            errs_poly.append(float(np.max(np.abs(got - chain.expected_poly_final[k]))))
+        errs_exact.append(float(np.max(np.abs(got - chain.expected_final[k]))))
+        log(f"token {k}: {per_token[-1]:.2f}s error vs polynomial "
+            f"{errs_poly[-1] if errs_poly else float('nan'):.2e} vs exact {errs_exact[-1]:.2e}")
+    s = dec.ev.stats
+    return {
+        "schema": "fhemamba-m2-decode-result-v1",
+        "encrypted": True,
+        "layers": chain.n_layers,
+        "tokens": n_tok,
+        "ring_dimension": cc.GetRingDimension(),
+        "slots": slots,
+        "setup_seconds": setup,
+        "seconds_per_token": per_token,
+        "first_token_seconds": per_token[0],
+        "carried_token_seconds": (sum(per_token[1:]) / (n_tok - 1)) if n_tok > 1 else None,
+        "max_abs_error_vs_polynomial": max(errs_poly) if errs_poly else None,
+        "max_abs_error_vs_exact": max(errs_exact),
+        "per_token_errors_vs_polynomial": errs_poly,
+        "bootstraps": s["bootstraps"],
+        "logical_refreshes": s["logical_refreshes"],
+        "bootstrap_seconds": s["bootstrap_seconds"],
+        "rotations": s["rotations"],
+        "ct_ct_mul": s["ct_ct"],
+        "ct_pt_mul": s["ct_pt"],
+        "rotation_keys_generated": s["rotation_keys"],
+        "keygen_seconds": s["keygen_seconds"],
+    }
+
+
+def main(argv=None) -> int:
+    import argparse
+    import json
+    import sys
+    ap = argparse.ArgumentParser(description="encrypted Mamba-2 decode of a chain payload")
+    ap.add_argument("payload")
+    ap.add_argument("result")
+    ap.add_argument("--tokens", type=int, default=0)
+    ap.add_argument("--bootstrap-passes", type=int, default=2, choices=(1, 2))
+    ap.add_argument("--tolerance", type=float, default=1e-3,
+                    help="pass threshold on the error against the polynomial circuit")
+    args = ap.parse_args(sys.argv[1:] if argv is None else argv)
+    try:
+        report = run_payload(args.payload, tokens=args.tokens,
+                             bootstrap_passes=args.bootstrap_passes)
+    except Exception as exc:  # noqa: BLE001 - reported as exit code 2
+        print(exc, file=sys.stderr)
+        return 2
+    err = report["max_abs_error_vs_polynomial"]
+    report["passed"] = bool(err is not None and err <= args.tolerance)
+    with open(args.result, "w") as f:
+        json.dump(report, f)
+    return 0 if report["passed"] else 1
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

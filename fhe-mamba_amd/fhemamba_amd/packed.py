@@ -421,7 +421,15 @@ class PackedEvaluator:
             self.stats["ct_pt"] += 1
             if ct.GetNoiseScaleDeg() >= 2:
                 ct = self.cc.Rescale(ct)
-            ck = None if key is None else (key, ct.GetLevel())
+            big = float(np.max(np.abs(v))) if len(v) else 0.0
+            k = 1
+            if big > 4.0:
+                # a power-of-two integer part (exact, no level) keeps the
+                # encoded values inside the 62-bit coefficient range
+                k = 1 << math.ceil(math.log2(big / 2.0))
+                ct = self.cc.MultByInteger(ct, k)
+                v = v / k
+            ck = None if key is None else (key, ct.GetLevel(), k)
             pt = self._pt_cache.get(ck) if ck else None
             if pt is None:
                 pt = self.cc.MakeCKKSPackedPlaintext(v, 1, ct.GetLevel(), slots=self.slots)
@@ -441,9 +449,15 @@ class PackedEvaluator:
         return out
 
     # ------------------------------------------------------------- refresh
-    def refresh(self, ct, bound: float, size: int):
+    def refresh(self, ct, bound: float, support):
+        """Mask ct to its support (a width or a 0/1 slot vector; padding is
+        never bootstrapped), scale into [-1, 1] by 1 / bound, bootstrap and
+        scale back."""
         t0 = time.perf_counter()
-        x = self.mask(ct, size)                   # never bootstrap padding
+        if isinstance(support, (int, np.integer)):
+            x = self.mask(ct, int(support)) if support < self.slots else ct
+        else:
+            x = self.plain(ct, support, True)
         x = self.scale(x, 1.0 / bound)
         self.cc.RescaleInPlace(x)
         out = self.cc.EvalBootstrap(x, self.bootstrap_passes, REFRESH_SCALE_BITS)
@@ -653,6 +667,10 @@ class _CountingContext:
     def EvalSub(self, a, b):  # noqa: N802
         self._stats["adds"] += 1
         return self._cc.EvalSub(a, b)
+
+    def __getattr__(self, name):
+        # Rescale, EvalLinearWSum and the rest go straight through
+        return getattr(self._cc, name)
 
 
 # ----------------------------------------------------------------- client head

@@ -135,6 +135,9 @@ class SlotContext:
     def GetRingDimension(self):  # noqa: N802
         return self.n
 
+    def GetBatchSize(self):  # noqa: N802
+        return self.slots
+
     def _plain(self, v):
         return SlotCt(np.asarray(v, dtype=complex))
 
@@ -192,6 +195,12 @@ class SlotContext:
     def EvalSquare(self, a):  # noqa: N802
         return self.EvalMult(a, a)
 
+    def EvalLinearWSum(self, cts, weights):  # noqa: N802
+        cts = [self._rescaled(c) for c in cts]
+        lv = max(c.level for c in cts)
+        self._check(lv + 1)
+        return SlotCt(sum(float(w) * c.z for c, w in zip(cts, weights)), lv, 2)
+
     def MultByInteger(self, a, v):  # noqa: N802
         return SlotCt(a.z * int(v), a.level, a.deg)
 
@@ -246,6 +255,8 @@ class SlotContext:
     def EvalBootstrap(self, ct, passes=1, precision=0):  # noqa: N802
         ct = self._rescaled(ct)
         assert ct.level <= self.L - 2, "bootstrap input too deep"
+        # the refresh bound must bring every slot into [-1, 1]
+        assert np.max(np.abs(ct.z)) <= 1.0 + 1e-9, f"bootstrap input {np.max(np.abs(ct.z))}"
         self.bootstraps += passes
         return SlotCt(ct.z, self.boot_depth, 1)
 

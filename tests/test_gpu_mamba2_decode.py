@@ -1,0 +1,36 @@
+"""Encrypted Mamba-2 decode on the GPU at the 130M shape (two layers of a
+seeded random-init payload, N = 2^16, 32768 slots, depth 44): three tokens
+with carried state (SSM state and conv FIFO ciphertexts), decrypted and
+compared with the payload's polynomial-circuit reference.  Tolerance 1e-4
+on the final normed hidden (values ~1); measured ~4e-6."""
+import json
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+F = pytest.importorskip("fhemamba_amd")
+from fhemamba_amd import mamba2_decode as D  # noqa: E402
+from fhemamba_amd import mamba2_payload as M  # noqa: E402
+
+TOL = 1e-4
+
+
+def test_two_layer_decode_with_carried_state(tmp_path):
+    M.synthetic_chain(str(tmp_path), n_layers=2, n_test_tokens=3, seed=3)
+    report = D.run_payload(str(tmp_path), seed=4)
+    print(f"decode: {report['seconds_per_token']} s/token, errors "
+          f"{report['per_token_errors_vs_polynomial']}", flush=True)
+    assert report["max_abs_error_vs_polynomial"] < TOL
+    assert report["logical_refreshes"] > 0 and report["bootstraps"] == 2 * report["logical_refreshes"]
+
+
+def test_command_line(tmp_path):
+    M.synthetic_chain(str(tmp_path / "p"), n_layers=1, n_test_tokens=1, seed=5)
+    res = tmp_path / "r.json"
+    assert D.main([str(tmp_path / "p"), str(res), "--tolerance", str(TOL)]) == 0
+    rep = json.loads(res.read_text())
+    assert rep["passed"] is True and rep["schema"] == "fhemamba-m2-decode-result-v1"
+    assert rep["layers"] == 1 and rep["ring_dimension"] == 65536
+    assert D.main([str(tmp_path / "missing"), str(res)]) == 2
