@@ -26,9 +26,28 @@ FHE_HD uint64_t shoup_lazy(uint64_t a, uint64_t w, uint64_t wp, uint64_t q) {
   return a * w - mulhi64(a, wp) * q;
 }
 
+// Shoup product with an approximate quotient: the low partial product
+// a_lo * wp_lo and the carries of the two middle products are dropped, so
+// the quotient is low by 0, 1 or 2 and the result a*w mod q plus 0..3 q lies
+// in [0, 4q) for any a < 2^64 (three 32x32 multiplies for the quotient
+// instead of four and the carry chain).  Needs 4q < 2^64.
+FHE_HD uint64_t shoup_lazy4(uint64_t a, uint64_t w, uint64_t wp, uint64_t q) {
+  const uint32_t a0 = (uint32_t)a, a1 = (uint32_t)(a >> 32);
+  const uint32_t p0 = (uint32_t)wp, p1 = (uint32_t)(wp >> 32);
+  const uint64_t qt = (uint64_t)a1 * p1 + (((uint64_t)a0 * p1) >> 32) +
+                      (((uint64_t)a1 * p0) >> 32);
+  return a * w - qt * q;
+}
+
 FHE_HD uint64_t reduce_2q(uint64_t x, uint64_t q) { return x >= q ? x - q : x; }
 
 FHE_HD uint64_t reduce_4q(uint64_t x, uint64_t q) {
+  x = x >= 2 * q ? x - 2 * q : x;
+  return x >= q ? x - q : x;
+}
+
+FHE_HD uint64_t reduce_8q(uint64_t x, uint64_t q) {
+  x = x >= 4 * q ? x - 4 * q : x;
   x = x >= 2 * q ? x - 2 * q : x;
   return x >= q ? x - q : x;
 }

@@ -19,9 +19,10 @@
 // which keeps both the stride-1 and the stride-16 access patterns free of
 // bank conflicts.  Workgroups are 256 threads (4096 elements, ~35 KB LDS).
 //
-// Arithmetic: Harvey lazy butterflies.  Forward values stay in [0, 4q),
-// inverse values in [0, 2q); the final launch reduces to [0, q).  This
-// needs 4q < 2^64, guaranteed by q < 2^61.
+// Arithmetic: Harvey lazy butterflies with an approximate-quotient Shoup
+// product (shoup_lazy4, result in [0, 4q)).  Forward values stay in [0, 8q),
+// inverse values in [0, 4q); the final launch reduces to [0, q).  This
+// needs 8q < 2^64, guaranteed by q < 2^61.
 //
 // Grid: (tiles per limb, poly, limb).  The limb index is the slowest grid
 // dimension so consecutive workgroups share one modulus and its twiddle
@@ -78,7 +79,10 @@ __device__ __forceinline__ void ntt_body(uint64_t* __restrict__ data, size_t pol
   // Workgroup-uniform: a slot without work exits before any barrier.
   uint32_t pos, midx;
   if (!map.resolve(blockIdx.y, blockIdx.z, pos, midx)) return;
-  const uint64_t q = mc[midx].q, q2 = 2 * q;
+  // Lazy ranges (approximate Shoup products land in [0, 4q)): forward
+  // stage outputs stay in [0, 8q), inverse ones in [0, 4q); 8q < 2^64 as
+  // every prime is below 2^61.
+  const uint64_t q = mc[midx].q, q4 = 4 * q;
   const uint64_t* __restrict__ tw = tw_all + (size_t)midx * n * 2;
   uint64_t* __restrict__ base = data + (size_t)blockIdx.y * poly_stride + (size_t)pos * n;
 
@@ -176,10 +180,10 @@ __device__ __forceinline__ void ntt_body(uint64_t* __restrict__ data, size_t pol
           const uint32_t ti = (twbase << (S - 1 - beta)) | (u >> (beta + 1));
           const uint64_t wv = tw[2 * ti], ws = tw[2 * ti + 1];
           uint64_t X = x[v];
-          X = X >= q2 ? X - q2 : X;
-          const uint64_t T = shoup_lazy(x[v + d], wv, ws, q);
+          X = X >= q4 ? X - q4 : X;
+          const uint64_t T = shoup_lazy4(x[v + d], wv, ws, q);
           x[v] = X + T;
-          x[v + d] = X + q2 - T;
+          x[v + d] = X + q4 - T;
         }
       }
     } else {
@@ -194,8 +198,8 @@ __device__ __forceinline__ void ntt_body(uint64_t* __restrict__ data, size_t pol
           const uint64_t wv = tw[2 * ti], ws = tw[2 * ti + 1];
           const uint64_t X = x[v], Y = x[v + d];
           uint64_t Sx = X + Y;
-          Sx = Sx >= q2 ? Sx - q2 : Sx;
-          x[v + d] = shoup_lazy(X + q2 - Y, wv, ws, q);
+          Sx = Sx >= q4 ? Sx - q4 : Sx;
+          x[v + d] = shoup_lazy4(X + q4 - Y, wv, ws, q);
           x[v] = Sx;
         }
       }
@@ -205,11 +209,11 @@ __device__ __forceinline__ void ntt_body(uint64_t* __restrict__ data, size_t pol
       if (last) {
         if (!INV) {
 #pragma unroll
-          for (int v = 0; v < R; ++v) x[v] = reduce_4q(x[v], q);
+          for (int v = 0; v < R; ++v) x[v] = reduce_8q(x[v], q);
         } else {
           const uint64_t ni = mc[midx].ninv, nis = mc[midx].ninv_sh;
 #pragma unroll
-          for (int v = 0; v < R; ++v) x[v] = reduce_2q(shoup_lazy(x[v], ni, nis, q), q);
+          for (int v = 0; v < R; ++v) x[v] = reduce_4q(shoup_lazy4(x[v], ni, nis, q), q);
         }
       }
       if (contiguous) {
