@@ -735,20 +735,26 @@ class CryptoContext:
         return self._bootstrapper().depth()
 
     def EvalBootstrap(self, ct: "Ciphertext", numIterations: int = 1,  # noqa: N802,N803
-                      precision: int = 0) -> "Ciphertext":
+                      precision: int = 0, *, scale: float = 1.0) -> "Ciphertext":
         """Refresh `ct` to level GetBootstrapDepth() (slot values kept to
         bootstrapping precision).  numIterations = 2 runs a second pass on
         the scaled residual of the first (precision = log2 of that scale;
-        0 picks 12)."""
+        0 picks 12).  `scale` (an extension of the OpenFHE call) admits
+        slots in [-scale, scale]: the division and the multiplication back
+        ride on the bootstrap's own scale-down and SlotToCoeff constants,
+        so they cost no level."""
         boot = self._bootstrapper()
-        out = boot.bootstrap(ct)
+        scale = float(scale)
+        if not scale > 0:
+            raise ValueError("bootstrap scale must be positive")
+        out = boot.bootstrap(ct, pre=1.0 / scale, post=scale)
         if int(numIterations) <= 1:
             return out
         if int(numIterations) != 2:
             raise ValueError("numIterations must be 1 or 2")
         bits = int(precision) or 12
         residual = self.EvalSub(ct, out)
-        fix = boot.bootstrap(residual, pre=2.0 ** bits, post=2.0 ** -bits)
+        fix = boot.bootstrap(residual, pre=2.0 ** bits / scale, post=scale * 2.0 ** -bits)
         return self.EvalAdd(out, fix)
 
 

@@ -66,7 +66,7 @@ class LayerCtState:
 
 class EncryptedMamba2Decoder:
     def __init__(self, cc, keys, chain: ChainPayload, *, bootstrap_passes: int = 2,
-                 refresh_ceiling: int = 39, bounds: dict | None = None, log=None):
+                 refresh_ceiling: int | None = None, bounds: dict | None = None, log=None):
         first = chain.layers[0]
         self.chain, self.cc = chain, cc
         self.slots = cc.GetBatchSize()

@@ -10,9 +10,10 @@ interface on the GPU.
   default mode (replicated linear, radix-8 monotone routing): every value
   occupies the leading `size` slots of one ciphertext with zero padding.
 * Refresh: before a node runs, a parent whose level plus the node's level
-  need would pass the ceiling (39 of 44) is masked to its width, scaled by
-  1 / bound, bootstrapped (two passes: the second refreshes the residual
-  times 4096) and scaled back (:235-282).
+  need would pass the ceiling is masked to its width, scaled by 1 / bound,
+  bootstrapped (two passes: the second refreshes the residual times 4096)
+  and scaled back (:235-282); the scalings ride on the bootstrap's own
+  constants, and the ceiling is L - 3 (42 of 44; the reference's is 39).
 * Command line `python -m fhemamba_amd.packed PROGRAM RESULT POLY_TOL
   EXACT_TOL [options]` with the reference's argv and the
   `fhemamba-packed-result-v1` report that src/fhemamba/benchmarks/
@@ -332,14 +333,18 @@ class PackedEvaluator:
     """Evaluates a PackedProgram on a CryptoContext of this package."""
 
     def __init__(self, cc, keys, slots: int, *, bootstrap_passes: int = 2,
-                 refresh_ceiling: int = 39, replicated_linear: bool = True,
+                 refresh_ceiling: int | None = None, replicated_linear: bool = True,
                  trace_levels: bool = False, level_budget=(4, 4), client=None,
                  log=None):
         if bootstrap_passes not in (1, 2):
             raise ValueError("bootstrap passes must be 1 or 2")
         self.cc, self.keys, self.slots = cc, keys, int(slots)
         self.bootstrap_passes = bootstrap_passes
-        self.refresh_ceiling = refresh_ceiling
+        # deepest level a value may reach and still be masked (one level)
+        # and bootstrapped (input at most L - 2): L - 3, 42 for the
+        # reference's depth-44 chain (its executor stops at 39, :1132)
+        self.refresh_ceiling = refresh_ceiling if refresh_ceiling is not None else \
+            len(cc.GetModuli()[0]) - 3
         self.replicated_linear = replicated_linear
         self.trace_levels = trace_levels
         self.client = client
@@ -458,12 +463,11 @@ class PackedEvaluator:
             x = self.mask(ct, int(support)) if support < self.slots else ct
         else:
             x = self.plain(ct, support, True)
-        x = self.scale(x, 1.0 / bound)
-        self.cc.RescaleInPlace(x)
-        out = self.cc.EvalBootstrap(x, self.bootstrap_passes, REFRESH_SCALE_BITS)
+        # 1 / bound and bound ride on the bootstrap's own constants (no level)
+        out = self.cc.EvalBootstrap(x, self.bootstrap_passes, REFRESH_SCALE_BITS,
+                                    scale=float(bound))
         self.stats["bootstraps"] += self.bootstrap_passes
         self.stats["logical_refreshes"] += 1
-        out = self.scale(out, bound)
         self.stats["bootstrap_seconds"] += time.perf_counter() - t0
         return out
 

@@ -138,6 +138,9 @@ class SlotContext:
     def GetBatchSize(self):  # noqa: N802
         return self.slots
 
+    def GetModuli(self):  # noqa: N802
+        return [0] * self.L, []
+
     def _plain(self, v):
         return SlotCt(np.asarray(v, dtype=complex))
 
@@ -252,11 +255,12 @@ class SlotContext:
                 return []
         return _B()
 
-    def EvalBootstrap(self, ct, passes=1, precision=0):  # noqa: N802
+    def EvalBootstrap(self, ct, passes=1, precision=0, *, scale=1.0):  # noqa: N802
         ct = self._rescaled(ct)
         assert ct.level <= self.L - 2, "bootstrap input too deep"
         # the refresh bound must bring every slot into [-1, 1]
-        assert np.max(np.abs(ct.z)) <= 1.0 + 1e-9, f"bootstrap input {np.max(np.abs(ct.z))}"
+        top = np.max(np.abs(ct.z)) / scale
+        assert top <= 1.0 + 1e-9, f"bootstrap input {top}"
         self.bootstraps += passes
         return SlotCt(ct.z, self.boot_depth, 1)
 

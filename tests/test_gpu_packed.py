@@ -76,7 +76,7 @@ def test_deep_chain_refreshes():
     b = ProgramBuilder(64, bound=4.0)
     v = b.input(rng.uniform(0.5, 1.5, 8))
     w = b.input(np.ones(8))
-    for _ in range(40):                     # v <- (v * w) * 1: two levels, same value,
+    for _ in range(60):                     # v <- (v * w) * 1: two levels, same value,
         v = b.mulp(b.mul(v, w), np.ones(8))  # errors add (no amplification)
     b.output(v)
     ev, errs = evaluate(b)

@@ -204,12 +204,12 @@ def test_large_monotone_gather_uses_routing_stages():
 
 
 def test_deep_chain_is_refreshed():
-    """Eighty levels of products pass the ceiling several times."""
+    """120 levels of products pass the ceiling several times."""
     rng = np.random.default_rng(8)
     b = ProgramBuilder(64, bound=4.0)
     v = b.input(rng.uniform(0.5, 1.5, 8))
     w = b.input(np.ones(8))
-    for _ in range(40):                     # v <- (v * w) * 1: two levels, same value,
+    for _ in range(60):                     # v <- (v * w) * 1: two levels, same value,
         v = b.mulp(b.mul(v, w), np.ones(8))  # errors add (no amplification)
     b.output(v)
     program, ev, values = run_slots(b)
