@@ -54,6 +54,10 @@ void* Pool::get(size_t bytes) {
   void* p = nullptr;
   hipError_t e = hipMalloc(&p, bytes);
   if (e != hipSuccess) {
+    // A failed hipMalloc also sets the thread's last error; clear it so the
+    // next launch check does not report an allocation that the retry below
+    // satisfies.
+    (void)hipGetLastError();
     trim();
     hip_check(hipMalloc(&p, bytes), "hipMalloc");
   }

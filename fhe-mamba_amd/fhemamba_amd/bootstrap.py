@@ -32,6 +32,7 @@ from dataclasses import dataclass, field
 import numpy as np
 
 from .ckks_probes import cheb_ps_depth, chebyshev_ps
+from .ptcache import PlaintextCache
 
 Diag = dict  # rotation offset -> complex diagonal vector
 
@@ -271,7 +272,8 @@ class CKKSBootstrapper:
     transforms then act on the n slots as they do at full packing, and 1/R
     joins the CoeffToSlot constant."""
 
-    def __init__(self, cc, config: BootstrapConfig | None = None, slots: int = 0):
+    def __init__(self, cc, config: BootstrapConfig | None = None, slots: int = 0,
+                 pt_cache_bytes: int = 16 << 30):
         self.cc = cc
         self.cfg = config or BootstrapConfig.for_ring(cc.GetRingDimension())
         self.N = cc.GetRingDimension()
@@ -284,7 +286,7 @@ class CKKSBootstrapper:
         self.s2c = [plan_group(D, self.n) for D in
                     fft_groups(self.n, self.cfg.level_budget[1], inverse=False)]
         self._coeffs = self.cfg.sine.coeffs
-        self._pts: dict = {}
+        self._pts = PlaintextCache(self.N, pt_cache_bytes)
 
     def trace_rotations(self) -> list[int]:
         """Rotations n, 2n, ..., N/4 of the subring trace (empty at full packing)."""
@@ -308,23 +310,43 @@ class CKKSBootstrapper:
     # --------------------------------------------------------------- helpers
     def _group_pts(self, which: str, idx: int, plan: GroupPlan, level: int, factor: float):
         key = (which, idx, level, factor)
-        if key not in self._pts:
-            self._pts[key] = [None if d is None else
-                              self.cc.MakeCKKSPackedPlaintext(d * factor, 1, level,
-                                                              slots=self.n)
-                              for d in plan.prerotated()]
-        return self._pts[key]
+        pts = self._pts.get(key)
+        if pts is None:
+            pts = [None if d is None else
+                   self.cc.MakeCKKSPackedPlaintext(d * factor, 1, level, slots=self.n)
+                   for d in plan.prerotated()]
+            self._pts.put(key, pts)
+        return pts
 
-    def _transform(self, ct, plans: list, which: str, total: float):
-        """Apply the groups in order; the constant `total` is spread evenly
-        over them (each diagonal set scaled by total^(1/groups))."""
-        factor = abs(total) ** (1.0 / len(plans))
-        sign = -1.0 if total < 0 else 1.0
+    @staticmethod
+    def group_factors(total: float, groups: int, power_last: bool = False) -> list[float]:
+        """Per-group constants whose product is `total`: spread evenly, or
+        (power_last) the mantissa m of |total| = m 2^e spread as
+        (m 2^(groups-1))^(1/groups) and the rest of the power of two on the
+        last group, so that totals sharing a mantissa share the diagonals
+        of every group but the last."""
+        mag = abs(total)
+        if mag == 0.0:
+            raise ValueError("transform constant must be non-zero")
+        if power_last:
+            fr, ex = math.frexp(mag)                          # mag = fr 2^ex, fr in [1/2, 1)
+            base = (2.0 * fr * 2.0 ** (groups - 1)) ** (1.0 / groups)
+            out = [base] * groups
+            out[-1] = base * 2.0 ** (ex - groups)
+        else:
+            out = [mag ** (1.0 / groups)] * groups
+        if total < 0:
+            out[0] = -out[0]
+        return out
+
+    def _transform(self, ct, plans: list, which: str, total: float, power_last: bool = False):
+        """Apply the groups in order, their diagonals scaled by
+        group_factors(total)."""
+        factors = self.group_factors(total, len(plans), power_last)
         for idx, plan in enumerate(plans):
             if ct.GetNoiseScaleDeg() >= 2:
                 self.cc.RescaleInPlace(ct)
-            f = factor * (sign if idx == 0 else 1.0)
-            pts = self._group_pts(which, idx, plan, ct.GetLevel(), f)
+            pts = self._group_pts(which, idx, plan, ct.GetLevel(), factors[idx])
             # offsets mod n: rotations act on the n slots (5^-h and 5^(n-h)
             # differ as automorphisms once n < N/2)
             self.cc.LinearTransformInPlace(ct, plan.rows, plan.bstep, pts, plan.stride,
@@ -361,11 +383,15 @@ class CKKSBootstrapper:
         if x.GetLevel() > L - 2:
             raise ValueError(f"EvalBootstrap needs the input at level <= {L - 2}")
         x.SetLevel(L - 2)
-        c = self.correction_bits(cc.GetScalingFactorReal(L - 1), q0,
-                                 cc.GetScalingFactorReal(0))
-        x = cc.EvalMult(x, pre * 2.0 ** -c)
+        in_scale = cc.GetScalingFactorReal(L - 1)
+        c = self.correction_bits(in_scale, q0, cc.GetScalingFactorReal(0))
+        # The product by sf[L-2] / scale(x) makes the rescaled scale
+        # sf[L-2]^2 / q1 = sf[L-1] whatever level x came from, so the
+        # constants below (and their cached diagonals) depend on pre and
+        # post alone.
+        x = cc.EvalMult(x, pre * 2.0 ** -c * cc.GetScalingFactorReal(L - 2) / x.GetScalingFactor())
         cc.RescaleInPlace(x)                                  # one limb left
-        in_scale = x.GetScalingFactor()
+        x.SetScalingFactor(in_scale)
         raised = cc.ModRaise(x)                               # decrypts to t = P + q0 I
         for r in self.trace_rotations():                      # sparse: R (P + q0 I')
             raised = cc.EvalAdd(raised, cc.EvalRotate(raised, r))
@@ -388,4 +414,4 @@ class CKKSBootstrapper:
         re_m = self._eval_mod(re, gain)                       # gain sin(2 pi u)
         im_m = self._eval_mod(im, gain)                       #   ~ gain 2 pi P / q0
         w = cc.EvalAdd(re_m, cc.MultByMonomial(im_m, N // 2))
-        return self._transform(w, self.s2c, "s2c", back / gain)
+        return self._transform(w, self.s2c, "s2c", back / gain, power_last=True)

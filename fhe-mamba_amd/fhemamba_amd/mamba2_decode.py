@@ -178,14 +178,14 @@ class EncryptedMamba2Decoder:
             out.append(self.ev.rotation_sum(m, self.ns, -self.gb))
         return out
 
-    def spread_heads(self, ct, start: int):
+    def spread_heads(self, ct, start: int, gain: float = 1.0):
         """Per-head values at slots [start, start + nh) -> compact channel
-        layout (value of head h at h hd + p)."""
+        layout (gain times the value of head h at h hd + p)."""
         masks: dict = {}
         for h in range(self.nh):
             off = start + h - h * self.hd          # rot(x, off)[h hd] = x[start + h]
-            masks.setdefault(off, np.zeros(self.slots))[h * self.hd] = 1.0
-        lone = self.ev.transform(ct, masks)
+            masks.setdefault(off, np.zeros(self.slots))[h * self.hd] = gain
+        lone = self.ev.transform(ct, masks, key=("spread", start, gain))
         return self.ev.rotation_sum(lone, self.hd, -1)
 
     def replicate_states(self, ct, start: int):
@@ -194,7 +194,7 @@ class EncryptedMamba2Decoder:
         for n in range(self.ns):
             off = start + n - n * self.gb
             masks.setdefault(off, np.zeros(self.slots))[n * self.gb] = 1.0
-        lone = self.ev.transform(ct, masks)
+        lone = self.ev.transform(ct, masks, key=("replicate", start))
         return self.ev.rotation_sum(lone, self.gb, -1)
 
     # ------------------------------------------------------------ layer
@@ -240,8 +240,19 @@ class EncryptedMamba2Decoder:
         dt = ev.plain(ev.mul(q, q), ds, True, key=("dt", d0))
         dec = lay.polys["decay_exp"]
         A = -np.exp(t("a_log"))
-        dt = self.ready(dt, self.cheb_need(dec) + dec.squarings + 2, B["dt"], ds)
-        e = self.cheb(ev.plain(dt, self._vec({d0: A}), True), dec, ds, dec.squarings)
+        # act (xBC slots) and dt (dt slots) occupy disjoint slots of the proj
+        # layout: when either needs a refresh both go through one bootstrap,
+        # dt first scaled by a power of two (exact, no level) into act's
+        # range; every consumer below masks, and dt's masks carry 1 / f
+        need_act = 7
+        need_dt = self.cheb_need(dec) + dec.squarings + 6
+        f = 1
+        if max(ev._level(act) + need_act, ev._level(dt) + need_dt) > ev.refresh_ceiling:
+            f = 1 << max(0, math.ceil(math.log2(B["act"] / B["dt"])))
+            comb = ev.add(act, cc.MultByInteger(dt, f) if f > 1 else dt)
+            comb = ev.refresh(comb, max(B["act"], B["dt"] * f), xs + ds)
+            act = dt = comb
+        e = self.cheb(ev.plain(dt, self._vec({d0: A / f}), True), dec, ds, dec.squarings)
         for _ in range(dec.squarings):
             e = self.ev.mul(e, e)
         hm = dec.head_mask if dec.head_mask is not None else np.ones(self.nh)
@@ -249,12 +260,15 @@ class EncryptedMamba2Decoder:
         # expansions into the state packing
         # compact values refreshed with room for the expansions and the
         # state update, so the expanded ciphertexts need no refresh
-        act = self.ready(act, 7, B["act"], xs)
+        act = self.ready(act, need_act, B["act"], xs)
         x_groups = self.expand_compact(act, di)
         b_rep = self.replicate_states(act, di + di)
         c_rep = self.replicate_states(act, di + di + ns)
-        dt = self.ready(dt, 6, B["dt"], ds)
-        dt_groups = self.expand_compact(self.spread_heads(dt, d0), 0)
+        if f > 1:
+            dt_c = self.spread_heads(dt, d0, 1.0 / f)
+        else:
+            dt_c = self.spread_heads(self.ready(dt, 6, B["dt"], ds), d0)
+        dt_groups = self.expand_compact(dt_c, 0)
         decay = self.ready(decay, 5, B["decay"], ds)
         decay_groups = self.expand_compact(self.spread_heads(decay, d0), 0)
         # state update and readout

@@ -34,6 +34,8 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
+from .ptcache import PlaintextCache
+
 PACKED_MAX_NODES = 1_000_000
 REFRESH_SCALE_BITS = 12          # the reference's 4096 residual scale
 CHEB_COEFF_FLOOR = 1e-14         # packed_fideslib.cpp chebyshev(): |c_i| < 1e-14 skipped
@@ -335,7 +337,7 @@ class PackedEvaluator:
     def __init__(self, cc, keys, slots: int, *, bootstrap_passes: int = 2,
                  refresh_ceiling: int | None = None, replicated_linear: bool = True,
                  trace_levels: bool = False, level_budget=(4, 4), client=None,
-                 log=None):
+                 log=None, pt_cache_bytes: int = 48 << 30):
         if bootstrap_passes not in (1, 2):
             raise ValueError("bootstrap passes must be 1 or 2")
         self.cc, self.keys, self.slots = cc, keys, int(slots)
@@ -350,7 +352,7 @@ class PackedEvaluator:
         self.client = client
         self.log = log or (lambda msg: None)
         self._rot_keys: set = set()
-        self._pt_cache: dict = {}
+        self._pt_cache = PlaintextCache(cc.GetRingDimension(), pt_cache_bytes)
         self.stats = dict(ct_ct=0, ct_pt=0, rotations=0, adds=0, bootstraps=0,
                           logical_refreshes=0, bootstrap_seconds=0.0, keygen_seconds=0.0,
                           rotation_keys=0, evaluated_nodes=0)
@@ -439,7 +441,7 @@ class PackedEvaluator:
             if pt is None:
                 pt = self.cc.MakeCKKSPackedPlaintext(v, 1, ct.GetLevel(), slots=self.slots)
                 if ck:
-                    self._pt_cache[ck] = pt
+                    self._pt_cache.put(ck, pt)
             return self.cc.EvalMult(ct, pt)
         self.stats["adds"] += 1
         return self.cc.EvalAdd(ct, self.cc.MakeCKKSPackedPlaintext(v, 1, 0, slots=self.slots))
@@ -463,25 +465,60 @@ class PackedEvaluator:
             x = self.mask(ct, int(support)) if support < self.slots else ct
         else:
             x = self.plain(ct, support, True)
-        # 1 / bound and bound ride on the bootstrap's own constants (no level)
+        # 1 / bound and bound ride on the bootstrap's own constants (no
+        # level); a power of two keeps the SlotToCoeff diagonals the same
+        # for every bound (it goes into EvalMod's integer gain or the last
+        # group's constant), at most one bit of the range given up
+        bound = 2.0 ** math.ceil(math.log2(max(float(bound), 2.0 ** -30)))
         out = self.cc.EvalBootstrap(x, self.bootstrap_passes, REFRESH_SCALE_BITS,
-                                    scale=float(bound))
+                                    scale=bound)
         self.stats["bootstraps"] += self.bootstrap_passes
         self.stats["logical_refreshes"] += 1
         self.stats["bootstrap_seconds"] += time.perf_counter() - t0
         return out
 
     # ------------------------------------------------------------- node kinds
-    def transform(self, x, masks: dict):
-        """sum over offsets of rot(x, offset) * mask (rotations hoisted)."""
+    def transform(self, x, masks: dict, key=None):
+        """sum over offsets of rot(x, offset) * mask.  Offsets on an
+        arithmetic progression (8 or more) go through the baby-step
+        giant-step transform (about 2 sqrt(count) rotations and keys, as
+        the reference's plan_packed_diagonals, include/packed_routing.hpp:
+        23-45); others are hoisted rotations of x.  `key` names the mask set
+        for the plaintext cache."""
         if not masks:
             return self.scale(x, 0.0)
         offs = sorted(masks)
+        step = offs[1] - offs[0] if len(offs) > 1 else 0
+        if len(offs) >= 8 and step and all(b - a == step for a, b in zip(offs, offs[1:])):
+            return self._transform_bsgs(x, offs, step, masks, key)
         rots = self.rotate_hoisted(x, offs)
         out = None
         for off, r in zip(offs, rots):
             term = self.plain(r, masks[off], True)
             out = term if out is None else self.add(out, term)
+        return out
+
+    def _transform_bsgs(self, x, offs, step, masks, key):
+        rows = len(offs)
+        b = max(2, 1 << round(math.log2(math.sqrt(rows))))
+        if x.GetNoiseScaleDeg() >= 2:
+            x = self.cc.Rescale(x)
+        level = x.GetLevel()
+        ck = None if key is None else (key, "bsgs", level)
+        pts = self._pt_cache.get(ck) if ck else None
+        if pts is None:
+            pts = [self.cc.MakeCKKSPackedPlaintext(np.roll(masks[o], (k // b) * b * step), 1,
+                                                   level, slots=self.slots)
+                   for k, o in enumerate(offs)]
+            if ck:
+                self._pt_cache.put(ck, pts)
+        giants = -(-rows // b)
+        self._ensure_keys([j * step for j in range(1, min(b, rows))] +
+                          ([b * step] if rows > b else []) + [offs[0]])
+        self.stats["rotations"] += (min(b, rows) - 1) + (giants - 1) + (1 if offs[0] % self.slots else 0)
+        self.stats["ct_pt"] += rows
+        out = x.Clone()
+        self.cc.LinearTransformInPlace(out, rows, b, pts, step % self.slots, offs[0] % self.slots)
         return out
 
     def gather(self, x, indices, size: int, scatter: bool, bound: float, width: int):
@@ -530,7 +567,7 @@ class PackedEvaluator:
                     mask = np.roll(mask, (k // b) * b * stride)
                     pts.append(self.cc.MakeCKKSPackedPlaintext(mask, 1, rep.GetLevel(),
                                                                slots=self.slots))
-                self._pt_cache[cache_key] = pts
+                self._pt_cache.put(cache_key, pts)
             used = [bb * stride for bb in range(1, b)]
             if shape.per_replica > b:
                 used.append(b * stride)

@@ -210,6 +210,7 @@ class SimCC:
 
 
 SimCt.GetScalingFactor = lambda self: 2.0 ** 59
+SimCt.SetScalingFactor = lambda self, scale: None
 
 
 @pytest.mark.parametrize("log_n,budget", [(8, (2, 2)), (10, (3, 3)), (11, (4, 2))])
@@ -260,3 +261,27 @@ def test_bootstrap_rejects_a_fresh_top_level_input():
     boot = B.CKKSBootstrapper(cc, B.BootstrapConfig.for_ring(256, (2, 2)))
     with pytest.raises(ValueError):
         boot.bootstrap(SimCt(np.zeros(128), 29))
+
+
+@pytest.mark.parametrize("total", [37.25, -37.25, 3.0e-5, 1.0, 16.0, -0.75])
+@pytest.mark.parametrize("groups", [1, 2, 3, 4])
+def test_group_factors(total, groups):
+    """The group constants multiply to the total (even spread or power of
+    two on the last group); with the power on the last group, totals that
+    differ by a power of two share every other group's constant, and a
+    total in (2^(g-1), 2^g) is spread evenly."""
+    for power_last in (False, True):
+        f = B.CKKSBootstrapper.group_factors(total, groups, power_last)
+        assert len(f) == groups
+        assert math.isclose(math.prod(f), total, rel_tol=1e-12)
+    f = B.CKKSBootstrapper.group_factors(total, groups, True)
+    for k in (-13, -1, 3):
+        g = B.CKKSBootstrapper.group_factors(total * 2.0 ** k, groups, True)
+        assert g[:-1] == f[:-1]
+        assert g[-1] == f[-1] * 2.0 ** k
+    inside = 1.5 * 2.0 ** (groups - 1)
+    even = B.CKKSBootstrapper.group_factors(inside, groups, False)
+    split = B.CKKSBootstrapper.group_factors(inside, groups, True)
+    assert all(math.isclose(a, b, rel_tol=1e-14) for a, b in zip(even, split))
+    with pytest.raises(ValueError):
+        B.CKKSBootstrapper.group_factors(0.0, groups)
