@@ -207,6 +207,7 @@ Context::~Context() {
   for (auto& kv : plans) {
     ConvPlan* pl = kv.second.get();
     hipFree(pl->d_qhat_inv);
+    hipFree(pl->d_src_scale);
     hipFree(pl->d_qhat_mont);
     hipFree(pl->d_dst_idx);
     hipFree(pl->d_src_idx32);
@@ -234,6 +235,7 @@ ConvPlan* Context::build_plan(const std::vector<uint32_t>& src, const std::vecto
   pl->src_idx = src;
   pl->dst_idx = dst;
   std::vector<uint64_t> qhat_inv(2 * src.size()), qhat_mont(src.size() * dst.size());
+  std::vector<uint64_t> src_scale(2 * src.size());
   for (size_t a = 0; a < src.size(); ++a) {
     const uint64_t qa = mods[src[a]];
     uint64_t h = 1 % qa;
@@ -242,6 +244,9 @@ ConvPlan* Context::build_plan(const std::vector<uint32_t>& src, const std::vecto
     const uint64_t hi = host_invmod(h, qa);
     qhat_inv[2 * a] = hi;
     qhat_inv[2 * a + 1] = host_shoup(hi, qa);
+    const uint64_t sc = host_mulmod(hi, host_invmod(n % qa, qa), qa);
+    src_scale[2 * a] = sc;
+    src_scale[2 * a + 1] = host_shoup(sc, qa);
     for (size_t k = 0; k < dst.size(); ++k) {
       const uint64_t t = mods[dst[k]];
       uint64_t hk = 1 % t;
@@ -253,6 +258,7 @@ ConvPlan* Context::build_plan(const std::vector<uint32_t>& src, const std::vecto
   }
   pl->d_qhat_inv = upload(qhat_inv);
   pl->d_qhat_mont = upload(qhat_mont);
+  pl->d_src_scale = upload(src_scale);
   pl->d_dst_idx = upload(dst);
   pl->d_src_idx32 = upload(src);
   ConvPlan* raw = pl.get();

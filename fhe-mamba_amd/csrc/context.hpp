@@ -67,6 +67,9 @@ struct ConvPlan {
   uint32_t nsrc = 0, ndst = 0;
   std::vector<uint32_t> src_idx, dst_idx;  // modulus indices
   uint64_t* d_qhat_inv = nullptr;          // [nsrc][2]  (value, Shoup)
+  // qhat_inv_i * N^-1 mod s_i (value, Shoup): the first factor with the
+  // inverse NTT's scaling folded in, for conversions fused after a transform.
+  uint64_t* d_src_scale = nullptr;         // [nsrc][2]
   uint64_t* d_qhat_mont = nullptr;         // [nsrc][ndst]
   uint32_t* d_dst_idx = nullptr;           // [ndst]
   uint32_t* d_src_idx32 = nullptr;         // [nsrc]
@@ -263,6 +266,14 @@ void ntt_forward_moddown(Context& c, uint64_t* y, uint32_t npoly, uint32_t nq,
 // formed while the first pass loads its input (epi.digits / key / mc / kl /
 // nd / ne / nq / L are used; the output fields are not).
 void ntt_inverse_ksk(Context& c, uint64_t* ext_p, uint32_t npoly, const ModDownEpi& epi);
+// ModDown of a key-switch batch in three launches for ring dimensions
+// 2^13..2^17 with every Q_l and P modulus below 2^60: the first inverse pass
+// with the P-limb inner products (into ext_p, blocked layout), one kernel
+// for the inverse column stages + conversion P -> Q_l + forward column
+// stages (into y, blocked), and the last forward pass with the epilogue.
+bool moddown_fused_ok(const Context& c, uint32_t nq);
+void moddown_fused(Context& c, uint64_t* ext_p, uint64_t* y, uint32_t npoly, uint32_t nq,
+                   const ConvPlan& pl, const ModDownEpi& epi);
 // Forward NTT of the converted limbs of the ModUp digits of `count`
 // ciphertexts, [count][nd][nq+K][N].
 void ntt_forward_digits(Context& c, uint64_t* digits, uint32_t count, uint32_t nd, uint32_t nq);

@@ -375,6 +375,10 @@ void keyswitch_batch(Context& c, const uint64_t* const* digits, uint32_t nq,
   // P limbs of the inner product (formed by the inverse NTT's first pass),
   // to coefficient form, converted to Q; then the forward NTT with the
   // Q-limb products and the combine in its last pass.
+  if (moddown_fused_ok(c, nq)) {
+    moddown_fused(c, ext.p, y.p, 2 * batch, nq, c.moddown_plan(nq), epi);
+    return;
+  }
   ntt_inverse_ksk(c, ext.p, 2 * batch, epi);
   convert(c, c.moddown_plan(nq), ext.p, kw, y.p, (size_t)nq * n, nq, 2 * batch);
   ntt_forward_moddown(c, y.p, 2 * batch, nq, epi);

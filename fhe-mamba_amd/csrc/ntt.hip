@@ -61,8 +61,13 @@ struct PlainLoad {
   __device__ __forceinline__ uint64_t get(size_t, uint64_t) const { return 0; }
 };
 
+// BLK_IN / BLK_OUT (BLOCKS kind): the first pass's input / the last pass's
+// output uses the blocked layout described with blocked_off below.  A
+// workgroup's tile then still occupies the words [wg0, wg0 + LINES * LEN),
+// in the order p = u * LINES + line, and is staged through LDS whatever the
+// window.
 template <int S, int KIND, bool INV, int RHO_, class Store, class Load = PlainLoad,
-          class Map = LimbMap>
+          class Map = LimbMap, bool BLK_IN = false, bool BLK_OUT = false>
 __device__ __forceinline__ void ntt_body(uint64_t* __restrict__ data, size_t poly_stride,
                                          const ModConst* __restrict__ mc,
                                          const uint64_t* __restrict__ tw_all, uint32_t log_n,
@@ -123,13 +128,14 @@ __device__ __forceinline__ void ntt_body(uint64_t* __restrict__ data, size_t pol
     // so that lanes touch consecutive addresses.
     const bool contiguous = KIND != COLS && w == 0;
 
-    if (sp == 0 && contiguous) {
+    if (sp == 0 && (contiguous || BLK_IN)) {
       const size_t wg0 = ((size_t)blockIdx.x * LINES) << S;
 #pragma unroll
       for (int k = 0; k < R; ++k) {
         const uint32_t p = k * blockDim.x + tid;
-        lds[lds_idx(p >> S, p & (G::LEN - 1), G::PITCH)] =
-            Load::kLoad ? load.get(wg0 + p, q) : base[wg0 + p];
+        const uint32_t li = BLK_IN ? lds_idx(p % LINES, p / LINES, G::PITCH)
+                                   : lds_idx(p >> S, p & (G::LEN - 1), G::PITCH);
+        lds[li] = Load::kLoad ? load.get(wg0 + p, q) : base[wg0 + p];
       }
       __syncthreads();
 #pragma unroll
@@ -216,7 +222,7 @@ __device__ __forceinline__ void ntt_body(uint64_t* __restrict__ data, size_t pol
           for (int v = 0; v < R; ++v) x[v] = reduce_4q(shoup_lazy4(x[v], ni, nis, q), q);
         }
       }
-      if (contiguous) {
+      if (contiguous || BLK_OUT) {
         if (sp > 0 || NSP == 1) __syncthreads();
 #pragma unroll
         for (int v = 0; v < R; ++v) {
@@ -228,8 +234,9 @@ __device__ __forceinline__ void ntt_body(uint64_t* __restrict__ data, size_t pol
 #pragma unroll
         for (int k = 0; k < R; ++k) {
           const uint32_t p = k * blockDim.x + tid;
-          store.fin(base, wg0 + p, lds[lds_idx(p >> S, p & (G::LEN - 1), G::PITCH)],
-                    pre[Store::kPre ? k : 0], q);
+          const uint32_t li = BLK_OUT ? lds_idx(p % LINES, p / LINES, G::PITCH)
+                                      : lds_idx(p >> S, p & (G::LEN - 1), G::PITCH);
+          store.fin(base, wg0 + p, lds[li], pre[Store::kPre ? k : 0], q);
         }
       } else {
 #pragma unroll
@@ -348,25 +355,251 @@ struct KskLoad {
   }
 };
 
+// Blocked limb layout of ModDown's intermediates (P limbs between the first
+// inverse pass and the fused middle kernel, y between that kernel and the
+// last forward pass).  With the split index s = b * N2 + u (row b < N1,
+// column u < N2 = 2^S2), rows are grouped by BLO, the line count of a radix-8
+// block-pass workgroup:
+//   offset(b, u) = (b / BLO) * BLO * N2 + u * BLO + b % BLO.
+// A block-pass workgroup (BLO consecutive rows, all columns) then touches
+// one contiguous BLO * N2 run, and a column (all rows, one u) is N1 / BLO
+// runs of BLO words.
+template <int S2>
+constexpr int blocked_rows() {
+  return 256 >> (S2 - RHO_EPILOGUE);
+}
+
+template <int S2>
+__device__ __forceinline__ size_t blocked_off(uint32_t b, uint32_t u) {
+  constexpr uint32_t BLO = blocked_rows<S2>();
+  return (size_t)(b / BLO) * ((size_t)BLO << S2) + (size_t)u * BLO + (b % BLO);
+}
+
 // First inverse pass of ModDown (BLOCKS or SINGLE kind) fed by KskLoad.
-template <int S, int KIND, int ND>
+// BLK: BLOCKS pass that writes the blocked layout.
+template <int S, int KIND, int ND, bool BLK>
 __global__ void __launch_bounds__(256)
     ntt_pass_ksk(uint64_t* __restrict__ data, size_t poly_stride, const ModConst* __restrict__ mc,
                  const uint64_t* __restrict__ tw_all, uint32_t log_n, uint32_t s_other,
                  int last, const ModDownEpi epi) {
-  ntt_body<S, KIND, true, epilogue_rho<S, KIND>()>(
+  ntt_body<S, KIND, true, epilogue_rho<S, KIND>(), PlainStore, KskLoad<ND>, LimbMap, false, BLK>(
       data, poly_stride, mc, tw_all, log_n, LimbMap::contiguous(epi.L), s_other, last,
       PlainStore{}, KskLoad<ND>{epi, 1u << log_n});
 }
 
-template <int S, int KIND, int ND>
+// BLK: y is read from the blocked layout.
+template <int S, int KIND, int ND, bool BLK>
 __global__ void __launch_bounds__(256)
     ntt_pass_moddown(uint64_t* __restrict__ data, size_t poly_stride,
                      const ModConst* __restrict__ mc, const uint64_t* __restrict__ tw_all,
                      uint32_t log_n, uint32_t s_other, const ModDownEpi epi) {
-  ntt_body<S, KIND, false, epilogue_rho<S, KIND>()>(data, poly_stride, mc, tw_all, log_n,
-                                                    LimbMap::contiguous(0), s_other, 1,
-                                                    EpiStore<ND>{epi, 1u << log_n, log_n});
+  ntt_body<S, KIND, false, epilogue_rho<S, KIND>(), EpiStore<ND>, PlainLoad, LimbMap, BLK>(
+      data, poly_stride, mc, tw_all, log_n, LimbMap::contiguous(0), s_other, 1,
+      EpiStore<ND>{epi, 1u << log_n, log_n});
+}
+
+// ---- Fused middle of a batched ModDown, ring dimensions 2^13 .. 2^17 ----
+//
+// One workgroup per (poly, column u): the last S1 inverse stages of the K
+// P limbs (the column stages; the first pass wrote the blocked P limbs), the
+// scaling by N^-1 * [P/p_t]^-1 folded into one Shoup product, the fast
+// conversion P -> Q_l (30-bit split MACs, one REDC per output, constants in
+// Montgomery form with -P^-1 folded in), and the first S1 forward stages of
+// every Q limb, written to the blocked y.  This replaces an inverse column
+// pass, a conversion and a forward column pass, and the three round trips
+// of the P limbs and y through HBM between them.
+//
+// Each column line of M = 2^S1 rows belongs to TPL = min(64, M / 4) lanes of
+// one wavefront (radix M / TPL per lane), so its sub-passes exchange through
+// LDS with wavefront-level ordering only; the four waves of a workgroup meet
+// at a single barrier, once the converted sources are in LDS.  With one line
+// per wave the modulus, its twiddles and the conversion constants are
+// wavefront-uniform.  Stage order, twiddle indices and lazy ranges are those
+// of the column passes of ntt_body.
+
+template <int S1>
+constexpr uint32_t mid_pitch() {
+  return (1u << S1) + (1u << S1) / 16 + 1;
+}
+template <int S1>
+constexpr int mid_lanes_per_line() {
+  return (1 << S1) / 4 < 64 ? (1 << S1) / 4 : 64;
+}
+template <int S1>
+constexpr int mid_lines() {  // lines in flight per workgroup (4 waves)
+  return 4 * (64 / mid_lanes_per_line<S1>());
+}
+
+// LDS writes of this wavefront before the call are seen by its reads after
+// the call (LDS executes a wavefront's instructions in order; this keeps the
+// compiler from moving accesses across).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <int S1, int S2>
+__global__ void __launch_bounds__(256)
+    k_moddown_mid(const uint64_t* __restrict__ ext, uint64_t* __restrict__ y,
+                  const ModConst* __restrict__ mc, const uint64_t* __restrict__ tw_inv,
+                  const uint64_t* __restrict__ tw_fwd, const uint64_t* __restrict__ src_scale,
+                  const uint64_t* __restrict__ qhat_mont, uint32_t K, uint32_t nq, uint32_t L) {
+  constexpr int M = 1 << S1, TPL = mid_lanes_per_line<S1>(), R = M / TPL;
+  constexpr int RHO = R == 4 ? 2 : 3, LPW = 64 / TPL, NL = mid_lines<S1>();
+  constexpr int NSP = (S1 + RHO - 1) / RHO;
+  constexpr uint32_t PITCH = mid_pitch<S1>(), N2 = 1u << S2;
+  constexpr size_t N = (size_t)M << S2;
+  constexpr uint32_t M30 = (1u << 30) - 1;
+  static_assert(R * TPL == M && (1 << RHO) == R, "column split");
+  extern __shared__ uint64_t lds_dyn[];
+  uint64_t* const src = lds_dyn;
+  uint64_t* const work = lds_dyn + (size_t)K * PITCH;
+
+  // Tiles in XCD order: workgroup i runs on XCD i % 8, and each XCD takes a
+  // contiguous range of (poly, column) tiles, so neighbouring columns, which
+  // share cache lines of the blocked layout, meet in one L2.
+  const uint32_t per = gridDim.x / 8;
+  const uint32_t tile = (blockIdx.x % 8) * per + blockIdx.x / 8;
+  const uint32_t p = tile / N2, col = tile % N2;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t lane = threadIdx.x & 63, sub = lane / TPL, tau = lane % TPL;
+  const uint32_t first = wave * LPW + sub;
+
+  // Inverse column stages of the P limbs; each limb is one line of src.
+  for (uint32_t t = first; t < K; t += NL) {
+    const uint32_t midx = L + t;
+    const uint64_t q = mc[midx].q, q4 = 4 * q;
+    const uint64_t* __restrict__ tw = tw_inv + (size_t)midx * N * 2;
+    uint64_t* const line = src + (size_t)t * PITCH;
+    uint64_t x[R];
+    // First window (bits 0 .. RHO-1): rows R tau + v, one blocked run.
+    const uint64_t* g = ext + ((size_t)p * K + t) * N + blocked_off<S2>(R * tau, col);
+#pragma unroll
+    for (int v = 0; v < R; ++v) x[v] = g[v];
+#pragma unroll
+    for (int sp = 0; sp < NSP; ++sp) {
+      const int lo = RHO * sp;
+      const int w = lo + RHO <= S1 ? lo : S1 - RHO;
+      const int bhi = lo + RHO <= S1 ? lo + RHO - 1 : S1 - 1;
+      const uint32_t thi = (tau >> w) << (w + RHO), tlo = tau & ((1u << w) - 1);
+      if (sp > 0) {
+#pragma unroll
+        for (int v = 0; v < R; ++v) x[v] = line[lds_idx(0, thi | ((uint32_t)v << w) | tlo, 0)];
+      }
+#pragma unroll
+      for (int beta = lo; beta <= bhi; ++beta) {
+        const int d = 1 << (beta - w);
+#pragma unroll
+        for (int v = 0; v < R; ++v) {
+          if (v & d) continue;
+          const uint32_t u = thi | ((uint32_t)v << w) | tlo;
+          const uint32_t ti = (1u << (S1 - 1 - beta)) | (u >> (beta + 1));
+          const uint64_t wv = tw[2 * ti], ws = tw[2 * ti + 1];
+          const uint64_t X = x[v], Y = x[v + d];
+          uint64_t Sx = X + Y;
+          Sx = Sx >= q4 ? Sx - q4 : Sx;
+          x[v + d] = shoup_lazy4(X + q4 - Y, wv, ws, q);
+          x[v] = Sx;
+        }
+      }
+      if (sp == NSP - 1) {
+        // v_t = x N^-1 [P/p_t]^-1 mod p_t, stored as 30-bit halves.
+        const uint64_t f = src_scale[2 * t], fs = src_scale[2 * t + 1];
+#pragma unroll
+        for (int v = 0; v < R; ++v) {
+          const uint64_t z = reduce_4q(shoup_lazy4(x[v], f, fs, q), q);
+          x[v] = ((uint64_t)(uint32_t)(z >> 30) << 32) | ((uint32_t)z & M30);
+        }
+      }
+      wave_lds_sync();
+#pragma unroll
+      for (int v = 0; v < R; ++v) line[lds_idx(0, thi | ((uint32_t)v << w) | tlo, 0)] = x[v];
+      wave_lds_sync();
+    }
+  }
+  __syncthreads();
+
+  // Conversion into the Q limbs, one line of `work` per line in flight, then
+  // their forward column stages.
+  uint64_t* const line = work + (size_t)first * PITCH;
+  for (uint32_t k = first; k < nq; k += NL) {
+    const uint64_t q = mc[k].q, q4 = 4 * q, qn = mc[k].qinv_neg;
+    const uint64_t* __restrict__ tw = tw_fwd + (size_t)k * N * 2;
+    uint64_t x[R];
+    {
+      // First forward window (bits S1-RHO .. S1-1): rows thi | v << w | tlo.
+      constexpr int w = S1 - RHO;
+      const uint32_t thi = (tau >> w) << (w + RHO), tlo = tau & ((1u << w) - 1);
+      uint64_t a0[R], a1a[R], a1b[R], a2[R];
+#pragma unroll
+      for (int v = 0; v < R; ++v) a0[v] = a1a[v] = a1b[v] = a2[v] = 0;
+      for (uint32_t i = 0; i < K; ++i) {
+        const uint64_t cv = qhat_mont[(size_t)i * nq + k];
+        const uint32_t cl = (uint32_t)cv & M30, ch = (uint32_t)(cv >> 30);
+        const uint64_t* sl = src + (size_t)i * PITCH;
+#pragma unroll
+        for (int v = 0; v < R; ++v) {
+          const uint64_t sv = sl[lds_idx(0, thi | ((uint32_t)v << w) | tlo, 0)];
+          const uint32_t vl = (uint32_t)sv, vh = (uint32_t)(sv >> 32);
+          a0[v] += (uint64_t)vl * cl;
+          a1a[v] += (uint64_t)vl * ch;
+          a1b[v] += (uint64_t)vh * cl;
+          a2[v] += (uint64_t)vh * ch;
+        }
+      }
+#pragma unroll
+      for (int v = 0; v < R; ++v) {
+        // T = a0 + (a1a + a1b) 2^30 + a2 2^60 < K 2^60 q <= q 2^64.
+        const uint64_t s1 = a1a[v] + a1b[v];
+        const uint64_t c1 = s1 < a1a[v];
+        const uint64_t m1 = s1 << 30, m2 = a2[v] << 60;
+        const uint64_t lo = a0[v] + m1;
+        uint64_t hh = (s1 >> 34) + (c1 << 30) + (a2[v] >> 4) + (lo < m1);
+        const uint64_t lo2 = lo + m2;
+        hh += lo2 < m2;
+        x[v] = redc(hh, lo2, q, qn);
+      }
+    }
+#pragma unroll
+    for (int sp = 0; sp < NSP; ++sp) {
+      const int hi = S1 - RHO * sp;
+      const int w = hi >= RHO ? hi - RHO : 0;
+      const int bhi = hi - 1;
+      const uint32_t thi = (tau >> w) << (w + RHO), tlo = tau & ((1u << w) - 1);
+      if (sp > 0) {
+#pragma unroll
+        for (int v = 0; v < R; ++v) x[v] = line[lds_idx(0, thi | ((uint32_t)v << w) | tlo, 0)];
+      }
+#pragma unroll
+      for (int beta = bhi; beta >= w; --beta) {
+        const int d = 1 << (beta - w);
+#pragma unroll
+        for (int v = 0; v < R; ++v) {
+          if (v & d) continue;
+          const uint32_t u = thi | ((uint32_t)v << w) | tlo;
+          const uint32_t ti = (1u << (S1 - 1 - beta)) | (u >> (beta + 1));
+          const uint64_t wv = tw[2 * ti], ws = tw[2 * ti + 1];
+          uint64_t X = x[v];
+          X = X >= q4 ? X - q4 : X;
+          const uint64_t T = shoup_lazy4(x[v + d], wv, ws, q);
+          x[v] = X + T;
+          x[v + d] = X + q4 - T;
+        }
+      }
+      if (sp < NSP - 1) {
+        wave_lds_sync();
+#pragma unroll
+        for (int v = 0; v < R; ++v) line[lds_idx(0, thi | ((uint32_t)v << w) | tlo, 0)] = x[v];
+        wave_lds_sync();
+      } else {
+        // Last window (bits 0 .. RHO-1): rows R tau + v, one blocked run.
+        uint64_t* g = y + ((size_t)p * nq + k) * N + blocked_off<S2>(R * tau, col);
+#pragma unroll
+        for (int v = 0; v < R; ++v) g[v] = x[v];
+      }
+    }
+  }
 }
 
 template <int S, int KIND, bool INV, class Map>
@@ -420,7 +653,7 @@ void launch_blocks(Context& c, uint32_t s1, uint32_t s2, uint64_t* data, uint32_
   }
 }
 
-template <int S, int KIND>
+template <int S, int KIND, bool BLK = false>
 void launch_moddown(Context& c, uint64_t* y, uint32_t npoly, uint32_t nq, uint32_t s_other,
                     const ModDownEpi& epi) {
   using G = Geo<S, epilogue_rho<S, KIND>()>;
@@ -431,18 +664,19 @@ void launch_moddown(Context& c, uint64_t* y, uint32_t npoly, uint32_t nq, uint32
   switch (epi.nd) {
 #define CASE(D)                                                                               \
   case D:                                                                                     \
-    FHE_LAUNCH(c, name, (ntt_pass_moddown<S, KIND, D>), dim3(tiles, npoly, nq), dim3(threads), \
+    FHE_LAUNCH(c, name, (ntt_pass_moddown<S, KIND, D, BLK>), dim3(tiles, npoly, nq),          \
+               dim3(threads),                                                                  \
                0, y, (size_t)nq * c.n, c.d_const, c.d_tw_fwd, c.log_n, s_other, epi);         \
     return;
     CASE(1) CASE(2) CASE(3)
 #undef CASE
     default:
-      FHE_LAUNCH(c, name, (ntt_pass_moddown<S, KIND, 0>), dim3(tiles, npoly, nq), dim3(threads), 0,
+      FHE_LAUNCH(c, name, (ntt_pass_moddown<S, KIND, 0, BLK>), dim3(tiles, npoly, nq), dim3(threads), 0,
                  y, (size_t)nq * c.n, c.d_const, c.d_tw_fwd, c.log_n, s_other, epi);
   }
 }
 
-template <int S, int KIND>
+template <int S, int KIND, bool BLK = false>
 void launch_ksk(Context& c, uint64_t* ext, uint32_t npoly, uint32_t s_other, bool last,
                 const ModDownEpi& epi) {
   using G = Geo<S, epilogue_rho<S, KIND>()>;
@@ -455,18 +689,69 @@ void launch_ksk(Context& c, uint64_t* ext, uint32_t npoly, uint32_t s_other, boo
   switch (epi.nd) {
 #define CASE(D)                                                                         \
   case D:                                                                               \
-    FHE_LAUNCH(c, name, (ntt_pass_ksk<S, KIND, D>), grid, dim3(threads), 0, ext, ps,     \
+    FHE_LAUNCH(c, name, (ntt_pass_ksk<S, KIND, D, BLK>), grid, dim3(threads), 0, ext, ps, \
                c.d_const, c.d_tw_inv, c.log_n, s_other, (int)last, epi);                \
     return;
     CASE(1) CASE(2) CASE(3)
 #undef CASE
     default:
-      FHE_LAUNCH(c, name, (ntt_pass_ksk<S, KIND, 0>), grid, dim3(threads), 0, ext, ps, c.d_const,
+      FHE_LAUNCH(c, name, (ntt_pass_ksk<S, KIND, 0, BLK>), grid, dim3(threads), 0, ext, ps, c.d_const,
                  c.d_tw_inv, c.log_n, s_other, (int)last, epi);
   }
 }
 
+template <int S1, int S2>
+size_t mid_lds_bytes(uint32_t K) {
+  return (size_t)(K + mid_lines<S1>()) * mid_pitch<S1>() * 8;
+}
+
+template <int S1, int S2>
+void launch_mid(Context& c, const ConvPlan& pl, const uint64_t* ext, uint64_t* y,
+                uint32_t npoly, uint32_t nq) {
+  FHE_LAUNCH(c, "k_moddown_mid", (k_moddown_mid<S1, S2>), dim3(npoly << S2), dim3(256),
+             (mid_lds_bytes<S1, S2>(c.K)), ext, y, c.d_const, c.d_tw_inv, c.d_tw_fwd,
+             pl.d_src_scale, pl.d_qhat_mont, c.K, nq, c.L);
+}
+
 }  // namespace
+
+bool moddown_fused_ok(const Context& c, uint32_t nq) {
+  if (c.log_n < 13 || c.log_n > 17 || c.K == 0 || c.K > 16) return false;
+  if (nq == 0 || nq > c.L) return false;
+  for (uint32_t i = 0; i < nq; ++i)
+    if (c.mods[i] >= (1ull << 60)) return false;
+  for (uint32_t t = 0; t < c.K; ++t)
+    if (c.mods[c.L + t] >= (1ull << 60)) return false;
+  size_t lds = 0;
+  switch (c.log_n) {
+    case 13: lds = mid_lds_bytes<7, 6>(c.K); break;
+    case 14: lds = mid_lds_bytes<7, 7>(c.K); break;
+    case 15: lds = mid_lds_bytes<8, 7>(c.K); break;
+    case 16: lds = mid_lds_bytes<8, 8>(c.K); break;
+    default: lds = mid_lds_bytes<9, 8>(c.K); break;
+  }
+  return lds <= 65536;
+}
+
+void moddown_fused(Context& c, uint64_t* ext_p, uint64_t* y, uint32_t npoly, uint32_t nq,
+                   const ConvPlan& pl, const ModDownEpi& epi) {
+  if (npoly == 0) return;
+  if (npoly > 2 * MAX_KS_BATCH) throw ArgError("ModDown batch too large");
+  if (!moddown_fused_ok(c, nq)) throw ArgError("fused ModDown does not apply");
+  const uint32_t s1 = (c.log_n + 1) / 2, s2 = c.log_n / 2;
+  switch (c.log_n) {
+#define CASE(LN, A, B)                                                   \
+  case LN:                                                               \
+    launch_ksk<B, BLOCKS, true>(c, ext_p, npoly, s1, false, epi);        \
+    launch_mid<A, B>(c, pl, ext_p, y, npoly, nq);                        \
+    launch_moddown<B, BLOCKS, true>(c, y, npoly, nq, s1, epi);           \
+    return;
+    CASE(13, 7, 6) CASE(14, 7, 7) CASE(15, 8, 7) CASE(16, 8, 8) CASE(17, 9, 8)
+#undef CASE
+    default: throw ArgError("unsupported ring dimension");
+  }
+  (void)s2;
+}
 
 void ntt_forward_digits(Context& c, uint64_t* digits, uint32_t count, uint32_t nd,
                         uint32_t nq) {

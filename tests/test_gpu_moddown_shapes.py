@@ -1,0 +1,70 @@
+"""Key switching at every ring dimension of the three-launch ModDown
+(2^13 .. 2^17: column lengths 128 / 256 / 512 rows, blocked row groups of
+32 / 16 / 8) and at the rotation benchmark's shape (N=2^16, 24 limbs,
+8 special primes, dnum 3), bit-exact against the oracle."""
+import numpy as np
+import pytest
+
+import oracle as O
+from gpu_helpers import residues
+
+pytestmark = pytest.mark.gpu
+
+F = pytest.importorskip("fhemamba_amd")
+
+# (log_n, depth, scale bits, first bits, dnum); N=2^13 is covered by
+# test_gpu_keyswitch.py.
+SHAPES = [(14, 3, 50, 60, 2), (15, 3, 50, 60, 2), (16, 3, 50, 60, 3), (17, 2, 50, 60, 1)]
+
+
+@pytest.fixture(scope="module", params=SHAPES, ids=lambda p: f"logn{p[0]}")
+def setup(request):
+    log_n, depth, sb, fb, dnum = request.param
+    q, p = O.gen_moduli(log_n, depth, sb, fb, dnum)
+    ctx, orc = F.Context(log_n, q, p, dnum), O.Ctx(log_n, q, p, dnum)
+    return ctx, orc, orc.secret(21)
+
+
+def test_keyswitch_every_level(setup):
+    ctx, orc, s = setup
+    rng = np.random.default_rng(3)
+    key = orc.relin_key(s, 6)
+    dkey = ctx.load_key(key)
+    for nq in range(1, ctx.L + 1):
+        a = residues(rng, ctx.q[:nq], (1,), ctx.n)
+        got = ctx.keyswitch(ctx.upload(a), dkey).numpy()
+        assert np.array_equal(got, orc.keyswitch(a[0], key)), nq
+
+
+def test_hoisted_rotations(setup):
+    ctx, orc, s = setup
+    steps = [1, -3, 64]
+    gal = [O.galois_elt(r, ctx.n) for r in steps] + [2 * ctx.n - 1]
+    keys = [orc.galois_key(s, g, 90 + i) for i, g in enumerate(gal)]
+    ct = residues(np.random.default_rng(4), ctx.q, (2,), ctx.n)
+    dct = ctx.upload(ct)
+    digits = ctx.rotation_precompute(dct)
+    outs = ctx.rotate_hoisted(dct, digits, [ctx.load_key(k) for k in keys], gal)
+    for out, key, g in zip(outs, keys, gal):
+        assert np.array_equal(out.numpy(), orc.rotate(ct, key, g)), g
+
+
+def test_benchmark_shape_rotations():
+    """Two hoisted rotations and one single rotation one level down at the
+    benchmark's parameters (the shape its timed step runs)."""
+    q, p = O.gen_moduli(16, 23, 59, 60, 3)
+    ctx, orc = F.Context(16, q, p, 3), O.Ctx(16, q, p, 3)
+    assert (ctx.L, ctx.K) == (24, 8)
+    s = orc.secret(5)
+    gal = [O.galois_elt(r, ctx.n) for r in (1, -4096)]
+    keys = [orc.galois_key(s, g, 31 + i) for i, g in enumerate(gal)]
+    dkeys = [ctx.load_key(k) for k in keys]
+    rng = np.random.default_rng(6)
+    ct = residues(rng, ctx.q, (2,), ctx.n)
+    dct = ctx.upload(ct)
+    outs = ctx.rotate_hoisted(dct, ctx.rotation_precompute(dct), dkeys, gal)
+    for out, key, g in zip(outs, keys, gal):
+        assert np.array_equal(out.numpy(), orc.rotate(ct, key, g)), g
+    low = residues(rng, ctx.q[:ctx.L - 1], (2,), ctx.n)
+    got = ctx.rotate(ctx.upload(low), dkeys[0], gal[0]).numpy()
+    assert np.array_equal(got, orc.rotate(low, keys[0], gal[0]))
