@@ -155,6 +155,8 @@ Context::Context(uint32_t log_n_, const uint64_t* q, uint32_t num_q, const uint6
     mc.r2 = (uint64_t)((u128)mc.r64 * mc.r64 % qi);
     mc.ninv = host_invmod(n % qi, qi);
     mc.ninv_sh = host_shoup(mc.ninv, qi);
+    mc.neg_q = 0 - qi;
+    mc.neg_q4 = 0 - 4 * qi;
   }
   d_const = upload(hconst);
   d_tw_fwd = upload(fwd);

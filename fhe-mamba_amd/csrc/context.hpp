@@ -34,7 +34,7 @@ inline void hip_check(hipError_t e, const char* what) {
   if (e != hipSuccess) throw HipError(std::string(what) + ": " + hipGetErrorString(e));
 }
 
-// Per-modulus scalar constants, 64-byte aligned record.
+// Per-modulus scalar constants.
 struct ModConst {
   uint64_t q;
   uint64_t qinv_neg;   // -q^-1 mod 2^64
@@ -44,6 +44,10 @@ struct ModConst {
   uint64_t ninv;       // N^-1 mod q
   uint64_t ninv_sh;
   uint64_t r2;         // 2^128 mod q (to Montgomery form via redc)
+  // 2^64 - q and 2^64 - 4q, read from memory so that the compiler keeps
+  // additions of them (shoup_lazy4n, lazy_sub) instead of folding them back
+  // into borrow-chain subtractions.
+  uint64_t neg_q, neg_q4;
 };
 
 // x mod q for a 128-bit x = hi * 2^64 + lo (any hi): hi * (2^64 mod q) by

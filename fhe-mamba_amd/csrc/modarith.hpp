@@ -39,6 +39,30 @@ FHE_HD uint64_t shoup_lazy4(uint64_t a, uint64_t w, uint64_t wp, uint64_t q) {
   return a * w - qt * q;
 }
 
+// shoup_lazy4 with the remainder accumulated against qneg = 2^64 - q:
+// a*w - qt*q = a*w + qt*qneg (mod 2^64), which the VALU forms with
+// v_mad_u64_u32 accumulations and no borrow chain.  Same quotient, so the
+// same value in [0, 4q).
+FHE_HD uint64_t shoup_lazy4n(uint64_t a, uint64_t w, uint64_t wp, uint64_t qneg) {
+  const uint32_t a0 = (uint32_t)a, a1 = (uint32_t)(a >> 32);
+  const uint32_t p0 = (uint32_t)wp, p1 = (uint32_t)(wp >> 32);
+  const uint32_t w0 = (uint32_t)w, w1 = (uint32_t)(w >> 32);
+  const uint32_t n0 = (uint32_t)qneg, n1 = (uint32_t)(qneg >> 32);
+  const uint64_t qt = (uint64_t)a1 * p1 + (((uint64_t)a0 * p1) >> 32) +
+                      (((uint64_t)a1 * p0) >> 32);
+  const uint32_t t0 = (uint32_t)qt, t1 = (uint32_t)(qt >> 32);
+  const uint64_t lo = (uint64_t)t0 * n0 + (uint64_t)a0 * w0;
+  const uint32_t hi = (uint32_t)(lo >> 32) + a0 * w1 + a1 * w0 + t0 * n1 + t1 * n0;
+  return ((uint64_t)hi << 32) | (uint32_t)lo;
+}
+
+// x >= m ? x - m : x for nm = 2^64 - m, m <= 2^63 and x - m < 2^63 when
+// x >= m: d = x - m wraps above 2^63 exactly when x < m.
+FHE_HD uint64_t lazy_sub(uint64_t x, uint64_t nm) {
+  const uint64_t d = x + nm;
+  return (int64_t)d < 0 ? x : d;
+}
+
 FHE_HD uint64_t reduce_2q(uint64_t x, uint64_t q) { return x >= q ? x - q : x; }
 
 FHE_HD uint64_t reduce_4q(uint64_t x, uint64_t q) {

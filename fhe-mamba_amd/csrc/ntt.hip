@@ -20,7 +20,7 @@
 // bank conflicts.  Workgroups are 256 threads (4096 elements, ~35 KB LDS).
 //
 // Arithmetic: Harvey lazy butterflies with an approximate-quotient Shoup
-// product (shoup_lazy4, result in [0, 4q)).  Forward values stay in [0, 8q),
+// product (shoup_lazy4n, result in [0, 4q)).  Forward values stay in [0, 8q),
 // inverse values in [0, 4q); the final launch reduces to [0, q).  This
 // needs 8q < 2^64, guaranteed by q < 2^61.
 //
@@ -87,7 +87,7 @@ __device__ __forceinline__ void ntt_body(uint64_t* __restrict__ data, size_t pol
   // Lazy ranges (approximate Shoup products land in [0, 4q)): forward
   // stage outputs stay in [0, 8q), inverse ones in [0, 4q); 8q < 2^64 as
   // every prime is below 2^61.
-  const uint64_t q = mc[midx].q, q4 = 4 * q;
+  const uint64_t q = mc[midx].q, q4 = 4 * q, qneg = mc[midx].neg_q, q4neg = mc[midx].neg_q4;
   const uint64_t* __restrict__ tw = tw_all + (size_t)midx * n * 2;
   uint64_t* __restrict__ base = data + (size_t)blockIdx.y * poly_stride + (size_t)pos * n;
 
@@ -185,9 +185,8 @@ __device__ __forceinline__ void ntt_body(uint64_t* __restrict__ data, size_t pol
           const uint32_t u = thi | ((uint32_t)v << w) | tlo;
           const uint32_t ti = (twbase << (S - 1 - beta)) | (u >> (beta + 1));
           const uint64_t wv = tw[2 * ti], ws = tw[2 * ti + 1];
-          uint64_t X = x[v];
-          X = X >= q4 ? X - q4 : X;
-          const uint64_t T = shoup_lazy4(x[v + d], wv, ws, q);
+          const uint64_t X = lazy_sub(x[v], q4neg);
+          const uint64_t T = shoup_lazy4n(x[v + d], wv, ws, qneg);
           x[v] = X + T;
           x[v + d] = X + q4 - T;
         }
@@ -203,10 +202,8 @@ __device__ __forceinline__ void ntt_body(uint64_t* __restrict__ data, size_t pol
           const uint32_t ti = (twbase << (S - 1 - beta)) | (u >> (beta + 1));
           const uint64_t wv = tw[2 * ti], ws = tw[2 * ti + 1];
           const uint64_t X = x[v], Y = x[v + d];
-          uint64_t Sx = X + Y;
-          Sx = Sx >= q4 ? Sx - q4 : Sx;
-          x[v + d] = shoup_lazy4(X + q4 - Y, wv, ws, q);
-          x[v] = Sx;
+          x[v + d] = shoup_lazy4n(X + q4 - Y, wv, ws, qneg);
+          x[v] = lazy_sub(X + Y, q4neg);
         }
       }
     }
@@ -469,7 +466,7 @@ __global__ void __launch_bounds__(256)
   // Inverse column stages of the P limbs; each limb is one line of src.
   for (uint32_t t = first; t < K; t += NL) {
     const uint32_t midx = L + t;
-    const uint64_t q = mc[midx].q, q4 = 4 * q;
+    const uint64_t q = mc[midx].q, q4 = 4 * q, qneg = mc[midx].neg_q, q4neg = mc[midx].neg_q4;
     const uint64_t* __restrict__ tw = tw_inv + (size_t)midx * N * 2;
     uint64_t* const line = src + (size_t)t * PITCH;
     uint64_t x[R];
@@ -497,10 +494,8 @@ __global__ void __launch_bounds__(256)
           const uint32_t ti = (1u << (S1 - 1 - beta)) | (u >> (beta + 1));
           const uint64_t wv = tw[2 * ti], ws = tw[2 * ti + 1];
           const uint64_t X = x[v], Y = x[v + d];
-          uint64_t Sx = X + Y;
-          Sx = Sx >= q4 ? Sx - q4 : Sx;
-          x[v + d] = shoup_lazy4(X + q4 - Y, wv, ws, q);
-          x[v] = Sx;
+          x[v + d] = shoup_lazy4n(X + q4 - Y, wv, ws, qneg);
+          x[v] = lazy_sub(X + Y, q4neg);
         }
       }
       if (sp == NSP - 1) {
@@ -525,6 +520,7 @@ __global__ void __launch_bounds__(256)
   uint64_t* const line = work + (size_t)first * PITCH;
   for (uint32_t k = first; k < nq; k += NL) {
     const uint64_t q = mc[k].q, q4 = 4 * q, qn = mc[k].qinv_neg;
+    const uint64_t qneg = mc[k].neg_q, q4neg = mc[k].neg_q4;
     const uint64_t* __restrict__ tw = tw_fwd + (size_t)k * N * 2;
     uint64_t x[R];
     {
@@ -580,9 +576,8 @@ __global__ void __launch_bounds__(256)
           const uint32_t u = thi | ((uint32_t)v << w) | tlo;
           const uint32_t ti = (1u << (S1 - 1 - beta)) | (u >> (beta + 1));
           const uint64_t wv = tw[2 * ti], ws = tw[2 * ti + 1];
-          uint64_t X = x[v];
-          X = X >= q4 ? X - q4 : X;
-          const uint64_t T = shoup_lazy4(x[v + d], wv, ws, q);
+          const uint64_t X = lazy_sub(x[v], q4neg);
+          const uint64_t T = shoup_lazy4n(x[v + d], wv, ws, qneg);
           x[v] = X + T;
           x[v + d] = X + q4 - T;
         }
