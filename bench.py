@@ -41,7 +41,11 @@ HBM_PEAK = 8.0e12  # B/s, MI355X HBM3E
 # WRITE_SIZE on this workload (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0, the factors
 # a plain copy of known size reads back); recorded in
 # profiles/rotation_step_n65536_l24.md together with the commands.
-MEASURED_TRAFFIC = {"ntt_fwd_blocks_moddown": 3_102_681_498 + 754_974_720}
+MEASURED_TRAFFIC = {
+    "ntt_fwd_blocks_moddown": 3_103_023_104 + 754_974_720,
+    "k_moddown_mid": 253_264_486 + 757_881_446,
+    "ntt_inv_blocks_ksk": 776_358_912 + 251_658_240,
+}
 LOG_N, DEPTH, SCALE_BITS, FIRST_BITS, DNUM = 16, 23, 59, 60, 3
 N = 1 << LOG_N
 LIMB = N * 8  # bytes per limb
@@ -526,32 +530,35 @@ def copy_probe(F) -> None:
 
 def step_kernel_bytes(L: int, K: int, R: int) -> dict:
     """Bytes each kernel of one rotation step must move (read + write once),
-    summed over its launches in the step.  R hoisted rotations, ne = L + K
-    extended limbs, alpha = ceil(L / dnum) limbs per digit:
+    summed over its launches in the step, for the three-launch ModDown used
+    at this ring dimension.  R hoisted rotations, ne = L + K extended limbs,
+    alpha = ceil(L / dnum) limbs per digit:
       ntt_inv_blocks_ksk      first inverse ModDown pass, fed by the P-limb
                               key inner product: digits dnum*K once per batch,
                               per rotation the key's P limbs dnum*2*K read and
                               2*K written;
+      k_moddown_mid           inverse column stages + conversion P -> Q +
+                              forward column stages: per rotation 2K read,
+                              2L written;
       ntt_fwd_blocks_moddown  last ModDown pass with the Q-limb inner product:
                               digits dnum*L and c0 L once per batch, per
                               rotation y 2L and the key's Q limbs dnum*2*L
                               read, output 2L written;
       k_convert               ModUp: dnum*ne (alpha read, ne-alpha written per
-                              digit); ModDown: per rotation 2K read, 2L written;
-      ntt_{fwd,inv}_{cols,blocks}  read + write of every limb of the pass:
-                              forward ModUp dnum*(ne-alpha) + ModDown R*2L
-                              (cols only), inverse blocks ModUp L, inverse
-                              cols ModUp L + ModDown R*2K."""
+                              digit);
+      ntt_{fwd,inv}_{cols,blocks}  ModUp: read + write of every limb of the
+                              pass, forward dnum*(ne-alpha), inverse L."""
     ne = L + K
     alpha = -(-L // DNUM)
     modup_fwd = DNUM * (ne - alpha)
     return {k: v * LIMB for k, v in {
         "ntt_inv_blocks_ksk": DNUM * K + R * (DNUM * 2 * K + 2 * K),
+        "k_moddown_mid": R * (2 * K + 2 * L),
         "ntt_fwd_blocks_moddown": DNUM * L + L + R * (2 * L + DNUM * 2 * L + 2 * L),
-        "k_convert": DNUM * ne + R * 2 * (K + L),
-        "ntt_fwd_cols": 2 * (modup_fwd + R * 2 * L),
+        "k_convert": DNUM * ne,
+        "ntt_fwd_cols": 2 * modup_fwd,
         "ntt_fwd_blocks": 2 * modup_fwd,
-        "ntt_inv_cols": 2 * (L + R * 2 * K),
+        "ntt_inv_cols": 2 * L,
         "ntt_inv_blocks": 2 * L,
     }.items()}
 

@@ -272,10 +272,49 @@ __device__ __forceinline__ uint32_t brev_bits(uint32_t x, uint32_t bits) {
   return __brev(x) >> (32 - bits);
 }
 
+// Key inner product sum_j d_j k_j reduced once by REDC (keys in Montgomery
+// form).  SPLIT (every modulus below 2^60, at most 7 digits): operands split
+// at bit 30 and accumulated carry-free in three 64-bit sums with
+// v_mad_u64_u32, T = a0 + a1 2^30 + a2 2^60; otherwise 128-bit products.
+template <int ND, bool SPLIT>
+__device__ __forceinline__ uint64_t key_dot(const uint64_t* dg, size_t dstride, const uint64_t* kr,
+                                            size_t kstride, uint32_t nd_rt, uint64_t q,
+                                            uint64_t qinv_neg) {
+  if constexpr (SPLIT && ND > 0 && ND <= 7) {
+    constexpr uint32_t M30 = (1u << 30) - 1;
+    uint64_t a0 = 0, a1 = 0, a2 = 0;
+#pragma unroll
+    for (int j = 0; j < ND; ++j) {
+      const uint64_t d = dg[j * dstride], k = kr[j * kstride];
+      const uint32_t dl = (uint32_t)d & M30, dh = (uint32_t)(d >> 30);
+      const uint32_t kl = (uint32_t)k & M30, kh = (uint32_t)(k >> 30);
+      a0 += (uint64_t)dl * kl;
+      a1 += (uint64_t)dl * kh;
+      a1 += (uint64_t)dh * kl;
+      a2 += (uint64_t)dh * kh;
+    }
+    const uint64_t m1 = a1 << 30, m2 = a2 << 60;
+    const uint64_t lo = a0 + m1;
+    uint64_t hi = (a1 >> 34) + (a2 >> 4) + (lo < m1);
+    const uint64_t lo2 = lo + m2;
+    hi += lo2 < m2;
+    return redc(hi, lo2, q, qinv_neg);
+  } else {
+    Acc128 acc;
+    if (ND > 0) {
+#pragma unroll
+      for (int j = 0; j < ND; ++j) acc.mac(dg[j * dstride], kr[j * kstride]);
+    } else {
+      for (uint32_t j = 0; j < nd_rt; ++j) acc.mac(dg[j * dstride], kr[j * kstride]);
+    }
+    return redc(acc.hi, acc.lo, q, qinv_neg);
+  }
+}
+
 // ModDown epilogue (see ModDownEpi): the value at evaluation slot s goes to
 // slot d(s) of the output, d being the inverse Galois permutation.  ND > 0
 // fixes the digit count at compile time (ND = 0: e.nd at run time).
-template <int ND>
+template <int ND, bool SPLIT = false>
 struct EpiStore {
   static constexpr bool kPre = true;
   const ModDownEpi& e;
@@ -286,14 +325,7 @@ struct EpiStore {
     const uint64_t* dg = e.digits[r] + (size_t)i * n + s;
     const uint64_t* kr = e.key[r] + (size_t)b * e.kl + (size_t)i * n + s;
     const size_t dstride = (size_t)e.ne * n, kstride = 2 * e.kl;
-    Acc128 acc;
-    if (ND > 0) {
-#pragma unroll
-      for (int j = 0; j < ND; ++j) acc.mac(dg[j * dstride], kr[j * kstride]);
-    } else {
-      for (uint32_t j = 0; j < e.nd; ++j) acc.mac(dg[j * dstride], kr[j * kstride]);
-    }
-    uint64_t t = redc(acc.hi, acc.lo, q, e.mc[i].qinv_neg);
+    uint64_t t = key_dot<ND, SPLIT>(dg, dstride, kr, kstride, e.nd, q, e.mc[i].qinv_neg);
     const uint64_t* add = e.add[r][b];
     if (add) t = add_mod(t, add[(size_t)i * n + s], q);
     return t;
@@ -331,7 +363,7 @@ constexpr int epilogue_rho() {
 
 // P-limb key inner product as the input of ModDown's inverse NTT: launch
 // poly p is key switch r = p / 2, component b = p % 2, limb t is P limb t.
-template <int ND>
+template <int ND, bool SPLIT = false>
 struct KskLoad {
   static constexpr bool kLoad = true;
   const ModDownEpi& e;
@@ -341,14 +373,7 @@ struct KskLoad {
     const uint64_t* dg = e.digits[r] + (size_t)(e.nq + t) * n + s;
     const uint64_t* kr = e.key[r] + (size_t)b * e.kl + (size_t)(e.L + t) * n + s;
     const size_t dstride = (size_t)e.ne * n, kstride = 2 * e.kl;
-    Acc128 acc;
-    if (ND > 0) {
-#pragma unroll
-      for (int j = 0; j < ND; ++j) acc.mac(dg[j * dstride], kr[j * kstride]);
-    } else {
-      for (uint32_t j = 0; j < e.nd; ++j) acc.mac(dg[j * dstride], kr[j * kstride]);
-    }
-    return redc(acc.hi, acc.lo, q, e.mc[e.L + t].qinv_neg);
+    return key_dot<ND, SPLIT>(dg, dstride, kr, kstride, e.nd, q, e.mc[e.L + t].qinv_neg);
   }
 };
 
@@ -373,26 +398,28 @@ __device__ __forceinline__ size_t blocked_off(uint32_t b, uint32_t u) {
 }
 
 // First inverse pass of ModDown (BLOCKS or SINGLE kind) fed by KskLoad.
-// BLK: BLOCKS pass that writes the blocked layout.
+// BLK: BLOCKS pass of the fused ModDown (moduli below 2^60), writing the
+// blocked layout.
 template <int S, int KIND, int ND, bool BLK>
 __global__ void __launch_bounds__(256)
     ntt_pass_ksk(uint64_t* __restrict__ data, size_t poly_stride, const ModConst* __restrict__ mc,
                  const uint64_t* __restrict__ tw_all, uint32_t log_n, uint32_t s_other,
                  int last, const ModDownEpi epi) {
-  ntt_body<S, KIND, true, epilogue_rho<S, KIND>(), PlainStore, KskLoad<ND>, LimbMap, false, BLK>(
-      data, poly_stride, mc, tw_all, log_n, LimbMap::contiguous(epi.L), s_other, last,
-      PlainStore{}, KskLoad<ND>{epi, 1u << log_n});
+  ntt_body<S, KIND, true, epilogue_rho<S, KIND>(), PlainStore, KskLoad<ND, BLK>, LimbMap, false,
+           BLK>(data, poly_stride, mc, tw_all, log_n, LimbMap::contiguous(epi.L), s_other, last,
+                PlainStore{}, KskLoad<ND, BLK>{epi, 1u << log_n});
 }
 
-// BLK: y is read from the blocked layout.
+// BLK: pass of the fused ModDown (moduli below 2^60), y read from the
+// blocked layout.
 template <int S, int KIND, int ND, bool BLK>
 __global__ void __launch_bounds__(256)
     ntt_pass_moddown(uint64_t* __restrict__ data, size_t poly_stride,
                      const ModConst* __restrict__ mc, const uint64_t* __restrict__ tw_all,
                      uint32_t log_n, uint32_t s_other, const ModDownEpi epi) {
-  ntt_body<S, KIND, false, epilogue_rho<S, KIND>(), EpiStore<ND>, PlainLoad, LimbMap, BLK>(
+  ntt_body<S, KIND, false, epilogue_rho<S, KIND>(), EpiStore<ND, BLK>, PlainLoad, LimbMap, BLK>(
       data, poly_stride, mc, tw_all, log_n, LimbMap::contiguous(0), s_other, 1,
-      EpiStore<ND>{epi, 1u << log_n, log_n});
+      EpiStore<ND, BLK>{epi, 1u << log_n, log_n});
 }
 
 // ---- Fused middle of a batched ModDown, ring dimensions 2^13 .. 2^17 ----
