@@ -439,7 +439,10 @@ __global__ void __launch_bounds__(256)
 // at a single barrier, once the converted sources are in LDS.  With one line
 // per wave the modulus, its twiddles and the conversion constants are
 // wavefront-uniform.  Stage order, twiddle indices and lazy ranges are those
-// of the column passes of ntt_body.
+// of the column passes of ntt_body.  Workgroups have NW waves: 4 for large
+// batches, 8 when a launch has too few (poly, column) tiles to fill the
+// chip, which halves each workgroup's serial line count and doubles the
+// waves in flight.
 
 template <int S1>
 constexpr uint32_t mid_pitch() {
@@ -449,9 +452,9 @@ template <int S1>
 constexpr int mid_lanes_per_line() {
   return (1 << S1) / 4 < 64 ? (1 << S1) / 4 : 64;
 }
-template <int S1>
-constexpr int mid_lines() {  // lines in flight per workgroup (4 waves)
-  return 4 * (64 / mid_lanes_per_line<S1>());
+template <int S1, int NW>
+constexpr int mid_lines() {  // lines in flight per workgroup of NW waves
+  return NW * (64 / mid_lanes_per_line<S1>());
 }
 
 // LDS writes of this wavefront before the call are seen by its reads after
@@ -463,14 +466,14 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-template <int S1, int S2>
-__global__ void __launch_bounds__(256)
+template <int S1, int S2, int NW>
+__global__ void __launch_bounds__(64 * NW)
     k_moddown_mid(const uint64_t* __restrict__ ext, uint64_t* __restrict__ y,
                   const ModConst* __restrict__ mc, const uint64_t* __restrict__ tw_inv,
                   const uint64_t* __restrict__ tw_fwd, const uint64_t* __restrict__ src_scale,
                   const uint64_t* __restrict__ qhat_mont, uint32_t K, uint32_t nq, uint32_t L) {
   constexpr int M = 1 << S1, TPL = mid_lanes_per_line<S1>(), R = M / TPL;
-  constexpr int RHO = R == 4 ? 2 : 3, LPW = 64 / TPL, NL = mid_lines<S1>();
+  constexpr int RHO = R == 4 ? 2 : 3, LPW = 64 / TPL, NL = mid_lines<S1, NW>();
   constexpr int NSP = (S1 + RHO - 1) / RHO;
   constexpr uint32_t PITCH = mid_pitch<S1>(), N2 = 1u << S2;
   constexpr size_t N = (size_t)M << S2;
@@ -722,16 +725,26 @@ void launch_ksk(Context& c, uint64_t* ext, uint32_t npoly, uint32_t s_other, boo
   }
 }
 
-template <int S1, int S2>
+template <int S1, int NW>
 size_t mid_lds_bytes(uint32_t K) {
-  return (size_t)(K + mid_lines<S1>()) * mid_pitch<S1>() * 8;
+  return (size_t)(K + mid_lines<S1, NW>()) * mid_pitch<S1>() * 8;
 }
+
+// Launches with fewer (poly, column) tiles than this use 8-wave workgroups.
+constexpr uint32_t MID_SMALL_TILES = 4096;
 
 template <int S1, int S2>
 void launch_mid(Context& c, const ConvPlan& pl, const uint64_t* ext, uint64_t* y,
                 uint32_t npoly, uint32_t nq) {
-  FHE_LAUNCH(c, "k_moddown_mid", (k_moddown_mid<S1, S2>), dim3(npoly << S2), dim3(256),
-             (mid_lds_bytes<S1, S2>(c.K)), ext, y, c.d_const, c.d_tw_inv, c.d_tw_fwd,
+  const uint32_t tiles = npoly << S2;
+  if (tiles < MID_SMALL_TILES && mid_lds_bytes<S1, 8>(c.K) <= 65536) {
+    FHE_LAUNCH(c, "k_moddown_mid", (k_moddown_mid<S1, S2, 8>), dim3(tiles), dim3(512),
+               (mid_lds_bytes<S1, 8>(c.K)), ext, y, c.d_const, c.d_tw_inv, c.d_tw_fwd,
+               pl.d_src_scale, pl.d_qhat_mont, c.K, nq, c.L);
+    return;
+  }
+  FHE_LAUNCH(c, "k_moddown_mid", (k_moddown_mid<S1, S2, 4>), dim3(tiles), dim3(256),
+             (mid_lds_bytes<S1, 4>(c.K)), ext, y, c.d_const, c.d_tw_inv, c.d_tw_fwd,
              pl.d_src_scale, pl.d_qhat_mont, c.K, nq, c.L);
 }
 
@@ -746,11 +759,9 @@ bool moddown_fused_ok(const Context& c, uint32_t nq) {
     if (c.mods[c.L + t] >= (1ull << 60)) return false;
   size_t lds = 0;
   switch (c.log_n) {
-    case 13: lds = mid_lds_bytes<7, 6>(c.K); break;
-    case 14: lds = mid_lds_bytes<7, 7>(c.K); break;
-    case 15: lds = mid_lds_bytes<8, 7>(c.K); break;
-    case 16: lds = mid_lds_bytes<8, 8>(c.K); break;
-    default: lds = mid_lds_bytes<9, 8>(c.K); break;
+    case 13: case 14: lds = mid_lds_bytes<7, 4>(c.K); break;
+    case 15: case 16: lds = mid_lds_bytes<8, 4>(c.K); break;
+    default: lds = mid_lds_bytes<9, 4>(c.K); break;
   }
   return lds <= 65536;
 }

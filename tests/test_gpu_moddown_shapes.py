@@ -50,21 +50,41 @@ def test_hoisted_rotations(setup):
 
 
 def test_benchmark_shape_rotations():
-    """Two hoisted rotations and one single rotation one level down at the
-    benchmark's parameters (the shape its timed step runs)."""
+    """Eight hoisted rotations (16 polys x 256 columns: the 4-wave middle
+    kernel) and one single rotation one level down (the 8-wave one) at the
+    benchmark's parameters."""
     q, p = O.gen_moduli(16, 23, 59, 60, 3)
     ctx, orc = F.Context(16, q, p, 3), O.Ctx(16, q, p, 3)
     assert (ctx.L, ctx.K) == (24, 8)
     s = orc.secret(5)
-    gal = [O.galois_elt(r, ctx.n) for r in (1, -4096)]
-    keys = [orc.galois_key(s, g, 31 + i) for i, g in enumerate(gal)]
-    dkeys = [ctx.load_key(k) for k in keys]
+    gal = [O.galois_elt(r, ctx.n) for r in (1, -4096, 5, 2 * ctx.n - 1)]
+    gal = gal + gal[::-1]
+    keys = {g: orc.galois_key(s, g, 31 + i) for i, g in enumerate(dict.fromkeys(gal))}
+    dkeys = {g: ctx.load_key(k) for g, k in keys.items()}
     rng = np.random.default_rng(6)
     ct = residues(rng, ctx.q, (2,), ctx.n)
     dct = ctx.upload(ct)
-    outs = ctx.rotate_hoisted(dct, ctx.rotation_precompute(dct), dkeys, gal)
+    outs = ctx.rotate_hoisted(dct, ctx.rotation_precompute(dct), [dkeys[g] for g in gal], gal)
+    want = {g: orc.rotate(ct, keys[g], g) for g in keys}
+    for out, g in zip(outs, gal):
+        assert np.array_equal(out.numpy(), want[g]), g
+    low = residues(rng, ctx.q[:ctx.L - 1], (2,), ctx.n)
+    got = ctx.rotate(ctx.upload(low), dkeys[gal[0]], gal[0]).numpy()
+    assert np.array_equal(got, orc.rotate(low, keys[gal[0]], gal[0]))
+
+
+def test_full_batch_small_ring():
+    """32 hoisted rotations at N=2^13 (64 polys x 64 columns: the 4-wave
+    middle kernel with two column lines per wavefront)."""
+    q, p = O.gen_moduli(13, 7, 50, 60, 2)
+    ctx, orc = F.Context(13, q, p, 2), O.Ctx(13, q, p, 2)
+    s = orc.secret(8)
+    steps = list(range(1, 17)) + [-r for r in range(1, 17)]
+    gal = [O.galois_elt(r, ctx.n) for r in steps]
+    keys = [orc.galois_key(s, g, 200 + i) for i, g in enumerate(gal)]
+    ct = residues(np.random.default_rng(9), ctx.q, (2,), ctx.n)
+    dct = ctx.upload(ct)
+    outs = ctx.rotate_hoisted(dct, ctx.rotation_precompute(dct),
+                              [ctx.load_key(k) for k in keys], gal)
     for out, key, g in zip(outs, keys, gal):
         assert np.array_equal(out.numpy(), orc.rotate(ct, key, g)), g
-    low = residues(rng, ctx.q[:ctx.L - 1], (2,), ctx.n)
-    got = ctx.rotate(ctx.upload(low), dkeys[0], gal[0]).numpy()
-    assert np.array_equal(got, orc.rotate(low, keys[0], gal[0]))
