@@ -61,11 +61,28 @@ struct PlainLoad {
   __device__ __forceinline__ uint64_t get(size_t, uint64_t) const { return 0; }
 };
 
+// LDS writes of this wavefront before the call are seen by its reads after
+// the call (LDS executes a wavefront's instructions in order; this keeps the
+// compiler from moving accesses across).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // BLK_IN / BLK_OUT (BLOCKS kind): the first pass's input / the last pass's
 // output uses the blocked layout described with blocked_off below.  A
 // workgroup's tile then still occupies the words [wg0, wg0 + LINES * LEN),
 // in the order p = u * LINES + line, and is staged through LDS whatever the
 // window.
+//
+// BLOCKS launches keep every line inside one wavefront (TPL <= 64 lanes, LPW
+// = 64 / TPL lines per wave), so their sub-passes exchange through LDS with
+// wavefront-level ordering only, and staging of a contiguous window is done
+// per wavefront over its own lines (p = wave * 64R + k * 64 + lane, one
+// 512-byte run per instruction).  Only blocked-layout staging, which
+// interleaves the lines of the whole workgroup word by word, keeps a
+// workgroup barrier.
 template <int S, int KIND, bool INV, int RHO_, class Store, class Load = PlainLoad,
           class Map = LimbMap, bool BLK_IN = false, bool BLK_OUT = false>
 __device__ __forceinline__ void ntt_body(uint64_t* __restrict__ data, size_t poly_stride,
@@ -102,6 +119,17 @@ __device__ __forceinline__ void ntt_body(uint64_t* __restrict__ data, size_t pol
   }
   const uint32_t gline = blockIdx.x * LINES + line;
   const uint32_t twbase = KIND == BLOCKS ? (1u << s_other) + gline : 1u;
+  constexpr bool WL = KIND == BLOCKS;
+  static_assert(!WL || G::TPL <= 64, "a block line spans one wavefront");
+  // Staged position k of this thread: per wavefront (WL) or per workgroup.
+  auto staged = [&](int k) -> uint32_t {
+    return WL ? (tid >> 6) * (64u * R) + (uint32_t)k * 64u + (tid & 63)
+              : (uint32_t)k * blockDim.x + tid;
+  };
+  auto sync_lines = [&]() {
+    if (WL) wave_lds_sync();
+    else __syncthreads();
+  };
 
   uint64_t x[R];
   uint64_t pre[Store::kPre ? R : 1];
@@ -132,12 +160,13 @@ __device__ __forceinline__ void ntt_body(uint64_t* __restrict__ data, size_t pol
       const size_t wg0 = ((size_t)blockIdx.x * LINES) << S;
 #pragma unroll
       for (int k = 0; k < R; ++k) {
-        const uint32_t p = k * blockDim.x + tid;
+        const uint32_t p = BLK_IN ? (uint32_t)k * blockDim.x + tid : staged(k);
         const uint32_t li = BLK_IN ? lds_idx(p % LINES, p / LINES, G::PITCH)
                                    : lds_idx(p >> S, p & (G::LEN - 1), G::PITCH);
         lds[li] = Load::kLoad ? load.get(wg0 + p, q) : base[wg0 + p];
       }
-      __syncthreads();
+      if (BLK_IN) __syncthreads();
+      else sync_lines();
 #pragma unroll
       for (int v = 0; v < R; ++v) {
         const uint32_t u = thi | ((uint32_t)v << w) | tlo;
@@ -151,7 +180,7 @@ __device__ __forceinline__ void ntt_body(uint64_t* __restrict__ data, size_t pol
         x[v] = Load::kLoad ? load.get(g, q) : base[g];
       }
     } else {
-      __syncthreads();
+      sync_lines();
 #pragma unroll
       for (int v = 0; v < R; ++v) {
         const uint32_t u = thi | ((uint32_t)v << w) | tlo;
@@ -168,7 +197,7 @@ __device__ __forceinline__ void ntt_body(uint64_t* __restrict__ data, size_t pol
 #pragma unroll
       for (int k = 0; k < R; ++k) {
         const uint32_t u = thi | ((uint32_t)k << w) | tlo;
-        const size_t g = kFinalContig ? wg0 + (size_t)k * blockDim.x + tid
+        const size_t g = kFinalContig ? wg0 + staged(k)
                          : KIND == COLS ? gline + ((size_t)u << s_other)
                                         : ((size_t)gline << S) + u;
         pre[Store::kPre ? k : 0] = store.pre(g, q);
@@ -220,17 +249,18 @@ __device__ __forceinline__ void ntt_body(uint64_t* __restrict__ data, size_t pol
         }
       }
       if (contiguous || BLK_OUT) {
-        if (sp > 0 || NSP == 1) __syncthreads();
+        if (sp > 0 || NSP == 1) sync_lines();
 #pragma unroll
         for (int v = 0; v < R; ++v) {
           const uint32_t u = thi | ((uint32_t)v << w) | tlo;
           lds[lds_idx(line, u, G::PITCH)] = x[v];
         }
-        __syncthreads();
+        if (BLK_OUT) __syncthreads();
+        else sync_lines();
         const size_t wg0 = ((size_t)blockIdx.x * LINES) << S;
 #pragma unroll
         for (int k = 0; k < R; ++k) {
-          const uint32_t p = k * blockDim.x + tid;
+          const uint32_t p = BLK_OUT ? (uint32_t)k * blockDim.x + tid : staged(k);
           const uint32_t li = BLK_OUT ? lds_idx(p % LINES, p / LINES, G::PITCH)
                                       : lds_idx(p >> S, p & (G::LEN - 1), G::PITCH);
           store.fin(base, wg0 + p, lds[li], pre[Store::kPre ? k : 0], q);
@@ -245,7 +275,7 @@ __device__ __forceinline__ void ntt_body(uint64_t* __restrict__ data, size_t pol
         }
       }
     } else {
-      if (sp > 0 || (KIND != COLS && INV)) __syncthreads();
+      if (sp > 0 || (KIND != COLS && INV)) sync_lines();
 #pragma unroll
       for (int v = 0; v < R; ++v) {
         const uint32_t u = thi | ((uint32_t)v << w) | tlo;
@@ -455,15 +485,6 @@ constexpr int mid_lanes_per_line() {
 template <int S1, int NW>
 constexpr int mid_lines() {  // lines in flight per workgroup of NW waves
   return NW * (64 / mid_lanes_per_line<S1>());
-}
-
-// LDS writes of this wavefront before the call are seen by its reads after
-// the call (LDS executes a wavefront's instructions in order; this keeps the
-// compiler from moving accesses across).
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 template <int S1, int S2, int NW>
