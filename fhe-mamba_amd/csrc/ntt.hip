@@ -58,6 +58,8 @@ __device__ __forceinline__ uint32_t lds_idx(uint32_t line, uint32_t u, uint32_t 
 // of data when Load::kLoad.
 struct PlainLoad {
   static constexpr bool kLoad = false;
+  static constexpr bool kPair = false;
+  __device__ __forceinline__ void get2(size_t, uint64_t, uint64_t&, uint64_t&) const {}
   __device__ __forceinline__ uint64_t get(size_t, uint64_t) const { return 0; }
 };
 
@@ -122,7 +124,13 @@ __device__ __forceinline__ void ntt_body(uint64_t* __restrict__ data, size_t pol
   constexpr bool WL = KIND == BLOCKS;
   static_assert(!WL || G::TPL <= 64, "a block line spans one wavefront");
   // Staged position k of this thread: per wavefront (WL) or per workgroup.
+  // PAIR: the per-position store terms or loads come two adjacent positions
+  // per lane (16-byte accesses): staged position k is then
+  // wave * 64R + (k / 2) * 128 + 2 * lane + k % 2.
+  constexpr bool PAIR = WL && (Store::kPair || Load::kPair);
   auto staged = [&](int k) -> uint32_t {
+    if (PAIR)
+      return (tid >> 6) * (64u * R) + (uint32_t)(k >> 1) * 128u + 2 * (tid & 63) + (k & 1);
     return WL ? (tid >> 6) * (64u * R) + (uint32_t)k * 64u + (tid & 63)
               : (uint32_t)k * blockDim.x + tid;
   };
@@ -158,12 +166,23 @@ __device__ __forceinline__ void ntt_body(uint64_t* __restrict__ data, size_t pol
 
     if (sp == 0 && (contiguous || BLK_IN)) {
       const size_t wg0 = ((size_t)blockIdx.x * LINES) << S;
+      if constexpr (Load::kPair && PAIR && !BLK_IN) {
 #pragma unroll
-      for (int k = 0; k < R; ++k) {
-        const uint32_t p = BLK_IN ? (uint32_t)k * blockDim.x + tid : staged(k);
-        const uint32_t li = BLK_IN ? lds_idx(p % LINES, p / LINES, G::PITCH)
-                                   : lds_idx(p >> S, p & (G::LEN - 1), G::PITCH);
-        lds[li] = Load::kLoad ? load.get(wg0 + p, q) : base[wg0 + p];
+        for (int k = 0; k < R; k += 2) {
+          const uint32_t p = staged(k);
+          uint64_t v0, v1;
+          load.get2(wg0 + p, q, v0, v1);
+          lds[lds_idx(p >> S, p & (G::LEN - 1), G::PITCH)] = v0;
+          lds[lds_idx((p + 1) >> S, (p + 1) & (G::LEN - 1), G::PITCH)] = v1;
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < R; ++k) {
+          const uint32_t p = BLK_IN ? (uint32_t)k * blockDim.x + tid : staged(k);
+          const uint32_t li = BLK_IN ? lds_idx(p % LINES, p / LINES, G::PITCH)
+                                     : lds_idx(p >> S, p & (G::LEN - 1), G::PITCH);
+          lds[li] = Load::kLoad ? load.get(wg0 + p, q) : base[wg0 + p];
+        }
       }
       if (BLK_IN) __syncthreads();
       else sync_lines();
@@ -194,13 +213,18 @@ __device__ __forceinline__ void ntt_body(uint64_t* __restrict__ data, size_t pol
     constexpr bool kFinalContig = !INV && KIND != COLS;
     if (Store::kPre && last && sp == (kFinalContig ? 0 : NSP - 1)) {
       const size_t wg0 = ((size_t)blockIdx.x * LINES) << S;
+      if constexpr (Store::kPair && PAIR && kFinalContig) {
 #pragma unroll
-      for (int k = 0; k < R; ++k) {
-        const uint32_t u = thi | ((uint32_t)k << w) | tlo;
-        const size_t g = kFinalContig ? wg0 + staged(k)
-                         : KIND == COLS ? gline + ((size_t)u << s_other)
-                                        : ((size_t)gline << S) + u;
-        pre[Store::kPre ? k : 0] = store.pre(g, q);
+        for (int k = 0; k < R; k += 2) store.pre2(wg0 + staged(k), q, pre[k], pre[k + 1]);
+      } else {
+#pragma unroll
+        for (int k = 0; k < R; ++k) {
+          const uint32_t u = thi | ((uint32_t)k << w) | tlo;
+          const size_t g = kFinalContig ? wg0 + staged(k)
+                           : KIND == COLS ? gline + ((size_t)u << s_other)
+                                          : ((size_t)gline << S) + u;
+          pre[Store::kPre ? k : 0] = store.pre(g, q);
+        }
       }
     }
 
@@ -291,6 +315,8 @@ __device__ __forceinline__ void ntt_body(uint64_t* __restrict__ data, size_t pol
 // butterflies; fin then writes f(y, t).
 struct PlainStore {
   static constexpr bool kPre = false;
+  static constexpr bool kPair = false;
+  __device__ __forceinline__ void pre2(size_t, uint64_t, uint64_t&, uint64_t&) const {}
   __device__ __forceinline__ uint64_t pre(size_t, uint64_t) const { return 0; }
   __device__ __forceinline__ void fin(uint64_t* base, size_t g, uint64_t v, uint64_t,
                                       uint64_t) const {
@@ -341,14 +367,69 @@ __device__ __forceinline__ uint64_t key_dot(const uint64_t* dg, size_t dstride, 
   }
 }
 
+// key_dot for positions s and s + 1 (s even, operands 16-byte aligned) with
+// 16-byte loads, in the SPLIT form only (every modulus below 2^60, 1..7
+// digits): half the load instructions of two key_dot calls.
+template <int ND>
+__device__ __forceinline__ void key_dot2(const uint64_t* dg, size_t dstride, const uint64_t* kr,
+                                         size_t kstride, uint64_t q, uint64_t qinv_neg,
+                                         uint64_t& t0, uint64_t& t1) {
+  static_assert(ND > 0 && ND <= 7, "split key products");
+  constexpr uint32_t M30 = (1u << 30) - 1;
+  uint64_t a0[2] = {0, 0}, a1[2] = {0, 0}, a2[2] = {0, 0};
+#pragma unroll
+  for (int j = 0; j < ND; ++j) {
+    const ulonglong2 dv = *reinterpret_cast<const ulonglong2*>(dg + j * dstride);
+    const ulonglong2 kv = *reinterpret_cast<const ulonglong2*>(kr + j * kstride);
+    const uint64_t dd[2] = {dv.x, dv.y}, kk[2] = {kv.x, kv.y};
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t dl = (uint32_t)dd[h] & M30, dh = (uint32_t)(dd[h] >> 30);
+      const uint32_t kl = (uint32_t)kk[h] & M30, kh = (uint32_t)(kk[h] >> 30);
+      a0[h] += (uint64_t)dl * kl;
+      a1[h] += (uint64_t)dl * kh;
+      a1[h] += (uint64_t)dh * kl;
+      a2[h] += (uint64_t)dh * kh;
+    }
+  }
+  uint64_t t[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint64_t m1 = a1[h] << 30, m2 = a2[h] << 60;
+    const uint64_t lo = a0[h] + m1;
+    uint64_t hi = (a1[h] >> 34) + (a2[h] >> 4) + (lo < m1);
+    const uint64_t lo2 = lo + m2;
+    hi += lo2 < m2;
+    t[h] = redc(hi, lo2, q, qinv_neg);
+  }
+  t0 = t[0];
+  t1 = t[1];
+}
+
 // ModDown epilogue (see ModDownEpi): the value at evaluation slot s goes to
 // slot d(s) of the output, d being the inverse Galois permutation.  ND > 0
 // fixes the digit count at compile time (ND = 0: e.nd at run time).
 template <int ND, bool SPLIT = false>
 struct EpiStore {
   static constexpr bool kPre = true;
+  static constexpr bool kPair = SPLIT && ND > 0 && ND <= 7;
   const ModDownEpi& e;
   uint32_t n, log_n;
+  // pre() for positions s and s + 1 (s even), kPair only.
+  __device__ __forceinline__ void pre2(size_t s, uint64_t q, uint64_t& t0, uint64_t& t1) const {
+    if constexpr (kPair) {
+      const uint32_t p = blockIdx.y, r = p >> 1, b = p & 1, i = blockIdx.z;
+      key_dot2<ND>(e.digits[r] + (size_t)i * n + s, (size_t)e.ne * n,
+                   e.key[r] + (size_t)b * e.kl + (size_t)i * n + s, 2 * e.kl, q,
+                   e.mc[i].qinv_neg, t0, t1);
+      const uint64_t* add = e.add[r][b];
+      if (add) {
+        const ulonglong2 av = *reinterpret_cast<const ulonglong2*>(add + (size_t)i * n + s);
+        t0 = add_mod(t0, av.x, q);
+        t1 = add_mod(t1, av.y, q);
+      }
+    }
+  }
   // Q-limb key inner product plus the addend at position s.
   __device__ __forceinline__ uint64_t pre(size_t s, uint64_t q) const {
     const uint32_t p = blockIdx.y, r = p >> 1, b = p & 1, i = blockIdx.z;
@@ -396,6 +477,7 @@ constexpr int epilogue_rho() {
 template <int ND, bool SPLIT = false>
 struct KskLoad {
   static constexpr bool kLoad = true;
+  static constexpr bool kPair = SPLIT && ND > 0 && ND <= 7;
   const ModDownEpi& e;
   uint32_t n;
   __device__ __forceinline__ uint64_t get(size_t s, uint64_t q) const {
@@ -404,6 +486,15 @@ struct KskLoad {
     const uint64_t* kr = e.key[r] + (size_t)b * e.kl + (size_t)(e.L + t) * n + s;
     const size_t dstride = (size_t)e.ne * n, kstride = 2 * e.kl;
     return key_dot<ND, SPLIT>(dg, dstride, kr, kstride, e.nd, q, e.mc[e.L + t].qinv_neg);
+  }
+  // get() for positions s and s + 1 (s even), kPair only.
+  __device__ __forceinline__ void get2(size_t s, uint64_t q, uint64_t& v0, uint64_t& v1) const {
+    if constexpr (kPair) {
+      const uint32_t p = blockIdx.y, r = p >> 1, b = p & 1, t = blockIdx.z;
+      key_dot2<ND>(e.digits[r] + (size_t)(e.nq + t) * n + s, (size_t)e.ne * n,
+                   e.key[r] + (size_t)b * e.kl + (size_t)(e.L + t) * n + s, 2 * e.kl, q,
+                   e.mc[e.L + t].qinv_neg, v0, v1);
+    }
   }
 };
 
