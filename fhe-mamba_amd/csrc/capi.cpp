@@ -700,6 +700,15 @@ int fhe_keygen_secret(fhe_context* ctx, uint64_t seed, int64_t* s_coef) {
   });
 }
 
+int fhe_keygen_secret_sparse(fhe_context* ctx, uint64_t seed, uint32_t h, int64_t* s_coef) {
+  return guard([&] {
+    need(ctx && s_coef, "null argument");
+    need(h >= 1 && h <= ctx->c->n, "sparse secret: Hamming weight must be in [1, N]");
+    fhe::sample_sparse_ternary_host(fhe::stream_key(seed, fhe::TAG_SECRET, 0), s_coef,
+                                    ctx->c->n, h);
+  });
+}
+
 int fhe_keygen_public(fhe_context* ctx, const int64_t* s_coef, uint64_t seed, fhe_poly* pk) {
   return guard([&] {
     need(ctx && s_coef && pk && pk->c == ctx->c, "null argument");

@@ -106,6 +106,9 @@ void signed_small_to_eval(Context& c, const std::vector<int64_t>& coef, uint32_t
 }  // namespace
 
 void sample_ternary_host(uint64_t key, int64_t* out, uint32_t n) { sample_ternary(key, out, n); }
+void sample_sparse_ternary_host(uint64_t key, int64_t* out, uint32_t n, uint32_t h) {
+  sample_sparse_ternary(key, out, n, h);
+}
 
 void signed_to_eval(Context& c, const int64_t* coef_host, uint32_t idx0, uint32_t nlimb,
                     uint64_t* out) {

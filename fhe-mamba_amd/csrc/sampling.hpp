@@ -8,6 +8,10 @@
 //   stream(s,t,i)  = fmix64(s ^ fmix64((t << 32) ^ i ^ 0x5851F42D4C957F2D))
 //   uniform mod q  = floor((draw(2i) * 2^64 + draw(2i+1)) * q / 2^128)
 //   ternary        = {0, 1, -1}[draw(i) mod 3]
+//   sparse ternary = h nonzeros: for i < h, swap position i with position
+//                    i + floor(draw(2i) (n - i) / 2^64) of 0..n-1 (partial
+//                    Fisher-Yates), then that position gets
+//                    (draw(2i+1) & 1) ? -1 : 1
 //   error          = popcount(d & 0x1FFFFF) - popcount((d >> 21) & 0x1FFFFF)
 //                    (centred binomial, eta = 21, sigma ~ 3.24, in place of
 //                    OpenFHE's discrete Gaussian with sigma 3.19)
@@ -56,6 +60,23 @@ inline void sample_ternary(uint64_t key, int64_t* out, uint32_t n) {
     const uint64_t d = draw(key, i) % 3;
     out[i] = d == 0 ? 0 : (d == 1 ? 1 : -1);
   }
+}
+
+// Exactly h nonzero coefficients, each +-1 (1 <= h <= n).
+inline void sample_sparse_ternary(uint64_t key, int64_t* out, uint32_t n, uint32_t h) {
+  uint32_t* idx = new uint32_t[n];
+  for (uint32_t i = 0; i < n; ++i) {
+    idx[i] = i;
+    out[i] = 0;
+  }
+  for (uint32_t i = 0; i < h; ++i) {
+    const uint32_t j = i + (uint32_t)mulhi64(draw(key, 2 * (uint64_t)i), n - i);
+    const uint32_t t = idx[i];
+    idx[i] = idx[j];
+    idx[j] = t;
+    out[idx[i]] = (draw(key, 2 * (uint64_t)i + 1) & 1) ? -1 : 1;
+  }
+  delete[] idx;
 }
 
 inline void sample_cbd(uint64_t key, int64_t* out, uint32_t n) {

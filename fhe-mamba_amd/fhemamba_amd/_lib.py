@@ -81,6 +81,7 @@ SIGNATURES = {
     "fhe_encode": [_p, _p, _p, _u32, _u32, _dbl, _u32, _p],
     "fhe_decode": [_p, _p, _u32, _dbl, _p, _p],
     "fhe_keygen_secret": [_p, _u64, _p],
+    "fhe_keygen_secret_sparse": [_p, _u64, _u32, _p],
     "fhe_keygen_public": [_p, _p, _u64, _p],
     "fhe_keygen_relin": [_p, _p, _u64, _pp],
     "fhe_keygen_galois": [_p, _p, _u32, _u64, _pp],

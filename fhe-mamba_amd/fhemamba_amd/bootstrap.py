@@ -217,22 +217,33 @@ def uniform_ternary_bound(ring_dim: int) -> float:
     return float(1 << math.ceil(math.log2(8.0 * math.sqrt(ring_dim / 18.0))))
 
 
+def secret_bound(hamming_weight: float) -> float:
+    """K for a secret with `hamming_weight` nonzero +-1 coefficients: I is a
+    sum of hamming_weight + 1 terms uniform in [-1/2, 1/2], standard
+    deviation sqrt((h + 1) / 12); K covers 8 of them (h = 2N/3 gives
+    uniform_ternary_bound; h = 192 gives 64)."""
+    return float(1 << math.ceil(math.log2(8.0 * math.sqrt((hamming_weight + 1.0) / 12.0))))
+
+
 NOISE_MODEL_OFFSET_BITS = 4.0
 
 
 def correction_bits_for(ring_dim: int, sine: SineApprox, in_scale: float, q0: float,
-                        scale: float, slots: int = 0) -> int:
+                        scale: float, slots: int = 0, hamming_weight: float = 0.0) -> int:
     """Scale-down c (the message enters ModRaise times 2^-c) balancing the
     two errors of one bootstrap, in message units for a coefficient of size 1:
-      * noise: rescale / key-switch rounding of about N / sqrt(18) per
-        coefficient (uniform ternary secret) at the working scale, times K
-        (v = u / K), 2^r (double angles), sqrt(slots) (SlotToCoeff gain) and
-        q0 / (2 pi in_scale) (the way back), all times 2^c; the offset
-        NOISE_MODEL_OFFSET_BITS is measured (N = 2^12 and 2^16, 59-bit scale);
+      * noise: rescale / key-switch rounding of about sqrt(N h / 12) per
+        coefficient (h nonzero secret coefficients; N / sqrt(18) for a
+        uniform-ternary secret, h = 2N/3, the default) at the working scale,
+        times K (v = u / K), 2^r (double angles), sqrt(slots) (SlotToCoeff
+        gain) and q0 / (2 pi in_scale) (the way back), all times 2^c; the
+        offset NOISE_MODEL_OFFSET_BITS is measured (N = 2^12 and 2^16,
+        59-bit scale, uniform ternary);
       * the sine's cubic term: (2 pi a)^2 / 6 relative, a = 2^-c in_scale / q0.
     Equal at 3c = log2((2 pi rho)^2 / 6) - e0, rho = in_scale / q0."""
     rho = in_scale / q0
-    e0 = (math.log2(ring_dim / math.sqrt(18.0) / scale) + math.log2(sine.K) + sine.r
+    h = float(hamming_weight) or 2.0 * ring_dim / 3.0
+    e0 = (math.log2(math.sqrt(ring_dim * h / 12.0) / scale) + math.log2(sine.K) + sine.r
           + 0.5 * math.log2(slots or ring_dim // 2)
           + math.log2(q0 / (2 * math.pi * in_scale))
           + NOISE_MODEL_OFFSET_BITS)
@@ -245,19 +256,23 @@ class BootstrapConfig:
     level_budget: tuple = (3, 3)
     correction_bits: int = 0            # 0: chosen by correction_bits_for()
     sine: SineApprox = field(default_factory=lambda: SineApprox(K=128.0, r=5, degree=59))
+    hamming_weight: float = 0.0         # nonzero secret coefficients; 0: uniform ternary
 
     @classmethod
-    def for_ring(cls, ring_dim: int, level_budget=(3, 3), correction_bits: int = 0):
-        """K from the secret's bound; r double angles bring the interpolated
-        cosine down to K / 2^r = 4 periods over [-K, K] (degree 59) or 8
-        (degree 89) for the larger rings."""
-        K = uniform_ternary_bound(ring_dim)
+    def for_ring(cls, ring_dim: int, level_budget=(3, 3), correction_bits: int = 0,
+                 hamming_weight: float = 0.0):
+        """K from the secret's bound (uniform ternary unless hamming_weight
+        is given); r double angles bring the interpolated cosine down to
+        K / 2^r = 4 periods over [-K, K] (degree 59) or 8 (degree 89) for
+        the larger K."""
+        h = float(hamming_weight) or 2.0 * ring_dim / 3.0
+        K = secret_bound(h)
         if K <= 128:
             sine = SineApprox(K=K, r=max(0, int(math.log2(K)) - 2), degree=59)
         else:
             sine = SineApprox(K=K, r=int(math.log2(K)) - 3, degree=89)
         return cls(level_budget=tuple(level_budget), correction_bits=int(correction_bits),
-                   sine=sine)
+                   sine=sine, hamming_weight=h)
 
 
 class CKKSBootstrapper:
@@ -305,7 +320,8 @@ class CKKSBootstrapper:
     def correction_bits(self, in_scale: float, q0: float, scale: float) -> int:
         if self.cfg.correction_bits:
             return self.cfg.correction_bits
-        return correction_bits_for(self.N, self.cfg.sine, in_scale, q0, scale, self.n)
+        return correction_bits_for(self.N, self.cfg.sine, in_scale, q0, scale, self.n,
+                                   self.cfg.hamming_weight)
 
     # --------------------------------------------------------------- helpers
     def _group_pts(self, which: str, idx: int, plan: GroupPlan, level: int, factor: float):

@@ -68,6 +68,10 @@ class SecretKeyDist(enum.Enum):
     SPARSE_TERNARY = 2
 
 
+# Nonzero coefficients of a SPARSE_TERNARY secret (+-1 each, the rest 0).
+SPARSE_HAMMING_WEIGHT = 192
+
+
 class SecurityLevel(enum.Enum):
     HEStd_128_classic = 0
     HEStd_192_classic = 1
@@ -157,8 +161,8 @@ def select_chain(params: CCParamsCKKSRNS):
         raise NotImplementedError("only HYBRID key switching is implemented")
     if g["ScalingTechnique"] != ScalingTechnique.FLEXIBLEAUTO:
         raise NotImplementedError("only FLEXIBLEAUTO scaling is implemented")
-    if g["SecretKeyDist"] != SecretKeyDist.UNIFORM_TERNARY:
-        raise NotImplementedError("only UNIFORM_TERNARY secrets are implemented")
+    if g["SecretKeyDist"] not in (SecretKeyDist.UNIFORM_TERNARY, SecretKeyDist.SPARSE_TERNARY):
+        raise NotImplementedError("only UNIFORM_TERNARY and SPARSE_TERNARY secrets are implemented")
     depth, sbits, fbits = (int(g["MultiplicativeDepth"]), int(g["ScalingModSize"]),
                            int(g["FirstModSize"]))
     if depth < 0 or not 20 <= sbits <= 60 or not sbits <= fbits <= 60:
@@ -221,6 +225,7 @@ class CryptoContext:
         self._draws = 0
         self._cache: dict = {}
         self._boot = None
+        self._secret_dist = g["SecretKeyDist"]
 
     # ------------------------------------------------------------ set-up
     def _next_seed(self) -> int:
@@ -253,8 +258,19 @@ class CryptoContext:
         return self._ctx
 
     # ------------------------------------------------------------ keys
+    def secret_hamming_weight(self) -> float:
+        """Expected number of nonzero secret coefficients: h for a sparse
+        secret, 2N/3 for a uniform-ternary one."""
+        if self._secret_dist == SecretKeyDist.SPARSE_TERNARY:
+            return float(SPARSE_HAMMING_WEIGHT)
+        return 2.0 * self.n / 3.0
+
     def KeyGen(self) -> "KeyPair":  # noqa: N802
-        s = self._ctx.keygen_secret(self._next_seed())
+        if self._secret_dist == SecretKeyDist.SPARSE_TERNARY:
+            s = self._ctx.keygen_secret_sparse(self._next_seed(),
+                                               min(SPARSE_HAMMING_WEIGHT, self.n))
+        else:
+            s = self._ctx.keygen_secret(self._next_seed())
         sk = PrivateKey(self, s)
         pk = PublicKey(self, self._ctx.keygen_public(s, self._next_seed()))
         return KeyPair(pk, sk)
@@ -715,7 +731,8 @@ class CryptoContext:
         from .bootstrap import BootstrapConfig, CKKSBootstrapper
         slots = int(slots) or self._slots
         cfg = BootstrapConfig.for_ring(self.n, tuple(int(b) for b in levelBudget),
-                                       int(correctionFactor))
+                                       int(correctionFactor),
+                                       hamming_weight=self.secret_hamming_weight())
         self._boot = CKKSBootstrapper(self, cfg, slots)
 
     def _bootstrapper(self):

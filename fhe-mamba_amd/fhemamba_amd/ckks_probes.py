@@ -197,15 +197,16 @@ class CkksPrimitives:
 
 
 def build_toy_context(*, ring_dimension, batch, depth, scale_bits, first_mod_bits,
-                      rotations=(), backend=None, seed=None):
-    """CKKS context with TOY security for probes: uniform-ternary secret,
-    FLEXIBLEAUTO, HYBRID, explicit ring dimension and batch; keys for
-    multiplication and the given rotations.  `backend` is any module with
-    the OpenFHE names (default: fhemamba_amd.ckks)."""
+                      rotations=(), backend=None, seed=None, secret_dist=None):
+    """CKKS context with TOY security for probes: uniform-ternary secret
+    (unless `secret_dist` names another SecretKeyDist member), FLEXIBLEAUTO,
+    HYBRID, explicit ring dimension and batch; keys for multiplication and
+    the given rotations.  `backend` is any module with the OpenFHE names
+    (default: fhemamba_amd.ckks)."""
     if backend is None:
         from . import ckks as backend
     params = backend.CCParamsCKKSRNS()
-    params.SetSecretKeyDist(backend.SecretKeyDist.UNIFORM_TERNARY)
+    params.SetSecretKeyDist(getattr(backend.SecretKeyDist, secret_dist or "UNIFORM_TERNARY"))
     params.SetSecurityLevel(backend.SecurityLevel.HEStd_NotSet)
     params.SetRingDim(ring_dimension)
     params.SetScalingTechnique(backend.ScalingTechnique.FLEXIBLEAUTO)

@@ -268,6 +268,12 @@ class Context:
         call("fhe_keygen_secret", self.handle, seed, _ptr(s))
         return s
 
+    def keygen_secret_sparse(self, seed: int, h: int) -> np.ndarray:
+        """Sparse-ternary secret: exactly h coefficients +-1, the rest 0."""
+        s = np.zeros(self.n, dtype=np.int64)
+        call("fhe_keygen_secret_sparse", self.handle, seed, h, _ptr(s))
+        return s
+
     def keygen_public(self, s, seed: int) -> "Poly":
         s = np.ascontiguousarray(s, dtype=np.int64)
         pk = Poly(self, 2, self.L)

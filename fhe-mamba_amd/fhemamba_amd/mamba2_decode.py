@@ -360,18 +360,27 @@ def expected_rotation_count(lay: LayerPayload, slots: int) -> dict:
 
 
 # ----------------------------------------------------------------- command line
+SECRET_KEY_DISTS = {"sparse-ternary": "SPARSE_TERNARY", "uniform-ternary": "UNIFORM_TERNARY"}
+
+
 def run_payload(payload_dir: str, *, tokens: int = 0, bootstrap_passes: int = 2, seed=None,
-                log=print) -> dict:
+                secret_key_dist: str = "sparse-ternary", log=print) -> dict:
     """Decode the payload's test embeddings in turn (carried state) and
     compare the decrypted outputs with its polynomial-circuit and exact
-    references; returns the report."""
+    references; returns the report.  The secret is sparse ternary by
+    default, as the reference decoder's (stage1_mamba2_config.hpp:211,
+    resolve_secret_key_dist in stage1_mamba2_decode_fideslib.cpp:284-291)."""
+    from . import ckks
     from .mamba2_payload import read_chain_payload
     from .packed import build_context
+    if secret_key_dist not in SECRET_KEY_DISTS:
+        raise ValueError(f"secret key distribution must be one of {sorted(SECRET_KEY_DISTS)}")
     chain = read_chain_payload(payload_dir)
     n_tok = tokens or chain.n_test_tokens
     slots = 32768
     t0 = time.perf_counter()
-    cc, keys = build_context(slots, seed=seed)
+    cc, keys = build_context(slots, seed=seed, secret_dist=getattr(
+        ckks.SecretKeyDist, SECRET_KEY_DISTS[secret_key_dist]))
     dec = EncryptedMamba2Decoder(cc, keys, chain, bootstrap_passes=bootstrap_passes, log=log)
     setup = time.perf_counter() - t0
     states = dec.initial_states()
@@ -396,6 +405,7 @@ def run_payload(payload_dir: str, *, tokens: int = 0, bootstrap_passes: int = 2,
         "tokens": n_tok,
         "ring_dimension": cc.GetRingDimension(),
         "slots": slots,
+        "secret_key_dist": secret_key_dist,
         "setup_seconds": setup,
         "seconds_per_token": per_token,
         "first_token_seconds": per_token[0],
@@ -425,10 +435,13 @@ def main(argv=None) -> int:
     ap.add_argument("--bootstrap-passes", type=int, default=2, choices=(1, 2))
     ap.add_argument("--tolerance", type=float, default=1e-3,
                     help="pass threshold on the error against the polynomial circuit")
+    ap.add_argument("--secret-key-dist", default="sparse-ternary",
+                    choices=sorted(SECRET_KEY_DISTS))
     args = ap.parse_args(sys.argv[1:] if argv is None else argv)
     try:
         report = run_payload(args.payload, tokens=args.tokens,
-                             bootstrap_passes=args.bootstrap_passes)
+                             bootstrap_passes=args.bootstrap_passes,
+                             secret_key_dist=args.secret_key_dist)
     except Exception as exc:  # noqa: BLE001 - reported as exit code 2
         print(exc, file=sys.stderr)
         return 2

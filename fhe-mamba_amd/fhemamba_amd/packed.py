@@ -823,14 +823,15 @@ def parse_args(argv):
 
 
 def build_context(slots: int, *, ring_dim: int = 65536, depth: int = 44, scale_bits: int = 59,
-                  first_mod_bits: int = 60, dnum: int = 3, seed=None):
+                  first_mod_bits: int = 60, dnum: int = 3, seed=None, secret_dist=None):
     """The reference executor's context (packed_fideslib.cpp:1060-1083):
-    uniform ternary, FLEXIBLEAUTO, HYBRID, depth 44, 59-bit scale, 60-bit
-    first prime, dnum 3, batch = program slots, security not set."""
+    uniform ternary (unless `secret_dist` says otherwise), FLEXIBLEAUTO,
+    HYBRID, depth 44, 59-bit scale, 60-bit first prime, dnum 3, batch =
+    program slots, security not set."""
     from . import ckks
     p = ckks.CCParamsCKKSRNS()
     p.SetSecurityLevel(ckks.SecurityLevel.HEStd_NotSet)
-    p.SetSecretKeyDist(ckks.SecretKeyDist.UNIFORM_TERNARY)
+    p.SetSecretKeyDist(secret_dist or ckks.SecretKeyDist.UNIFORM_TERNARY)
     p.SetRingDim(ring_dim)
     p.SetBatchSize(slots)
     p.SetMultiplicativeDepth(depth)

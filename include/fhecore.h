@@ -215,6 +215,12 @@ int fhe_decode(fhe_context *ctx, const fhe_poly *pt, uint32_t slots,
  * keys derived from it (KeyGen, EvalMultKeyGen, EvalRotateKeyGen:
  * packed_fideslib.cpp:1080-1083). */
 int fhe_keygen_secret(fhe_context *ctx, uint64_t seed, int64_t *s_coef);
+/* Seeded sparse-ternary secret with exactly h nonzero coefficients (+-1):
+ * KeyGen under SetSecretKeyDist(SPARSE_TERNARY), the Mamba-2 decoder's
+ * default (native/fideslib_stage0/src/stage1_mamba2_decode_fideslib.cpp:
+ * 1225, stage1_mamba2_config.hpp:211).  1 <= h <= N, else FHE_ERR_ARG. */
+int fhe_keygen_secret_sparse(fhe_context *ctx, uint64_t seed, uint32_t h,
+                             int64_t *s_coef);
 int fhe_keygen_public(fhe_context *ctx, const int64_t *s_coef, uint64_t seed,
                       fhe_poly *pk);
 int fhe_keygen_relin(fhe_context *ctx, const int64_t *s_coef, uint64_t seed,

@@ -678,6 +678,9 @@ void orc_relinearize(const orc_ctx *c, const uint64_t *ct3, uint32_t nq,
  *   draw(key, i)  = fmix64(key + (i + 1) * 0x9E3779B97F4A7C15)  (SplitMix64)
  *   uniform mod q = floor((draw(2i) * 2^64 + draw(2i+1)) * q / 2^128)
  *   ternary       = {0, 1, -1}[draw(i) mod 3]
+ *   sparse ternary (Hamming weight h): for i < h swap position i with
+ *                   i + floor(draw(2i) (n - i) / 2^64) of 0..n-1 (partial
+ *                   Fisher-Yates), that position gets (draw(2i+1) & 1) ? -1 : 1
  *   error         = centred binomial, eta = 21 (sigma ~ 3.24)
  * ====================================================================== */
 static inline uint64_t fmix64(uint64_t z) {
@@ -707,6 +710,22 @@ void orc_sample_ternary(uint64_t key, int64_t *out, uint32_t n) {
     uint64_t d = orc_draw(key, i) % 3;
     out[i] = d == 0 ? 0 : (d == 1 ? 1 : -1);
   }
+}
+
+void orc_sample_sparse_ternary(uint64_t key, int64_t *out, uint32_t n, uint32_t h) {
+  uint32_t *idx = malloc(sizeof(uint32_t) * n);
+  for (uint32_t i = 0; i < n; ++i) {
+    idx[i] = i;
+    out[i] = 0;
+  }
+  for (uint32_t i = 0; i < h && i < n; ++i) {
+    uint32_t j = i + (uint32_t)(((u128)orc_draw(key, 2 * (uint64_t)i) * (n - i)) >> 64);
+    uint32_t t = idx[i];
+    idx[i] = idx[j];
+    idx[j] = t;
+    out[idx[i]] = (orc_draw(key, 2 * (uint64_t)i + 1) & 1) ? -1 : 1;
+  }
+  free(idx);
 }
 
 void orc_sample_cbd(uint64_t key, int64_t *out, uint32_t n) {
@@ -745,6 +764,10 @@ void orc_signed_to_eval(const orc_ctx *c, const int64_t *coef, uint32_t idx0,
 
 void orc_keygen_secret(uint64_t seed, uint32_t n, int64_t *s_coef) {
   orc_sample_ternary(orc_stream_key(seed, TAG_SECRET, 0), s_coef, n);
+}
+
+void orc_keygen_secret_sparse(uint64_t seed, uint32_t n, uint32_t h, int64_t *s_coef) {
+  orc_sample_sparse_ternary(orc_stream_key(seed, TAG_SECRET, 0), s_coef, n, h);
 }
 
 void orc_keygen_public(const orc_ctx *c, const int64_t *s_coef, uint64_t seed,

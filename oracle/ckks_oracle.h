@@ -120,6 +120,7 @@ uint64_t orc_stream_key(uint64_t seed, uint64_t tag, uint64_t index);
 void orc_sample_uniform(uint64_t key, uint64_t q, uint64_t *out, uint32_t n);
 void orc_sample_ternary(uint64_t key, int64_t *out, uint32_t n);
 void orc_sample_cbd(uint64_t key, int64_t *out, uint32_t n);
+void orc_sample_sparse_ternary(uint64_t key, int64_t *out, uint32_t n, uint32_t h);
 
 /* Signed small coefficients -> evaluation form over modulus indices
  * [idx0, idx0+nlimb). */
@@ -127,6 +128,8 @@ void orc_signed_to_eval(const orc_ctx *c, const int64_t *coef,
                         uint32_t idx0, uint32_t nlimb, uint64_t *out);
 /* Key generation.  s_coef: ternary secret (N int64). */
 void orc_keygen_secret(uint64_t seed, uint32_t n, int64_t *s_coef);
+/* Sparse-ternary secret: exactly h coefficients +-1 (h <= n). */
+void orc_keygen_secret_sparse(uint64_t seed, uint32_t n, uint32_t h, int64_t *s_coef);
 void orc_keygen_public(const orc_ctx *c, const int64_t *s_coef, uint64_t seed,
                        uint64_t *pk /* [2][L][N] */);
 /* Switching key from s_old to s_new, both given as evaluation form over

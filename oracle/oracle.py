@@ -72,6 +72,7 @@ def _load():
         "orc_sample_cbd": (None, [_u64, _p, _u32]),
         "orc_signed_to_eval": (None, [_p, _p, _u32, _u32, _p]),
         "orc_keygen_secret": (None, [_u64, _u32, _p]),
+        "orc_keygen_secret_sparse": (None, [_u64, _u32, _u32, _p]),
         "orc_keygen_public": (None, [_p, _p, _u64, _p]),
         "orc_keygen_switch": (None, [_p, _p, _p, _u64, _u64, _p]),
         "orc_keygen_galois": (None, [_p, _p, _u32, _u64, _p]),
@@ -235,6 +236,12 @@ class Ctx:
     def secret(self, seed):
         s = np.zeros(self.n, dtype=np.int64)
         lib.orc_keygen_secret(seed, self.n, ptr(s))
+        return s
+
+    def secret_sparse(self, seed, h):
+        """Sparse-ternary secret with exactly h coefficients +-1."""
+        s = np.zeros(self.n, dtype=np.int64)
+        lib.orc_keygen_secret_sparse(seed, self.n, h, ptr(s))
         return s
 
     def signed_to_eval(self, coef, idx0, nlimb):

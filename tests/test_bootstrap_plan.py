@@ -87,9 +87,29 @@ def test_uniform_ternary_bound():
     assert B.uniform_ternary_bound(2 ** 16) == 512
 
 
-@pytest.mark.parametrize("ring", [2 ** 10, 2 ** 12, 2 ** 16])
-def test_sine_approximation(ring):
-    s = B.BootstrapConfig.for_ring(ring).sine
+def test_secret_bound_and_sparse_plan():
+    """K from the secret's Hamming weight: 2N/3 reproduces the uniform
+    bound; h = 192 (sparse ternary) gives K = 64, four double angles and a
+    degree-59 cosine, three levels fewer than the uniform plan at N=2^16."""
+    for ring in (2 ** 12, 2 ** 16):
+        assert B.secret_bound(2 * ring / 3) == B.uniform_ternary_bound(ring)
+    assert B.secret_bound(192) == 64
+    sparse = B.BootstrapConfig.for_ring(2 ** 16, (4, 4), hamming_weight=192).sine
+    dense = B.BootstrapConfig.for_ring(2 ** 16, (4, 4)).sine
+    assert (sparse.K, sparse.r, sparse.degree) == (64, 4, 59)
+    assert (dense.K, dense.r, dense.degree) == (512, 6, 89)
+    assert dense.depth() - sparse.depth() == 3
+    # a sparse secret's smaller rounding noise (and smaller K) leaves room
+    # for a larger scale-down, which shrinks the sine's cubic term
+    c_sparse = B.correction_bits_for(2 ** 16, sparse, 2.0 ** 59, 2.0 ** 60, 2.0 ** 59,
+                                     hamming_weight=192)
+    c_dense = B.correction_bits_for(2 ** 16, dense, 2.0 ** 59, 2.0 ** 60, 2.0 ** 59)
+    assert (c_sparse, c_dense) == (10, 7)
+
+
+@pytest.mark.parametrize("ring,hw", [(2 ** 10, 0), (2 ** 12, 0), (2 ** 16, 0), (2 ** 16, 192)])
+def test_sine_approximation(ring, hw):
+    s = B.BootstrapConfig.for_ring(ring, hamming_weight=hw).sine
     K = int(s.K)
     u = (np.arange(-K + 1, K)[:, None] + np.linspace(-2 ** -10, 2 ** -10, 17)[None, :]).ravel()
     assert np.max(np.abs(s.plain(u) - np.sin(2 * np.pi * u))) < 1e-9

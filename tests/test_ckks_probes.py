@@ -203,8 +203,12 @@ def test_select_chain_smallest_secure_ring():
 def test_select_chain_rejects_unimplemented():
     for kw in ({"ScalingTechnique": ckks.ScalingTechnique.FIXEDMANUAL},
                {"KeySwitchTechnique": ckks.KeySwitchTechnique.BV},
-               {"SecretKeyDist": ckks.SecretKeyDist.SPARSE_TERNARY}):
+               {"SecretKeyDist": ckks.SecretKeyDist.GAUSSIAN}):
         with pytest.raises(NotImplementedError):
             ckks.select_chain(_params(RingDim=1024, **kw))
+    # sparse-ternary secrets use the same chain as uniform-ternary ones
+    assert ckks.select_chain(_params(RingDim=1024, SecurityLevel=ckks.SecurityLevel.HEStd_NotSet,
+                                     SecretKeyDist=ckks.SecretKeyDist.SPARSE_TERNARY)) == \
+        ckks.select_chain(_params(RingDim=1024, SecurityLevel=ckks.SecurityLevel.HEStd_NotSet))
     with pytest.raises(ValueError):
         ckks.select_chain(_params(SecurityLevel=ckks.SecurityLevel.HEStd_NotSet))

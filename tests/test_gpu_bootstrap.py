@@ -118,3 +118,44 @@ def test_sparse_packing_bootstrap(slots):
         err = np.max(np.abs(np.asarray(pt.GetRealPackedValue()) - x))
         print(f"sparse {slots} slots, {passes} pass(es): error 2^{np.log2(err):.1f}", flush=True)
         assert err < tol
+
+
+# ------------------------------------------------------- sparse-ternary secret
+def test_sparse_secret_matches_oracle():
+    """The library's seeded sparse-ternary sampler equals the oracle's."""
+    import oracle as O
+    q, p = O.gen_moduli(LOG_N, 6, 45, 60, 3)
+    ctx, orc = F.Context(LOG_N, q, p, 3), O.Ctx(LOG_N, q, p, 3)
+    for seed, h in ((3, 192), (4, 64), (5, 1 << LOG_N)):
+        s = ctx.keygen_secret_sparse(seed, h)
+        assert int(np.count_nonzero(s)) == h
+        assert np.array_equal(s, orc.secret_sparse(seed, h))
+    with pytest.raises(ValueError):
+        ctx.keygen_secret_sparse(1, (1 << LOG_N) + 1)
+
+
+def test_sparse_secret_bootstrap():
+    """A SPARSE_TERNARY context (h = 192): K = 64, four double angles, a
+    degree-59 cosine, so the bootstrap consumes fewer levels than the
+    uniform-ternary one and keeps the one-pass tolerance."""
+    from fhemamba_amd import ckks
+    cc, keys = build_toy_context(ring_dimension=1 << LOG_N, batch=SLOTS, depth=44,
+                                 scale_bits=59, first_mod_bits=60, seed=98,
+                                 secret_dist="SPARSE_TERNARY")
+    assert int(np.count_nonzero(keys.secretKey.s)) == ckks.SPARSE_HAMMING_WEIGHT
+    cc.EvalBootstrapSetup([3, 3], [0, 0], SLOTS)
+    cc.EvalBootstrapKeyGen(keys.secretKey, SLOTS)
+    boot = cc._bootstrapper()
+    assert (boot.cfg.sine.K, boot.cfg.sine.r) == (64, 4)
+    L = len(cc.GetModuli()[0])
+    x = np.random.default_rng(5).uniform(-1, 1, SLOTS)
+    ct = enc_at(cc, keys, x, L - 2)
+    out = cc.EvalBootstrap(ct)
+    assert out.GetLevel() == cc.GetBootstrapDepth() < L - 2
+    err = np.max(np.abs(dec(cc, keys, out) - x))
+    print(f"sparse-secret one-pass bootstrap error 2^{np.log2(err):.1f}", flush=True)
+    assert err < ONE_PASS_TOL
+    out2 = cc.EvalBootstrap(ct, 2)
+    err2 = np.max(np.abs(dec(cc, keys, out2) - x))
+    print(f"sparse-secret two-pass bootstrap error 2^{np.log2(err2):.1f}", flush=True)
+    assert err2 < TWO_PASS_TOL

@@ -377,3 +377,29 @@ def test_sampling_ranges_and_moments():
     e = np.zeros(n, dtype=np.int64)
     O.lib.orc_sample_cbd(6, O.ptr(e), n)
     assert abs(e.var() - 10.5) < 0.5 and abs(e).max() <= 21
+
+
+@pytest.mark.parametrize("h", [1, 64, 192, 4096])
+def test_sparse_ternary_sampler(h):
+    """Exactly h coefficients +-1 (h = n gives no zero), deterministic per
+    seed; over many seeds every position and both signs are equally likely
+    (a partial Fisher-Yates shuffle: no position bias from the modular
+    reduction)."""
+    n = 4096
+    ctx = O.Ctx(12, O.ntt_friendly_primes(12, 50, 1), [], 1)
+    s = ctx.secret_sparse(17, h)
+    assert int(np.count_nonzero(s)) == h and set(np.unique(s)) <= {-1, 0, 1}
+    assert np.array_equal(s, ctx.secret_sparse(17, h))
+    if h < n:
+        assert not np.array_equal(s, ctx.secret_sparse(18, h))
+    if h == 192:
+        hits = np.zeros(n)
+        signs = 0
+        for seed in range(400):
+            t = ctx.secret_sparse(1000 + seed, h)
+            hits += t != 0
+            signs += int(t.sum())
+        # 400 * 192 / 4096 = 18.75 expected hits per position
+        buckets = hits.reshape(16, 256).sum(axis=1)
+        assert np.all(np.abs(buckets / buckets.mean() - 1) < 0.05)
+        assert abs(signs) < 4 * np.sqrt(400 * h)
