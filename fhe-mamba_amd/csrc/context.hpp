@@ -278,6 +278,15 @@ void ntt_inverse_ksk(Context& c, uint64_t* ext_p, uint32_t npoly, const ModDownE
 bool moddown_fused_ok(const Context& c, uint32_t nq);
 void moddown_fused(Context& c, uint64_t* ext_p, uint64_t* y, uint32_t npoly, uint32_t nq,
                    const ConvPlan& pl, const ModDownEpi& epi);
+// ModUp of `count` c1 polys (nq limbs each) into digits [count][nd][nq+K][N]
+// in four launches for ring dimensions 2^13..2^17 with every modulus below
+// 2^60: the first inverse pass reading c1 (blocked out), one kernel for the
+// inverse column stages + the conversion of every digit + the forward
+// column stages, the last forward pass, and the copy of each digit's own
+// limbs.
+bool modup_fused_ok(const Context& c, uint32_t nq, uint32_t count);
+void modup_fused(Context& c, const uint64_t* const* as, uint32_t count, uint32_t nq,
+                 uint64_t* digits);
 // Forward NTT of the converted limbs of the ModUp digits of `count`
 // ciphertexts, [count][nd][nq+K][N].
 void ntt_forward_digits(Context& c, uint64_t* digits, uint32_t count, uint32_t nd, uint32_t nq);

@@ -262,6 +262,10 @@ void modup_batch(Context& c, const uint64_t* const* as, uint32_t count, uint32_t
                  uint64_t* digits) {
   if (nq == 0 || nq > c.L) throw ArgError("modup: bad level");
   if (count == 0) return;
+  if (modup_fused_ok(c, nq, count)) {
+    modup_fused(c, as, count, nq, digits);
+    return;
+  }
   const size_t n = c.n, ne = nq + c.K, pl = (size_t)nq * n;
   const uint32_t nd = num_digits(c, nq);
   const size_t ct_words = (size_t)nd * ne * n;

@@ -27,7 +27,7 @@
 // Grid: (tiles per limb, poly, limb).  The limb index is the slowest grid
 // dimension so consecutive workgroups share one modulus and its twiddle
 // table stays hot in L2.
-#include "context.hpp"
+#include "ops.hpp"
 
 namespace fhe {
 namespace {
@@ -543,6 +543,58 @@ __global__ void __launch_bounds__(256)
       EpiStore<ND, BLK>{epi, 1u << log_n, log_n});
 }
 
+// ModUp input: limb blockIdx.z of ciphertext blockIdx.y's c1, read from the
+// caller's polys (the first inverse pass reads them in place of a copy).
+constexpr int MODUP_MAX_CT = 32;
+struct SrcLoad {
+  static constexpr bool kLoad = true;
+  static constexpr bool kPair = false;
+  const uint64_t* const* src;  // MODUP_MAX_CT entries in kernel arguments
+  uint32_t n;
+  __device__ __forceinline__ uint64_t get(size_t g, uint64_t) const {
+    return src[blockIdx.y][(size_t)blockIdx.z * n + g];
+  }
+  __device__ __forceinline__ void get2(size_t, uint64_t, uint64_t&, uint64_t&) const {}
+};
+struct SrcPtrs {
+  const uint64_t* p[MODUP_MAX_CT];
+};
+
+// First inverse pass of a fused ModUp: c1 of each ciphertext -> coef
+// (blocked layout).
+template <int S>
+__global__ void __launch_bounds__(256)
+    ntt_pass_modup_in(uint64_t* __restrict__ coef, size_t poly_stride,
+                      const ModConst* __restrict__ mc, const uint64_t* __restrict__ tw_all,
+                      uint32_t log_n, uint32_t s_other, const SrcPtrs src) {
+  ntt_body<S, BLOCKS, true, RHO_EPILOGUE, PlainStore, SrcLoad, LimbMap, false, true>(
+      coef, poly_stride, mc, tw_all, log_n, LimbMap::contiguous(0), s_other, 0, PlainStore{},
+      SrcLoad{src.p, 1u << log_n});
+}
+
+// Last forward pass of a fused ModUp over the digits' converted limbs
+// (blocked layout in, standard out).
+template <int S>
+__global__ void __launch_bounds__(256)
+    ntt_pass_modup_out(uint64_t* __restrict__ digits, size_t poly_stride,
+                       const ModConst* __restrict__ mc, const uint64_t* __restrict__ tw_all,
+                       uint32_t log_n, DigitMap map, uint32_t s_other) {
+  ntt_body<S, BLOCKS, false, RHO_EPILOGUE, PlainStore, PlainLoad, DigitMap, true, false>(
+      digits, poly_stride, mc, tw_all, log_n, map, s_other, 1, PlainStore{});
+}
+
+// Each digit's own limbs, in evaluation form, from c1 into the digit buffer:
+// limb i of ciphertext blockIdx.z goes to digit i / alpha at position i.
+// grid (N / 256, nq, count).
+__global__ void __launch_bounds__(256)
+    k_copy_own_limbs(uint64_t* __restrict__ digits, const SrcPtrs src, uint32_t n,
+                     uint32_t alpha, uint32_t nd, uint32_t ne) {
+  const uint32_t i = blockIdx.y, ct = blockIdx.z;
+  const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const uint32_t d = i / alpha;
+  digits[(((size_t)ct * nd + d) * ne + i) * n + e] = src.p[ct][(size_t)i * n + e];
+}
+
 // ---- Fused middle of a batched ModDown, ring dimensions 2^13 .. 2^17 ----
 //
 // One workgroup per (poly, column u): the last S1 inverse stages of the K
@@ -578,12 +630,33 @@ constexpr int mid_lines() {  // lines in flight per workgroup of NW waves
   return NW * (64 / mid_lanes_per_line<S1>());
 }
 
+// What one (poly, column) tile converts.  Poly p of the launch uses plan
+// p % nplan; its sources are limbs src_limb0 .. src_limb0 + nsrc - 1 of
+// source group p / nplan (moduli src_mod0 + t), its targets the limbs
+// pos(k) = k < skip_at ? k : k + skip_len of output group p (moduli
+// dst_idx[k]).  ModDown: one plan, sources the K P limbs of ext poly p,
+// targets Q limbs 0..nq-1 of y poly p.  ModUp: one plan per digit d,
+// sources the digit's limbs of ciphertext p / nd, targets the rest of
+// Q_l + P in the digit buffer's order (the digit's own limbs skipped).
+constexpr int MID_MAXPLAN = 8;
+struct MidPlan {
+  const uint64_t* src_scale;  // [nsrc][2]: [Q/q_t]^-1 N^-1 mod q_t (Shoup)
+  const uint64_t* qhat_mont;  // [nsrc][ndst], Montgomery form w.r.t. the target
+  const uint32_t* dst_idx;    // [ndst] target modulus indices
+  uint32_t nsrc, ndst, src_mod0, src_limb0, skip_at, skip_len;
+};
+struct MidArgs {
+  const uint64_t* src;        // blocked, inverse block stages done, [0, 4q)
+  uint64_t* out;              // blocked, forward column stages done, [0, 8q)
+  size_t src_group_words, out_group_words;
+  MidPlan plan[MID_MAXPLAN];
+  uint32_t nplan;
+};
+
 template <int S1, int S2, int NW>
 __global__ void __launch_bounds__(64 * NW)
-    k_moddown_mid(const uint64_t* __restrict__ ext, uint64_t* __restrict__ y,
-                  const ModConst* __restrict__ mc, const uint64_t* __restrict__ tw_inv,
-                  const uint64_t* __restrict__ tw_fwd, const uint64_t* __restrict__ src_scale,
-                  const uint64_t* __restrict__ qhat_mont, uint32_t K, uint32_t nq, uint32_t L) {
+    k_convert_mid(const MidArgs a, const ModConst* __restrict__ mc,
+                  const uint64_t* __restrict__ tw_inv, const uint64_t* __restrict__ tw_fwd) {
   constexpr int M = 1 << S1, TPL = mid_lanes_per_line<S1>(), R = M / TPL;
   constexpr int RHO = R == 4 ? 2 : 3, LPW = 64 / TPL, NL = mid_lines<S1, NW>();
   constexpr int NSP = (S1 + RHO - 1) / RHO;
@@ -592,8 +665,6 @@ __global__ void __launch_bounds__(64 * NW)
   constexpr uint32_t M30 = (1u << 30) - 1;
   static_assert(R * TPL == M && (1 << RHO) == R, "column split");
   extern __shared__ uint64_t lds_dyn[];
-  uint64_t* const src = lds_dyn;
-  uint64_t* const work = lds_dyn + (size_t)K * PITCH;
 
   // Tiles in XCD order: workgroup i runs on XCD i % 8, and each XCD takes a
   // contiguous range of (poly, column) tiles, so neighbouring columns, which
@@ -601,19 +672,28 @@ __global__ void __launch_bounds__(64 * NW)
   const uint32_t per = gridDim.x / 8;
   const uint32_t tile = (blockIdx.x % 8) * per + blockIdx.x / 8;
   const uint32_t p = tile / N2, col = tile % N2;
+  const MidPlan& pl = a.plan[p % a.nplan];
+  const uint32_t K = pl.nsrc, nq = pl.ndst;
+  const uint64_t* const ext = a.src + (size_t)(p / a.nplan) * a.src_group_words +
+                              (size_t)pl.src_limb0 * N;
+  uint64_t* const y = a.out + (size_t)p * a.out_group_words;
+  const uint64_t* __restrict__ src_scale = pl.src_scale;
+  const uint64_t* __restrict__ qhat_mont = pl.qhat_mont;
+  uint64_t* const src = lds_dyn;
+  uint64_t* const work = lds_dyn + (size_t)K * PITCH;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t lane = threadIdx.x & 63, sub = lane / TPL, tau = lane % TPL;
   const uint32_t first = wave * LPW + sub;
 
   // Inverse column stages of the P limbs; each limb is one line of src.
   for (uint32_t t = first; t < K; t += NL) {
-    const uint32_t midx = L + t;
+    const uint32_t midx = pl.src_mod0 + t;
     const uint64_t q = mc[midx].q, q4 = 4 * q, qneg = mc[midx].neg_q, q4neg = mc[midx].neg_q4;
     const uint64_t* __restrict__ tw = tw_inv + (size_t)midx * N * 2;
     uint64_t* const line = src + (size_t)t * PITCH;
     uint64_t x[R];
     // First window (bits 0 .. RHO-1): rows R tau + v, one blocked run.
-    const uint64_t* g = ext + ((size_t)p * K + t) * N + blocked_off<S2>(R * tau, col);
+    const uint64_t* g = ext + (size_t)t * N + blocked_off<S2>(R * tau, col);
 #pragma unroll
     for (int v = 0; v < R; ++v) x[v] = g[v];
 #pragma unroll
@@ -661,9 +741,11 @@ __global__ void __launch_bounds__(64 * NW)
   // their forward column stages.
   uint64_t* const line = work + (size_t)first * PITCH;
   for (uint32_t k = first; k < nq; k += NL) {
-    const uint64_t q = mc[k].q, q4 = 4 * q, qn = mc[k].qinv_neg;
-    const uint64_t qneg = mc[k].neg_q, q4neg = mc[k].neg_q4;
-    const uint64_t* __restrict__ tw = tw_fwd + (size_t)k * N * 2;
+    const uint32_t kmod = pl.dst_idx[k];
+    const uint32_t kpos = k < pl.skip_at ? k : k + pl.skip_len;
+    const uint64_t q = mc[kmod].q, q4 = 4 * q, qn = mc[kmod].qinv_neg;
+    const uint64_t qneg = mc[kmod].neg_q, q4neg = mc[kmod].neg_q4;
+    const uint64_t* __restrict__ tw = tw_fwd + (size_t)kmod * N * 2;
     uint64_t x[R];
     {
       // First forward window (bits S1-RHO .. S1-1): rows thi | v << w | tlo.
@@ -731,7 +813,7 @@ __global__ void __launch_bounds__(64 * NW)
         wave_lds_sync();
       } else {
         // Last window (bits 0 .. RHO-1): rows R tau + v, one blocked run.
-        uint64_t* g = y + ((size_t)p * nq + k) * N + blocked_off<S2>(R * tau, col);
+        uint64_t* g = y + (size_t)kpos * N + blocked_off<S2>(R * tau, col);
 #pragma unroll
         for (int v = 0; v < R; ++v) g[v] = x[v];
       }
@@ -846,18 +928,38 @@ size_t mid_lds_bytes(uint32_t K) {
 constexpr uint32_t MID_SMALL_TILES = 4096;
 
 template <int S1, int S2>
-void launch_mid(Context& c, const ConvPlan& pl, const uint64_t* ext, uint64_t* y,
-                uint32_t npoly, uint32_t nq) {
+void launch_mid(Context& c, const MidArgs& a, uint32_t npoly, uint32_t max_src) {
   const uint32_t tiles = npoly << S2;
-  if (tiles < MID_SMALL_TILES && mid_lds_bytes<S1, 8>(c.K) <= 65536) {
-    FHE_LAUNCH(c, "k_moddown_mid", (k_moddown_mid<S1, S2, 8>), dim3(tiles), dim3(512),
-               (mid_lds_bytes<S1, 8>(c.K)), ext, y, c.d_const, c.d_tw_inv, c.d_tw_fwd,
-               pl.d_src_scale, pl.d_qhat_mont, c.K, nq, c.L);
+  if (tiles < MID_SMALL_TILES && mid_lds_bytes<S1, 8>(max_src) <= 65536) {
+    FHE_LAUNCH(c, "k_convert_mid", (k_convert_mid<S1, S2, 8>), dim3(tiles), dim3(512),
+               (mid_lds_bytes<S1, 8>(max_src)), a, c.d_const, c.d_tw_inv, c.d_tw_fwd);
     return;
   }
-  FHE_LAUNCH(c, "k_moddown_mid", (k_moddown_mid<S1, S2, 4>), dim3(tiles), dim3(256),
-             (mid_lds_bytes<S1, 4>(c.K)), ext, y, c.d_const, c.d_tw_inv, c.d_tw_fwd,
-             pl.d_src_scale, pl.d_qhat_mont, c.K, nq, c.L);
+  FHE_LAUNCH(c, "k_convert_mid", (k_convert_mid<S1, S2, 4>), dim3(tiles), dim3(256),
+             (mid_lds_bytes<S1, 4>(max_src)), a, c.d_const, c.d_tw_inv, c.d_tw_fwd);
+}
+
+MidPlan mid_plan(const ConvPlan& pl, uint32_t src_mod0, uint32_t src_limb0, uint32_t skip_at,
+                 uint32_t skip_len) {
+  return MidPlan{pl.d_src_scale, pl.d_qhat_mont, pl.d_dst_idx, pl.nsrc, pl.ndst,
+                 src_mod0, src_limb0, skip_at, skip_len};
+}
+
+bool mid_lds_fits(const Context& c, uint32_t nsrc) {
+  switch (c.log_n) {
+    case 13: case 14: return mid_lds_bytes<7, 4>(nsrc) <= 65536;
+    case 15: case 16: return mid_lds_bytes<8, 4>(nsrc) <= 65536;
+    case 17: return mid_lds_bytes<9, 4>(nsrc) <= 65536;
+    default: return false;
+  }
+}
+
+bool below_2_60_all(const Context& c, uint32_t nq) {
+  for (uint32_t i = 0; i < nq; ++i)
+    if (c.mods[i] >= (1ull << 60)) return false;
+  for (uint32_t t = 0; t < c.K; ++t)
+    if (c.mods[c.L + t] >= (1ull << 60)) return false;
+  return true;
 }
 
 }  // namespace
@@ -865,17 +967,7 @@ void launch_mid(Context& c, const ConvPlan& pl, const uint64_t* ext, uint64_t* y
 bool moddown_fused_ok(const Context& c, uint32_t nq) {
   if (c.log_n < 13 || c.log_n > 17 || c.K == 0 || c.K > 16) return false;
   if (nq == 0 || nq > c.L) return false;
-  for (uint32_t i = 0; i < nq; ++i)
-    if (c.mods[i] >= (1ull << 60)) return false;
-  for (uint32_t t = 0; t < c.K; ++t)
-    if (c.mods[c.L + t] >= (1ull << 60)) return false;
-  size_t lds = 0;
-  switch (c.log_n) {
-    case 13: case 14: lds = mid_lds_bytes<7, 4>(c.K); break;
-    case 15: case 16: lds = mid_lds_bytes<8, 4>(c.K); break;
-    default: lds = mid_lds_bytes<9, 4>(c.K); break;
-  }
-  return lds <= 65536;
+  return below_2_60_all(c, nq) && mid_lds_fits(c, c.K);
 }
 
 void moddown_fused(Context& c, uint64_t* ext_p, uint64_t* y, uint32_t npoly, uint32_t nq,
@@ -884,11 +976,18 @@ void moddown_fused(Context& c, uint64_t* ext_p, uint64_t* y, uint32_t npoly, uin
   if (npoly > 2 * MAX_KS_BATCH) throw ArgError("ModDown batch too large");
   if (!moddown_fused_ok(c, nq)) throw ArgError("fused ModDown does not apply");
   const uint32_t s1 = (c.log_n + 1) / 2, s2 = c.log_n / 2;
+  MidArgs a{};
+  a.src = ext_p;
+  a.out = y;
+  a.src_group_words = (size_t)c.K * c.n;
+  a.out_group_words = (size_t)nq * c.n;
+  a.plan[0] = mid_plan(pl, c.L, 0, nq, 0);
+  a.nplan = 1;
   switch (c.log_n) {
 #define CASE(LN, A, B)                                                   \
   case LN:                                                               \
     launch_ksk<B, BLOCKS, true>(c, ext_p, npoly, s1, false, epi);        \
-    launch_mid<A, B>(c, pl, ext_p, y, npoly, nq);                        \
+    launch_mid<A, B>(c, a, npoly, c.K);                                  \
     launch_moddown<B, BLOCKS, true>(c, y, npoly, nq, s1, epi);           \
     return;
     CASE(13, 7, 6) CASE(14, 7, 7) CASE(15, 8, 7) CASE(16, 8, 8) CASE(17, 9, 8)
@@ -896,6 +995,59 @@ void moddown_fused(Context& c, uint64_t* ext_p, uint64_t* y, uint32_t npoly, uin
     default: throw ArgError("unsupported ring dimension");
   }
   (void)s2;
+}
+
+bool modup_fused_ok(const Context& c, uint32_t nq, uint32_t count) {
+  if (c.log_n < 13 || c.log_n > 17 || c.K == 0 || c.alpha == 0 || c.alpha > 16) return false;
+  if (nq == 0 || nq > c.L || count == 0 || count > (uint32_t)MODUP_MAX_CT) return false;
+  const uint32_t nd = num_digits(c, nq);
+  if (nd > (uint32_t)MID_MAXPLAN || (uint64_t)count * nd > 65535) return false;
+  return below_2_60_all(c, nq) && mid_lds_fits(c, c.alpha);
+}
+
+void modup_fused(Context& c, const uint64_t* const* as, uint32_t count, uint32_t nq,
+                 uint64_t* digits) {
+  if (!modup_fused_ok(c, nq, count)) throw ArgError("fused ModUp does not apply");
+  const size_t n = c.n;
+  const uint32_t ne = nq + c.K, nd = num_digits(c, nq);
+  Scratch coef(c, (size_t)count * nq * n);
+  SrcPtrs sp{};
+  for (uint32_t i = 0; i < count; ++i) sp.p[i] = as[i];
+  MidArgs a{};
+  a.src = coef.p;
+  a.out = digits;
+  a.src_group_words = (size_t)nq * n;
+  a.out_group_words = (size_t)ne * n;
+  a.nplan = nd;
+  uint32_t max_src = 0;
+  for (uint32_t d = 0; d < nd; ++d) {
+    const uint32_t s0 = d * c.alpha, e0 = s0 + c.alpha < nq ? s0 + c.alpha : nq;
+    a.plan[d] = mid_plan(c.modup_plan(s0, e0, nq), s0, s0, s0, e0 - s0);
+    max_src = max_src > e0 - s0 ? max_src : e0 - s0;
+  }
+  // The last digit is the narrowest and so has the most converted limbs.
+  const uint32_t w_last = nq - (nd - 1) * c.alpha;
+  const DigitMap map{c.alpha, nq, c.L, ne, nd};
+  const uint32_t s1 = (c.log_n + 1) / 2;
+  switch (c.log_n) {
+#define CASE(LN, A, B)                                                                        \
+  case LN: {                                                                                  \
+    using G = Geo<B, RHO_EPILOGUE>;                                                           \
+    const uint32_t tiles = (1u << s1) / (256 / G::TPL);                                       \
+    FHE_LAUNCH(c, "ntt_inv_blocks_modup", (ntt_pass_modup_in<B>), dim3(tiles, count, nq),     \
+               dim3(256), 0, coef.p, (size_t)nq * n, c.d_const, c.d_tw_inv, c.log_n, s1, sp); \
+    launch_mid<A, B>(c, a, count * nd, max_src);                                              \
+    FHE_LAUNCH(c, "ntt_fwd_blocks_modup", (ntt_pass_modup_out<B>),                            \
+               dim3(tiles, count * nd, ne - w_last), dim3(256), 0, digits, (size_t)ne * n,    \
+               c.d_const, c.d_tw_fwd, c.log_n, map, s1);                                      \
+    break;                                                                                    \
+  }
+    CASE(13, 7, 6) CASE(14, 7, 7) CASE(15, 8, 7) CASE(16, 8, 8) CASE(17, 9, 8)
+#undef CASE
+    default: throw ArgError("unsupported ring dimension");
+  }
+  FHE_LAUNCH(c, "k_copy_own_limbs", k_copy_own_limbs, dim3(c.n / 256, nq, count), dim3(256), 0,
+             digits, sp, c.n, c.alpha, nd, ne);
 }
 
 void ntt_forward_digits(Context& c, uint64_t* digits, uint32_t count, uint32_t nd,
