@@ -278,6 +278,9 @@ void ntt_inverse_ksk(Context& c, uint64_t* ext_p, uint32_t npoly, const ModDownE
 bool moddown_fused_ok(const Context& c, uint32_t nq);
 void moddown_fused(Context& c, uint64_t* ext_p, uint64_t* y, uint32_t npoly, uint32_t nq,
                    const ConvPlan& pl, const ModDownEpi& epi);
+// Rescale of [npoly][nq][N] into out [npoly][nq-1][N] (out != a) in four
+// launches, for ring dimensions 2^13..2^17.
+void rescale_fused(Context& c, uint64_t* out, const uint64_t* a, uint32_t npoly, uint32_t nq);
 // ModUp of `count` c1 polys (nq limbs each) into digits [count][nd][nq+K][N]
 // in four launches for ring dimensions 2^13..2^17 with every modulus below
 // 2^60: the first inverse pass reading c1 (blocked out), one kernel for the

@@ -543,6 +543,84 @@ __global__ void __launch_bounds__(256)
       EpiStore<ND, BLK>{epi, 1u << log_n, log_n});
 }
 
+// ---- Rescale in four launches (ring dimensions 2^13 .. 2^17) ----
+// The inverse NTT of the last limb reads it from the input (LastLimbLoad);
+// the forward column pass lifts it to modulus i as it loads (LiftLoad:
+// x mod q_i, minus q_l mod q_i in the upper half, the centred lift); the
+// last forward pass stores (a_i - t_i) * q_l^-1 (RescaleStore).
+struct LastLimbLoad {
+  static constexpr bool kLoad = true;
+  static constexpr bool kPair = false;
+  const uint64_t* a;
+  size_t poly_words, last_off;
+  __device__ __forceinline__ uint64_t get(size_t g, uint64_t) const {
+    return a[(size_t)blockIdx.y * poly_words + last_off + g];
+  }
+  __device__ __forceinline__ void get2(size_t, uint64_t, uint64_t&, uint64_t&) const {}
+};
+struct LiftLoad {
+  static constexpr bool kLoad = true;
+  static constexpr bool kPair = false;
+  const uint64_t* last;  // [npoly][N], coefficient form mod q_l, in [0, q_l)
+  const ModConst* mc;
+  const uint64_t* rs;
+  uint32_t n, l, L;
+  uint64_t half;         // q_l >> 1
+  __device__ __forceinline__ uint64_t get(size_t g, uint64_t q) const {
+    const uint32_t i = blockIdx.z;
+    const uint64_t x = last[(size_t)blockIdx.y * n + g];
+    const uint64_t r = reduce_2q(x - mulhi64(x, mc[i].mu64) * q, q);
+    return x > half ? sub_mod(r, rs[((size_t)l * L + i) * 4], q) : r;
+  }
+  __device__ __forceinline__ void get2(size_t, uint64_t, uint64_t&, uint64_t&) const {}
+};
+struct RescaleStore {
+  static constexpr bool kPre = true;
+  static constexpr bool kPair = false;
+  const uint64_t* a;
+  uint64_t* out;
+  const uint64_t* rs;
+  uint32_t n, l, L;
+  __device__ __forceinline__ uint64_t pre(size_t s, uint64_t) const {
+    return a[((size_t)blockIdx.y * (l + 1) + blockIdx.z) * n + s];
+  }
+  __device__ __forceinline__ void pre2(size_t, uint64_t, uint64_t&, uint64_t&) const {}
+  __device__ __forceinline__ void fin(uint64_t*, size_t s, uint64_t y, uint64_t x,
+                                      uint64_t q) const {
+    const uint32_t i = blockIdx.z;
+    const uint64_t* c = rs + ((size_t)l * L + i) * 4;
+    out[((size_t)blockIdx.y * l + i) * n + s] = shoup(x + q - y, c[1], c[2], q);
+  }
+};
+
+template <int S>
+__global__ void __launch_bounds__(256)
+    ntt_pass_rescale_in(uint64_t* __restrict__ last, const ModConst* __restrict__ mc,
+                        const uint64_t* __restrict__ tw_all, uint32_t log_n, uint32_t s_other,
+                        const LastLimbLoad ld, uint32_t l) {
+  ntt_body<S, BLOCKS, true, RHO_PLAIN, PlainStore, LastLimbLoad>(
+      last, (size_t)1 << log_n, mc, tw_all, log_n, LimbMap::contiguous(l), s_other, 0,
+      PlainStore{}, ld);
+}
+
+template <int S>
+__global__ void __launch_bounds__(256)
+    ntt_pass_rescale_lift(uint64_t* __restrict__ t, size_t poly_stride,
+                          const ModConst* __restrict__ mc, const uint64_t* __restrict__ tw_all,
+                          uint32_t log_n, uint32_t s_other, const LiftLoad ld) {
+  ntt_body<S, COLS, false, RHO_PLAIN, PlainStore, LiftLoad>(
+      t, poly_stride, mc, tw_all, log_n, LimbMap::contiguous(0), s_other, 0, PlainStore{}, ld);
+}
+
+template <int S>
+__global__ void __launch_bounds__(256)
+    ntt_pass_rescale_out(uint64_t* __restrict__ t, size_t poly_stride,
+                         const ModConst* __restrict__ mc, const uint64_t* __restrict__ tw_all,
+                         uint32_t log_n, uint32_t s_other, const RescaleStore st) {
+  ntt_body<S, BLOCKS, false, RHO_PLAIN, RescaleStore>(
+      t, poly_stride, mc, tw_all, log_n, LimbMap::contiguous(0), s_other, 1, st);
+}
+
 // ModUp input: limb blockIdx.z of ciphertext blockIdx.y's c1, read from the
 // caller's polys (the first inverse pass reads them in place of a copy).
 constexpr int MODUP_MAX_CT = 32;
@@ -995,6 +1073,36 @@ void moddown_fused(Context& c, uint64_t* ext_p, uint64_t* y, uint32_t npoly, uin
     default: throw ArgError("unsupported ring dimension");
   }
   (void)s2;
+}
+
+void rescale_fused(Context& c, uint64_t* out, const uint64_t* a, uint32_t npoly, uint32_t nq) {
+  if (c.log_n < 13 || c.log_n > 17) throw ArgError("fused rescale needs N = 2^13 .. 2^17");
+  if (nq < 2 || npoly == 0 || npoly > 65535) throw ArgError("rescale: bad shape");
+  const uint32_t l = nq - 1, n = c.n;
+  const uint32_t s1 = (c.log_n + 1) / 2, s2 = c.log_n / 2;
+  Scratch last(c, (size_t)npoly * n), t(c, (size_t)npoly * l * n);
+  const LastLimbLoad in{a, (size_t)nq * n, (size_t)l * n};
+  const LiftLoad lift{last.p, c.d_const, c.d_rescale, n, l, c.L, c.mods[l] >> 1};
+  const RescaleStore st{a, out, c.d_rescale, n, l, c.L};
+  switch (c.log_n) {
+#define CASE(LN, A, B)                                                                        \
+  case LN: {                                                                                  \
+    using GB = Geo<B, RHO_PLAIN>;                                                             \
+    using GA = Geo<A, RHO_PLAIN>;                                                             \
+    const uint32_t tb = (1u << s1) / (256 / GB::TPL), ta = (1u << s2) / (256 / GA::TPL);      \
+    FHE_LAUNCH(c, "ntt_inv_blocks_rescale", (ntt_pass_rescale_in<B>), dim3(tb, npoly, 1),     \
+               dim3(256), 0, last.p, c.d_const, c.d_tw_inv, c.log_n, s1, in, l);              \
+    launch_cols<true>(c, s1, s2, last.p, npoly, n, 1, LimbMap::contiguous(l), true);          \
+    FHE_LAUNCH(c, "ntt_fwd_cols_rescale", (ntt_pass_rescale_lift<A>), dim3(ta, npoly, l),     \
+               dim3(256), 0, t.p, (size_t)l * n, c.d_const, c.d_tw_fwd, c.log_n, s2, lift);   \
+    FHE_LAUNCH(c, "ntt_fwd_blocks_rescale", (ntt_pass_rescale_out<B>), dim3(tb, npoly, l),    \
+               dim3(256), 0, t.p, (size_t)l * n, c.d_const, c.d_tw_fwd, c.log_n, s1, st);     \
+    return;                                                                                   \
+  }
+    CASE(13, 7, 6) CASE(14, 7, 7) CASE(15, 8, 7) CASE(16, 8, 8) CASE(17, 9, 8)
+#undef CASE
+    default: throw ArgError("unsupported ring dimension");
+  }
 }
 
 bool modup_fused_ok(const Context& c, uint32_t nq, uint32_t count) {

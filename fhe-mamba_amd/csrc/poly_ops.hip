@@ -377,6 +377,10 @@ void poly_mod_raise(Context& c, uint64_t* out, uint32_t nq_out, const uint64_t* 
 
 void poly_rescale(Context& c, uint64_t* out, const uint64_t* a, uint32_t npoly, uint32_t nq) {
   if (nq < 2) throw ArgError("rescale needs at least two limbs");
+  if (c.log_n >= 13 && c.log_n <= 17) {
+    rescale_fused(c, out, a, npoly, nq);
+    return;
+  }
   const uint32_t l = nq - 1;
   Scratch last(c, (size_t)npoly * c.n), t(c, (size_t)npoly * l * c.n);
   // last limb of every poly -> [npoly][N], to coefficient form with q_l

@@ -1,4 +1,5 @@
-"""Key switching at every ring dimension of the three-launch ModDown
+"""Key switching and rescaling at every ring dimension of the fused ModUp /
+ModDown / rescale paths
 (2^13 .. 2^17: column lengths 128 / 256 / 512 rows, blocked row groups of
 32 / 16 / 8) and at the rotation benchmark's shape (N=2^16, 24 limbs,
 8 special primes, dnum 3), bit-exact against the oracle."""
@@ -34,6 +35,17 @@ def test_keyswitch_every_level(setup):
         a = residues(rng, ctx.q[:nq], (1,), ctx.n)
         got = ctx.keyswitch(ctx.upload(a), dkey).numpy()
         assert np.array_equal(got, orc.keyswitch(a[0], key)), nq
+
+
+def test_rescale_shapes(setup):
+    """Rescale (four-launch form at these ring dimensions) of 1 and 2 polys
+    at every level, against the oracle."""
+    ctx, orc, s = setup
+    rng = np.random.default_rng(11)
+    for npoly in (1, 2):
+        for nq in range(2, ctx.L + 1):
+            a = residues(rng, ctx.q[:nq], (npoly,), ctx.n)
+            assert np.array_equal(ctx.rescale(ctx.upload(a)).numpy(), orc.rescale(a)), nq
 
 
 def test_hoisted_rotations(setup):
