@@ -548,9 +548,16 @@ def copy_probe(F) -> None:
 
 def step_kernel_bytes(L: int, K: int, R: int) -> dict:
     """Bytes each kernel of one rotation step must move (read + write once),
-    summed over its launches in the step, for the three-launch ModDown used
-    at this ring dimension.  R hoisted rotations, ne = L + K extended limbs,
-    alpha = ceil(L / dnum) limbs per digit:
+    summed over its launches in the step, for the fused ModUp / ModDown /
+    rescale used at this ring dimension.  R hoisted rotations, ne = L + K
+    extended limbs, alpha = ceil(L / dnum) limbs per digit:
+      ntt_inv_blocks_modup    ModUp's first inverse pass: c1's L limbs read,
+                              L written (blocked);
+      k_modup_mid             column stages + conversion of every digit: L
+                              read, dnum*(ne-alpha) written;
+      ntt_fwd_blocks_modup    last forward pass of the converted limbs:
+                              dnum*(ne-alpha) read and written;
+      k_copy_own_limbs        each digit's own limbs: L read, L written;
       ntt_inv_blocks_ksk      first inverse ModDown pass, fed by the P-limb
                               key inner product: digits dnum*K once per batch,
                               per rotation the key's P limbs dnum*2*K read and
@@ -562,22 +569,25 @@ def step_kernel_bytes(L: int, K: int, R: int) -> dict:
                               digits dnum*L and c0 L once per batch, per
                               rotation y 2L and the key's Q limbs dnum*2*L
                               read, output 2L written;
-      k_convert               ModUp: dnum*ne (alpha read, ne-alpha written per
-                              digit);
-      ntt_{fwd,inv}_{cols,blocks}  ModUp: read + write of every limb of the
-                              pass, forward dnum*(ne-alpha), inverse L."""
+      rescale (2 polys)       last-limb inverse NTT 2 + 2 per pass, lifted
+                              forward column pass 2 read + 2(L-1) written,
+                              last pass 2(L-1) read + 2(L-1) of the input
+                              read + 2(L-1) written."""
     ne = L + K
     alpha = -(-L // DNUM)
-    modup_fwd = DNUM * (ne - alpha)
+    conv = DNUM * (ne - alpha)
     return {k: v * LIMB for k, v in {
+        "ntt_inv_blocks_modup": 2 * L,
+        "k_modup_mid": L + conv,
+        "ntt_fwd_blocks_modup": 2 * conv,
+        "k_copy_own_limbs": 2 * L,
         "ntt_inv_blocks_ksk": DNUM * K + R * (DNUM * 2 * K + 2 * K),
         "k_moddown_mid": R * (2 * K + 2 * L),
         "ntt_fwd_blocks_moddown": DNUM * L + L + R * (2 * L + DNUM * 2 * L + 2 * L),
-        "k_convert": DNUM * ne,
-        "ntt_fwd_cols": 2 * modup_fwd,
-        "ntt_fwd_blocks": 2 * modup_fwd,
-        "ntt_inv_cols": 2 * L,
-        "ntt_inv_blocks": 2 * L,
+        "ntt_inv_blocks_rescale": 4,
+        "ntt_inv_cols": 4,
+        "ntt_fwd_cols_rescale": 2 + 2 * (L - 1),
+        "ntt_fwd_blocks_rescale": 6 * (L - 1),
     }.items()}
 
 

@@ -711,24 +711,25 @@ constexpr int mid_lines() {  // lines in flight per workgroup of NW waves
 // What one (poly, column) tile converts.  Poly p of the launch uses plan
 // p % nplan; its sources are limbs src_limb0 .. src_limb0 + nsrc - 1 of
 // source group p / nplan (moduli src_mod0 + t), its targets the limbs
-// pos(k) = k < skip_at ? k : k + skip_len of output group p (moduli
-// dst_idx[k]).  ModDown: one plan, sources the K P limbs of ext poly p,
-// targets Q limbs 0..nq-1 of y poly p.  ModUp: one plan per digit d,
-// sources the digit's limbs of ciphertext p / nd, targets the rest of
-// Q_l + P in the digit buffer's order (the digit's own limbs skipped).
+// pos(k) = k < skip_at ? k : k + skip_len of output group p, target k in
+// the plan's constant order having modulus pos < qlimbs ? pos : L + pos -
+// qlimbs (Q limbs, then P limbs).  ModDown: one plan, sources the K P limbs
+// of ext poly p, targets Q limbs 0..nq-1 of y poly p.  ModUp: one plan per
+// digit d, sources the digit's limbs of ciphertext p / nd, targets the
+// rest of Q_l + P in the digit buffer's order (the digit's own limbs
+// skipped), which is the order of Context::modup_plan's targets.
 constexpr int MID_MAXPLAN = 8;
 struct MidPlan {
   const uint64_t* src_scale;  // [nsrc][2]: [Q/q_t]^-1 N^-1 mod q_t (Shoup)
   const uint64_t* qhat_mont;  // [nsrc][ndst], Montgomery form w.r.t. the target
-  const uint32_t* dst_idx;    // [ndst] target modulus indices
-  uint32_t nsrc, ndst, src_mod0, src_limb0, skip_at, skip_len;
+  uint32_t nsrc, ndst, src_mod0, src_limb0, skip_at, skip_len, qlimbs;
 };
 struct MidArgs {
   const uint64_t* src;        // blocked, inverse block stages done, [0, 4q)
   uint64_t* out;              // blocked, forward column stages done, [0, 8q)
   size_t src_group_words, out_group_words;
   MidPlan plan[MID_MAXPLAN];
-  uint32_t nplan;
+  uint32_t nplan, L;
 };
 
 template <int S1, int S2, int NW>
@@ -755,8 +756,12 @@ __global__ void __launch_bounds__(64 * NW)
   const uint64_t* const ext = a.src + (size_t)(p / a.nplan) * a.src_group_words +
                               (size_t)pl.src_limb0 * N;
   uint64_t* const y = a.out + (size_t)p * a.out_group_words;
-  const uint64_t* __restrict__ src_scale = pl.src_scale;
-  const uint64_t* __restrict__ qhat_mont = pl.qhat_mont;
+  // The conversion tables are read-only for the whole launch: reading them
+  // through the constant address space lets uniform loads use the scalar
+  // cache, as for kernel-argument tables.
+  typedef const uint64_t __attribute__((address_space(4))) cu64;
+  cu64* const src_scale = (cu64*)pl.src_scale;
+  cu64* const qhat_mont = (cu64*)pl.qhat_mont;
   uint64_t* const src = lds_dyn;
   uint64_t* const work = lds_dyn + (size_t)K * PITCH;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -819,8 +824,8 @@ __global__ void __launch_bounds__(64 * NW)
   // their forward column stages.
   uint64_t* const line = work + (size_t)first * PITCH;
   for (uint32_t k = first; k < nq; k += NL) {
-    const uint32_t kmod = pl.dst_idx[k];
     const uint32_t kpos = k < pl.skip_at ? k : k + pl.skip_len;
+    const uint32_t kmod = kpos < pl.qlimbs ? kpos : a.L + (kpos - pl.qlimbs);
     const uint64_t q = mc[kmod].q, q4 = 4 * q, qn = mc[kmod].qinv_neg;
     const uint64_t qneg = mc[kmod].neg_q, q4neg = mc[kmod].neg_q4;
     const uint64_t* __restrict__ tw = tw_fwd + (size_t)kmod * N * 2;
@@ -1006,21 +1011,28 @@ size_t mid_lds_bytes(uint32_t K) {
 constexpr uint32_t MID_SMALL_TILES = 4096;
 
 template <int S1, int S2>
-void launch_mid(Context& c, const MidArgs& a, uint32_t npoly, uint32_t max_src) {
+void launch_mid(Context& c, const char* name, const MidArgs& a, uint32_t npoly,
+                uint32_t max_src) {
   const uint32_t tiles = npoly << S2;
   if (tiles < MID_SMALL_TILES && mid_lds_bytes<S1, 8>(max_src) <= 65536) {
-    FHE_LAUNCH(c, "k_convert_mid", (k_convert_mid<S1, S2, 8>), dim3(tiles), dim3(512),
+    FHE_LAUNCH(c, name, (k_convert_mid<S1, S2, 8>), dim3(tiles), dim3(512),
                (mid_lds_bytes<S1, 8>(max_src)), a, c.d_const, c.d_tw_inv, c.d_tw_fwd);
     return;
   }
-  FHE_LAUNCH(c, "k_convert_mid", (k_convert_mid<S1, S2, 4>), dim3(tiles), dim3(256),
+  FHE_LAUNCH(c, name, (k_convert_mid<S1, S2, 4>), dim3(tiles), dim3(256),
              (mid_lds_bytes<S1, 4>(max_src)), a, c.d_const, c.d_tw_inv, c.d_tw_fwd);
 }
 
-MidPlan mid_plan(const ConvPlan& pl, uint32_t src_mod0, uint32_t src_limb0, uint32_t skip_at,
-                 uint32_t skip_len) {
-  return MidPlan{pl.d_src_scale, pl.d_qhat_mont, pl.d_dst_idx, pl.nsrc, pl.ndst,
-                 src_mod0, src_limb0, skip_at, skip_len};
+// The target order of `pl` must be the one MidPlan describes (checked).
+MidPlan mid_plan(const Context& c, const ConvPlan& pl, uint32_t src_mod0, uint32_t src_limb0,
+                 uint32_t skip_at, uint32_t skip_len, uint32_t qlimbs) {
+  for (uint32_t k = 0; k < pl.ndst; ++k) {
+    const uint32_t pos = k < skip_at ? k : k + skip_len;
+    if (pl.dst_idx[k] != (pos < qlimbs ? pos : c.L + (pos - qlimbs)))
+      throw ArgError("conversion plan target order");
+  }
+  return MidPlan{pl.d_src_scale, pl.d_qhat_mont, pl.nsrc, pl.ndst,
+                 src_mod0, src_limb0, skip_at, skip_len, qlimbs};
 }
 
 bool mid_lds_fits(const Context& c, uint32_t nsrc) {
@@ -1059,13 +1071,14 @@ void moddown_fused(Context& c, uint64_t* ext_p, uint64_t* y, uint32_t npoly, uin
   a.out = y;
   a.src_group_words = (size_t)c.K * c.n;
   a.out_group_words = (size_t)nq * c.n;
-  a.plan[0] = mid_plan(pl, c.L, 0, nq, 0);
+  a.plan[0] = mid_plan(c, pl, c.L, 0, nq, 0, nq);
   a.nplan = 1;
+  a.L = c.L;
   switch (c.log_n) {
 #define CASE(LN, A, B)                                                   \
   case LN:                                                               \
     launch_ksk<B, BLOCKS, true>(c, ext_p, npoly, s1, false, epi);        \
-    launch_mid<A, B>(c, a, npoly, c.K);                                  \
+    launch_mid<A, B>(c, "k_moddown_mid", a, npoly, c.K);                 \
     launch_moddown<B, BLOCKS, true>(c, y, npoly, nq, s1, epi);           \
     return;
     CASE(13, 7, 6) CASE(14, 7, 7) CASE(15, 8, 7) CASE(16, 8, 8) CASE(17, 9, 8)
@@ -1127,10 +1140,11 @@ void modup_fused(Context& c, const uint64_t* const* as, uint32_t count, uint32_t
   a.src_group_words = (size_t)nq * n;
   a.out_group_words = (size_t)ne * n;
   a.nplan = nd;
+  a.L = c.L;
   uint32_t max_src = 0;
   for (uint32_t d = 0; d < nd; ++d) {
     const uint32_t s0 = d * c.alpha, e0 = s0 + c.alpha < nq ? s0 + c.alpha : nq;
-    a.plan[d] = mid_plan(c.modup_plan(s0, e0, nq), s0, s0, s0, e0 - s0);
+    a.plan[d] = mid_plan(c, c.modup_plan(s0, e0, nq), s0, s0, s0, e0 - s0, nq);
     max_src = max_src > e0 - s0 ? max_src : e0 - s0;
   }
   // The last digit is the narrowest and so has the most converted limbs.
@@ -1144,7 +1158,7 @@ void modup_fused(Context& c, const uint64_t* const* as, uint32_t count, uint32_t
     const uint32_t tiles = (1u << s1) / (256 / G::TPL);                                       \
     FHE_LAUNCH(c, "ntt_inv_blocks_modup", (ntt_pass_modup_in<B>), dim3(tiles, count, nq),     \
                dim3(256), 0, coef.p, (size_t)nq * n, c.d_const, c.d_tw_inv, c.log_n, s1, sp); \
-    launch_mid<A, B>(c, a, count * nd, max_src);                                              \
+    launch_mid<A, B>(c, "k_modup_mid", a, count * nd, max_src);                               \
     FHE_LAUNCH(c, "ntt_fwd_blocks_modup", (ntt_pass_modup_out<B>),                            \
                dim3(tiles, count * nd, ne - w_last), dim3(256), 0, digits, (size_t)ne * n,    \
                c.d_const, c.d_tw_fwd, c.log_n, map, s1);                                      \
