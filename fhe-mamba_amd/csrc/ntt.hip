@@ -55,11 +55,17 @@ __device__ __forceinline__ uint32_t lds_idx(uint32_t line, uint32_t u, uint32_t 
 // Final stores go through `store.fin(base, offset_in_limb, value, t, q)`,
 // with t = store.pre(offset_in_limb, q) when Store::kPre.
 // The first pass's input comes from `load.get(offset_in_limb, q)` instead
-// of data when Load::kLoad.
+// of data when Load::kLoad.  kPair functors also produce the terms of two
+// adjacent positions from 16-byte loads in two steps, fetch2 (every load of
+// the pair, issued together into an Ops2) and comb2 (the arithmetic).
+// Prefetching the next pair's operands before a pair's products was
+// measured slower: the extra registers cost more waves than they hide.
 struct PlainLoad {
   static constexpr bool kLoad = false;
   static constexpr bool kPair = false;
-  __device__ __forceinline__ void get2(size_t, uint64_t, uint64_t&, uint64_t&) const {}
+  struct Ops2 {};
+  __device__ __forceinline__ void fetch2(size_t, Ops2&) const {}
+  __device__ __forceinline__ void comb2(const Ops2&, uint64_t, uint64_t&, uint64_t&) const {}
   __device__ __forceinline__ uint64_t get(size_t, uint64_t) const { return 0; }
 };
 
@@ -170,8 +176,10 @@ __device__ __forceinline__ void ntt_body(uint64_t* __restrict__ data, size_t pol
 #pragma unroll
         for (int k = 0; k < R; k += 2) {
           const uint32_t p = staged(k);
+          typename Load::Ops2 ops;
           uint64_t v0, v1;
-          load.get2(wg0 + p, q, v0, v1);
+          load.fetch2(wg0 + p, ops);
+          load.comb2(ops, q, v0, v1);
           lds[lds_idx(p >> S, p & (G::LEN - 1), G::PITCH)] = v0;
           lds[lds_idx((p + 1) >> S, (p + 1) & (G::LEN - 1), G::PITCH)] = v1;
         }
@@ -215,7 +223,11 @@ __device__ __forceinline__ void ntt_body(uint64_t* __restrict__ data, size_t pol
       const size_t wg0 = ((size_t)blockIdx.x * LINES) << S;
       if constexpr (Store::kPair && PAIR && kFinalContig) {
 #pragma unroll
-        for (int k = 0; k < R; k += 2) store.pre2(wg0 + staged(k), q, pre[k], pre[k + 1]);
+        for (int k = 0; k < R; k += 2) {
+          typename Store::Ops2 ops;
+          store.fetch2(wg0 + staged(k), ops);
+          store.comb2(ops, q, pre[k], pre[k + 1]);
+        }
       } else {
 #pragma unroll
         for (int k = 0; k < R; ++k) {
@@ -316,7 +328,9 @@ __device__ __forceinline__ void ntt_body(uint64_t* __restrict__ data, size_t pol
 struct PlainStore {
   static constexpr bool kPre = false;
   static constexpr bool kPair = false;
-  __device__ __forceinline__ void pre2(size_t, uint64_t, uint64_t&, uint64_t&) const {}
+  struct Ops2 {};
+  __device__ __forceinline__ void fetch2(size_t, Ops2&) const {}
+  __device__ __forceinline__ void comb2(const Ops2&, uint64_t, uint64_t&, uint64_t&) const {}
   __device__ __forceinline__ uint64_t pre(size_t, uint64_t) const { return 0; }
   __device__ __forceinline__ void fin(uint64_t* base, size_t g, uint64_t v, uint64_t,
                                       uint64_t) const {
@@ -326,6 +340,22 @@ struct PlainStore {
 
 __device__ __forceinline__ uint32_t brev_bits(uint32_t x, uint32_t bits) {
   return __brev(x) >> (32 - bits);
+}
+
+// Switching-key words are read once per launch: their loads are marked
+// non-temporal so that they do not displace the digits, which every key
+// switch of the batch re-reads, from the caches (measured ~1% faster on the
+// ModDown passes; non-temporal stores of the outputs were slower).
+__device__ __forceinline__ uint64_t load_stream(const uint64_t* p) {
+  return __builtin_nontemporal_load(p);
+}
+__device__ __forceinline__ ulonglong2 load_stream2(const uint64_t* p) {
+  typedef unsigned long long v2u __attribute__((ext_vector_type(2)));
+  const v2u v = __builtin_nontemporal_load(reinterpret_cast<const v2u*>(p));
+  ulonglong2 r;
+  r.x = v.x;
+  r.y = v.y;
+  return r;
 }
 
 // Key inner product sum_j d_j k_j reduced once by REDC (keys in Montgomery
@@ -341,7 +371,7 @@ __device__ __forceinline__ uint64_t key_dot(const uint64_t* dg, size_t dstride, 
     uint64_t a0 = 0, a1 = 0, a2 = 0;
 #pragma unroll
     for (int j = 0; j < ND; ++j) {
-      const uint64_t d = dg[j * dstride], k = kr[j * kstride];
+      const uint64_t d = dg[j * dstride], k = load_stream(kr + j * kstride);
       const uint32_t dl = (uint32_t)d & M30, dh = (uint32_t)(d >> 30);
       const uint32_t kl = (uint32_t)k & M30, kh = (uint32_t)(k >> 30);
       a0 += (uint64_t)dl * kl;
@@ -359,9 +389,9 @@ __device__ __forceinline__ uint64_t key_dot(const uint64_t* dg, size_t dstride, 
     Acc128 acc;
     if (ND > 0) {
 #pragma unroll
-      for (int j = 0; j < ND; ++j) acc.mac(dg[j * dstride], kr[j * kstride]);
+      for (int j = 0; j < ND; ++j) acc.mac(dg[j * dstride], load_stream(kr + j * kstride));
     } else {
-      for (uint32_t j = 0; j < nd_rt; ++j) acc.mac(dg[j * dstride], kr[j * kstride]);
+      for (uint32_t j = 0; j < nd_rt; ++j) acc.mac(dg[j * dstride], load_stream(kr + j * kstride));
     }
     return redc(acc.hi, acc.lo, q, qinv_neg);
   }
@@ -369,19 +399,26 @@ __device__ __forceinline__ uint64_t key_dot(const uint64_t* dg, size_t dstride, 
 
 // key_dot for positions s and s + 1 (s even, operands 16-byte aligned) with
 // 16-byte loads, in the SPLIT form only (every modulus below 2^60, 1..7
-// digits): half the load instructions of two key_dot calls.
+// digits): half the load instructions of two key_dot calls.  key_fetch2
+// issues the loads, key_comb2 forms the two sums.
 template <int ND>
-__device__ __forceinline__ void key_dot2(const uint64_t* dg, size_t dstride, const uint64_t* kr,
-                                         size_t kstride, uint64_t q, uint64_t qinv_neg,
-                                         uint64_t& t0, uint64_t& t1) {
+__device__ __forceinline__ void key_fetch2(const uint64_t* dg, size_t dstride, const uint64_t* kr,
+                                           size_t kstride, ulonglong2* d, ulonglong2* k) {
   static_assert(ND > 0 && ND <= 7, "split key products");
+#pragma unroll
+  for (int j = 0; j < ND; ++j) {
+    d[j] = *reinterpret_cast<const ulonglong2*>(dg + j * dstride);
+    k[j] = load_stream2(kr + j * kstride);
+  }
+}
+template <int ND>
+__device__ __forceinline__ void key_comb2(const ulonglong2* d, const ulonglong2* k, uint64_t q,
+                                          uint64_t qinv_neg, uint64_t& t0, uint64_t& t1) {
   constexpr uint32_t M30 = (1u << 30) - 1;
   uint64_t a0[2] = {0, 0}, a1[2] = {0, 0}, a2[2] = {0, 0};
 #pragma unroll
   for (int j = 0; j < ND; ++j) {
-    const ulonglong2 dv = *reinterpret_cast<const ulonglong2*>(dg + j * dstride);
-    const ulonglong2 kv = *reinterpret_cast<const ulonglong2*>(kr + j * kstride);
-    const uint64_t dd[2] = {dv.x, dv.y}, kk[2] = {kv.x, kv.y};
+    const uint64_t dd[2] = {d[j].x, d[j].y}, kk[2] = {k[j].x, k[j].y};
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const uint32_t dl = (uint32_t)dd[h] & M30, dh = (uint32_t)(dd[h] >> 30);
@@ -415,18 +452,30 @@ struct EpiStore {
   static constexpr bool kPair = SPLIT && ND > 0 && ND <= 7;
   const ModDownEpi& e;
   uint32_t n, log_n;
-  // pre() for positions s and s + 1 (s even), kPair only.
-  __device__ __forceinline__ void pre2(size_t s, uint64_t q, uint64_t& t0, uint64_t& t1) const {
+  // pre() for positions s and s + 1 (s even), kPair only.  The addend is
+  // loaded with the key operands; without one the first digit's words are
+  // read again (a cache hit) so that the load needs no branch.
+  struct Ops2 {
+    ulonglong2 d[kPair ? ND : 1], k[kPair ? ND : 1], add;
+  };
+  __device__ __forceinline__ void fetch2(size_t s, Ops2& o) const {
     if constexpr (kPair) {
       const uint32_t p = blockIdx.y, r = p >> 1, b = p & 1, i = blockIdx.z;
-      key_dot2<ND>(e.digits[r] + (size_t)i * n + s, (size_t)e.ne * n,
-                   e.key[r] + (size_t)b * e.kl + (size_t)i * n + s, 2 * e.kl, q,
-                   e.mc[i].qinv_neg, t0, t1);
+      const uint64_t* dg = e.digits[r] + (size_t)i * n + s;
+      key_fetch2<ND>(dg, (size_t)e.ne * n, e.key[r] + (size_t)b * e.kl + (size_t)i * n + s,
+                     2 * e.kl, o.d, o.k);
       const uint64_t* add = e.add[r][b];
-      if (add) {
-        const ulonglong2 av = *reinterpret_cast<const ulonglong2*>(add + (size_t)i * n + s);
-        t0 = add_mod(t0, av.x, q);
-        t1 = add_mod(t1, av.y, q);
+      o.add = *reinterpret_cast<const ulonglong2*>(add ? add + (size_t)i * n + s : dg);
+    }
+  }
+  __device__ __forceinline__ void comb2(const Ops2& o, uint64_t q, uint64_t& t0,
+                                        uint64_t& t1) const {
+    if constexpr (kPair) {
+      const uint32_t p = blockIdx.y, r = p >> 1, b = p & 1, i = blockIdx.z;
+      key_comb2<ND>(o.d, o.k, q, e.mc[i].qinv_neg, t0, t1);
+      if (e.add[r][b]) {
+        t0 = add_mod(t0, o.add.x, q);
+        t1 = add_mod(t1, o.add.y, q);
       }
     }
   }
@@ -488,13 +537,20 @@ struct KskLoad {
     return key_dot<ND, SPLIT>(dg, dstride, kr, kstride, e.nd, q, e.mc[e.L + t].qinv_neg);
   }
   // get() for positions s and s + 1 (s even), kPair only.
-  __device__ __forceinline__ void get2(size_t s, uint64_t q, uint64_t& v0, uint64_t& v1) const {
+  struct Ops2 {
+    ulonglong2 d[kPair ? ND : 1], k[kPair ? ND : 1];
+  };
+  __device__ __forceinline__ void fetch2(size_t s, Ops2& o) const {
     if constexpr (kPair) {
       const uint32_t p = blockIdx.y, r = p >> 1, b = p & 1, t = blockIdx.z;
-      key_dot2<ND>(e.digits[r] + (size_t)(e.nq + t) * n + s, (size_t)e.ne * n,
-                   e.key[r] + (size_t)b * e.kl + (size_t)(e.L + t) * n + s, 2 * e.kl, q,
-                   e.mc[e.L + t].qinv_neg, v0, v1);
+      key_fetch2<ND>(e.digits[r] + (size_t)(e.nq + t) * n + s, (size_t)e.ne * n,
+                     e.key[r] + (size_t)b * e.kl + (size_t)(e.L + t) * n + s, 2 * e.kl, o.d,
+                     o.k);
     }
+  }
+  __device__ __forceinline__ void comb2(const Ops2& o, uint64_t q, uint64_t& v0,
+                                        uint64_t& v1) const {
+    if constexpr (kPair) key_comb2<ND>(o.d, o.k, q, e.mc[e.L + blockIdx.z].qinv_neg, v0, v1);
   }
 };
 
@@ -556,7 +612,9 @@ struct LastLimbLoad {
   __device__ __forceinline__ uint64_t get(size_t g, uint64_t) const {
     return a[(size_t)blockIdx.y * poly_words + last_off + g];
   }
-  __device__ __forceinline__ void get2(size_t, uint64_t, uint64_t&, uint64_t&) const {}
+  struct Ops2 {};
+  __device__ __forceinline__ void fetch2(size_t, Ops2&) const {}
+  __device__ __forceinline__ void comb2(const Ops2&, uint64_t, uint64_t&, uint64_t&) const {}
 };
 struct LiftLoad {
   static constexpr bool kLoad = true;
@@ -572,7 +630,9 @@ struct LiftLoad {
     const uint64_t r = reduce_2q(x - mulhi64(x, mc[i].mu64) * q, q);
     return x > half ? sub_mod(r, rs[((size_t)l * L + i) * 4], q) : r;
   }
-  __device__ __forceinline__ void get2(size_t, uint64_t, uint64_t&, uint64_t&) const {}
+  struct Ops2 {};
+  __device__ __forceinline__ void fetch2(size_t, Ops2&) const {}
+  __device__ __forceinline__ void comb2(const Ops2&, uint64_t, uint64_t&, uint64_t&) const {}
 };
 struct RescaleStore {
   static constexpr bool kPre = true;
@@ -584,7 +644,9 @@ struct RescaleStore {
   __device__ __forceinline__ uint64_t pre(size_t s, uint64_t) const {
     return a[((size_t)blockIdx.y * (l + 1) + blockIdx.z) * n + s];
   }
-  __device__ __forceinline__ void pre2(size_t, uint64_t, uint64_t&, uint64_t&) const {}
+  struct Ops2 {};
+  __device__ __forceinline__ void fetch2(size_t, Ops2&) const {}
+  __device__ __forceinline__ void comb2(const Ops2&, uint64_t, uint64_t&, uint64_t&) const {}
   __device__ __forceinline__ void fin(uint64_t*, size_t s, uint64_t y, uint64_t x,
                                       uint64_t q) const {
     const uint32_t i = blockIdx.z;
@@ -632,7 +694,9 @@ struct SrcLoad {
   __device__ __forceinline__ uint64_t get(size_t g, uint64_t) const {
     return src[blockIdx.y][(size_t)blockIdx.z * n + g];
   }
-  __device__ __forceinline__ void get2(size_t, uint64_t, uint64_t&, uint64_t&) const {}
+  struct Ops2 {};
+  __device__ __forceinline__ void fetch2(size_t, Ops2&) const {}
+  __device__ __forceinline__ void comb2(const Ops2&, uint64_t, uint64_t&, uint64_t&) const {}
 };
 struct SrcPtrs {
   const uint64_t* p[MODUP_MAX_CT];
