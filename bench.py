@@ -291,7 +291,7 @@ def _bootstrap_once(secret_dist: str, steps: int, warmup: int) -> dict:
     return res
 
 
-def run_bootstrap(steps: int = 3, warmup: int = 1):
+def run_bootstrap(steps: int = 3, warmup: int = 2):
     """EvalBootstrap of one full-packing ciphertext (32768 slots) at N=2^16,
     45 limbs (multiplicative depth 44, 59-bit scale, 60-bit q0), dnum 3,
     level budget (4, 4): one pass and the two-pass refresh, for a
