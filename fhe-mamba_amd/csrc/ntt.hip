@@ -599,6 +599,156 @@ __global__ void __launch_bounds__(256)
       EpiStore<ND, BLK>{epi, 1u << log_n, log_n});
 }
 
+// Last forward pass of a batched ModDown over the blocked y, both polys of
+// each key switch in one workgroup (ND = 1..7 digits, every modulus below
+// 2^60).  Eight wavefronts; lane tid holds the same R = 4 positions of row
+// `line` in both polys (radix 4: one row per wavefront at N2 = 256, two or
+// four at 128 / 64), so the digits' words and the twiddles are loaded once
+// for both key products and both transforms, and the Galois target index is
+// computed once for both stores.  The workgroup's rows are one blocked
+// group (LINES = BLO).  Stage order, twiddle indices and lazy ranges are
+// those of ntt_body's forward BLOCKS pass; the epilogue is EpiStore's:
+// out_b[d(s)] = sum_j digit_j[s] key_j,b[s] (REDC) + add_b[s] + y_b[s].
+template <int S, int ND>
+__global__ void __launch_bounds__(512)
+    ntt_pass_moddown_pair(const uint64_t* __restrict__ y, const ModConst* __restrict__ mc,
+                          const uint64_t* __restrict__ tw_all, uint32_t log_n, uint32_t s_other,
+                          const ModDownEpi e) {
+  constexpr int RHO = 2, R = 4, TPL = 1 << (S - RHO), LINES = 512 / TPL;
+  constexpr int NSP = (S + RHO - 1) / RHO;
+  constexpr uint32_t LEN = 1u << S, PITCH = LEN + LEN / 16 + 1;
+  static_assert(TPL <= 64 && LINES * TPL == 512 && ND > 0 && ND <= 7, "pair epilogue");
+  __shared__ uint64_t lds[2][LINES * PITCH];
+  const uint32_t n = 1u << log_n, r = blockIdx.y, i = blockIdx.z, tid = threadIdx.x;
+  const uint64_t q = mc[i].q, q4 = 4 * q, qneg = mc[i].neg_q, q4neg = mc[i].neg_q4;
+  const uint64_t* __restrict__ tw = tw_all + (size_t)i * n * 2;
+  const size_t ps = (size_t)e.nq * n, wg0 = ((size_t)blockIdx.x * LINES) << S;
+  const uint32_t tau = tid % TPL, line = tid / TPL;
+  const uint32_t twbase = (1u << s_other) + blockIdx.x * LINES + line;
+  // Key-product and store positions of this lane: two adjacent pairs in its
+  // wavefront's own 64R-word run (the wavefront's rows).
+  auto staged = [&](int k) -> uint32_t {
+    return (tid >> 6) * (64u * R) + (uint32_t)(k >> 1) * 128u + 2 * (tid & 63) + (k & 1);
+  };
+
+  // The blocked group of both polys into LDS, word p = u * LINES + row.
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint64_t* __restrict__ src = y + (size_t)(2 * r + h) * ps + (size_t)i * n + wg0;
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+      const uint32_t p = (uint32_t)k * 512u + tid;
+      lds[h][lds_idx(p % LINES, p / LINES, PITCH)] = src[p];
+    }
+  }
+  __syncthreads();
+
+  // Key products of both polys at this lane's positions, the digits' words
+  // read once (16-byte loads, two positions each).
+  uint64_t pre[2][R];
+  {
+    const size_t dstride = (size_t)e.ne * n, kstride = 2 * e.kl;
+    const uint64_t* const a0 = e.add[r][0];
+    const uint64_t* const a1 = e.add[r][1];
+    const uint64_t qn = e.mc[i].qinv_neg;
+#pragma unroll
+    for (int k = 0; k < R; k += 2) {
+      const size_t s = wg0 + staged(k);
+      const uint64_t* dg = e.digits[r] + (size_t)i * n + s;
+      const uint64_t* kr = e.key[r] + (size_t)i * n + s;
+      ulonglong2 d[ND], k0[ND], k1[ND];
+#pragma unroll
+      for (int j = 0; j < ND; ++j) {
+        d[j] = *reinterpret_cast<const ulonglong2*>(dg + j * dstride);
+        k0[j] = load_stream2(kr + j * kstride);
+        k1[j] = load_stream2(kr + e.kl + j * kstride);
+      }
+      // Without an addend the first digit's words are read again (a cache
+      // hit), so that the load is issued with the others, without a branch.
+      const ulonglong2 av = *reinterpret_cast<const ulonglong2*>(a0 ? a0 + (size_t)i * n + s : dg);
+      key_comb2<ND>(d, k0, q, qn, pre[0][k], pre[0][k + 1]);
+      key_comb2<ND>(d, k1, q, qn, pre[1][k], pre[1][k + 1]);
+      if (a0) {
+        pre[0][k] = add_mod(pre[0][k], av.x, q);
+        pre[0][k + 1] = add_mod(pre[0][k + 1], av.y, q);
+      }
+      if (a1) {
+        const ulonglong2 bv = *reinterpret_cast<const ulonglong2*>(a1 + (size_t)i * n + s);
+        pre[1][k] = add_mod(pre[1][k], bv.x, q);
+        pre[1][k + 1] = add_mod(pre[1][k + 1], bv.y, q);
+      }
+    }
+  }
+
+  uint64_t x[2][R];
+#pragma unroll
+  for (int sp = 0; sp < NSP; ++sp) {
+    const int hi = S - RHO * sp;
+    const int w = hi >= RHO ? hi - RHO : 0;
+    const uint32_t thi = (tau >> w) << (w + RHO), tlo = tau & ((1u << w) - 1);
+    if (sp > 0) wave_lds_sync();
+#pragma unroll
+    for (int v = 0; v < R; ++v) {
+      const uint32_t u = thi | ((uint32_t)v << w) | tlo;
+      x[0][v] = lds[0][lds_idx(line, u, PITCH)];
+      x[1][v] = lds[1][lds_idx(line, u, PITCH)];
+    }
+#pragma unroll
+    for (int beta = hi - 1; beta >= w; --beta) {
+      const int d = 1 << (beta - w);
+#pragma unroll
+      for (int v = 0; v < R; ++v) {
+        if (v & d) continue;
+        const uint32_t u = thi | ((uint32_t)v << w) | tlo;
+        const uint32_t ti = (twbase << (S - 1 - beta)) | (u >> (beta + 1));
+        const uint64_t wv = tw[2 * ti], ws = tw[2 * ti + 1];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint64_t X = lazy_sub(x[h][v], q4neg);
+          const uint64_t T = shoup_lazy4n(x[h][v + d], wv, ws, qneg);
+          x[h][v] = X + T;
+          x[h][v + d] = X + q4 - T;
+        }
+      }
+    }
+    if (sp == NSP - 1) {
+#pragma unroll
+      for (int v = 0; v < R; ++v) {
+        x[0][v] = reduce_8q(x[0][v], q);
+        x[1][v] = reduce_8q(x[1][v], q);
+      }
+    }
+    wave_lds_sync();
+#pragma unroll
+    for (int v = 0; v < R; ++v) {
+      const uint32_t u = thi | ((uint32_t)v << w) | tlo;
+      lds[0][lds_idx(line, u, PITCH)] = x[0][v];
+      lds[1][lds_idx(line, u, PITCH)] = x[1][v];
+    }
+  }
+  wave_lds_sync();
+
+  // Stores through the inverse Galois permutation, shared by both polys.
+  const uint32_t gi = e.ginv[r];
+  uint64_t* const out0 = e.out[r] + (size_t)i * n;
+  uint64_t* const out1 = e.out[r] + ((size_t)e.nq + i) * n;
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    const uint32_t p = staged(k);
+    const uint32_t s = (uint32_t)wg0 + p;
+    uint32_t dst = s;
+    if (gi != 1) {
+      // 32-bit wrap-around is exact here: only the product mod 2N matters.
+      const uint32_t jj = brev_bits(s, log_n);
+      const uint32_t ex = ((2u * jj + 1u) * gi) & (2u * n - 1u);
+      dst = brev_bits((ex - 1u) >> 1, log_n);
+    }
+    const uint32_t li = lds_idx(p >> S, p & (LEN - 1), PITCH);
+    out0[dst] = add_mod(pre[0][k], lds[0][li], q);
+    out1[dst] = add_mod(pre[1][k], lds[1][li], q);
+  }
+}
+
 // ---- Rescale in four launches (ring dimensions 2^13 .. 2^17) ----
 // The inverse NTT of the last limb reads it from the input (LastLimbLoad);
 // the forward column pass lifts it to modulus i as it loads (LiftLoad:
@@ -1027,6 +1177,19 @@ void launch_moddown(Context& c, uint64_t* y, uint32_t npoly, uint32_t nq, uint32
   const uint32_t threads = KIND == SINGLE ? G::TPL : 256;
   const uint32_t tiles = KIND == SINGLE ? 1 : (1u << s_other) / lines;
   const char* name = KIND == SINGLE ? "ntt_fwd_single_moddown" : "ntt_fwd_blocks_moddown";
+  if constexpr (BLK && KIND == BLOCKS) {
+    // Both polys of each key switch in one workgroup (blocked y, digits
+    // 1..3): rows per workgroup = one blocked group.
+    constexpr uint32_t pair_lines = 512u >> (S - 2);
+    if (npoly % 2 == 0 && epi.nd >= 1 && epi.nd <= 3) {
+      const dim3 grid((1u << s_other) / pair_lines, npoly / 2, nq);
+      switch (epi.nd) {
+#define CASE(D)                                                                                 case D:                                                                                         FHE_LAUNCH(c, name, (ntt_pass_moddown_pair<S, D>), grid, dim3(512), 0, y, c.d_const,                     c.d_tw_fwd, c.log_n, s_other, epi);                                                return;
+        CASE(1) CASE(2) CASE(3)
+#undef CASE
+      }
+    }
+  }
   switch (epi.nd) {
 #define CASE(D)                                                                               \
   case D:                                                                                     \
