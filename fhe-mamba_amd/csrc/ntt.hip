@@ -749,6 +749,116 @@ __global__ void __launch_bounds__(512)
   }
 }
 
+// First inverse pass of a batched ModDown with both polys of each key
+// switch in one workgroup (the counterpart of ntt_pass_moddown_pair; ND =
+// 1..7 digits, every modulus below 2^60): lane tid forms the P-limb key
+// products of both polys at the same positions, the digits' words read
+// once, runs the first S2 inverse stages of both polys with shared
+// twiddles, and the workgroup stores its rows (one blocked group) to the
+// blocked layout.  The values stay in [0, 4q); N^-1 is applied later.
+template <int S, int ND>
+__global__ void __launch_bounds__(512)
+    ntt_pass_ksk_pair(uint64_t* __restrict__ ext, size_t ps, const ModConst* __restrict__ mc,
+                      const uint64_t* __restrict__ tw_all, uint32_t log_n, uint32_t s_other,
+                      const ModDownEpi e) {
+  constexpr int RHO = 2, R = 4, TPL = 1 << (S - RHO), LINES = 512 / TPL;
+  constexpr int NSP = (S + RHO - 1) / RHO;
+  constexpr uint32_t LEN = 1u << S, PITCH = LEN + LEN / 16 + 1;
+  static_assert(TPL <= 64 && LINES * TPL == 512 && ND > 0 && ND <= 7, "pair ksk pass");
+  __shared__ uint64_t lds[2][LINES * PITCH];
+  const uint32_t n = 1u << log_n, r = blockIdx.y, t = blockIdx.z, tid = threadIdx.x;
+  const uint32_t midx = e.L + t;
+  const uint64_t q = mc[midx].q, q4 = 4 * q, qneg = mc[midx].neg_q, q4neg = mc[midx].neg_q4;
+  const uint64_t* __restrict__ tw = tw_all + (size_t)midx * n * 2;
+  const size_t wg0 = ((size_t)blockIdx.x * LINES) << S;
+  const uint32_t tau = tid % TPL, line = tid / TPL;
+  const uint32_t twbase = (1u << s_other) + blockIdx.x * LINES + line;
+  auto staged = [&](int k) -> uint32_t {
+    return (tid >> 6) * (64u * R) + (uint32_t)(k >> 1) * 128u + 2 * (tid & 63) + (k & 1);
+  };
+
+  // P-limb key products of both polys into LDS (this wavefront's rows).
+  {
+    const size_t dstride = (size_t)e.ne * n, kstride = 2 * e.kl;
+    const uint64_t qn = e.mc[midx].qinv_neg;
+#pragma unroll
+    for (int k = 0; k < R; k += 2) {
+      const uint32_t p = staged(k);
+      const size_t s = wg0 + p;
+      const uint64_t* dg = e.digits[r] + (size_t)(e.nq + t) * n + s;
+      const uint64_t* kr = e.key[r] + (size_t)midx * n + s;
+      ulonglong2 d[ND], k0[ND], k1[ND];
+#pragma unroll
+      for (int j = 0; j < ND; ++j) {
+        d[j] = *reinterpret_cast<const ulonglong2*>(dg + j * dstride);
+        k0[j] = load_stream2(kr + j * kstride);
+        k1[j] = load_stream2(kr + e.kl + j * kstride);
+      }
+      uint64_t v0, v1;
+      const uint32_t l0 = lds_idx(p >> S, p & (LEN - 1), PITCH);
+      const uint32_t l1 = lds_idx((p + 1) >> S, (p + 1) & (LEN - 1), PITCH);
+      key_comb2<ND>(d, k0, q, qn, v0, v1);
+      lds[0][l0] = v0;
+      lds[0][l1] = v1;
+      key_comb2<ND>(d, k1, q, qn, v0, v1);
+      lds[1][l0] = v0;
+      lds[1][l1] = v1;
+    }
+  }
+
+  uint64_t x[2][R];
+#pragma unroll
+  for (int sp = 0; sp < NSP; ++sp) {
+    const int lo = RHO * sp;
+    const int w = lo + RHO <= S ? lo : S - RHO;
+    const int bhi = lo + RHO <= S ? lo + RHO - 1 : S - 1;
+    const uint32_t thi = (tau >> w) << (w + RHO), tlo = tau & ((1u << w) - 1);
+    wave_lds_sync();
+#pragma unroll
+    for (int v = 0; v < R; ++v) {
+      const uint32_t u = thi | ((uint32_t)v << w) | tlo;
+      x[0][v] = lds[0][lds_idx(line, u, PITCH)];
+      x[1][v] = lds[1][lds_idx(line, u, PITCH)];
+    }
+#pragma unroll
+    for (int beta = lo; beta <= bhi; ++beta) {
+      const int d = 1 << (beta - w);
+#pragma unroll
+      for (int v = 0; v < R; ++v) {
+        if (v & d) continue;
+        const uint32_t u = thi | ((uint32_t)v << w) | tlo;
+        const uint32_t ti = (twbase << (S - 1 - beta)) | (u >> (beta + 1));
+        const uint64_t wv = tw[2 * ti], ws = tw[2 * ti + 1];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint64_t X = x[h][v], Y = x[h][v + d];
+          x[h][v + d] = shoup_lazy4n(X + q4 - Y, wv, ws, qneg);
+          x[h][v] = lazy_sub(X + Y, q4neg);
+        }
+      }
+    }
+    wave_lds_sync();
+#pragma unroll
+    for (int v = 0; v < R; ++v) {
+      const uint32_t u = thi | ((uint32_t)v << w) | tlo;
+      lds[0][lds_idx(line, u, PITCH)] = x[0][v];
+      lds[1][lds_idx(line, u, PITCH)] = x[1][v];
+    }
+  }
+  __syncthreads();
+
+  // The blocked group of both polys, word p = u * LINES + row.
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    uint64_t* __restrict__ dst = ext + (size_t)(2 * r + h) * ps + (size_t)t * n + wg0;
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+      const uint32_t p = (uint32_t)k * 512u + tid;
+      dst[p] = lds[h][lds_idx(p % LINES, p / LINES, PITCH)];
+    }
+  }
+}
+
 // ---- Rescale in four launches (ring dimensions 2^13 .. 2^17) ----
 // The inverse NTT of the last limb reads it from the input (LastLimbLoad);
 // the forward column pass lifts it to modulus i as it loads (LiftLoad:
@@ -1215,6 +1325,23 @@ void launch_ksk(Context& c, uint64_t* ext, uint32_t npoly, uint32_t s_other, boo
   const char* name = KIND == SINGLE ? "ntt_inv_single_ksk" : "ntt_inv_blocks_ksk";
   const dim3 grid(tiles, npoly, c.K);
   const size_t ps = (size_t)c.K * c.n;
+  if constexpr (BLK && KIND == BLOCKS) {
+    // Both polys of each key switch in one workgroup (blocked output, digits
+    // 1..3, no final scaling): rows per workgroup = one blocked group.
+    constexpr uint32_t pair_lines = 512u >> (S - 2);
+    if (!last && npoly % 2 == 0 && epi.nd >= 1 && epi.nd <= 3) {
+      const dim3 pgrid((1u << s_other) / pair_lines, npoly / 2, c.K);
+      switch (epi.nd) {
+#define CASE(D)                                                                              \
+  case D:                                                                                    \
+    FHE_LAUNCH(c, name, (ntt_pass_ksk_pair<S, D>), pgrid, dim3(512), 0, ext, ps, c.d_const,  \
+               c.d_tw_inv, c.log_n, s_other, epi);                                           \
+    return;
+        CASE(1) CASE(2) CASE(3)
+#undef CASE
+      }
+    }
+  }
   switch (epi.nd) {
 #define CASE(D)                                                                         \
   case D:                                                                               \
