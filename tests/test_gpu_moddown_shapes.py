@@ -85,6 +85,29 @@ def test_benchmark_shape_rotations():
     assert np.array_equal(got, orc.rotate(low, keys[gal[0]], gal[0]))
 
 
+@pytest.mark.parametrize("log_n,depth,dnum", [(14, 7, 4), (15, 9, 5)])
+def test_many_digits(log_n, depth, dnum):
+    """More than three digits: the fused ModUp converts four or five digits
+    in one launch, and ModDown's first and last passes take the run-time
+    digit-count kernels instead of the paired ones."""
+    q, p = O.gen_moduli(log_n, depth, 50, 60, dnum)
+    ctx, orc = F.Context(log_n, q, p, dnum), O.Ctx(log_n, q, p, dnum)
+    s = orc.secret(12)
+    rng = np.random.default_rng(13)
+    key = orc.relin_key(s, 7)
+    dkey = ctx.load_key(key)
+    for nq in (ctx.L, ctx.L - 3):
+        a = residues(rng, ctx.q[:nq], (1,), ctx.n)
+        assert np.array_equal(ctx.keyswitch(ctx.upload(a), dkey).numpy(), orc.keyswitch(a[0], key)), nq
+    gal = [O.galois_elt(r, ctx.n) for r in (1, -2)]
+    keys = [orc.galois_key(s, g, 40 + i) for i, g in enumerate(gal)]
+    ct = residues(rng, ctx.q, (2,), ctx.n)
+    dct = ctx.upload(ct)
+    outs = ctx.rotate_hoisted(dct, ctx.rotation_precompute(dct), [ctx.load_key(k) for k in keys], gal)
+    for out, k, g in zip(outs, keys, gal):
+        assert np.array_equal(out.numpy(), orc.rotate(ct, k, g)), g
+
+
 def test_full_batch_small_ring():
     """32 hoisted rotations at N=2^13 (64 polys x 64 columns: the 4-wave
     middle kernel with two column lines per wavefront)."""
