@@ -1289,13 +1289,13 @@ void launch_moddown(Context& c, uint64_t* y, uint32_t npoly, uint32_t nq, uint32
   const char* name = KIND == SINGLE ? "ntt_fwd_single_moddown" : "ntt_fwd_blocks_moddown";
   if constexpr (BLK && KIND == BLOCKS) {
     // Both polys of each key switch in one workgroup (blocked y, digits
-    // 1..3): rows per workgroup = one blocked group.
+    // 1..7): rows per workgroup = one blocked group.
     constexpr uint32_t pair_lines = 512u >> (S - 2);
-    if (npoly % 2 == 0 && epi.nd >= 1 && epi.nd <= 3) {
+    if (npoly % 2 == 0 && epi.nd >= 1 && epi.nd <= 7) {
       const dim3 grid((1u << s_other) / pair_lines, npoly / 2, nq);
       switch (epi.nd) {
 #define CASE(D)                                                                                 case D:                                                                                         FHE_LAUNCH(c, name, (ntt_pass_moddown_pair<S, D>), grid, dim3(512), 0, y, c.d_const,                     c.d_tw_fwd, c.log_n, s_other, epi);                                                return;
-        CASE(1) CASE(2) CASE(3)
+        CASE(1) CASE(2) CASE(3) CASE(4) CASE(5) CASE(6) CASE(7)
 #undef CASE
       }
     }
@@ -1327,9 +1327,9 @@ void launch_ksk(Context& c, uint64_t* ext, uint32_t npoly, uint32_t s_other, boo
   const size_t ps = (size_t)c.K * c.n;
   if constexpr (BLK && KIND == BLOCKS) {
     // Both polys of each key switch in one workgroup (blocked output, digits
-    // 1..3, no final scaling): rows per workgroup = one blocked group.
+    // 1..7, no final scaling): rows per workgroup = one blocked group.
     constexpr uint32_t pair_lines = 512u >> (S - 2);
-    if (!last && npoly % 2 == 0 && epi.nd >= 1 && epi.nd <= 3) {
+    if (!last && npoly % 2 == 0 && epi.nd >= 1 && epi.nd <= 7) {
       const dim3 pgrid((1u << s_other) / pair_lines, npoly / 2, c.K);
       switch (epi.nd) {
 #define CASE(D)                                                                              \
@@ -1337,7 +1337,7 @@ void launch_ksk(Context& c, uint64_t* ext, uint32_t npoly, uint32_t s_other, boo
     FHE_LAUNCH(c, name, (ntt_pass_ksk_pair<S, D>), pgrid, dim3(512), 0, ext, ps, c.d_const,  \
                c.d_tw_inv, c.log_n, s_other, epi);                                           \
     return;
-        CASE(1) CASE(2) CASE(3)
+        CASE(1) CASE(2) CASE(3) CASE(4) CASE(5) CASE(6) CASE(7)
 #undef CASE
       }
     }
