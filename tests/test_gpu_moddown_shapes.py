@@ -85,11 +85,11 @@ def test_benchmark_shape_rotations():
     assert np.array_equal(got, orc.rotate(low, keys[gal[0]], gal[0]))
 
 
-@pytest.mark.parametrize("log_n,depth,dnum", [(14, 7, 4), (15, 9, 5)])
+@pytest.mark.parametrize("log_n,depth,dnum", [(14, 7, 4), (15, 9, 5), (13, 15, 8)])
 def test_many_digits(log_n, depth, dnum):
-    """More than three digits: the fused ModUp converts four or five digits
-    in one launch, and ModDown's first and last passes take the run-time
-    digit-count kernels instead of the paired ones."""
+    """More than three digits: the fused ModUp converts four to eight digits
+    in one launch; ModDown's first and last passes run the paired kernels up
+    to seven digits and the run-time digit-count kernels for eight."""
     q, p = O.gen_moduli(log_n, depth, 50, 60, dnum)
     ctx, orc = F.Context(log_n, q, p, dnum), O.Ctx(log_n, q, p, dnum)
     s = orc.secret(12)
