@@ -42,9 +42,9 @@ HBM_PEAK = 8.0e12  # B/s, MI355X HBM3E
 # a plain copy of known size reads back); recorded in
 # profiles/rotation_step_n65536_l24.md together with the commands.
 MEASURED_TRAFFIC = {
-    "ntt_fwd_blocks_moddown": 3_097_276_211 + 755_389_133,
-    "k_moddown_mid": 253_229_466 + 757_191_168,
-    "ntt_inv_blocks_ksk": 776_181_146 + 251_658_240,
+    "ntt_fwd_blocks_moddown": 3_096_813_286 + 755_675_366,
+    "k_moddown_mid": 253_238_067 + 757_507_110,
+    "ntt_inv_blocks_ksk": 776_195_430 + 251_658_240,
 }
 LOG_N, DEPTH, SCALE_BITS, FIRST_BITS, DNUM = 16, 23, 59, 60, 3
 N = 1 << LOG_N
