@@ -94,10 +94,11 @@ class PKESchemeFeature(enum.Enum):
 
 
 # Largest log2(Q*P) per ring dimension for a uniform-ternary secret
-# (HomomorphicEncryption.org standard, classical attacks).
+# (HomomorphicEncryption.org standard, classical attacks), used to pick or
+# check the ring dimension as GenCryptoContext does.
 _HE_STD_MAX_LOGQ = {
     SecurityLevel.HEStd_128_classic: {1024: 27, 2048: 54, 4096: 109, 8192: 218, 16384: 438,
-                                      32768: 881},
+                                      32768: 881, 65536: 1747, 131072: 3523},
     SecurityLevel.HEStd_192_classic: {1024: 19, 2048: 37, 4096: 75, 8192: 152, 16384: 305,
                                       32768: 611},
     SecurityLevel.HEStd_256_classic: {1024: 14, 2048: 29, 4096: 58, 8192: 118, 16384: 237,
@@ -150,6 +151,58 @@ def _log2_qp(q, p) -> float:
     return sum(math.log2(x) for x in list(q) + list(p))
 
 
+# Classical-128 bound on the bit length of Q*P for a uniform-ternary secret
+# with error sigma 3.19 (2024 Security Guidelines, Table 5.2), as the
+# reference tabulates it: native/fideslib_stage0/src/fideslib_security.hpp:18-30.
+CLASSICAL128_MAX_QP_BITS = {1024: 26, 2048: 53, 4096: 106, 8192: 214, 16384: 430, 32768: 868,
+                            65536: 1747, 131072: 3523}
+# Standard deviation of the encryption error.  OpenFHE samples a discrete
+# Gaussian with sigma 3.19; this library draws a centred binomial with
+# eta = 21 (variance 21 / 2, sigma 3.24), never narrower.
+ERROR_SIGMA = math.sqrt(21 / 2)
+
+
+def audit_chain(ring: int, q, p, dnum: int, *, security_level: "SecurityLevel",
+                secret_dist: "SecretKeyDist", sigma: float = ERROR_SIGMA) -> dict:
+    """Classical-128 audit of a HYBRID chain, the fields and rule of the
+    reference's CkksSecurityAudit (fideslib_security.hpp:33-80): exact bit
+    lengths of Q, P and Q*P (not sums of per-prime sizes), the guideline
+    bound for the ring dimension, and a pass only for HEStd_128_classic
+    with a uniform-ternary secret, sigma >= 3.19 and Q*P within the bound."""
+    qprod, pprod = math.prod(int(x) for x in q), math.prod(int(x) for x in p)
+    a = {
+        "ring_dimension": int(ring),
+        "q_bits": qprod.bit_length(),
+        "p_bits": pprod.bit_length(),
+        "qp_bits": (qprod * pprod).bit_length(),
+        "q_towers": len(q),
+        "p_towers": len(p),
+        "hybrid_digits": int(dnum),
+        "error_sigma": float(sigma),
+        "guideline_max_qp_bits": CLASSICAL128_MAX_QP_BITS.get(int(ring), 0),
+        "library_classical128": security_level == SecurityLevel.HEStd_128_classic,
+        "uniform_ternary": secret_dist == SecretKeyDist.UNIFORM_TERNARY,
+        "hybrid": True,
+    }
+    a["passed"] = bool(a["library_classical128"] and a["uniform_ternary"] and a["hybrid"]
+                       and math.isfinite(sigma) and sigma >= 3.19
+                       and a["guideline_max_qp_bits"] and a["q_towers"] and a["p_towers"]
+                       and a["qp_bits"] <= a["guideline_max_qp_bits"])
+    a["basis"] = "2024 Security Guidelines Table 5.2; classical RLWE parameter bound"
+    return a
+
+
+def flexibleauto_scaling_factors(q) -> list[float]:
+    """FLEXIBLEAUTO scaling factor per level (limbs dropped) of the Q chain:
+    sf[0] = q_{L-1} and sf[l] = sf[l-1]^2 / q_{L-l}, in double precision, so
+    that rescaling a degree-2 ciphertext at level l lands on sf[l+1]."""
+    L = len(q)
+    sf = [float(q[-1])]
+    for lev in range(1, L):
+        sf.append(sf[-1] * sf[-1] / float(q[L - lev]))
+    return sf
+
+
 def select_chain(params: CCParamsCKKSRNS):
     """(ring dimension, Q primes, P primes, dnum) for a parameter set.
 
@@ -196,8 +249,11 @@ def GenCryptoContext(params: CCParamsCKKSRNS, seed: int | None = None,
                      device: int = 0) -> "CryptoContext":  # noqa: N802 - OpenFHE name
     """Build the prime chain, key-switching primes and device context.
 
-    `seed` fixes every key and encryption sample drawn through this context
-    (default: fresh from the OS)."""
+    Without `seed` (the default) every key and encryption sample comes from
+    ChaCha20 under a 256-bit master key drawn from OS entropy.  A `seed`
+    selects the seeded sampling family instead: it fixes every sample drawn
+    through this context, which makes runs reproducible for tests and
+    benchmarks and is NOT secure (the public key reveals the seed)."""
     return CryptoContext(params, seed=seed, device=device)
 
 
@@ -206,21 +262,20 @@ class CryptoContext:
         g = params._v
         ring, q, p, self._dnum = select_chain(params)
         self._params = params
-        self._ctx = Context(ring.bit_length() - 1, q, p, self._dnum, device)
+        self._ctx = Context(ring.bit_length() - 1, q, p, self._dnum, device,
+                            sampling="chacha20" if seed is None else "seeded")
         self.n = ring
         self.L = len(q)
         batch = int(g["BatchSize"]) or ring // 2
         if batch & (batch - 1) or batch > ring // 2:
             raise ValueError("BatchSize must be a power of two <= RingDim / 2")
         self._slots = batch
-        # FLEXIBLEAUTO scaling factor per level (limbs dropped).
-        sf = [float(q[-1])]
-        for lev in range(1, self.L):
-            sf.append(sf[-1] * sf[-1] / float(q[self.L - lev]))
-        self._sf = sf
+        self._sf = flexibleauto_scaling_factors(q)
         self._features: set = set()
         self._relin = None
         self._galois: dict = {}
+        # Per-call stream labels.  With ChaCha20 sampling they are public
+        # nonces (the secrecy is the library's master key).
         self._seed = int.from_bytes(os.urandom(8), "little") if seed is None else int(seed)
         self._draws = 0
         self._cache: dict = {}

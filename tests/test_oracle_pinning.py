@@ -403,3 +403,89 @@ def test_sparse_ternary_sampler(h):
         buckets = hits.reshape(16, 256).sum(axis=1)
         assert np.all(np.abs(buckets / buckets.mean() - 1) < 0.05)
         assert abs(signs) < 4 * np.sqrt(400 * h)
+
+
+# ------------------------------------------------------------- plaintext MAC
+@pytest.mark.parametrize("count", [1, 31, 32, 33, 64, 65, 200])
+@pytest.mark.parametrize("extreme", [False, True])
+def test_mac_batch_matches_big_integer_sum(count, extreme):
+    """acc[b][l][e] = sum_i x[i][b][l][e] * w[i][l][e] mod q_l, checked with
+    Python integers.  Counts 31..33 and 64 straddle the oracle's periodic
+    reduction of its 128-bit accumulator (every 32 terms); all-(q-1)
+    operands at 61-bit primes (the largest the library accepts) give the
+    largest partial sums: more than 64 products of (q-1)^2 exceed 2^128
+    unless the accumulator is folded (catches a dropped or misplaced reduction, an
+    overflowing accumulator, or a poly / limb index mix-up between x and w)."""
+    log_n = 3
+    n = 1 << log_n
+    q = O.ntt_friendly_primes(log_n, 61, 1) + O.ntt_friendly_primes(log_n, 60, 1) + \
+        O.ntt_friendly_primes(log_n, 59, 1)
+    c = O.Ctx(log_n, q, [], 1)
+    rng = np.random.default_rng(count)
+    nq = len(q)
+    if extreme:
+        x = np.stack([np.stack([np.full((nq, n), 0, dtype=np.uint64)] * 2)] * count)
+        w = np.zeros((count, nq, n), dtype=np.uint64)
+        for l, ql in enumerate(q):
+            x[:, :, l, :] = ql - 1
+            w[:, l, :] = ql - 1
+    else:
+        x = np.zeros((count, 2, nq, n), dtype=np.uint64)
+        w = np.zeros((count, nq, n), dtype=np.uint64)
+        for l, ql in enumerate(q):
+            x[:, :, l, :] = rng.integers(0, ql, (count, 2, n), dtype=np.uint64)
+            w[:, l, :] = rng.integers(0, ql, (count, n), dtype=np.uint64)
+    got = c.mac(x, w)
+    for b in range(2):
+        for l, ql in enumerate(q):
+            for e in range(n):
+                want = sum(int(x[i, b, l, e]) * int(w[i, l, e]) for i in range(count)) % ql
+                assert int(got[b, l, e]) == want, (b, l, e)
+
+
+# ------------------------------------------------------------- FLEXIBLEAUTO scale table
+def _golden_chain():
+    with open(os.path.join(GOLDEN, "openfhe_prime_chain_n131072.json")) as fh:
+        gold = json.load(fh)
+    return gold["primes"][: gold["num_q"]], gold["primes"][gold["num_q"]:]
+
+
+def test_flexibleauto_scale_matches_openfhe_record():
+    """The reference records OpenFHE's scaling factor of a degree-2
+    ciphertext at level 35 of the 45-prime N=2^17 chain:
+    results/b300/2026-09-28/long-accuracy/replay-controls-smoke/
+    native.json.refresh-replay.json (inputs[0]: level 35, degree 2,
+    scaling_factor 3.3230699877697935e+35).  The table must give exactly
+    that double, and its neighbours must not (catches an off-by-one-prime
+    recursion, which no decryption tolerance can see)."""
+    from fhemamba_amd.ckks import flexibleauto_scaling_factors
+
+    q, _ = _golden_chain()
+    sf = flexibleauto_scaling_factors(q)
+    assert len(sf) == len(q) and sf[0] == float(q[-1])
+    recorded = 3.3230699877697935e+35
+    assert sf[35] * sf[35] == recorded
+    assert sf[34] * sf[34] != recorded and sf[36] * sf[36] != recorded
+
+
+def test_classical128_audit_matches_openfhe_record():
+    """The same run's security audit (native.json `security_audit`):
+    ring 131072, q_bits 2656, p_bits 720, qp_bits 3376, 45 Q towers, 12 P
+    towers, 4 digits, bound 3523, passed -- as fideslib_security.hpp:33-80
+    computes it (exact bit lengths of Q, P and Q*P)."""
+    from fhemamba_amd.ckks import SecretKeyDist, SecurityLevel, audit_chain
+
+    q, p = _golden_chain()
+    a = audit_chain(131072, q, p, 4, security_level=SecurityLevel.HEStd_128_classic,
+                    secret_dist=SecretKeyDist.UNIFORM_TERNARY)
+    assert (a["ring_dimension"], a["q_bits"], a["p_bits"], a["qp_bits"]) == (131072, 2656, 720,
+                                                                            3376)
+    assert (a["q_towers"], a["p_towers"], a["hybrid_digits"]) == (45, 12, 4)
+    assert a["guideline_max_qp_bits"] == 3523 and a["passed"] is True
+    sparse = audit_chain(131072, q, p, 4, security_level=SecurityLevel.HEStd_128_classic,
+                         secret_dist=SecretKeyDist.SPARSE_TERNARY)
+    assert sparse["passed"] is False and sparse["uniform_ternary"] is False
+    # The same 45 + 12 chain at N=2^16 exceeds the 1747-bit bound.
+    small = audit_chain(65536, q, p, 4, security_level=SecurityLevel.HEStd_128_classic,
+                        secret_dist=SecretKeyDist.UNIFORM_TERNARY)
+    assert small["guideline_max_qp_bits"] == 1747 and small["passed"] is False
