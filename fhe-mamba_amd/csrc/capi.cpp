@@ -375,6 +375,9 @@ int fhe_mul_plain(fhe_poly* out, const fhe_poly* ct, const fhe_poly* pt) {
     same_ctx(ct, pt);
     same_ctx(out, ct);
     need(pt->npoly == 1 && pt->nlimb >= ct->nlimb, "plaintext must be one poly at >= limbs");
+    // Reshaping the plaintext's own handle would free it before it is read.
+    need(out != pt || (ct->npoly == 1 && ct->nlimb == pt->nlimb),
+         "output may alias the plaintext only when the shapes match");
     prepare_out(out, ct->npoly, ct->nlimb);
     fhe::poly_mul_plain(*ct->c, out->data, ct->data, pt->data, ct->npoly, ct->nlimb);
   });
@@ -385,6 +388,9 @@ int fhe_add_plain(fhe_poly* out, const fhe_poly* ct, const fhe_poly* pt) {
     same_ctx(ct, pt);
     same_ctx(out, ct);
     need(pt->npoly == 1 && pt->nlimb >= ct->nlimb, "plaintext must be one poly at >= limbs");
+    // Reshaping the plaintext's own handle would free it before it is read.
+    need(out != pt || (ct->npoly == 1 && ct->nlimb == pt->nlimb),
+         "output may alias the plaintext only when the shapes match");
     prepare_out(out, ct->npoly, ct->nlimb);
     fhe::poly_add_plain(*ct->c, out->data, ct->data, pt->data, ct->npoly, ct->nlimb);
   });
@@ -574,8 +580,10 @@ int fhe_rotate_hoisted(const fhe_poly* ct, const fhe_poly* digits, const fhe_key
          "digits do not belong to this ciphertext level");
     for (uint32_t r = 0; r < count; ++r) {
       check_key(ct, keys[r]);
-      need(outs[r] && outs[r]->c == &c && outs[r] != ct, "bad output handle");
+      need(outs[r] && outs[r]->c == &c && outs[r] != ct && outs[r] != digits,
+           "bad output handle");
       need((galois[r] & 1) && galois[r] < 2 * c.n, "Galois element must be odd and < 2N");
+      for (uint32_t s = 0; s < r; ++s) need(outs[s] != outs[r], "outputs must be distinct");
     }
     for (uint32_t r = 0; r < count; ++r) prepare_out(outs[r], 2, nq);
     std::vector<const uint64_t*> kp(count);
@@ -693,10 +701,33 @@ int fhe_decode(fhe_context* ctx, const fhe_poly* pt, uint32_t slots, double scal
   });
 }
 
+int fhe_context_set_sampling(fhe_context* ctx, int mode, const uint8_t* key32) {
+  return guard([&] {
+    need(ctx != nullptr, "null argument");
+    fhe::SamplingKey k;
+    if (mode == FHE_SAMPLING_CHACHA20) {
+      if (key32) {
+        for (int i = 0; i < 8; ++i)
+          k.master[i] = (uint32_t)key32[4 * i] | ((uint32_t)key32[4 * i + 1] << 8) |
+                        ((uint32_t)key32[4 * i + 2] << 16) | ((uint32_t)key32[4 * i + 3] << 24);
+      } else {
+        fhe::fill_entropy(k.master, sizeof(k.master));
+      }
+      k.secure = true;
+    } else {
+      need(mode == FHE_SAMPLING_SEEDED, "sampling mode must be FHE_SAMPLING_CHACHA20 or "
+                                        "FHE_SAMPLING_SEEDED");
+      need(key32 == nullptr, "the seeded sampling family takes no key");
+      k.secure = false;
+    }
+    ctx->c->sampling = k;
+  });
+}
+
 int fhe_keygen_secret(fhe_context* ctx, uint64_t seed, int64_t* s_coef) {
   return guard([&] {
     need(ctx && s_coef, "null argument");
-    fhe::sample_ternary_host(fhe::stream_key(seed, fhe::TAG_SECRET, 0), s_coef, ctx->c->n);
+    fhe::sample_secret_host(*ctx->c, seed, s_coef);
   });
 }
 
@@ -704,8 +735,7 @@ int fhe_keygen_secret_sparse(fhe_context* ctx, uint64_t seed, uint32_t h, int64_
   return guard([&] {
     need(ctx && s_coef, "null argument");
     need(h >= 1 && h <= ctx->c->n, "sparse secret: Hamming weight must be in [1, N]");
-    fhe::sample_sparse_ternary_host(fhe::stream_key(seed, fhe::TAG_SECRET, 0), s_coef,
-                                    ctx->c->n, h);
+    fhe::sample_sparse_secret_host(*ctx->c, seed, s_coef, h);
   });
 }
 

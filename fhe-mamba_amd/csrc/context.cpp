@@ -5,6 +5,8 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <cerrno>
+#include <sys/random.h>
 
 #include "context.hpp"
 #include "params.hpp"
@@ -78,6 +80,21 @@ void Pool::trim() {
   free_.clear();
 }
 
+// Fills buf with bytes from the kernel's CSPRNG (getrandom); fails loudly
+// rather than falling back to anything weaker.
+void fill_entropy(void* buf, size_t bytes) {
+  uint8_t* p = static_cast<uint8_t*>(buf);
+  while (bytes) {
+    const ssize_t got = getrandom(p, bytes, 0);
+    if (got < 0) {
+      if (errno == EINTR) continue;
+      throw std::runtime_error("getrandom failed: no OS entropy for the sampling key");
+    }
+    p += got;
+    bytes -= (size_t)got;
+  }
+}
+
 static uint32_t bitrev(uint32_t x, uint32_t bits) {
   uint32_t r = 0;
   for (uint32_t i = 0; i < bits; ++i) {
@@ -118,6 +135,8 @@ Context::Context(uint32_t log_n_, const uint64_t* q, uint32_t num_q, const uint6
     for (size_t j = 0; j < i; ++j)
       if (mods[j] == qi) throw ArgError("duplicate modulus");
   }
+  fill_entropy(sampling.master, sizeof(sampling.master));
+  sampling.secure = true;
   hip_check(hipSetDevice(device), "hipSetDevice");
   hip_check(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "hipStreamCreate");
   own_stream = true;

@@ -20,6 +20,7 @@
 #include <vector>
 
 #include "modarith.hpp"
+#include "sampling.hpp"
 
 namespace fhe {
 
@@ -108,6 +109,9 @@ class Pool {
   std::multimap<size_t, void*> free_;
 };
 
+// Bytes from the OS CSPRNG (getrandom); throws if none are available.
+void fill_entropy(void* buf, size_t bytes);
+
 struct Context {
   int device = 0;
   hipStream_t stream = nullptr;
@@ -136,6 +140,11 @@ struct Context {
   // Special-FFT twiddles per slot count: (inverse, forward), each [slots-1] x (cos, sin).
   std::mutex fft_mu;
   std::map<uint32_t, std::pair<double*, double*>> fft_tables;
+
+  // Stream family for key generation and encryption: ChaCha20 under a
+  // master key from OS entropy unless the caller sets one (or chooses the
+  // seeded parity family).
+  SamplingKey sampling;
 
   std::unique_ptr<Pool> pool;
   Profiler prof;

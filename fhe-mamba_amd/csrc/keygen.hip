@@ -2,8 +2,9 @@
 //
 // Mirrors OpenFHE's KeyGen / EvalMultKeyGen / EvalRotateKeyGen / Encrypt /
 // Decrypt as called by the reference (native/fideslib_stage0/src/
-// packed_fideslib.cpp:1080-1083, :204-205, :1227) with this library's seeded
-// sampling streams (sampling.hpp):
+// packed_fideslib.cpp:1080-1083, :204-205, :1227) with this library's
+// sampling streams (sampling.hpp; ChaCha20 unless the context was switched
+// to the seeded parity family):
 //   public key      b = -a s + e over Q, a uniform in evaluation form
 //   switching key   digit j: b_j = -a_j s_new + e_j + [P]_{q_i} s_old on the
 //                   Q limbs of digit j (KeySwitchHYBRID key generation)
@@ -40,12 +41,33 @@ __global__ void k_lift_signed(const int64_t* coef, uint64_t* out, const ModConst
   out[(size_t)blockIdx.y * n + e] = r;
 }
 
-// out[j][e] = uniform_mod(stream(seed, tag, index0 + j), e, q_{midx(j)}).
-__global__ void k_uniform(uint64_t* out, const ModConst* mc, uint32_t n, uint64_t seed,
-                          uint64_t tag, uint64_t index_base, uint32_t mod0) {
-  const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x, j = blockIdx.y;
-  const uint64_t key = stream_key(seed, tag, index_base | j);
-  out[(size_t)j * n + e] = uniform_mod(key, e, mc[mod0 + j].q);
+// out[j][e] = uniform mod q_{mod0+j} from words 2e, 2e+1 of stream
+// (seed, tag, index_base | j); each thread draws four consecutive samples
+// (one ChaCha20 block).  `base` carries the family, the call key and the
+// tag; the limb's index goes into the nonce here.
+__global__ void k_uniform(uint64_t* out, const ModConst* mc, uint32_t n, Stream base,
+                          uint64_t seed, uint64_t tag, uint64_t index_base, uint32_t mod0) {
+  const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x, j = blockIdx.y;
+  const uint64_t q = mc[mod0 + j].q;
+  uint64_t w[8];
+  if (base.secure) {
+    Stream s = base;
+    s.nonce[1] = (uint32_t)(index_base | j);
+    stream_block(s, t, w);
+  } else {
+    const uint64_t key = stream_key(seed, tag, index_base | j);
+    for (int i = 0; i < 8; ++i) w[i] = draw(key, 8ull * t + i);
+  }
+  uint64_t* o = out + (size_t)j * n + 4ull * t;
+  for (int i = 0; i < 4; ++i) o[i] = uniform_from(w[2 * i], w[2 * i + 1], q);
+}
+
+void launch_uniform(Context& c, uint64_t* out, uint32_t nlimb, uint64_t seed, uint64_t tag,
+                    uint64_t index_base, uint32_t mod0) {
+  const Stream base = make_stream(c.sampling, seed, tag, 0);
+  const uint32_t quads = c.n / 4, tpb = quads < TPB ? quads : TPB;
+  FHE_LAUNCH(c, "k_uniform", k_uniform, dim3(quads / tpb, nlimb), dim3(tpb), 0, out, c.d_const,
+             c.n, base, seed, tag, index_base, mod0);
 }
 
 // b = e - a * s (+ f * s_old when f is given); all [nlimb][N], limb j uses
@@ -105,9 +127,11 @@ void signed_small_to_eval(Context& c, const std::vector<int64_t>& coef, uint32_t
 
 }  // namespace
 
-void sample_ternary_host(uint64_t key, int64_t* out, uint32_t n) { sample_ternary(key, out, n); }
-void sample_sparse_ternary_host(uint64_t key, int64_t* out, uint32_t n, uint32_t h) {
-  sample_sparse_ternary(key, out, n, h);
+void sample_secret_host(Context& c, uint64_t seed, int64_t* out) {
+  sample_ternary(make_stream(c.sampling, seed, TAG_SECRET, 0), out, c.n);
+}
+void sample_sparse_secret_host(Context& c, uint64_t seed, int64_t* out, uint32_t h) {
+  sample_sparse_ternary(make_stream(c.sampling, seed, TAG_SECRET, 0), out, c.n, h);
 }
 
 void signed_to_eval(Context& c, const int64_t* coef_host, uint32_t idx0, uint32_t nlimb,
@@ -121,10 +145,10 @@ void keygen_public(Context& c, const int64_t* s_coef, uint64_t seed, uint64_t* p
   Scratch s(c, c.L * n), e(c, c.L * n);
   signed_to_eval(c, s_coef, 0, c.L, s.p);
   std::vector<int64_t> ec(n);
-  sample_cbd(stream_key(seed, TAG_PK_E, 0), ec.data(), c.n);
+  sample_cbd(make_stream(c.sampling, seed, TAG_PK_E, 0), ec.data(), c.n);
   signed_small_to_eval(c, ec, 0, c.L, e.p);
   uint64_t* a = pk + (size_t)c.L * n;
-  FHE_LAUNCH(c, "k_uniform", k_uniform, dim3(c.n / tpb_for(c), c.L), dim3(tpb_for(c)), 0, a, c.d_const, c.n, seed, (uint64_t)TAG_PK_A, 0ull, 0u);
+  launch_uniform(c, a, c.L, seed, TAG_PK_A, 0, 0);
   FHE_LAUNCH(c, "k_key_combine", k_key_combine, dim3(c.n / tpb_for(c), c.L), dim3(tpb_for(c)), 0, pk, a, s.p, e.p, nullptr, nullptr, c.d_const, c.n, 0u);
   hip_check(hipStreamSynchronize(c.stream), "keygen sync");
 }
@@ -144,13 +168,13 @@ void keygen_switch(Context& c, const uint64_t* s_old, const uint64_t* s_new, uin
   std::vector<uint64_t> fac(nm);
   for (uint32_t j = 0; j < c.dnum; ++j) {
     const uint32_t s = j * c.alpha, end = s + c.alpha < c.L ? s + c.alpha : c.L;
-    sample_cbd(stream_key(seed, tag + TAG_KSK_E, j), ec.data(), c.n);
+    sample_cbd(make_stream(c.sampling, seed, tag + TAG_KSK_E, j), ec.data(), c.n);
     signed_small_to_eval(c, ec, 0, nm, e.p);
     for (uint32_t i = 0; i < nm; ++i) fac[i] = (i >= s && i < end) ? pmod[i] : 0;
     hip_check(hipMemcpyAsync(f.p, fac.data(), nm * 8, hipMemcpyHostToDevice, c.stream), "fac");
     uint64_t* b = key + ((size_t)j * 2) * nm * n;
     uint64_t* a = b + (size_t)nm * n;
-    FHE_LAUNCH(c, "k_uniform", k_uniform, dim3(c.n / tpb_for(c), nm), dim3(tpb_for(c)), 0, a, c.d_const, c.n, seed, tag + TAG_KSK_A, (uint64_t)j << 16, 0u);
+    launch_uniform(c, a, nm, seed, tag + TAG_KSK_A, (uint64_t)j << 16, 0);
     FHE_LAUNCH(c, "k_key_combine", k_key_combine, dim3(c.n / tpb_for(c), nm), dim3(tpb_for(c)), 0, b, a, s_new, e.p, s_old, f.p, c.d_const, c.n, 0u);
     hip_check(hipStreamSynchronize(c.stream), "keygen sync");
   }
@@ -178,11 +202,11 @@ void encrypt_pk(Context& c, const uint64_t* pk, const uint64_t* m, uint32_t nq, 
   const size_t n = c.n;
   Scratch v(c, nq * n), e0(c, nq * n), e1(c, nq * n);
   std::vector<int64_t> tmp(n);
-  sample_ternary(stream_key(seed, TAG_ENC_V, 0), tmp.data(), c.n);
+  sample_ternary(make_stream(c.sampling, seed, TAG_ENC_V, 0), tmp.data(), c.n);
   signed_small_to_eval(c, tmp, 0, nq, v.p);
-  sample_cbd(stream_key(seed, TAG_ENC_E, 0), tmp.data(), c.n);
+  sample_cbd(make_stream(c.sampling, seed, TAG_ENC_E, 0), tmp.data(), c.n);
   signed_small_to_eval(c, tmp, 0, nq, e0.p);
-  sample_cbd(stream_key(seed, TAG_ENC_E, 1), tmp.data(), c.n);
+  sample_cbd(make_stream(c.sampling, seed, TAG_ENC_E, 1), tmp.data(), c.n);
   signed_small_to_eval(c, tmp, 0, nq, e1.p);
   FHE_LAUNCH(c, "k_encrypt", k_encrypt, dim3(c.n / tpb_for(c), nq), dim3(tpb_for(c)), 0, ct, pk, v.p, e0.p, e1.p, m, c.d_const, c.n, nq, c.L);
 }

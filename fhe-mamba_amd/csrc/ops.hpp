@@ -116,8 +116,8 @@ void decode(Context& c, const uint64_t* pt, uint32_t nlimb, uint32_t slots, doub
             double* re, double* im);
 
 // ---- key material (keygen.hip) ----
-void sample_ternary_host(uint64_t key, int64_t* out, uint32_t n);
-void sample_sparse_ternary_host(uint64_t key, int64_t* out, uint32_t n, uint32_t h);
+void sample_secret_host(Context& c, uint64_t seed, int64_t* out);
+void sample_sparse_secret_host(Context& c, uint64_t seed, int64_t* out, uint32_t h);
 void signed_to_eval(Context& c, const int64_t* coef_host, uint32_t idx0, uint32_t nlimb,
                     uint64_t* out);
 void keygen_public(Context& c, const int64_t* s_coef, uint64_t seed, uint64_t* pk);

@@ -35,13 +35,19 @@ def gen_moduli(log_n: int, depth: int, scale_bits: int, first_bits: int, dnum: i
 class Context:
     """Device context over Q = q[0..L) and P = p[0..K) for ring 2^log_n."""
 
-    def __init__(self, log_n: int, q, p, dnum: int, device: int = 0):
+    def __init__(self, log_n: int, q, p, dnum: int, device: int = 0,
+                 sampling: str = "chacha20", sampling_key: bytes | None = None):
+        """sampling: "chacha20" (default; keys and encryption samples from
+        ChaCha20 under a 32-byte master key, `sampling_key` or fresh OS
+        entropy) or "seeded" (the seed of each call alone fixes its samples:
+        reproducible for parity tests, not secure)."""
         qa = np.ascontiguousarray(q, dtype=np.uint64)
         pa = np.ascontiguousarray(p if len(p) else [0], dtype=np.uint64)
         h = ctypes.c_void_p()
         call("fhe_context_create", log_n, _ptr(qa), len(qa), _ptr(pa), len(p), dnum, device,
              ctypes.byref(h))
         self._h = h
+        self.set_sampling(sampling, sampling_key)
         info = np.zeros(5, dtype=np.uint32)
         call("fhe_context_info", h, _ptr(info))
         self.log_n, self.L, self.K, self.dnum, self.alpha = (int(x) for x in info)
@@ -58,6 +64,20 @@ class Context:
         if self._h is None:
             raise ValueError("context is closed")
         return self._h
+
+    def set_sampling(self, sampling: str = "chacha20", key: bytes | None = None):
+        if sampling == "chacha20":
+            if key is not None and len(key) != 32:
+                raise ValueError("the ChaCha20 sampling key is 32 bytes")
+            buf = None if key is None else ctypes.create_string_buffer(bytes(key), 32)
+            call("fhe_context_set_sampling", self.handle, 0, buf)
+        elif sampling == "seeded":
+            if key is not None:
+                raise ValueError("the seeded sampling family takes no key")
+            call("fhe_context_set_sampling", self.handle, 1, None)
+        else:
+            raise ValueError(f"unknown sampling family {sampling!r}")
+        self.sampling = sampling
 
     def close(self):
         if getattr(self, "_h", None):

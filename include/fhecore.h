@@ -211,11 +211,26 @@ int fhe_decode(fhe_context *ctx, const fhe_poly *pt, uint32_t slots,
                double scale, double *re, double *im);
 
 /* ---- client-side key material and encryption ---------------------------
- * Seeded ternary secret (N int64 coefficients) and the public / switching
- * keys derived from it (KeyGen, EvalMultKeyGen, EvalRotateKeyGen:
+ * Every sample below is drawn from a stream named by (seed, sample kind,
+ * limb / digit).  A new context uses the ChaCha20 family under a 256-bit
+ * master key from OS entropy: secure, and the seed is only a per-call
+ * label.  fhe_context_set_sampling replaces the master key
+ * (FHE_SAMPLING_CHACHA20 with key32 = 32 bytes, or NULL for fresh OS
+ * entropy) or selects the seeded family (FHE_SAMPLING_SEEDED, key32 NULL):
+ * there the seed alone fixes every sample, which makes keys reproducible
+ * for parity tests and NOT secure (a public key reveals the seed).  Takes
+ * effect for later calls.  No counterpart in the reference: OpenFHE draws
+ * from its own PRNG (packed_fideslib.cpp:1080-1083). */
+enum {
+  FHE_SAMPLING_CHACHA20 = 0,
+  FHE_SAMPLING_SEEDED = 1
+};
+int fhe_context_set_sampling(fhe_context *ctx, int mode, const uint8_t *key32);
+/* Ternary secret (N int64 coefficients) and the public / switching keys
+ * derived from it (KeyGen, EvalMultKeyGen, EvalRotateKeyGen:
  * packed_fideslib.cpp:1080-1083). */
 int fhe_keygen_secret(fhe_context *ctx, uint64_t seed, int64_t *s_coef);
-/* Seeded sparse-ternary secret with exactly h nonzero coefficients (+-1):
+/* Sparse-ternary secret with exactly h nonzero coefficients (+-1):
  * KeyGen under SetSecretKeyDist(SPARSE_TERNARY), the Mamba-2 decoder's
  * default (native/fideslib_stage0/src/stage1_mamba2_decode_fideslib.cpp:
  * 1225, stage1_mamba2_config.hpp:211).  1 <= h <= N, else FHE_ERR_ARG. */

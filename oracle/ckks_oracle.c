@@ -673,14 +673,22 @@ void orc_relinearize(const orc_ctx *c, const uint64_t *ct3, uint32_t nq,
 }
 
 /* ======================================================================
- * Deterministic sampling.  The stream definition is shared with the HIP
- * library's key generation so that both produce identical keys.
- *   draw(key, i)  = fmix64(key + (i + 1) * 0x9E3779B97F4A7C15)  (SplitMix64)
- *   uniform mod q = floor((draw(2i) * 2^64 + draw(2i+1)) * q / 2^128)
- *   ternary       = {0, 1, -1}[draw(i) mod 3]
+ * Sampling streams.  The definition is shared with the HIP library's key
+ * generation so that both produce identical keys.  Sample word i of the
+ * stream named (seed, tag, index) comes from one of two families:
+ *   seeded (the default here; parity only, not secure):
+ *     key    = fmix64(seed ^ fmix64((tag << 32) ^ index ^ 0x5851F42D4C957F2D))
+ *     word i = fmix64(key + (i + 1) * 0x9E3779B97F4A7C15)        (SplitMix64)
+ *   ChaCha20 (RFC 8439) under a 256-bit master key (orc_set_sampling_key):
+ *     K1     = ChaCha20Block(master, 0, nonce (lo32 seed, hi32 seed, 0))[0..7]
+ *     word i = 64-bit little-endian word i of the keystream under K1 with
+ *              nonce (tag, index, 1), block counter i / 8
+ * Samples from words:
+ *   uniform mod q = floor((word(2i) * 2^64 + word(2i+1)) * q / 2^128)
+ *   ternary       = {0, 1, -1}[word(i) mod 3]
  *   sparse ternary (Hamming weight h): for i < h swap position i with
- *                   i + floor(draw(2i) (n - i) / 2^64) of 0..n-1 (partial
- *                   Fisher-Yates), that position gets (draw(2i+1) & 1) ? -1 : 1
+ *                   i + floor(word(2i) (n - i) / 2^64) of 0..n-1 (partial
+ *                   Fisher-Yates), that position gets (word(2i+1) & 1) ? -1 : 1
  *   error         = centred binomial, eta = 21 (sigma ~ 3.24)
  * ====================================================================== */
 static inline uint64_t fmix64(uint64_t z) {
@@ -697,43 +705,145 @@ uint64_t orc_stream_key(uint64_t seed, uint64_t tag, uint64_t index) {
   return fmix64(seed ^ fmix64((tag << 32) ^ index ^ 0x5851F42D4C957F2Dull));
 }
 
-void orc_sample_uniform(uint64_t key, uint64_t q, uint64_t *out, uint32_t n) {
+static inline uint32_t rotl32(uint32_t x, int r) { return (x << r) | (x >> (32 - r)); }
+
+/* RFC 8439 section 2.3, written from the RFC's quarter-round definition. */
+void orc_chacha20_block(const uint32_t key[8], uint32_t counter, const uint32_t nonce[3],
+                        uint32_t out[16]) {
+  uint32_t st[16] = {0x61707865u, 0x3320646eu, 0x79622d32u, 0x6b206574u,
+                     key[0], key[1], key[2], key[3], key[4], key[5], key[6], key[7],
+                     counter, nonce[0], nonce[1], nonce[2]};
+  uint32_t x[16];
+  static const int qr[8][4] = {{0, 4, 8, 12}, {1, 5, 9, 13}, {2, 6, 10, 14}, {3, 7, 11, 15},
+                               {0, 5, 10, 15}, {1, 6, 11, 12}, {2, 7, 8, 13}, {3, 4, 9, 14}};
+  memcpy(x, st, sizeof(x));
+  for (int r = 0; r < 10; ++r)
+    for (int k = 0; k < 8; ++k) {
+      uint32_t *a = &x[qr[k][0]], *b = &x[qr[k][1]], *c = &x[qr[k][2]], *d = &x[qr[k][3]];
+      *a += *b; *d ^= *a; *d = rotl32(*d, 16);
+      *c += *d; *b ^= *c; *b = rotl32(*b, 12);
+      *a += *b; *d ^= *a; *d = rotl32(*d, 8);
+      *c += *d; *b ^= *c; *b = rotl32(*b, 7);
+    }
+  for (int i = 0; i < 16; ++i) out[i] = x[i] + st[i];
+}
+
+static int g_secure = 0;
+static uint32_t g_master[8];
+
+void orc_set_sampling_key(const uint8_t *key32) {
+  g_secure = key32 != NULL;
+  for (int i = 0; key32 && i < 8; ++i)
+    g_master[i] = (uint32_t)key32[4 * i] | ((uint32_t)key32[4 * i + 1] << 8) |
+                  ((uint32_t)key32[4 * i + 2] << 16) | ((uint32_t)key32[4 * i + 3] << 24);
+}
+
+typedef struct {
+  int secure;
+  uint32_t key[8], nonce[3];
+  uint64_t sm, cached, buf[8];
+} orc_stream;
+
+static orc_stream stream_open(uint64_t seed, uint64_t tag, uint64_t index) {
+  orc_stream s;
+  memset(&s, 0, sizeof(s));
+  s.secure = g_secure;
+  s.cached = ~0ull;
+  if (!g_secure) {
+    s.sm = orc_stream_key(seed, tag, index);
+    return s;
+  }
+  uint32_t n0[3] = {(uint32_t)seed, (uint32_t)(seed >> 32), 0u}, blk[16];
+  orc_chacha20_block(g_master, 0u, n0, blk);
+  memcpy(s.key, blk, sizeof(s.key));
+  s.nonce[0] = (uint32_t)tag;
+  s.nonce[1] = (uint32_t)index;
+  s.nonce[2] = 1u;
+  return s;
+}
+
+static uint64_t stream_word(orc_stream *s, uint64_t i) {
+  if (!s->secure) return orc_draw(s->sm, i);
+  if (s->cached != i / 8) {
+    uint32_t o[16];
+    orc_chacha20_block(s->key, (uint32_t)(i / 8), s->nonce, o);
+    for (int k = 0; k < 8; ++k) s->buf[k] = (uint64_t)o[2 * k] | ((uint64_t)o[2 * k + 1] << 32);
+    s->cached = i / 8;
+  }
+  return s->buf[i % 8];
+}
+
+static orc_stream seeded_stream(uint64_t key) {
+  orc_stream s;
+  memset(&s, 0, sizeof(s));
+  s.sm = key;
+  return s;
+}
+
+static void sample_uniform(orc_stream *st, uint64_t q, uint64_t *out, uint32_t n) {
   for (uint32_t i = 0; i < n; ++i) {
-    uint64_t hi = orc_draw(key, 2 * (uint64_t)i), lo = orc_draw(key, 2 * (uint64_t)i + 1);
+    uint64_t hi = stream_word(st, 2 * (uint64_t)i), lo = stream_word(st, 2 * (uint64_t)i + 1);
     u128 t = (u128)hi * q + (uint64_t)(((u128)lo * q) >> 64);
     out[i] = (uint64_t)(t >> 64);
   }
 }
 
-void orc_sample_ternary(uint64_t key, int64_t *out, uint32_t n) {
+static void sample_ternary(orc_stream *st, int64_t *out, uint32_t n) {
   for (uint32_t i = 0; i < n; ++i) {
-    uint64_t d = orc_draw(key, i) % 3;
+    uint64_t d = stream_word(st, i) % 3;
     out[i] = d == 0 ? 0 : (d == 1 ? 1 : -1);
   }
 }
 
-void orc_sample_sparse_ternary(uint64_t key, int64_t *out, uint32_t n, uint32_t h) {
+static void sample_sparse_ternary(orc_stream *st, int64_t *out, uint32_t n, uint32_t h) {
   uint32_t *idx = malloc(sizeof(uint32_t) * n);
   for (uint32_t i = 0; i < n; ++i) {
     idx[i] = i;
     out[i] = 0;
   }
   for (uint32_t i = 0; i < h && i < n; ++i) {
-    uint32_t j = i + (uint32_t)(((u128)orc_draw(key, 2 * (uint64_t)i) * (n - i)) >> 64);
+    uint32_t j = i + (uint32_t)(((u128)stream_word(st, 2 * (uint64_t)i) * (n - i)) >> 64);
     uint32_t t = idx[i];
     idx[i] = idx[j];
     idx[j] = t;
-    out[idx[i]] = (orc_draw(key, 2 * (uint64_t)i + 1) & 1) ? -1 : 1;
+    out[idx[i]] = (stream_word(st, 2 * (uint64_t)i + 1) & 1) ? -1 : 1;
   }
   free(idx);
 }
 
-void orc_sample_cbd(uint64_t key, int64_t *out, uint32_t n) {
+static void sample_cbd(orc_stream *st, int64_t *out, uint32_t n) {
   for (uint32_t i = 0; i < n; ++i) {
-    uint64_t d = orc_draw(key, i);
+    uint64_t d = stream_word(st, i);
     out[i] = (int64_t)__builtin_popcountll(d & 0x1FFFFFull) -
              (int64_t)__builtin_popcountll((d >> 21) & 0x1FFFFFull);
   }
+}
+
+/* Seeded-family samplers on an explicit SplitMix64 stream key. */
+void orc_sample_uniform(uint64_t key, uint64_t q, uint64_t *out, uint32_t n) {
+  orc_stream s = seeded_stream(key);
+  sample_uniform(&s, q, out, n);
+}
+
+void orc_sample_ternary(uint64_t key, int64_t *out, uint32_t n) {
+  orc_stream s = seeded_stream(key);
+  sample_ternary(&s, out, n);
+}
+
+void orc_sample_sparse_ternary(uint64_t key, int64_t *out, uint32_t n, uint32_t h) {
+  orc_stream s = seeded_stream(key);
+  sample_sparse_ternary(&s, out, n, h);
+}
+
+void orc_sample_cbd(uint64_t key, int64_t *out, uint32_t n) {
+  orc_stream s = seeded_stream(key);
+  sample_cbd(&s, out, n);
+}
+
+/* Word i of stream (seed, tag, index) of the current family. */
+uint64_t orc_stream_word(uint64_t seed, uint64_t tag, uint64_t index, uint64_t i) {
+  orc_stream s = stream_open(seed, tag, index);
+  return stream_word(&s, i);
 }
 
 enum {
@@ -763,11 +873,17 @@ void orc_signed_to_eval(const orc_ctx *c, const int64_t *coef, uint32_t idx0,
 }
 
 void orc_keygen_secret(uint64_t seed, uint32_t n, int64_t *s_coef) {
-  orc_sample_ternary(orc_stream_key(seed, TAG_SECRET, 0), s_coef, n);
+  {
+    orc_stream st = stream_open(seed, TAG_SECRET, 0);
+    sample_ternary(&st, s_coef, n);
+  }
 }
 
 void orc_keygen_secret_sparse(uint64_t seed, uint32_t n, uint32_t h, int64_t *s_coef) {
-  orc_sample_sparse_ternary(orc_stream_key(seed, TAG_SECRET, 0), s_coef, n, h);
+  {
+    orc_stream st = stream_open(seed, TAG_SECRET, 0);
+    sample_sparse_ternary(&st, s_coef, n, h);
+  }
 }
 
 void orc_keygen_public(const orc_ctx *c, const int64_t *s_coef, uint64_t seed,
@@ -776,12 +892,18 @@ void orc_keygen_public(const orc_ctx *c, const int64_t *s_coef, uint64_t seed,
   uint64_t *s = malloc(sizeof(uint64_t) * L * n), *e = malloc(sizeof(uint64_t) * L * n);
   int64_t *ec = malloc(sizeof(int64_t) * n);
   orc_signed_to_eval(c, s_coef, 0, L, s);
-  orc_sample_cbd(orc_stream_key(seed, TAG_PK_E, 0), ec, n);
+  {
+    orc_stream st = stream_open(seed, TAG_PK_E, 0);
+    sample_cbd(&st, ec, n);
+  }
   orc_signed_to_eval(c, ec, 0, L, e);
   for (uint32_t i = 0; i < L; ++i) {
     uint64_t q = c->mods[i];
     uint64_t *a = pk + ((size_t)L + i) * n, *b = pk + (size_t)i * n;
-    orc_sample_uniform(orc_stream_key(seed, TAG_PK_A, i), q, a, n);
+    {
+      orc_stream st = stream_open(seed, TAG_PK_A, i);
+      sample_uniform(&st, q, a, n);
+    }
     for (uint32_t k = 0; k < n; ++k) {
       size_t o = (size_t)i * n + k;
       b[k] = submod(e[o], orc_mulmod(a[k], s[o], q), q);
@@ -802,13 +924,19 @@ void orc_keygen_switch(const orc_ctx *c, const uint64_t *s_old_qp,
   int64_t *ec = malloc(sizeof(int64_t) * n);
   for (uint32_t j = 0; j < c->dnum; ++j) {
     uint32_t s = j * c->alpha, end = s + c->alpha < L ? s + c->alpha : L;
-    orc_sample_cbd(orc_stream_key(seed, tag + TAG_KSK_E, j), ec, n);
+    {
+      orc_stream st = stream_open(seed, tag + TAG_KSK_E, j);
+      sample_cbd(&st, ec, n);
+    }
     orc_signed_to_eval(c, ec, 0, nm, e);
     for (uint32_t i = 0; i < nm; ++i) {
       uint64_t q = c->mods[i];
       uint64_t *b = key + (((size_t)j * 2 + 0) * nm + i) * n;
       uint64_t *a = key + (((size_t)j * 2 + 1) * nm + i) * n;
-      orc_sample_uniform(orc_stream_key(seed, tag + TAG_KSK_A, ((uint64_t)j << 16) | i), q, a, n);
+      {
+        orc_stream st = stream_open(seed, tag + TAG_KSK_A, ((uint64_t)j << 16) | i);
+        sample_uniform(&st, q, a, n);
+      }
       uint64_t pmod = 1;
       for (uint32_t k = 0; k < K; ++k) pmod = orc_mulmod(pmod, c->mods[L + k] % q, q);
       int in_digit = i >= s && i < end;
@@ -867,11 +995,20 @@ void orc_encrypt_pk(const orc_ctx *c, const uint64_t *pk, const uint64_t *m,
   int64_t *vc = malloc(sizeof(int64_t) * n), *ec = malloc(sizeof(int64_t) * n);
   uint64_t *v = malloc(sizeof(uint64_t) * nq * n), *e0 = malloc(sizeof(uint64_t) * nq * n),
            *e1 = malloc(sizeof(uint64_t) * nq * n);
-  orc_sample_ternary(orc_stream_key(seed, TAG_ENC_V, 0), vc, n);
+  {
+    orc_stream st = stream_open(seed, TAG_ENC_V, 0);
+    sample_ternary(&st, vc, n);
+  }
   orc_signed_to_eval(c, vc, 0, nq, v);
-  orc_sample_cbd(orc_stream_key(seed, TAG_ENC_E, 0), ec, n);
+  {
+    orc_stream st = stream_open(seed, TAG_ENC_E, 0);
+    sample_cbd(&st, ec, n);
+  }
   orc_signed_to_eval(c, ec, 0, nq, e0);
-  orc_sample_cbd(orc_stream_key(seed, TAG_ENC_E, 1), ec, n);
+  {
+    orc_stream st = stream_open(seed, TAG_ENC_E, 1);
+    sample_cbd(&st, ec, n);
+  }
   orc_signed_to_eval(c, ec, 0, nq, e1);
   for (uint32_t i = 0; i < nq; ++i) {
     uint64_t q = c->mods[i];

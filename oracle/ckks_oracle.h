@@ -121,6 +121,14 @@ void orc_sample_uniform(uint64_t key, uint64_t q, uint64_t *out, uint32_t n);
 void orc_sample_ternary(uint64_t key, int64_t *out, uint32_t n);
 void orc_sample_cbd(uint64_t key, int64_t *out, uint32_t n);
 void orc_sample_sparse_ternary(uint64_t key, int64_t *out, uint32_t n, uint32_t h);
+/* ChaCha20 block function (RFC 8439 section 2.3). */
+void orc_chacha20_block(const uint32_t key[8], uint32_t counter, const uint32_t nonce[3],
+                        uint32_t out[16]);
+/* Sampling family of every later key generation / encryption call: NULL
+ * selects the seeded family (the default), a 32-byte key the ChaCha20
+ * family under that master key. */
+void orc_set_sampling_key(const uint8_t *key32);
+uint64_t orc_stream_word(uint64_t seed, uint64_t tag, uint64_t index, uint64_t i);
 
 /* Signed small coefficients -> evaluation form over modulus indices
  * [idx0, idx0+nlimb). */

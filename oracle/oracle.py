@@ -71,6 +71,9 @@ def _load():
         "orc_sample_ternary": (None, [_u64, _p, _u32]),
         "orc_sample_cbd": (None, [_u64, _p, _u32]),
         "orc_signed_to_eval": (None, [_p, _p, _u32, _u32, _p]),
+        "orc_chacha20_block": (None, [_p, _u32, _p, _p]),
+        "orc_set_sampling_key": (None, [_p]),
+        "orc_stream_word": (_u64, [_u64, _u64, _u64, _u64]),
         "orc_keygen_secret": (None, [_u64, _u32, _p]),
         "orc_keygen_secret_sparse": (None, [_u64, _u32, _u32, _p]),
         "orc_keygen_public": (None, [_p, _p, _u64, _p]),
@@ -93,6 +96,34 @@ def _load():
 
 
 lib = _load()
+
+
+class sampling_key:
+    """Context manager: the ChaCha20 sampling family under `key` (32 bytes)
+    for the oracle's key generation and encryption inside the block; the
+    seeded family (the oracle's default) again afterwards."""
+
+    def __init__(self, key: bytes):
+        if len(key) != 32:
+            raise ValueError("the ChaCha20 sampling key is 32 bytes")
+        self.key = ctypes.create_string_buffer(bytes(key), 32)
+
+    def __enter__(self):
+        lib.orc_set_sampling_key(self.key)
+        return self
+
+    def __exit__(self, *exc):
+        lib.orc_set_sampling_key(None)
+        return False
+
+
+def chacha20_block(key: bytes, counter: int, nonce: bytes) -> bytes:
+    """RFC 8439 ChaCha20 block: 64 bytes of keystream."""
+    k = np.frombuffer(bytes(key), dtype="<u4").astype(np.uint32).copy()
+    nc = np.frombuffer(bytes(nonce), dtype="<u4").astype(np.uint32).copy()
+    out = np.zeros(16, dtype=np.uint32)
+    lib.orc_chacha20_block(k.ctypes.data, counter, nc.ctypes.data, out.ctypes.data)
+    return out.astype("<u4").tobytes()
 
 
 def ptr(a: np.ndarray) -> int:

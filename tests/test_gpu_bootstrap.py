@@ -125,7 +125,7 @@ def test_sparse_secret_matches_oracle():
     """The library's seeded sparse-ternary sampler equals the oracle's."""
     import oracle as O
     q, p = O.gen_moduli(LOG_N, 6, 45, 60, 3)
-    ctx, orc = F.Context(LOG_N, q, p, 3), O.Ctx(LOG_N, q, p, 3)
+    ctx, orc = F.Context(LOG_N, q, p, 3, sampling="seeded"), O.Ctx(LOG_N, q, p, 3)
     for seed, h in ((3, 192), (4, 64), (5, 1 << LOG_N)):
         s = ctx.keygen_secret_sparse(seed, h)
         assert int(np.count_nonzero(s)) == h

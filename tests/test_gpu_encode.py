@@ -13,7 +13,7 @@ F = pytest.importorskip("fhemamba_amd")
 def pair(request):
     log_n, depth, sb = request.param
     q, p = O.gen_moduli(log_n, depth, sb, 60, 2)
-    return F.Context(log_n, q, p, 2), O.Ctx(log_n, q, p, 2)
+    return F.Context(log_n, q, p, 2, sampling="seeded"), O.Ctx(log_n, q, p, 2)
 
 
 @pytest.mark.parametrize("slots_div", [2, 8, 64])

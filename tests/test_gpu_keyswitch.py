@@ -19,7 +19,7 @@ PARAMS = [(13, 7, 50, 60, 2), (12, 6, 45, 60, 3), (11, 4, 40, 60, 1)]
 def setup(request):
     log_n, depth, sb, fb, dnum = request.param
     q, p = O.gen_moduli(log_n, depth, sb, fb, dnum)
-    ctx, orc = F.Context(log_n, q, p, dnum), O.Ctx(log_n, q, p, dnum)
+    ctx, orc = F.Context(log_n, q, p, dnum, sampling="seeded"), O.Ctx(log_n, q, p, dnum)
     s = orc.secret(11)
     return ctx, orc, s
 

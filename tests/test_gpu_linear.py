@@ -18,7 +18,7 @@ PARAMS = [(12, 5, 45, 60, 2), (11, 4, 40, 60, 3)]
 def setup(request):
     log_n, depth, sb, fb, dnum = request.param
     q, p = O.gen_moduli(log_n, depth, sb, fb, dnum)
-    ctx, orc = F.Context(log_n, q, p, dnum), O.Ctx(log_n, q, p, dnum)
+    ctx, orc = F.Context(log_n, q, p, dnum, sampling="seeded"), O.Ctx(log_n, q, p, dnum)
     s = orc.secret(21)
     return ctx, orc, s, {}
 

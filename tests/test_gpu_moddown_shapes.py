@@ -22,7 +22,7 @@ SHAPES = [(14, 3, 50, 60, 2), (15, 3, 50, 60, 2), (16, 3, 50, 60, 3), (17, 2, 50
 def setup(request):
     log_n, depth, sb, fb, dnum = request.param
     q, p = O.gen_moduli(log_n, depth, sb, fb, dnum)
-    ctx, orc = F.Context(log_n, q, p, dnum), O.Ctx(log_n, q, p, dnum)
+    ctx, orc = F.Context(log_n, q, p, dnum, sampling="seeded"), O.Ctx(log_n, q, p, dnum)
     return ctx, orc, orc.secret(21)
 
 
@@ -66,7 +66,7 @@ def test_benchmark_shape_rotations():
     kernel) and one single rotation one level down (the 8-wave one) at the
     benchmark's parameters."""
     q, p = O.gen_moduli(16, 23, 59, 60, 3)
-    ctx, orc = F.Context(16, q, p, 3), O.Ctx(16, q, p, 3)
+    ctx, orc = F.Context(16, q, p, 3, sampling="seeded"), O.Ctx(16, q, p, 3)
     assert (ctx.L, ctx.K) == (24, 8)
     s = orc.secret(5)
     gal = [O.galois_elt(r, ctx.n) for r in (1, -4096, 5, 2 * ctx.n - 1)]
@@ -85,13 +85,17 @@ def test_benchmark_shape_rotations():
     assert np.array_equal(got, orc.rotate(low, keys[gal[0]], gal[0]))
 
 
-@pytest.mark.parametrize("log_n,depth,dnum", [(14, 7, 4), (15, 9, 5), (13, 15, 8)])
+@pytest.mark.parametrize("log_n,depth,dnum", [(14, 7, 4), (15, 9, 5), (13, 15, 8),
+                                               (16, 7, 4), (16, 9, 5), (16, 11, 6),
+                                               (16, 13, 7)])
 def test_many_digits(log_n, depth, dnum):
     """More than three digits: the fused ModUp converts four to eight digits
     in one launch; ModDown's first and last passes run the paired kernels up
-    to seven digits and the run-time digit-count kernels for eight."""
+    to seven digits and the run-time digit-count kernels for eight.  At
+    N=2^16 (two digit limbs each) the paired passes run with their radix-8
+    block size for four to seven digits."""
     q, p = O.gen_moduli(log_n, depth, 50, 60, dnum)
-    ctx, orc = F.Context(log_n, q, p, dnum), O.Ctx(log_n, q, p, dnum)
+    ctx, orc = F.Context(log_n, q, p, dnum, sampling="seeded"), O.Ctx(log_n, q, p, dnum)
     s = orc.secret(12)
     rng = np.random.default_rng(13)
     key = orc.relin_key(s, 7)
@@ -112,7 +116,7 @@ def test_full_batch_small_ring():
     """32 hoisted rotations at N=2^13 (64 polys x 64 columns: the 4-wave
     middle kernel with two column lines per wavefront)."""
     q, p = O.gen_moduli(13, 7, 50, 60, 2)
-    ctx, orc = F.Context(13, q, p, 2), O.Ctx(13, q, p, 2)
+    ctx, orc = F.Context(13, q, p, 2, sampling="seeded"), O.Ctx(13, q, p, 2)
     s = orc.secret(8)
     steps = list(range(1, 17)) + [-r for r in range(1, 17)]
     gal = [O.galois_elt(r, ctx.n) for r in steps]

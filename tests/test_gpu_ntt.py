@@ -15,7 +15,7 @@ def pair(request):
     log_n = request.param
     q = O.ntt_friendly_primes(log_n, 60, 3)
     p = O.ntt_friendly_primes(log_n, 59, 2)
-    ctx = F.Context(log_n, q, p, 2)
+    ctx = F.Context(log_n, q, p, 2, sampling="seeded")
     orc = O.Ctx(log_n, q, p, 2)
     return log_n, ctx, orc
 

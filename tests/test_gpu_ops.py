@@ -14,7 +14,7 @@ F = pytest.importorskip("fhemamba_amd")
 def pair(request):
     log_n, depth = request.param
     q, p = O.gen_moduli(log_n, depth, 50, 60, 2)
-    return F.Context(log_n, q, p, 2), O.Ctx(log_n, q, p, 2)
+    return F.Context(log_n, q, p, 2, sampling="seeded"), O.Ctx(log_n, q, p, 2)
 
 
 def _obj(a):
