@@ -5,6 +5,7 @@
 #include <cstring>
 #include <map>
 #include <memory>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -50,6 +51,9 @@ int guard(F&& f) {
   } catch (const fhe::HipError& e) {
     g_err = e.what();
     return FHE_ERR_HIP;
+  } catch (const fhe::StateError& e) {
+    g_err = e.what();
+    return FHE_ERR_STATE;
   } catch (const std::out_of_range& e) {
     g_err = e.what();
     return FHE_ERR_RANGE;
@@ -546,6 +550,95 @@ int fhe_rotate(fhe_poly* out, const fhe_poly* ct, const fhe_key* key, uint32_t g
     fhe::Scratch t(c, 2 * (size_t)nq * c.n);
     fhe::rotate(c, t.p, ct->data, nq, key->data, galois);
     reshape(out, 2, nq);
+    fhe::hip_check(hipMemcpyAsync(out->data, t.p, out->bytes, hipMemcpyDeviceToDevice, c.stream),
+                   "rotate");
+  });
+}
+
+// ---- rotation without allocation -------------------------------------------
+// Device scratch of fhe_rotate_noalloc: one copy per GPU, held until the
+// process ends.  In host code `scratch` names a host-side stand-in, never
+// device memory: its device address comes from hipGetSymbolAddress, once per
+// device, and only that address is handed to kernels.
+constexpr size_t kNoAllocScratchBytes = size_t(128) << 20;
+static __device__ __align__(256) uint64_t scratch[kNoAllocScratchBytes / 8];
+
+namespace {
+std::mutex g_scratch_mu;
+std::map<int, uint64_t*> g_scratch_ptr;  // device -> address of its `scratch`
+
+uint64_t* scratch_for_device(int device) {
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  auto it = g_scratch_ptr.find(device);
+  if (it != g_scratch_ptr.end()) return it->second;
+  int prev = 0;
+  fhe::hip_check(hipGetDevice(&prev), "hipGetDevice");
+  fhe::hip_check(hipSetDevice(device), "hipSetDevice");
+  void* ptr = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  fhe::hip_check(hipSetDevice(prev), "hipSetDevice");
+  fhe::hip_check(e, "hipGetSymbolAddress(scratch)");
+  if (!ptr) throw fhe::HipError("hipGetSymbolAddress(scratch) returned no address");
+  g_scratch_ptr[device] = static_cast<uint64_t*>(ptr);
+  return static_cast<uint64_t*>(ptr);
+}
+
+// Scratch words a rotation at nq limbs takes from the arena: the ModUp
+// digits, the ModUp input staging, the ModDown P limbs and y, and a
+// ciphertext-sized result when the output aliases the input.  Each buffer
+// is rounded up to 256 bytes as the arena does.
+size_t rotate_scratch_words(const fhe::Context& c, uint32_t nq, bool aliased) {
+  auto r = [](size_t w) { return (w + 31) & ~(size_t)31; };
+  const size_t n = c.n, nd = fhe::num_digits(c, nq);
+  size_t w = r(nd * (nq + c.K) * n) + r((size_t)nq * n) + r(2 * (size_t)c.K * n) +
+             r(2 * (size_t)nq * n);
+  if (aliased) w += r(2 * (size_t)nq * n);
+  return w;
+}
+
+struct ArenaScope {
+  fhe::Context& c;
+  ArenaScope(fhe::Context& ctx, uint64_t* base, size_t words) : c(ctx) {
+    c.arena.base = base;
+    c.arena.words = words;
+    c.arena.used = 0;
+  }
+  ~ArenaScope() {
+    c.arena.base = nullptr;
+    c.arena.words = c.arena.used = 0;
+  }
+};
+}  // namespace
+
+int fhe_rotate_noalloc(fhe_poly* out, const fhe_poly* ct, const fhe_key* key, uint32_t galois) {
+  return guard([&] {
+    same_ctx(out, ct);
+    check_key(ct, key);
+    need(ct->npoly == 2 && ct->nlimb >= 1 && ct->nlimb <= ct->c->L,
+         "rotate needs a 2-poly ciphertext");
+    need((galois & 1) && galois < 2 * ct->c->n, "Galois element must be odd and < 2N");
+    fhe::Context& c = *ct->c;
+    const uint32_t nq = ct->nlimb;
+    need(out->npoly == 2 && out->nlimb == nq && out->data,
+         "no-allocation rotate: the output must already hold 2 polys at the input's limbs");
+    const bool aliased = out == ct;
+    const size_t need_words = rotate_scratch_words(c, nq, aliased);
+    if (need_words * 8 > kNoAllocScratchBytes)
+      throw fhe::ArgError("no-allocation rotate: this shape needs " +
+                          std::to_string(need_words * 8) + " bytes of scratch, above the " +
+                          std::to_string(kNoAllocScratchBytes) + "-byte limit");
+    if (!c.has_keyswitch_plans(nq))
+      throw fhe::StateError(
+          "no-allocation rotate: the conversion tables for this level are not built yet "
+          "(any allocating key switch at this level builds them)");
+    uint64_t* base = scratch_for_device(c.device);
+    ArenaScope arena(c, base, kNoAllocScratchBytes / 8);
+    if (!aliased) {
+      fhe::rotate(c, out->data, ct->data, nq, key->data, galois);
+      return;
+    }
+    fhe::Scratch t(c, 2 * (size_t)nq * c.n);
+    fhe::rotate(c, t.p, ct->data, nq, key->data, galois);
     fhe::hip_check(hipMemcpyAsync(out->data, t.p, out->bytes, hipMemcpyDeviceToDevice, c.stream),
                    "rotate");
   });

@@ -305,6 +305,17 @@ const ConvPlan& Context::modup_plan(uint32_t s, uint32_t e, uint32_t nq) {
   return *raw;
 }
 
+bool Context::has_keyswitch_plans(uint32_t nq) {
+  std::lock_guard<std::mutex> g(plan_mu);
+  if (!plans.count({(uint64_t)1 << 62, nq})) return false;
+  const uint32_t nd = (nq + alpha - 1) / alpha < dnum ? (nq + alpha - 1) / alpha : dnum;
+  for (uint32_t j = 0; j < nd; ++j) {
+    const uint32_t s = j * alpha, e = s + alpha < nq ? s + alpha : nq;
+    if (!plans.count({((uint64_t)1 << 63) | ((uint64_t)s << 32) | e, nq})) return false;
+  }
+  return true;
+}
+
 const ConvPlan& Context::moddown_plan(uint32_t nq) {
   std::lock_guard<std::mutex> g(plan_mu);
   const uint64_t key1 = ((uint64_t)1 << 62), key2 = nq;

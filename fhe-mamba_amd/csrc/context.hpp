@@ -27,6 +27,9 @@ namespace fhe {
 struct HipError : std::runtime_error {
   using std::runtime_error::runtime_error;
 };
+struct StateError : std::logic_error {
+  using std::logic_error::logic_error;
+};
 struct ArgError : std::invalid_argument {
   using std::invalid_argument::invalid_argument;
 };
@@ -164,6 +167,19 @@ struct Context {
   void* alloc(size_t bytes) { return pool->get(bytes); }
   void release(void* p, size_t bytes) { pool->put(p, bytes); }
 
+  // While `base` is set, Scratch carves its buffers from this caller-given
+  // device region (LIFO, 256-byte aligned) instead of the pool, and throws
+  // when the region is too small.  Used by the entry point that must not
+  // allocate.
+  struct Arena {
+    uint64_t* base = nullptr;
+    size_t words = 0, used = 0;
+  } arena;
+
+  // Whether the conversion plans of a key switch at nq limbs (every ModUp
+  // digit and the ModDown) are built; never builds them.
+  bool has_keyswitch_plans(uint32_t nq);
+
  private:
   // factor (optional, per target) multiplies every constant of target k.
   ConvPlan* build_plan(const std::vector<uint32_t>& src, const std::vector<uint32_t>& dst,
@@ -209,9 +225,26 @@ struct Scratch {
   Context& c;
   uint64_t* p;
   size_t bytes;
-  Scratch(Context& ctx, size_t words)
-      : c(ctx), p((uint64_t*)ctx.alloc(words * 8)), bytes(words * 8) {}
-  ~Scratch() { c.release(p, bytes); }
+  size_t mark = 0;  // arena position to restore (arena buffers only)
+  Scratch(Context& ctx, size_t words) : c(ctx), p(nullptr), bytes(words * 8) {
+    Context::Arena& a = ctx.arena;
+    if (!a.base) {
+      p = (uint64_t*)ctx.alloc(bytes);
+      return;
+    }
+    const size_t take = (words + 31) & ~(size_t)31;
+    if (take > a.words - a.used)
+      throw ArgError("the operation needs more device scratch than the no-allocation limit");
+    mark = a.used;
+    p = a.base + a.used;
+    a.used += take;
+  }
+  ~Scratch() {
+    if (c.arena.base)
+      c.arena.used = mark;
+    else
+      c.release(p, bytes);
+  }
   Scratch(const Scratch&) = delete;
   Scratch& operator=(const Scratch&) = delete;
 };

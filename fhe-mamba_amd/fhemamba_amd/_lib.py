@@ -73,6 +73,7 @@ SIGNATURES = {
     "fhe_keyswitch": [_p, _p, _p],
     "fhe_relinearize": [_p, _p, _p],
     "fhe_rotate": [_p, _p, _p, _u32],
+    "fhe_rotate_noalloc": [_p, _p, _p, _u32],
     "fhe_rotation_precompute": [_p, _pp],
     "fhe_rotate_hoisted": [_p, _p, _p, _p, _u32, _p],
     "fhe_linear_transform": [_p, _p, _p, _u32, _u32, _p, _p, _p, _u32],

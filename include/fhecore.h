@@ -161,6 +161,19 @@ int fhe_relinearize(fhe_poly *out, const fhe_poly *ct3, const fhe_key *key);
  *  :2342). */
 int fhe_rotate(fhe_poly *out, const fhe_poly *ct, const fhe_key *key,
                uint32_t galois);
+/* fhe_rotate without any device allocation, for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  No counterpart in the reference.  Same result
+ * as fhe_rotate, word for word.  `out` must already hold [2][nq][N] (it may
+ * be `ct`).  Intermediates live in a fixed 128 MiB device array of the
+ * library, one per GPU, kept until the process ends: shapes needing more
+ * (roughly N*(dnum_eff*(nq+K) + 3nq + 2K) words, + 2nq*N when out == ct)
+ * give FHE_ERR_ARG.  The level's conversion tables must already exist (any
+ * allocating key switch at that level builds them), else FHE_ERR_STATE.
+ * Calls on one GPU share the array: calls that overlap on one GPU (two
+ * host threads, or two streams) race. */
+int fhe_rotate_noalloc(fhe_poly *out, const fhe_poly *ct, const fhe_key *key,
+                       uint32_t galois);
 /* EvalFastRotationPrecompute: ModUp'd digits of c1, in a new poly handle of
  * shape [dnum_eff][nq+K][N] (native/fideslib_stage0/src/fideslib_rotation_batch.hpp:17). */
 int fhe_rotation_precompute(const fhe_poly *ct, fhe_poly **digits);
