@@ -176,6 +176,15 @@ Context::Context(uint32_t log_n_, const uint64_t* q, uint32_t num_q, const uint6
     mc.ninv_sh = host_shoup(mc.ninv, qi);
     mc.neg_q = 0 - qi;
     mc.neg_q4 = 0 - 4 * qi;
+    mc.qinv = 0 - mc.qinv_neg;
+    mc.neg_q8 = qi < (1ull << 61) ? 0 - 8 * qi : 0;
+    {
+      // Rounded down, so the quotient estimate never exceeds the quotient.
+      const double want = 4294967296.0 / (double)qi * (1.0 - 1.0 / 1048576.0);
+      float f = (float)want;
+      while ((double)f > want) f = std::nextafter(f, 0.0f);
+      mc.rq = f;
+    }
   }
   d_const = upload(hconst);
   d_tw_fwd = upload(fwd);

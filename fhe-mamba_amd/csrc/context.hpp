@@ -52,6 +52,10 @@ struct ModConst {
   // additions of them (shoup_lazy4n, lazy_sub) instead of folding them back
   // into borrow-chain subtractions.
   uint64_t neg_q, neg_q4;
+  uint64_t qinv;       // q^-1 mod 2^64 (redc_lazy)
+  uint64_t neg_q8;     // 2^64 - 8q (lazy_sub at 8q; 0 when 8q >= 2^64)
+  float rq;            // 2^32 / q (1 - 2^-20), rounded down (reduce_est)
+  uint32_t pad_;
 };
 
 // x mod q for a 128-bit x = hi * 2^64 + lo (any hi): hi * (2^64 mod q) by

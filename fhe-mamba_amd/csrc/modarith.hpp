@@ -106,6 +106,30 @@ FHE_HD uint64_t mont_mul(uint64_t a, uint64_t b, uint64_t q, uint64_t qinv_neg) 
   return redc((uint64_t)(p >> 64), (uint64_t)p, q, qinv_neg);
 }
 
+// Montgomery reduction without the final correction: for T = hi*2^64 + lo
+// with hi < q and qinv = q^-1 mod 2^64, m = lo * qinv makes T - m q a
+// multiple of 2^64 whose low word cancels exactly, so
+//   (T - m q) / 2^64 = hi - mulhi64(m, q)  in (-q, q),
+// and the result hi + q - mulhi64(m, q) = T * 2^-64 mod q lies in (0, 2q).
+FHE_HD uint64_t redc_lazy(uint64_t hi, uint64_t lo, uint64_t q, uint64_t qinv) {
+  const uint64_t m = lo * qinv;
+  return hi + q - mulhi64(m, q);
+}
+
+// x mod q for x < 2^18 q and q in [2^33, 2^61), from the estimate
+// e = floor(float(x >> 32) * rq), rq = 2^32 / q (1 - 2^-20) rounded down.
+// The float errors (three roundings of 2^-24 each) stay inside the 2^-20
+// margin, so e <= floor(x / q); they cost at most 2^18 * 2^-19.9 < 1/4 of a
+// quotient unit, and dropping x's low word less than 2^32 / q <= 1/2, so
+// e >= floor(x / q) - 1.  Then x - e q lies in [0, 2q): one conditional
+// subtraction (qneg = 2^64 - q).
+FHE_HD uint64_t reduce_est(uint64_t x, uint64_t qneg, float rq) {
+  const uint32_t e = (uint32_t)((float)(uint32_t)(x >> 32) * rq);
+  const uint64_t r = x + (uint64_t)e * qneg;
+  const uint64_t d = r + qneg;
+  return (int64_t)d < 0 ? r : d;
+}
+
 // 128-bit accumulator for sums of products that are reduced once.
 struct Acc128 {
   uint64_t lo, hi;

@@ -443,6 +443,41 @@ __device__ __forceinline__ void key_comb2(const ulonglong2* d, const ulonglong2*
   t1 = t[1];
 }
 
+// key_comb2 with the reduction left lazy: redc_lazy, each sum in (0, 2q)
+// (T < nd q^2 keeps T's high word below q for nd q < 2^64).
+template <int ND>
+__device__ __forceinline__ void key_comb2_lazy(const ulonglong2* d, const ulonglong2* k,
+                                               uint64_t q, uint64_t qinv, uint64_t& t0,
+                                               uint64_t& t1) {
+  constexpr uint32_t M30 = (1u << 30) - 1;
+  uint64_t a0[2] = {0, 0}, a1[2] = {0, 0}, a2[2] = {0, 0};
+#pragma unroll
+  for (int j = 0; j < ND; ++j) {
+    const uint64_t dd[2] = {d[j].x, d[j].y}, kk[2] = {k[j].x, k[j].y};
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t dl = (uint32_t)dd[h] & M30, dh = (uint32_t)(dd[h] >> 30);
+      const uint32_t kl = (uint32_t)kk[h] & M30, kh = (uint32_t)(kk[h] >> 30);
+      a0[h] += (uint64_t)dl * kl;
+      a1[h] += (uint64_t)dl * kh;
+      a1[h] += (uint64_t)dh * kl;
+      a2[h] += (uint64_t)dh * kh;
+    }
+  }
+  uint64_t t[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint64_t m1 = a1[h] << 30, m2 = a2[h] << 60;
+    const uint64_t lo = a0[h] + m1;
+    uint64_t hi = (a1[h] >> 34) + (a2[h] >> 4) + (lo < m1);
+    const uint64_t lo2 = lo + m2;
+    hi += lo2 < m2;
+    t[h] = redc_lazy(hi, lo2, q, qinv);
+  }
+  t0 = t[0];
+  t1 = t[1];
+}
+
 // ModDown epilogue (see ModDownEpi): the value at evaluation slot s goes to
 // slot d(s) of the output, d being the inverse Galois permutation.  ND > 0
 // fixes the digit count at compile time (ND = 0: e.nd at run time).
@@ -600,8 +635,8 @@ __global__ void __launch_bounds__(256)
 }
 
 // Last forward pass of a batched ModDown over the blocked y, both polys of
-// each key switch in one workgroup (ND = 1..7 digits, every modulus below
-// 2^60).  Eight wavefronts; lane tid holds the same R = 4 positions of row
+// each key switch in one workgroup (ND = 1..7 digits, every modulus in
+// [2^33, 2^60)).  Eight wavefronts; lane tid holds the same R = 4 positions of row
 // `line` in both polys (radix 4: one row per wavefront at N2 = 256, two or
 // four at 128 / 64), so the digits' words and the twiddles are loaded once
 // for both key products and both transforms, and the Galois target index is
@@ -609,9 +644,17 @@ __global__ void __launch_bounds__(256)
 // group (LINES = BLO).  Stage order, twiddle indices and lazy ranges are
 // those of ntt_body's forward BLOCKS pass; the epilogue is EpiStore's:
 // out_b[d(s)] = sum_j digit_j[s] key_j,b[s] (REDC) + add_b[s] + y_b[s].
-// Up to three digits and rows of 128 or 256 words the kernel fits 80 VGPRs
-// without spills: three 8-wave workgroups per CU instead of two (measured 4%
-// faster for 30 key switches at N=2^16, 24 limbs, 3 digits).
+// Lazy ranges: y arrives below 16q from the middle kernel's alternating
+// stages (k_convert_mid, ALT); stages with an even bit beta first bring X
+// below 8q (lazy_sub at 8q), the others add to it, so values stay below
+// 16q and the last stage (beta = 0) leaves them below 12q.  The key sum
+// (redc_lazy, below 2q) plus the addend (below q) plus that is below 15q,
+// reduced once by reduce_est.
+// The key products are formed after the transform, with the stores: the
+// butterflies then hold only the transform's values, and up to three digits
+// the kernel fits 64 VGPRs, four 8-wave workgroups per CU (0.84 -> 0.80 ms
+// for 30 key switches at N=2^16, 24 limbs, 3 digits, against forming them
+// first and keeping them in registers).
 template <int S, int ND>
 __global__ void __launch_bounds__(512)
     __attribute__((amdgpu_waves_per_eu(ND <= 3 && S >= 7 ? 6 : 1, 8)))
@@ -624,7 +667,8 @@ __global__ void __launch_bounds__(512)
   static_assert(TPL <= 64 && LINES * TPL == 512 && ND > 0 && ND <= 7, "pair epilogue");
   __shared__ uint64_t lds[2][LINES * PITCH];
   const uint32_t n = 1u << log_n, r = blockIdx.y, i = blockIdx.z, tid = threadIdx.x;
-  const uint64_t q = mc[i].q, q4 = 4 * q, qneg = mc[i].neg_q, q4neg = mc[i].neg_q4;
+  const uint64_t q = mc[i].q, q4 = 4 * q, qneg = mc[i].neg_q, q8neg = mc[i].neg_q8;
+  const float rq = mc[i].rq;
   const uint64_t* __restrict__ tw = tw_all + (size_t)i * n * 2;
   const size_t ps = (size_t)e.nq * n, wg0 = ((size_t)blockIdx.x * LINES) << S;
   const uint32_t tau = tid % TPL, line = tid / TPL;
@@ -646,43 +690,6 @@ __global__ void __launch_bounds__(512)
     }
   }
   __syncthreads();
-
-  // Key products of both polys at this lane's positions, the digits' words
-  // read once (16-byte loads, two positions each).
-  uint64_t pre[2][R];
-  {
-    const size_t dstride = (size_t)e.ne * n, kstride = 2 * e.kl;
-    const uint64_t* const a0 = e.add[r][0];
-    const uint64_t* const a1 = e.add[r][1];
-    const uint64_t qn = e.mc[i].qinv_neg;
-#pragma unroll
-    for (int k = 0; k < R; k += 2) {
-      const size_t s = wg0 + staged(k);
-      const uint64_t* dg = e.digits[r] + (size_t)i * n + s;
-      const uint64_t* kr = e.key[r] + (size_t)i * n + s;
-      ulonglong2 d[ND], k0[ND], k1[ND];
-#pragma unroll
-      for (int j = 0; j < ND; ++j) {
-        d[j] = *reinterpret_cast<const ulonglong2*>(dg + j * dstride);
-        k0[j] = load_stream2(kr + j * kstride);
-        k1[j] = load_stream2(kr + e.kl + j * kstride);
-      }
-      // Without an addend the first digit's words are read again (a cache
-      // hit), so that the load is issued with the others, without a branch.
-      const ulonglong2 av = *reinterpret_cast<const ulonglong2*>(a0 ? a0 + (size_t)i * n + s : dg);
-      key_comb2<ND>(d, k0, q, qn, pre[0][k], pre[0][k + 1]);
-      key_comb2<ND>(d, k1, q, qn, pre[1][k], pre[1][k + 1]);
-      if (a0) {
-        pre[0][k] = add_mod(pre[0][k], av.x, q);
-        pre[0][k + 1] = add_mod(pre[0][k + 1], av.y, q);
-      }
-      if (a1) {
-        const ulonglong2 bv = *reinterpret_cast<const ulonglong2*>(a1 + (size_t)i * n + s);
-        pre[1][k] = add_mod(pre[1][k], bv.x, q);
-        pre[1][k + 1] = add_mod(pre[1][k + 1], bv.y, q);
-      }
-    }
-  }
 
   uint64_t x[2][R];
 #pragma unroll
@@ -708,18 +715,11 @@ __global__ void __launch_bounds__(512)
         const uint64_t wv = tw[2 * ti], ws = tw[2 * ti + 1];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-          const uint64_t X = lazy_sub(x[h][v], q4neg);
+          const uint64_t X = beta % 2 == 0 ? lazy_sub(x[h][v], q8neg) : x[h][v];
           const uint64_t T = shoup_lazy4n(x[h][v + d], wv, ws, qneg);
           x[h][v] = X + T;
           x[h][v + d] = X + q4 - T;
         }
-      }
-    }
-    if (sp == NSP - 1) {
-#pragma unroll
-      for (int v = 0; v < R; ++v) {
-        x[0][v] = reduce_8q(x[0][v], q);
-        x[1][v] = reduce_8q(x[1][v], q);
       }
     }
     wave_lds_sync();
@@ -732,24 +732,56 @@ __global__ void __launch_bounds__(512)
   }
   wave_lds_sync();
 
-  // Stores through the inverse Galois permutation, shared by both polys.
+  // Key products of both polys at this lane's positions, the digits' words
+  // read once (16-byte loads, two positions each), plus the transform, out
+  // through the inverse Galois permutation.
   const uint32_t gi = e.ginv[r];
   uint64_t* const out0 = e.out[r] + (size_t)i * n;
   uint64_t* const out1 = e.out[r] + ((size_t)e.nq + i) * n;
+  const size_t dstride = (size_t)e.ne * n, kstride = 2 * e.kl;
+  const uint64_t* const a0 = e.add[r][0];
+  const uint64_t* const a1 = e.add[r][1];
+  const uint64_t qn = e.mc[i].qinv;
 #pragma unroll
-  for (int k = 0; k < R; ++k) {
-    const uint32_t p = staged(k);
-    const uint32_t s = (uint32_t)wg0 + p;
-    uint32_t dst = s;
-    if (gi != 1) {
-      // 32-bit wrap-around is exact here: only the product mod 2N matters.
-      const uint32_t jj = brev_bits(s, log_n);
-      const uint32_t ex = ((2u * jj + 1u) * gi) & (2u * n - 1u);
-      dst = brev_bits((ex - 1u) >> 1, log_n);
+  for (int k = 0; k < R; k += 2) {
+    const size_t s0 = wg0 + staged(k);
+    const uint64_t* dg = e.digits[r] + (size_t)i * n + s0;
+    const uint64_t* kr = e.key[r] + (size_t)i * n + s0;
+    ulonglong2 d[ND], k0[ND], k1[ND];
+#pragma unroll
+    for (int j = 0; j < ND; ++j) {
+      d[j] = *reinterpret_cast<const ulonglong2*>(dg + j * dstride);
+      k0[j] = load_stream2(kr + j * kstride);
+      k1[j] = load_stream2(kr + e.kl + j * kstride);
     }
-    const uint32_t li = lds_idx(p >> S, p & (LEN - 1), PITCH);
-    out0[dst] = add_mod(pre[0][k], lds[0][li], q);
-    out1[dst] = add_mod(pre[1][k], lds[1][li], q);
+    const ulonglong2 av = *reinterpret_cast<const ulonglong2*>(a0 ? a0 + (size_t)i * n + s0 : dg);
+    uint64_t pre[2][2];
+    key_comb2_lazy<ND>(d, k0, q, qn, pre[0][0], pre[0][1]);
+    key_comb2_lazy<ND>(d, k1, q, qn, pre[1][0], pre[1][1]);
+    if (a0) {
+      pre[0][0] += av.x;
+      pre[0][1] += av.y;
+    }
+    if (a1) {
+      const ulonglong2 bv = *reinterpret_cast<const ulonglong2*>(a1 + (size_t)i * n + s0);
+      pre[1][0] += bv.x;
+      pre[1][1] += bv.y;
+    }
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const uint32_t p = staged(k + kk);
+      const uint32_t s = (uint32_t)wg0 + p;
+      uint32_t dst = s;
+      if (gi != 1) {
+        // 32-bit wrap-around is exact here: only the product mod 2N matters.
+        const uint32_t jj = brev_bits(s, log_n);
+        const uint32_t ex = ((2u * jj + 1u) * gi) & (2u * n - 1u);
+        dst = brev_bits((ex - 1u) >> 1, log_n);
+      }
+      const uint32_t li = lds_idx(p >> S, p & (LEN - 1), PITCH);
+      out0[dst] = reduce_est(pre[0][kk] + lds[0][li], qneg, rq);
+      out1[dst] = reduce_est(pre[1][kk] + lds[1][li], qneg, rq);
+    }
   }
 }
 
@@ -760,8 +792,12 @@ __global__ void __launch_bounds__(512)
 // once, runs the first S2 inverse stages of both polys with shared
 // twiddles, and the workgroup stores its rows (one blocked group) to the
 // blocked layout.  The values stay in [0, 4q); N^-1 is applied later.
+// Up to three digits it fits 64 VGPRs without spills, so four 8-wave
+// workgroups share a CU (LDS allows four; measured 2% faster than three at
+// N=2^16, 24 limbs).
 template <int S, int ND>
 __global__ void __launch_bounds__(512)
+    __attribute__((amdgpu_waves_per_eu(ND <= 3 ? 8 : 1, 8)))
     ntt_pass_ksk_pair(uint64_t* __restrict__ ext, size_t ps, const ModConst* __restrict__ mc,
                       const uint64_t* __restrict__ tw_all, uint32_t log_n, uint32_t s_other,
                       const ModDownEpi e) {
@@ -781,10 +817,11 @@ __global__ void __launch_bounds__(512)
     return (tid >> 6) * (64u * R) + (uint32_t)(k >> 1) * 128u + 2 * (tid & 63) + (k & 1);
   };
 
-  // P-limb key products of both polys into LDS (this wavefront's rows).
+  // P-limb key products of both polys into LDS (this wavefront's rows), in
+  // (0, 2q) as the first inverse stage accepts them.
   {
     const size_t dstride = (size_t)e.ne * n, kstride = 2 * e.kl;
-    const uint64_t qn = e.mc[midx].qinv_neg;
+    const uint64_t qn = e.mc[midx].qinv;
 #pragma unroll
     for (int k = 0; k < R; k += 2) {
       const uint32_t p = staged(k);
@@ -801,10 +838,10 @@ __global__ void __launch_bounds__(512)
       uint64_t v0, v1;
       const uint32_t l0 = lds_idx(p >> S, p & (LEN - 1), PITCH);
       const uint32_t l1 = lds_idx((p + 1) >> S, (p + 1) & (LEN - 1), PITCH);
-      key_comb2<ND>(d, k0, q, qn, v0, v1);
+      key_comb2_lazy<ND>(d, k0, q, qn, v0, v1);
       lds[0][l0] = v0;
       lds[0][l1] = v1;
-      key_comb2<ND>(d, k1, q, qn, v0, v1);
+      key_comb2_lazy<ND>(d, k1, q, qn, v0, v1);
       lds[1][l0] = v0;
       lds[1][l1] = v1;
     }
@@ -1060,7 +1097,12 @@ struct MidArgs {
   uint32_t nplan, L;
 };
 
-template <int S1, int S2, int NW>
+// ALT: the forward column stages use the alternating lazy range of the
+// paired ModDown epilogue (a stage whose global index g has logN - 1 - g
+// even first brings X below 8q; values stay below 16q), and the output may
+// reach 16q; otherwise every stage brings X below 4q and the output stays
+// below 8q.
+template <int S1, int S2, int NW, bool ALT>
 __global__ void __launch_bounds__(64 * NW)
     k_convert_mid(const MidArgs a, const ModConst* __restrict__ mc,
                   const uint64_t* __restrict__ tw_inv, const uint64_t* __restrict__ tw_fwd) {
@@ -1154,8 +1196,8 @@ __global__ void __launch_bounds__(64 * NW)
   for (uint32_t k = first; k < nq; k += NL) {
     const uint32_t kpos = k < pl.skip_at ? k : k + pl.skip_len;
     const uint32_t kmod = kpos < pl.qlimbs ? kpos : a.L + (kpos - pl.qlimbs);
-    const uint64_t q = mc[kmod].q, q4 = 4 * q, qn = mc[kmod].qinv_neg;
-    const uint64_t qneg = mc[kmod].neg_q, q4neg = mc[kmod].neg_q4;
+    const uint64_t q = mc[kmod].q, q4 = 4 * q, qn = mc[kmod].qinv;
+    const uint64_t qneg = mc[kmod].neg_q, q4neg = mc[kmod].neg_q4, q8neg = mc[kmod].neg_q8;
     const uint64_t* __restrict__ tw = tw_fwd + (size_t)kmod * N * 2;
     uint64_t x[R];
     {
@@ -1189,7 +1231,7 @@ __global__ void __launch_bounds__(64 * NW)
         uint64_t hh = (s1 >> 34) + (c1 << 30) + (a2[v] >> 4) + (lo < m1);
         const uint64_t lo2 = lo + m2;
         hh += lo2 < m2;
-        x[v] = redc(hh, lo2, q, qn);
+        x[v] = redc_lazy(hh, lo2, q, qn);  // (0, 2q)
       }
     }
 #pragma unroll
@@ -1211,7 +1253,8 @@ __global__ void __launch_bounds__(64 * NW)
           const uint32_t u = thi | ((uint32_t)v << w) | tlo;
           const uint32_t ti = (1u << (S1 - 1 - beta)) | (u >> (beta + 1));
           const uint64_t wv = tw[2 * ti], ws = tw[2 * ti + 1];
-          const uint64_t X = lazy_sub(x[v], q4neg);
+          const uint64_t X = !ALT ? lazy_sub(x[v], q4neg)
+                             : (S2 + beta) % 2 == 0 ? lazy_sub(x[v], q8neg) : x[v];
           const uint64_t T = shoup_lazy4n(x[v + d], wv, ws, qneg);
           x[v] = X + T;
           x[v + d] = X + q4 - T;
@@ -1368,16 +1411,16 @@ size_t mid_lds_bytes(uint32_t K) {
 // Launches with fewer (poly, column) tiles than this use 8-wave workgroups.
 constexpr uint32_t MID_SMALL_TILES = 4096;
 
-template <int S1, int S2>
+template <int S1, int S2, bool ALT = false>
 void launch_mid(Context& c, const char* name, const MidArgs& a, uint32_t npoly,
                 uint32_t max_src) {
   const uint32_t tiles = npoly << S2;
   if (tiles < MID_SMALL_TILES && mid_lds_bytes<S1, 8>(max_src) <= 65536) {
-    FHE_LAUNCH(c, name, (k_convert_mid<S1, S2, 8>), dim3(tiles), dim3(512),
+    FHE_LAUNCH(c, name, (k_convert_mid<S1, S2, 8, ALT>), dim3(tiles), dim3(512),
                (mid_lds_bytes<S1, 8>(max_src)), a, c.d_const, c.d_tw_inv, c.d_tw_fwd);
     return;
   }
-  FHE_LAUNCH(c, name, (k_convert_mid<S1, S2, 4>), dim3(tiles), dim3(256),
+  FHE_LAUNCH(c, name, (k_convert_mid<S1, S2, 4, ALT>), dim3(tiles), dim3(256),
              (mid_lds_bytes<S1, 4>(max_src)), a, c.d_const, c.d_tw_inv, c.d_tw_fwd);
 }
 
@@ -1402,11 +1445,14 @@ bool mid_lds_fits(const Context& c, uint32_t nsrc) {
   }
 }
 
+// Every modulus of the launch in [2^33, 2^60): the fused kernels' lazy
+// ranges (16q < 2^64) and reduce_est's quotient estimate (q >= 2^33).
 bool below_2_60_all(const Context& c, uint32_t nq) {
+  auto ok = [](uint64_t m) { return m < (1ull << 60) && m >= (1ull << 33); };
   for (uint32_t i = 0; i < nq; ++i)
-    if (c.mods[i] >= (1ull << 60)) return false;
+    if (!ok(c.mods[i])) return false;
   for (uint32_t t = 0; t < c.K; ++t)
-    if (c.mods[c.L + t] >= (1ull << 60)) return false;
+    if (!ok(c.mods[c.L + t])) return false;
   return true;
 }
 
@@ -1432,11 +1478,18 @@ void moddown_fused(Context& c, uint64_t* ext_p, uint64_t* y, uint32_t npoly, uin
   a.plan[0] = mid_plan(c, pl, c.L, 0, nq, 0, nq);
   a.nplan = 1;
   a.L = c.L;
+  // The paired epilogue (both polys of each key switch, 1..7 digits) takes
+  // the middle kernel's alternating lazy range; the other epilogues the
+  // plain one.
+  const bool pair = npoly % 2 == 0 && epi.nd >= 1 && epi.nd <= 7;
   switch (c.log_n) {
 #define CASE(LN, A, B)                                                   \
   case LN:                                                               \
     launch_ksk<B, BLOCKS, true>(c, ext_p, npoly, s1, false, epi);        \
-    launch_mid<A, B>(c, "k_moddown_mid", a, npoly, c.K);                 \
+    if (pair)                                                            \
+      launch_mid<A, B, true>(c, "k_moddown_mid", a, npoly, c.K);         \
+    else                                                                 \
+      launch_mid<A, B>(c, "k_moddown_mid", a, npoly, c.K);               \
     launch_moddown<B, BLOCKS, true>(c, y, npoly, nq, s1, epi);           \
     return;
     CASE(13, 7, 6) CASE(14, 7, 7) CASE(15, 8, 7) CASE(16, 8, 8) CASE(17, 9, 8)
