@@ -78,9 +78,15 @@ class EncryptedMamba2Decoder:
         self.nh, self.hd, self.kc = first.num_heads, first.head_dim, first.conv_kernel
         self.cd = first.conv_dim
         per = self.hd * self.ns
-        if self.slots % per or self.nh % (self.slots // per):
+        # heads per state ciphertext: the largest power of two that divides
+        # the head count and fits the slots (the state's rotate-sums walk
+        # power-of-two block strides)
+        hp = 1
+        while self.nh % (2 * hp) == 0 and 2 * hp * per <= self.slots:
+            hp *= 2
+        if per > self.slots or self.slots % per or per & (per - 1):
             raise ValueError("slots must hold whole heads and the heads whole ciphertexts")
-        self.hp = self.slots // per                    # heads per state ciphertext
+        self.hp = hp                                   # heads per state ciphertext
         self.gb = self.hp * self.hd                    # group block
         self.groups = self.nh // self.hp
         if first.proj_dim > self.slots or self.d > self.slots:

@@ -1,0 +1,27 @@
+"""Encrypted Mamba-2 decode on the GPU of a payload written by the
+reference's own exporter (tests/golden/m2_chain_tiny: export_chain_payload,
+src/fhemamba/m1_payload.py:901, on the reference tests' tiny seeded
+Mamba-2; two layers, two test tokens with carried state).  Pass criterion
+as the exporter states it (m1_payload.py:1067) and the reference decoder
+gates it: decrypted final hidden against chain_expected_poly_final within
+1e-3 (the decoder's default --tolerance); measured errors are printed."""
+import os
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+F = pytest.importorskip("fhemamba_amd")
+from fhemamba_amd import mamba2_decode as D  # noqa: E402
+
+FIX = os.path.join(os.path.dirname(__file__), "golden", "m2_chain_tiny")
+TOL = 1e-3
+
+
+def test_reference_exported_payload_decodes_within_tolerance():
+    report = D.run_payload(FIX, seed=31, log=lambda m: None)
+    print(f"reference payload: {report['seconds_per_token']} s/token, errors vs polynomial "
+          f"{report['per_token_errors_vs_polynomial']}, vs exact "
+          f"{report['max_abs_error_vs_exact']:.2e}", flush=True)
+    assert report["tokens"] == 2 and report["layers"] == 2
+    assert report["max_abs_error_vs_polynomial"] < TOL
