@@ -40,12 +40,32 @@ HBM_PEAK = 8.0e12  # B/s, MI355X HBM3E
 # HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE and
 # WRITE_SIZE on this workload (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0, the factors
 # a plain copy of known size reads back); recorded in
-# profiles/rotation_step_n65536_l24.md together with the commands.
+# profiles/rotation_step_n65536_l24.md together with the commands and the
+# hash of the kernel sources they were measured on.  A build from other
+# sources reports traffic as null.
 MEASURED_TRAFFIC = {
-    "ntt_fwd_blocks_moddown": 3_096_813_286 + 755_675_366,
-    "k_moddown_mid": 253_238_067 + 757_507_110,
-    "ntt_inv_blocks_ksk": 776_195_430 + 251_658_240,
+    "csrc_sha16": "",
+    "kernels": {},
 }
+
+
+def csrc_sha16() -> str:
+    """First 16 hex digits of the SHA-256 over the library's kernel sources
+    (fhe-mamba_amd/csrc, file names and contents in name order)."""
+    import hashlib
+    d = os.path.join(ROOT, "fhe-mamba_amd", "csrc")
+    h = hashlib.sha256()
+    for name in sorted(os.listdir(d)):
+        h.update(name.encode())
+        with open(os.path.join(d, name), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
+def measured_traffic(kernel: str):
+    if MEASURED_TRAFFIC["csrc_sha16"] != csrc_sha16():
+        return None
+    return MEASURED_TRAFFIC["kernels"].get(kernel)
 LOG_N, DEPTH, SCALE_BITS, FIRST_BITS, DNUM = 16, 23, 59, 60, 3
 N = 1 << LOG_N
 LIMB = N * 8  # bytes per limb
@@ -385,49 +405,108 @@ def _is_prime(n: int) -> bool:
     return True
 
 
-def cpu_baseline(budget_s: float = 20.0):
-    """Oracle (C restatement) on the host: hoisted-set rotations at the
-    benchmark shape, one thread; NTT batch throughput on all cores."""
+def _cpu_threads() -> tuple[int, int]:
+    """(threads used for the all-core figures, nproc): the cores this process
+    may run on, capped by OMP_NUM_THREADS when set and by 16 (a one-GPU
+    share of the host)."""
+    nproc = os.cpu_count() or 1
+    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else nproc
+    omp = int(os.environ.get("OMP_NUM_THREADS") or usable)
+    return max(1, min(usable, omp, 16)), nproc
+
+
+def cpu_baseline(budget_s: float = 24.0):
+    """The oracle (this build's scalar C restatement of the same algorithms;
+    OpenFHE is not installed on this host) at the benchmark shape on a
+    bounded sample:
+      * hoisted rotations from one shared ModUp (the GPU step's operation),
+        on one thread and on all threads (independent rotations of the set
+        in parallel, the ModUp once), with the GPU step's ModUp and rescale
+        amortised over 30 rotations for the headline figure;
+      * non-hoisted rotations (own ModUp each) on one thread;
+      * the forward NTT of 8 ciphertexts x 24 limbs on one and all threads."""
+    import concurrent.futures as cf
+
     import numpy as np
 
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
 
+    threads, nproc = _cpu_threads()
     q, p = O.gen_moduli(LOG_N, DEPTH, SCALE_BITS, FIRST_BITS, DNUM)
     c = O.Ctx(LOG_N, q, p, DNUM)
     s = c.secret(1)
     rng = np.random.default_rng(7)
     ct = np.stack([np.stack([rng.integers(0, qj, N, dtype=np.uint64) for qj in q])
                    for _ in range(2)])
-    keys = [(O.galois_elt(r, N), None) for r in (1, -1)]
-    keys = [(g, c.galois_key(s, g, 1000 + i)) for i, (g, _) in enumerate(keys)]
-    done, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < budget_s * 0.6 or done < 2:
-        g, k = keys[done % 2]
+    steps = (1, -1, 2, -2)
+    keys = [(O.galois_elt(r, N), c.galois_key(s, O.galois_elt(r, N), 1000 + i))
+            for i, r in enumerate(steps)]
+
+    def timed(fn, min_s, min_n=1):
+        n, t0 = 0, time.perf_counter()
+        while n < min_n or time.perf_counter() - t0 < min_s:
+            fn(n)
+            n += 1
+        return n, time.perf_counter() - t0
+
+    t0 = time.perf_counter()
+    digits = c.modup(ct[1])
+    modup_s = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    c.rescale(ct)
+    rescale_s = time.perf_counter() - t0
+
+    def hoisted(i):
+        g, k = keys[i % len(keys)]
+        c.rotate_hoisted(ct, digits, k, g)
+
+    n1, t1 = timed(hoisted, budget_s * 0.15, 2)
+    one_core = n1 / t1
+    with cf.ThreadPoolExecutor(threads) as ex:
+        jobs = 2 * threads
+        t0 = time.perf_counter()
+        list(ex.map(hoisted, range(jobs)))
+        all_core = jobs / (time.perf_counter() - t0)
+
+    def single(i):
+        g, k = keys[i % len(keys)]
         c.rotate(ct, k, g)
-        done += 1
-    rot_rate = done / (time.perf_counter() - t0)
-    cores = min(16, os.cpu_count() or 1)
+
+    n2, t2 = timed(single, budget_s * 0.15, 2)
+    rots = len(STEPS)
+    step_all = modup_s + rots / all_core + rescale_s
+    step_one = modup_s + rots / one_core + rescale_s
+
     qn = [int(x) for x in ntt_primes(LOG_N, 60, 24)]
     cn = O.Ctx(LOG_N, qn, [], 1)
     batch = np.stack([np.stack([rng.integers(0, qj, N, dtype=np.uint64) for qj in qn])
                       for _ in range(8)])
-    reps, t1 = 0, time.perf_counter()
-    while time.perf_counter() - t1 < budget_s * 0.3 or reps < 1:
-        cn.ntt_fwd_batch(batch, 0, nthreads=cores)
-        reps += 1
-    ntt_rate = reps * batch.size * 8 * 2 / (time.perf_counter() - t1) / 1e9
+    ntt_bytes = batch.size * 8 * 2  # read + write once
+
+    def ntt_rate(nthreads):
+        n, t = timed(lambda i: cn.ntt_fwd_batch(batch, 0, nthreads=nthreads),
+                     budget_s * 0.1, 1)
+        return n * ntt_bytes / t / 1e9
+
     return {
-        "value": rot_rate,
+        "value": rots / step_all,
         "unit": "rotations/s",
-        "cores": 1,
+        "cores": threads,
         "kind": "port",
-        "sample": (f"{done} single (non-hoisted) hybrid key-switched rotations of one "
-                   f"N=2^16, L=24, K=8, dnum=3 ciphertext (steps +1/-1) by the scalar C "
-                   f"oracle; OpenFHE CPU: unavailable on this host"),
-        "ntt_gbps": ntt_rate,
-        "ntt_cores": cores,
-        "ntt_sample": f"{reps} forward NTTs of 8 polys x 24 limbs at N=2^16 on {cores} threads",
+        "sample": (f"hoisted-set rotations of one N=2^16, L=24, K=8, dnum=3 ciphertext by the "
+                   f"scalar C oracle: {jobs} rotations on {threads} threads (steps +-1, +-2), "
+                   f"one ModUp and one rescale amortised over {rots} rotations as in the GPU "
+                   f"step; OpenFHE CPU: unavailable on this host"),
+        "nproc": nproc,
+        "hoisted_rotations_per_s_all_threads_amortised": rots / step_all,
+        "hoisted_rotations_per_s_one_thread_amortised": rots / step_one,
+        "hoisted_rotation_only_per_s": {"one_thread": one_core, "all_threads": all_core},
+        "single_rotations_per_s_one_thread": n2 / t2,
+        "modup_s": modup_s,
+        "rescale_s": rescale_s,
+        "ntt_gbps": {"one_thread": ntt_rate(1), "all_threads": ntt_rate(threads)},
+        "ntt_sample": "forward NTT of 8 ciphertexts x 24 limbs (60-bit primes) at N=2^16",
     }
 
 
@@ -471,7 +550,8 @@ def main() -> int:
         "peak": HBM_PEAK / 1e9,
         "unit": "GB/s",
         "frac": achieved / HBM_PEAK if achieved else None,
-        "traffic": MEASURED_TRAFFIC.get(dom),
+        "traffic": measured_traffic(dom),
+        "csrc_sha16": csrc_sha16(),
         "bytes_per_launch": per_launch,
         "avg_launch_us": avg_s * 1e6,
         "step_frac": rot["step_bytes"] / (rot["ms_per_step"] * 1e-3) / HBM_PEAK,

@@ -140,93 +140,114 @@ __global__ void __launch_bounds__(TPB)
   }
 }
 
-// MAC: grid (N/512, nq, 2); each thread accumulates n products per word in
-// 128 bits, folding every 32 terms so the sum never overflows.
+// Fold a 128-bit accumulator to its value mod q (kept in lo).
+__device__ __forceinline__ void fold(Acc128& a, const ModConst& m) {
+  a.lo = reduce128(a.hi, a.lo, m);
+  a.hi = 0;
+}
+
+// MAC: grid (N/512, nq); each thread takes two adjacent words of both polys
+// of every ciphertext, so each plaintext word is read once for both, and
+// accumulates the products in 128 bits, folding every 32 terms so the sums
+// never overflow.
 __global__ void __launch_bounds__(TPB)
     k_mac(uint64_t* acc, const uint64_t* x, const uint64_t* w, const ModConst* mc, uint32_t n,
           uint32_t nq, uint32_t cnt) {
   const ModConst m = mc[blockIdx.y];
-  const uint32_t poly = blockIdx.z;
-  const size_t e = pair_off();
-  const size_t limb_off = (size_t)blockIdx.y * n + e;
-  const size_t xs = 2 * (size_t)nq * n, ws = (size_t)nq * n;
-  const uint64_t* xp = x + (size_t)poly * nq * n + limb_off;
+  const size_t limb_off = (size_t)blockIdx.y * n + pair_off();
+  const size_t pl = (size_t)nq * n, xs = 2 * pl, ws = pl;
+  const uint64_t* xp = x + limb_off;
   const uint64_t* wp = w + limb_off;
-  Acc128 s0, s1;
+  Acc128 s[2][2];
   uint32_t i = 0;
   while (i < cnt) {
     const uint32_t end = i + 32 < cnt ? i + 32 : cnt;
-    // Eight independent loads in flight per thread before the products.
-    for (; i + 8 <= end; i += 8) {
-      U2 xv[8], wv[8];
+    // Twelve independent 16-byte loads in flight per thread.
+    for (; i + 4 <= end; i += 4) {
+      U2 x0[4], x1[4], wv[4];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        xv[u] = ld2(xp + (i + u) * xs);
+      for (int u = 0; u < 4; ++u) {
+        x0[u] = ld2(xp + (i + u) * xs);
+        x1[u] = ld2(xp + (i + u) * xs + pl);
         wv[u] = ld2(wp + (i + u) * ws);
       }
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        s0.mac(xv[u].x, wv[u].x);
-        s1.mac(xv[u].y, wv[u].y);
+      for (int u = 0; u < 4; ++u) {
+        s[0][0].mac(x0[u].x, wv[u].x);
+        s[0][1].mac(x0[u].y, wv[u].y);
+        s[1][0].mac(x1[u].x, wv[u].x);
+        s[1][1].mac(x1[u].y, wv[u].y);
       }
     }
     for (; i < end; ++i) {
-      const U2 xv = ld2(xp + i * xs), wv = ld2(wp + i * ws);
-      s0.mac(xv.x, wv.x);
-      s1.mac(xv.y, wv.y);
+      const U2 a = ld2(xp + i * xs), b = ld2(xp + i * xs + pl), wv = ld2(wp + i * ws);
+      s[0][0].mac(a.x, wv.x);
+      s[0][1].mac(a.y, wv.y);
+      s[1][0].mac(b.x, wv.x);
+      s[1][1].mac(b.y, wv.y);
     }
-    // Fold: keep the reduced value in lo, clear hi.
-    s0.lo = reduce128(s0.hi, s0.lo, m);
-    s0.hi = 0;
-    s1.lo = reduce128(s1.hi, s1.lo, m);
-    s1.hi = 0;
+    fold(s[0][0], m);
+    fold(s[0][1], m);
+    fold(s[1][0], m);
+    fold(s[1][1], m);
   }
-  st2(acc + (size_t)poly * nq * n + limb_off, s0.lo, s1.lo);
+  st2(acc + limb_off, s[0][0].lo, s[0][1].lo);
+  st2(acc + pl + limb_off, s[1][0].lo, s[1][1].lo);
 }
 
 // acc[p][j] = (acc[p][j] if accumulate) + sum_i x_i[p][j] * w_i[j] mod q_j for
 // ciphertexts x_i [2][nq][N] and plaintexts w_i (limb j at w_i + j * N)
-// given by address; same 128-bit accumulation as k_mac.
+// given by address; both polys per thread and the same 128-bit accumulation
+// as k_mac.
 __global__ void __launch_bounds__(TPB)
     k_mac_table(uint64_t* acc, const MacTable t, const ModConst* mc, uint32_t n, uint32_t nq,
                 uint32_t cnt, uint32_t accumulate) {
   const ModConst m = mc[blockIdx.y];
   const size_t limb_off = (size_t)blockIdx.y * n + pair_off();
-  const size_t xoff = (size_t)blockIdx.z * nq * n + limb_off;
-  Acc128 s0, s1;
+  const size_t pl = (size_t)nq * n;
+  Acc128 s[2][2];
   uint32_t i = 0;
   while (i < cnt) {
     const uint32_t end = i + 32 < cnt ? i + 32 : cnt;
     for (; i + 4 <= end; i += 4) {
-      U2 xv[4], wv[4];
+      U2 x0[4], x1[4], wv[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        xv[u] = ld2(t.x[i + u] + xoff);
+        x0[u] = ld2(t.x[i + u] + limb_off);
+        x1[u] = ld2(t.x[i + u] + pl + limb_off);
         wv[u] = ld2(t.w[i + u] + limb_off);
       }
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        s0.mac(xv[u].x, wv[u].x);
-        s1.mac(xv[u].y, wv[u].y);
+        s[0][0].mac(x0[u].x, wv[u].x);
+        s[0][1].mac(x0[u].y, wv[u].y);
+        s[1][0].mac(x1[u].x, wv[u].x);
+        s[1][1].mac(x1[u].y, wv[u].y);
       }
     }
     for (; i < end; ++i) {
-      const U2 xv = ld2(t.x[i] + xoff), wv = ld2(t.w[i] + limb_off);
-      s0.mac(xv.x, wv.x);
-      s1.mac(xv.y, wv.y);
+      const U2 a = ld2(t.x[i] + limb_off), b = ld2(t.x[i] + pl + limb_off);
+      const U2 wv = ld2(t.w[i] + limb_off);
+      s[0][0].mac(a.x, wv.x);
+      s[0][1].mac(a.y, wv.y);
+      s[1][0].mac(b.x, wv.x);
+      s[1][1].mac(b.y, wv.y);
     }
-    s0.lo = reduce128(s0.hi, s0.lo, m);
-    s0.hi = 0;
-    s1.lo = reduce128(s1.hi, s1.lo, m);
-    s1.hi = 0;
+    fold(s[0][0], m);
+    fold(s[0][1], m);
+    fold(s[1][0], m);
+    fold(s[1][1], m);
   }
-  uint64_t* ap = acc + xoff;
-  if (accumulate) {
-    const U2 a = ld2(ap);
-    s0.lo = add_mod(s0.lo, a.x, m.q);
-    s1.lo = add_mod(s1.lo, a.y, m.q);
+  for (int p = 0; p < 2; ++p) {
+    uint64_t* ap = acc + (size_t)p * pl + limb_off;
+    uint64_t v0 = s[p][0].lo, v1 = s[p][1].lo;
+    if (accumulate) {
+      const U2 a = ld2(ap);
+      v0 = add_mod(v0, a.x, m.q);
+      v1 = add_mod(v1, a.y, m.q);
+    }
+    st2(ap, v0, v1);
   }
-  st2(ap, s0.lo, s1.lo);
 }
 
 // Rescale step 1: centred lift of the (inverse-NTT'd) last limb into limbs
@@ -346,7 +367,7 @@ void poly_tensor(Context& c, uint64_t* out3, const uint64_t* a, const uint64_t* 
 
 void poly_mac(Context& c, uint64_t* acc, const uint64_t* x, const uint64_t* w, uint32_t n,
               uint32_t nq) {
-  FHE_LAUNCH(c, "k_mac", k_mac, grid_for(c, nq, 2), dim3(tpb_for(c)), 0, acc, x, w, c.d_const, c.n, nq, n);
+  FHE_LAUNCH(c, "k_mac", k_mac, grid_for(c, nq, 1), dim3(tpb_for(c)), 0, acc, x, w, c.d_const, c.n, nq, n);
 }
 
 void poly_mac_table(Context& c, uint64_t* acc, const uint64_t* const* x,
@@ -360,7 +381,7 @@ void poly_mac_table(Context& c, uint64_t* acc, const uint64_t* const* x,
       t.w[j] = w[i + j];
     }
     const uint32_t acc_flag = (accumulate || i > 0) ? 1u : 0u;
-    FHE_LAUNCH(c, "k_mac_table", k_mac_table, grid_for(c, nq, 2), dim3(tpb_for(c)), 0, acc, t, c.d_const, c.n, nq, k, acc_flag);
+    FHE_LAUNCH(c, "k_mac_table", k_mac_table, grid_for(c, nq, 1), dim3(tpb_for(c)), 0, acc, t, c.d_const, c.n, nq, k, acc_flag);
     i += k;
   } while (i < cnt);
 }

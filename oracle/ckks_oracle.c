@@ -614,6 +614,31 @@ void orc_rotate(const orc_ctx *c, const uint64_t *ct, uint32_t nq,
   free(ks);
 }
 
+/* EvalFastRotation with a shared precompute (src/fideslib_rotation_batch.hpp:
+ * 17-18): digits = ModUp(c1) computed once (orc_modup); per rotation the key
+ * inner product, ModDown, + c0 and the permutation, as orc_rotate. */
+void orc_rotate_hoisted(const orc_ctx *c, const uint64_t *ct, uint32_t nq,
+                        const uint64_t *digits, const uint64_t *key, uint32_t galois,
+                        uint64_t *out) {
+  const uint32_t n = c->n, ne = nq + c->K;
+  uint64_t *ext = malloc(sizeof(uint64_t) * 2 * ne * n);
+  uint64_t *ks = malloc(sizeof(uint64_t) * 2 * nq * n);
+  orc_ksk_inner(c, digits, nq, key, ext);
+  orc_moddown(c, ext, nq, ks);
+  orc_moddown(c, ext + (size_t)ne * n, nq, ks + (size_t)nq * n);
+  for (uint32_t i = 0; i < nq; ++i) {
+    uint64_t q = c->mods[i];
+    for (uint32_t e = 0; e < n; ++e)
+      ks[(size_t)i * n + e] = addmod(ks[(size_t)i * n + e], ct[(size_t)i * n + e], q);
+  }
+  for (uint32_t p = 0; p < 2; ++p)
+    for (uint32_t i = 0; i < nq; ++i)
+      orc_automorph_ntt(ks + ((size_t)p * nq + i) * n, out + ((size_t)p * nq + i) * n, n,
+                        galois);
+  free(ext);
+  free(ks);
+}
+
 /* OpenFHE DropLastElementAndScale: y_i = (x_i - [lift(x_l)]_{q_i}) q_l^-1,
  * lift centred on (q_l >> 1). */
 void orc_rescale(const orc_ctx *c, const uint64_t *in, uint32_t npoly,

@@ -107,6 +107,9 @@ void orc_keyswitch(const orc_ctx *c, const uint64_t *a, uint32_t nq,
                    const uint64_t *key, uint64_t *out /* [2][nq][N] */);
 void orc_rotate(const orc_ctx *c, const uint64_t *ct, uint32_t nq,
                 const uint64_t *key, uint32_t galois, uint64_t *out);
+void orc_rotate_hoisted(const orc_ctx *c, const uint64_t *ct, uint32_t nq,
+                        const uint64_t *digits, const uint64_t *key, uint32_t galois,
+                        uint64_t *out);
 void orc_rescale(const orc_ctx *c, const uint64_t *in, uint32_t npoly,
                  uint32_t nq, uint64_t *out /* [npoly][nq-1][N] */);
 void orc_tensor(const orc_ctx *c, const uint64_t *a, const uint64_t *b,

@@ -62,6 +62,7 @@ def _load():
         "orc_moddown": (None, [_p, _p, _u32, _p]),
         "orc_keyswitch": (None, [_p, _p, _u32, _p, _p]),
         "orc_rotate": (None, [_p, _p, _u32, _p, _u32, _p]),
+        "orc_rotate_hoisted": (None, [_p, _p, _u32, _p, _p, _u32, _p]),
         "orc_rescale": (None, [_p, _p, _u32, _u32, _p]),
         "orc_tensor": (None, [_p, _p, _p, _u32, _p]),
         "orc_relinearize": (None, [_p, _p, _u32, _p, _p]),
@@ -242,6 +243,14 @@ class Ctx:
         ct, key = u64(ct), u64(key)
         out = np.zeros_like(ct)
         lib.orc_rotate(self.h, ptr(ct), ct.shape[1], ptr(key), galois, ptr(out))
+        return out
+
+    def rotate_hoisted(self, ct, digits, key, galois):
+        """One rotation of a hoisted set: digits = self.modup(ct[1])."""
+        ct, digits, key = u64(ct), u64(digits), u64(key)
+        out = np.zeros_like(ct)
+        lib.orc_rotate_hoisted(self.h, ptr(ct), ct.shape[1], ptr(digits), ptr(key), galois,
+                               ptr(out))
         return out
 
     def rescale(self, x):

@@ -489,3 +489,17 @@ def test_classical128_audit_matches_openfhe_record():
     small = audit_chain(65536, q, p, 4, security_level=SecurityLevel.HEStd_128_classic,
                         secret_dist=SecretKeyDist.UNIFORM_TERNARY)
     assert small["guideline_max_qp_bits"] == 1747 and small["passed"] is False
+
+
+def test_hoisted_rotation_equals_single_rotation(small_scheme):
+    """A rotation from shared ModUp digits equals the full rotation (the
+    precompute only moves the ModUp out of the loop)."""
+    c, s = small_scheme[0], small_scheme[1]
+    rng = np.random.default_rng(41)
+    ct = np.stack([np.stack([rng.integers(0, q, c.n, dtype=np.uint64) for q in c.q])
+                   for _ in range(2)])
+    digits = c.modup(ct[1])
+    for step in (1, -3):
+        g = O.galois_elt(step, c.n)
+        key = c.galois_key(s, g, 50 + step)
+        assert np.array_equal(c.rotate_hoisted(ct, digits, key, g), c.rotate(ct, key, g))
