@@ -15,7 +15,8 @@ x 24 limbs at N = 2^16: forward NTT, plaintext MAC over the 64
 ciphertexts, inverse NTT) and reports NTT HBM GB/s, one encrypted Mamba-2
 SSM layer step at the 130M shape, and EvalBootstrap at N = 2^16 (one pass
 and the two-pass refresh, 45 limbs), and a 24-layer encrypted Mamba-2 decode
-(s/token, first and carried-state token).
+(s/token, first and carried-state token) at N = 2^16 and at the audited
+classical-128 setting (N = 2^17).
 
 Per-kernel times come from HIP events recorded on the library's stream
 around every launch (fhe_profile_begin / fhe_profile_end) over a profiled
@@ -340,19 +341,40 @@ def run_bootstrap(steps: int = 3, warmup: int = 2):
 REF_TOKEN_S = 396.6
 
 
-def run_decode(tokens: int = 2):
+def run_decode(tokens: int = 2, security: str = "not-set"):
     """Encrypted Mamba-2 decode of a seeded random-init 24-layer payload at
     the 130M shape (d_model 768, d_inner 1536, 24 heads x 64, state 128,
-    conv 4): N=2^16, 32768 slots, depth 44, 59-bit scale; the first token
-    from zero state, then carried-state tokens.  Errors against the
-    payload's polynomial circuit after decryption."""
+    conv 4), depth 44, 59-bit scale; the first token from zero state, then
+    carried-state tokens.  Errors against the payload's polynomial circuit
+    after decryption.  security "not-set": N=2^16, 32768 slots, sparse
+    ternary secret (the reference decoder's); "128-classic": the audited
+    classical-128 setting, N=2^17, 65536 slots, 45 Q + 12 P primes, four
+    digits, uniform ternary secret."""
     import tempfile
     from fhemamba_amd import mamba2_decode as D
     from fhemamba_amd import mamba2_payload as M
     with tempfile.TemporaryDirectory() as d:
         M.synthetic_chain(d, n_layers=24, n_test_tokens=tokens, seed=13)
-        rep = D.run_payload(d, seed=14, log=lambda m: None)
+        rep = D.run_payload(d, seed=14, security=security, log=lambda m: None)
     carried = rep["carried_token_seconds"]
+    if security == "128-classic":
+        a = rep["security_audit"]
+        return {
+            "s_per_token_first": rep["first_token_seconds"],
+            "s_per_token_carried": carried,
+            "max_abs_err_vs_polynomial": rep["max_abs_error_vs_polynomial"],
+            "bootstraps_per_token": rep["bootstraps"] / tokens,
+            "rotations_per_token": rep["rotations"] / tokens,
+            "security_audit": {k: a[k] for k in ("ring_dimension", "q_bits", "p_bits",
+                                                 "qp_bits", "q_towers", "p_towers",
+                                                 "hybrid_digits", "guideline_max_qp_bits",
+                                                 "passed")},
+            "secret_key_dist": rep["secret_key_dist"],
+            "workload": ("encrypted Mamba-2-130M-shaped decode, 24 layers (seeded random-init "
+                         "weights, synthetic payload), classical-128: N=2^17, 65536 slots, "
+                         "depth 44, 45 Q + 12 P primes, 4 digits, uniform ternary secret; "
+                         "first token from zero state, then carried state"),
+        }
     return {
         "s_per_token_first": rep["first_token_seconds"],
         "s_per_token_carried": carried,
@@ -601,6 +623,8 @@ def main() -> int:
     if not args.skip_decode:
         log("mamba-2 decode workload")
         out["mamba2_decode"] = run_decode()
+        log("mamba-2 decode workload, classical-128")
+        out["mamba2_decode_classical128"] = run_decode(security="128-classic")
     if args.copy_probe:
         log("copy probe")
         copy_probe(F)

@@ -307,6 +307,24 @@ class CryptoContext:
     def GetModuli(self) -> tuple[list[int], list[int]]:  # noqa: N802
         return list(self._ctx.q), list(self._ctx.p)
 
+    def SecurityAudit(self) -> dict:  # noqa: N802
+        """This context's classical-128 audit (audit_chain; the reference's
+        audit_ckks_context, fideslib_security.hpp:57-78)."""
+        q, p = self.GetModuli()
+        g = self._params._v
+        return audit_chain(self.n, q, p, self._dnum, security_level=g["SecurityLevel"],
+                           secret_dist=g["SecretKeyDist"])
+
+    def RequireClassical128(self) -> dict:  # noqa: N802
+        """The audit, or ValueError when it fails (require_classical128,
+        fideslib_security.hpp:37-41)."""
+        a = self.SecurityAudit()
+        if not a["passed"]:
+            raise ValueError("classical-128 CKKS audit failed: require HEStd_128_classic, "
+                             "uniform ternary, sigma >= 3.19 and actual HYBRID Q*P within "
+                             "the published dimension bound")
+        return a
+
     @property
     def device(self) -> Context:
         """The underlying device context (raw residue-level operations)."""

@@ -370,23 +370,49 @@ SECRET_KEY_DISTS = {"sparse-ternary": "SPARSE_TERNARY", "uniform-ternary": "UNIF
 
 
 def run_payload(payload_dir: str, *, tokens: int = 0, bootstrap_passes: int = 2, seed=None,
-                secret_key_dist: str = "sparse-ternary", log=print) -> dict:
+                secret_key_dist: str | None = None, security: str = "not-set",
+                layers: int = 0, log=print) -> dict:
     """Decode the payload's test embeddings in turn (carried state) and
     compare the decrypted outputs with its polynomial-circuit and exact
-    references; returns the report.  The secret is sparse ternary by
-    default, as the reference decoder's (stage1_mamba2_config.hpp:211,
-    resolve_secret_key_dist in stage1_mamba2_decode_fideslib.cpp:284-291)."""
+    references; returns the report.
+
+    security "not-set": N=2^16, 32768 slots, depth 44, dnum 3, and a sparse
+    ternary secret by default, as the reference decoder's
+    (stage1_mamba2_config.hpp:211, resolve_secret_key_dist in
+    stage1_mamba2_decode_fideslib.cpp:284-291).  security "128-classic": the
+    reference's audited classical-128 setting (packed_fideslib.cpp:
+    1060-1075, results/b300/2026-09-28/long-accuracy/*/native.json
+    security_audit): N=2^17, 65536 slots (batch = ring / 2, as the
+    decoder's stage1_mamba2_decode_fideslib.cpp:1005), depth 44, four HYBRID
+    digits (45 Q + 12 P primes, QP = 3376 bits against the 3523-bit bound),
+    a uniform ternary secret by default, and the audit must pass.  `layers`
+    > 0 decodes only the first layers (and the final norm)."""
     from . import ckks
     from .mamba2_payload import read_chain_payload
-    from .packed import build_context
+    from .packed import CLASSICAL128, build_context
+    if security not in ("not-set", "128-classic"):
+        raise ValueError("security must be not-set or 128-classic")
+    classical = security == "128-classic"
+    if secret_key_dist is None:
+        secret_key_dist = "uniform-ternary" if classical else "sparse-ternary"
     if secret_key_dist not in SECRET_KEY_DISTS:
         raise ValueError(f"secret key distribution must be one of {sorted(SECRET_KEY_DISTS)}")
     chain = read_chain_payload(payload_dir)
+    if layers:
+        if not 1 <= layers <= chain.n_layers:
+            raise ValueError("layers must be in 1..n_layers")
+        chain.layers = chain.layers[:layers]
+        chain.n_layers = layers
+        from .mamba2_payload import decode_tokens
+        chain.expected_final, _ = decode_tokens(chain, chain.input_embeddings, False)
+        chain.expected_poly_final, _ = decode_tokens(chain, chain.input_embeddings, True)
     n_tok = tokens or chain.n_test_tokens
-    slots = 32768
+    slots = 65536 if classical else 32768
     t0 = time.perf_counter()
+    extra = dict(CLASSICAL128) if classical else {}
     cc, keys = build_context(slots, seed=seed, secret_dist=getattr(
-        ckks.SecretKeyDist, SECRET_KEY_DISTS[secret_key_dist]))
+        ckks.SecretKeyDist, SECRET_KEY_DISTS[secret_key_dist]), **extra)
+    audit = cc.SecurityAudit() if classical else None
     dec = EncryptedMamba2Decoder(cc, keys, chain, bootstrap_passes=bootstrap_passes, log=log)
     setup = time.perf_counter() - t0
     states = dec.initial_states()
@@ -411,6 +437,8 @@ def run_payload(payload_dir: str, *, tokens: int = 0, bootstrap_passes: int = 2,
         "tokens": n_tok,
         "ring_dimension": cc.GetRingDimension(),
         "slots": slots,
+        "security": security,
+        "security_audit": audit,
         "secret_key_dist": secret_key_dist,
         "setup_seconds": setup,
         "seconds_per_token": per_token,
@@ -441,13 +469,17 @@ def main(argv=None) -> int:
     ap.add_argument("--bootstrap-passes", type=int, default=2, choices=(1, 2))
     ap.add_argument("--tolerance", type=float, default=1e-3,
                     help="pass threshold on the error against the polynomial circuit")
-    ap.add_argument("--secret-key-dist", default="sparse-ternary",
-                    choices=sorted(SECRET_KEY_DISTS))
+    ap.add_argument("--secret-key-dist", default=None, choices=sorted(SECRET_KEY_DISTS),
+                    help="default: sparse-ternary, uniform-ternary under 128-classic")
+    ap.add_argument("--security", default="not-set", choices=("not-set", "128-classic"))
+    ap.add_argument("--layers", type=int, default=0,
+                    help="decode only the first LAYERS layers (0: all)")
     args = ap.parse_args(sys.argv[1:] if argv is None else argv)
     try:
         report = run_payload(args.payload, tokens=args.tokens,
                              bootstrap_passes=args.bootstrap_passes,
-                             secret_key_dist=args.secret_key_dist)
+                             secret_key_dist=args.secret_key_dist, security=args.security,
+                             layers=args.layers)
     except Exception as exc:  # noqa: BLE001 - reported as exit code 2
         print(exc, file=sys.stderr)
         return 2

@@ -813,8 +813,13 @@ def parse_args(argv):
         i += 1
     if opts["security"] not in ("not-set", "128-classic"):
         raise ValueError("security must be not-set or 128-classic")
-    if opts["security"] == "128-classic":
-        raise ValueError("classical-128 (N = 2^17) is not supported by this executor")
+    # --security-digits: HYBRID digits of the classical-128 context, 1..16,
+    # only with 128-classic (packed_fideslib.cpp:913-914, :974, :991-992)
+    digits = [a for a in opts["accepted"] if a.startswith("--security-digits ")]
+    opts["accepted"] = [a for a in opts["accepted"] if not a.startswith("--security-digits ")]
+    opts["security_digits"] = int(digits[-1].split()[1]) if digits else 4
+    if not 1 <= opts["security_digits"] <= 16 or (digits and opts["security"] != "128-classic"):
+        raise ValueError("--security-digits must be 1..16 and requires --security 128-classic")
     if not (math.isfinite(poly_tol) and math.isfinite(exact_tol)) or poly_tol <= 0 or \
             exact_tol <= 0:
         raise ValueError("invalid error tolerance")
@@ -822,15 +827,28 @@ def parse_args(argv):
     return opts
 
 
+# Classical-128 as the reference executor sets it up (packed_fideslib.cpp:
+# 1042, 1060-1075): ring 2^17, full packing (65536 slots), uniform ternary,
+# HEStd_128_classic and `security_digits` HYBRID digits (default 4), the
+# audit required before any key is made.
+CLASSICAL128 = dict(ring_dim=131072, dnum=4, security="128-classic")
+
+
 def build_context(slots: int, *, ring_dim: int = 65536, depth: int = 44, scale_bits: int = 59,
-                  first_mod_bits: int = 60, dnum: int = 3, seed=None, secret_dist=None):
+                  first_mod_bits: int = 60, dnum: int = 3, seed=None, secret_dist=None,
+                  security: str = "not-set"):
     """The reference executor's context (packed_fideslib.cpp:1060-1083):
     uniform ternary (unless `secret_dist` says otherwise), FLEXIBLEAUTO,
     HYBRID, depth 44, 59-bit scale, 60-bit first prime, dnum 3, batch =
-    program slots, security not set."""
+    program slots, security not set; with security "128-classic" the
+    security level is HEStd_128_classic and the context must pass the
+    classical-128 audit (RequireClassical128) before keys are generated."""
     from . import ckks
+    if security not in ("not-set", "128-classic"):
+        raise ValueError("security must be not-set or 128-classic")
     p = ckks.CCParamsCKKSRNS()
-    p.SetSecurityLevel(ckks.SecurityLevel.HEStd_NotSet)
+    p.SetSecurityLevel(ckks.SecurityLevel.HEStd_128_classic if security == "128-classic"
+                       else ckks.SecurityLevel.HEStd_NotSet)
     p.SetSecretKeyDist(secret_dist or ckks.SecretKeyDist.UNIFORM_TERNARY)
     p.SetRingDim(ring_dim)
     p.SetBatchSize(slots)
@@ -841,6 +859,8 @@ def build_context(slots: int, *, ring_dim: int = 65536, depth: int = 44, scale_b
     p.SetKeySwitchTechnique(ckks.KeySwitchTechnique.HYBRID)
     p.SetNumLargeDigits(dnum)
     cc = ckks.GenCryptoContext(p, seed=seed)
+    if security == "128-classic":
+        cc.RequireClassical128()
     for f in (ckks.PKESchemeFeature.PKE, ckks.PKESchemeFeature.KEYSWITCH,
               ckks.PKESchemeFeature.LEVELEDSHE, ckks.PKESchemeFeature.ADVANCEDSHE,
               ckks.PKESchemeFeature.FHE):
@@ -853,7 +873,20 @@ def build_context(slots: int, *, ring_dim: int = 65536, depth: int = 44, scale_b
 def run(program: PackedProgram, opts: dict, *, context_args=None, log=print) -> tuple[dict, bool]:
     """Evaluate, decrypt and compare; returns (report, passed)."""
     t_setup = time.perf_counter()
-    cc, keys = build_context(program.slots, **(context_args or {}))
+    args = dict(context_args or {})
+    classical = opts.get("security") == "128-classic"
+    if classical:
+        # full packing, as the reference's S2C-first circuit requires
+        # (packed_fideslib.cpp:1040-1042); node widths stay the program's
+        program.slots = 65536
+        args.update(CLASSICAL128, dnum=opts.get("security_digits", 4))
+    cc, keys = build_context(program.slots, **args)
+    audit = cc.SecurityAudit() if classical else None
+    if classical and opts.get("result"):
+        with open(opts["result"] + ".parameters.json", "w") as f:
+            f.write(json.dumps(audit) + "\n")
+        log(f"classical128 ring={audit['ring_dimension']} QP_bits={audit['qp_bits']} "
+            f"bound={audit['guideline_max_qp_bits']} digits={audit['hybrid_digits']}")
     client = GenerationClient(opts["client_head"]) if opts.get("client_head") else None
     if client is not None and program.nodes[program.outputs[-1].node].size != client.width:
         raise ValueError("client head and final hidden width mismatch")
@@ -909,7 +942,7 @@ def run(program: PackedProgram, opts: dict, *, context_args=None, log=print) -> 
         "depth": len(cc.GetModuli()[0]) - 1,
         "scale_bits": round(math.log2(cc.GetScalingFactorReal(0))),
         "refresh_ring_dimension": cc.GetRingDimension(),
-        "security_audit": None,
+        "security_audit": audit,
         "gpu_dual_ring": False,
         "nodes": len(program.nodes),
         "setup_seconds": setup_s,

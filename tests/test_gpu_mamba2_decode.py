@@ -34,3 +34,20 @@ def test_command_line(tmp_path):
     assert rep["passed"] is True and rep["schema"] == "fhemamba-m2-decode-result-v1"
     assert rep["layers"] == 1 and rep["ring_dimension"] == 65536
     assert D.main([str(tmp_path / "missing"), str(res)]) == 2
+
+
+def test_classical128_two_layer_decode(tmp_path):
+    """Two layers of the 130M-shape payload at the audited classical-128
+    setting (N=2^17, 65536 slots, 45 Q + 12 P primes, four digits, uniform
+    ternary secret; QP 3376 bits within the 3523-bit bound), two tokens
+    with carried state, within the decode tolerance of the polynomial
+    circuit."""
+    M.synthetic_chain(str(tmp_path), n_layers=2, n_test_tokens=2, seed=6)
+    report = D.run_payload(str(tmp_path), seed=7, security="128-classic")
+    a = report["security_audit"]
+    print(f"classical-128 decode: {report['seconds_per_token']} s/token, errors "
+          f"{report['per_token_errors_vs_polynomial']}, audit {a}", flush=True)
+    assert report["ring_dimension"] == 131072 and report["slots"] == 65536
+    assert a["passed"] and a["qp_bits"] == 3376 and a["hybrid_digits"] == 4
+    assert report["secret_key_dist"] == "uniform-ternary"
+    assert report["max_abs_error_vs_polynomial"] < 1e-3

@@ -127,3 +127,36 @@ def test_full_batch_small_ring():
                               [ctx.load_key(k) for k in keys], gal)
     for out, key, g in zip(outs, keys, gal):
         assert np.array_equal(out.numpy(), orc.rotate(ct, key, g)), g
+
+
+def test_classical128_chain_key_switch():
+    """The reference's audited classical-128 chain (N=2^17, 45 Q + 12 P
+    primes, four digits: the golden OpenFHE chain) at the full level and at
+    31 limbs: relinearisation key switch and two hoisted rotations, word for
+    word against the oracle (the unfused ModUp / ModDown path: the fused
+    middle kernel's LDS does not hold 12 source lines at N=2^17)."""
+    import json
+    import os
+    gold = json.load(open(os.path.join(os.path.dirname(__file__), "golden",
+                                       "openfhe_prime_chain_n131072.json")))
+    q, p = gold["primes"][:gold["num_q"]], gold["primes"][gold["num_q"]:]
+    print(f"[classical-128] N=2^17 Q={len(q)} P={len(p)} dnum=4", flush=True)
+    ctx, orc = F.Context(17, q, p, 4, sampling="seeded"), O.Ctx(17, q, p, 4)
+    assert (ctx.L, ctx.K, ctx.dnum) == (45, 12, 4)
+    s = orc.secret(17)
+    rng = np.random.default_rng(18)
+    key = orc.relin_key(s, 19)
+    dkey = ctx.load_key(key)
+    gal = [O.galois_elt(r, ctx.n) for r in (1, -8)]
+    gkeys = [orc.galois_key(s, g, 60 + i) for i, g in enumerate(gal)]
+    dgk = [ctx.load_key(k) for k in gkeys]
+    for nq in (45, 31):
+        a = residues(rng, ctx.q[:nq], (1,), ctx.n)
+        assert np.array_equal(ctx.keyswitch(ctx.upload(a), dkey).numpy(),
+                              orc.keyswitch(a[0], key)), nq
+        ct = residues(rng, ctx.q[:nq], (2,), ctx.n)
+        dct = ctx.upload(ct)
+        outs = ctx.rotate_hoisted(dct, ctx.rotation_precompute(dct), dgk, gal)
+        for out, k, g in zip(outs, gkeys, gal):
+            assert np.array_equal(out.numpy(), orc.rotate(ct, k, g)), (nq, g)
+    ctx.close()

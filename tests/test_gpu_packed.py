@@ -111,3 +111,32 @@ def test_command_line_report(tmp_path):
     prog.write_text("\n".join(bad[:-1] + [" ".join(last)]) + "\n")
     assert P.main([str(prog), str(res), str(TOL), str(TOL)]) == 1
     assert json.loads(res.read_text())["passed"] is False
+
+
+def test_command_line_classical128(tmp_path):
+    """--security 128-classic as the reference executor runs it
+    (packed_fideslib.cpp:1040-1075): ring 2^17, full packing (65536 slots),
+    four HYBRID digits, uniform ternary, the audit written beside the
+    report (RESULT.parameters.json) and in it; a deep enough program to
+    refresh by full-packing bootstrapping at N=2^17."""
+    rng = np.random.default_rng(12)
+    b = ProgramBuilder(256, bound=4.0)
+    v = b.input(rng.uniform(0.5, 1.5, 16))
+    w = b.input(np.ones(16))
+    for _ in range(30):
+        v = b.mulp(b.mul(v, w), np.ones(16))
+    b.output(v)
+    prog, res = tmp_path / "program.txt", tmp_path / "native.json"
+    prog.write_text(b.text())
+    rc = P.main([str(prog), str(res), str(TOL), str(TOL), "--security", "128-classic"])
+    report = json.loads(res.read_text())
+    audit = json.loads((tmp_path / "native.json.parameters.json").read_text())
+    print(f"classical-128 packed: eval {report['eval_seconds']:.2f}s, "
+          f"{report['bootstraps']} bootstraps, error {report['max_abs_error_vs_polynomial']:.2e}",
+          flush=True)
+    assert rc == 0 and report["passed"] is True and report["security"] == "128-classic"
+    assert report["ring_dimension"] == 131072 and report["slots"] == 65536
+    assert report["security_audit"] == audit and audit["passed"] is True
+    assert (audit["qp_bits"], audit["hybrid_digits"], audit["guideline_max_qp_bits"]) == \
+        (3376, 4, 3523)
+    assert report["logical_refreshes"] >= 1

@@ -247,9 +247,41 @@ def test_command_line_options():
     for bad in (["p", "r", "1"], ["p", "r", "0", "1"], ["p", "r", "1", "1", "--bogus"],
                 ["p", "r", "1", "1", "--bootstrap-passes", "3"],
                 ["p", "r", "1", "1", "--security", "256"],
+                ["p", "r", "1", "1", "--security-digits", "3"],
+                ["p", "r", "1", "1", "--security", "128-classic", "--security-digits", "0"],
+                ["p", "r", "1", "1", "--security", "128-classic", "--security-digits", "17"],
                 ["p", "r", "1", "1", "--s2c-first"]):
         with pytest.raises(ValueError):
             P.parse_args(bad)
+
+
+def test_classical128_options():
+    """--security 128-classic with the reference's digit rule: 4 digits by
+    default, --security-digits 1..16 only with it (packed_fideslib.cpp:913,
+    974, 991-992)."""
+    o = P.parse_args(["p", "r", "1e-3", "1e-2", "--security", "128-classic"])
+    assert o["security"] == "128-classic" and o["security_digits"] == 4
+    o = P.parse_args(["p", "r", "1e-3", "1e-2", "--security", "128-classic",
+                      "--security-digits", "6"])
+    assert o["security_digits"] == 6 and o["accepted"] == []
+
+
+def test_classical128_chain_passes_the_audit_at_n17_only():
+    """The classical-128 chain the executor builds (depth 44, scale 59,
+    first 60, 4 digits, uniform ternary) passes the audit at N=2^17 with the
+    recorded QP of 3376 bits; the same depth at N=2^16 cannot (its bound is
+    1747 bits), nor can a sparse-ternary secret."""
+    from fhemamba_amd import ckks
+    from fhemamba_amd.core import gen_moduli
+    q, p = gen_moduli(17, 44, 59, 60, 4)
+    a = ckks.audit_chain(131072, q, p, 4, security_level=ckks.SecurityLevel.HEStd_128_classic,
+                         secret_dist=ckks.SecretKeyDist.UNIFORM_TERNARY)
+    assert a["passed"] and a["qp_bits"] == 3376 and a["q_towers"] == 45 and a["p_towers"] == 12
+    q16, p16 = gen_moduli(16, 44, 59, 60, 4)
+    a16 = ckks.audit_chain(65536, q16, p16, 4,
+                           security_level=ckks.SecurityLevel.HEStd_128_classic,
+                           secret_dist=ckks.SecretKeyDist.UNIFORM_TERNARY)
+    assert not a16["passed"] and a16["qp_bits"] > 1747
 
 
 def test_client_head_reader(tmp_path):
