@@ -138,6 +138,12 @@ Context::Context(uint32_t log_n_, const uint64_t* q, uint32_t num_q, const uint6
   fill_entropy(sampling.master, sizeof(sampling.master));
   sampling.secure = true;
   hip_check(hipSetDevice(device), "hipSetDevice");
+  {
+    int lds = 0;
+    hip_check(hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, device),
+              "hipDeviceGetAttribute(LDS)");
+    lds_per_block = lds > 0 ? (uint32_t)lds : 65536u;
+  }
   hip_check(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "hipStreamCreate");
   own_stream = true;
   pool.reset(new Pool(device));

@@ -124,6 +124,7 @@ struct Context {
   hipStream_t stream = nullptr;
   bool own_stream = false;
   uint32_t log_n = 0, n = 0, L = 0, K = 0, dnum = 0, alpha = 0;
+  uint32_t lds_per_block = 65536;    // LDS a workgroup may allocate (160 KB on gfx950)
   std::vector<uint64_t> mods;        // L + K
   std::vector<uint64_t> psi;         // minimal primitive 2N-th roots
   std::vector<ModConst> hconst;

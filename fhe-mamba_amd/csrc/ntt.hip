@@ -1415,7 +1415,7 @@ template <int S1, int S2, bool ALT = false>
 void launch_mid(Context& c, const char* name, const MidArgs& a, uint32_t npoly,
                 uint32_t max_src) {
   const uint32_t tiles = npoly << S2;
-  if (tiles < MID_SMALL_TILES && mid_lds_bytes<S1, 8>(max_src) <= 65536) {
+  if (tiles < MID_SMALL_TILES && mid_lds_bytes<S1, 8>(max_src) <= c.lds_per_block) {
     FHE_LAUNCH(c, name, (k_convert_mid<S1, S2, 8, ALT>), dim3(tiles), dim3(512),
                (mid_lds_bytes<S1, 8>(max_src)), a, c.d_const, c.d_tw_inv, c.d_tw_fwd);
     return;
@@ -1438,9 +1438,9 @@ MidPlan mid_plan(const Context& c, const ConvPlan& pl, uint32_t src_mod0, uint32
 
 bool mid_lds_fits(const Context& c, uint32_t nsrc) {
   switch (c.log_n) {
-    case 13: case 14: return mid_lds_bytes<7, 4>(nsrc) <= 65536;
-    case 15: case 16: return mid_lds_bytes<8, 4>(nsrc) <= 65536;
-    case 17: return mid_lds_bytes<9, 4>(nsrc) <= 65536;
+    case 13: case 14: return mid_lds_bytes<7, 4>(nsrc) <= c.lds_per_block;
+    case 15: case 16: return mid_lds_bytes<8, 4>(nsrc) <= c.lds_per_block;
+    case 17: return mid_lds_bytes<9, 4>(nsrc) <= c.lds_per_block;
     default: return false;
   }
 }

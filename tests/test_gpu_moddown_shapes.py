@@ -133,8 +133,8 @@ def test_classical128_chain_key_switch():
     """The reference's audited classical-128 chain (N=2^17, 45 Q + 12 P
     primes, four digits: the golden OpenFHE chain) at the full level and at
     31 limbs: relinearisation key switch and two hoisted rotations, word for
-    word against the oracle (the unfused ModUp / ModDown path: the fused
-    middle kernel's LDS does not hold 12 source lines at N=2^17)."""
+    word against the oracle (the fused middle kernel holds the 12 source
+    lines of a column in up to 160 KB of LDS per workgroup)."""
     import json
     import os
     gold = json.load(open(os.path.join(os.path.dirname(__file__), "golden",
