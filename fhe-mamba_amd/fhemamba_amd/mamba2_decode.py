@@ -139,9 +139,39 @@ class EncryptedMamba2Decoder:
     def cheb_need(self, spec: PolySpec) -> int:
         return 1 + cheb_ps_depth(len(spec.coeffs) - 1) + 1
 
+    def sched_inv_sqrt(self, v, spec, vbound: float, ibound: float):
+        """Scheduled normalization (ScheduledInvSqrtSpec): u = v seed^2 in
+        (0, 1], per stage f = a - b u, y <- y f, u <- u f^2, then the
+        recomputed Newton step y (1.5 - 0.5 v y^2).  The schedule keeps u in
+        (0, 1] and y below 1 / sqrt(v), so u refreshes at bound 1, y at the
+        inverse's bound and f at the largest a."""
+        ev, cc = self.ev, self.cc
+        fbound = BOUND_MARGIN * max(a for a, _ in spec.coefficients)
+        ubound = BOUND_MARGIN
+        n = len(spec.coefficients)
+        v = self.ready(v, 3, vbound)
+        u = ev.scale(v, spec.seed * spec.seed)
+        y = None
+        for i, (a, b) in enumerate(spec.coefficients):
+            u = self.ready(u, 4, ubound)
+            f = cc.EvalAdd(ev.scale(u, -b), a)
+            if y is None:
+                y = ev.scale(f, spec.seed)
+            else:
+                y = ev.mul(self.ready(y, 1, ibound), self.ready(f, 1, fbound))
+            if i + 1 < n:
+                f = self.ready(f, 2, fbound)
+                u = ev.mul(u, ev.mul(f, f))
+        y = self.ready(y, 3, ibound)
+        v = self.ready(v, 2, vbound)
+        t = ev.mul(v, ev.mul(y, y))
+        return ev.mul(y, cc.EvalAdd(ev.scale(t, -0.5), 1.5))
+
     def inv_sqrt(self, v, spec: PolySpec, vbound: float, ibound: float):
         """The payload's Newton inverse square root of v (v in every slot,
         so refreshes need no mask)."""
+        if spec.kind == "scaled-goldschmidt-invsqrt-v1":
+            return self.sched_inv_sqrt(v, spec, vbound, ibound)
         v = self.ready(v, self.cheb_need(spec) + 2, vbound)
         q = self.cheb(v, spec, np.ones(self.slots))
         if spec.kind == "poly-newton":
@@ -345,7 +375,7 @@ class EncryptedMamba2Decoder:
                      f"bootstraps {self.ev.stats['bootstraps']}")
         last = self.chain.layers[-1]
         B = self.bounds[-1]
-        inv = self.rms_scale(h, self.d, self.chain.final_norm_eps, last.polys["rms_invsqrt"],
+        inv = self.rms_scale(h, self.d, self.chain.final_norm_eps, self.chain.final_invsqrt(),
                              B["out_residual"], B["out_variance"], B["out_inv"])
         h = self.ready(h, 2, B["out_residual"], self._support(0, self.d))
         final = self.ev.plain(h, self._vec({0: self.chain.final_norm_w}), True)

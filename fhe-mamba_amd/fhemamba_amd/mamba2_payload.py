@@ -17,8 +17,10 @@ Polynomial kinds (src/fhemamba/m1_payload.py:379-408 and
 src/fhemamba/ops.py:178-459): "cheb" (Chebyshev series on [lo, hi]),
 "cheb-squared" (p(x)^2), "cheb-resquared" (p(x / 2^s)^(2^s), optional head
 mask), "poly-newton" (y = 0.9 p(v), Newton steps y <- y (1.5 - v y^2 / 2)),
-"sq-poly-newton" (y = damping q(v)^2, Newton steps).  The joint-gate and
-scheduled-normalization variants are not read.
+"sq-poly-newton" (y = damping q(v)^2, Newton steps), and the scheduled
+normalization recipe "scaled-goldschmidt-invsqrt-v1" for the block, gated
+and final norms (chain.json final_norm_poly).  Joint-gate payloads
+("fhemamba-m1-joint-v1", "fhemamba-m2-chain-joint-v1") are refused.
 
 Decode semantics per layer (src/fhemamba/reference.py:182-339, ngroups 1,
 no MLP split): hidden -> RMSNorm (rms_invsqrt) -> in_proj -> z | xBC | dt;
@@ -111,6 +113,66 @@ class PolySpec:
                    None if mask is None else np.asarray(mask, dtype=np.float64))
 
 
+@dataclass
+class ScheduledInvSqrtSpec:
+    """Scheduled normalization ("scaled-goldschmidt-invsqrt-v1"): a public
+    schedule of Goldschmidt stages and one final recomputed Newton step,
+    the recipe the reference exports (src/fhemamba/normalization.py:40-91,
+    read by native/fideslib_stage0/src/stage1_mamba2_payload.cpp:437-441):
+      u = v seed^2, y = seed;
+      per stage (a, b): f = a - b u, y <- y f, u <- u f^2 (not after the
+      last stage);
+      y <- y (1.5 - 0.5 v y^2).
+    Evaluated in float64, as the recipe's oracle workspace."""
+    lo: float
+    hi: float
+    seed: float
+    coefficients: tuple
+    tolerance: float
+    kind: str = "scaled-goldschmidt-invsqrt-v1"
+
+    def __call__(self, v):
+        v = np.asarray(v, dtype=np.float64)
+        u = v * self.seed * self.seed
+        y = self.seed
+        n = len(self.coefficients)
+        for i, (a, b) in enumerate(self.coefficients):
+            f = a - b * u
+            y = y * f
+            if i + 1 < n:
+                u = u * (f * f)
+        return y * (1.5 - 0.5 * (v * (y * y)))
+
+    def to_json(self) -> dict:
+        return {"kind": self.kind, "lo": self.lo, "hi": self.hi, "seed": self.seed,
+                "coefficients": [list(p) for p in self.coefficients],
+                "tolerance": self.tolerance, "final_recomputed_newton": True,
+                "oracle_workspace_dtype": "float64"}
+
+    @classmethod
+    def from_json(cls, d: dict) -> "ScheduledInvSqrtSpec":
+        """The reference's recipe check (normalization.py:142-155, :55-63)."""
+        if (d.get("kind") != "scaled-goldschmidt-invsqrt-v1"
+                or d.get("final_recomputed_newton") is not True
+                or d.get("oracle_workspace_dtype") != "float64"):
+            raise ValueError("unsupported inverse-square-root recipe")
+        coeffs = tuple((float(a), float(b)) for a, b in d["coefficients"])
+        lo, hi, seed, tol = (float(d[k]) for k in ("lo", "hi", "seed", "tolerance"))
+        vals = [lo, hi, seed, tol] + [x for pr in coeffs for x in pr]
+        if not all(math.isfinite(x) for x in vals) or not 0 < lo < hi or not seed > 0 \
+                or not 0 < tol < 1 or not coeffs:
+            raise ValueError("invalid inverse-square-root schedule")
+        return cls(lo, hi, seed, coeffs, tol)
+
+
+def read_poly(d: dict):
+    """A site's polynomial spec: a Chebyshev-based PolySpec or a scheduled
+    inverse square root."""
+    if d.get("kind") == "scaled-goldschmidt-invsqrt-v1":
+        return ScheduledInvSqrtSpec.from_json(d)
+    return PolySpec.from_json(d)
+
+
 def fit_chebyshev(fn, lo: float, hi: float, degree: int) -> np.ndarray:
     """Least-squares Chebyshev fit of fn on [lo, hi] at Chebyshev points."""
     if not hi > lo:
@@ -165,6 +227,12 @@ class ChainPayload:
     expected_final: np.ndarray
     expected_poly_final: np.ndarray | None
     layers: list = field(default_factory=list)
+    # dedicated final-norm inverse square root (scheduled payloads); None:
+    # the last layer's rms_invsqrt (m1_payload.py:421-426)
+    final_norm_poly: object = None
+
+    def final_invsqrt(self):
+        return self.final_norm_poly or self.layers[-1].polys["rms_invsqrt"]
 
 
 def _read_bin(path: str, shape) -> np.ndarray:
@@ -188,9 +256,10 @@ def read_layer_payload(directory: str) -> LayerPayload:
     polys = {}
     for name in SITES:
         spec = meta["polys"][name]
-        if spec.get("kind") == "scaled-goldschmidt-invsqrt-v1":
-            raise ValueError("scheduled normalization recipes are not supported")
-        polys[name] = PolySpec.from_json(spec)
+        if spec.get("kind") == "scaled-goldschmidt-invsqrt-v1" and \
+                name not in ("rms_invsqrt", "gated_rms_invsqrt"):
+            raise ValueError(f"a scheduled inverse square root cannot serve {name}")
+        polys[name] = read_poly(spec)
     tensors = {name: _read_bin(os.path.join(directory, name + ".bin"), meta["tensors"][name])
                for name in LAYER_TENSORS}
     layer = LayerPayload(int(d["d_model"]), int(d["d_inner"]), int(d["num_heads"]),
@@ -206,7 +275,7 @@ def read_layer_payload(directory: str) -> LayerPayload:
         raise ValueError("the decoder supports one B/C group")
     if layer.conv_dim != layer.d_inner + 2 * layer.state_size:
         raise ValueError("conv_dim must be d_inner + 2 * state_size")
-    mask = polys["decay_exp"].head_mask
+    mask = getattr(polys["decay_exp"], "head_mask", None)
     if mask is not None and (len(mask) != layer.num_heads or
                              not np.all((mask == 0) | (mask == 1))):
         raise ValueError("decay_exp head_mask must hold one 0/1 value per head")
@@ -235,6 +304,8 @@ def read_chain_payload(directory: str) -> ChainPayload:
                          rb("chain_expected_poly_final") if "chain_expected_poly_final" in tens
                          else None)
     chain.layers = [read_layer_payload(os.path.join(directory, d)) for d in dirs]
+    if meta.get("final_norm_poly") is not None:
+        chain.final_norm_poly = read_poly(meta["final_norm_poly"])
     first = chain.layers[0]
     for i, lay in enumerate(chain.layers):
         if (lay.d_model, lay.d_inner, lay.num_heads, lay.head_dim, lay.state_size,
@@ -298,7 +369,7 @@ def layer_step(lay: LayerPayload, hidden: np.ndarray, state: LayerState, polynom
 
 def final_norm(chain: ChainPayload, hidden: np.ndarray, polynomial: bool):
     v = np.mean(hidden ** 2) + chain.final_norm_eps
-    poly = chain.layers[-1].polys["rms_invsqrt"] if polynomial else None
+    poly = chain.final_invsqrt() if polynomial else None
     return hidden * rms_inv(v, poly) * chain.final_norm_w
 
 

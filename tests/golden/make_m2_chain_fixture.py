@@ -1,4 +1,4 @@
-"""Write tests/golden/m2_chain_tiny/ with the reference's own chain exporter.
+"""Write the Mamba-2 chain payload fixtures with the reference's own exporter.
 
 Runs `export_chain_payload` (src/fhemamba/m1_payload.py:901) of the
 reference tree at /root/reference on the tiny seeded Hugging Face Mamba-2
@@ -6,8 +6,17 @@ that the reference's own tests build (tests/conftest.py:9-34: vocab 97,
 hidden 32, state 8, 2 layers, conv 4, expand 2, 4 heads x 16, 1 group,
 chunk 8, torch seed 19) with the reference tests' tokenizer stand-in
 (tests/conftest.py:37-50), the prompt "The capital of France is" and two
-test tokens.  Only the payload it writes (float32 tensors and JSON) is kept:
-nothing of the reference is copied, and nothing here runs at test time.
+test tokens:
+  m2_chain_tiny/        the default payload (fhemamba-m1-v1 layers);
+  m2_chain_tiny_sched/  scheduled normalization: the bundle the reference's
+                        tests build (tests/test_scheduled_payload.py:18-33,
+                        plan_invsqrt(1e-6, hi) for every block, gated and
+                        final norm), 16 calibration tokens;
+  m2_chain_tiny_joint/  the same plus shared-factor joint gates from the
+                        gate bundle of tests/test_scheduled_payload.py:42-67
+                        (fhemamba-m1-joint-v1 / fhemamba-m2-chain-joint-v1).
+Only the payloads it writes (float32 tensors and JSON) are kept: nothing of
+the reference is copied, and nothing here runs at test time.
 
     python tests/golden/make_m2_chain_fixture.py [REFERENCE_ROOT]
 """
@@ -18,7 +27,6 @@ import tempfile
 from types import SimpleNamespace
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-OUT = os.path.join(HERE, "m2_chain_tiny")
 
 
 class Tokenizer:
@@ -43,17 +51,63 @@ def tiny_mamba2(seed=19):
     return transformers.Mamba2ForCausalLM(config).float().eval()
 
 
+def normalization_bundle(path):
+    """The reference tests' schedule bundle (tests/test_scheduled_payload.py:18-33)."""
+    import json
+    from fhemamba.normalization import plan_invsqrt
+    bundle = {
+        "format": "fhemamba-normalization-schedules-v1",
+        "operators": [
+            {"layer": layer, "site": site, "recipe": plan_invsqrt(1e-6, hi).recipe()}
+            for layer, site, hi in ((0, "rms_invsqrt", 50), (0, "gated_rms_invsqrt", 100),
+                                    (1, "rms_invsqrt", 50), (1, "gated_rms_invsqrt", 100),
+                                    (2, "rms_invsqrt", 200))
+        ],
+    }
+    with open(path, "w") as f:
+        json.dump(bundle, f)
+
+
+def gate_bundle(path, model):
+    """The reference tests' joint-gate bundle (tests/test_scheduled_payload.py:42-67)."""
+    import json
+    import numpy as np
+    from fhemamba.payload_surrogate import public_gate_domains
+    arrays = {}
+    for layer, block in enumerate(model.backbone.layers):
+        lo, hi = public_gate_domains(block)
+        for name, value in {"lo": lo, "hi": hi, "p": np.full((1, len(lo)), 0.5),
+                            "q": np.full((1, len(lo)), 0.75),
+                            "rates": block.mixer.A_log.detach().exp().double().numpy()}.items():
+            arrays[f"layer_{layer}_{name}"] = value
+    arrays["manifest"] = np.array(json.dumps({"format": "dissipative-mamba2-gates-v1",
+                                              "layers": [0, 1],
+                                              "input_payload_sha256": "0" * 64}))
+    np.savez(path, **arrays)
+
+
 def main(reference_root="/root/reference"):
     sys.path.insert(0, os.path.join(reference_root, "src"))
     from fhemamba.m1_payload import export_chain_payload
     model = tiny_mamba2()
     with tempfile.TemporaryDirectory() as tmp:
-        out = export_chain_payload(model, Tokenizer(), os.path.join(tmp, "chain"),
-                                   n_test_tokens=2)
-        if os.path.isdir(OUT):
-            shutil.rmtree(OUT)
-        shutil.copytree(out, OUT)
-    print(OUT)
+        norms, gates = os.path.join(tmp, "norms.json"), os.path.join(tmp, "gates.npz")
+        normalization_bundle(norms)
+        gate_bundle(gates, model)
+        runs = {
+            "m2_chain_tiny": dict(),
+            "m2_chain_tiny_sched": dict(cal_tokens=16, normalization_bundle=norms),
+            "m2_chain_tiny_joint": dict(cal_tokens=16, normalization_bundle=norms,
+                                        stabilized_gate_bundle=gates),
+        }
+        for name, kw in runs.items():
+            out = export_chain_payload(model, Tokenizer(), os.path.join(tmp, name),
+                                       n_test_tokens=2, **kw)
+            dest = os.path.join(HERE, name)
+            if os.path.isdir(dest):
+                shutil.rmtree(dest)
+            shutil.copytree(out, dest)
+            print(dest)
 
 
 if __name__ == "__main__":

@@ -25,3 +25,15 @@ def test_reference_exported_payload_decodes_within_tolerance():
           f"{report['max_abs_error_vs_exact']:.2e}", flush=True)
     assert report["tokens"] == 2 and report["layers"] == 2
     assert report["max_abs_error_vs_polynomial"] < TOL
+
+
+def test_reference_scheduled_normalization_payload_decodes():
+    """The exporter's scheduled-normalization payload (Goldschmidt schedules
+    for the block, gated and final norms) decoded on the GPU, two tokens
+    with carried state, against its chain_expected_poly_final."""
+    sched = os.path.join(os.path.dirname(__file__), "golden", "m2_chain_tiny_sched")
+    report = D.run_payload(sched, seed=32, log=lambda m: None)
+    print(f"scheduled payload: {report['seconds_per_token']} s/token, {report['bootstraps']} "
+          f"bootstraps, errors vs polynomial {report['per_token_errors_vs_polynomial']}",
+          flush=True)
+    assert report["max_abs_error_vs_polynomial"] < TOL

@@ -97,3 +97,63 @@ def test_decoder_circuit_on_slots_meets_exporter_criterion(chain):
         ct, states = dec.step(e, states)
         got = dec.decrypt(ct)
         assert _rel(got, chain.expected_poly_final[k]) < 1e-5, k
+
+
+# ------------------------------------------------------------- variants
+SCHED = os.path.join(os.path.dirname(__file__), "golden", "m2_chain_tiny_sched")
+JOINT = os.path.join(os.path.dirname(__file__), "golden", "m2_chain_tiny_joint")
+
+
+def _ref(directory, name):
+    meta = json.load(open(os.path.join(directory, "chain.json")))
+    return np.fromfile(os.path.join(directory, name + ".bin"), dtype="<f4").reshape(
+        meta["tensors"][name]).astype(np.float64)
+
+
+def test_scheduled_normalization_payload():
+    """The exporter's scheduled-normalization payload (the reference tests'
+    plan_invsqrt bundle): block, gated and final norms read as
+    scaled-goldschmidt-invsqrt-v1 recipes, the final norm from chain.json's
+    final_norm_poly, and the polynomial decode reproduces the exporter's
+    circuit (chain_expected_poly_final)."""
+    ch = M.read_chain_payload(SCHED)
+    for lay in ch.layers:
+        assert lay.polys["rms_invsqrt"].kind == "scaled-goldschmidt-invsqrt-v1"
+        assert lay.polys["gated_rms_invsqrt"].kind == "scaled-goldschmidt-invsqrt-v1"
+    assert ch.final_norm_poly is not None and ch.final_norm_poly.hi == 200
+    finals, _ = M.decode_tokens(ch, ch.input_embeddings, True)
+    assert _rel(finals, ch.expected_poly_final) < 1e-5
+    exact, _ = M.decode_tokens(ch, ch.input_embeddings, False)
+    assert _rel(exact, ch.expected_final) < 1e-5
+
+
+def test_scheduled_recipe_matches_inverse_square_root():
+    """Each schedule meets its own relative-error target on its interval
+    (the certificate's claim, normalization.py:173-210)."""
+    ch = M.read_chain_payload(SCHED)
+    spec = ch.final_norm_poly
+    v = np.geomspace(spec.lo, spec.hi, 2001)
+    assert np.max(np.abs(spec(v) * np.sqrt(v) - 1)) < spec.tolerance * 1.01
+
+
+def test_scheduled_decoder_circuit_on_slots():
+    from fhemamba_amd.mamba2_decode import EncryptedMamba2Decoder
+    from packed_builder import SlotContext, SlotKeys
+    ch = M.read_chain_payload(SCHED)
+    dec = EncryptedMamba2Decoder(SlotContext(1024), SlotKeys(), ch)
+    states = dec.initial_states()
+    for k, e in enumerate(ch.input_embeddings):
+        ct, states = dec.step(e, states)
+        assert _rel(dec.decrypt(ct), ch.expected_poly_final[k]) < 1e-5, k
+
+
+def test_joint_gate_payload_is_refused():
+    """The exporter's joint-gate payload (fhemamba-m2-chain-joint-v1 with
+    fhemamba-m1-joint-v1 layers: shared-dissipation-factor gates in place of
+    dt_softplus and decay_exp) is refused by format, not misread."""
+    meta = json.load(open(os.path.join(JOINT, "chain.json")))
+    assert meta["format"] == "fhemamba-m2-chain-joint-v1"
+    with pytest.raises(ValueError, match="format"):
+        M.read_chain_payload(JOINT)
+    with pytest.raises(ValueError, match="joint"):
+        M.read_layer_payload(os.path.join(JOINT, "layer_00"))
