@@ -60,9 +60,10 @@ def _giant_split(n: int, m: int) -> int:
     return k
 
 
-def cheb_ps_depth(degree: int) -> int:
-    """Multiplicative depth the Paterson-Stockmeyer evaluation spends."""
-    m = cheb_baby_size(degree)
+def cheb_ps_depth(degree: int, baby: int | None = None) -> int:
+    """Multiplicative depth the Paterson-Stockmeyer evaluation spends
+    (baby-step size `baby`, default cheb_baby_size(degree))."""
+    m = baby or cheb_baby_size(degree)
     memo: dict[int, int] = {}
 
     def t_depth(i: int) -> int:
@@ -86,6 +87,40 @@ def cheb_ps_depth(degree: int) -> int:
     return depth(degree)
 
 
+class ChebBasis:
+    """T_i(u) built on demand from T_1 = u by T_2j = 2 T_j^2 - 1 and
+    T_2j+1 = 2 T_j+1 T_j - u, each kept once (series of one input may share
+    it).  Backends with Rescale keep each basis polynomial rescaled once (it
+    is multiplied many times)."""
+
+    def __init__(self, cc, u):
+        self.cc, self.u = cc, u
+        self.settle = getattr(cc, "Rescale", None) or (lambda ct: ct)
+        self.cache = {1: u}
+
+    def __call__(self, i: int):
+        if i not in self.cache:
+            cc = self.cc
+            if i % 2 == 0:
+                h = self(i // 2)
+                sq = cc.EvalMult(h, h)
+                self.cache[i] = self.settle(cc.EvalSub(cc.EvalAdd(sq, sq), 1.0))
+            else:
+                pr = cc.EvalMult(self(i // 2 + 1), self(i // 2))
+                self.cache[i] = self.settle(cc.EvalSub(cc.EvalAdd(pr, pr), self.u))
+        return self.cache[i]
+
+
+def _ps_split(c, n: int, k: int):
+    """p = rem + T_k quot for sum_{i<=n} c_i T_i, from T_k T_j =
+    (T_{k+j} + T_{k-j}) / 2 (coefficients scalars or arrays)."""
+    quot = [c[k]] + [2.0 * c[k + j] for j in range(1, n - k + 1)]
+    rem = list(c[:k])
+    for i in range(k + 1, n + 1):
+        rem[2 * k - i] = rem[2 * k - i] - c[i]
+    return rem, quot
+
+
 def chebyshev_ps(cc, u, coeffs: Sequence[float], floor: float = CHEB_COEFF_FLOOR,
                  const_ct=None):
     """sum_i coeffs[i] T_i(u) by Paterson-Stockmeyer
@@ -100,24 +135,10 @@ def chebyshev_ps(cc, u, coeffs: Sequence[float], floor: float = CHEB_COEFF_FLOOR
     if degree < 1:
         return constant(coeffs[0] if len(coeffs) else 0.0)
     m = cheb_baby_size(degree)
-    # Backends with Rescale keep each basis polynomial rescaled once (it is
-    # multiplied many times); with EvalLinearWSum a leaf's sum of c_i T_i is
-    # one weighted sum at the deepest T_i level instead of products aligned
-    # pairwise.  Both leave the result's value unchanged.
-    settle = getattr(cc, "Rescale", None) or (lambda ct: ct)
+    # with EvalLinearWSum a leaf's sum of c_i T_i is one weighted sum at the
+    # deepest T_i level instead of products aligned pairwise (same value)
     wsum = getattr(cc, "EvalLinearWSum", None)
-    cache = {1: u}
-
-    def cheb(i: int):
-        if i not in cache:
-            if i % 2 == 0:
-                h = cheb(i // 2)
-                sq = cc.EvalMult(h, h)
-                cache[i] = settle(cc.EvalSub(cc.EvalAdd(sq, sq), 1.0))
-            else:
-                pr = cc.EvalMult(cheb(i // 2 + 1), cheb(i // 2))
-                cache[i] = settle(cc.EvalSub(cc.EvalAdd(pr, pr), u))
-        return cache[i]
+    cheb = ChebBasis(cc, u)
 
     def evaluate(c: list[float]):
         n = len(c) - 1
@@ -135,16 +156,43 @@ def chebyshev_ps(cc, u, coeffs: Sequence[float], floor: float = CHEB_COEFF_FLOOR
             if abs(c[0]) >= floor:
                 acc = cc.EvalAdd(acc, c[0])
             return acc
-        # p = a' + T_k * b~ using T_k T_j = (T_{k+j} + T_{k-j}) / 2.
         k = _giant_split(n, m)
-        quot = [c[k]] + [2.0 * c[k + j] for j in range(1, n - k + 1)]
-        rem = list(c[:k])
-        for i in range(k + 1, n + 1):
-            rem[2 * k - i] -= c[i]
+        rem, quot = _ps_split(c, n, k)
         giant = cc.EvalMult(cheb(k), evaluate(quot))
         return cc.EvalAdd(evaluate(rem), giant)
 
     return evaluate(list(coeffs))
+
+
+def chebyshev_ps_rows(basis: ChebBasis, rows, baby: int, mul, add, const):
+    """sum_i rows[i] (.) T_i(u) with one coefficient per slot (rows[i] a
+    vector): the vector-coefficient Paterson-Stockmeyer evaluation of
+    native/fideslib_stage0/include/stage1_joint_gates.hpp:68-125 (same
+    split as chebyshev_ps, baby-step size `baby` so that series of one input
+    share the basis).  mul(ct, row, key) is a plaintext product, add(ct, row)
+    a plaintext addition and const(row) a ciphertext holding row; `key`
+    names the row's place in the recursion (a plaintext cache key).  Only
+    all-zero rows are skipped: no coefficient threshold."""
+    cc = basis.cc
+
+    def evaluate(c: list, path: str):
+        n = len(c) - 1
+        if n < baby:
+            acc = None
+            for i in range(1, n + 1):
+                if not np.any(c[i]):
+                    continue
+                term = mul(basis(i), c[i], (path, i))
+                acc = term if acc is None else cc.EvalAdd(acc, term)
+            if acc is None:
+                return const(c[0])
+            return add(acc, c[0]) if np.any(c[0]) else acc
+        k = _giant_split(n, baby)
+        rem, quot = _ps_split(c, n, k)
+        giant = cc.EvalMult(basis(k), evaluate(quot, path + "q"))
+        return cc.EvalAdd(evaluate(rem, path + "r"), giant)
+
+    return evaluate([np.asarray(r, dtype=np.float64) for r in rows], "")
 
 
 class CkksPrimitives:

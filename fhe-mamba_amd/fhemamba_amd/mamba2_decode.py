@@ -18,6 +18,10 @@ polynomial circuit), all ciphertexts of `slots` = N/2 slots:
     the payload's Chebyshev series;
   * gates: SiLU(z); dt = (Chebyshev sqrt-softplus)^2 on dt + dt_bias;
     decay = exp(dt A) by Chebyshev and squarings, times the head mask;
+    with a joint gate (JointGateSpec) instead: per-head affine map of
+    dt + dt_bias onto [-1, 1], the two per-head Chebyshev series p and q by
+    a vector-coefficient Paterson-Stockmeyer over one shared basis
+    (:3781-3830), write = p^2 q^2 in place of dt and decay = 1 - p^2;
   * SSM in the reference's packing (:23-27): state group g holds heads
     heads_per_ct g ... at slot n * group_block + h_local * head_dim + p;
     x, dt and decay are expanded to it (a rotation, a mask, a rotate-sum
@@ -43,8 +47,9 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
-from .ckks_probes import cheb_ps_depth, chebyshev_ps
-from .mamba2_payload import ChainPayload, LayerPayload, PolySpec
+from .ckks_probes import (ChebBasis, affine, cheb_baby_size, cheb_ps_depth, chebyshev_ps,
+                          chebyshev_ps_rows)
+from .mamba2_payload import ChainPayload, JointGateSpec, LayerPayload, PolySpec
 from .packed import PackedEvaluator, replicated_shape
 
 # Refresh bounds by checkpoint where a payload carries no calibration maxima
@@ -109,6 +114,11 @@ class EncryptedMamba2Decoder:
         b = dict(DEFAULT_BOUNDS)
         for k, v in lay.bounds.items():
             b[k] = max(BOUND_MARGIN * float(v), 1e-12)
+        if lay.joint is not None:
+            # a joint gate's write and decay take the refresh bounds its
+            # coefficients certify (the calibration "dt" is softplus's)
+            w, d = lay.joint.bounds()
+            b["dt"], b["decay"] = BOUND_MARGIN * w, BOUND_MARGIN * d
         b.update(override or {})
         return b
 
@@ -138,6 +148,41 @@ class EncryptedMamba2Decoder:
 
     def cheb_need(self, spec: PolySpec) -> int:
         return 1 + cheb_ps_depth(len(spec.coeffs) - 1) + 1
+
+    @staticmethod
+    def joint_need(spec: JointGateSpec) -> int:
+        """Levels from dt + dt_bias to write and decay: the affine map, the
+        deeper series, p^2 and q^2, their product (decay's negating mask is
+        no deeper)."""
+        m = cheb_baby_size(max(spec.degree, 1))
+        return 1 + max(cheb_ps_depth(len(c) - 1, m) for c in (spec.p, spec.q)) + 2
+
+    def joint_gates(self, li: int, dtin, spec: JointGateSpec, d0: int):
+        """(write, decay) of a joint gate for dt + dt_bias at slots
+        [d0, d0 + nh): u = a_h (dt + dt_bias) + b_h maps each head's domain
+        onto [-1, 1]; p and q share one Chebyshev basis of u."""
+        ev = self.ev
+        ab = [affine(lo, hi) for lo, hi in zip(spec.lo, spec.hi)]
+        u = ev.plain(dtin, self._vec({d0: [a for a, _ in ab]}), True, key=("joint_a", li))
+        u = ev.plain(u, self._vec({d0: [b for _, b in ab]}), False)
+        basis = ChebBasis(self.cc, u)
+        baby = cheb_baby_size(max(spec.degree, 1))
+
+        def series(coeffs, name):
+            rows = [self._vec({d0: r}) for r in coeffs]
+            return chebyshev_ps_rows(
+                basis, rows, baby,
+                lambda ct, row, key: ev.plain(ct, row, True, key=("joint", li, name) + key),
+                lambda ct, row: ev.plain(ct, row, False),
+                lambda row: ev.plain(ev.scale(u, 0.0), row, False))
+
+        p, q = series(spec.p, "p"), series(spec.q, "q")
+        d = ev.mul(p, p)
+        write = ev.mul(d, ev.mul(q, q))
+        decay = ev.plain(ev.plain(d, self._vec({d0: -np.ones(self.nh)}), True,
+                                  key=("joint_neg", d0)),
+                         self._vec({d0: np.ones(self.nh)}), False)
+        return write, decay
 
     def sched_inv_sqrt(self, v, spec, vbound: float, ibound: float):
         """Scheduled normalization (ScheduledInvSqrtSpec): u = v seed^2 in
@@ -250,7 +295,8 @@ class EncryptedMamba2Decoder:
                                 psup, B["inv"])
         # one refresh serves every consumer of proj (conv, gate, dt, FIFO)
         need = max(2, self.cheb_need(lay.polys["gate_silu"]),
-                   self.cheb_need(lay.polys["dt_softplus"]) + 2)
+                   self.cheb_need(lay.polys["dt_softplus"]) + 2 if lay.joint is None
+                   else self.joint_need(lay.joint))
         proj = self.ready(proj, need, B["proj"], psup)
         # conv over the FIFO of raw proj ciphertexts (taps on the xBC slots)
         window = list(st.fifo) + [proj]
@@ -272,27 +318,32 @@ class EncryptedMamba2Decoder:
         ds = self._support(d0, self.nh)
         sp = lay.polys["dt_softplus"]
         dtin = ev.plain(proj, self._vec({d0: t("dt_bias")}), False)
-        q = self.cheb(dtin, sp, ds)
-        dt = ev.plain(ev.mul(q, q), ds, True, key=("dt", d0))
         dec = lay.polys["decay_exp"]
+        if lay.joint is None:
+            q = self.cheb(dtin, sp, ds)
+            dt = ev.plain(ev.mul(q, q), ds, True, key=("dt", d0))
+            need_dt = self.cheb_need(dec) + dec.squarings + 6
+        else:
+            dt, decay = self.joint_gates(li, dtin, lay.joint, d0)
+            need_dt = 6
         A = -np.exp(t("a_log"))
         # act (xBC slots) and dt (dt slots) occupy disjoint slots of the proj
         # layout: when either needs a refresh both go through one bootstrap,
         # dt first scaled by a power of two (exact, no level) into act's
         # range; every consumer below masks, and dt's masks carry 1 / f
         need_act = 7
-        need_dt = self.cheb_need(dec) + dec.squarings + 6
         f = 1
         if max(ev._level(act) + need_act, ev._level(dt) + need_dt) > ev.refresh_ceiling:
             f = 1 << max(0, math.ceil(math.log2(B["act"] / B["dt"])))
             comb = ev.add(act, cc.MultByInteger(dt, f) if f > 1 else dt)
             comb = ev.refresh(comb, max(B["act"], B["dt"] * f), xs + ds)
             act = dt = comb
-        e = self.cheb(ev.plain(dt, self._vec({d0: A / f}), True), dec, ds, dec.squarings)
-        for _ in range(dec.squarings):
-            e = self.ev.mul(e, e)
-        hm = dec.head_mask if dec.head_mask is not None else np.ones(self.nh)
-        decay = ev.plain(e, self._vec({d0: hm}), True)
+        if lay.joint is None:
+            e = self.cheb(ev.plain(dt, self._vec({d0: A / f}), True), dec, ds, dec.squarings)
+            for _ in range(dec.squarings):
+                e = self.ev.mul(e, e)
+            hm = dec.head_mask if dec.head_mask is not None else np.ones(self.nh)
+            decay = ev.plain(e, self._vec({d0: hm}), True)
         # expansions into the state packing
         # compact values refreshed with room for the expansions and the
         # state update, so the expanded ciphertexts need no refresh
@@ -464,6 +515,7 @@ def run_payload(payload_dir: str, *, tokens: int = 0, bootstrap_passes: int = 2,
         "schema": "fhemamba-m2-decode-result-v1",
         "encrypted": True,
         "layers": chain.n_layers,
+        "joint_gate_layers": sum(lay.joint is not None for lay in chain.layers),
         "tokens": n_tok,
         "ring_dimension": cc.GetRingDimension(),
         "slots": slots,

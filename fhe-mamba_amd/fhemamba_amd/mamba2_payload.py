@@ -20,7 +20,9 @@ mask), "poly-newton" (y = 0.9 p(v), Newton steps y <- y (1.5 - v y^2 / 2)),
 "sq-poly-newton" (y = damping q(v)^2, Newton steps), and the scheduled
 normalization recipe "scaled-goldschmidt-invsqrt-v1" for the block, gated
 and final norms (chain.json final_norm_poly).  Joint-gate payloads
-("fhemamba-m1-joint-v1", "fhemamba-m2-chain-joint-v1") are refused.
+(layer format "fhemamba-m1-joint-v1", chain format
+"fhemamba-m2-chain-joint-v1") carry a "shared-dissipation-factor-v1" gate
+that replaces dt_softplus and decay_exp on every head (JointGateSpec).
 
 Decode semantics per layer (src/fhemamba/reference.py:182-339, ngroups 1,
 no MLP split): hidden -> RMSNorm (rms_invsqrt) -> in_proj -> z | xBC | dt;
@@ -165,6 +167,91 @@ class ScheduledInvSqrtSpec:
         return cls(lo, hi, seed, coeffs, tol)
 
 
+@dataclass
+class JointGateSpec:
+    """Joint selective gate ("shared-dissipation-factor-v1"): per head h a
+    public domain [lo_h, hi_h] and two Chebyshev series p_h, q_h whose
+    coefficient matrices are stored degree-major, head-minor.  For
+    z = dt + dt_bias,
+      t = (2 z - (lo + hi)) / (hi - lo),  p = sum_i p[i, h] T_i(t),
+      q likewise,  write = p^2 q^2,  decay = 1 - p^2;
+    write takes the place of dt in the state update (h = decay h +
+    (write x) B).  Semantics of src/fhemamba/selective_gates.py:113-135 and
+    ops.py:553-571; payload checks of
+    native/fideslib_stage0/include/stage1_joint_gates.hpp:51-66 and
+    src/stage1_mamba2_payload.cpp:208-230.  Evaluated in float64."""
+    lo: np.ndarray
+    hi: np.ndarray
+    p: np.ndarray            # [degree_p + 1][heads]
+    q: np.ndarray            # [degree_q + 1][heads]
+    rates: np.ndarray
+    kind: str = "shared-dissipation-factor-v1"
+
+    @property
+    def heads(self) -> int:
+        return len(self.lo)
+
+    @property
+    def degree(self) -> int:
+        """The larger of the two series' degrees (the shared basis size)."""
+        return max(len(self.p), len(self.q)) - 1
+
+    def roots(self, z):
+        """(p, q) for z of shape [..., heads]."""
+        z = np.asarray(z, dtype=np.float64)
+        t = (2.0 * z - (self.lo + self.hi)) / (self.hi - self.lo)
+        cv = np.polynomial.chebyshev.chebval
+        p = np.stack([cv(t[..., h], self.p[:, h]) for h in range(self.heads)], axis=-1)
+        q = np.stack([cv(t[..., h], self.q[:, h]) for h in range(self.heads)], axis=-1)
+        return p, q
+
+    def __call__(self, z):
+        """(write, decay) for z = dt + dt_bias."""
+        p, q = self.roots(z)
+        d = p * p
+        return d * (q * q), 1.0 - d
+
+    def bounds(self) -> tuple:
+        """Certified maxima of |write| and |decay| for z inside every head's
+        domain (|T_i| <= 1 on [-1, 1])."""
+        pm = np.abs(self.p).sum(axis=0)
+        qm = np.abs(self.q).sum(axis=0)
+        return float(np.max(pm * pm * qm * qm)), float(max(1.0, np.max(pm * pm - 1.0)))
+
+    def to_json(self) -> dict:
+        return {"kind": self.kind, "lo": list(self.lo), "hi": list(self.hi),
+                "p": list(self.p.reshape(-1)), "q": list(self.q.reshape(-1)),
+                "rates": list(self.rates), "coefficient_layout": "degree-major-head-minor",
+                "all_heads_retained": True}
+
+    @classmethod
+    def from_json(cls, d: dict, heads: int) -> "JointGateSpec":
+        if d.get("kind") != "shared-dissipation-factor-v1" or \
+                d.get("coefficient_layout") != "degree-major-head-minor":
+            raise ValueError("unsupported joint gate recipe")
+        arrays = {}
+        for name in ("lo", "hi", "p", "q", "rates"):
+            v = d.get(name)
+            if not isinstance(v, list) or not v or \
+                    not all(isinstance(x, (int, float)) and not isinstance(x, bool) for x in v):
+                raise ValueError("invalid joint gate numeric array")
+            arrays[name] = np.asarray(v, dtype=np.float64)
+            if not np.all(np.isfinite(arrays[name])):
+                raise ValueError("joint gate contains non-finite values")
+        lo, hi, rates = arrays["lo"], arrays["hi"], arrays["rates"]
+        if heads < 1 or len(lo) != heads or len(hi) != heads or len(rates) != heads:
+            raise ValueError("joint gate requires one domain/rate per head")
+        if np.any(lo >= hi) or np.any(rates <= 0):
+            raise ValueError("invalid joint gate domain/rate")
+        mats = []
+        for name in ("p", "q"):
+            c = arrays[name]
+            if len(c) % heads or len(c) // heads > 4097:
+                raise ValueError("invalid joint gate coefficient matrix shape")
+            mats.append(c.reshape(-1, heads))
+        return cls(lo, hi, mats[0], mats[1], rates)
+
+
 def read_poly(d: dict):
     """A site's polynomial spec: a Chebyshev-based PolySpec or a scheduled
     inverse square root."""
@@ -208,6 +295,7 @@ class LayerPayload:
     polys: dict
     tensors: dict
     bounds: dict = field(default_factory=dict)   # calibration |value| maxima by checkpoint
+    joint: JointGateSpec | None = None           # joint gate (replaces dt_softplus, decay_exp)
 
     @property
     def proj_dim(self) -> int:
@@ -248,10 +336,11 @@ def read_layer_payload(directory: str) -> LayerPayload:
     with open(os.path.join(directory, "meta.json")) as f:
         meta = json.load(f)
     fmt = meta.get("format")
-    if fmt == "fhemamba-m1-joint-v1":
-        raise ValueError("joint-gate payloads are not supported by this decoder")
-    if fmt != "fhemamba-m1-v1":
+    joint = fmt == "fhemamba-m1-joint-v1"
+    if fmt != "fhemamba-m1-v1" and not joint:
         raise ValueError("unexpected payload format (want fhemamba-m1-v1)")
+    if not joint and "joint_gates" in meta:
+        raise ValueError("joint gate payload requires the versioned joint format")
     d, eps = meta["dims"], meta["eps"]
     polys = {}
     for name in SITES:
@@ -279,6 +368,13 @@ def read_layer_payload(directory: str) -> LayerPayload:
     if mask is not None and (len(mask) != layer.num_heads or
                              not np.all((mask == 0) | (mask == 1))):
         raise ValueError("decay_exp head_mask must hold one 0/1 value per head")
+    if joint:
+        layer.joint = JointGateSpec.from_json(meta.get("joint_gates") or {}, layer.num_heads)
+        if mask is not None and np.any(mask != 1):
+            raise ValueError("joint gates retain all heads")
+        # the gate's rates are the layer's -A (ops.py:557-560)
+        if not np.allclose(np.exp(layer.t("a_log")), layer.joint.rates, rtol=2e-7, atol=0):
+            raise ValueError("joint gate rates differ from the layer's A")
     if layer.t("in_proj_w").shape != (layer.proj_dim, layer.d_model):
         raise ValueError("in_proj_w shape does not match the dims")
     return layer
@@ -287,7 +383,7 @@ def read_layer_payload(directory: str) -> LayerPayload:
 def read_chain_payload(directory: str) -> ChainPayload:
     with open(os.path.join(directory, "chain.json")) as f:
         meta = json.load(f)
-    if meta.get("format") not in ("fhemamba-m2-chain-v1",):
+    if meta.get("format") not in ("fhemamba-m2-chain-v1", "fhemamba-m2-chain-joint-v1"):
         raise ValueError("unexpected chain payload format (want fhemamba-m2-chain-v1)")
     n_layers = int(meta["n_layers"])
     dirs = meta["layer_dirs"]
@@ -347,14 +443,17 @@ def layer_step(lay: LayerPayload, hidden: np.ndarray, state: LayerState, polynom
     act = P["conv_silu"](conv) if polynomial else silu(conv)
     x, B, C = act[:di], act[di:di + ns], act[di + ns:]
     t = dt_raw + lay.t("dt_bias")
-    dt = P["dt_softplus"](t) if polynomial else softplus(t)
     A = -np.exp(lay.t("a_log"))
-    if polynomial:
+    if polynomial and lay.joint is not None:
+        dt, decay = lay.joint(t)
+    elif polynomial:
+        dt = P["dt_softplus"](t)
         decay = P["decay_exp"](dt * A)
         mask = P["decay_exp"].head_mask
         if mask is not None:
             decay = decay * mask
     else:
+        dt = softplus(t)
         decay = np.exp(dt * A)
     xh = x.reshape(nh, hd)
     h = decay[:, None, None] * state.ssm + (dt[:, None] * xh)[:, :, None] * B[None, None, :]
@@ -403,12 +502,19 @@ def _write_bin(directory, name, arr, manifest):
 def synthetic_chain(directory: str, *, seed: int = 0, n_layers: int = 24, n_test_tokens: int = 2,
                     d_model: int = 768, d_inner: int = 1536, num_heads: int = 24,
                     head_dim: int = 64, state_size: int = 128, conv_kernel: int = 4,
-                    degrees=None, calibration_tokens: int = 8) -> ChainPayload:
+                    degrees=None, calibration_tokens: int = 8,
+                    joint_degrees: tuple | None = None) -> ChainPayload:
     """Write a chain payload for a random-init Mamba-2 model of the given
     shape (weights N(0, 0.02), A = -exp(U[0, ln 16]), dt_bias so that dt
     starts in [0.001, 0.1], D = 1, norm weights 1): polynomial intervals come
     from an exact plain decode of `calibration_tokens` random embeddings,
-    widened by 30%, and the test vectors from a separate draw."""
+    widened by 30%, and the test vectors from a separate draw.
+
+    joint_degrees = (degree_p, degree_q) writes joint-gate payloads instead
+    (_fit_joint_gate): per head, on that head's widened range of
+    dt + dt_bias, p fits sqrt(1 - exp(dt A)) and q fits
+    sqrt(dt / (1 - exp(dt A))), so that write = p^2 q^2 ~ dt and
+    decay = 1 - p^2 ~ exp(dt A)."""
     degrees = dict(DEGREES, **(degrees or {}))
     rng = np.random.default_rng(seed)
     os.makedirs(directory, exist_ok=True)
@@ -444,6 +550,8 @@ def synthetic_chain(directory: str, *, seed: int = 0, n_layers: int = 24, n_test
     for i, lay in enumerate(layers):
         lay.polys = _fit_layer_polys(ranges[i], lay, degrees)
         lay.bounds = peaks[i]
+        if joint_degrees is not None:
+            lay.joint = _fit_joint_gate(lay, ranges[i]["t_heads"], *joint_degrees)
     chain = ChainPayload(n_layers, n_test_tokens, 1e-5, np.ones(d_model),
                          rng.normal(0, 1, (n_test_tokens, d_model)).astype(np.float32)
                          .astype(np.float64), None, None, layers)
@@ -497,6 +605,8 @@ def _calibrated_step(lay, hidden, state, rng_, peak):
     x, B, C = act[:di], act[di:di + ns], act[di + ns:]
     t = dt_raw + lay.t("dt_bias")
     rec("dt_softplus", t)
+    th = rng_.setdefault("t_heads", [np.full(len(t), np.inf), np.full(len(t), -np.inf)])
+    th[0], th[1] = np.minimum(th[0], t), np.maximum(th[1], t)
     dt = softplus(t)
     top("dt", dt)
     A = -np.exp(lay.t("a_log"))
@@ -556,6 +666,22 @@ def _fit_layer_polys(r, lay, degrees) -> dict:
     return polys
 
 
+def _fit_joint_gate(lay, t_range, degree_p: int, degree_q: int) -> JointGateSpec:
+    lo_t, hi_t = t_range
+    pad = 0.3 * np.maximum(hi_t - lo_t, 1e-3)
+    lo, hi = lo_t - pad, hi_t + pad
+    rates = np.exp(lay.t("a_log"))
+    p = np.zeros((degree_p + 1, lay.num_heads))
+    q = np.zeros((degree_q + 1, lay.num_heads))
+    for h in range(lay.num_heads):
+        def keep(z, h=h):
+            return -np.expm1(-softplus(z) * rates[h])      # 1 - exp(dt A) > 0
+        p[:, h] = fit_chebyshev(lambda z: np.sqrt(keep(z)), lo[h], hi[h], degree_p)
+        q[:, h] = fit_chebyshev(lambda z: np.sqrt(softplus(z) / keep(z)), lo[h], hi[h],
+                                degree_q)
+    return JointGateSpec(lo, hi, p, q, rates)
+
+
 def write_chain_payload(directory: str, chain: ChainPayload) -> None:
     os.makedirs(directory, exist_ok=True)
     dirs = []
@@ -566,7 +692,8 @@ def write_chain_payload(directory: str, chain: ChainPayload) -> None:
         manifest: dict = {}
         for t in LAYER_TENSORS:
             _write_bin(ld, t, lay.tensors[t], manifest)
-        meta = {"format": "fhemamba-m1-v1", "layer_index": i,
+        meta = {"format": "fhemamba-m1-v1" if lay.joint is None else "fhemamba-m1-joint-v1",
+                "layer_index": i,
                 "dims": {"d_model": lay.d_model, "d_inner": lay.d_inner,
                          "num_heads": lay.num_heads, "head_dim": lay.head_dim,
                          "state_size": lay.state_size, "n_groups": lay.n_groups,
@@ -577,6 +704,8 @@ def write_chain_payload(directory: str, chain: ChainPayload) -> None:
                 "carried_bounds": {"source": "calibration_text",
                                    "checkpoint_abs_max": lay.bounds},
                 "tensors": manifest}
+        if lay.joint is not None:
+            meta["joint_gates"] = lay.joint.to_json()
         with open(os.path.join(ld, "meta.json"), "w") as f:
             json.dump(meta, f)
         dirs.append(name)
@@ -587,7 +716,9 @@ def write_chain_payload(directory: str, chain: ChainPayload) -> None:
     if chain.expected_poly_final is not None:
         _write_bin(directory, "chain_expected_poly_final", chain.expected_poly_final, manifest)
     with open(os.path.join(directory, "chain.json"), "w") as f:
-        json.dump({"format": "fhemamba-m2-chain-v1", "n_layers": chain.n_layers,
+        joint = any(lay.joint is not None for lay in chain.layers)
+        json.dump({"format": "fhemamba-m2-chain-joint-v1" if joint else "fhemamba-m2-chain-v1",
+                   "n_layers": chain.n_layers,
                    "n_test_tokens": chain.n_test_tokens,
                    "final_norm_eps": chain.final_norm_eps, "layer_dirs": dirs,
                    "tensors": manifest}, f)

@@ -14,11 +14,19 @@ test tokens:
                         final norm), 16 calibration tokens;
   m2_chain_tiny_joint/  the same plus shared-factor joint gates from the
                         gate bundle of tests/test_scheduled_payload.py:42-67
-                        (fhemamba-m1-joint-v1 / fhemamba-m2-chain-joint-v1).
+                        (fhemamba-m1-joint-v1 / fhemamba-m2-chain-joint-v1);
+                        that bundle's gates are constants (degree 0);
+  m2_chain_tiny_joint_cheb/  joint gates of degree 7 (p) and 5 (q) per head:
+                        on each head's public domain (the exporter's own
+                        public_gate_domains), p interpolates
+                        sqrt(1 - exp(-softplus(z) rate)) (scaled so that
+                        sum |p_k| <= 0.999, which the exporter's gate
+                        certificate requires) and q interpolates
+                        sqrt(softplus(z) / (1 - exp(-softplus(z) rate))).
 Only the payloads it writes (float32 tensors and JSON) are kept: nothing of
 the reference is copied, and nothing here runs at test time.
 
-    python tests/golden/make_m2_chain_fixture.py [REFERENCE_ROOT]
+    python tests/golden/make_m2_chain_fixture.py [REFERENCE_ROOT [NAME ...]]
 """
 import os
 import shutil
@@ -86,21 +94,58 @@ def gate_bundle(path, model):
     np.savez(path, **arrays)
 
 
-def main(reference_root="/root/reference"):
+def cheb_gate_bundle(path, model, degree_p=7, degree_q=5):
+    """Per-head Chebyshev joint gates (p: degree_p, q: degree_q) on the
+    exporter's public domains."""
+    import json
+    import numpy as np
+    from fhemamba.payload_surrogate import public_gate_domains
+    arrays = {}
+    for layer, block in enumerate(model.backbone.layers):
+        lo, hi = public_gate_domains(block)
+        rates = block.mixer.A_log.detach().exp().double().numpy()
+        p = np.zeros((degree_p + 1, len(lo)))
+        q = np.zeros((degree_q + 1, len(lo)))
+        for h in range(len(lo)):
+            def dt(t, h=h):
+                return np.logaddexp(0.0, lo[h] + (t + 1.0) * 0.5 * (hi[h] - lo[h]))
+
+            def keep(t, h=h):
+                return -np.expm1(-dt(t) * rates[h])
+            ph = np.polynomial.chebyshev.chebinterpolate(lambda t: np.sqrt(keep(t)), degree_p)
+            ph *= min(1.0, 0.999 / np.abs(ph).sum())
+            p[:, h] = ph
+            q[:, h] = np.polynomial.chebyshev.chebinterpolate(
+                lambda t: np.sqrt(dt(t) / keep(t)), degree_q)
+        for name, value in {"lo": lo, "hi": hi, "p": p, "q": q, "rates": rates}.items():
+            arrays[f"layer_{layer}_{name}"] = value
+    arrays["manifest"] = np.array(json.dumps({"format": "dissipative-mamba2-gates-v1",
+                                              "layers": [0, 1],
+                                              "input_payload_sha256": "0" * 64}))
+    np.savez(path, **arrays)
+
+
+def main(reference_root="/root/reference", *names):
     sys.path.insert(0, os.path.join(reference_root, "src"))
     from fhemamba.m1_payload import export_chain_payload
     model = tiny_mamba2()
     with tempfile.TemporaryDirectory() as tmp:
         norms, gates = os.path.join(tmp, "norms.json"), os.path.join(tmp, "gates.npz")
+        cheb_gates = os.path.join(tmp, "cheb_gates.npz")
         normalization_bundle(norms)
         gate_bundle(gates, model)
+        cheb_gate_bundle(cheb_gates, model)
         runs = {
             "m2_chain_tiny": dict(),
             "m2_chain_tiny_sched": dict(cal_tokens=16, normalization_bundle=norms),
             "m2_chain_tiny_joint": dict(cal_tokens=16, normalization_bundle=norms,
                                         stabilized_gate_bundle=gates),
+            "m2_chain_tiny_joint_cheb": dict(cal_tokens=16, normalization_bundle=norms,
+                                             stabilized_gate_bundle=cheb_gates),
         }
         for name, kw in runs.items():
+            if names and name not in names:
+                continue
             out = export_chain_payload(model, Tokenizer(), os.path.join(tmp, name),
                                        n_test_tokens=2, **kw)
             dest = os.path.join(HERE, name)

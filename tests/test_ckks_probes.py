@@ -212,3 +212,35 @@ def test_select_chain_rejects_unimplemented():
         ckks.select_chain(_params(RingDim=1024, SecurityLevel=ckks.SecurityLevel.HEStd_NotSet))
     with pytest.raises(ValueError):
         ckks.select_chain(_params(SecurityLevel=ckks.SecurityLevel.HEStd_NotSet))
+
+
+@pytest.mark.parametrize("degrees", [(0, 0), (1, 3), (7, 5), (15, 7), (31, 2), (59, 59)])
+def test_vector_coefficient_series(degrees):
+    """chebyshev_ps_rows (one coefficient per slot) over one shared basis:
+    each slot's value equals numpy's Chebyshev series of that slot's
+    coefficient column, and the depth ledger equals cheb_ps_depth with the
+    shared baby-step size (zero rows are skipped, and a series with no
+    term is the constant ciphertext)."""
+    from fhemamba_amd.ckks_probes import ChebBasis, chebyshev_ps_rows
+    rng = np.random.default_rng(sum(degrees))
+    slots = 12
+    x = np.linspace(-0.97, 0.97, slots)
+    baby = cheb_baby_size(max(max(degrees), 1))
+    be = ArrayBackend()
+    basis = ChebBasis(be, x)
+    for deg in degrees:
+        rows = rng.normal(size=(deg + 1, slots))
+        rows[:, 3] = 0.0                         # an inactive slot
+        if deg >= 2:
+            rows[1] = 0.0                        # a zero row is skipped
+        got = chebyshev_ps_rows(basis, rows, baby, lambda c, r, k: c * r,
+                                lambda c, r: c + r, lambda r: r.copy())
+        want = [np.polynomial.chebyshev.chebval(x[s], rows[:, s]) for s in range(slots)]
+        np.testing.assert_allclose(got, want, rtol=1e-10, atol=1e-10)
+        assert got[3] == 0.0
+    db = DepthBackend()
+    dbasis = ChebBasis(db, 0)
+    for deg in degrees:
+        depth = chebyshev_ps_rows(dbasis, np.ones((deg + 1, 2)), baby,
+                                  lambda c, r, k: c + 1, lambda c, r: c, lambda r: 0)
+        assert depth == cheb_ps_depth(deg, baby)

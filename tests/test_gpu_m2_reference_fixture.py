@@ -37,3 +37,15 @@ def test_reference_scheduled_normalization_payload_decodes():
           f"bootstraps, errors vs polynomial {report['per_token_errors_vs_polynomial']}",
           flush=True)
     assert report["max_abs_error_vs_polynomial"] < TOL
+
+
+@pytest.mark.parametrize("name", ["m2_chain_tiny_joint", "m2_chain_tiny_joint_cheb"])
+def test_reference_joint_gate_payload_decodes(name):
+    """The exporter's joint-gate payloads (constant gates of the reference
+    tests' bundle; per-head degree-7 / degree-5 Chebyshev gates) decoded on
+    the GPU, two tokens with carried state, against chain_expected_poly_final."""
+    path = os.path.join(os.path.dirname(__file__), "golden", name)
+    report = D.run_payload(path, seed=33, log=lambda m: None)
+    print(f"{name}: {report['seconds_per_token']} s/token, {report['bootstraps']} bootstraps, "
+          f"errors vs polynomial {report['per_token_errors_vs_polynomial']}", flush=True)
+    assert report["max_abs_error_vs_polynomial"] < TOL

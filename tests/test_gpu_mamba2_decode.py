@@ -36,6 +36,18 @@ def test_command_line(tmp_path):
     assert D.main([str(tmp_path / "missing"), str(res)]) == 2
 
 
+def test_joint_gate_decode_at_130m_shape(tmp_path):
+    """One layer of the 130M shape with joint gates (per-head degree-15 p
+    and degree-7 q over a shared basis, write = p^2 q^2, decay = 1 - p^2),
+    two tokens with carried state, within the decode tolerance."""
+    M.synthetic_chain(str(tmp_path), n_layers=1, n_test_tokens=2, seed=8,
+                      joint_degrees=(15, 7))
+    report = D.run_payload(str(tmp_path), seed=9)
+    print(f"joint decode: {report['seconds_per_token']} s/token, errors "
+          f"{report['per_token_errors_vs_polynomial']}", flush=True)
+    assert report["max_abs_error_vs_polynomial"] < TOL
+
+
 def test_classical128_two_layer_decode(tmp_path):
     """Two layers of the 130M-shape payload at the audited classical-128
     setting (N=2^17, 65536 slots, 45 Q + 12 P primes, four digits, uniform

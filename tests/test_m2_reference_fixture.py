@@ -147,13 +147,144 @@ def test_scheduled_decoder_circuit_on_slots():
         assert _rel(dec.decrypt(ct), ch.expected_poly_final[k]) < 1e-5, k
 
 
-def test_joint_gate_payload_is_refused():
-    """The exporter's joint-gate payload (fhemamba-m2-chain-joint-v1 with
+JOINT_CHEB = os.path.join(os.path.dirname(__file__), "golden", "m2_chain_tiny_joint_cheb")
+
+
+def _layer_ref_in(directory, i, name):
+    d = os.path.join(directory, f"layer_{i:02d}")
+    meta = json.load(open(os.path.join(d, "meta.json")))
+    return np.fromfile(os.path.join(d, name + ".bin"), dtype="<f4").reshape(
+        meta["tensors"][name]).astype(np.float64)
+
+
+@pytest.mark.parametrize("directory", [JOINT, JOINT_CHEB], ids=["constant", "chebyshev"])
+def test_joint_gate_payload_decodes_like_exporter(directory):
+    """The exporter's joint-gate payloads (fhemamba-m2-chain-joint-v1 with
     fhemamba-m1-joint-v1 layers: shared-dissipation-factor gates in place of
-    dt_softplus and decay_exp) is refused by format, not misread."""
-    meta = json.load(open(os.path.join(JOINT, "chain.json")))
+    dt_softplus and decay_exp): the gates read degree-major, head-minor, and
+    the polynomial decode reproduces every layer's output and state and the
+    final hidden of the exporter's own circuit; the exact decode its
+    exact-model references."""
+    meta = json.load(open(os.path.join(directory, "chain.json")))
     assert meta["format"] == "fhemamba-m2-chain-joint-v1"
+    ch = M.read_chain_payload(directory)
+    for lay in ch.layers:
+        assert lay.joint is not None and lay.joint.heads == lay.num_heads
+        assert np.allclose(lay.joint.rates, np.exp(lay.t("a_log")), rtol=2e-7)
+    finals, outs, sts = _run(ch, polynomial=True)
+    assert _rel(finals, ch.expected_poly_final) < 1e-5
+    for i in range(ch.n_layers):
+        assert _rel(outs[i], _layer_ref_in(directory, i, "test_layer_output_poly")) < 1e-5
+        assert _rel(sts[i], _layer_ref_in(directory, i, "test_state_output_poly")) < 1e-4
+    exact, _, _ = _run(ch, polynomial=False)
+    assert _rel(exact, ch.expected_final) < 1e-5
+
+
+def test_constant_joint_gate_values():
+    """The reference tests' constant gate bundle (p = 0.5, q = 0.75 on every
+    head) gives write 0.140625 and decay 0.75 for any input, the values the
+    reference's own test asserts (tests/test_scheduled_payload.py:95-102)."""
+    gate = M.read_chain_payload(JOINT).layers[0].joint
+    write, decay = gate(np.array([[0.0] * 4, [-3.0, 1.0, 7.5, -20.0]]))
+    assert np.array_equal(write, np.full((2, 4), 0.140625))
+    assert np.array_equal(decay, np.full((2, 4), 0.75))
+
+
+def test_chebyshev_joint_gate_against_power_series():
+    """The degree-7 / degree-5 gates evaluated through the power basis
+    (numpy's cheb2poly, then Horner) at points inside and outside each
+    head's domain: the Chebyshev evaluation and the head-minor layout agree;
+    decay = 1 - p^2 stays in [0, 1] on the domain (|p| <= sum |p_k| <= 1)."""
+    gate = M.read_chain_payload(JOINT_CHEB).layers[1].joint
+    rng = np.random.default_rng(5)
+    z = gate.lo + (gate.hi - gate.lo) * rng.uniform(-0.2, 1.2, (64, gate.heads))
+    write, decay = gate(z)
+    t = (2 * z - (gate.lo + gate.hi)) / (gate.hi - gate.lo)
+    for h in range(gate.heads):
+        p = np.polyval(np.polynomial.chebyshev.cheb2poly(gate.p[:, h])[::-1], t[:, h])
+        q = np.polyval(np.polynomial.chebyshev.cheb2poly(gate.q[:, h])[::-1], t[:, h])
+        np.testing.assert_allclose(write[:, h], p * p * q * q, rtol=1e-9, atol=1e-12)
+        np.testing.assert_allclose(decay[:, h], 1 - p * p, rtol=1e-9, atol=1e-12)
+    inside = (t >= -1) & (t <= 1)
+    assert np.all((decay[inside] >= 0) & (decay[inside] <= 1))
+    assert np.all(np.abs(gate.p).sum(axis=0) <= 1)
+
+
+@pytest.mark.parametrize("directory", [JOINT, JOINT_CHEB], ids=["constant", "chebyshev"])
+def test_joint_decoder_circuit_on_slots(directory):
+    """The encrypted decoder's joint-gate circuit (per-head affine map, the
+    vector-coefficient Paterson-Stockmeyer p and q over one basis, write and
+    decay) on the slot-level stand-in, two tokens with carried state,
+    against chain_expected_poly_final."""
+    from fhemamba_amd.mamba2_decode import EncryptedMamba2Decoder
+    from packed_builder import SlotContext, SlotKeys
+    ch = M.read_chain_payload(directory)
+    dec = EncryptedMamba2Decoder(SlotContext(1024), SlotKeys(), ch)
+    states = dec.initial_states()
+    for k, e in enumerate(ch.input_embeddings):
+        ct, states = dec.step(e, states)
+        assert _rel(dec.decrypt(ct), ch.expected_poly_final[k]) < 1e-5, k
+
+
+def _copy_with(tmp_path, edit_layer=None, edit_chain=None):
+    import shutil
+    dst = tmp_path / "p"
+    shutil.copytree(JOINT_CHEB, dst)
+    if edit_layer:
+        path = dst / "layer_00" / "meta.json"
+        meta = json.loads(path.read_text())
+        edit_layer(meta)
+        path.write_text(json.dumps(meta))
+    if edit_chain:
+        path = dst / "chain.json"
+        meta = json.loads(path.read_text())
+        edit_chain(meta)
+        path.write_text(json.dumps(meta))
+    return str(dst)
+
+
+def _set(d, key, value):
+    d[key] = value
+
+
+@pytest.mark.parametrize("edit, match", [
+    (lambda m: _set(m["joint_gates"], "kind", "other"), "recipe"),
+    (lambda m: _set(m["joint_gates"], "coefficient_layout", "head-major"), "recipe"),
+    (lambda m: _set(m["joint_gates"], "p", m["joint_gates"]["p"][:-1]), "matrix shape"),
+    (lambda m: _set(m["joint_gates"], "lo", m["joint_gates"]["hi"]), "domain"),
+    (lambda m: _set(m["joint_gates"], "rates", [2 * r for r in m["joint_gates"]["rates"]]),
+     "rates"),
+    (lambda m: _set(m["joint_gates"], "rates", m["joint_gates"]["rates"][:2]), "per head"),
+    (lambda m: _set(m["joint_gates"], "q", ["x"] + m["joint_gates"]["q"][1:]), "numeric"),
+    (lambda m: _set(m["polys"]["decay_exp"], "head_mask", [1, 0, 1, 1]), "retain all heads"),
+    (lambda m: _set(m, "format", "fhemamba-m1-v1"), "versioned joint format"),
+    (lambda m: m.pop("joint_gates"), "recipe"),
+])
+def test_joint_gate_payload_checks(tmp_path, edit, match):
+    """Malformed joint payloads are refused with the reference reader's
+    reasons (stage1_joint_gates.hpp:51-66, stage1_mamba2_payload.cpp:208-230,
+    :293-317; rates against the layer's A as ops.py:557-560)."""
+    with pytest.raises(ValueError, match=match):
+        M.read_chain_payload(_copy_with(tmp_path, edit_layer=edit))
+
+
+def test_unknown_chain_format_is_refused(tmp_path):
     with pytest.raises(ValueError, match="format"):
-        M.read_chain_payload(JOINT)
-    with pytest.raises(ValueError, match="joint"):
-        M.read_layer_payload(os.path.join(JOINT, "layer_00"))
+        M.read_chain_payload(_copy_with(tmp_path, edit_chain=lambda m: _set(
+            m, "format", "fhemamba-m3-chain-v1")))
+
+
+def test_synthetic_joint_chain_round_trip(tmp_path):
+    """The synthetic writer's joint payloads (per-head fits of the exact
+    gates) read back to the same gates and format, and their polynomial
+    decode stays near the exact model's."""
+    ch = M.synthetic_chain(str(tmp_path), n_layers=2, n_test_tokens=2, seed=3, d_model=64,
+                           d_inner=128, num_heads=8, head_dim=16, state_size=16,
+                           joint_degrees=(15, 7))
+    meta = json.load(open(tmp_path / "chain.json"))
+    assert meta["format"] == "fhemamba-m2-chain-joint-v1"
+    g = ch.layers[1].joint
+    assert g.p.shape == (16, 8) and g.q.shape == (8, 8)
+    again = M.read_chain_payload(str(tmp_path)).layers[1].joint
+    assert np.array_equal(again.p, g.p) and np.array_equal(again.lo, g.lo)
+    assert _rel(ch.expected_poly_final, ch.expected_final) < 1e-3
