@@ -446,13 +446,46 @@ def expected_rotation_count(lay: LayerPayload, slots: int) -> dict:
     return {"in_proj_masks": s_in.per_replica, "out_proj_masks": s_out.per_replica}
 
 
+def token_loop(dec: EncryptedMamba2Decoder, chain: ChainPayload, n_tok: int, ar=None,
+               sync=lambda: None, log=print) -> dict:
+    """Decode n_tok tokens with carried state: the payload's test embeddings,
+    or with `ar` (AutoregressiveAssets) the client-in-loop greedy protocol;
+    per token the seconds, the errors of the decrypted final hidden against
+    the polynomial and exact references, and the client's selections."""
+    states = dec.initial_states()
+    out = dict(seconds=[], errors_poly=[], errors_exact=[], selected=[], client_seconds=0.0)
+    selected = out["selected"]
+    want_poly = ar.expected_poly_final if ar else chain.expected_poly_final
+    want_exact = ar.expected_exact_final if ar else chain.expected_final
+    for k in range(n_tok):
+        sync()
+        t = time.perf_counter()
+        ct, states = dec.step(ar.input_for(k, selected) if ar else chain.input_embeddings[k],
+                              states)
+        sync()
+        out["seconds"].append(time.perf_counter() - t)
+        t = time.perf_counter()
+        got = dec.decrypt(ct)
+        if ar is not None and k >= ar.prompt_tokens - 1:
+            selected.append(ar.select(got))
+            out["client_seconds"] += time.perf_counter() - t
+        if want_poly is not None:
+            out["errors_poly"].append(float(np.max(np.abs(got - want_poly[k]))))
+        out["errors_exact"].append(float(np.max(np.abs(got - want_exact[k]))))
+        ep = out["errors_poly"][-1] if out["errors_poly"] else float("nan")
+        log(f"token {k}: {out['seconds'][-1]:.2f}s error vs polynomial {ep:.2e} vs exact "
+            f"{out['errors_exact'][-1]:.2e}"
+            + (f" selected {selected[-1]}" if ar is not None and selected else ""))
+    return out
+
+
 # ----------------------------------------------------------------- command line
 SECRET_KEY_DISTS = {"sparse-ternary": "SPARSE_TERNARY", "uniform-ternary": "UNIFORM_TERNARY"}
 
 
 def run_payload(payload_dir: str, *, tokens: int = 0, bootstrap_passes: int = 2, seed=None,
                 secret_key_dist: str | None = None, security: str = "not-set",
-                layers: int = 0, log=print) -> dict:
+                layers: int = 0, autoregressive: bool = False, log=print) -> dict:
     """Decode the payload's test embeddings in turn (carried state) and
     compare the decrypted outputs with its polynomial-circuit and exact
     references; returns the report.
@@ -467,7 +500,15 @@ def run_payload(payload_dir: str, *, tokens: int = 0, bootstrap_passes: int = 2,
     decoder's stage1_mamba2_decode_fideslib.cpp:1005), depth 44, four HYBRID
     digits (45 Q + 12 P primes, QP = 3376 bits against the 3523-bit bound),
     a uniform ternary secret by default, and the audit must pass.  `layers`
-    > 0 decodes only the first layers (and the final norm)."""
+    > 0 decodes only the first layers (and the final norm).
+
+    autoregressive: the client-in-loop greedy protocol over the payload's
+    autoregressive assets (AutoregressiveAssets; the reference decoder's
+    --autoregressive-client-loop): the prompt embeddings, then after each
+    evaluation from the last prompt token on the client decrypts, selects
+    the greedy token from its logits and encrypts that token's embedding
+    next; errors are taken against the assets' polynomial and exact final
+    hiddens, and the selected ids against the exporter's greedy ids."""
     from . import ckks
     from .mamba2_payload import read_chain_payload
     from .packed import CLASSICAL128, build_context
@@ -479,6 +520,15 @@ def run_payload(payload_dir: str, *, tokens: int = 0, bootstrap_passes: int = 2,
     if secret_key_dist not in SECRET_KEY_DISTS:
         raise ValueError(f"secret key distribution must be one of {sorted(SECRET_KEY_DISTS)}")
     chain = read_chain_payload(payload_dir)
+    ar = chain.autoregressive if autoregressive else None
+    if autoregressive:
+        if ar is None:
+            raise ValueError("autoregressive client loop requested but the payload has no assets")
+        if layers and layers != chain.n_layers:
+            raise ValueError("the autoregressive client loop requires the full layer chain")
+        if tokens > ar.server_evaluations:
+            raise ValueError(f"tokens exceeds the autoregressive server_evaluations "
+                             f"({ar.server_evaluations})")
     if layers:
         if not 1 <= layers <= chain.n_layers:
             raise ValueError("layers must be in 1..n_layers")
@@ -487,7 +537,9 @@ def run_payload(payload_dir: str, *, tokens: int = 0, bootstrap_passes: int = 2,
         from .mamba2_payload import decode_tokens
         chain.expected_final, _ = decode_tokens(chain, chain.input_embeddings, False)
         chain.expected_poly_final, _ = decode_tokens(chain, chain.input_embeddings, True)
-    n_tok = tokens or chain.n_test_tokens
+    n_tok = tokens or (ar.server_evaluations if ar else chain.n_test_tokens)
+    if ar is None and n_tok > chain.n_test_tokens:
+        raise ValueError("tokens exceeds the payload's n_test_tokens")
     slots = 65536 if classical else 32768
     t0 = time.perf_counter()
     extra = dict(CLASSICAL128) if classical else {}
@@ -496,22 +548,19 @@ def run_payload(payload_dir: str, *, tokens: int = 0, bootstrap_passes: int = 2,
     audit = cc.SecurityAudit() if classical else None
     dec = EncryptedMamba2Decoder(cc, keys, chain, bootstrap_passes=bootstrap_passes, log=log)
     setup = time.perf_counter() - t0
-    states = dec.initial_states()
-    per_token, errs_poly, errs_exact = [], [], []
-    for k in range(n_tok):
-        cc.device.sync()
-        t = time.perf_counter()
-        ct, states = dec.step(chain.input_embeddings[k], states)
-        cc.device.sync()
-        per_token.append(time.perf_counter() - t)
-        got = dec.decrypt(ct)
-        if chain.expected_poly_final is not None:
-            errs_poly.append(float(np.max(np.abs(got - chain.expected_poly_final[k]))))
-        errs_exact.append(float(np.max(np.abs(got - chain.expected_final[k]))))
-        log(f"token {k}: {per_token[-1]:.2f}s error vs polynomial "
-            f"{errs_poly[-1] if errs_poly else float('nan'):.2e} vs exact {errs_exact[-1]:.2e}")
+    loop = token_loop(dec, chain, n_tok, ar, cc.device.sync, log)
+    per_token, errs_poly, errs_exact = loop["seconds"], loop["errors_poly"], loop["errors_exact"]
+    selected, client_seconds = loop["selected"], loop["client_seconds"]
     s = dec.ev.stats
-    return {
+    ar_report = {}
+    if ar is not None:
+        expected = ar.expected_ids[:max(0, n_tok - ar.prompt_tokens + 1)]
+        ar_report = {"autoregressive_protocol": "client-in-loop-greedy-v1",
+                     "autoregressive_selected_ids": selected,
+                     "autoregressive_expected_ids": expected,
+                     "autoregressive_tokens_match": selected == expected,
+                     "autoregressive_client_seconds": client_seconds}
+    return {**ar_report,
         "schema": "fhemamba-m2-decode-result-v1",
         "encrypted": True,
         "layers": chain.n_layers,
@@ -556,17 +605,21 @@ def main(argv=None) -> int:
     ap.add_argument("--security", default="not-set", choices=("not-set", "128-classic"))
     ap.add_argument("--layers", type=int, default=0,
                     help="decode only the first LAYERS layers (0: all)")
+    ap.add_argument("--autoregressive-client-loop", action="store_true",
+                    help="greedy client-in-loop decoding over the payload's assets")
     args = ap.parse_args(sys.argv[1:] if argv is None else argv)
     try:
         report = run_payload(args.payload, tokens=args.tokens,
                              bootstrap_passes=args.bootstrap_passes,
                              secret_key_dist=args.secret_key_dist, security=args.security,
-                             layers=args.layers)
+                             layers=args.layers,
+                             autoregressive=args.autoregressive_client_loop)
     except Exception as exc:  # noqa: BLE001 - reported as exit code 2
         print(exc, file=sys.stderr)
         return 2
     err = report["max_abs_error_vs_polynomial"]
-    report["passed"] = bool(err is not None and err <= args.tolerance)
+    report["passed"] = bool(err is not None and err <= args.tolerance and
+                            report.get("autoregressive_tokens_match", True))
     with open(args.result, "w") as f:
         json.dump(report, f)
     return 0 if report["passed"] else 1

@@ -22,7 +22,10 @@ normalization recipe "scaled-goldschmidt-invsqrt-v1" for the block, gated
 and final norms (chain.json final_norm_poly).  Joint-gate payloads
 (layer format "fhemamba-m1-joint-v1", chain format
 "fhemamba-m2-chain-joint-v1") carry a "shared-dissipation-factor-v1" gate
-that replaces dt_softplus and decay_exp on every head (JointGateSpec).
+that replaces dt_softplus and decay_exp on every head (JointGateSpec).  A
+chain.json "autoregressive" block with client_embedding_w (and optionally
+client_lm_head_w / _b) holds the client-in-loop greedy assets
+(AutoregressiveAssets).
 
 Decode semantics per layer (src/fhemamba/reference.py:182-339, ngroups 1,
 no MLP split): hidden -> RMSNorm (rms_invsqrt) -> in_proj -> z | xBC | dt;
@@ -319,8 +322,59 @@ class ChainPayload:
     # the last layer's rms_invsqrt (m1_payload.py:421-426)
     final_norm_poly: object = None
 
+    # client-in-loop greedy assets (chain.json "autoregressive"); None: none
+    autoregressive: "AutoregressiveAssets | None" = None
+
     def final_invsqrt(self):
         return self.final_norm_poly or self.layers[-1].polys["rms_invsqrt"]
+
+
+@dataclass
+class AutoregressiveAssets:
+    """Client-in-loop greedy decoding ("client-in-loop-greedy-v1"): the
+    server evaluates prompt_tokens + generate_tokens - 1 embeddings; after
+    each evaluation from the last prompt token on, the client decrypts the
+    final normed hidden, takes logits = lm_head_w hidden (+ lm_head_b; the
+    embedding table when the two are tied), selects the first maximal logit
+    and sends that token's embedding next (src/fhemamba/m1_payload.py:
+    519-618 writes the assets, native/fideslib_stage0/src/
+    stage1_mamba2_payload.cpp:476-528 reads them and
+    stage1_mamba2_decode_fideslib.cpp:4549-4611 runs the client step)."""
+    prompt_tokens: int
+    generate_tokens: int
+    server_evaluations: int
+    prompt_ids: list
+    expected_ids: list               # poly_generated_ids: the pass criterion
+    embedding_w: np.ndarray          # [vocab][d_model]
+    lm_head_w: np.ndarray | None     # None: tied to embedding_w
+    lm_head_b: np.ndarray | None
+    embeddings: np.ndarray           # [server_evaluations][d_model]
+    expected_poly_final: np.ndarray
+    expected_exact_final: np.ndarray
+
+    @property
+    def vocab(self) -> int:
+        return self.embedding_w.shape[0]
+
+    def select(self, hidden) -> int:
+        """The client's greedy choice for a decrypted final hidden."""
+        w = self.embedding_w if self.lm_head_w is None else self.lm_head_w
+        with np.errstate(invalid="ignore", over="ignore"):
+            logits = w @ np.asarray(hidden, dtype=np.float64)
+            if self.lm_head_b is not None:
+                logits = logits + self.lm_head_b
+        if not np.all(np.isfinite(logits)):
+            raise ValueError("non-finite autoregressive client logit")
+        return int(np.argmax(logits))
+
+    def input_for(self, step: int, selected: list) -> np.ndarray:
+        """The embedding evaluated at `step`: the prompt's, then the client's
+        previous choice."""
+        if step < self.prompt_tokens:
+            return self.embeddings[step]
+        if len(selected) != step - self.prompt_tokens + 1:
+            raise ValueError("missing client-selected autoregressive embedding")
+        return self.embedding_w[selected[-1]]
 
 
 def _read_bin(path: str, shape) -> np.ndarray:
@@ -402,6 +456,9 @@ def read_chain_payload(directory: str) -> ChainPayload:
     chain.layers = [read_layer_payload(os.path.join(directory, d)) for d in dirs]
     if meta.get("final_norm_poly") is not None:
         chain.final_norm_poly = read_poly(meta["final_norm_poly"])
+    if isinstance(meta.get("autoregressive"), dict):
+        chain.autoregressive = _read_autoregressive(meta["autoregressive"], tens, rb,
+                                                    chain.layers[0].d_model)
     first = chain.layers[0]
     for i, lay in enumerate(chain.layers):
         if (lay.d_model, lay.d_inner, lay.num_heads, lay.head_dim, lay.state_size,
@@ -409,6 +466,36 @@ def read_chain_payload(directory: str) -> ChainPayload:
                                      first.head_dim, first.state_size, first.conv_kernel):
             raise ValueError(f"chain layer payload dims mismatch at index {i}")
     return chain
+
+
+def _read_autoregressive(ar: dict, tens: dict, rb, d_model: int) -> AutoregressiveAssets:
+    """Checks of stage1_mamba2_payload.cpp:476-528 and
+    stage1_mamba2_decode_fideslib.cpp:791-876."""
+    if ar.get("protocol") != "client-in-loop-greedy-v1":
+        raise ValueError("unsupported autoregressive payload protocol")
+    pt, gt, ev = (int(ar[k]) for k in ("prompt_tokens", "generate_tokens",
+                                        "server_evaluations"))
+    if pt < 1 or gt < 1 or ev != pt + gt - 1:
+        raise ValueError("invalid autoregressive evaluation count")
+    ids = [int(v) for v in ar.get("poly_generated_ids", [])]
+    emb = rb("client_embedding_w")
+    if emb.ndim != 2 or emb.shape[1] != d_model:
+        raise ValueError("client_embedding_w must be rank 2 with d_model columns")
+    vocab = emb.shape[0]
+    head = rb("client_lm_head_w") if "client_lm_head_w" in tens else None
+    bias = rb("client_lm_head_b") if "client_lm_head_b" in tens else None
+    assets = AutoregressiveAssets(
+        pt, gt, ev, [int(v) for v in ar.get("prompt_ids", [])], ids, emb, head, bias,
+        rb("autoregressive_poly_embeddings"), rb("autoregressive_poly_expected_final"),
+        rb("autoregressive_exact_expected_final"))
+    if len(ids) != gt or any(not 0 <= i < vocab for i in ids) or \
+            (head is not None and head.shape != (vocab, d_model)) or \
+            (bias is not None and bias.shape != (vocab,)) or \
+            any(a.shape != (ev, d_model) for a in (assets.embeddings,
+                                                   assets.expected_poly_final,
+                                                   assets.expected_exact_final)):
+        raise ValueError("autoregressive tensor shape mismatch")
+    return assets
 
 
 # ----------------------------------------------------------------- plain decode
@@ -470,6 +557,27 @@ def final_norm(chain: ChainPayload, hidden: np.ndarray, polynomial: bool):
     v = np.mean(hidden ** 2) + chain.final_norm_eps
     poly = chain.final_invsqrt() if polynomial else None
     return hidden * rms_inv(v, poly) * chain.final_norm_w
+
+
+def autoregressive_decode(chain: ChainPayload, polynomial: bool, evaluations: int = 0):
+    """The client-in-loop greedy protocol on the plain decode: (final
+    hiddens [evaluations][d_model], selected ids)."""
+    ar = chain.autoregressive
+    if ar is None:
+        raise ValueError("the payload has no autoregressive assets")
+    n = evaluations or ar.server_evaluations
+    if not 1 <= n <= ar.server_evaluations:
+        raise ValueError("evaluations exceed the payload's server_evaluations")
+    states = [zero_state(lay) for lay in chain.layers]
+    finals, selected = [], []
+    for step in range(n):
+        h = ar.input_for(step, selected)
+        for i, lay in enumerate(chain.layers):
+            h, states[i] = layer_step(lay, h, states[i], polynomial)
+        finals.append(final_norm(chain, h, polynomial))
+        if step >= ar.prompt_tokens - 1:
+            selected.append(ar.select(finals[-1]))
+    return np.array(finals), selected
 
 
 def decode_tokens(chain: ChainPayload, embeddings: np.ndarray, polynomial: bool,

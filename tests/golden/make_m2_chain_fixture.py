@@ -23,6 +23,13 @@ test tokens:
                         sum |p_k| <= 0.999, which the exporter's gate
                         certificate requires) and q interpolates
                         sqrt(softplus(z) / (1 - exp(-softplus(z) rate))).
+  m2_chain_tiny_ar/     the scheduled-normalization payload plus the
+                        client-in-loop greedy assets, as the reference's
+                        test exports them (tests/test_scheduled_payload.py:
+                        autoregressive_prompt_tokens 2,
+                        autoregressive_generate_tokens 2: client embedding
+                        table, the embeddings of the evaluated tokens, the
+                        polynomial and exact final hiddens and the greedy ids).
 Only the payloads it writes (float32 tensors and JSON) are kept: nothing of
 the reference is copied, and nothing here runs at test time.
 
@@ -140,6 +147,9 @@ def main(reference_root="/root/reference", *names):
             "m2_chain_tiny_sched": dict(cal_tokens=16, normalization_bundle=norms),
             "m2_chain_tiny_joint": dict(cal_tokens=16, normalization_bundle=norms,
                                         stabilized_gate_bundle=gates),
+            "m2_chain_tiny_ar": dict(cal_tokens=16, normalization_bundle=norms,
+                                     autoregressive_prompt_tokens=2,
+                                     autoregressive_generate_tokens=2),
             "m2_chain_tiny_joint_cheb": dict(cal_tokens=16, normalization_bundle=norms,
                                              stabilized_gate_bundle=cheb_gates),
         }

@@ -49,3 +49,18 @@ def test_reference_joint_gate_payload_decodes(name):
     print(f"{name}: {report['seconds_per_token']} s/token, {report['bootstraps']} bootstraps, "
           f"errors vs polynomial {report['per_token_errors_vs_polynomial']}", flush=True)
     assert report["max_abs_error_vs_polynomial"] < TOL
+
+
+def test_reference_autoregressive_client_loop():
+    """The exporter's client-in-loop assets on the GPU: three server
+    evaluations (two prompt tokens, then the client's own greedy choice),
+    each final hidden within the tolerance of the exporter's polynomial
+    trace, and the client selects the exporter's greedy ids."""
+    path = os.path.join(os.path.dirname(__file__), "golden", "m2_chain_tiny_ar")
+    report = D.run_payload(path, seed=34, autoregressive=True, log=lambda m: None)
+    print(f"client loop: selected {report['autoregressive_selected_ids']} expected "
+          f"{report['autoregressive_expected_ids']}, errors vs polynomial "
+          f"{report['per_token_errors_vs_polynomial']}", flush=True)
+    assert report["tokens"] == 3
+    assert report["autoregressive_tokens_match"]
+    assert report["max_abs_error_vs_polynomial"] < TOL

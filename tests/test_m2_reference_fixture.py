@@ -288,3 +288,93 @@ def test_synthetic_joint_chain_round_trip(tmp_path):
     again = M.read_chain_payload(str(tmp_path)).layers[1].joint
     assert np.array_equal(again.p, g.p) and np.array_equal(again.lo, g.lo)
     assert _rel(ch.expected_poly_final, ch.expected_final) < 1e-3
+
+
+# ------------------------------------------------------------- client loop
+AR = os.path.join(os.path.dirname(__file__), "golden", "m2_chain_tiny_ar")
+
+
+def test_autoregressive_assets_read():
+    """The exporter's client-in-loop assets (tests/test_scheduled_payload.py's
+    export: two prompt tokens, two generated): protocol, counts, untied
+    lm_head, tensor shapes."""
+    ar = M.read_chain_payload(AR).autoregressive
+    assert (ar.prompt_tokens, ar.generate_tokens, ar.server_evaluations) == (2, 2, 3)
+    assert ar.vocab == 97 and ar.lm_head_w is not None and ar.lm_head_b is None
+    assert ar.embeddings.shape == (3, 32) and len(ar.expected_ids) == 2
+    # the evaluated embeddings are the table's rows of the evaluated ids
+    meta = json.load(open(os.path.join(AR, "chain.json")))["autoregressive"]
+    for k, tok in enumerate(meta["poly_evaluated_ids"]):
+        assert np.array_equal(ar.embeddings[k], ar.embedding_w[tok])
+
+
+@pytest.mark.parametrize("polynomial", [True, False])
+def test_autoregressive_plain_loop_selects_exporter_ids(polynomial):
+    """The plain client loop reproduces the exporter's traces: the final
+    hiddens of the polynomial (exact) circuit and the greedy ids it chose."""
+    ch = M.read_chain_payload(AR)
+    ar = ch.autoregressive
+    finals, ids = M.autoregressive_decode(ch, polynomial)
+    meta = json.load(open(os.path.join(AR, "chain.json")))["autoregressive"]
+    want = ar.expected_poly_final if polynomial else ar.expected_exact_final
+    assert _rel(finals, want) < 1e-5
+    assert ids == meta["poly_generated_ids" if polynomial else "exact_generated_ids"]
+
+
+def test_autoregressive_client_loop_on_slots():
+    """The decoder's token loop with the client in it, on the slot-level
+    stand-in: every server evaluation matches the polynomial trace and the
+    client selects the exporter's ids (the third input is the client's own
+    choice, not a stored embedding)."""
+    from fhemamba_amd.mamba2_decode import EncryptedMamba2Decoder, token_loop
+    from packed_builder import SlotContext, SlotKeys
+    ch = M.read_chain_payload(AR)
+    dec = EncryptedMamba2Decoder(SlotContext(1024), SlotKeys(), ch)
+    out = token_loop(dec, ch, ch.autoregressive.server_evaluations, ch.autoregressive,
+                     log=lambda m: None)
+    assert out["selected"] == ch.autoregressive.expected_ids
+    assert max(out["errors_poly"]) < 1e-5
+
+
+def test_autoregressive_selection_rules():
+    """Greedy choice: first maximal logit, bias added, tied head uses the
+    embedding table, non-finite logits refused; a missing client choice is
+    refused."""
+    emb = np.array([[1.0, 0.0], [0.0, 1.0], [1.0, 1.0]])
+    mk = lambda head, bias: M.AutoregressiveAssets(  # noqa: E731
+        1, 2, 2, [0], [2, 2], emb, head, bias, emb[:2], emb[:2], emb[:2])
+    assert mk(None, None).select([1.0, 1.0]) == 2
+    assert mk(None, np.array([0.0, 0.0, -1.0])).select([1.0, 1.0]) == 0   # tie: first
+    assert mk(emb[::-1].copy(), None).select([1.0, 0.0]) == 0
+    with pytest.raises(ValueError, match="non-finite"):
+        mk(None, None).select([np.inf, 0.0])
+    with pytest.raises(ValueError, match="missing"):
+        mk(None, None).input_for(1, [])
+
+
+@pytest.mark.parametrize("edit, match", [
+    (lambda m: _set(m["autoregressive"], "protocol", "sampled"), "protocol"),
+    (lambda m: _set(m["autoregressive"], "server_evaluations", 4), "evaluation count"),
+    (lambda m: _set(m["autoregressive"], "poly_generated_ids", [85]), "shape"),
+    (lambda m: _set(m["autoregressive"], "poly_generated_ids", [85, 97]), "shape"),
+])
+def test_autoregressive_payload_checks(tmp_path, edit, match):
+    import shutil
+    dst = tmp_path / "p"
+    shutil.copytree(AR, dst)
+    meta = json.loads((dst / "chain.json").read_text())
+    edit(meta)
+    (dst / "chain.json").write_text(json.dumps(meta))
+    with pytest.raises(ValueError, match=match):
+        M.read_chain_payload(str(dst))
+
+
+def test_autoregressive_command_line_refusals(tmp_path):
+    """--autoregressive-client-loop on a payload without assets, or with a
+    truncated chain, exits 2 before any device work."""
+    from fhemamba_amd import mamba2_decode as D
+    res = str(tmp_path / "r.json")
+    assert D.main([FIX, res, "--autoregressive-client-loop"]) == 2
+    assert D.main([AR, res, "--autoregressive-client-loop", "--layers", "1"]) == 2
+    assert D.main([AR, res, "--autoregressive-client-loop", "--tokens", "4"]) == 2
+    assert D.main([FIX, res, "--tokens", "3"]) == 2
