@@ -273,7 +273,7 @@ BOOT_DEPTH, BOOT_BUDGET = 44, (4, 4)
 REF_BOOTSTRAP_S = 1083.2 / 2187
 
 
-def _bootstrap_once(secret_dist: str, steps: int, warmup: int) -> dict:
+def _bootstrap_once(secret_dist: str, steps: int, warmup: int, s2c_first: bool = False) -> dict:
     import numpy as np
     from fhemamba_amd.ckks_probes import build_toy_context
 
@@ -281,12 +281,12 @@ def _bootstrap_once(secret_dist: str, steps: int, warmup: int) -> dict:
     cc, keys = build_toy_context(ring_dimension=N, batch=slots, depth=BOOT_DEPTH,
                                  scale_bits=SCALE_BITS, first_mod_bits=FIRST_BITS, seed=21,
                                  secret_dist=secret_dist)
-    cc.EvalBootstrapSetup(list(BOOT_BUDGET), [0, 0], slots)
+    cc.EvalBootstrapSetup(list(BOOT_BUDGET), [0, 0], slots, s2c_first=s2c_first,
+                          real_slots=s2c_first)
     cc.EvalBootstrapKeyGen(keys.secretKey, slots)
-    L = len(cc.GetModuli()[0])
     x = np.random.default_rng(8).uniform(-1, 1, slots)
     ct = cc.Encrypt(keys.publicKey, cc.MakeCKKSPackedPlaintext(list(x)))
-    ct.SetLevel(L - 2)
+    ct.SetLevel(cc.GetBootstrapInputCeiling())
     res = {}
     for passes in (1, 2):
         for _ in range(warmup):
@@ -305,6 +305,7 @@ def _bootstrap_once(secret_dist: str, steps: int, warmup: int) -> dict:
     sine = cc._boot.cfg.sine
     res.update({
         "levels_consumed": cc.GetBootstrapDepth(),
+        "input_ceiling": cc.GetBootstrapInputCeiling(),
         "output_level": int(out.GetLevel()),
         "rotation_keys": len(cc._boot.rotation_indices()),
         "eval_mod": {"K": sine.K, "double_angles": sine.r, "degree": sine.degree},
@@ -322,6 +323,8 @@ def run_bootstrap(steps: int = 3, warmup: int = 2):
     one before timing; errors are measured after timing."""
     res = _bootstrap_once("UNIFORM_TERNARY", steps, warmup)
     res["sparse_secret"] = _bootstrap_once("SPARSE_TERNARY", steps, warmup)
+    res["s2c_first"] = _bootstrap_once("UNIFORM_TERNARY", steps, warmup, True)
+    res["s2c_first_sparse_secret"] = _bootstrap_once("SPARSE_TERNARY", steps, warmup, True)
     res.update({
         "reference_gb10_ms_per_bootstrap": REF_BOOTSTRAP_S * 1e3,
         "speedup_vs_reference_one_pass": REF_BOOTSTRAP_S / (res["one_pass"]["ms"] * 1e-3),
@@ -372,8 +375,9 @@ def run_decode(tokens: int = 2, security: str = "not-set"):
             "secret_key_dist": rep["secret_key_dist"],
             "workload": ("encrypted Mamba-2-130M-shaped decode, 24 layers (seeded random-init "
                          "weights, synthetic payload), classical-128: N=2^17, 65536 slots, "
-                         "depth 44, 45 Q + 12 P primes, 4 digits, uniform ternary secret; "
-                         "first token from zero state, then carried state"),
+                         "depth 44, 45 Q + 12 P primes, 4 digits, uniform ternary secret, "
+                         "SlotToCoeff-first two-pass refreshes; first token from zero state, "
+                         "then carried state"),
         }
     return {
         "s_per_token_first": rep["first_token_seconds"],
@@ -386,8 +390,9 @@ def run_decode(tokens: int = 2, security: str = "not-set"):
         "secret_key_dist": rep["secret_key_dist"],
         "workload": ("encrypted Mamba-2-130M-shaped decode, 24 layers (seeded random-init "
                      "weights and calibrated polynomials, synthetic payload), N=2^16, "
-                     "depth 44, sparse-ternary secret (h=192) as the reference decoder's; "
-                     "first token from zero state, then carried state"),
+                     "depth 44, sparse-ternary secret (h=192) as the reference decoder's, "
+                     "SlotToCoeff-first two-pass refreshes; first token from zero state, "
+                     "then carried state"),
     }
 
 

@@ -18,6 +18,18 @@ The FFTs are factored into their radix-2 stages, grouped by the level
 budget; each group is one baby-step giant-step linear transform over the
 diagonals of the group's product (LinearTransformInPlace).
 
+S2C-first ordering (EvalBootstrapSetup(..., s2c_first=True), the
+reference's --s2c-first circuit, packed_fideslib.cpp:1084-1086, :1131-1134;
+full packing only): SlotToCoeff runs first, on the input at its low level,
+so that the plaintext's coefficients j and j + n become the real and
+imaginary parts of slot brv(j); then scale-down, ModRaise, CoeffToSlot and
+EvalMod leave the message in the slots with no transform after EvalMod.
+The input needs the SlotToCoeff levels before the drop to one limb (a
+lower refresh ceiling) and the output keeps them (a higher refreshed
+level).  For real slots (real_slots=True) the imaginary half carries no
+message: one EvalMod on the real part and a projection onto the real
+part (one conjugation) are the whole result.
+
 The stage structure follows the encoder's special FFT (oracle/ckks_oracle.c
 fft_special / fft_special_inv: roots zeta^(5^j) of order 4 * slots).
 OpenFHE's exact bootstrapping (its level-budget split of the FFT, its sine
@@ -288,13 +300,18 @@ class CKKSBootstrapper:
     joins the CoeffToSlot constant."""
 
     def __init__(self, cc, config: BootstrapConfig | None = None, slots: int = 0,
-                 pt_cache_bytes: int = 16 << 30):
+                 pt_cache_bytes: int = 16 << 30, s2c_first: bool = False,
+                 real_slots: bool = False):
         self.cc = cc
         self.cfg = config or BootstrapConfig.for_ring(cc.GetRingDimension())
         self.N = cc.GetRingDimension()
         self.n = int(slots) or self.N // 2
         if self.n < 2 or self.n & (self.n - 1) or self.n > self.N // 2:
             raise ValueError(f"bootstrapping slots must be a power of two in [2, {self.N // 2}]")
+        if s2c_first and self.n != self.N // 2:
+            raise ValueError("S2C-first bootstrapping requires full packing")
+        self.s2c_first = bool(s2c_first)
+        self.real_slots = bool(real_slots)
         self.R = self.N // (2 * self.n)
         self.c2s = [plan_group(D, self.n) for D in
                     fft_groups(self.n, self.cfg.level_budget[0], inverse=True)]
@@ -315,7 +332,12 @@ class CKKSBootstrapper:
 
     def depth(self) -> int:
         """Levels from ModRaise (level 0) to the output."""
-        return len(self.c2s) + self.cfg.sine.depth() + len(self.s2c)
+        return len(self.c2s) + self.cfg.sine.depth() + (0 if self.s2c_first else len(self.s2c))
+
+    def input_ceiling(self) -> int:
+        """Deepest input level (limbs consumed) EvalBootstrap accepts:
+        L - 2, less the SlotToCoeff levels under S2C-first."""
+        return len(self.cc.GetModuli()[0]) - 2 - (len(self.s2c) if self.s2c_first else 0)
 
     def correction_bits(self, in_scale: float, q0: float, scale: float) -> int:
         if self.cfg.correction_bits:
@@ -386,11 +408,28 @@ class CKKSBootstrapper:
             c = self.cc.MultByInteger(c, gain)
         return c
 
+    def _eval_mod_amplitude(self, v, amp: float):
+        """amp sin(2 pi u) for v = u / K and any real amp > 0: the
+        interpolant carries a_0 = amp^(2^-r) and each double angle
+        y <- 2 y^2 - a_(k+1) with a_(k+1) = a_k^2, so y_k = a_k cos(2^k x)
+        and y_r = amp cos(2^r x) with integer products only."""
+        r = self.cfg.sine.r
+        a = amp ** (2.0 ** -r)
+        # the floor scales with a: the same terms as the unscaled interpolant
+        c = chebyshev_ps(self.cc, v, [a * x for x in self._coeffs], floor=1e-14 * a)
+        for _ in range(r):
+            a = a * a
+            sq = self.cc.EvalSquare(c)
+            c = self.cc.EvalSub(self.cc.EvalAdd(sq, sq), a)
+        return c
+
     # --------------------------------------------------------------- bootstrap
     def bootstrap(self, ct, pre: float = 1.0, post: float = 1.0):
         """Refresh ct; the slots are multiplied by `pre` on the way in (in
         the scale-down step) and by `post` on the way out (in SlotToCoeff),
         so a residual pass spends no extra level."""
+        if self.s2c_first:
+            return self._bootstrap_s2c_first(ct, pre, post)
         cc, n, N = self.cc, self.n, self.N
         L = len(cc.GetModuli()[0])
         q0 = float(cc.GetModuli()[0][0])
@@ -431,3 +470,57 @@ class CKKSBootstrapper:
         im_m = self._eval_mod(im, gain)                       #   ~ gain 2 pi P / q0
         w = cc.EvalAdd(re_m, cc.MultByMonomial(im_m, N // 2))
         return self._transform(w, self.s2c, "s2c", back / gain, power_last=True)
+
+    def _bootstrap_s2c_first(self, ct, pre: float, post: float):
+        """SlotToCoeff, scale-down, ModRaise, CoeffToSlot, EvalMod.
+
+        The SlotToCoeff constant k and the scale-down's `pre` make the
+        one-limb plaintext's coefficients P_j + i P_{j+n} = in_scale k
+        v[brv(j)] for v = pre m; EvalMod with amplitude A returns
+        A 2 pi P / q0 = pre post m when k = post q0 / (A 2 pi in_scale).  A
+        is the ordinary pipeline's way-back factor q0 2^c post /
+        (2 pi in_scale), so k = 2^-c and |P / q0| (the sine's argument) has
+        the same size as there; A, whatever real value, rides on the
+        double-angle constants (_eval_mod_amplitude), no level.  The input
+        is first dropped
+        to the fixed level input_ceiling(), so the SlotToCoeff diagonals are
+        encoded at one level whatever level the input came from."""
+        cc, n, N = self.cc, self.n, self.N
+        L = len(cc.GetModuli()[0])
+        q0 = float(cc.GetModuli()[0][0])
+        x = ct.Clone()
+        cc.RescaleInPlace(x)
+        top = self.input_ceiling()
+        if x.GetLevel() > top:
+            raise ValueError(f"S2C-first EvalBootstrap needs the input at level <= {top}")
+        x.SetLevel(top)
+        in_scale = cc.GetScalingFactorReal(L - 1)
+        c = self.correction_bits(in_scale, q0, cc.GetScalingFactorReal(0))
+        amp = q0 / (2 * math.pi * in_scale) * 2.0 ** c * post        # EvalMod's amplitude
+        k = post * q0 / (amp * 2 * math.pi * in_scale)               # = 2^-c
+        y = self._transform(x, self.s2c, "s2c_first", k, power_last=True)
+        # level L - 2: times pre (which may be large: a plain constant has
+        # no encoding limit) to one limb at scale sf[L-1], as the ordinary
+        # scale-down
+        y = cc.EvalMult(y, pre * cc.GetScalingFactorReal(L - 2) / y.GetScalingFactor())
+        cc.RescaleInPlace(y)
+        y.SetScalingFactor(in_scale)
+        raised = cc.ModRaise(y)
+        K = self.cfg.sine.K
+        z = self._transform(raised, self.c2s, "c2s", raised.GetScalingFactor() / (q0 * n * 2 * K))
+        zc = cc.EvalConjugate(z)
+        if self.real_slots:
+            # EvalMod turns the conjugation's key-switch noise in Re(u) / K
+            # into imaginary slot noise amp 2 pi K times larger, which a
+            # second pass would not see and high-degree polynomials would
+            # fold back into the real parts: the result is projected onto
+            # its real part, (y + conj(y)) / 2 with the 1/2 in the amplitude
+            out = self._eval_mod_amplitude(cc.EvalAdd(z, zc), amp / 2)
+            cc.RescaleInPlace(out)
+            out = cc.EvalAdd(out, cc.EvalConjugate(out))             # pre post Re(m)
+        else:
+            out = self._eval_mod_amplitude(cc.EvalAdd(z, zc), amp)
+            im = cc.MultByMonomial(cc.EvalSub(z, zc), 3 * N // 2)
+            out = cc.EvalAdd(out, cc.MultByMonomial(self._eval_mod_amplitude(im, amp), N // 2))
+            cc.RescaleInPlace(out)
+        return out

@@ -796,17 +796,23 @@ class CryptoContext:
         return self._wrap(poly, 0, 1, self._sf[0], a.slots)
 
     def EvalBootstrapSetup(self, levelBudget=(5, 5), dim1=(0, 0), slots: int = 0,  # noqa: N802,N803
-                           correctionFactor: int = 0, precompute: bool = True) -> None:
+                           correctionFactor: int = 0, precompute: bool = True, *,
+                           s2c_first: bool = False, real_slots: bool = False) -> None:
         """Plan CoeffToSlot / SlotToCoeff for `slots`-slot ciphertexts (full
         or sparse packing) with levelBudget = (levels for CoeffToSlot, levels
         for SlotToCoeff).  correctionFactor 0 picks the message scale-down
-        automatically."""
+        automatically.  s2c_first: the SlotToCoeff-first ordering of the
+        reference's patched EvalBootstrapSetup (packed_fideslib.cpp:1084-1086;
+        full packing; the input must sit SlotToCoeff levels lower, the output
+        keeps them); real_slots: the caller's slots are real, so S2C-first
+        runs EvalMod on the real part only."""
         from .bootstrap import BootstrapConfig, CKKSBootstrapper
         slots = int(slots) or self._slots
         cfg = BootstrapConfig.for_ring(self.n, tuple(int(b) for b in levelBudget),
                                        int(correctionFactor),
                                        hamming_weight=self.secret_hamming_weight())
-        self._boot = CKKSBootstrapper(self, cfg, slots)
+        self._boot = CKKSBootstrapper(self, cfg, slots, s2c_first=s2c_first,
+                                      real_slots=real_slots)
 
     def _bootstrapper(self):
         if self._boot is None:
@@ -823,6 +829,10 @@ class CryptoContext:
     def GetBootstrapDepth(self) -> int:  # noqa: N802
         """Levels one EvalBootstrap consumes after ModRaise."""
         return self._bootstrapper().depth()
+
+    def GetBootstrapInputCeiling(self) -> int:  # noqa: N802
+        """Deepest level an EvalBootstrap input may sit at."""
+        return self._bootstrapper().input_ceiling()
 
     def EvalBootstrap(self, ct: "Ciphertext", numIterations: int = 1,  # noqa: N802,N803
                       precision: int = 0, *, scale: float = 1.0) -> "Ciphertext":

@@ -71,13 +71,15 @@ class LayerCtState:
 
 class EncryptedMamba2Decoder:
     def __init__(self, cc, keys, chain: ChainPayload, *, bootstrap_passes: int = 2,
-                 refresh_ceiling: int | None = None, bounds: dict | None = None, log=None):
+                 refresh_ceiling: int | None = None, bounds: dict | None = None, log=None,
+                 s2c_first: bool = False):
         first = chain.layers[0]
         self.chain, self.cc = chain, cc
         self.slots = cc.GetBatchSize()
         self.log = log or (lambda m: None)
         self.ev = PackedEvaluator(cc, keys, self.slots, bootstrap_passes=bootstrap_passes,
-                                  refresh_ceiling=refresh_ceiling, log=self.log)
+                                  refresh_ceiling=refresh_ceiling, log=self.log,
+                                  s2c_first=s2c_first)
         self.bounds = [self._layer_bounds(lay, bounds) for lay in chain.layers]
         self.d, self.di, self.ns = first.d_model, first.d_inner, first.state_size
         self.nh, self.hd, self.kc = first.num_heads, first.head_dim, first.conv_kernel
@@ -485,7 +487,8 @@ SECRET_KEY_DISTS = {"sparse-ternary": "SPARSE_TERNARY", "uniform-ternary": "UNIF
 
 def run_payload(payload_dir: str, *, tokens: int = 0, bootstrap_passes: int = 2, seed=None,
                 secret_key_dist: str | None = None, security: str = "not-set",
-                layers: int = 0, autoregressive: bool = False, log=print) -> dict:
+                layers: int = 0, autoregressive: bool = False, s2c_first: bool = True,
+                log=print) -> dict:
     """Decode the payload's test embeddings in turn (carried state) and
     compare the decrypted outputs with its polynomial-circuit and exact
     references; returns the report.
@@ -508,7 +511,12 @@ def run_payload(payload_dir: str, *, tokens: int = 0, bootstrap_passes: int = 2,
     evaluation from the last prompt token on the client decrypts, selects
     the greedy token from its logits and encrypts that token's embedding
     next; errors are taken against the assets' polynomial and exact final
-    hiddens, and the selected ids against the exporter's greedy ids."""
+    hiddens, and the selected ids against the exporter's greedy ids.
+
+    s2c_first (default): refresh with the SlotToCoeff-first bootstrap (the
+    packed executor's --s2c-first circuit; real slots, one EvalMod), about
+    40% less bootstrap time than the ordinary order at the same usable
+    level interval and precision; False: the ordinary order."""
     from . import ckks
     from .mamba2_payload import read_chain_payload
     from .packed import CLASSICAL128, build_context
@@ -546,7 +554,8 @@ def run_payload(payload_dir: str, *, tokens: int = 0, bootstrap_passes: int = 2,
     cc, keys = build_context(slots, seed=seed, secret_dist=getattr(
         ckks.SecretKeyDist, SECRET_KEY_DISTS[secret_key_dist]), **extra)
     audit = cc.SecurityAudit() if classical else None
-    dec = EncryptedMamba2Decoder(cc, keys, chain, bootstrap_passes=bootstrap_passes, log=log)
+    dec = EncryptedMamba2Decoder(cc, keys, chain, bootstrap_passes=bootstrap_passes, log=log,
+                                 s2c_first=s2c_first)
     setup = time.perf_counter() - t0
     loop = token_loop(dec, chain, n_tok, ar, cc.device.sync, log)
     per_token, errs_poly, errs_exact = loop["seconds"], loop["errors_poly"], loop["errors_exact"]
@@ -570,6 +579,7 @@ def run_payload(payload_dir: str, *, tokens: int = 0, bootstrap_passes: int = 2,
         "slots": slots,
         "security": security,
         "security_audit": audit,
+        "s2c_first": s2c_first,
         "secret_key_dist": secret_key_dist,
         "setup_seconds": setup,
         "seconds_per_token": per_token,
@@ -607,13 +617,16 @@ def main(argv=None) -> int:
                     help="decode only the first LAYERS layers (0: all)")
     ap.add_argument("--autoregressive-client-loop", action="store_true",
                     help="greedy client-in-loop decoding over the payload's assets")
+    ap.add_argument("--ordinary-bootstrap", action="store_true",
+                    help="refresh with the ordinary bootstrap order instead of SlotToCoeff-first")
     args = ap.parse_args(sys.argv[1:] if argv is None else argv)
     try:
         report = run_payload(args.payload, tokens=args.tokens,
                              bootstrap_passes=args.bootstrap_passes,
                              secret_key_dist=args.secret_key_dist, security=args.security,
                              layers=args.layers,
-                             autoregressive=args.autoregressive_client_loop)
+                             autoregressive=args.autoregressive_client_loop,
+                             s2c_first=not args.ordinary_bootstrap)
     except Exception as exc:  # noqa: BLE001 - reported as exit code 2
         print(exc, file=sys.stderr)
         return 2

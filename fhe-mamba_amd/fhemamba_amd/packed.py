@@ -337,16 +337,22 @@ class PackedEvaluator:
     def __init__(self, cc, keys, slots: int, *, bootstrap_passes: int = 2,
                  refresh_ceiling: int | None = None, replicated_linear: bool = True,
                  trace_levels: bool = False, level_budget=(4, 4), client=None,
-                 log=None, pt_cache_bytes: int = 48 << 30):
+                 log=None, pt_cache_bytes: int = 48 << 30, s2c_first: bool = False):
         if bootstrap_passes not in (1, 2):
             raise ValueError("bootstrap passes must be 1 or 2")
         self.cc, self.keys, self.slots = cc, keys, int(slots)
         self.bootstrap_passes = bootstrap_passes
+        self.s2c_first = bool(s2c_first)
+        # every value here is real: under S2C-first one EvalMod (the real
+        # part) is the whole refresh
+        cc.EvalBootstrapSetup(list(level_budget), [0, 0], self.slots, s2c_first=self.s2c_first,
+                              real_slots=True)
         # deepest level a value may reach and still be masked (one level)
-        # and bootstrapped (input at most L - 2): L - 3, 42 for the
-        # reference's depth-44 chain (its executor stops at 39, :1132)
+        # and bootstrapped: the bootstrap's input ceiling less one, L - 3
+        # (42 for the reference's depth-44 chain; its executor stops at 39,
+        # :1132) or, S2C-first, the SlotToCoeff levels lower (:1133)
         self.refresh_ceiling = refresh_ceiling if refresh_ceiling is not None else \
-            len(cc.GetModuli()[0]) - 3
+            cc.GetBootstrapInputCeiling() - 1
         self.replicated_linear = replicated_linear
         self.trace_levels = trace_levels
         self.client = client
@@ -359,7 +365,6 @@ class PackedEvaluator:
         self.operation_stats: dict = {}
         self.client_tokens: list = []
         self.client_margins: list = []
-        cc.EvalBootstrapSetup(list(level_budget), [0, 0], self.slots)
         t0 = time.perf_counter()
         cc.EvalBootstrapKeyGen(keys.secretKey, self.slots)
         self.stats["keygen_seconds"] += time.perf_counter() - t0
@@ -773,7 +778,7 @@ _FLAG_OPTIONS = {
 }
 _VALUE_OPTIONS = {"--plaintext-cache-capacity", "--prefetch-workers", "--frontier-live-limit",
                   "--security-digits"}
-_UNSUPPORTED = {"--s2c-first", "--gpu-dual-ring", "--diagnostic-reference",
+_UNSUPPORTED = {"--gpu-dual-ring", "--diagnostic-reference",
                 "--diagnostic-output", "--diagnostic-refresh-pair"}
 
 
@@ -781,7 +786,8 @@ def parse_args(argv):
     if len(argv) < 4:
         raise ValueError(USAGE)
     opts = dict(program=argv[0], result=argv[1], direct_linear=False, bootstrap_passes=2,
-                trace_levels=False, client_head=None, security="not-set", accepted=[])
+                trace_levels=False, client_head=None, security="not-set", s2c_first=False,
+                accepted=[])
     poly_tol, exact_tol = float(argv[2]), float(argv[3])
     i = 4
     while i < len(argv):
@@ -790,6 +796,8 @@ def parse_args(argv):
             opts["direct_linear"] = True
         elif a == "--trace-levels":
             opts["trace_levels"] = True
+        elif a == "--s2c-first":
+            opts["s2c_first"] = True
         elif a == "--bootstrap-passes" and i + 1 < len(argv):
             i += 1
             opts["bootstrap_passes"] = int(argv[i])
@@ -813,6 +821,13 @@ def parse_args(argv):
         i += 1
     if opts["security"] not in ("not-set", "128-classic"):
         raise ValueError("security must be not-set or 128-classic")
+    # refresh-planning rules of packed_fideslib.cpp:1013-1017
+    acc = set(opts["accepted"])
+    if "--batch-refresh" in acc and ("--planned-refresh" not in acc or
+                                     opts["bootstrap_passes"] != 2):
+        raise ValueError("batch refresh requires planned refresh and two bootstrap passes")
+    if opts["s2c_first"] and "--batch-refresh" not in acc:
+        raise ValueError("S2C-first requires planned two-pass batch refresh")
     # --security-digits: HYBRID digits of the classical-128 context, 1..16,
     # only with 128-classic (packed_fideslib.cpp:913-914, :974, :991-992)
     digits = [a for a in opts["accepted"] if a.startswith("--security-digits ")]
@@ -880,6 +895,8 @@ def run(program: PackedProgram, opts: dict, *, context_args=None, log=print) -> 
         # (packed_fideslib.cpp:1040-1042); node widths stay the program's
         program.slots = 65536
         args.update(CLASSICAL128, dnum=opts.get("security_digits", 4))
+    if opts.get("s2c_first") and program.slots != args.get("ring_dim", 65536) // 2:
+        raise ValueError("S2C-first requires full packing (program slots = ring dimension / 2)")
     cc, keys = build_context(program.slots, **args)
     audit = cc.SecurityAudit() if classical else None
     if classical and opts.get("result"):
@@ -909,7 +926,8 @@ def run(program: PackedProgram, opts: dict, *, context_args=None, log=print) -> 
     ev = PackedEvaluator(cc, keys, program.slots, bootstrap_passes=opts["bootstrap_passes"],
                          replicated_linear=not opts["direct_linear"],
                          trace_levels=opts["trace_levels"],
-                         client=client_step if client else None, log=log)
+                         client=client_step if client else None, log=log,
+                         s2c_first=opts.get("s2c_first", False))
     setup_s = time.perf_counter() - t_setup
     log(f"setup_seconds={setup_s}")
     t0 = time.perf_counter()
@@ -961,6 +979,7 @@ def run(program: PackedProgram, opts: dict, *, context_args=None, log=print) -> 
         "routing_method": "radix8-direct32" if ev.replicated_linear else "direct",
         "refresh_policy": "baseline",
         "refresh_ceiling": ev.refresh_ceiling,
+        "s2c_first": ev.s2c_first,
         "bootstrap_passes": ev.bootstrap_passes,
         "accepted_options": opts.get("accepted", []),
         "max_abs_error_vs_polynomial": poly_err,

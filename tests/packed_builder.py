@@ -242,8 +242,13 @@ class SlotContext:
             out = self._rot(SlotCt(out), bstep * stride).z + inner
         ct._assign(SlotCt(out, lv, 2))
 
-    def EvalBootstrapSetup(self, budget, dims, slots):  # noqa: N802
-        pass
+    def EvalBootstrapSetup(self, budget, dims, slots, correction=0, precompute=True, *,  # noqa: N802
+                           s2c_first=False, real_slots=False):
+        # S2C-first moves the SlotToCoeff levels from the output to the input
+        self.boot_s2c_levels = int(budget[1]) if s2c_first else 0
+
+    def GetBootstrapInputCeiling(self):  # noqa: N802
+        return self.L - 2 - getattr(self, "boot_s2c_levels", 0)
 
     def EvalBootstrapKeyGen(self, sk, slots):  # noqa: N802
         pass
@@ -257,12 +262,12 @@ class SlotContext:
 
     def EvalBootstrap(self, ct, passes=1, precision=0, *, scale=1.0):  # noqa: N802
         ct = self._rescaled(ct)
-        assert ct.level <= self.L - 2, "bootstrap input too deep"
+        assert ct.level <= self.GetBootstrapInputCeiling(), "bootstrap input too deep"
         # the refresh bound must bring every slot into [-1, 1]
         top = np.max(np.abs(ct.z)) / scale
         assert top <= 1.0 + 1e-9, f"bootstrap input {top}"
         self.bootstraps += passes
-        return SlotCt(ct.z, self.boot_depth, 1)
+        return SlotCt(ct.z, self.boot_depth - getattr(self, "boot_s2c_levels", 0), 1)
 
 
 class _SlotPlain:

@@ -305,3 +305,53 @@ def test_group_factors(total, groups):
     assert all(math.isclose(a, b, rel_tol=1e-14) for a, b in zip(even, split))
     with pytest.raises(ValueError):
         B.CKKSBootstrapper.group_factors(0.0, groups)
+
+
+@pytest.mark.parametrize("log_n,budget", [(8, (2, 2)), (10, (3, 3)), (11, (2, 4))])
+@pytest.mark.parametrize("real", [False, True])
+def test_s2c_first_bootstrap_circuit_on_slots(log_n, budget, real):
+    """S2C-first ordering: SlotToCoeff on the input, ModRaise, CoeffToSlot,
+    EvalMod.  The output holds the message (complex, or with real_slots
+    the real message from one EvalMod) at depth len(c2s) + sine depth; the
+    input ceiling is the SlotToCoeff levels lower; the residual pass's
+    pre / post constants ride through as in the ordinary order."""
+    cc = SimCC(log_n, L=40)
+    cfg = B.BootstrapConfig.for_ring(1 << log_n, budget)
+    cc.ibound = int(cfg.sine.K) // 2
+    boot = B.CKKSBootstrapper(cc, cfg, s2c_first=True, real_slots=real)
+    plain = B.CKKSBootstrapper(cc, cfg)
+    assert boot.depth() == plain.depth() - budget[1]
+    assert boot.input_ceiling() == plain.input_ceiling() - budget[1] == 40 - 2 - budget[1]
+    n = cc.N // 2
+    rng = np.random.default_rng(log_n)
+    m = rng.uniform(-1, 1, n) + (0 if real else 1j * rng.uniform(-1, 1, n))
+    out = boot.bootstrap(SimCt(m, 5))
+    assert out.level == boot.depth()
+    assert np.max(np.abs(out.z - m)) < 1e-5
+    if real:
+        assert np.max(np.abs(out.z.imag)) < 1e-12
+    # a residual-style pass: slots scaled up by 2^12 on the way in, down on the way out
+    r = 1e-4 * m
+    out = boot.bootstrap(SimCt(r, 5), pre=2.0 ** 12, post=2.0 ** -12)
+    assert np.max(np.abs(out.z - r)) < 1e-9
+    with pytest.raises(ValueError, match="level"):
+        boot.bootstrap(SimCt(m, boot.input_ceiling() + 1))
+    with pytest.raises(ValueError, match="full packing"):
+        B.CKKSBootstrapper(cc, cfg, n // 2, s2c_first=True)
+
+
+def test_s2c_first_residual_pass_with_a_small_bound():
+    """A residual pass for a small refresh bound (pre = 2^12 / 2^-10): pre
+    rides on the scale-down constant, not on the SlotToCoeff diagonals,
+    whose constants stay those of every other bound."""
+    cc = SimCC(10, L=40)
+    cfg = B.BootstrapConfig.for_ring(1 << 10, (2, 2))
+    cc.ibound = int(cfg.sine.K) // 2
+    boot = B.CKKSBootstrapper(cc, cfg, s2c_first=True, real_slots=True)
+    m = np.random.default_rng(3).uniform(-1, 1, 512) * 2.0 ** -22
+    out = boot.bootstrap(SimCt(m, 5), pre=2.0 ** 22, post=2.0 ** -22)
+    assert np.max(np.abs(out.z - m)) < 2.0 ** -40
+    keys = {k for k in boot._pts._d if k[0] == "s2c_first"}
+    assert keys
+    boot.bootstrap(SimCt(m * 2.0 ** 8, 5), pre=2.0 ** 14, post=2.0 ** -14)
+    assert {k for k in boot._pts._d if k[0] == "s2c_first"} == keys

@@ -159,3 +159,63 @@ def test_sparse_secret_bootstrap():
     err2 = np.max(np.abs(dec(cc, keys, out2) - x))
     print(f"sparse-secret two-pass bootstrap error 2^{np.log2(err2):.1f}", flush=True)
     assert err2 < TWO_PASS_TOL
+
+
+@pytest.mark.parametrize("real", [False, True])
+def test_s2c_first_bootstrap(real):
+    """S2C-first ordering (SlotToCoeff on the input, then ModRaise,
+    CoeffToSlot, EvalMod): the output keeps the SlotToCoeff levels, the
+    input must sit that many levels lower, and the refreshed slots meet
+    the one- and two-pass tolerances (complex slots, or real slots with
+    one EvalMod).  With real_slots the imaginary part of the input is
+    dropped and the output projected onto its real part: its imaginary
+    parts hold only the projection's key-switch noise (below 2^-30)."""
+    cc, keys = build_toy_context(ring_dimension=1 << LOG_N, batch=SLOTS, depth=44,
+                                 scale_bits=59, first_mod_bits=60, seed=11)
+    cc.EvalBootstrapSetup([3, 3], [0, 0], SLOTS, s2c_first=True, real_slots=real)
+    cc.EvalBootstrapKeyGen(keys.secretKey, SLOTS)
+    L = len(cc.GetModuli()[0])
+    assert cc.GetBootstrapInputCeiling() == L - 2 - 3
+    rng = np.random.default_rng(12)
+    z = rng.uniform(-1, 1, SLOTS) + (0 if real else 1j * rng.uniform(-1, 1, SLOTS))
+    ct = enc_at(cc, keys, z, L - 5)
+    for passes, tol in ((1, ONE_PASS_TOL), (2, TWO_PASS_TOL)):
+        out = cc.EvalBootstrap(ct, passes, 15)
+        assert out.GetLevel() == cc.GetBootstrapDepth()
+        got = dec(cc, keys, out, complex_=True)
+        err = np.max(np.abs((got.real if real else got) - z))
+        print(f"S2C-first ({'real' if real else 'complex'}) {passes} pass(es): "
+              f"error 2^{np.log2(err):.1f}, imaginary 2^{np.log2(np.max(np.abs(got.imag))):.1f}",
+              flush=True)
+        assert err < tol
+        if real:
+            assert np.max(np.abs(got.imag)) < 2.0 ** -30
+    with pytest.raises(ValueError, match="level"):
+        cc.EvalBootstrap(enc_at(cc, keys, z, L - 4))
+    with pytest.raises(ValueError, match="full packing"):
+        cc.EvalBootstrapSetup([3, 3], [0, 0], SLOTS // 2, s2c_first=True)
+
+
+@pytest.mark.parametrize("s2c_first", [False, True])
+def test_bootstrap_at_ring_2_16(s2c_first):
+    """Full packing at N = 2^16 (32768 slots, the decoder's ring) with the
+    uniform-ternary secret (K = 512, degree 89, 6 double angles), both
+    orderings, level budget (4, 4): one pass within 2^-11, two passes
+    within 2^-22 (measured about 2^-12.9 and 2^-25)."""
+    n = 1 << 16
+    cc, keys = build_toy_context(ring_dimension=n, batch=n // 2, depth=44, scale_bits=59,
+                                 first_mod_bits=60, seed=16)
+    cc.EvalBootstrapSetup([4, 4], [0, 0], n // 2, s2c_first=s2c_first, real_slots=s2c_first)
+    cc.EvalBootstrapKeyGen(keys.secretKey, n // 2)
+    x = np.random.default_rng(17).uniform(-1, 1, n // 2)
+    ct = cc.Encrypt(keys.publicKey, cc.MakeCKKSPackedPlaintext(list(x)))
+    ct.SetLevel(cc.GetBootstrapInputCeiling())
+    for passes, tol in ((1, 2.0 ** -11), (2, 2.0 ** -22)):
+        out = cc.EvalBootstrap(ct, passes, 12)
+        pt = cc.Decrypt(out, keys.secretKey)
+        pt.SetLength(n // 2)
+        err = np.max(np.abs(np.asarray(pt.GetRealPackedValue()) - x))
+        print(f"N=2^16 {'S2C-first' if s2c_first else 'ordinary'} {passes} pass(es): "
+              f"level {out.GetLevel()}, error 2^{np.log2(err):.1f}", flush=True)
+        assert out.GetLevel() == cc.GetBootstrapDepth()
+        assert err < tol

@@ -140,3 +140,31 @@ def test_command_line_classical128(tmp_path):
     assert (audit["qp_bits"], audit["hybrid_digits"], audit["guideline_max_qp_bits"]) == \
         (3376, 4, 3523)
     assert report["logical_refreshes"] >= 1
+
+
+def test_command_line_s2c_first(tmp_path):
+    """--planned-refresh --batch-refresh --s2c-first (packed_fideslib.cpp:
+    1013-1017, 1084-1086, 1131-1134): full packing at N = 2^16, refreshes by
+    the SlotToCoeff-first bootstrap under a ceiling four levels lower, and
+    the outputs within tolerance; a program that is not fully packed is
+    refused."""
+    rng = np.random.default_rng(13)
+    b = ProgramBuilder(32768, bound=4.0)
+    v = b.input(rng.uniform(0.5, 1.5, 64))
+    w = b.input(np.ones(64))
+    for _ in range(30):
+        v = b.mulp(b.mul(v, w), np.ones(64))
+    b.output(v)
+    prog, res = tmp_path / "program.txt", tmp_path / "native.json"
+    prog.write_text(b.text())
+    flags = ["--planned-refresh", "--batch-refresh", "--s2c-first"]
+    rc = P.main([str(prog), str(res), str(TOL), str(TOL)] + flags)
+    report = json.loads(res.read_text())
+    print(f"S2C-first packed: eval {report['eval_seconds']:.2f}s, {report['bootstraps']} "
+          f"bootstraps, error {report['max_abs_error_vs_polynomial']:.2e}", flush=True)
+    assert rc == 0 and report["passed"] is True and report["s2c_first"] is True
+    assert report["refresh_ceiling"] == 45 - 3 - 4 and report["logical_refreshes"] >= 1
+    small = ProgramBuilder(1024)
+    small.output(small.input(np.ones(4)))
+    prog.write_text(small.text())
+    assert P.main([str(prog), str(res), str(TOL), str(TOL)] + flags) == 2

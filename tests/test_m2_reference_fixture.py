@@ -378,3 +378,17 @@ def test_autoregressive_command_line_refusals(tmp_path):
     assert D.main([AR, res, "--autoregressive-client-loop", "--layers", "1"]) == 2
     assert D.main([AR, res, "--autoregressive-client-loop", "--tokens", "4"]) == 2
     assert D.main([FIX, res, "--tokens", "3"]) == 2
+
+
+def test_s2c_first_decoder_circuit_on_slots(chain):
+    """With S2C-first refreshes the ceiling is the SlotToCoeff levels lower
+    and refreshed values come back that much higher; the decoder's level
+    planning still reaches the exporter's circuit."""
+    from fhemamba_amd.mamba2_decode import EncryptedMamba2Decoder
+    from packed_builder import SlotContext, SlotKeys
+    dec = EncryptedMamba2Decoder(SlotContext(1024), SlotKeys(), chain, s2c_first=True)
+    assert dec.ev.refresh_ceiling == 45 - 3 - 4
+    states = dec.initial_states()
+    for k, e in enumerate(chain.input_embeddings):
+        ct, states = dec.step(e, states)
+        assert _rel(dec.decrypt(ct), chain.expected_poly_final[k]) < 1e-5, k

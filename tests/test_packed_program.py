@@ -250,9 +250,23 @@ def test_command_line_options():
                 ["p", "r", "1", "1", "--security-digits", "3"],
                 ["p", "r", "1", "1", "--security", "128-classic", "--security-digits", "0"],
                 ["p", "r", "1", "1", "--security", "128-classic", "--security-digits", "17"],
-                ["p", "r", "1", "1", "--s2c-first"]):
+                ["p", "r", "1", "1", "--s2c-first"],
+                ["p", "r", "1", "1", "--s2c-first", "--batch-refresh"],
+                ["p", "r", "1", "1", "--batch-refresh", "--planned-refresh",
+                 "--bootstrap-passes", "1"],
+                ["p", "r", "1", "1", "--gpu-dual-ring"]):
         with pytest.raises(ValueError):
             P.parse_args(bad)
+
+
+def test_s2c_first_options():
+    """--s2c-first needs planned two-pass batch refresh
+    (packed_fideslib.cpp:1013-1017); it is recorded as its own option."""
+    o = P.parse_args(["p", "r", "1e-3", "1e-2", "--planned-refresh", "--batch-refresh",
+                      "--s2c-first"])
+    assert o["s2c_first"] and o["accepted"] == ["--planned-refresh", "--batch-refresh"]
+    with pytest.raises(ValueError, match="batch refresh"):
+        P.parse_args(["p", "r", "1e-3", "1e-2", "--planned-refresh", "--s2c-first"])
 
 
 def test_classical128_options():
