@@ -490,6 +490,18 @@ int fhe_key_load(fhe_context* ctx, const uint64_t* host, fhe_key** out) {
   });
 }
 
+int fhe_key_download(const fhe_key* k, uint64_t* host) {
+  return guard([&] {
+    need(k && host, "null argument");
+    fhe::Context& c = *k->c;
+    fhe::Scratch t(c, k->bytes / 8);
+    fhe::key_from_montgomery(c, t.p, k->data);
+    fhe::hip_check(hipMemcpyAsync(host, t.p, k->bytes, hipMemcpyDeviceToHost, c.stream),
+                   "key download");
+    fhe::hip_check(hipStreamSynchronize(c.stream), "key sync");
+  });
+}
+
 int fhe_key_destroy(fhe_key* k) {
   return guard([&] {
     if (!k) return;

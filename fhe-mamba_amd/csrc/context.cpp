@@ -226,6 +226,11 @@ Context::Context(uint32_t log_n_, const uint64_t* q, uint32_t num_q, const uint6
   for (uint32_t i = 0; i < nm; ++i)
     keyfac[i] = i < L ? host_mulmod(pinv_host[i], hconst[i].r2, mods[i]) : hconst[i].r2;
   d_keyfac = upload(keyfac);
+  // the inverse map, device key -> standard form: a Montgomery product by
+  // P mod q_i undoes P^-1 R on the Q limbs, by 1 undoes R on the P limbs
+  std::vector<uint64_t> keyfac_out(nm, 1);
+  for (uint32_t i = 0; i < L; ++i) keyfac_out[i] = host_invmod(pinv_host[i], mods[i]);
+  d_keyfac_out = upload(keyfac_out);
 
   std::vector<uint64_t> garner((size_t)L * L * 2, 0);
   for (uint32_t i = 0; i < L; ++i)
@@ -254,6 +259,7 @@ Context::~Context() {
   hipFree(d_rescale);
   hipFree(d_pinv_q);
   hipFree(d_keyfac);
+  hipFree(d_keyfac_out);
   hipFree(d_garner);
   for (auto& kv : fft_tables) {
     hipFree(kv.second.first);

@@ -142,6 +142,7 @@ struct Context {
   // or 2^128 (P limbs) mod the limb's modulus: Montgomery form with P^-1
   // folded into the Q limbs, so the key inner product yields ext * P^-1.
   uint64_t* d_keyfac = nullptr;      // [L+K]
+  uint64_t* d_keyfac_out = nullptr;  // [L+K]: P mod q_i (Q limbs), 1 (P limbs)
 
   // Garner CRT inverses g[i][j] = (q_j^-1 mod q_i, Shoup) for j < i (decode).
   uint64_t* d_garner = nullptr;      // [L][L][2]

@@ -196,6 +196,16 @@ __global__ void __launch_bounds__(TPB)
   key[o] = mont_mul(key[o], fac[i], m.q, m.qinv_neg);
 }
 
+// Device key -> standard form (the inverse of k_to_mont), into `out`.
+__global__ void __launch_bounds__(TPB)
+    k_from_mont(uint64_t* out, const uint64_t* key, const ModConst* mc, const uint64_t* fac,
+                uint32_t n, uint32_t nm) {
+  const uint32_t i = blockIdx.y;
+  const ModConst m = mc[i];
+  const size_t o = ((size_t)blockIdx.z * nm + i) * n + (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  out[o] = mont_mul(key[o], fac[i], m.q, m.qinv_neg);
+}
+
 // Terms per REDC so that terms * max_q < 2^64.
 uint32_t redc_chunk(const Context& c, const std::vector<uint32_t>& idx) {
   uint64_t mx = 1;
@@ -501,6 +511,11 @@ void automorph(Context& c, uint64_t* out, const uint64_t* in, uint32_t npoly, ui
 void key_to_montgomery(Context& c, uint64_t* key) {
   const uint32_t tpb = tpb_for(c, 1);
   FHE_LAUNCH(c, "k_to_mont", k_to_mont, dim3(c.n / tpb, c.L + c.K, c.dnum * 2), dim3(tpb), 0, key, c.d_const, c.d_keyfac, c.n, c.L + c.K);
+}
+
+void key_from_montgomery(Context& c, uint64_t* out, const uint64_t* key) {
+  const uint32_t tpb = tpb_for(c, 1);
+  FHE_LAUNCH(c, "k_from_mont", k_from_mont, dim3(c.n / tpb, c.L + c.K, c.dnum * 2), dim3(tpb), 0, out, key, c.d_const, c.d_keyfac_out, c.n, c.L + c.K);
 }
 
 }  // namespace fhe

@@ -107,6 +107,8 @@ void automorph(Context& c, uint64_t* out, const uint64_t* in, uint32_t npoly, ui
                uint32_t galois);
 // Convert a standard-form key [dnum][2][L+K][N] to Montgomery form in place.
 void key_to_montgomery(Context& c, uint64_t* key);
+// The inverse: a device key back to standard form, written to `out`.
+void key_from_montgomery(Context& c, uint64_t* out, const uint64_t* key);
 
 // ---- encoding (encode.hip) ----
 // Returns false if a scaled coefficient does not fit.

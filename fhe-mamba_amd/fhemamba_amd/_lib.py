@@ -69,6 +69,7 @@ SIGNATURES = {
     "fhe_rescale": [_p, _p],
     "fhe_tensor": [_p, _p, _p],
     "fhe_key_load": [_p, _p, _pp],
+    "fhe_key_download": [_p, _p],
     "fhe_key_destroy": [_p],
     "fhe_keyswitch": [_p, _p, _p],
     "fhe_relinearize": [_p, _p, _p],

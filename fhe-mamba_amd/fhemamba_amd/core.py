@@ -396,6 +396,13 @@ class Key:
             raise ValueError("key is closed")
         return self._h
 
+    def numpy(self) -> np.ndarray:
+        """The key's residues [dnum][2][L+K][N] in the form load_key takes."""
+        c = self.ctx
+        out = np.empty((c.dnum, 2, c.L + c.K, c.n), dtype=np.uint64)
+        call("fhe_key_download", self.handle, _ptr(out))
+        return out
+
     def close(self):
         if getattr(self, "_h", None):
             call("fhe_key_destroy", self._h)

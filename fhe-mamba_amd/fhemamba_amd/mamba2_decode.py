@@ -418,7 +418,11 @@ class EncryptedMamba2Decoder:
     def step(self, embedding, states: list):
         """One token: encrypt the embedding (client side), run every layer,
         final RMSNorm; returns (final ciphertext, new states)."""
-        h = self.ev.encrypt(np.asarray(embedding, dtype=np.float64))
+        return self.step_ct(self.ev.encrypt(np.asarray(embedding, dtype=np.float64)), states)
+
+    def step_ct(self, h, states: list):
+        """One token from an encrypted embedding (a server that holds no
+        secret key)."""
         new_states = []
         for li, st in enumerate(states):
             t0 = time.perf_counter()
@@ -485,10 +489,46 @@ def token_loop(dec: EncryptedMamba2Decoder, chain: ChainPayload, n_tok: int, ar=
 SECRET_KEY_DISTS = {"sparse-ternary": "SPARSE_TERNARY", "uniform-ternary": "UNIFORM_TERNARY"}
 
 
+def _decode_setup(payload_dir, security, secret_key_dist, ring_dim):
+    from .mamba2_payload import read_chain_payload
+    from .packed import CLASSICAL128
+    if security not in ("not-set", "128-classic"):
+        raise ValueError("security must be not-set or 128-classic")
+    classical = security == "128-classic"
+    if secret_key_dist is None:
+        secret_key_dist = "uniform-ternary" if classical else "sparse-ternary"
+    if secret_key_dist not in SECRET_KEY_DISTS:
+        raise ValueError(f"secret key distribution must be one of {sorted(SECRET_KEY_DISTS)}")
+    if ring_dim and (classical or ring_dim < 4096 or ring_dim & (ring_dim - 1)):
+        raise ValueError("ring_dim: a power of two >= 4096, and only with security not-set")
+    chain = read_chain_payload(payload_dir)
+    extra = dict(CLASSICAL128) if classical else ({"ring_dim": ring_dim} if ring_dim else {})
+    slots = extra.get("ring_dim", 65536) // 2
+    return chain, classical, secret_key_dist, slots, extra
+
+
+def _truncate(chain, layers: int) -> None:
+    if layers:
+        from .mamba2_payload import decode_tokens
+        if not 1 <= layers <= chain.n_layers:
+            raise ValueError("layers must be in 1..n_layers")
+        chain.layers = chain.layers[:layers]
+        chain.n_layers = layers
+        chain.expected_final, _ = decode_tokens(chain, chain.input_embeddings, False)
+        chain.expected_poly_final, _ = decode_tokens(chain, chain.input_embeddings, True)
+
+
+def _build(slots, seed, secret_key_dist, extra):
+    from . import ckks
+    from .packed import build_context
+    return build_context(slots, seed=seed, secret_dist=getattr(
+        ckks.SecretKeyDist, SECRET_KEY_DISTS[secret_key_dist]), **extra)
+
+
 def run_payload(payload_dir: str, *, tokens: int = 0, bootstrap_passes: int = 2, seed=None,
                 secret_key_dist: str | None = None, security: str = "not-set",
                 layers: int = 0, autoregressive: bool = False, s2c_first: bool = True,
-                log=print) -> dict:
+                ring_dim: int = 0, log=print) -> dict:
     """Decode the payload's test embeddings in turn (carried state) and
     compare the decrypted outputs with its polynomial-circuit and exact
     references; returns the report.
@@ -516,18 +556,10 @@ def run_payload(payload_dir: str, *, tokens: int = 0, bootstrap_passes: int = 2,
     s2c_first (default): refresh with the SlotToCoeff-first bootstrap (the
     packed executor's --s2c-first circuit; real slots, one EvalMod), about
     40% less bootstrap time than the ordinary order at the same usable
-    level interval and precision; False: the ordinary order."""
-    from . import ckks
-    from .mamba2_payload import read_chain_payload
-    from .packed import CLASSICAL128, build_context
-    if security not in ("not-set", "128-classic"):
-        raise ValueError("security must be not-set or 128-classic")
-    classical = security == "128-classic"
-    if secret_key_dist is None:
-        secret_key_dist = "uniform-ternary" if classical else "sparse-ternary"
-    if secret_key_dist not in SECRET_KEY_DISTS:
-        raise ValueError(f"secret key distribution must be one of {sorted(SECRET_KEY_DISTS)}")
-    chain = read_chain_payload(payload_dir)
+    level interval and precision; False: the ordinary order.  ring_dim
+    (not-set only; default 2^16) picks a smaller ring for small payloads."""
+    chain, classical, secret_key_dist, slots, extra = _decode_setup(
+        payload_dir, security, secret_key_dist, ring_dim)
     ar = chain.autoregressive if autoregressive else None
     if autoregressive:
         if ar is None:
@@ -537,22 +569,12 @@ def run_payload(payload_dir: str, *, tokens: int = 0, bootstrap_passes: int = 2,
         if tokens > ar.server_evaluations:
             raise ValueError(f"tokens exceeds the autoregressive server_evaluations "
                              f"({ar.server_evaluations})")
-    if layers:
-        if not 1 <= layers <= chain.n_layers:
-            raise ValueError("layers must be in 1..n_layers")
-        chain.layers = chain.layers[:layers]
-        chain.n_layers = layers
-        from .mamba2_payload import decode_tokens
-        chain.expected_final, _ = decode_tokens(chain, chain.input_embeddings, False)
-        chain.expected_poly_final, _ = decode_tokens(chain, chain.input_embeddings, True)
+    _truncate(chain, layers)
     n_tok = tokens or (ar.server_evaluations if ar else chain.n_test_tokens)
     if ar is None and n_tok > chain.n_test_tokens:
         raise ValueError("tokens exceeds the payload's n_test_tokens")
-    slots = 65536 if classical else 32768
     t0 = time.perf_counter()
-    extra = dict(CLASSICAL128) if classical else {}
-    cc, keys = build_context(slots, seed=seed, secret_dist=getattr(
-        ckks.SecretKeyDist, SECRET_KEY_DISTS[secret_key_dist]), **extra)
+    cc, keys = _build(slots, seed, secret_key_dist, extra)
     audit = cc.SecurityAudit() if classical else None
     dec = EncryptedMamba2Decoder(cc, keys, chain, bootstrap_passes=bootstrap_passes, log=log,
                                  s2c_first=s2c_first)
@@ -619,14 +641,46 @@ def main(argv=None) -> int:
                     help="greedy client-in-loop decoding over the payload's assets")
     ap.add_argument("--ordinary-bootstrap", action="store_true",
                     help="refresh with the ordinary bootstrap order instead of SlotToCoeff-first")
+    ap.add_argument("--process-role", default="inline",
+                    choices=("inline", "client-init", "server-eval", "client-decrypt"),
+                    help="process-separated decode through --handoff-dir (fhemamba_amd.handoff)")
+    ap.add_argument("--handoff-dir", default="")
+    ap.add_argument("--ring-dim", type=int, default=0,
+                    help="ring dimension under security not-set (default 65536)")
     args = ap.parse_args(sys.argv[1:] if argv is None else argv)
+    if args.process_role != "inline":
+        from . import handoff as H
+        try:
+            if not args.handoff_dir:
+                raise ValueError("non-inline process-role requires --handoff-dir")
+            if args.autoregressive_client_loop:
+                raise ValueError("process-separated autoregressive loop is not implemented")
+            if args.process_role == "client-init":
+                report = H.client_init(
+                    args.payload, args.handoff_dir, tokens=args.tokens,
+                    bootstrap_passes=args.bootstrap_passes,
+                    secret_key_dist=args.secret_key_dist, security=args.security,
+                    layers=args.layers, s2c_first=not args.ordinary_bootstrap,
+                    ring_dim=args.ring_dim)
+            elif args.process_role == "server-eval":
+                report = H.server_eval(args.payload, args.handoff_dir, tokens=args.tokens,
+                                       layers=args.layers)
+            else:
+                report = H.client_decrypt(args.payload, args.handoff_dir, tokens=args.tokens,
+                                          layers=args.layers, tolerance=args.tolerance)
+        except Exception as exc:  # noqa: BLE001 - reported as exit code 2
+            print(exc, file=sys.stderr)
+            return 2
+        with open(args.result, "w") as f:
+            json.dump(report, f)
+        return 0 if report["passed"] else 1
     try:
         report = run_payload(args.payload, tokens=args.tokens,
                              bootstrap_passes=args.bootstrap_passes,
                              secret_key_dist=args.secret_key_dist, security=args.security,
                              layers=args.layers,
                              autoregressive=args.autoregressive_client_loop,
-                             s2c_first=not args.ordinary_bootstrap)
+                             s2c_first=not args.ordinary_bootstrap, ring_dim=args.ring_dim)
     except Exception as exc:  # noqa: BLE001 - reported as exit code 2
         print(exc, file=sys.stderr)
         return 2

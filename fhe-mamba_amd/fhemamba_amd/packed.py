@@ -365,10 +365,16 @@ class PackedEvaluator:
         self.operation_stats: dict = {}
         self.client_tokens: list = []
         self.client_margins: list = []
-        t0 = time.perf_counter()
-        cc.EvalBootstrapKeyGen(keys.secretKey, self.slots)
-        self.stats["keygen_seconds"] += time.perf_counter() - t0
-        self._rot_keys.update(int(k) % self.slots for k in cc._bootstrapper().rotation_indices())
+        boot_rot = [int(k) % self.slots for k in cc._bootstrapper().rotation_indices()]
+        if getattr(keys, "secretKey", None) is None:
+            # a server without the secret: every key must have been loaded
+            if not cc.HasRotationKeys(boot_rot) or not cc.HasConjugationKey():
+                raise ValueError("the loaded key set lacks the bootstrapping keys")
+        else:
+            t0 = time.perf_counter()
+            cc.EvalBootstrapKeyGen(keys.secretKey, self.slots)
+            self.stats["keygen_seconds"] += time.perf_counter() - t0
+        self._rot_keys.update(boot_rot)
 
     # ------------------------------------------------------------- primitives
     def _level(self, ct) -> int:
@@ -385,7 +391,11 @@ class PackedEvaluator:
 
     def _ensure_keys(self, offsets):
         need = sorted({int(o) % self.slots for o in offsets} - {0} - self._rot_keys)
-        if need:
+        if need and getattr(self.keys, "secretKey", None) is None:
+            if not self.cc.HasRotationKeys(need):
+                raise KeyError(f"rotation keys for offsets {need} are not in the loaded key set")
+            self._rot_keys.update(need)
+        elif need:
             t0 = time.perf_counter()
             self.cc.EvalRotateKeyGen(self.keys.secretKey, need)
             self.stats["keygen_seconds"] += time.perf_counter() - t0

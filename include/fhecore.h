@@ -148,6 +148,12 @@ int fhe_tensor(fhe_poly *out3, const fhe_poly *a, const fhe_poly *b);
  * EvalMultKeyGen / EvalRotateKeyGen + LoadContext key upload
  * (packed_fideslib.cpp:1080-1083). */
 int fhe_key_load(fhe_context *ctx, const uint64_t *host, fhe_key **out);
+/* The inverse of fhe_key_load: the key's residues [dnum][2][L+K][N] in the
+ * same standard evaluation form, into `host` (for serialising the
+ * evaluation keys of the client/server handoff: SerializeEvalMultKey /
+ * SerializeEvalAutomorphismKey, stage1_mamba2_decode_fideslib.cpp:
+ * 1466-1477). */
+int fhe_key_download(const fhe_key *k, uint64_t *host);
 int fhe_key_destroy(fhe_key *k);
 
 /* ---- key switching ----------------------------------------------------
