@@ -45,8 +45,16 @@ HBM_PEAK = 8.0e12  # B/s, MI355X HBM3E
 # hash of the kernel sources they were measured on.  A build from other
 # sources reports traffic as null.
 MEASURED_TRAFFIC = {
-    "csrc_sha16": "",
-    "kernels": {},
+    "csrc_sha16": "9b99b41750e00609",
+    "kernels": {
+        # 30-rotation batch launches of the rotation step
+        "ntt_fwd_blocks_moddown": 3_096_560_025 + 757_550_080,
+        "k_moddown_mid": 253_459_661 + 760_442_163,
+        "ntt_inv_blocks_ksk": 776_156_365 + 251_658_240,
+        # NTT batch (64 ciphertexts x 2 polys x 24 limbs): one pass, and the MAC
+        "ntt_pass": 1_636_318_618 + 1_610_612_736,
+        "k_mac": 2_416_044_646 + 25_165_824,
+    },
 }
 
 
@@ -619,6 +627,10 @@ def main() -> int:
         out["ntt"]["workload"] = ("64 ciphertexts x 2 polys x 24 limbs, N=2^16: forward NTT, "
                                   "MAC over 64 plaintexts, inverse NTT")
         out["ntt"]["frac"] = ntt["ntt_gbps"] * 1e9 / HBM_PEAK
+        # counter-measured HBM bytes of one two-pass NTT launch over the
+        # batch (each pass reads and writes every limb) and of the MAC
+        out["ntt"]["traffic_per_pass"] = measured_traffic("ntt_pass")
+        out["ntt"]["mac_traffic"] = measured_traffic("k_mac")
     if not args.skip_ssm:
         log("ssm layer step workload")
         out["ssm_layer_step"] = run_ssm_step()
