@@ -745,44 +745,85 @@ int fhe_rotate_many(fhe_poly* const* outs, const fhe_poly* const* cts, const fhe
   });
 }
 
+static void linear_transform_checked(fhe_poly* out, const fhe_poly* ct,
+                                     const fhe_poly* const* pts, uint32_t count, uint32_t bstep,
+                                     const fhe_key* const* baby_keys,
+                                     const uint32_t* baby_galois, const fhe_key* const* giant_keys,
+                                     const uint32_t* giant_galois, uint32_t n_giant_keys) {
+  need(ct && pts, "null argument");
+  same_ctx(out, ct);
+  fhe::Context& c = *ct->c;
+  need(ct->npoly == 2 && ct->nlimb <= c.L, "linear transform needs a 2-poly ciphertext");
+  need(count >= 1 && bstep >= 1 && bstep <= fhe::MAC_TABLE,
+       "need count >= 1 and 1 <= bstep <= 64");
+  const uint32_t nq = ct->nlimb, giants = (count + bstep - 1) / bstep;
+  std::vector<const uint64_t*> pp(count, nullptr);
+  bool any = false;
+  for (uint32_t k = 0; k < count; ++k) {
+    if (!pts[k]) continue;
+    need(pts[k]->c == &c && pts[k]->npoly == 1 && pts[k]->nlimb >= nq,
+         "diagonal must be a one-poly plaintext with at least the ciphertext's limbs");
+    pp[k] = pts[k]->data;
+    any = true;
+  }
+  need(any, "linear transform has no nonzero diagonal");
+  const uint32_t nb = std::min(bstep, count);
+  std::vector<const uint64_t*> bk(nb, nullptr);
+  std::vector<uint32_t> bg(nb, 1);
+  for (uint32_t b = 0; b < nb; ++b) {
+    if (!baby_keys || !baby_keys[b]) continue;
+    need(baby_galois != nullptr, "null argument");
+    check_key(ct, baby_keys[b]);
+    need((baby_galois[b] & 1) && baby_galois[b] < 2 * c.n, "bad Galois element");
+    bk[b] = baby_keys[b]->data;
+    bg[b] = baby_galois[b];
+  }
+  std::vector<const uint64_t*> gk;
+  std::vector<uint32_t> gg;
+  if (giants > 1) {
+    need(n_giant_keys == 1 || n_giant_keys == giants - 1,
+         "one giant-step key, or one per giant step");
+    need(giant_keys && giant_galois, "giant-step key required when count > bstep");
+    for (uint32_t g = 0; g < n_giant_keys; ++g) {
+      need(giant_keys[g] != nullptr, "giant-step key required when count > bstep");
+      check_key(ct, giant_keys[g]);
+      need((giant_galois[g] & 1) && giant_galois[g] < 2 * c.n, "bad Galois element");
+      gk.push_back(giant_keys[g]->data);
+      gg.push_back(giant_galois[g]);
+    }
+  }
+  prepare_out(out, 2, nq);
+  fhe::linear_transform(c, out->data, ct->data, nq, pp.data(), count, bstep, bk.data(),
+                        bg.data(), gk.data(), gg.data(), giants > 1 ? n_giant_keys : 0);
+}
+
 int fhe_linear_transform(fhe_poly* out, const fhe_poly* ct, const fhe_poly* const* pts,
                          uint32_t count, uint32_t bstep, const fhe_key* const* baby_keys,
                          const uint32_t* baby_galois, const fhe_key* giant_key,
                          uint32_t giant_galois) {
   return guard([&] {
-    need(ct && pts && (bstep <= 1 || (baby_keys && baby_galois)), "null argument");
-    same_ctx(out, ct);
-    fhe::Context& c = *ct->c;
-    need(ct->npoly == 2 && ct->nlimb <= c.L, "linear transform needs a 2-poly ciphertext");
-    need(count >= 1 && bstep >= 1 && bstep <= fhe::MAC_TABLE,
-         "need count >= 1 and 1 <= bstep <= 64");
-    const uint32_t nq = ct->nlimb, giants = (count + bstep - 1) / bstep;
-    std::vector<const uint64_t*> pp(count, nullptr);
-    bool any = false;
-    for (uint32_t k = 0; k < count; ++k) {
-      if (!pts[k]) continue;
-      need(pts[k]->c == &c && pts[k]->npoly == 1 && pts[k]->nlimb >= nq,
-           "diagonal must be a one-poly plaintext with at least the ciphertext's limbs");
-      pp[k] = pts[k]->data;
-      any = true;
-    }
-    need(any, "linear transform has no nonzero diagonal");
+    need(bstep <= 1 || (baby_keys && baby_galois), "null argument");
     const uint32_t nb = std::min(bstep, count);
-    std::vector<const uint64_t*> bk(nb > 1 ? nb - 1 : 1, nullptr);
+    // baby b >= 1 of the hoisted form is baby_keys[b - 1] here; baby 0 is ct
+    std::vector<const fhe_key*> bk(std::max<uint32_t>(nb, 1), nullptr);
+    std::vector<uint32_t> bg(std::max<uint32_t>(nb, 1), 1);
     for (uint32_t b = 1; b < nb; ++b) {
-      if (!baby_keys[b - 1]) continue;
-      check_key(ct, baby_keys[b - 1]);
-      need((baby_galois[b - 1] & 1) && baby_galois[b - 1] < 2 * c.n, "bad Galois element");
-      bk[b - 1] = baby_keys[b - 1]->data;
+      bk[b] = baby_keys[b - 1];
+      bg[b] = baby_galois[b - 1];
     }
-    if (giants > 1) {
-      need(giant_key != nullptr, "giant-step key required when count > bstep");
-      check_key(ct, giant_key);
-      need((giant_galois & 1) && giant_galois < 2 * c.n, "bad Galois element");
-    }
-    prepare_out(out, 2, nq);
-    fhe::linear_transform(c, out->data, ct->data, nq, pp.data(), count, bstep, bk.data(),
-                          baby_galois, giants > 1 ? giant_key->data : nullptr, giant_galois);
+    linear_transform_checked(out, ct, pts, count, bstep, bk.data(), bg.data(), &giant_key,
+                             &giant_galois, 1);
+  });
+}
+
+int fhe_linear_transform_hoisted(fhe_poly* out, const fhe_poly* ct, const fhe_poly* const* pts,
+                                 uint32_t count, uint32_t bstep, const fhe_key* const* baby_keys,
+                                 const uint32_t* baby_galois, const fhe_key* const* giant_keys,
+                                 const uint32_t* giant_galois, uint32_t n_giant_keys) {
+  return guard([&] {
+    need(baby_keys && baby_galois, "null argument");
+    linear_transform_checked(out, ct, pts, count, bstep, baby_keys, baby_galois, giant_keys,
+                             giant_galois, n_giant_keys);
   });
 }
 

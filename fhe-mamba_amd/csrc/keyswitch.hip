@@ -446,37 +446,42 @@ void rotate_many(Context& c, uint64_t* const* outs, const uint64_t* const* cts, 
 void linear_transform(Context& c, uint64_t* out, const uint64_t* ct, uint32_t nq,
                       const uint64_t* const* pts, uint32_t count, uint32_t bstep,
                       const uint64_t* const* baby_keys, const uint32_t* baby_galois,
-                      const uint64_t* giant_key, uint32_t giant_galois) {
+                      const uint64_t* const* giant_keys, const uint32_t* giant_galois,
+                      uint32_t n_giant_keys) {
   if (count == 0 || bstep == 0) throw ArgError("linear transform: no diagonals");
   const size_t n = c.n, ne = nq + c.K, pl = 2 * (size_t)nq * n;
   const uint32_t giants = (count + bstep - 1) / bstep, nb = std::min(bstep, count);
-  if (giants > 1 && !giant_key) throw ArgError("linear transform: giant-step key missing");
+  const bool batched = giants > 1 && n_giant_keys == giants - 1;
+  if (giants > 1 && !batched && n_giant_keys != 1)
+    throw ArgError("linear transform: one giant-step key, or one per giant step");
+  for (uint32_t g = 0; g + 1 < giants && g < n_giant_keys; ++g)
+    if (!giant_keys[g]) throw ArgError("linear transform: giant-step key missing");
   std::vector<uint8_t> used(nb, 0);
   for (uint32_t k = 0; k < count; ++k)
     if (pts[k]) used[k % bstep] = 1;
-  // Babies rot_b(ct) for the b some diagonal uses, from one ModUp.
+  // Babies rot(ct) for the b some diagonal uses, all from one ModUp; baby 0
+  // is ct itself unless baby_keys[0] gives it an offset rotation.
   std::vector<const uint64_t*> baby(nb, nullptr);
-  baby[0] = ct;
-  Scratch babies(c, std::max<size_t>(1, (nb - 1) * pl));
+  Scratch babies(c, std::max<size_t>(1, nb * pl));
   Scratch dig(c, num_digits(c, nq) * ne * n);
   std::vector<const uint64_t*> keys;
   std::vector<KeySwitchOut> outs;
-  for (uint32_t b = 1; b < nb; ++b) {
+  for (uint32_t b = 0; b < nb; ++b) {
+    if (b == 0 && !baby_keys[0]) {
+      baby[0] = ct;
+      continue;
+    }
     if (!used[b]) continue;
-    if (!baby_keys[b - 1]) throw ArgError("linear transform: baby-step key missing");
-    uint64_t* dst = babies.p + (b - 1) * pl;
+    if (!baby_keys[b]) throw ArgError("linear transform: baby-step key missing");
+    uint64_t* dst = babies.p + b * pl;
     baby[b] = dst;
-    keys.push_back(baby_keys[b - 1]);
-    outs.push_back(KeySwitchOut{dst, ct, nullptr, baby_galois[b - 1]});
+    keys.push_back(baby_keys[b]);
+    outs.push_back(KeySwitchOut{dst, ct, nullptr, baby_galois[b]});
   }
   if (!keys.empty()) {
     modup(c, ct + (size_t)nq * n, nq, dig.p);
     keyswitch_hoisted(c, dig.p, nq, keys.data(), outs.data(), (uint32_t)keys.size());
   }
-  // Giant steps by Horner's rule: acc = inner_{G-1}; acc = inner_g + rot(acc).
-  Scratch acc0(c, pl), acc1(c, pl);
-  uint64_t* cur = acc0.p;
-  uint64_t* nxt = acc1.p;
   std::vector<const uint64_t*> xs, ws;
   auto inner = [&](uint32_t g, uint64_t* acc, bool accumulate) {
     xs.clear();
@@ -490,11 +495,31 @@ void linear_transform(Context& c, uint64_t* out, const uint64_t* ct, uint32_t nq
     }
     poly_mac_table(c, acc, xs.data(), ws.data(), (uint32_t)xs.size(), nq, accumulate);
   };
+  if (batched) {
+    // Every giant step's inner sum, then their rotations by g giant strides
+    // as one batch of independent key switches, then the sum.
+    Scratch in(c, giants * pl), rot(c, (giants - 1) * pl);
+    for (uint32_t g = 0; g < giants; ++g) inner(g, in.p + g * pl, false);
+    std::vector<uint64_t*> ro(giants - 1);
+    std::vector<const uint64_t*> ri(giants - 1);
+    for (uint32_t g = 1; g < giants; ++g) {
+      ro[g - 1] = rot.p + (g - 1) * pl;
+      ri[g - 1] = in.p + g * pl;
+    }
+    rotate_many(c, ro.data(), ri.data(), nq, giant_keys, giant_galois, giants - 1);
+    poly_binary(c, OP_ADD, out, in.p, rot.p, 2, nq);
+    for (uint32_t g = 2; g < giants; ++g) poly_binary(c, OP_ADD, out, out, ro[g - 1], 2, nq);
+    return;
+  }
+  // Giant steps by Horner's rule: acc = inner_{G-1}; acc = inner_g + rot(acc).
+  Scratch acc0(c, pl), acc1(c, pl);
+  uint64_t* cur = acc0.p;
+  uint64_t* nxt = acc1.p;
   inner(giants - 1, cur, false);
   for (int g = (int)giants - 2; g >= 0; --g) {
     modup(c, cur + (size_t)nq * n, nq, dig.p);
-    const KeySwitchOut ko{nxt, cur, nullptr, giant_galois};
-    keyswitch_batch(c, dig.p, nq, &giant_key, 1, &ko);
+    const KeySwitchOut ko{nxt, cur, nullptr, giant_galois[0]};
+    keyswitch_batch(c, dig.p, nq, &giant_keys[0], 1, &ko);
     inner((uint32_t)g, nxt, true);
     std::swap(cur, nxt);
   }

@@ -92,14 +92,19 @@ void rotate(Context& c, uint64_t* out, const uint64_t* ct, uint32_t nq, const ui
 void rotate_many(Context& c, uint64_t* const* outs, const uint64_t* const* cts, uint32_t nq,
                  const uint64_t* const* keys, const uint32_t* galois, uint32_t count);
 // Baby-step giant-step plaintext linear transform of ct [2][nq][N]:
-//   out = sum_{g < G} rot_giant^g( sum_{b < bstep} pts[g*bstep + b] (.) rot_b(ct) ),
-// G = ceil(count / bstep), rot_b by baby_keys[b - 1] (b >= 1; rot_0 = id, all
-// babies from one ModUp), the giant sum evaluated by Horner's rule with the
-// one giant key.  Null pts are skipped.  out may alias ct.
+//   out = sum_{g < G} rot_giant^g( sum_{b < bstep} pts[g*bstep + b] (.) baby_b ),
+// G = ceil(count / bstep), baby_b = ct rotated by baby_keys[b] (all babies
+// from one ModUp; baby_keys[0] null: baby_0 = ct, otherwise it rotates ct by
+// an offset that the other babies' keys include).  With one giant key
+// (n_giant_keys = 1) the giant sum runs by Horner's rule; with one key per
+// giant step (n_giant_keys = G - 1, giant_keys[g - 1] rotating by g giant
+// strides) the G - 1 rotations run as one batch of independent key
+// switches.  Null pts are skipped.  out may alias ct.
 void linear_transform(Context& c, uint64_t* out, const uint64_t* ct, uint32_t nq,
                       const uint64_t* const* pts, uint32_t count, uint32_t bstep,
                       const uint64_t* const* baby_keys, const uint32_t* baby_galois,
-                      const uint64_t* giant_key, uint32_t giant_galois);
+                      const uint64_t* const* giant_keys, const uint32_t* giant_galois,
+                      uint32_t n_giant_keys);
 // g^-1 mod 2N for an odd Galois element g < 2N.
 uint32_t galois_inverse(uint32_t g, uint32_t n);
 // Galois permutation X -> X^galois of evaluation-form limbs.

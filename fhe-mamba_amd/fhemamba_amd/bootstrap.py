@@ -45,6 +45,7 @@ import numpy as np
 
 from .ckks_probes import cheb_ps_depth, chebyshev_ps
 from .ptcache import PlaintextCache
+from .rotation import bsgs_rotations
 
 Diag = dict  # rotation offset -> complex diagonal vector
 
@@ -160,12 +161,10 @@ class GroupPlan:
         return len(self.diags)
 
     def rotations(self) -> list[int]:
-        out = [b * self.stride for b in range(1, min(self.bstep, self.rows))]
-        if self.rows > self.bstep:
-            out.append(self.bstep * self.stride)
-        if self.offset:
-            out.append(self.offset)
-        return out
+        """Keys of LinearTransformInPlace's fast schedule (the offset folded
+        into the babies' shared ModUp, the giant steps as one batch)."""
+        used = sorted({k % self.bstep for k, d in enumerate(self.diags) if d is not None})
+        return bsgs_rotations(self.rows, self.bstep, self.stride, self.offset, used)
 
     def prerotated(self) -> list:
         """pts[k] rotated by -(k // bstep) * bstep * stride (LinearTransformInPlace)."""

@@ -39,6 +39,7 @@ from typing import Iterable, Sequence
 import numpy as np
 
 from .core import Context, Poly, conjugation_element, galois_element, gen_moduli
+from .rotation import bsgs_rotations  # noqa: F401
 from .serial import (BINARY, JSON, DeserializeCiphertext, DeserializeCryptoContext,  # noqa: F401
                      DeserializePrivateKey, DeserializePublicKey, SerializeToFile, SerType)
 
@@ -761,40 +762,48 @@ class CryptoContext:
 
         pts[k] (None for a zero diagonal) must already be rotated by
         -(k // bStep) * bStep * stride, as the reference's pre-rotated
-        masks are.  A nonzero offset first rotates ct by `offset`."""
+        masks are.  A nonzero offset first rotates ct by `offset`.
+
+        The key set decides the schedule (`bsgs_rotations` lists the keys of
+        the fast one): with keys for offset + b*stride the offset rotation
+        joins the babies' shared ModUp instead of costing a key switch of
+        its own, and with keys for every multiple g*bStep*stride the giant
+        steps run as one batch of independent rotations instead of Horner's
+        rule; otherwise the offset is one rotation and the giants use the
+        bStep*stride key.  All schedules give the same sum."""
         count, bstep = int(rowSize), int(bStep)
         if len(pts) < count:
             raise ValueError("fewer plaintexts than rowSize")
         pts = list(pts[:count])
-        if offset:
-            ct._assign(self.EvalRotate(ct, offset))
-        if ct.deg >= 2:
-            ct._assign(self._rescaled(ct))
         present = [p for p in pts if p is not None]
         if not present:
             raise ValueError("linear transform has no nonzero diagonal")
+        nb = min(bstep, count)
+        giants = -(-count // bstep)
+        used = sorted({k % bstep for k in range(count) if pts[k] is not None})
+        has = lambda r: galois_element(int(r), self.n) in self._galois  # noqa: E731
+        fold = bool(offset) and all(has(offset + b * stride) for b in used)
+        batch = giants > 2 and all(has(g * bstep * stride) for g in range(1, giants))
+        if offset and not fold:
+            ct._assign(self.EvalRotate(ct, offset))
+        off = offset if fold else 0
+        if ct.deg >= 2:
+            ct._assign(self._rescaled(ct))
         deg, scale = present[0].deg, present[0].scale
         if any(p.deg != deg or abs(p.scale / scale - 1) > 1e-12 for p in present):
             raise ValueError("diagonals must share one scale and degree")
         if any(p.level > ct.level for p in present):
             ct._assign(self._dropped(ct, max(p.level for p in present)))
-        nb = min(bstep, count)
-        used = {k % bstep for k in range(count) if pts[k] is not None}
-        baby_keys, baby_gal = [], []
-        for b in range(1, max(nb, 1)):
-            if b in used:
-                g = galois_element(b * stride, self.n)
-                baby_keys.append(self._key_for(g))
-                baby_gal.append(g)
-            else:
-                baby_keys.append(None)
-                baby_gal.append(1)
-        gk, gg = None, 1
-        if count > bstep:
-            gg = galois_element(bstep * stride, self.n)
-            gk = self._key_for(gg)
-        poly = self._ctx.linear_transform(ct.poly, [None if p is None else p.poly for p in pts],
-                                          bstep, baby_keys, baby_gal, gk, gg)
+        baby_keys, baby_gal = [None] * nb, [1] * nb
+        for b in used:
+            if b or off:
+                g = galois_element(off + b * stride, self.n)
+                baby_keys[b], baby_gal[b] = self._key_for(g), g
+        steps = range(1, giants) if batch else ([1] if giants > 1 else [])
+        gal = [galois_element(g * bstep * stride, self.n) for g in steps]
+        poly = self._ctx.linear_transform_hoisted(
+            ct.poly, [None if p is None else p.poly for p in pts], bstep, baby_keys, baby_gal,
+            [self._key_for(g) for g in gal], gal)
         ct._assign(self._wrap(poly, ct.level, ct.deg + deg, ct.scale * scale, ct.slots))
 
     # ------------------------------------------------------------ bootstrapping

@@ -266,6 +266,30 @@ class Context:
              giant_key.handle if giant_key is not None else None, giant_galois)
         return out
 
+    def linear_transform_hoisted(self, ct, pts, bstep: int, baby_keys, baby_galois,
+                                 giant_keys=(), giant_galois=(), out=None):
+        """The same sum with baby b = ct rotated by baby_keys[b] (b = 0 ..
+        min(bstep, count) - 1; baby_keys[0] None: baby 0 is ct, else it is
+        ct's offset rotation and the other keys include the offset), all
+        from one ModUp; giant_keys: one key (Horner's rule) or one per giant
+        step g = 1 .. G - 1 (rotations by g giant strides, one batch)."""
+        count = len(pts)
+        out = self._out(out, 2, ct.nlimb)
+        ph = (ctypes.c_void_p * count)(*[p.handle.value if p is not None else None
+                                         for p in pts])
+        nb = max(1, min(bstep, count))
+        bk = (ctypes.c_void_p * nb)(*([k.handle.value if k is not None else None
+                                       for k in baby_keys] + [None] * (nb - len(baby_keys))))
+        bg = np.ones(nb, dtype=np.uint32)
+        bg[: len(baby_galois)] = baby_galois
+        ng = len(giant_keys)
+        gk = (ctypes.c_void_p * max(ng, 1))(*([k.handle.value for k in giant_keys] or [None]))
+        gg = np.ones(max(ng, 1), dtype=np.uint32)
+        gg[:ng] = giant_galois
+        call("fhe_linear_transform_hoisted", out.handle, ct.handle, ph, count, bstep, bk,
+             _ptr(bg), gk, _ptr(gg), ng)
+        return out
+
     # -------------------------------------------------------------- encoding
     def encode(self, values, slots: int, scale: float, nlimb: int, out=None) -> "Poly":
         v = np.asarray(values)

@@ -35,6 +35,7 @@ from dataclasses import dataclass, field
 import numpy as np
 
 from .ptcache import PlaintextCache
+from .rotation import bsgs_rotations
 
 PACKED_MAX_NODES = 1_000_000
 REFRESH_SCALE_BITS = 12          # the reference's 4096 residual scale
@@ -528,8 +529,7 @@ class PackedEvaluator:
             if ck:
                 self._pt_cache.put(ck, pts)
         giants = -(-rows // b)
-        self._ensure_keys([j * step for j in range(1, min(b, rows))] +
-                          ([b * step] if rows > b else []) + [offs[0]])
+        self._ensure_keys(bsgs_rotations(rows, b, step, offs[0]))
         self.stats["rotations"] += (min(b, rows) - 1) + (giants - 1) + (1 if offs[0] % self.slots else 0)
         self.stats["ct_pt"] += rows
         out = x.Clone()
@@ -583,10 +583,7 @@ class PackedEvaluator:
                     pts.append(self.cc.MakeCKKSPackedPlaintext(mask, 1, rep.GetLevel(),
                                                                slots=self.slots))
                 self._pt_cache.put(cache_key, pts)
-            used = [bb * stride for bb in range(1, b)]
-            if shape.per_replica > b:
-                used.append(b * stride)
-            self._ensure_keys(used)
+            self._ensure_keys(bsgs_rotations(shape.per_replica, b, stride))
             giants = -(-shape.per_replica // b)
             self.stats["rotations"] += (b - 1) + (giants - 1)
             self.stats["ct_pt"] += shape.per_replica

@@ -7,7 +7,9 @@ same offsets:
     form, ascending magnitude; offsets folded into (-slots/2, slots/2]);
   * rotate_prefix_batch follows include/rotation_batch.hpp:17-62: outputs
     sharing a prefix of their step sequence share its rotations, and the
-    children of one node are produced by one hoisted call.
+    children of one node are produced by one hoisted call;
+  * bsgs_rotations lists the keys of a baby-step giant-step transform's
+    hoisted schedule (CryptoContext.LinearTransformInPlace).
 """
 from __future__ import annotations
 
@@ -116,3 +118,16 @@ def rotate_prefix_batch(value, offsets: Sequence[int], slots: int, naf: bool,
             for (_, child), v in reversed(list(zip(kids, vals))):
                 stack.append((child, v))
     return results
+
+
+def bsgs_rotations(count: int, bstep: int, stride: int, offset: int = 0,
+                   used=None) -> list[int]:
+    """Rotation indices whose keys give LinearTransformInPlace its fast
+    schedule for `count` diagonals at `stride` from `offset`: the babies
+    offset + b*stride (b in `used`, default every baby; b = 0 only with an
+    offset) and every giant multiple g*bstep*stride."""
+    nb = min(bstep, count)
+    used = range(nb) if used is None else used
+    out = [offset + b * stride for b in used if b or offset]
+    out += [g * bstep * stride for g in range(1, -(-count // bstep))]
+    return out

@@ -214,6 +214,23 @@ int fhe_linear_transform(fhe_poly *out, const fhe_poly *ct,
                          uint32_t bstep, const fhe_key *const *baby_keys,
                          const uint32_t *baby_galois, const fhe_key *giant_key,
                          uint32_t giant_galois);
+/* The same sum with the caller's pre-rotation and the giant steps folded
+ * in (LinearTransformInPlace with a nonzero offset: the ciphertext rotated
+ * by `offset` first, packed_fideslib.cpp:447-516; no separate counterpart):
+ * baby_keys[b] / baby_galois[b] for b = 0..min(bstep, count)-1 rotate ct by
+ * offset + b strides (baby_keys[0] null: baby 0 is ct itself, no offset),
+ * all babies from one ModUp, so the offset costs no key switch of its own.
+ * n_giant_keys = 1: giant_keys[0] rotates by bstep strides, applied by
+ * Horner's rule; n_giant_keys = G - 1 (G = ceil(count / bstep)):
+ * giant_keys[g-1] rotates by g * bstep strides and the G - 1 giant
+ * rotations run as one batch of independent key switches. */
+int fhe_linear_transform_hoisted(fhe_poly *out, const fhe_poly *ct,
+                                 const fhe_poly *const *pts, uint32_t count,
+                                 uint32_t bstep, const fhe_key *const *baby_keys,
+                                 const uint32_t *baby_galois,
+                                 const fhe_key *const *giant_keys,
+                                 const uint32_t *giant_galois,
+                                 uint32_t n_giant_keys);
 
 /* ---- encoding -----------------------------------------------------------
  * MakeCKKSPackedPlaintext (packed_fideslib.cpp:204): special inverse FFT of

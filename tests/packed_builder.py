@@ -225,21 +225,33 @@ class SlotContext:
         return [self._rot(a, k) for k in idx]
 
     def LinearTransformInPlace(self, ct, rows, bstep, pts, stride=1, offset=0):  # noqa: N802
-        x = self._rot(ct, offset) if offset else ct
-        x = self._rescaled(x)
+        """The schedules of CryptoContext.LinearTransformInPlace, chosen the
+        same way by the keys present (each rotation asserts its key)."""
+        used = sorted({k % bstep for k in range(rows) if pts[k] is not None})
+        giants = -(-rows // bstep)
+        have = lambda r: r % self.slots == 0 or r % self.slots in self.keys  # noqa: E731
+        fold = bool(offset) and all(have(offset + b * stride) for b in used)
+        batch = giants > 2 and all(have(g * bstep * stride) for g in range(1, giants))
+        x = self._rescaled(ct if fold or not offset else self._rot(ct, offset))
+        off = offset if fold else 0
         lv = x.level
         inners = []
-        for g in range((rows + bstep - 1) // bstep):
+        for g in range(giants):
             inner = np.zeros(self.slots, dtype=complex)
             for b in range(bstep):
                 k = g * bstep + b
                 if k < rows and pts[k] is not None:
-                    inner += pts[k][1] * self._rot(x, b * stride).z
+                    inner += pts[k][1] * self._rot(x, off + b * stride).z
                     lv = max(lv, pts[k][2])
             inners.append(inner)
-        out = inners[-1]                    # giant steps by Horner's rule: one key
-        for inner in reversed(inners[:-1]):
-            out = self._rot(SlotCt(out), bstep * stride).z + inner
+        if batch:                          # every giant rotation from its own key
+            out = inners[0].copy()
+            for g in range(1, giants):
+                out += self._rot(SlotCt(inners[g]), g * bstep * stride).z
+        else:                              # Horner's rule: one giant key
+            out = inners[-1]
+            for inner in reversed(inners[:-1]):
+                out = self._rot(SlotCt(out), bstep * stride).z + inner
         ct._assign(SlotCt(out, lv, 2))
 
     def EvalBootstrapSetup(self, budget, dims, slots, correction=0, precompute=True, *,  # noqa: N802

@@ -105,3 +105,114 @@ def test_linear_transform_rejects_bad_arguments(setup):
     short = ctx.upload(residues(rng, ctx.q[:2], (1,), ctx.n))
     with pytest.raises(ValueError):  # plaintext with fewer limbs than ct
         ctx.linear_transform(ct, [short], 1, [], [])
+
+
+def oracle_transform_hoisted(orc, q, ct, pts, bstep, offset_keys, giant_keys):
+    """The hoisted schedule: babies ct rotated by offset + b strides (each
+    from ct), every giant step's inner sum rotated by its own key, summed."""
+    count, nq = len(pts), ct.shape[1]
+    qa = np.array(q[:nq], dtype=np.uint64)[None, :, None]
+    used = {k % bstep for k in range(count) if pts[k] is not None}
+    babies = {}
+    for b in used:
+        babies[b] = ct if offset_keys.get(b) is None else \
+            orc.rotate(ct, offset_keys[b][1], offset_keys[b][0])
+
+    def inner(g):
+        xs, ws = [], []
+        for b in range(bstep):
+            k = g * bstep + b
+            if k < count and pts[k] is not None:
+                xs.append(babies[b])
+                ws.append(pts[k][:nq])
+        if not xs:
+            return np.zeros_like(ct)
+        return orc.mac(np.stack(xs), np.stack(ws))
+
+    giants = -(-count // bstep)
+    acc = inner(0)
+    for g in range(1, giants):
+        gk = giant_keys[g - 1]
+        acc = (acc + orc.rotate(inner(g), gk[1], gk[0])) % qa
+    return acc
+
+
+HOISTED = [
+    # (count, bstep, stride, offset, null diagonals)
+    (9, 3, 1, -4, (4,)),
+    (12, 4, 2, -11, ()),
+    (7, 4, 1, 0, (2,)),
+    (16, 4, 3, 5, (0, 13)),
+]
+
+
+@pytest.mark.parametrize("count,bstep,stride,offset,nulls", HOISTED)
+def test_hoisted_linear_transform_matches_oracle(setup, count, bstep, stride, offset, nulls):
+    """fhe_linear_transform_hoisted: the offset folded into the babies'
+    shared ModUp and one key per giant step (the giant rotations as one
+    batch), bit-exact against the same composition of oracle rotations."""
+    ctx, orc, s, _ = setup
+    rng = np.random.default_rng(300 + count + bstep + offset)
+    nq = ctx.L - 1
+    ct = residues(rng, ctx.q[:nq], (2,), ctx.n)
+    pts_host = [None if k in nulls else residues(rng, ctx.q, (), ctx.n)
+                for k in range(count)]
+    pts_dev = [None if p is None else ctx.upload(p[None]) for p in pts_host]
+    nb = min(bstep, count)
+    used = {k % bstep for k in range(count) if pts_host[k] is not None}
+    okeys = {b: (_key(setup, offset + b * stride)[:2] if (b or offset) else None)
+             for b in used}
+    bdev = [(_key(setup, offset + b * stride)[2] if b in used and (b or offset) else None)
+            for b in range(nb)]
+    bgal = [(_key(setup, offset + b * stride)[0] if b in used and (b or offset) else 1)
+            for b in range(nb)]
+    giants = -(-count // bstep)
+    gks = [_key(setup, g * bstep * stride) for g in range(1, giants)]
+    got = ctx.linear_transform_hoisted(ctx.upload(ct), pts_dev, bstep, bdev, bgal,
+                                       [k[2] for k in gks], [k[0] for k in gks]).numpy()
+    want = oracle_transform_hoisted(orc, ctx.q, ct, pts_host, bstep, okeys,
+                                    [k[:2] for k in gks])
+    assert np.array_equal(got, want)
+    # Horner's rule with the single giant key, through the same entry
+    if giants > 2:
+        g1 = _key(setup, bstep * stride)
+        got1 = ctx.linear_transform_hoisted(ctx.upload(ct), pts_dev, bstep, bdev, bgal,
+                                            [g1[2]], [g1[0]]).numpy()
+        babies_first = {b: okeys.get(b) for b in used}
+        want1 = oracle_transform_horner_from_babies(orc, ctx.q, ct, pts_host, bstep,
+                                                    babies_first, g1[:2])
+        assert np.array_equal(got1, want1)
+
+
+def oracle_transform_horner_from_babies(orc, q, ct, pts, bstep, offset_keys, giant):
+    count, nq = len(pts), ct.shape[1]
+    qa = np.array(q[:nq], dtype=np.uint64)[None, :, None]
+    babies = {b: ct if k is None else orc.rotate(ct, k[1], k[0]) for b, k in offset_keys.items()}
+
+    def inner(g):
+        xs, ws = [], []
+        for b in range(bstep):
+            k = g * bstep + b
+            if k < count and pts[k] is not None:
+                xs.append(babies[b])
+                ws.append(pts[k][:nq])
+        return orc.mac(np.stack(xs), np.stack(ws)) if xs else np.zeros_like(ct)
+
+    giants = -(-count // bstep)
+    acc = inner(giants - 1)
+    for g in range(giants - 2, -1, -1):
+        acc = (orc.rotate(acc, giant[1], giant[0]) + inner(g)) % qa
+    return acc
+
+
+def test_hoisted_linear_transform_rejects_bad_giant_keys(setup):
+    ctx, orc, s, _ = setup
+    rng = np.random.default_rng(6)
+    ct = ctx.upload(residues(rng, ctx.q, (2,), ctx.n))
+    pts = [ctx.upload(residues(rng, ctx.q, (1,), ctx.n)) for _ in range(9)]
+    k1 = _key(setup, 1)
+    with pytest.raises(ValueError):  # three keys for three giant steps (one or two)
+        ctx.linear_transform_hoisted(ct, pts, 3, [None, k1[2], k1[2]], [1, k1[0], k1[0]],
+                                     [k1[2]] * 3, [k1[0]] * 3)
+    with pytest.raises(ValueError):  # no giant key at all
+        ctx.linear_transform_hoisted(ct, pts, 3, [None, k1[2], k1[2]], [1, k1[0], k1[0]])
