@@ -352,11 +352,12 @@ def run_bootstrap(steps: int = 3, warmup: int = 2):
 REF_TOKEN_S = 396.6
 
 
-def run_decode(tokens: int = 2, security: str = "not-set"):
+def run_decode(tokens: int = 5, security: str = "not-set"):
     """Encrypted Mamba-2 decode of a seeded random-init 24-layer payload at
     the 130M shape (d_model 768, d_inner 1536, 24 heads x 64, state 128,
     conv 4), depth 44, 59-bit scale; the first token from zero state, then
-    carried-state tokens.  Errors against the payload's polynomial circuit
+    carried-state tokens (their mean is the carried figure, as the
+    reference's mean of 4).  Errors against the payload's polynomial circuit
     after decryption.  security "not-set": N=2^16, 32768 slots, sparse
     ternary secret (the reference decoder's); "128-classic": the audited
     classical-128 setting, N=2^17, 65536 slots, 45 Q + 12 P primes, four
@@ -373,6 +374,7 @@ def run_decode(tokens: int = 2, security: str = "not-set"):
         return {
             "s_per_token_first": rep["first_token_seconds"],
             "s_per_token_carried": carried,
+            "s_per_token_all": rep["seconds_per_token"],
             "max_abs_err_vs_polynomial": rep["max_abs_error_vs_polynomial"],
             "bootstraps_per_token": rep["bootstraps"] / tokens,
             "rotations_per_token": rep["rotations"] / tokens,
@@ -390,6 +392,7 @@ def run_decode(tokens: int = 2, security: str = "not-set"):
     return {
         "s_per_token_first": rep["first_token_seconds"],
         "s_per_token_carried": carried,
+        "s_per_token_all": rep["seconds_per_token"],
         "max_abs_err_vs_polynomial": rep["max_abs_error_vs_polynomial"],
         "bootstraps_per_token": rep["bootstraps"] / tokens,
         "rotations_per_token": rep["rotations"] / tokens,
@@ -641,7 +644,7 @@ def main() -> int:
         log("mamba-2 decode workload")
         out["mamba2_decode"] = run_decode()
         log("mamba-2 decode workload, classical-128")
-        out["mamba2_decode_classical128"] = run_decode(security="128-classic")
+        out["mamba2_decode_classical128"] = run_decode(tokens=3, security="128-classic")
     if args.copy_probe:
         log("copy probe")
         copy_probe(F)

@@ -235,6 +235,15 @@ class EncryptedMamba2Decoder:
             y = self.ev.mul(y, self.cc.EvalAdd(t, 1.5))
         return y
 
+    def decay_policy(self, decay_level: int, state_level: int) -> bool:
+        """Refresh the compact decay before its expansion when its groups
+        (two levels deeper) would drag the carried state deeper than the
+        state itself: h' = decay h + ... takes the deeper operand's level, so
+        a deep decay makes all state groups refresh within a token or two
+        (one bootstrap each), where one bootstrap of the decay keeps the
+        state growing a level per token."""
+        return decay_level + 2 > state_level
+
     def rms_scale(self, x, width: int, eps: float, spec: PolySpec, xbound: float,
                   vbound: float, ibound: float):
         """inv_sqrt(mean(x^2) + eps) of the first `width` slots, in every slot
@@ -287,11 +296,14 @@ class EncryptedMamba2Decoder:
         di, cd, ns, gb = self.di, self.cd, self.ns, self.gb
         t = lay.t
         # block norm: in_proj(hidden * inv) = in_proj(hidden) * inv, so the
-        # matvec runs on the shallow residual (block_norm_w folded in)
+        # matvec runs on the shallow residual (block_norm_w folded in); one
+        # refresh of the residual serves the variance, the matvec and the
+        # residual add
+        hidden = self.ready(hidden, 4, B["residual"], self._support(0, self.d))
         inv = self.rms_scale(hidden, self.d, lay.eps_block, lay.polys["rms_invsqrt"],
                              B["residual"], B["variance"], B["inv"])
         w_in = t("in_proj_w") * t("block_norm_w")[None, :]
-        hin = self.ready(hidden, 4, B["residual"], self._support(0, self.d))
+        hin = hidden
         psup = self._support(0, lay.proj_dim)
         proj = self.times_scale(ev.linear(hin, w_in, ("in_proj", li)), inv, B["proj_raw"],
                                 psup, B["inv"])
@@ -359,6 +371,8 @@ class EncryptedMamba2Decoder:
             dt_c = self.spread_heads(self.ready(dt, 6, B["dt"], ds), d0)
         dt_groups = self.expand_compact(dt_c, 0)
         decay = self.ready(decay, 5, B["decay"], ds)
+        if st.ssm is not None and self.decay_policy(ev._level(decay), ev._level(st.ssm[0])):
+            decay = self.ev.refresh(decay, B["decay"], ds)
         decay_groups = self.expand_compact(self.spread_heads(decay, d0), 0)
         # state update and readout
         new_ssm, reads = [], []
@@ -397,11 +411,13 @@ class EncryptedMamba2Decoder:
         y = self.ready(y, 2, B["y"], zs)
         gate = self.ready(gate, 2, B["gate"], zs)
         gated = ev.mul(y, gate)
-        # gated norm: out_proj(gated * inv2) = out_proj(gated) * inv2
+        # gated norm: out_proj(gated * inv2) = out_proj(gated) * inv2 (one
+        # refresh of gated serves the variance and the matvec)
+        gated = self.ready(gated, 4, B["gated"], zs)
         inv2 = self.rms_scale(gated, di, lay.eps_gated, lay.polys["gated_rms_invsqrt"],
                               B["gated"], B["gated_variance"], B["gated_inv"])
         w_out = t("out_proj_w") * t("gated_norm_w")[None, :]
-        gin = self.ready(gated, 4, B["gated"], zs)
+        gin = gated
         dsup = self._support(0, self.d)
         out = self.times_scale(ev.linear(gin, w_out, ("out_proj", li)), inv2, B["out_raw"],
                                dsup, B["gated_inv"])
@@ -432,9 +448,9 @@ class EncryptedMamba2Decoder:
                      f"bootstraps {self.ev.stats['bootstraps']}")
         last = self.chain.layers[-1]
         B = self.bounds[-1]
+        h = self.ready(h, 3, B["out_residual"], self._support(0, self.d))
         inv = self.rms_scale(h, self.d, self.chain.final_norm_eps, self.chain.final_invsqrt(),
                              B["out_residual"], B["out_variance"], B["out_inv"])
-        h = self.ready(h, 2, B["out_residual"], self._support(0, self.d))
         final = self.ev.plain(h, self._vec({0: self.chain.final_norm_w}), True)
         final = self.times_scale(final, inv, B["out_residual"] * float(
             np.max(np.abs(self.chain.final_norm_w))), self._support(0, self.d), B["out_inv"])
