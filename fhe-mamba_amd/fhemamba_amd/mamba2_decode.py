@@ -264,11 +264,9 @@ class EncryptedMamba2Decoder:
         offs = [start + g * self.gb for g in range(self.groups)]
         rots = self.ev.rotate_hoisted(ct, offs)
         sup = self._support(0, self.gb)
-        out = []
-        for r in rots:
-            m = self.ev.plain(r, sup, True, key=("blk", self.gb))
-            out.append(self.ev.rotation_sum(m, self.ns, -self.gb))
-        return out
+        ms = [self.ev.plain(r, sup, True, key=("blk", self.gb)) for r in rots]
+        # the groups' rotate-sums in lockstep, one batched key switch a step
+        return self.ev.rotation_sum_many(ms, self.ns, -self.gb)
 
     def spread_heads(self, ct, start: int, gain: float = 1.0):
         """Per-head values at slots [start, start + nh) -> compact channel

@@ -471,6 +471,26 @@ class PackedEvaluator:
             out = self.add(out, self.rotate(out if acc else ct, off * stride))
         return out
 
+    def rotation_sum_many(self, cts, count: int, stride: int):
+        """rotation_sum of several ciphertexts in lockstep: each step's
+        rotations go out as one batch of key switches (EvalRotateMany)."""
+        if len(cts) < 2 or not hasattr(self.cc, "EvalRotateMany"):
+            return [self.rotation_sum(c, count, stride) for c in cts]
+        base = [self.cc.Rescale(c) if c.GetNoiseScaleDeg() >= 2 else c for c in cts]
+        outs = list(base)
+        for off, acc in rotation_sum_schedule(count):
+            k = (off * stride) % self.slots
+            if k == 0:
+                outs = [self.add(o, o if acc else b) for o, b in zip(outs, base)]
+                continue
+            self._ensure_keys([k])
+            self.stats["rotations"] += len(outs)
+            src = [o if acc else b for o, b in zip(outs, base)]
+            src = [self.cc.Rescale(c) if c.GetNoiseScaleDeg() >= 2 else c for c in src]
+            rots = self.cc.EvalRotateMany(src, k)
+            outs = [self.add(o, r) for o, r in zip(outs, rots)]
+        return outs
+
     # ------------------------------------------------------------- refresh
     def refresh(self, ct, bound: float, support):
         """Mask ct to its support (a width or a 0/1 slot vector; padding is

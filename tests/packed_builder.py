@@ -218,6 +218,11 @@ class SlotContext:
     def EvalRotate(self, a, k):  # noqa: N802
         return self._rot(a, k)
 
+    def EvalRotateMany(self, cts, k):  # noqa: N802
+        self.rotate_many_calls = getattr(self, "rotate_many_calls", 0) + 1
+        idx = list(k) if isinstance(k, (list, tuple)) else [k] * len(cts)
+        return [self._rot(c, i) for c, i in zip(cts, idx)]
+
     def EvalFastRotationPrecompute(self, a):  # noqa: N802
         return a
 

@@ -98,6 +98,8 @@ def test_decoder_circuit_on_slots(chain):
         assert np.max(np.abs(got - ch.expected_poly_final[k])) < 1e-6, k
     assert dec.ev.stats["logical_refreshes"] > 0
     assert all(len(s.ssm) == dec.groups and len(s.fifo) == 3 for s in states)
+    # the state groups' rotate-sums ran in lockstep batches
+    assert dec.groups > 1 and getattr(cc, "rotate_many_calls", 0) > 0
 
 
 def test_decoder_rejects_shapes_that_do_not_pack(chain):
