@@ -242,9 +242,30 @@ Context::Context(uint32_t log_n_, const uint64_t* q, uint32_t num_q, const uint6
   d_garner = upload(garner);
 }
 
+Context::Staging& Context::staging_slot(size_t bytes) {
+  Staging& s = staging[staging_next];
+  staging_next = (staging_next + 1) % kStagingSlots;
+  if (s.done)
+    hip_check(hipEventSynchronize(s.done), "staging wait");
+  else
+    hip_check(hipEventCreateWithFlags(&s.done, hipEventDisableTiming), "staging event");
+  if (s.bytes < bytes) {
+    if (s.host) hip_check(hipHostFree(s.host), "hipHostFree");
+    s.host = nullptr;
+    s.bytes = 0;
+    hip_check(hipHostMalloc(&s.host, bytes, hipHostMallocDefault), "hipHostMalloc");
+    s.bytes = bytes;
+  }
+  return s;
+}
+
 Context::~Context() {
   hipSetDevice(device);
   if (stream) hipStreamSynchronize(stream);
+  for (Staging& s : staging) {
+    if (s.host) hipHostFree(s.host);
+    if (s.done) hipEventDestroy(s.done);
+  }
   for (auto& kv : plans) {
     ConvPlan* pl = kv.second.get();
     hipFree(pl->d_qhat_inv);

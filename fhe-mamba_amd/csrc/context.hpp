@@ -150,6 +150,22 @@ struct Context {
   std::mutex fft_mu;
   std::map<uint32_t, std::pair<double*, double*>> fft_tables;
 
+  // Pinned host buffers staging encode inputs, so that their uploads are
+  // asynchronous: a ring whose slot is reused once the copy recorded on it
+  // has completed (staging_slot waits for that copy, not for the stream).
+  struct Staging {
+    void* host = nullptr;
+    size_t bytes = 0;
+    hipEvent_t done = nullptr;
+  };
+  static constexpr int kStagingSlots = 16;
+  std::mutex staging_mu;
+  Staging staging[kStagingSlots];
+  uint32_t staging_next = 0;
+  // The next ring slot, holding at least `bytes`; the caller records the
+  // completion of its copy out of the slot on `done`.
+  Staging& staging_slot(size_t bytes);
+
   // Stream family for key generation and encryption: ChaCha20 under a
   // master key from OS entropy unless the caller sets one (or chooses the
   // seeded parity family).

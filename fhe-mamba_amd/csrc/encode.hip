@@ -15,6 +15,7 @@
 // All floating-point operations are plain IEEE double add/sub/mul/div; the
 // library is compiled with -ffp-contract=off so none fuse into FMAs, which
 // keeps the encoder's rounding identical to the CPU definition.
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 
@@ -181,25 +182,47 @@ bool encode(Context& c, const double* re, const double* im, uint32_t count, uint
   if (count > slots) throw ArgError("more values than slots");
   if (nlimb == 0 || nlimb > c.L) throw ArgError("bad limb count");
   if (!(scale > 0) || !std::isfinite(scale)) throw ArgError("scale must be positive");
-  std::vector<double> host(2 * (size_t)slots, 0.0);
-  for (uint32_t j = 0; j < count; ++j) {
-    host[2 * j] = re[j];
-    host[2 * j + 1] = im ? im[j] : 0.0;
-  }
+  const size_t bytes = 2 * (size_t)slots * sizeof(double);
   const auto tw = fft_tables(c, slots);
   Scratch v(c, 2 * (size_t)slots), st(c, 1);
-  hip_check(hipMemcpyAsync(v.p, host.data(), host.size() * 8, hipMemcpyHostToDevice, c.stream),
-            "encode upload");
+  // Range bound: each inverse-FFT stage maps (a, b) to (a + b, (a - b) w)
+  // with |w| = 1, so an output's modulus is at most the sum of the inputs'
+  // and, after the division by slots, at most the largest input modulus.
+  // Inputs whose bound times the scale stays below 2^62 (the margin 2^-20
+  // is far above the transform's rounding) cannot fail k_round_lift's range
+  // check, so nothing waits for the device; other inputs read the check's
+  // status back, which waits for the stream.
+  double bound = 0.0;
+  bool finite = true;
+  {
+    std::lock_guard<std::mutex> g(c.staging_mu);
+    Context::Staging& sg = c.staging_slot(bytes);
+    double* host = static_cast<double*>(sg.host);
+    for (uint32_t j = 0; j < count; ++j) {
+      const double a = re[j], b = im ? im[j] : 0.0;
+      host[2 * j] = a;
+      host[2 * j + 1] = b;
+      finite = finite && std::isfinite(a) && std::isfinite(b);
+      bound = std::max(bound, std::hypot(a, b));
+    }
+    std::memset(host + 2 * (size_t)count, 0, bytes - 2 * (size_t)count * sizeof(double));
+    hip_check(hipMemcpyAsync(v.p, host, bytes, hipMemcpyHostToDevice, c.stream),
+              "encode upload");
+    hip_check(hipEventRecord(sg.done, c.stream), "encode staging event");
+  }
+  const bool checked = !(finite && bound * scale < 4611686018427387904.0 * (1.0 - 0x1p-20));
   hip_check(hipMemsetAsync(st.p, 0, 8, c.stream), "encode status");
   hip_check(hipMemsetAsync(out, 0, (size_t)nlimb * c.n * 8, c.stream), "encode clear");
   run_stages(c, reinterpret_cast<double2*>(v.p), tw.first, slots, true);
   const uint32_t threads = slots < TPB ? slots : TPB;
   FHE_LAUNCH(c, "k_round_lift", k_round_lift, dim3((slots + threads - 1) / threads), dim3(threads), 0, reinterpret_cast<const double2*>(v.p), out, c.d_const, slots, ilog2(slots), c.n / (2 * slots), c.n, nlimb, scale, reinterpret_cast<int*>(st.p));
-  int status = 0;
-  hip_check(hipMemcpyAsync(&status, st.p, sizeof(int), hipMemcpyDeviceToHost, c.stream),
-            "encode status");
-  hip_check(hipStreamSynchronize(c.stream), "encode sync");
-  if (status) return false;
+  if (checked) {
+    int status = 0;
+    hip_check(hipMemcpyAsync(&status, st.p, sizeof(int), hipMemcpyDeviceToHost, c.stream),
+              "encode status");
+    hip_check(hipStreamSynchronize(c.stream), "encode sync");
+    if (status) return false;
+  }
   ntt_forward(c, out, 1, 0, nlimb, LimbMap::contiguous(0));
   return true;
 }

@@ -43,6 +43,26 @@ def test_encode_real_partial_and_zero(pair):
     assert not ctx.encode(np.zeros(4), slots, scale, 1).numpy().any()
 
 
+def test_encode_range_check_path_and_queued_encodes(pair):
+    """An input whose largest slot exceeds 2^62 / scale takes the checked
+    path (status read back) and still encodes when its coefficients fit: one
+    nonzero slot spreads over 2 slots coefficients of 1/slots its size.
+    Then 40 encodes queued without waits (the staging ring's 16 slots
+    cycle) all equal the oracle."""
+    ctx, orc = pair
+    slots = ctx.n // 2
+    scale = 2.0**40
+    z = np.zeros(slots, dtype=complex)
+    z[3] = 1.5 * 2.0**22 + 0.5j * 2.0**22  # |z| scale > 2^62, coefficients < 2^62
+    got = ctx.encode(z, slots, scale, 2)
+    assert np.array_equal(got.numpy()[0], orc.encode(z, slots, scale, 2))
+    rng = np.random.default_rng(11)
+    zs = [rng.uniform(-4, 4, slots) for _ in range(40)]
+    outs = [ctx.encode(v, slots, scale, 2) for v in zs]
+    for v, o in zip(zs, outs):
+        assert np.array_equal(o.numpy()[0], orc.encode(v, slots, scale, 2))
+
+
 def test_encode_out_of_range_raises(pair):
     ctx, _ = pair
     with pytest.raises(OverflowError):

@@ -347,6 +347,25 @@ def test_encode_rounds_scaled_coefficients(small_scheme):
     assert np.abs(dec - z).max() < 1e-9
 
 
+@pytest.mark.parametrize("kind", ["uniform", "gauss", "constant", "spike", "alternating"])
+def test_special_inverse_fft_bounded_by_largest_slot(kind):
+    """The encoder's asynchronous path relies on this: every coefficient of
+    the special inverse FFT (division by slots included) has modulus at most
+    the largest slot's, so scale * max|z| < 2^62 rules out the range error.
+    A constant vector attains the bound (one coefficient equals it)."""
+    slots = 256
+    rng = np.random.default_rng(len(kind))
+    z = {"uniform": rng.uniform(-1, 1, slots) + 1j * rng.uniform(-1, 1, slots),
+         "gauss": rng.normal(0, 3, slots) + 1j * rng.normal(0, 3, slots),
+         "constant": np.full(slots, 2.5 - 1.5j),
+         "spike": np.eye(1, slots, 7)[0] * (3 + 4j),
+         "alternating": np.where(np.arange(slots) % 2, 1.0, -1.0) + 0j}[kind]
+    w = O.fft_special_inv(z)
+    assert np.abs(w).max() <= np.abs(z).max() * (1 + 1e-12)
+    if kind == "constant":
+        assert np.isclose(np.abs(w).max(), np.abs(z).max(), rtol=1e-12)
+
+
 def test_encode_rejects_out_of_range(small_scheme):
     c, _, _ = small_scheme
     with pytest.raises(ValueError):
