@@ -136,3 +136,16 @@ def check(rc: int) -> None:
 
 def call(name: str, *args) -> None:
     check(getattr(lib, name)(*args))
+
+
+def device_free_bytes() -> int | None:
+    """Free memory of the current HIP device (hipMemGetInfo from the HIP
+    runtime the library links), or None when it cannot be read."""
+    try:
+        hip = ctypes.CDLL("libamdhip64.so")
+        free, total = ctypes.c_size_t(0), ctypes.c_size_t(0)
+        if hip.hipMemGetInfo(ctypes.byref(free), ctypes.byref(total)) != 0:
+            return None
+        return int(free.value)
+    except OSError:
+        return None

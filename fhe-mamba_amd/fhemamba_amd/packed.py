@@ -332,13 +332,29 @@ def monotone_routing(indices, scatter: bool, bits: int = 3):
 
 
 # ----------------------------------------------------------------- evaluator
+def default_pt_cache_bytes() -> int:
+    """Device budget of the evaluator's plaintext cache: 96 GiB, less if
+    the device has under 192 GiB free when the evaluator is built (the
+    rotation and bootstrapping keys, made later, need the rest), and at
+    least 8 GiB.  A Mamba-2-130M-shaped decode at N=2^16 encodes ~53 GiB of
+    in_proj / out_proj diagonals per token; a budget below its working set
+    evicts each diagonal set before its next use (LRU over a cyclic
+    sequence), so every token would encode them again."""
+    from ._lib import device_free_bytes
+    free = device_free_bytes()
+    cap = 96 << 30
+    if free is None:
+        return 48 << 30
+    return int(max(8 << 30, min(cap, free - cap)))
+
+
 class PackedEvaluator:
     """Evaluates a PackedProgram on a CryptoContext of this package."""
 
     def __init__(self, cc, keys, slots: int, *, bootstrap_passes: int = 2,
                  refresh_ceiling: int | None = None, replicated_linear: bool = True,
                  trace_levels: bool = False, level_budget=(4, 4), client=None,
-                 log=None, pt_cache_bytes: int = 48 << 30, s2c_first: bool = False):
+                 log=None, pt_cache_bytes: int | None = None, s2c_first: bool = False):
         if bootstrap_passes not in (1, 2):
             raise ValueError("bootstrap passes must be 1 or 2")
         self.cc, self.keys, self.slots = cc, keys, int(slots)
@@ -359,7 +375,9 @@ class PackedEvaluator:
         self.client = client
         self.log = log or (lambda msg: None)
         self._rot_keys: set = set()
-        self._pt_cache = PlaintextCache(cc.GetRingDimension(), pt_cache_bytes)
+        self._pt_cache = PlaintextCache(cc.GetRingDimension(),
+                                        pt_cache_bytes if pt_cache_bytes is not None
+                                        else default_pt_cache_bytes())
         self.stats = dict(ct_ct=0, ct_pt=0, rotations=0, adds=0, bootstraps=0,
                           logical_refreshes=0, bootstrap_seconds=0.0, keygen_seconds=0.0,
                           rotation_keys=0, evaluated_nodes=0)
