@@ -93,6 +93,56 @@ __global__ void k_fft_fwd_stage(double2* v, const double* tw, uint32_t slots, ui
   v[i + h] = make_double2(u.x - vr, u.y - vi);
 }
 
+// The stages with len <= FFT_BLOCK pair elements inside aligned blocks of
+// FFT_BLOCK values, so one workgroup runs all of them on its block in LDS:
+// the same butterflies and twiddles as the per-stage kernels above, in the
+// same order per element, hence the same roundings.
+constexpr uint32_t FFT_BLOCK = 2048;
+
+// Inverse stages len = top, top / 2, ..., 2 on blocks of `top` values.
+__global__ void __launch_bounds__(256)
+    k_fft_inv_block(double2* v, const double* tw, uint32_t top) {
+  __shared__ double2 x[FFT_BLOCK];
+  double2* g = v + (size_t)blockIdx.x * top;
+  for (uint32_t k = threadIdx.x; k < top; k += blockDim.x) x[k] = g[k];
+  __syncthreads();
+  for (uint32_t len = top; len >= 2; len >>= 1) {
+    const uint32_t h = len / 2;
+    for (uint32_t t = threadIdx.x; t < top / 2; t += blockDim.x) {
+      const uint32_t j = t % h, i = (t / h) * len + j;
+      const double2 a = x[i], b = x[i + h];
+      const double wr = tw[2 * (h - 1 + j)], wi = tw[2 * (h - 1 + j) + 1];
+      const double vr = a.x - b.x, vi = a.y - b.y;
+      x[i] = make_double2(a.x + b.x, a.y + b.y);
+      x[i + h] = make_double2(vr * wr - vi * wi, vi * wr + vr * wi);
+    }
+    __syncthreads();
+  }
+  for (uint32_t k = threadIdx.x; k < top; k += blockDim.x) g[k] = x[k];
+}
+
+// Forward stages len = 2, 4, ..., top on blocks of `top` values.
+__global__ void __launch_bounds__(256)
+    k_fft_fwd_block(double2* v, const double* tw, uint32_t top) {
+  __shared__ double2 x[FFT_BLOCK];
+  double2* g = v + (size_t)blockIdx.x * top;
+  for (uint32_t k = threadIdx.x; k < top; k += blockDim.x) x[k] = g[k];
+  __syncthreads();
+  for (uint32_t len = 2; len <= top; len <<= 1) {
+    const uint32_t h = len / 2;
+    for (uint32_t t = threadIdx.x; t < top / 2; t += blockDim.x) {
+      const uint32_t j = t % h, i = (t / h) * len + j;
+      const double2 u = x[i], b = x[i + h];
+      const double wr = tw[2 * (h - 1 + j)], wi = tw[2 * (h - 1 + j) + 1];
+      const double vr = b.x * wr - b.y * wi, vi = b.y * wr + b.x * wi;
+      x[i] = make_double2(u.x + vr, u.y + vi);
+      x[i + h] = make_double2(u.x - vr, u.y - vi);
+    }
+    __syncthreads();
+  }
+  for (uint32_t k = threadIdx.x; k < top; k += blockDim.x) g[k] = x[k];
+}
+
 __device__ __forceinline__ uint32_t brev_bits(uint32_t x, uint32_t bits) {
   return bits ? __brev(x) >> (32 - bits) : 0;
 }
@@ -114,14 +164,20 @@ __global__ void k_round_lift(const double2* v, uint64_t* out, const ModConst* mc
   const double a = (x.x / (double)slots) * scale, b = (x.y / (double)slots) * scale;
   const double lim = 4611686018427387904.0;  // 2^62
   if (!isfinite(a) || !isfinite(b) || fabs(a) >= lim || fabs(b) >= lim) {
-    atomicOr(status, 1);
+    if (status) atomicOr(status, 1);
     return;
   }
   const int64_t ra = llround(a), rb = llround(b);
   for (uint32_t j = 0; j < nlimb; ++j) {
     const uint64_t q = mc[j].q;
-    out[(size_t)j * n + (size_t)i * gap] = lift_signed(ra, q);
-    out[(size_t)j * n + (size_t)(i + slots) * gap] = lift_signed(rb, q);
+    uint64_t* o = out + (size_t)j * n;
+    o[(size_t)i * gap] = lift_signed(ra, q);
+    o[(size_t)(i + slots) * gap] = lift_signed(rb, q);
+    // the other coefficients of this slot's two gap blocks are zero
+    for (uint32_t z = 1; z < gap; ++z) {
+      o[(size_t)i * gap + z] = 0;
+      o[(size_t)(i + slots) * gap + z] = 0;
+    }
   }
 }
 
@@ -160,11 +216,17 @@ void run_stages(Context& c, double2* v, const double* tw, uint32_t slots, bool i
   if (slots < 2) return;
   const uint32_t threads = slots / 2 < TPB ? slots / 2 : TPB;
   const uint32_t blocks = (slots / 2 + threads - 1) / threads;
+  const uint32_t top = slots < FFT_BLOCK ? slots : FFT_BLOCK;
+  const uint32_t bthreads = top / 2 < TPB ? top / 2 : TPB;
   if (inverse) {
-    for (uint32_t len = slots; len >= 2; len >>= 1)
+    for (uint32_t len = slots; len > top; len >>= 1)
       FHE_LAUNCH(c, "k_fft_inv_stage", k_fft_inv_stage, dim3(blocks), dim3(threads), 0, v, tw, slots, len);
+    FHE_LAUNCH(c, "k_fft_inv_block", k_fft_inv_block, dim3(slots / top), dim3(bthreads), 0, v, tw,
+               top);
   } else {
-    for (uint32_t len = 2; len <= slots; len <<= 1)
+    FHE_LAUNCH(c, "k_fft_fwd_block", k_fft_fwd_block, dim3(slots / top), dim3(bthreads), 0, v, tw,
+               top);
+    for (uint32_t len = 2 * top; len <= slots; len <<= 1)
       FHE_LAUNCH(c, "k_fft_fwd_stage", k_fft_fwd_stage, dim3(blocks), dim3(threads), 0, v, tw, slots, len);
   }
 }
@@ -192,30 +254,34 @@ bool encode(Context& c, const double* re, const double* im, uint32_t count, uint
   // is far above the transform's rounding) cannot fail k_round_lift's range
   // check, so nothing waits for the device; other inputs read the check's
   // status back, which waits for the stream.
-  double bound = 0.0;
-  bool finite = true;
+  // |z|^2 < (2^62 (1 - 2^-20) / scale)^2 for every value, with NaN and
+  // infinities failing the comparison.
+  const double lim = 4611686018427387904.0 * (1.0 - 0x1p-20) / scale;
+  const double lim2 = lim * lim;
+  bool checked = !(lim2 < INFINITY);
   {
     std::lock_guard<std::mutex> g(c.staging_mu);
     Context::Staging& sg = c.staging_slot(bytes);
     double* host = static_cast<double*>(sg.host);
+    int over = 0;
     for (uint32_t j = 0; j < count; ++j) {
       const double a = re[j], b = im ? im[j] : 0.0;
       host[2 * j] = a;
       host[2 * j + 1] = b;
-      finite = finite && std::isfinite(a) && std::isfinite(b);
-      bound = std::max(bound, std::hypot(a, b));
+      over |= !(a * a + b * b < lim2);
     }
+    checked = checked || over;
     std::memset(host + 2 * (size_t)count, 0, bytes - 2 * (size_t)count * sizeof(double));
     hip_check(hipMemcpyAsync(v.p, host, bytes, hipMemcpyHostToDevice, c.stream),
               "encode upload");
     hip_check(hipEventRecord(sg.done, c.stream), "encode staging event");
   }
-  const bool checked = !(finite && bound * scale < 4611686018427387904.0 * (1.0 - 0x1p-20));
-  hip_check(hipMemsetAsync(st.p, 0, 8, c.stream), "encode status");
-  hip_check(hipMemsetAsync(out, 0, (size_t)nlimb * c.n * 8, c.stream), "encode clear");
+  if (checked) hip_check(hipMemsetAsync(st.p, 0, 8, c.stream), "encode status");
   run_stages(c, reinterpret_cast<double2*>(v.p), tw.first, slots, true);
   const uint32_t threads = slots < TPB ? slots : TPB;
-  FHE_LAUNCH(c, "k_round_lift", k_round_lift, dim3((slots + threads - 1) / threads), dim3(threads), 0, reinterpret_cast<const double2*>(v.p), out, c.d_const, slots, ilog2(slots), c.n / (2 * slots), c.n, nlimb, scale, reinterpret_cast<int*>(st.p));
+  // k_round_lift writes every coefficient of the nlimb limbs (the slots'
+  // positions and the zeros between them).
+  FHE_LAUNCH(c, "k_round_lift", k_round_lift, dim3((slots + threads - 1) / threads), dim3(threads), 0, reinterpret_cast<const double2*>(v.p), out, c.d_const, slots, ilog2(slots), c.n / (2 * slots), c.n, nlimb, scale, checked ? reinterpret_cast<int*>(st.p) : nullptr);
   if (checked) {
     int status = 0;
     hip_check(hipMemcpyAsync(&status, st.p, sizeof(int), hipMemcpyDeviceToHost, c.stream),
