@@ -322,3 +322,14 @@ def test_launcher_reports_bad_arguments_with_exit_code_2():
     r = subprocess.run([sys.executable, launcher, "p.txt", "r.json", "1e-3"],
                        capture_output=True, text=True, timeout=120)
     assert r.returncode == 2 and "usage" in r.stderr
+
+
+@pytest.mark.parametrize("free_gib, want_gib", [(None, 48), (288, 96), (150, 54), (90, 8)])
+def test_plaintext_cache_budget_follows_free_device_memory(monkeypatch, free_gib, want_gib):
+    """96 GiB (the 130M-shape decode's projection diagonals, ~53 GiB per
+    token, fit), less when under 192 GiB are free, never below 8 GiB; 48 GiB
+    when the free memory cannot be read."""
+    from fhemamba_amd import _lib
+    monkeypatch.setattr(_lib, "device_free_bytes",
+                        lambda: None if free_gib is None else free_gib << 30)
+    assert P.default_pt_cache_bytes() == want_gib << 30
