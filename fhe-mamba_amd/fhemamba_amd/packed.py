@@ -375,6 +375,7 @@ class PackedEvaluator:
         self.client = client
         self.log = log or (lambda msg: None)
         self._rot_keys: set = set()
+        self._masks: dict = {}  # host-side replicated-layout masks by matrix key
         self._pt_cache = PlaintextCache(cc.GetRingDimension(),
                                         pt_cache_bytes if pt_cache_bytes is not None
                                         else default_pt_cache_bytes())
@@ -614,12 +615,9 @@ class PackedEvaluator:
             cache_key = (key, "replicated", rep.GetLevel())
             pts = self._pt_cache.get(cache_key)
             if pts is None:
-                pts = []
-                for k in range(shape.per_replica):
-                    mask = replicated_mask(W, k, shape, self.slots)
-                    mask = np.roll(mask, (k // b) * b * stride)
-                    pts.append(self.cc.MakeCKKSPackedPlaintext(mask, 1, rep.GetLevel(),
-                                                               slots=self.slots))
+                pts = [self.cc.MakeCKKSPackedPlaintext(mask, 1, rep.GetLevel(),
+                                                       slots=self.slots)
+                       for mask in self._replicated_masks(W, shape, b, stride, key)]
                 self._pt_cache.put(cache_key, pts)
             self._ensure_keys(bsgs_rotations(shape.per_replica, b, stride))
             giants = -(-shape.per_replica // b)
@@ -635,6 +633,21 @@ class PackedEvaluator:
                 if W[i, j] != 0:
                     masks.setdefault(j - i, np.zeros(self.slots))[i] = W[i, j]
         return self.transform(x, masks)
+
+    def _replicated_masks(self, W, shape, b: int, stride: int, key):
+        """The replicated layout's diagonal-group masks, each rolled for its
+        giant step.  They do not depend on the level, while their encodings
+        do: a matrix met at a new level (the carried state moves the
+        projections' levels from token to token) re-encodes from these
+        instead of rebuilding them."""
+        ck = None if key is None else (key, shape, b, stride)
+        masks = self._masks.get(ck) if ck is not None else None
+        if masks is None:
+            masks = [np.roll(replicated_mask(W, k, shape, self.slots), (k // b) * b * stride)
+                     for k in range(shape.per_replica)]
+            if ck is not None:
+                self._masks[ck] = masks
+        return masks
 
     def chebyshev(self, x, node: PackedNode):
         from .ckks_probes import chebyshev_ps
