@@ -523,3 +523,68 @@ class CKKSBootstrapper:
             out = cc.EvalAdd(out, cc.MultByMonomial(self._eval_mod_amplitude(im, amp), N // 2))
             cc.RescaleInPlace(out)
         return out
+
+
+def main(argv=None) -> int:
+    """Time EvalBootstrap on one seeded full-packing ciphertext:
+    python -m fhemamba_amd.bootstrap [--log-n 16] [--depth 44] [--secret
+    sparse|uniform] [--order s2c-first|ordinary] [--passes 1|2]
+    [--repeat K] [--warmup W].  Prints one JSON line (ms per call, its
+    launches when profiling, the decrypted error)."""
+    import argparse
+    import json
+    import time
+
+    import numpy as np
+
+    from .ckks_probes import build_toy_context
+
+    ap = argparse.ArgumentParser(prog="python -m fhemamba_amd.bootstrap")
+    ap.add_argument("--log-n", type=int, default=16)
+    ap.add_argument("--depth", type=int, default=44)
+    ap.add_argument("--secret", choices=("sparse", "uniform"), default="sparse")
+    ap.add_argument("--order", choices=("s2c-first", "ordinary"), default="s2c-first")
+    ap.add_argument("--passes", type=int, choices=(1, 2), default=1)
+    ap.add_argument("--repeat", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    args = ap.parse_args(argv)
+    n = 1 << args.log_n
+    slots = n // 2
+    s2c = args.order == "s2c-first"
+    cc, keys = build_toy_context(ring_dimension=n, batch=slots, depth=args.depth, scale_bits=59,
+                                 first_mod_bits=60, seed=21,
+                                 secret_dist="SPARSE_TERNARY" if args.secret == "sparse"
+                                 else "UNIFORM_TERNARY")
+    cc.EvalBootstrapSetup([4, 4], [0, 0], slots, s2c_first=s2c, real_slots=s2c)
+    cc.EvalBootstrapKeyGen(keys.secretKey, slots)
+    x = np.random.default_rng(8).uniform(-1, 1, slots)
+    ct = cc.Encrypt(keys.publicKey, cc.MakeCKKSPackedPlaintext(list(x)))
+    ct.SetLevel(cc.GetBootstrapInputCeiling())
+    for _ in range(args.warmup):
+        cc.EvalBootstrap(ct, args.passes)
+    cc.device.sync()
+    t0 = time.perf_counter()
+    for _ in range(args.repeat):
+        out = cc.EvalBootstrap(ct, args.passes)
+    cc.device.sync()
+    ms = (time.perf_counter() - t0) / max(args.repeat, 1) * 1e3
+    cc.device.profile_begin()
+    cc.EvalBootstrap(ct, args.passes)
+    prof = cc.device.profile_end()
+    pt = cc.Decrypt(out, keys.secretKey)
+    pt.SetLength(slots)
+    err = float(np.max(np.abs(np.asarray(pt.GetRealPackedValue()) - x)))
+    print(json.dumps({
+        "ring_dimension": n, "depth": args.depth, "secret": args.secret, "order": args.order,
+        "passes": args.passes, "ms_per_call": ms,
+        "kernel_ms_per_call": sum(v[1] for v in prof.values()),
+        "launches_per_call": sum(v[0] for v in prof.values()),
+        "max_abs_err": err, "output_level": int(out.GetLevel()),
+    }))
+    return 0
+
+
+if __name__ == "__main__":
+    import sys
+
+    sys.exit(main())
