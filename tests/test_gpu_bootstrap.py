@@ -219,3 +219,18 @@ def test_bootstrap_at_ring_2_16(s2c_first):
               f"level {out.GetLevel()}, error 2^{np.log2(err):.1f}", flush=True)
         assert out.GetLevel() == cc.GetBootstrapDepth()
         assert err < tol
+
+
+@pytest.mark.parametrize("order", ["s2c-first", "ordinary"])
+def test_bootstrap_command_line(order, capsys):
+    """python -m fhemamba_amd.bootstrap at N=2^12: one JSON line with the
+    timing, launch count and a refreshed value within 2^-10."""
+    import json
+
+    from fhemamba_amd import bootstrap as B
+    assert B.main(["--log-n", "12", "--order", order, "--repeat", "1", "--warmup", "0"]) == 0
+    rep = json.loads(capsys.readouterr().out.strip().splitlines()[-1])
+    print(rep, flush=True)
+    assert rep["ring_dimension"] == 4096 and rep["order"] == order
+    assert rep["launches_per_call"] > 0 and rep["ms_per_call"] > 0
+    assert rep["max_abs_err"] < 2.0**-10
