@@ -569,7 +569,8 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (got --gpus {args.gpus}): the path has no "
-              "multi-GPU component in this build; see DESIGN.md for how it would shard.",
+              "multi-GPU component in this build (one GPU's share of a sharded run is what it "
+              "measures).",
               file=sys.stderr)
         return 2
     import fhemamba_amd as F
