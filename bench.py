@@ -689,12 +689,12 @@ def step_kernel_bytes(L: int, K: int, R: int) -> dict:
     rescale used at this ring dimension.  R hoisted rotations, ne = L + K
     extended limbs, alpha = ceil(L / dnum) limbs per digit:
       ntt_inv_blocks_modup    ModUp's first inverse pass: c1's L limbs read,
-                              L written (blocked);
+                              L written (blocked) and L written as the
+                              digits' own limbs;
       k_modup_mid             column stages + conversion of every digit: L
                               read, dnum*(ne-alpha) written;
       ntt_fwd_blocks_modup    last forward pass of the converted limbs:
                               dnum*(ne-alpha) read and written;
-      k_copy_own_limbs        each digit's own limbs: L read, L written;
       ntt_inv_blocks_ksk      first inverse ModDown pass, fed by the P-limb
                               key inner product: digits dnum*K once per batch,
                               per rotation the key's P limbs dnum*2*K read and
@@ -714,10 +714,9 @@ def step_kernel_bytes(L: int, K: int, R: int) -> dict:
     alpha = -(-L // DNUM)
     conv = DNUM * (ne - alpha)
     return {k: v * LIMB for k, v in {
-        "ntt_inv_blocks_modup": 2 * L,
+        "ntt_inv_blocks_modup": 3 * L,
         "k_modup_mid": L + conv,
         "ntt_fwd_blocks_modup": 2 * conv,
-        "k_copy_own_limbs": 2 * L,
         "ntt_inv_blocks_ksk": DNUM * K + R * (DNUM * 2 * K + 2 * K),
         "k_moddown_mid": R * (2 * K + 2 * L),
         "ntt_fwd_blocks_moddown": DNUM * L + L + R * (2 * L + DNUM * 2 * L + 2 * L),

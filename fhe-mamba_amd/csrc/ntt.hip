@@ -986,14 +986,22 @@ __global__ void __launch_bounds__(256)
 
 // ModUp input: limb blockIdx.z of ciphertext blockIdx.y's c1, read from the
 // caller's polys (the first inverse pass reads them in place of a copy).
+// Each word is read once by the pass, which also stores it as the word of
+// its digit's own limb ([ct][d][ne][N], d = limb / alpha): the digits keep
+// c1's own limbs as they are.
 constexpr int MODUP_MAX_CT = 32;
 struct SrcLoad {
   static constexpr bool kLoad = true;
   static constexpr bool kPair = false;
   const uint64_t* const* src;  // MODUP_MAX_CT entries in kernel arguments
   uint32_t n;
+  uint64_t* digits;
+  uint32_t alpha, nd, ne;
   __device__ __forceinline__ uint64_t get(size_t g, uint64_t) const {
-    return src[blockIdx.y][(size_t)blockIdx.z * n + g];
+    const uint32_t ct = blockIdx.y, i = blockIdx.z;
+    const uint64_t v = src[ct][(size_t)i * n + g];
+    digits[(((size_t)ct * nd + i / alpha) * ne + i) * n + g] = v;
+    return v;
   }
   struct Ops2 {};
   __device__ __forceinline__ void fetch2(size_t, Ops2&) const {}
@@ -1009,10 +1017,11 @@ template <int S>
 __global__ void __launch_bounds__(256)
     ntt_pass_modup_in(uint64_t* __restrict__ coef, size_t poly_stride,
                       const ModConst* __restrict__ mc, const uint64_t* __restrict__ tw_all,
-                      uint32_t log_n, uint32_t s_other, const SrcPtrs src) {
+                      uint32_t log_n, uint32_t s_other, const SrcPtrs src, uint64_t* digits,
+                      uint32_t alpha, uint32_t nd, uint32_t ne) {
   ntt_body<S, BLOCKS, true, RHO_EPILOGUE, PlainStore, SrcLoad, LimbMap, false, true>(
       coef, poly_stride, mc, tw_all, log_n, LimbMap::contiguous(0), s_other, 0, PlainStore{},
-      SrcLoad{src.p, 1u << log_n});
+      SrcLoad{src.p, 1u << log_n, digits, alpha, nd, ne});
 }
 
 // Last forward pass of a fused ModUp over the digits' converted limbs
@@ -1024,18 +1033,6 @@ __global__ void __launch_bounds__(256)
                        uint32_t log_n, DigitMap map, uint32_t s_other) {
   ntt_body<S, BLOCKS, false, RHO_EPILOGUE, PlainStore, PlainLoad, DigitMap, true, false>(
       digits, poly_stride, mc, tw_all, log_n, map, s_other, 1, PlainStore{});
-}
-
-// Each digit's own limbs, in evaluation form, from c1 into the digit buffer:
-// limb i of ciphertext blockIdx.z goes to digit i / alpha at position i.
-// grid (N / 256, nq, count).
-__global__ void __launch_bounds__(256)
-    k_copy_own_limbs(uint64_t* __restrict__ digits, const SrcPtrs src, uint32_t n,
-                     uint32_t alpha, uint32_t nd, uint32_t ne) {
-  const uint32_t i = blockIdx.y, ct = blockIdx.z;
-  const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const uint32_t d = i / alpha;
-  digits[(((size_t)ct * nd + d) * ne + i) * n + e] = src.p[ct][(size_t)i * n + e];
 }
 
 // ---- Fused middle of a batched ModDown, ring dimensions 2^13 .. 2^17 ----
@@ -1568,7 +1565,8 @@ void modup_fused(Context& c, const uint64_t* const* as, uint32_t count, uint32_t
     using G = Geo<B, RHO_EPILOGUE>;                                                           \
     const uint32_t tiles = (1u << s1) / (256 / G::TPL);                                       \
     FHE_LAUNCH(c, "ntt_inv_blocks_modup", (ntt_pass_modup_in<B>), dim3(tiles, count, nq),     \
-               dim3(256), 0, coef.p, (size_t)nq * n, c.d_const, c.d_tw_inv, c.log_n, s1, sp); \
+               dim3(256), 0, coef.p, (size_t)nq * n, c.d_const, c.d_tw_inv, c.log_n, s1, sp,  \
+               digits, c.alpha, nd, ne);                                                      \
     launch_mid<A, B>(c, "k_modup_mid", a, count * nd, max_src);                               \
     FHE_LAUNCH(c, "ntt_fwd_blocks_modup", (ntt_pass_modup_out<B>),                            \
                dim3(tiles, count * nd, ne - w_last), dim3(256), 0, digits, (size_t)ne * n,    \
@@ -1579,8 +1577,6 @@ void modup_fused(Context& c, const uint64_t* const* as, uint32_t count, uint32_t
 #undef CASE
     default: throw ArgError("unsupported ring dimension");
   }
-  FHE_LAUNCH(c, "k_copy_own_limbs", k_copy_own_limbs, dim3(c.n / 256, nq, count), dim3(256), 0,
-             digits, sp, c.n, c.alpha, nd, ne);
 }
 
 void ntt_forward_digits(Context& c, uint64_t* digits, uint32_t count, uint32_t nd,
