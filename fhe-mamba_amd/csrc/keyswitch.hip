@@ -499,7 +499,30 @@ void linear_transform(Context& c, uint64_t* out, const uint64_t* ct, uint32_t nq
     // Every giant step's inner sum, then their rotations by g giant strides
     // as one batch of independent key switches, then the sum.
     Scratch in(c, giants * pl), rot(c, (giants - 1) * pl);
-    for (uint32_t g = 0; g < giants; ++g) inner(g, in.p + g * pl, false);
+    // the babies some diagonal uses (the others were not formed)
+    std::vector<uint32_t> bu;
+    for (uint32_t b = 0; b < nb; ++b)
+      if (baby[b]) bu.push_back(b);
+    if (!bu.empty() && bu.size() <= MACG_MAX_B) {
+      // the inner sums of up to MACG_MAX_G giants per pass over the babies
+      const uint32_t nu = (uint32_t)bu.size();
+      std::vector<const uint64_t*> xs(nu);
+      std::vector<uint64_t*> acc(giants);
+      std::vector<const uint64_t*> w((size_t)giants * nu, nullptr);
+      for (uint32_t j = 0; j < nu; ++j) xs[j] = baby[bu[j]];
+      for (uint32_t g = 0; g < giants; ++g) {
+        acc[g] = in.p + g * pl;
+        for (uint32_t j = 0; j < nu; ++j) {
+          const uint32_t k = g * bstep + bu[j];
+          if (k < count) w[(size_t)g * nu + j] = pts[k];
+        }
+      }
+      for (uint32_t g0 = 0; g0 < giants; g0 += MACG_MAX_G)
+        poly_mac_giants(c, acc.data() + g0, std::min<uint32_t>(MACG_MAX_G, giants - g0),
+                        xs.data(), nu, w.data() + (size_t)g0 * nu, nq);
+    } else {
+      for (uint32_t g = 0; g < giants; ++g) inner(g, in.p + g * pl, false);
+    }
     std::vector<uint64_t*> ro(giants - 1);
     std::vector<const uint64_t*> ri(giants - 1);
     for (uint32_t g = 1; g < giants; ++g) {

@@ -40,6 +40,13 @@ struct MacTable {
 };
 void poly_mac_table(Context& c, uint64_t* acc, const uint64_t* const* x,
                     const uint64_t* const* w, uint32_t cnt, uint32_t nq, bool accumulate);
+// The inner sums of several giant steps of a BSGS transform in one pass:
+// acc[g] [2][nq][N] = sum_b x[b] (.) w[g * nb + b] for g < ng, b < nb, null
+// w entries skipped; every x word is read once for all g (up to
+// MACG_MAX_G giants and MACG_MAX_B babies per call).
+constexpr uint32_t MACG_MAX_G = 8, MACG_MAX_B = 32;
+void poly_mac_giants(Context& c, uint64_t* const* acc, uint32_t ng, const uint64_t* const* x,
+                     uint32_t nb, const uint64_t* const* w, uint32_t nq);
 // ModRaise: limb 0 of each of npoly polys of a ([npoly][a_nlimb][N],
 // evaluation form mod q0) to coefficient form, centred, lifted to
 // q_0..q_{nq_out-1} and back to evaluation form in out [npoly][nq_out][N].

@@ -328,6 +328,45 @@ LimbConsts make_consts(const Context& c, const uint64_t* consts, uint32_t nlimb)
   return k;
 }
 
+// Inner sums of up to MACG_MAX_G giant steps: each thread holds one word
+// position of both polys of every baby in turn and accumulates it into every
+// giant's sum (128-bit, one reduction each: at most 32 products of two
+// words below 2^61), so the babies are read once instead of once per giant.
+// grid (N / 256, nq).
+struct MacGiants {
+  const uint64_t* x[MACG_MAX_B];
+  const uint64_t* w[MACG_MAX_G][MACG_MAX_B];
+  uint64_t* acc[MACG_MAX_G];
+};
+
+template <int G>
+__global__ void __launch_bounds__(TPB)
+    k_mac_giants(const MacGiants t, const ModConst* mc, uint32_t n, uint32_t nq, uint32_t nb) {
+  const ModConst m = mc[blockIdx.y];
+  const size_t off = (size_t)blockIdx.y * n + (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t pl = (size_t)nq * n;
+  Acc128 s[G][2];
+  for (uint32_t b = 0; b < nb; ++b) {
+    const uint64_t* xb = t.x[b];
+    const uint64_t x0 = xb[off], x1 = xb[pl + off];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const uint64_t* w = t.w[g][b];
+      if (w) {
+        const uint64_t wv = w[off];
+        s[g][0].mac(x0, wv);
+        s[g][1].mac(x1, wv);
+      }
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    uint64_t* a = t.acc[g] + off;
+    a[0] = reduce128(s[g][0].hi, s[g][0].lo, m);
+    a[pl] = reduce128(s[g][1].hi, s[g][1].lo, m);
+  }
+}
+
 }  // namespace
 
 void poly_binary(Context& c, BinOp op, uint64_t* out, const uint64_t* a, const uint64_t* b,
@@ -425,6 +464,30 @@ void poly_rescale(Context& c, uint64_t* out, const uint64_t* a, uint32_t npoly, 
   FHE_LAUNCH(c, "k_rescale_lift", k_rescale_lift, grid_for(c, l, npoly), dim3(tpb_for(c)), 0, t.p, last.p, c.d_const, c.d_rescale, c.n, l, c.L, c.mods[l]);
   ntt_forward(c, t.p, npoly, (size_t)l * c.n, l, LimbMap::contiguous(0));
   FHE_LAUNCH(c, "k_rescale_combine", k_rescale_combine, grid_for(c, l, npoly), dim3(tpb_for(c)), 0, out, a, t.p, c.d_const, c.d_rescale, c.n, l, c.L);
+}
+
+
+void poly_mac_giants(Context& c, uint64_t* const* acc, uint32_t ng, const uint64_t* const* x,
+                     uint32_t nb, const uint64_t* const* w, uint32_t nq) {
+  if (nb == 0 || nb > MACG_MAX_B || ng > MACG_MAX_G) throw ArgError("giant-step inner sums");
+  if (ng == 0) return;
+  MacGiants t{};
+  for (uint32_t b = 0; b < nb; ++b) t.x[b] = x[b];
+  for (uint32_t g = 0; g < ng; ++g) {
+    t.acc[g] = acc[g];
+    for (uint32_t b = 0; b < nb; ++b) t.w[g][b] = w[(size_t)g * nb + b];
+  }
+  const uint32_t tpb = c.n < TPB ? c.n : TPB;
+  const dim3 grid(c.n / tpb, nq);
+  switch (ng) {
+#define CASE(G)                                                                           \
+  case G:                                                                                 \
+    FHE_LAUNCH(c, "k_mac_giants", k_mac_giants<G>, grid, dim3(tpb), 0, t, c.d_const, c.n, \
+               nq, nb);                                                                   \
+    break;
+    CASE(1) CASE(2) CASE(3) CASE(4) CASE(5) CASE(6) CASE(7) CASE(8)
+#undef CASE
+  }
 }
 
 }  // namespace fhe
