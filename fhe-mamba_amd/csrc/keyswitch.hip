@@ -530,8 +530,15 @@ void linear_transform(Context& c, uint64_t* out, const uint64_t* ct, uint32_t nq
       ri[g - 1] = in.p + g * pl;
     }
     rotate_many(c, ro.data(), ri.data(), nq, giant_keys, giant_galois, giants - 1);
-    poly_binary(c, OP_ADD, out, in.p, rot.p, 2, nq);
-    for (uint32_t g = 2; g < giants; ++g) poly_binary(c, OP_ADD, out, out, ro[g - 1], 2, nq);
+    if (giants <= SUM_MAX) {
+      std::vector<const uint64_t*> terms(giants);
+      terms[0] = in.p;
+      for (uint32_t g = 1; g < giants; ++g) terms[g] = ro[g - 1];
+      poly_sum(c, out, terms.data(), giants, 2, nq);
+    } else {
+      poly_binary(c, OP_ADD, out, in.p, rot.p, 2, nq);
+      for (uint32_t g = 2; g < giants; ++g) poly_binary(c, OP_ADD, out, out, ro[g - 1], 2, nq);
+    }
     return;
   }
   // Giant steps by Horner's rule: acc = inner_{G-1}; acc = inner_g + rot(acc).

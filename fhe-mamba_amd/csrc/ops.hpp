@@ -9,6 +9,10 @@ namespace fhe {
 enum BinOp { OP_ADD = 0, OP_SUB = 1 };
 
 // Elementwise (out may alias an input).
+// out = sum of cnt polys in[j] [npoly][nlimb][N] (cnt <= SUM_MAX), one pass.
+constexpr uint32_t SUM_MAX = 16;
+void poly_sum(Context& c, uint64_t* out, const uint64_t* const* in, uint32_t cnt,
+              uint32_t npoly, uint32_t nlimb);
 void poly_binary(Context& c, BinOp op, uint64_t* out, const uint64_t* a, const uint64_t* b,
                  uint32_t npoly, uint32_t nlimb);
 void poly_negate(Context& c, uint64_t* out, const uint64_t* a, uint32_t npoly, uint32_t nlimb);

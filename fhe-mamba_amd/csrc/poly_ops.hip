@@ -367,6 +367,24 @@ __global__ void __launch_bounds__(TPB)
   }
 }
 
+// out = sum_j in[j], reduced after every addition (values below q).
+struct SumTable {
+  const uint64_t* p[SUM_MAX];
+};
+__global__ void __launch_bounds__(TPB)
+    k_sum(uint64_t* out, const SumTable t, uint32_t cnt, const ModConst* mc, uint32_t n,
+          uint32_t nlimb) {
+  const uint64_t q = mc[blockIdx.y].q;
+  const size_t o = elem_off(n, nlimb);
+  U2 acc = ld2(t.p[0] + o);
+  for (uint32_t j = 1; j < cnt; ++j) {
+    const U2 v = ld2(t.p[j] + o);
+    acc.x = add_mod(acc.x, v.x, q);
+    acc.y = add_mod(acc.y, v.y, q);
+  }
+  st2(out + o, acc.x, acc.y);
+}
+
 }  // namespace
 
 void poly_binary(Context& c, BinOp op, uint64_t* out, const uint64_t* a, const uint64_t* b,
@@ -375,6 +393,15 @@ void poly_binary(Context& c, BinOp op, uint64_t* out, const uint64_t* a, const u
     FHE_LAUNCH(c, "k_binary", k_binary<OP_ADD>, grid_for(c, nlimb, npoly), dim3(tpb_for(c)), 0, out, a, b, c.d_const, c.n, nlimb);
   else
     FHE_LAUNCH(c, "k_binary", k_binary<OP_SUB>, grid_for(c, nlimb, npoly), dim3(tpb_for(c)), 0, out, a, b, c.d_const, c.n, nlimb);
+}
+
+void poly_sum(Context& c, uint64_t* out, const uint64_t* const* in, uint32_t cnt,
+              uint32_t npoly, uint32_t nlimb) {
+  if (cnt == 0 || cnt > SUM_MAX) throw ArgError("poly_sum: 1..16 inputs");
+  SumTable t{};
+  for (uint32_t j = 0; j < cnt; ++j) t.p[j] = in[j];
+  FHE_LAUNCH(c, "k_sum", k_sum, grid_for(c, nlimb, npoly), dim3(tpb_for(c)), 0, out, t, cnt,
+             c.d_const, c.n, nlimb);
 }
 
 void poly_negate(Context& c, uint64_t* out, const uint64_t* a, uint32_t npoly, uint32_t nlimb) {
