@@ -143,6 +143,12 @@ HOISTED = [
     (12, 4, 2, -11, ()),
     (7, 4, 1, 0, (2,)),
     (16, 4, 3, 5, (0, 13)),
+    # ten giants (inner sums in two passes of at most eight), one all-null
+    (40, 4, 1, 0, (8, 9, 10, 11, 30)),
+    # eighteen giants (the giant-step sum in pairwise additions past 16)
+    (36, 2, 1, 3, (7,)),
+    # more babies than one inner-sum pass takes (35 > 32)
+    (70, 35, 1, 0, (3, 40)),
 ]
 
 
