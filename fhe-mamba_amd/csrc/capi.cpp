@@ -838,6 +838,26 @@ int fhe_encode(fhe_context* ctx, const double* re, const double* im, uint32_t co
   });
 }
 
+int fhe_encode_many(fhe_context* ctx, const double* re, const double* im, uint32_t count,
+                    uint32_t nvec, uint32_t slots, double scale, uint32_t nlimb,
+                    fhe_poly* const* outs) {
+  return guard([&] {
+    need(ctx && (outs || nvec == 0) && (re || count == 0 || nvec == 0), "null argument");
+    fhe::Context& c = *ctx->c;
+    std::vector<uint64_t*> ptrs(nvec);
+    std::vector<const fhe_poly*> seen(outs, outs + nvec);
+    for (const fhe_poly* o : seen) need(o && o->c == ctx->c, "null argument");
+    std::sort(seen.begin(), seen.end());
+    need(std::adjacent_find(seen.begin(), seen.end()) == seen.end(), "an output appears twice");
+    for (uint32_t r = 0; r < nvec; ++r) {
+      prepare_out(outs[r], 1, nlimb);
+      ptrs[r] = outs[r]->data;
+    }
+    if (!fhe::encode_many(c, re, im, count, nvec, slots, scale, nlimb, ptrs.data()))
+      throw std::out_of_range("encode: a scaled coefficient does not fit in 62 bits");
+  });
+}
+
 int fhe_decode(fhe_context* ctx, const fhe_poly* pt, uint32_t slots, double scale, double* re,
                double* im) {
   return guard([&] {

@@ -224,6 +224,18 @@ struct LimbMap {
   }
 };
 
+// Polys held in separate allocations: launch poly p lives at table[p] (a
+// device array of poly base pointers, [nlimb][N] each); limb j uses
+// modulus j.
+struct TableMap {
+  uint64_t* const* table;
+  FHE_HD bool resolve(uint32_t, uint32_t j, uint32_t& pos, uint32_t& mod) const {
+    pos = j;
+    mod = j;
+    return true;
+  }
+};
+
 // The converted limbs of ModUp digits [nd][ne][N]: digit (poly) d keeps its
 // own limbs [d*alpha, min((d+1)*alpha, nq)) of Q; slot t walks the other
 // limbs of Q_l + P in order (position pos, modulus pos < nq ? pos :
@@ -325,6 +337,9 @@ void ntt_forward(Context& c, uint64_t* data, uint32_t npoly, size_t poly_stride,
                  uint32_t nlimb, LimbMap map);
 void ntt_inverse(Context& c, uint64_t* data, uint32_t npoly, size_t poly_stride,
                  uint32_t nlimb, LimbMap map);
+// Forward NTT of npoly one-poly [nlimb][N] operands held in separate
+// allocations; `table` is a device array of their npoly base pointers.
+void ntt_forward_table(Context& c, uint64_t* const* table, uint32_t npoly, uint32_t nlimb);
 // Forward NTT of y [npoly][nq][N] (limb j mod q_j) whose last pass stores
 // through the ModDown epilogue instead of writing y back.
 void ntt_forward_moddown(Context& c, uint64_t* y, uint32_t npoly, uint32_t nq,

@@ -70,9 +70,11 @@ std::pair<double*, double*> fft_tables(Context& c, uint32_t slots) {
 }
 
 // One stage of the special inverse FFT: (a, b) -> (a + b, (a - b) * w).
+// Vector blockIdx.y of a batch of `slots`-value vectors.
 __global__ void k_fft_inv_stage(double2* v, const double* tw, uint32_t slots, uint32_t len) {
   const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= slots / 2) return;
+  v += (size_t)blockIdx.y * slots;
   const uint32_t h = len / 2, j = t % h, i = (t / h) * len + j;
   const double2 a = v[i], b = v[i + h];
   const double wr = tw[2 * (h - 1 + j)], wi = tw[2 * (h - 1 + j) + 1];
@@ -85,6 +87,7 @@ __global__ void k_fft_inv_stage(double2* v, const double* tw, uint32_t slots, ui
 __global__ void k_fft_fwd_stage(double2* v, const double* tw, uint32_t slots, uint32_t len) {
   const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= slots / 2) return;
+  v += (size_t)blockIdx.y * slots;
   const uint32_t h = len / 2, j = t % h, i = (t / h) * len + j;
   const double2 u = v[i], b = v[i + h];
   const double wr = tw[2 * (h - 1 + j)], wi = tw[2 * (h - 1 + j) + 1];
@@ -154,12 +157,17 @@ __device__ __forceinline__ uint64_t lift_signed(int64_t x, uint64_t q) {
 }
 
 // Round slot i of the transformed vector (read through the bit reversal)
-// and scatter its real / imaginary coefficient into every limb.
-__global__ void k_round_lift(const double2* v, uint64_t* out, const ModConst* mc, uint32_t slots,
-                             uint32_t bits, uint32_t gap, uint32_t n, uint32_t nlimb, double scale,
-                             int* status) {
+// and scatter its real / imaginary coefficient into every limb.  With a
+// table, vector blockIdx.y of the batch goes to table[blockIdx.y].
+__global__ void k_round_lift(const double2* v, uint64_t* out, uint64_t* const* table,
+                             const ModConst* mc, uint32_t slots, uint32_t bits, uint32_t gap,
+                             uint32_t n, uint32_t nlimb, double scale, int* status) {
   const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= slots) return;
+  if (table) {
+    v += (size_t)blockIdx.y * slots;
+    out = table[blockIdx.y];
+  }
   const double2 x = v[brev_bits(i, bits)];
   const double a = (x.x / (double)slots) * scale, b = (x.y / (double)slots) * scale;
   const double lim = 4611686018427387904.0;  // 2^62
@@ -212,22 +220,25 @@ __global__ void k_crt_decode(const uint64_t* coef, double2* v, const ModConst* m
   dst[t < slots ? 0 : 1] = val;
 }
 
-void run_stages(Context& c, double2* v, const double* tw, uint32_t slots, bool inverse) {
+// The special FFT of nvec contiguous vectors of `slots` values each.  The
+// block kernels' blocks of `top` values never straddle two vectors (top
+// divides slots), so they run over the batch as one array.
+void run_stages(Context& c, double2* v, const double* tw, uint32_t slots, bool inverse,
+                uint32_t nvec = 1) {
   if (slots < 2) return;
   const uint32_t threads = slots / 2 < TPB ? slots / 2 : TPB;
   const uint32_t blocks = (slots / 2 + threads - 1) / threads;
   const uint32_t top = slots < FFT_BLOCK ? slots : FFT_BLOCK;
   const uint32_t bthreads = top / 2 < TPB ? top / 2 : TPB;
+  const uint32_t nblk = nvec * (slots / top);
   if (inverse) {
     for (uint32_t len = slots; len > top; len >>= 1)
-      FHE_LAUNCH(c, "k_fft_inv_stage", k_fft_inv_stage, dim3(blocks), dim3(threads), 0, v, tw, slots, len);
-    FHE_LAUNCH(c, "k_fft_inv_block", k_fft_inv_block, dim3(slots / top), dim3(bthreads), 0, v, tw,
-               top);
+      FHE_LAUNCH(c, "k_fft_inv_stage", k_fft_inv_stage, dim3(blocks, nvec), dim3(threads), 0, v, tw, slots, len);
+    FHE_LAUNCH(c, "k_fft_inv_block", k_fft_inv_block, dim3(nblk), dim3(bthreads), 0, v, tw, top);
   } else {
-    FHE_LAUNCH(c, "k_fft_fwd_block", k_fft_fwd_block, dim3(slots / top), dim3(bthreads), 0, v, tw,
-               top);
+    FHE_LAUNCH(c, "k_fft_fwd_block", k_fft_fwd_block, dim3(nblk), dim3(bthreads), 0, v, tw, top);
     for (uint32_t len = 2 * top; len <= slots; len <<= 1)
-      FHE_LAUNCH(c, "k_fft_fwd_stage", k_fft_fwd_stage, dim3(blocks), dim3(threads), 0, v, tw, slots, len);
+      FHE_LAUNCH(c, "k_fft_fwd_stage", k_fft_fwd_stage, dim3(blocks, nvec), dim3(threads), 0, v, tw, slots, len);
   }
 }
 
@@ -281,7 +292,7 @@ bool encode(Context& c, const double* re, const double* im, uint32_t count, uint
   const uint32_t threads = slots < TPB ? slots : TPB;
   // k_round_lift writes every coefficient of the nlimb limbs (the slots'
   // positions and the zeros between them).
-  FHE_LAUNCH(c, "k_round_lift", k_round_lift, dim3((slots + threads - 1) / threads), dim3(threads), 0, reinterpret_cast<const double2*>(v.p), out, c.d_const, slots, ilog2(slots), c.n / (2 * slots), c.n, nlimb, scale, checked ? reinterpret_cast<int*>(st.p) : nullptr);
+  FHE_LAUNCH(c, "k_round_lift", k_round_lift, dim3((slots + threads - 1) / threads), dim3(threads), 0, reinterpret_cast<const double2*>(v.p), out, nullptr, c.d_const, slots, ilog2(slots), c.n / (2 * slots), c.n, nlimb, scale, checked ? reinterpret_cast<int*>(st.p) : nullptr);
   if (checked) {
     int status = 0;
     hip_check(hipMemcpyAsync(&status, st.p, sizeof(int), hipMemcpyDeviceToHost, c.stream),
@@ -290,6 +301,71 @@ bool encode(Context& c, const double* re, const double* im, uint32_t count, uint
     if (status) return false;
   }
   ntt_forward(c, out, 1, 0, nlimb, LimbMap::contiguous(0));
+  return true;
+}
+
+bool encode_many(Context& c, const double* re, const double* im, uint32_t count, uint32_t nvec,
+                 uint32_t slots, double scale, uint32_t nlimb, uint64_t* const* outs) {
+  check_slots(c, slots);
+  if (count > slots) throw ArgError("more values than slots");
+  if (nlimb == 0 || nlimb > c.L) throw ArgError("bad limb count");
+  if (!(scale > 0) || !std::isfinite(scale)) throw ArgError("scale must be positive");
+  const double lim = 4611686018427387904.0 * (1.0 - 0x1p-20) / scale;
+  const double lim2 = lim * lim;
+  const auto tw = fft_tables(c, slots);
+  // Up to kChunk vectors share one staging copy and one set of launches:
+  // the pointer table (padded to 16 bytes) and then the vectors' values.
+  constexpr uint32_t kChunk = 16;
+  for (uint32_t r0 = 0; r0 < nvec; r0 += kChunk) {
+    const uint32_t m = nvec - r0 < kChunk ? nvec - r0 : kChunk;
+    bool over = !(lim2 < INFINITY);
+    for (uint32_t r = r0; r < r0 + m && !over; ++r)
+      for (uint32_t j = 0; j < count; ++j) {
+        const double a = re[(size_t)r * count + j], b = im ? im[(size_t)r * count + j] : 0.0;
+        if (!(a * a + b * b < lim2)) {
+          over = true;
+          break;
+        }
+      }
+    if (over) {
+      // Values that may not fit take the checked single path, which
+      // reports the first vector that fails.
+      for (uint32_t r = r0; r < r0 + m; ++r)
+        if (!encode(c, re + (size_t)r * count, im ? im + (size_t)r * count : nullptr, count, slots,
+                    scale, nlimb, outs[r]))
+          return false;
+      continue;
+    }
+    const size_t tab_words = (m + 1) & ~1u, vec_words = 2 * (size_t)slots;
+    const size_t words = tab_words + m * vec_words;
+    Scratch buf(c, words);
+    double2* v = reinterpret_cast<double2*>(buf.p + tab_words);
+    {
+      std::lock_guard<std::mutex> g(c.staging_mu);
+      Context::Staging& sg = c.staging_slot(words * 8);
+      uint64_t* host = static_cast<uint64_t*>(sg.host);
+      for (uint32_t r = 0; r < m; ++r) host[r] = reinterpret_cast<uint64_t>(outs[r0 + r]);
+      double* hv = reinterpret_cast<double*>(host + tab_words);
+      for (uint32_t r = 0; r < m; ++r) {
+        const double* rr = re + (size_t)(r0 + r) * count;
+        const double* ri = im ? im + (size_t)(r0 + r) * count : nullptr;
+        double* h = hv + r * vec_words;
+        for (uint32_t j = 0; j < count; ++j) {
+          h[2 * j] = rr[j];
+          h[2 * j + 1] = ri ? ri[j] : 0.0;
+        }
+        std::memset(h + 2 * (size_t)count, 0, (vec_words - 2 * (size_t)count) * sizeof(double));
+      }
+      hip_check(hipMemcpyAsync(buf.p, host, words * 8, hipMemcpyHostToDevice, c.stream),
+                "encode upload");
+      hip_check(hipEventRecord(sg.done, c.stream), "encode staging event");
+    }
+    uint64_t* const* table = reinterpret_cast<uint64_t* const*>(buf.p);
+    run_stages(c, v, tw.first, slots, true, m);
+    const uint32_t threads = slots < TPB ? slots : TPB;
+    FHE_LAUNCH(c, "k_round_lift", k_round_lift, dim3((slots + threads - 1) / threads, m), dim3(threads), 0, v, nullptr, table, c.d_const, slots, ilog2(slots), c.n / (2 * slots), c.n, nlimb, scale, nullptr);
+    ntt_forward_table(c, table, m, nlimb);
+  }
   return true;
 }
 

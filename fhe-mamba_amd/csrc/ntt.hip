@@ -52,6 +52,17 @@ __device__ __forceinline__ uint32_t lds_idx(uint32_t line, uint32_t u, uint32_t 
   return line * pitch + u + (u >> 4);
 }
 
+// Base of launch poly p: data + p * poly_stride, or the table's entry for
+// polys held in separate allocations.
+template <class Map>
+__device__ __forceinline__ uint64_t* poly_base(const Map&, uint64_t* data, size_t poly_stride,
+                                               uint32_t p) {
+  return data + (size_t)p * poly_stride;
+}
+__device__ __forceinline__ uint64_t* poly_base(const TableMap& m, uint64_t*, size_t, uint32_t p) {
+  return m.table[p];
+}
+
 // Final stores go through `store.fin(base, offset_in_limb, value, t, q)`,
 // with t = store.pre(offset_in_limb, q) when Store::kPre.
 // The first pass's input comes from `load.get(offset_in_limb, q)` instead
@@ -114,7 +125,7 @@ __device__ __forceinline__ void ntt_body(uint64_t* __restrict__ data, size_t pol
   // every prime is below 2^61.
   const uint64_t q = mc[midx].q, q4 = 4 * q, qneg = mc[midx].neg_q, q4neg = mc[midx].neg_q4;
   const uint64_t* __restrict__ tw = tw_all + (size_t)midx * n * 2;
-  uint64_t* __restrict__ base = data + (size_t)blockIdx.y * poly_stride + (size_t)pos * n;
+  uint64_t* __restrict__ base = poly_base(map, data, poly_stride, blockIdx.y) + (size_t)pos * n;
 
   const uint32_t tid = threadIdx.x;
   uint32_t line, tau;
@@ -1659,6 +1670,19 @@ void ntt_forward(Context& c, uint64_t* data, uint32_t npoly, size_t poly_stride,
   const uint32_t s1 = (c.log_n + 1) / 2, s2 = c.log_n / 2;
   launch_cols<false>(c, s1, s2, data, npoly, poly_stride, nlimb, map, false);
   launch_blocks<false>(c, s1, s2, data, npoly, poly_stride, nlimb, map, true);
+}
+
+void ntt_forward_table(Context& c, uint64_t* const* table, uint32_t npoly, uint32_t nlimb) {
+  if (npoly == 0 || nlimb == 0) return;
+  if (npoly > 65535 || nlimb > c.L + c.K) throw ArgError("too many polys or limbs in one launch");
+  const TableMap map{table};
+  if (c.log_n <= 12) {
+    launch_single<false>(c, nullptr, npoly, 0, nlimb, map);
+    return;
+  }
+  const uint32_t s1 = (c.log_n + 1) / 2, s2 = c.log_n / 2;
+  launch_cols<false>(c, s1, s2, nullptr, npoly, 0, nlimb, map, false);
+  launch_blocks<false>(c, s1, s2, nullptr, npoly, 0, nlimb, map, true);
 }
 
 void ntt_inverse(Context& c, uint64_t* data, uint32_t npoly, size_t poly_stride, uint32_t nlimb,

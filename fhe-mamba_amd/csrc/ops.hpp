@@ -130,6 +130,10 @@ void key_from_montgomery(Context& c, uint64_t* out, const uint64_t* key);
 // Returns false if a scaled coefficient does not fit.
 bool encode(Context& c, const double* re, const double* im, uint32_t count, uint32_t slots,
             double scale, uint32_t nlimb, uint64_t* out);
+// nvec vectors of `count` values each (row r at re + r * count), one
+// [nlimb][N] output per vector; the same result as nvec encode calls.
+bool encode_many(Context& c, const double* re, const double* im, uint32_t count, uint32_t nvec,
+                 uint32_t slots, double scale, uint32_t nlimb, uint64_t* const* outs);
 void decode(Context& c, const uint64_t* pt, uint32_t nlimb, uint32_t slots, double scale,
             double* re, double* im);
 

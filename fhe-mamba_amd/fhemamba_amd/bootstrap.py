@@ -349,9 +349,13 @@ class CKKSBootstrapper:
         key = (which, idx, level, factor)
         pts = self._pts.get(key)
         if pts is None:
-            pts = [None if d is None else
-                   self.cc.MakeCKKSPackedPlaintext(d * factor, 1, level, slots=self.n)
-                   for d in plan.prerotated()]
+            diags = plan.prerotated()
+            rows = [d * factor for d in diags if d is not None]
+            batch = getattr(self.cc, "MakeCKKSPackedPlaintexts", None)
+            many = batch(rows, 1, level, slots=self.n) if batch else \
+                [self.cc.MakeCKKSPackedPlaintext(r, 1, level, slots=self.n) for r in rows]
+            it = iter(many)
+            pts = [None if d is None else next(it) for d in diags]
             self._pts.put(key, pts)
         return pts
 

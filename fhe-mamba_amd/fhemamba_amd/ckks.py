@@ -436,6 +436,38 @@ class CryptoContext:
                                 params=None, slots: int = 0) -> "Plaintext":
         return self._encode(values, int(level), int(noiseScaleDeg), int(slots) or self._slots)
 
+    def MakeCKKSPackedPlaintexts(self, rows, noiseScaleDeg: int = 1, level: int = 0,  # noqa: N802,N803
+                                 slots: int = 0) -> list:
+        """MakeCKKSPackedPlaintext of every vector in `rows` at one level and
+        degree, encoded in shared launches (fhe_encode_many): the same
+        plaintexts as one call per vector."""
+        level, deg, slots = int(level), int(noiseScaleDeg), int(slots) or self._slots
+        if not 0 <= level < self.L:
+            raise ValueError(f"level {level} outside [0, {self.L - 1}]")
+        if deg not in (1, 2):
+            raise ValueError("noise scale degree must be 1 or 2")
+        vals = [np.asarray(r).ravel() for r in rows]
+        if not vals:
+            return []
+        width = max(len(v) for v in vals)
+        if width > slots:
+            raise ValueError(f"{width} values do not fit {slots} slots")
+        cplx = any(np.iscomplexobj(v) for v in vals)
+        mat = np.zeros((len(vals), width), dtype=np.complex128 if cplx else np.float64)
+        for i, v in enumerate(vals):
+            mat[i, :len(v)] = v
+        nq = self.L - level
+        sf = self._sf[level]
+        polys = self._ctx.encode_many(mat, slots, sf, nq)
+        scale = sf
+        if deg == 2:
+            c = int(round(sf))
+            res = self._const_residues(c, nq)
+            for p in polys:
+                self._ctx.mul_const(p, res, out=p)
+            scale = sf * c
+        return [Plaintext(self, p, level, deg, scale, slots, v) for p, v in zip(polys, vals)]
+
     def _const_residues(self, c: int, nq: int) -> np.ndarray:
         return np.array([c % qi for qi in self._ctx.q[:nq]], dtype=np.uint64)
 

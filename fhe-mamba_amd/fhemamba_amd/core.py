@@ -300,6 +300,20 @@ class Context:
              out.handle)
         return out
 
+    def encode_many(self, rows, slots: int, scale: float, nlimb: int) -> list:
+        """One encode per row of `rows` (equal-length value vectors) in shared
+        launches; the same polys as encode() of each row."""
+        v = np.asarray(rows)
+        if v.ndim != 2:
+            raise ValueError("encode_many takes a 2-D array of rows")
+        re = np.ascontiguousarray(np.real(v), dtype=np.float64)
+        im = np.ascontiguousarray(np.imag(v), dtype=np.float64) if np.iscomplexobj(v) else None
+        outs = [Poly(self, 1, nlimb) for _ in range(v.shape[0])]
+        hs = (ctypes.c_void_p * max(len(outs), 1))(*([o.handle.value for o in outs] or [None]))
+        call("fhe_encode_many", self.handle, _ptr(re), _ptr(im) if im is not None else None,
+             v.shape[1], v.shape[0], slots, float(scale), nlimb, hs)
+        return outs
+
     def decode(self, pt, slots: int, scale: float) -> np.ndarray:
         re = np.zeros(slots)
         im = np.zeros(slots)

@@ -120,6 +120,9 @@ class KeyPlanContext:
     def MakeCKKSPackedPlaintext(self, values, deg=1, level=0, slots=0):  # noqa: N802
         return _SymPlain(int(level), int(deg))
 
+    def MakeCKKSPackedPlaintexts(self, rows, deg=1, level=0, slots=0):  # noqa: N802
+        return [_SymPlain(int(level), int(deg)) for _ in rows]
+
     def Encrypt(self, key, pt):  # noqa: N802
         return _SymCt(pt.level)
 

@@ -553,6 +553,14 @@ class PackedEvaluator:
             out = term if out is None else self.add(out, term)
         return out
 
+    def _encode_rows(self, rows, level: int) -> list:
+        """Degree-1 plaintexts of the slot vectors `rows` at `level`, in one
+        batched encode where the context offers it."""
+        many = getattr(self.cc, "MakeCKKSPackedPlaintexts", None)
+        if many is not None:
+            return many(rows, 1, level, slots=self.slots)
+        return [self.cc.MakeCKKSPackedPlaintext(r, 1, level, slots=self.slots) for r in rows]
+
     def _transform_bsgs(self, x, offs, step, masks, key):
         rows = len(offs)
         b = max(2, 1 << round(math.log2(math.sqrt(rows))))
@@ -562,9 +570,8 @@ class PackedEvaluator:
         ck = None if key is None else (key, "bsgs", level)
         pts = self._pt_cache.get(ck) if ck else None
         if pts is None:
-            pts = [self.cc.MakeCKKSPackedPlaintext(np.roll(masks[o], (k // b) * b * step), 1,
-                                                   level, slots=self.slots)
-                   for k, o in enumerate(offs)]
+            pts = self._encode_rows([np.roll(masks[o], (k // b) * b * step)
+                                     for k, o in enumerate(offs)], level)
             if ck:
                 self._pt_cache.put(ck, pts)
         giants = -(-rows // b)
@@ -615,9 +622,8 @@ class PackedEvaluator:
             cache_key = (key, "replicated", rep.GetLevel())
             pts = self._pt_cache.get(cache_key)
             if pts is None:
-                pts = [self.cc.MakeCKKSPackedPlaintext(mask, 1, rep.GetLevel(),
-                                                       slots=self.slots)
-                       for mask in self._replicated_masks(W, shape, b, stride, key)]
+                pts = self._encode_rows(self._replicated_masks(W, shape, b, stride, key),
+                                        rep.GetLevel())
                 self._pt_cache.put(cache_key, pts)
             self._ensure_keys(bsgs_rotations(shape.per_replica, b, stride))
             giants = -(-shape.per_replica // b)

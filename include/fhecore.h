@@ -241,6 +241,17 @@ int fhe_linear_transform_hoisted(fhe_poly *out, const fhe_poly *ct,
 int fhe_encode(fhe_context *ctx, const double *re, const double *im,
                uint32_t count, uint32_t slots, double scale, uint32_t nlimb,
                fhe_poly *out);
+/* nvec encodes in one call: row r of re / im (count values each, im may be
+ * NULL) into outs[r], each as fhe_encode would write it.  Replaces the
+ * reference decoder's look-ahead batches of MakeCKKSPackedPlaintext calls for
+ * uncached BSGS diagonals (stage1_mamba2_decode_fideslib.cpp:165-167,
+ * :440-447).  The vectors share the FFT, rounding and NTT launches, up to 16
+ * per set.  A row whose values may not fit 62 bits after scaling is encoded
+ * by the checked single path; FHE_ERR_RANGE names the first that fails (the
+ * outputs of earlier rows are then written).  Outputs must be distinct. */
+int fhe_encode_many(fhe_context *ctx, const double *re, const double *im,
+                    uint32_t count, uint32_t nvec, uint32_t slots, double scale,
+                    uint32_t nlimb, fhe_poly *const *outs);
 /* Decode a decrypted one-poly plaintext: iNTT, centred CRT, /scale and the
  * forward special FFT (GetRealPackedValue, packed_fideslib.cpp:1227-1236). */
 int fhe_decode(fhe_context *ctx, const fhe_poly *pt, uint32_t slots,

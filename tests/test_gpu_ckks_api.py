@@ -231,3 +231,18 @@ def test_errors(env):
     ct = c2.Encrypt(k2.publicKey, c2.MakeCKKSPackedPlaintext([1.0]))
     with pytest.raises(KeyError):  # no relinearization key yet
         c2.EvalMult(ct, ct)
+
+
+def test_batched_plaintexts_equal_single(env):
+    """MakeCKKSPackedPlaintexts (one batched encode) gives the residues,
+    level, degree and scale of MakeCKKSPackedPlaintext per vector, degree 2
+    included, for rows of unequal length."""
+    cc, _ = env
+    rows = [vec(40 + i, n) for i, n in enumerate((SLOTS, 5, SLOTS, 33))]
+    for level, deg in ((0, 1), (3, 1), (2, 2)):
+        many = cc.MakeCKKSPackedPlaintexts(rows, deg, level, slots=SLOTS)
+        for r, p in zip(rows, many):
+            one = cc.MakeCKKSPackedPlaintext(list(r), deg, level, None, SLOTS)
+            assert np.array_equal(p.poly.numpy(), one.poly.numpy())
+            assert (p.level, p.deg, p.scale, p.slots) == (one.level, one.deg, one.scale, one.slots)
+    assert cc.MakeCKKSPackedPlaintexts([], 1, 0) == []

@@ -69,6 +69,49 @@ def test_encode_out_of_range_raises(pair):
         ctx.encode([2.0**30], 8, 2.0**40, 1)
 
 
+@pytest.mark.parametrize("nvec,slots_div", [(1, 2), (5, 8), (16, 2), (37, 64)])
+def test_encode_many_equals_single_encodes(pair, nvec, slots_div):
+    """fhe_encode_many (shared FFT, rounding and NTT launches, outputs
+    reached through a device table, sets of 16 rows) writes every row's
+    plaintext exactly as one encode per row: complex rows at one and all
+    limbs, and short real rows against the oracle."""
+    ctx, orc = pair
+    slots = ctx.n // slots_div
+    rng = np.random.default_rng(nvec * 7 + slots_div)
+    scale = float(ctx.q[-1])
+    rows = rng.uniform(-1, 1, (nvec, slots)) + 1j * rng.uniform(-1, 1, (nvec, slots))
+    for nq in (1, ctx.L):
+        got = ctx.encode_many(rows, slots, scale, nq)
+        assert len(got) == nvec
+        for r, g in zip(rows, got):
+            assert np.array_equal(g.numpy()[0], ctx.encode(r, slots, scale, nq).numpy()[0])
+    real = rng.uniform(-3, 3, (nvec, 17))
+    got = ctx.encode_many(real, slots, 2.0**40, 2)
+    for r, g in zip(real[:3], got[:3]):
+        assert np.array_equal(g.numpy()[0], orc.encode(r, slots, 2.0**40, 2))
+    for r, g in zip(real[3:], got[3:]):
+        assert np.array_equal(g.numpy()[0], ctx.encode(r, slots, 2.0**40, 2).numpy()[0])
+
+
+def test_encode_many_checked_rows_and_errors(pair):
+    """A set holding a row over the host bound takes the checked single path:
+    rows whose coefficients fit still match the oracle; a row that does not
+    fit raises OverflowError; zero rows encode nothing."""
+    ctx, orc = pair
+    slots = ctx.n // 2
+    scale = 2.0**40
+    rows = np.zeros((3, slots), dtype=complex)
+    rows[0, 5] = 0.25
+    rows[1, 3] = 1.5 * 2.0**22 + 0.5j * 2.0**22  # over the bound, coefficients fit
+    rows[2, 7] = -0.75
+    got = ctx.encode_many(rows, slots, scale, 2)
+    for r, g in zip(rows, got):
+        assert np.array_equal(g.numpy()[0], orc.encode(r, slots, scale, 2))
+    with pytest.raises(OverflowError):
+        ctx.encode_many(np.full((2, 8), 2.0**30), 8, scale, 1)
+    assert ctx.encode_many(np.zeros((0, 8)), 8, scale, 1) == []
+
+
 def test_encrypt_decrypt_match_oracle(pair):
     ctx, orc = pair
     s = orc.secret(3)
