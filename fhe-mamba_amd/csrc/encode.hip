@@ -156,9 +156,20 @@ __device__ __forceinline__ uint64_t lift_signed(int64_t x, uint64_t q) {
   return r ? q - r : 0;
 }
 
+// x mod q for |x| < 2^63 by a Barrett step with mu64 = floor(2^64 / q): the
+// quotient estimate mulhi(|x|, mu64) is at most 1 below the true quotient,
+// so one conditional subtraction completes the reduction.
+__device__ __forceinline__ uint64_t lift_signed_mc(int64_t x, const ModConst& m) {
+  const uint64_t a = x >= 0 ? (uint64_t)x : (uint64_t)0 - (uint64_t)x;
+  uint64_t r = a - mulhi64(a, m.mu64) * m.q;
+  r = r >= m.q ? r - m.q : r;
+  return (x >= 0 || r == 0) ? r : m.q - r;
+}
+
 // Round slot i of the transformed vector (read through the bit reversal)
-// and scatter its real / imaginary coefficient into every limb.  With a
-// table, vector blockIdx.y of the batch goes to table[blockIdx.y].
+// and scatter its real / imaginary coefficient into limbs blockIdx.z,
+// blockIdx.z + gridDim.z, ...  With a table, vector blockIdx.y of the
+// batch goes to table[blockIdx.y].
 __global__ void k_round_lift(const double2* v, uint64_t* out, uint64_t* const* table,
                              const ModConst* mc, uint32_t slots, uint32_t bits, uint32_t gap,
                              uint32_t n, uint32_t nlimb, double scale, int* status) {
@@ -176,11 +187,10 @@ __global__ void k_round_lift(const double2* v, uint64_t* out, uint64_t* const* t
     return;
   }
   const int64_t ra = llround(a), rb = llround(b);
-  for (uint32_t j = 0; j < nlimb; ++j) {
-    const uint64_t q = mc[j].q;
+  for (uint32_t j = blockIdx.z; j < nlimb; j += gridDim.z) {
     uint64_t* o = out + (size_t)j * n;
-    o[(size_t)i * gap] = lift_signed(ra, q);
-    o[(size_t)(i + slots) * gap] = lift_signed(rb, q);
+    o[(size_t)i * gap] = lift_signed_mc(ra, mc[j]);
+    o[(size_t)(i + slots) * gap] = lift_signed_mc(rb, mc[j]);
     // the other coefficients of this slot's two gap blocks are zero
     for (uint32_t z = 1; z < gap; ++z) {
       o[(size_t)i * gap + z] = 0;
@@ -292,7 +302,7 @@ bool encode(Context& c, const double* re, const double* im, uint32_t count, uint
   const uint32_t threads = slots < TPB ? slots : TPB;
   // k_round_lift writes every coefficient of the nlimb limbs (the slots'
   // positions and the zeros between them).
-  FHE_LAUNCH(c, "k_round_lift", k_round_lift, dim3((slots + threads - 1) / threads), dim3(threads), 0, reinterpret_cast<const double2*>(v.p), out, nullptr, c.d_const, slots, ilog2(slots), c.n / (2 * slots), c.n, nlimb, scale, checked ? reinterpret_cast<int*>(st.p) : nullptr);
+  FHE_LAUNCH(c, "k_round_lift", k_round_lift, dim3((slots + threads - 1) / threads, 1, nlimb), dim3(threads), 0, reinterpret_cast<const double2*>(v.p), out, nullptr, c.d_const, slots, ilog2(slots), c.n / (2 * slots), c.n, nlimb, scale, checked ? reinterpret_cast<int*>(st.p) : nullptr);
   if (checked) {
     int status = 0;
     hip_check(hipMemcpyAsync(&status, st.p, sizeof(int), hipMemcpyDeviceToHost, c.stream),
@@ -363,7 +373,7 @@ bool encode_many(Context& c, const double* re, const double* im, uint32_t count,
     uint64_t* const* table = reinterpret_cast<uint64_t* const*>(buf.p);
     run_stages(c, v, tw.first, slots, true, m);
     const uint32_t threads = slots < TPB ? slots : TPB;
-    FHE_LAUNCH(c, "k_round_lift", k_round_lift, dim3((slots + threads - 1) / threads, m), dim3(threads), 0, v, nullptr, table, c.d_const, slots, ilog2(slots), c.n / (2 * slots), c.n, nlimb, scale, nullptr);
+    FHE_LAUNCH(c, "k_round_lift", k_round_lift, dim3((slots + threads - 1) / threads, m, nlimb), dim3(threads), 0, v, nullptr, table, c.d_const, slots, ilog2(slots), c.n / (2 * slots), c.n, nlimb, scale, nullptr);
     ntt_forward_table(c, table, m, nlimb);
   }
   return true;
