@@ -409,6 +409,29 @@ int fhe_mul_const(fhe_poly* out, const fhe_poly* a, const uint64_t* cst) {
   });
 }
 
+int fhe_linear_wsum(fhe_poly* out, const fhe_poly* const* xs, const uint64_t* weights,
+                    uint32_t count, uint32_t nlimb) {
+  return guard([&] {
+    need(out && xs && weights && count > 0, "null argument");
+    fhe::Context& c = *out->c;
+    need(nlimb >= 1 && nlimb <= c.L, "bad limb count");
+    std::vector<const uint64_t*> ptrs(count);
+    std::vector<uint32_t> nl(count);
+    for (uint32_t i = 0; i < count; ++i) {
+      need(xs[i] != nullptr, "null argument");
+      same_ctx(out, xs[i]);
+      need(xs[i] != out, "the output may not alias a term");
+      need(xs[i]->npoly == 2 && xs[i]->nlimb >= nlimb, "terms are 2-poly ciphertexts with nlimb limbs");
+    }
+    prepare_out(out, 2, nlimb);
+    for (uint32_t i = 0; i < count; ++i) {
+      ptrs[i] = xs[i]->data;
+      nl[i] = xs[i]->nlimb;
+    }
+    fhe::poly_linear_wsum(c, out->data, ptrs.data(), nl.data(), weights, count, nlimb);
+  });
+}
+
 int fhe_add_const(fhe_poly* out, const fhe_poly* a, const uint64_t* cst) {
   return guard([&] {
     same_ctx(out, a);

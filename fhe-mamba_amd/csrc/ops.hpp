@@ -44,6 +44,12 @@ struct MacTable {
 };
 void poly_mac_table(Context& c, uint64_t* acc, const uint64_t* const* x,
                     const uint64_t* const* w, uint32_t cnt, uint32_t nq, bool accumulate);
+// out [2][nq][N] = sum_i m_i * x_i mod q_j over ciphertexts x_i [2][nl_i][N]
+// (nl_i >= nq; their first nq limbs), with integer weights m_i given as
+// two's-complement 128-bit values (lo, hi); up to WSUM_MAX terms per launch.
+constexpr uint32_t WSUM_MAX = 16;
+void poly_linear_wsum(Context& c, uint64_t* out, const uint64_t* const* x, const uint32_t* x_nlimb,
+                      const uint64_t* weights, uint32_t cnt, uint32_t nq);
 // The inner sums of several giant steps of a BSGS transform in one pass:
 // acc[g] [2][nq][N] = sum_b x[b] (.) w[g * nb + b] for g < ng, b < nb, null
 // w entries skipped; every x word is read once for all g (up to

@@ -263,6 +263,47 @@ __global__ void __launch_bounds__(TPB)
   }
 }
 
+// Integer-weighted sum of ciphertexts (both polys per thread): the weight's
+// residue comes from its 128-bit magnitude by one reduction per thread, and
+// the 64x64-bit products of up to WSUM_MAX terms (each below 2^122) add in
+// 128 bits before one final reduction.
+struct WsumTable {
+  const uint64_t* x[WSUM_MAX];  // [2][nl_i][N]
+  uint64_t pl[WSUM_MAX];        // words per poly of term i, nl_i * N
+  uint64_t mlo[WSUM_MAX], mhi[WSUM_MAX];  // |m_i|
+  uint32_t neg;                 // bit i: m_i < 0
+};
+
+__global__ void __launch_bounds__(TPB)
+    k_wsum(uint64_t* out, const WsumTable t, const ModConst* mc, uint32_t n, uint32_t nq,
+           uint32_t cnt, uint32_t accumulate) {
+  const ModConst m = mc[blockIdx.y];
+  const size_t limb_off = (size_t)blockIdx.y * n + pair_off();
+  Acc128 s[2][2];
+  for (uint32_t i = 0; i < cnt; ++i) {
+    uint64_t w = reduce128(t.mhi[i], t.mlo[i], m);
+    if (((t.neg >> i) & 1u) && w) w = m.q - w;
+    const U2 a = ld2(t.x[i] + limb_off), b = ld2(t.x[i] + t.pl[i] + limb_off);
+    s[0][0].mac(a.x, w);
+    s[0][1].mac(a.y, w);
+    s[1][0].mac(b.x, w);
+    s[1][1].mac(b.y, w);
+  }
+  const size_t pl = (size_t)nq * n;
+  for (int p = 0; p < 2; ++p) {
+    fold(s[p][0], m);
+    fold(s[p][1], m);
+    uint64_t* op = out + (size_t)p * pl + limb_off;
+    uint64_t v0 = s[p][0].lo, v1 = s[p][1].lo;
+    if (accumulate) {
+      const U2 o = ld2(op);
+      v0 = add_mod(v0, o.x, m.q);
+      v1 = add_mod(v1, o.y, m.q);
+    }
+    st2(op, v0, v1);
+  }
+}
+
 // Rescale step 1: centred lift of the (inverse-NTT'd) last limb into limbs
 // i < l.  grid (N/512, l, npoly).  last: [npoly][N] coefficient form.
 __global__ void __launch_bounds__(TPB)
@@ -465,6 +506,30 @@ void poly_mac_table(Context& c, uint64_t* acc, const uint64_t* const* x,
     FHE_LAUNCH(c, "k_mac_table", k_mac_table, grid_for(c, nq, 1), dim3(tpb_for(c)), 0, acc, t, c.d_const, c.n, nq, k, acc_flag);
     i += k;
   } while (i < cnt);
+}
+
+void poly_linear_wsum(Context& c, uint64_t* out, const uint64_t* const* x, const uint32_t* x_nlimb,
+                      const uint64_t* weights, uint32_t cnt, uint32_t nq) {
+  if (cnt == 0) throw ArgError("a weighted sum needs at least one term");
+  for (uint32_t i0 = 0; i0 < cnt; i0 += WSUM_MAX) {
+    const uint32_t k = cnt - i0 < WSUM_MAX ? cnt - i0 : WSUM_MAX;
+    WsumTable t{};
+    for (uint32_t j = 0; j < k; ++j) {
+      const uint32_t i = i0 + j;
+      if (x_nlimb[i] < nq) throw ArgError("a term has fewer limbs than the sum");
+      uint64_t lo = weights[2 * i], hi = weights[2 * i + 1];
+      if (hi >> 63) {  // magnitude of a negative two's-complement value
+        lo = ~lo + 1;
+        hi = ~hi + (lo == 0);
+        t.neg |= 1u << j;
+      }
+      t.x[j] = x[i];
+      t.pl[j] = (uint64_t)x_nlimb[i] * c.n;
+      t.mlo[j] = lo;
+      t.mhi[j] = hi;
+    }
+    FHE_LAUNCH(c, "k_wsum", k_wsum, grid_for(c, nq, 1), dim3(tpb_for(c)), 0, out, t, c.d_const, c.n, nq, k, i0 > 0 ? 1u : 0u);
+  }
 }
 
 void poly_mod_raise(Context& c, uint64_t* out, uint32_t nq_out, const uint64_t* a,

@@ -83,6 +83,7 @@ SIGNATURES = {
     "fhe_mod_raise": [_p, _p, _u32],
     "fhe_encode": [_p, _p, _p, _u32, _u32, _dbl, _u32, _p],
     "fhe_encode_many": [_p, _p, _p, _u32, _u32, _u32, _dbl, _u32, _p],
+    "fhe_linear_wsum": [_p, _p, _p, _u32, _u32],
     "fhe_decode": [_p, _p, _u32, _dbl, _p, _p],
     "fhe_context_set_sampling": [_p, _int, _p],
     "fhe_keygen_secret": [_p, _u64, _p],

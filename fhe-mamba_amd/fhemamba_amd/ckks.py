@@ -680,14 +680,15 @@ class CryptoContext:
         t = max(c.level for c, _ in items)
         target = self._sf[t] * self._sf[t]
         nq = self.L - t
-        acc = None
+        terms, ms = [], []
         for c, w in items:
             m = int(round(w * target / c.scale))
-            if m == 0:
-                continue
-            x = c.poly if c.level == t else self._ctx.drop_limbs(c.poly, nq)
-            term = self._ctx.mul_const(x, self._const_residues(m, nq))
-            acc = term if acc is None else self._ctx.add(acc, term, out=acc)
+            if m != 0:
+                terms.append(c.poly)
+                ms.append(m)
+        # one pass over the terms' first nq limbs (no limb drops, no
+        # per-term products)
+        acc = self._ctx.linear_wsum(terms, ms, nq) if terms else None
         if acc is None:
             c0 = items[0][0]
             x = c0.poly if c0.level == t else self._ctx.drop_limbs(c0.poly, nq)

@@ -168,6 +168,23 @@ class Context:
         call("fhe_add_plain", out.handle, ct.handle, pt.handle)
         return out
 
+    def linear_wsum(self, terms, weights, nlimb: int, out=None):
+        """sum_i weights[i] * terms[i] (Python integers, |w| < 2^126) over the
+        first nlimb limbs of 2-poly ciphertexts, in one pass."""
+        if len(terms) != len(weights) or not terms:
+            raise ValueError("linear_wsum needs matching, non-empty terms and weights")
+        w = np.zeros(2 * len(weights), dtype=np.uint64)
+        for i, m in enumerate(weights):
+            m = int(m)
+            if m.bit_length() > 126:
+                raise ValueError("weight does not fit 127 bits")
+            w[2 * i] = m & 0xFFFFFFFFFFFFFFFF
+            w[2 * i + 1] = (m >> 64) & 0xFFFFFFFFFFFFFFFF
+        out = self._out(out, 2, nlimb)
+        hs = (ctypes.c_void_p * len(terms))(*[t.handle.value for t in terms])
+        call("fhe_linear_wsum", out.handle, hs, _ptr(w), len(terms), nlimb)
+        return out
+
     def mul_const(self, a, consts, out=None):
         c = np.ascontiguousarray(consts, dtype=np.uint64)
         out = self._out(out, a.npoly, a.nlimb)

@@ -128,6 +128,14 @@ int fhe_add_plain(fhe_poly *out, const fhe_poly *ct, const fhe_poly *pt);
  * (packed_fideslib.cpp:162) which adds c[j] to poly 0 only. */
 int fhe_mul_const(fhe_poly *out, const fhe_poly *a, const uint64_t *c);
 int fhe_add_const(fhe_poly *out, const fhe_poly *a, const uint64_t *c);
+/* out = sum_i m_i * xs[i] over count 2-poly ciphertexts, on their first
+ * nlimb limbs (each term holds at least nlimb), with integer weights m_i as
+ * two's-complement 128-bit values, weights[2i] the low and weights[2i+1]
+ * the high word: the Chebyshev leaf sum, a scaled term per basis element
+ * added into the accumulator (packed_fideslib.cpp:577-584), in one pass over
+ * the terms.  out is [2][nlimb] and may not alias a term. */
+int fhe_linear_wsum(fhe_poly *out, const fhe_poly *const *xs, const uint64_t *weights,
+                    uint32_t count, uint32_t nlimb);
 /* multIntScalar (native/fideslib_stage0/src/fideslib_refresh_correction.hpp:37). */
 int fhe_mul_int(fhe_poly *out, const fhe_poly *a, int64_t c);
 /* RescaleInPlace, FLEXIBLEAUTO (packed_fideslib.cpp:236): drop the last limb

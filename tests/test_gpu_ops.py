@@ -147,6 +147,31 @@ def test_mac(pair, count):
     assert np.array_equal(acc.numpy(), orc.mac(x, w))
 
 
+@pytest.mark.parametrize("count", [1, 5, 20])
+def test_linear_wsum_matches_big_integer_sum(pair, count):
+    """fhe_linear_wsum = sum_i m_i x_i mod q_j exactly (Python integers),
+    for terms holding more limbs than the sum, negative weights, weights
+    past 64 bits and 20 terms (two launches, the second accumulating)."""
+    ctx, _ = pair
+    rng = np.random.default_rng(count)
+    nq = ctx.L - 1
+    xs, hs, ms = [], [], []
+    for i in range(count):
+        nl = nq + int(rng.integers(0, 2))
+        a = residues(rng, ctx.q[:nl], (2,), ctx.n)
+        xs.append(a[:, :nq])
+        hs.append(ctx.upload(a))
+        m = int(rng.integers(-2**62, 2**62)) * (1 if i % 3 else 2**40 + 7)
+        ms.append(-m if i % 2 else m)
+    ms[0] = -(2**125) + 3
+    got = ctx.linear_wsum(hs, ms, nq).numpy()
+    qv = np.array(ctx.q[:nq], dtype=object)[None, :, None]
+    want = sum(_obj(x) * m for x, m in zip(xs, ms)) % qv
+    assert np.array_equal(got, want.astype(np.uint64))
+    with pytest.raises(ValueError):
+        ctx.linear_wsum(hs, [2**127] * count, nq)
+
+
 def test_argument_errors_raise(pair):
     ctx, _ = pair
     a = ctx.poly(2, 2)
