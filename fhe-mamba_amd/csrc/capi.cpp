@@ -96,6 +96,34 @@ void prepare_out(fhe_poly* out, uint32_t npoly, uint32_t nlimb) {
   if (out->npoly != npoly || out->nlimb != nlimb) reshape(out, npoly, nlimb);
 }
 
+// Writes a result of shape (npoly, nlimb) into `out` through f(dst), where
+// `in` is an input that f reads.  If out is that input, the result goes to
+// fresh pool storage which then replaces out's: the old storage returns to
+// the pool once the launches that read it are queued (the pool is stream
+// ordered), so no copy back is needed.
+template <class F>
+void write_result(fhe_poly* out, const fhe_poly* in, uint32_t npoly, uint32_t nlimb, F&& f) {
+  if (out != in) {
+    prepare_out(out, npoly, nlimb);
+    f(out->data);
+    return;
+  }
+  fhe::Context& c = *out->c;
+  const size_t bytes = words(c, npoly, nlimb) * 8;
+  uint64_t* fresh = static_cast<uint64_t*>(c.alloc(bytes));
+  try {
+    f(fresh);
+  } catch (...) {
+    c.release(fresh, bytes);
+    throw;
+  }
+  if (out->data) c.release(out->data, out->bytes);
+  out->data = fresh;
+  out->bytes = bytes;
+  out->npoly = npoly;
+  out->nlimb = nlimb;
+}
+
 fhe_key* new_key(const std::shared_ptr<fhe::Context>& own) {
   fhe::Context& c = *own;
   fhe_key* k = new fhe_key;
@@ -335,17 +363,12 @@ int fhe_drop_limbs(fhe_poly* out, const fhe_poly* a, uint32_t nlimb) {
     same_ctx(out, a);
     need(nlimb >= 1 && nlimb <= a->nlimb, "can only drop limbs");
     fhe::Context& c = *a->c;
-    if (out == a) {
-      if (nlimb == a->nlimb) return;
-      fhe::Scratch t(c, words(c, a->npoly, nlimb));
-      fhe::poly_copy_limbs(c, t.p, nlimb, a->data, a->nlimb, a->npoly, nlimb);
-      reshape(out, a->npoly, nlimb);
-      fhe::hip_check(hipMemcpyAsync(out->data, t.p, out->bytes, hipMemcpyDeviceToDevice, c.stream),
-                     "drop");
-      return;
-    }
-    prepare_out(out, a->npoly, nlimb);
-    fhe::poly_copy_limbs(c, out->data, nlimb, a->data, a->nlimb, a->npoly, nlimb);
+    if (out == a && nlimb == a->nlimb) return;
+    const uint32_t npoly = a->npoly, nl = a->nlimb;
+    const uint64_t* src = a->data;
+    write_result(out, a, npoly, nlimb, [&](uint64_t* dst) {
+      fhe::poly_copy_limbs(c, dst, nlimb, src, nl, npoly, nlimb);
+    });
   });
 }
 
@@ -461,12 +484,11 @@ int fhe_mod_raise(fhe_poly* out, const fhe_poly* a, uint32_t nlimb) {
     need(a->nlimb >= 1 && a->npoly >= 1, "ModRaise needs at least one limb");
     need(nlimb >= 1 && nlimb <= a->c->L, "ModRaise output must have 1..L limbs");
     fhe::Context& c = *a->c;
-    const uint32_t npoly = a->npoly;
-    fhe::Scratch t(c, words(c, npoly, nlimb));
-    fhe::poly_mod_raise(c, t.p, nlimb, a->data, a->nlimb, npoly);
-    reshape(out, npoly, nlimb);
-    fhe::hip_check(hipMemcpyAsync(out->data, t.p, out->bytes, hipMemcpyDeviceToDevice, c.stream),
-                   "mod raise");
+    const uint32_t npoly = a->npoly, nl = a->nlimb;
+    const uint64_t* src = a->data;
+    write_result(out, a, npoly, nlimb, [&](uint64_t* dst) {
+      fhe::poly_mod_raise(c, dst, nlimb, src, nl, npoly);
+    });
   });
 }
 
@@ -476,16 +498,9 @@ int fhe_rescale(fhe_poly* out, const fhe_poly* a) {
     need(a->nlimb >= 2 && a->nlimb <= a->c->L, "rescale needs 2..L limbs");
     fhe::Context& c = *a->c;
     const uint32_t npoly = a->npoly, nq = a->nlimb;
-    if (out == a) {
-      fhe::Scratch t(c, words(c, npoly, nq - 1));
-      fhe::poly_rescale(c, t.p, a->data, npoly, nq);
-      reshape(out, npoly, nq - 1);
-      fhe::hip_check(hipMemcpyAsync(out->data, t.p, out->bytes, hipMemcpyDeviceToDevice, c.stream),
-                     "rescale");
-      return;
-    }
-    prepare_out(out, npoly, nq - 1);
-    fhe::poly_rescale(c, out->data, a->data, npoly, nq);
+    const uint64_t* src = a->data;
+    write_result(out, a, npoly, nq - 1,
+                 [&](uint64_t* dst) { fhe::poly_rescale(c, dst, src, npoly, nq); });
   });
 }
 
@@ -544,16 +559,10 @@ int fhe_keyswitch(fhe_poly* out, const fhe_poly* a, const fhe_key* key) {
     need(a->npoly == 1 && a->nlimb >= 1 && a->nlimb <= a->c->L, "keyswitch input is one poly");
     fhe::Context& c = *a->c;
     const uint32_t nq = a->nlimb;
-    if (out == a) {
-      fhe::Scratch t(c, words(c, 2, nq));
-      fhe::keyswitch(c, a->data, nq, key->data, fhe::KeySwitchOut{t.p, nullptr, nullptr, 1});
-      reshape(out, 2, nq);
-      fhe::hip_check(hipMemcpyAsync(out->data, t.p, out->bytes, hipMemcpyDeviceToDevice, c.stream),
-                     "keyswitch");
-      return;
-    }
-    prepare_out(out, 2, nq);
-    fhe::keyswitch(c, a->data, nq, key->data, fhe::KeySwitchOut{out->data, nullptr, nullptr, 1});
+    const uint64_t* src = a->data;
+    write_result(out, a, 2, nq, [&](uint64_t* dst) {
+      fhe::keyswitch(c, src, nq, key->data, fhe::KeySwitchOut{dst, nullptr, nullptr, 1});
+    });
   });
 }
 
@@ -565,12 +574,10 @@ int fhe_relinearize(fhe_poly* out, const fhe_poly* ct3, const fhe_key* key) {
     fhe::Context& c = *ct3->c;
     const uint32_t nq = ct3->nlimb;
     const size_t pl = (size_t)nq * c.n;
-    fhe::Scratch t(c, 2 * pl);
-    fhe::keyswitch(c, ct3->data + 2 * pl, nq, key->data,
-                   fhe::KeySwitchOut{t.p, ct3->data, ct3->data + pl, 1});
-    reshape(out, 2, nq);
-    fhe::hip_check(hipMemcpyAsync(out->data, t.p, out->bytes, hipMemcpyDeviceToDevice, c.stream),
-                   "relinearize");
+    const uint64_t* src = ct3->data;
+    write_result(out, ct3, 2, nq, [&](uint64_t* dst) {
+      fhe::keyswitch(c, src + 2 * pl, nq, key->data, fhe::KeySwitchOut{dst, src, src + pl, 1});
+    });
   });
 }
 
@@ -582,11 +589,9 @@ int fhe_rotate(fhe_poly* out, const fhe_poly* ct, const fhe_key* key, uint32_t g
     need((galois & 1) && galois < 2 * ct->c->n, "Galois element must be odd and < 2N");
     fhe::Context& c = *ct->c;
     const uint32_t nq = ct->nlimb;
-    fhe::Scratch t(c, 2 * (size_t)nq * c.n);
-    fhe::rotate(c, t.p, ct->data, nq, key->data, galois);
-    reshape(out, 2, nq);
-    fhe::hip_check(hipMemcpyAsync(out->data, t.p, out->bytes, hipMemcpyDeviceToDevice, c.stream),
-                   "rotate");
+    const uint64_t* src = ct->data;
+    write_result(out, ct, 2, nq,
+                 [&](uint64_t* dst) { fhe::rotate(c, dst, src, nq, key->data, galois); });
   });
 }
 

@@ -17,8 +17,11 @@
  *     and plaintext polys are in evaluation (NTT) form unless stated.
  *   - Moduli index the joint list q_0..q_{L-1}, p_0..p_{K-1}.
  *   - Device work is asynchronous on the context's stream; host buffers
- *     passed to *_upload / *_download / fhe_encode / fhe_decode are only
- *     read or written during the call (those calls synchronise).
+ *     passed to *_upload / *_download / fhe_encode* / fhe_decode are only
+ *     read or written during the call (encodes copy their input to a
+ *     staging buffer; the others synchronise).
+ *   - Where an entry point lets its output alias an input, the result may
+ *     occupy new device storage: fhe_poly_data gives the current address.
  *   - Handles are owned by the caller and released explicitly.  One
  *     context is used by one host thread at a time.
  */
