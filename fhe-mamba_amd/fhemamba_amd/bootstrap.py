@@ -551,6 +551,9 @@ def main(argv=None) -> int:
     ap.add_argument("--passes", type=int, choices=(1, 2), default=1)
     ap.add_argument("--repeat", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--correction-factor", type=int, default=0,
+                    help="message scale-down exponent c (OpenFHE's correctionFactor; "
+                         "0 picks it from the ring, secret and order)")
     args = ap.parse_args(argv)
     n = 1 << args.log_n
     slots = n // 2
@@ -559,7 +562,8 @@ def main(argv=None) -> int:
                                  first_mod_bits=60, seed=21,
                                  secret_dist="SPARSE_TERNARY" if args.secret == "sparse"
                                  else "UNIFORM_TERNARY")
-    cc.EvalBootstrapSetup([4, 4], [0, 0], slots, s2c_first=s2c, real_slots=s2c)
+    cc.EvalBootstrapSetup([4, 4], [0, 0], slots, args.correction_factor, s2c_first=s2c,
+                          real_slots=s2c)
     cc.EvalBootstrapKeyGen(keys.secretKey, slots)
     x = np.random.default_rng(8).uniform(-1, 1, slots)
     ct = cc.Encrypt(keys.publicKey, cc.MakeCKKSPackedPlaintext(list(x)))
@@ -580,7 +584,8 @@ def main(argv=None) -> int:
     err = float(np.max(np.abs(np.asarray(pt.GetRealPackedValue()) - x)))
     print(json.dumps({
         "ring_dimension": n, "depth": args.depth, "secret": args.secret, "order": args.order,
-        "passes": args.passes, "ms_per_call": ms,
+        "passes": args.passes, "correction_factor": args.correction_factor or "auto",
+        "ms_per_call": ms,
         "kernel_ms_per_call": sum(v[1] for v in prof.values()),
         "launches_per_call": sum(v[0] for v in prof.values()),
         "max_abs_err": err, "output_level": int(out.GetLevel()),
