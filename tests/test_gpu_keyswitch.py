@@ -144,6 +144,31 @@ def test_relinearize_matches_oracle(setup):
     assert np.array_equal(got, orc.relinearize(t, key))
 
 
+def test_rotate_and_relinearize_in_place(setup):
+    """An output that aliases the input (rotate, relinearize of a 3-poly
+    tensor into itself) takes fresh storage and holds the oracle's result;
+    the old storage goes back to the pool and later results stay exact."""
+    ctx, orc, s = setup
+    rng = np.random.default_rng(41)
+    g = O.galois_elt(3, ctx.n)
+    gkey = orc.galois_key(s, g, 42)
+    ct = residues(rng, ctx.q, (2,), ctx.n)
+    d = ctx.upload(ct)
+    before = d.data_ptr()
+    ctx.rotate(d, ctx.load_key(gkey), g, out=d)
+    assert np.array_equal(d.numpy(), orc.rotate(ct, gkey, g))
+    assert d.data_ptr() != before
+    t = residues(rng, ctx.q, (3,), ctx.n)
+    rkey = orc.relin_key(s, 43)
+    dt = ctx.upload(t)
+    ctx.relinearize(dt, ctx.load_key(rkey), out=dt)
+    assert dt.shape == (2, ctx.L)
+    assert np.array_equal(dt.numpy(), orc.relinearize(t, rkey))
+    # the freed storage is reused by later allocations without corrupting them
+    again = ctx.rotate(ctx.upload(ct), ctx.load_key(gkey), g)
+    assert np.array_equal(again.numpy(), orc.rotate(ct, gkey, g))
+
+
 def test_gpu_keygen_matches_oracle_keys(setup):
     """GPU-generated keys equal the oracle's: their key switches agree
     word for word (keys are stored in Montgomery form on the device)."""
