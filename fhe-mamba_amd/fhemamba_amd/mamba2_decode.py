@@ -72,14 +72,14 @@ class LayerCtState:
 class EncryptedMamba2Decoder:
     def __init__(self, cc, keys, chain: ChainPayload, *, bootstrap_passes: int = 2,
                  refresh_ceiling: int | None = None, bounds: dict | None = None, log=None,
-                 s2c_first: bool = False):
+                 s2c_first: bool = False, level_budget=(4, 4)):
         first = chain.layers[0]
         self.chain, self.cc = chain, cc
         self.slots = cc.GetBatchSize()
         self.log = log or (lambda m: None)
         self.ev = PackedEvaluator(cc, keys, self.slots, bootstrap_passes=bootstrap_passes,
                                   refresh_ceiling=refresh_ceiling, log=self.log,
-                                  s2c_first=s2c_first)
+                                  s2c_first=s2c_first, level_budget=tuple(level_budget))
         self.bounds = [self._layer_bounds(lay, bounds) for lay in chain.layers]
         self.d, self.di, self.ns = first.d_model, first.d_inner, first.state_size
         self.nh, self.hd, self.kc = first.num_heads, first.head_dim, first.conv_kernel
@@ -473,25 +473,41 @@ def token_loop(dec: EncryptedMamba2Decoder, chain: ChainPayload, n_tok: int, ar=
     per token the seconds, the errors of the decrypted final hidden against
     the polynomial and exact references, and the client's selections."""
     states = dec.initial_states()
-    out = dict(seconds=[], errors_poly=[], errors_exact=[], selected=[], client_seconds=0.0)
+    out = dict(seconds=[], errors_poly=[], errors_exact=[], selected=[], client_seconds=0.0,
+               bootstraps=[], decrypt_seconds=0.0, token0={})
     selected = out["selected"]
     want_poly = ar.expected_poly_final if ar else chain.expected_poly_final
     want_exact = ar.expected_exact_final if ar else chain.expected_final
+
+    def max_err(got, want) -> float:
+        # A non-finite slot is a failed decrypt: the largest finite double,
+        # never a silent zero (np.max propagates NaN, but keep it explicit).
+        d = np.abs(got - want)
+        return float(np.max(d)) if np.all(np.isfinite(d)) else 1.0e308
+
     for k in range(n_tok):
         sync()
+        b0 = dec.ev.stats["bootstraps"]
         t = time.perf_counter()
         ct, states = dec.step(ar.input_for(k, selected) if ar else chain.input_embeddings[k],
                               states)
         sync()
         out["seconds"].append(time.perf_counter() - t)
+        out["bootstraps"].append(dec.ev.stats["bootstraps"] - b0)
         t = time.perf_counter()
         got = dec.decrypt(ct)
+        out["decrypt_seconds"] += time.perf_counter() - t
         if ar is not None and k >= ar.prompt_tokens - 1:
             selected.append(ar.select(got))
             out["client_seconds"] += time.perf_counter() - t
+        if k == 0:
+            ref = want_poly[0] if want_poly is not None else want_exact[0]
+            out["token0"] = {"decrypted": [float(v) for v in got[:8]],
+                             "expected": [float(v) for v in ref[:8]],
+                             "exact": [float(v) for v in want_exact[0][:8]]}
         if want_poly is not None:
-            out["errors_poly"].append(float(np.max(np.abs(got - want_poly[k]))))
-        out["errors_exact"].append(float(np.max(np.abs(got - want_exact[k]))))
+            out["errors_poly"].append(max_err(got, want_poly[k]))
+        out["errors_exact"].append(max_err(got, want_exact[k]))
         ep = out["errors_poly"][-1] if out["errors_poly"] else float("nan")
         log(f"token {k}: {out['seconds'][-1]:.2f}s error vs polynomial {ep:.2e} vs exact "
             f"{out['errors_exact'][-1]:.2e}"
@@ -503,7 +519,7 @@ def token_loop(dec: EncryptedMamba2Decoder, chain: ChainPayload, n_tok: int, ar=
 SECRET_KEY_DISTS = {"sparse-ternary": "SPARSE_TERNARY", "uniform-ternary": "UNIFORM_TERNARY"}
 
 
-def _decode_setup(payload_dir, security, secret_key_dist, ring_dim):
+def _decode_setup(payload_dir, security, secret_key_dist, ring_dim, sizes=None):
     from .mamba2_payload import read_chain_payload
     from .packed import CLASSICAL128
     if security not in ("not-set", "128-classic"):
@@ -517,6 +533,9 @@ def _decode_setup(payload_dir, security, secret_key_dist, ring_dim):
         raise ValueError("ring_dim: a power of two >= 4096, and only with security not-set")
     chain = read_chain_payload(payload_dir)
     extra = dict(CLASSICAL128) if classical else ({"ring_dim": ring_dim} if ring_dim else {})
+    # depth / scale_bits / first_mod_bits (the reference decoder's
+    # --multiplicative-depth, --scaling-mod-size, --first-mod-size)
+    extra.update(sizes or {})
     slots = extra.get("ring_dim", 65536) // 2
     return chain, classical, secret_key_dist, slots, extra
 
@@ -542,7 +561,8 @@ def _build(slots, seed, secret_key_dist, extra):
 def run_payload(payload_dir: str, *, tokens: int = 0, bootstrap_passes: int = 2, seed=None,
                 secret_key_dist: str | None = None, security: str = "not-set",
                 layers: int = 0, autoregressive: bool = False, s2c_first: bool = True,
-                ring_dim: int = 0, log=print) -> dict:
+                ring_dim: int = 0, sizes: dict | None = None, level_budget=(4, 4),
+                log=print) -> dict:
     """Decode the payload's test embeddings in turn (carried state) and
     compare the decrypted outputs with its polynomial-circuit and exact
     references; returns the report.
@@ -573,7 +593,8 @@ def run_payload(payload_dir: str, *, tokens: int = 0, bootstrap_passes: int = 2,
     level interval and precision; False: the ordinary order.  ring_dim
     (not-set only; default 2^16) picks a smaller ring for small payloads."""
     chain, classical, secret_key_dist, slots, extra = _decode_setup(
-        payload_dir, security, secret_key_dist, ring_dim)
+        payload_dir, security, secret_key_dist, ring_dim, sizes)
+    n_layers_total = chain.n_layers
     ar = chain.autoregressive if autoregressive else None
     if autoregressive:
         if ar is None:
@@ -591,7 +612,7 @@ def run_payload(payload_dir: str, *, tokens: int = 0, bootstrap_passes: int = 2,
     cc, keys = _build(slots, seed, secret_key_dist, extra)
     audit = cc.SecurityAudit() if classical else None
     dec = EncryptedMamba2Decoder(cc, keys, chain, bootstrap_passes=bootstrap_passes, log=log,
-                                 s2c_first=s2c_first)
+                                 s2c_first=s2c_first, level_budget=level_budget)
     setup = time.perf_counter() - t0
     loop = token_loop(dec, chain, n_tok, ar, cc.device.sync, log)
     per_token, errs_poly, errs_exact = loop["seconds"], loop["errors_poly"], loop["errors_exact"]
@@ -632,6 +653,17 @@ def run_payload(payload_dir: str, *, tokens: int = 0, bootstrap_passes: int = 2,
         "ct_pt_mul": s["ct_pt"],
         "rotation_keys_generated": s["rotation_keys"],
         "keygen_seconds": s["keygen_seconds"],
+        "n_layers_total": n_layers_total,
+        "per_token_errors_vs_exact": errs_exact,
+        "per_token_bootstraps": loop["bootstraps"],
+        "decrypt_seconds": loop["decrypt_seconds"],
+        "token0_samples": loop["token0"],
+        "level_budget": list(level_budget),
+        "multiplicative_depth": len(cc.GetModuli()[0]) - 1,
+        "dims": {"d_model": dec.d, "d_inner": dec.di, "num_heads": dec.nh,
+                 "head_dim": dec.hd, "state_size": dec.ns, "conv_kernel": dec.kc,
+                 "conv_dim": dec.cd, "proj_dim": chain.layers[0].proj_dim,
+                 "n_groups": chain.layers[0].n_groups, "state_group_count": dec.groups},
     }
 
 
