@@ -189,6 +189,13 @@ int fhe_context_info(const fhe_context* ctx, uint32_t* info5) {
   });
 }
 
+int fhe_alloc_count(uint64_t* count) {
+  return guard([&] {
+    need(count, "null argument");
+    *count = fhe::alloc_requests();
+  });
+}
+
 int fhe_context_moduli(const fhe_context* ctx, uint64_t* mods, uint64_t* psi) {
   return guard([&] {
     need(ctx, "null context");
@@ -604,24 +611,62 @@ constexpr size_t kNoAllocScratchBytes = size_t(128) << 20;
 static __device__ __align__(256) uint64_t scratch[kNoAllocScratchBytes / 8];
 
 namespace {
+// One GPU's `scratch` and the ordering of the calls that use it.  A call
+// holds `mu` while it binds the array and enqueues its work, and records
+// `done` on its stream when it is enqueued; a call on another stream (a
+// second context, or a caller stream) first makes its stream wait for
+// `done`, so calls on one GPU never overlap on the array, whichever
+// contexts and streams they come from.
+struct ScratchDevice {
+  uint64_t* ptr = nullptr;
+  hipEvent_t done = nullptr;
+  hipStream_t last = nullptr;  // stream `done` was last recorded on
+  bool recorded = false;
+  std::mutex mu;
+};
 std::mutex g_scratch_mu;
-std::map<int, uint64_t*> g_scratch_ptr;  // device -> address of its `scratch`
+std::map<int, std::unique_ptr<ScratchDevice>> g_scratch;  // device -> its state
 
-uint64_t* scratch_for_device(int device) {
+// Set-up, once per device with that device current: the array's device
+// address and the ordering event.
+ScratchDevice& scratch_for_device(int device) {
   std::lock_guard<std::mutex> lk(g_scratch_mu);
-  auto it = g_scratch_ptr.find(device);
-  if (it != g_scratch_ptr.end()) return it->second;
+  auto it = g_scratch.find(device);
+  if (it != g_scratch.end()) return *it->second;
   int prev = 0;
   fhe::hip_check(hipGetDevice(&prev), "hipGetDevice");
   fhe::hip_check(hipSetDevice(device), "hipSetDevice");
   void* ptr = nullptr;
-  const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  hipEvent_t ev = nullptr;
+  hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
   fhe::hip_check(hipSetDevice(prev), "hipSetDevice");
-  fhe::hip_check(e, "hipGetSymbolAddress(scratch)");
+  fhe::hip_check(e, "no-allocation scratch set-up");
   if (!ptr) throw fhe::HipError("hipGetSymbolAddress(scratch) returned no address");
-  g_scratch_ptr[device] = static_cast<uint64_t*>(ptr);
-  return static_cast<uint64_t*>(ptr);
+  auto d = std::make_unique<ScratchDevice>();
+  d->ptr = static_cast<uint64_t*>(ptr);
+  d->done = ev;
+  return *(g_scratch[device] = std::move(d));
 }
+
+// Orders one call after every earlier call on the same GPU (see
+// ScratchDevice) and records its own completion when it leaves, also when
+// it throws after enqueuing part of its work.
+struct ScratchTurn {
+  ScratchDevice& d;
+  hipStream_t s;
+  std::lock_guard<std::mutex> lk;
+  ScratchTurn(ScratchDevice& dev, hipStream_t stream) : d(dev), s(stream), lk(dev.mu) {
+    if (d.recorded && d.last != s)
+      fhe::hip_check(hipStreamWaitEvent(s, d.done, 0), "no-allocation rotate: stream wait");
+  }
+  ~ScratchTurn() {
+    if (hipEventRecord(d.done, s) == hipSuccess) {
+      d.last = s;
+      d.recorded = true;
+    }
+  }
+};
 
 // Scratch words a rotation at nq limbs takes from the arena: the ModUp
 // digits, the ModUp input staging, the ModDown P limbs and y, and a
@@ -671,8 +716,9 @@ int fhe_rotate_noalloc(fhe_poly* out, const fhe_poly* ct, const fhe_key* key, ui
       throw fhe::StateError(
           "no-allocation rotate: the conversion tables for this level are not built yet "
           "(any allocating key switch at this level builds them)");
-    uint64_t* base = scratch_for_device(c.device);
-    ArenaScope arena(c, base, kNoAllocScratchBytes / 8);
+    ScratchDevice& dev = scratch_for_device(c.device);
+    ScratchTurn turn(dev, c.stream);
+    ArenaScope arena(c, dev.ptr, kNoAllocScratchBytes / 8);
     if (!aliased) {
       fhe::rotate(c, out->data, ct->data, nq, key->data, galois);
       return;
@@ -791,6 +837,9 @@ static void linear_transform_checked(fhe_poly* out, const fhe_poly* ct,
     if (!pts[k]) continue;
     need(pts[k]->c == &c && pts[k]->npoly == 1 && pts[k]->nlimb >= nq,
          "diagonal must be a one-poly plaintext with at least the ciphertext's limbs");
+    // Shaping `out` as a ciphertext would free this diagonal's storage
+    // while the transform still reads it.
+    need(pts[k] != out, "the output must not be one of the diagonals");
     pp[k] = pts[k]->data;
     any = true;
   }

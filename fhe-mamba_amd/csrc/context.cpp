@@ -3,6 +3,7 @@
 // CCParams<CryptoContextCKKSRNS> / GenCryptoContext as used by the
 // reference executors (native/fideslib_stage0/src/packed_fideslib.cpp:1060-1068).
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstring>
 #include <cerrno>
@@ -42,7 +43,12 @@ Pool::~Pool() {
   for (auto& kv : free_) hipFree(kv.second);
 }
 
+static std::atomic<uint64_t> g_alloc_requests{0};
+void note_alloc() { g_alloc_requests.fetch_add(1, std::memory_order_relaxed); }
+uint64_t alloc_requests() { return g_alloc_requests.load(std::memory_order_relaxed); }
+
 void* Pool::get(size_t bytes) {
+  note_alloc();
   bytes = (bytes + 255) & ~size_t(255);
   {
     std::lock_guard<std::mutex> g(mu_);
@@ -108,6 +114,7 @@ template <typename T>
 static T* upload(const std::vector<T>& v) {
   T* d = nullptr;
   if (v.empty()) return nullptr;
+  note_alloc();
   hip_check(hipMalloc(&d, v.size() * sizeof(T)), "hipMalloc(table)");
   hip_check(hipMemcpy(d, v.data(), v.size() * sizeof(T), hipMemcpyHostToDevice), "upload table");
   return d;
@@ -253,6 +260,7 @@ Context::Staging& Context::staging_slot(size_t bytes) {
     if (s.host) hip_check(hipHostFree(s.host), "hipHostFree");
     s.host = nullptr;
     s.bytes = 0;
+    note_alloc();
     hip_check(hipHostMalloc(&s.host, bytes, hipHostMallocDefault), "hipHostMalloc");
     s.bytes = bytes;
   }

@@ -116,6 +116,12 @@ class Pool {
   std::multimap<size_t, void*> free_;
 };
 
+// Allocation requests the library has made in this process: every pool
+// request (fresh or reused) and every direct device or pinned-host
+// allocation of tables and staging buffers.
+void note_alloc();
+uint64_t alloc_requests();
+
 // Bytes from the OS CSPRNG (getrandom); throws if none are available.
 void fill_entropy(void* buf, size_t bytes);
 

@@ -61,6 +61,8 @@ std::pair<double*, double*> fft_tables(Context& c, uint32_t slots) {
     }
   }
   double *di = nullptr, *df = nullptr;
+  note_alloc();
+  note_alloc();
   hip_check(hipMalloc(&di, inv.size() * 8), "hipMalloc fft");
   hip_check(hipMalloc(&df, fwd.size() * 8), "hipMalloc fft");
   hip_check(hipMemcpy(di, inv.data(), inv.size() * 8, hipMemcpyHostToDevice), "fft table");

@@ -666,24 +666,38 @@ __global__ void __launch_bounds__(256)
 // the kernel fits 64 VGPRs, four 8-wave workgroups per CU (0.84 -> 0.80 ms
 // for 30 key switches at N=2^16, 24 limbs, 3 digits, against forming them
 // first and keeping them in registers).
+// Rows per workgroup of the paired passes (one blocked group) and the LDS
+// words of their two-poly tile.
+template <int S>
+constexpr uint32_t pair_lines() {
+  return 512u >> (S - 2);
+}
+template <int S>
+constexpr uint32_t pair_lds_words() {
+  return 2 * pair_lines<S>() * ((1u << S) + (1u << S) / 16 + 1);
+}
+
+// Body of the paired epilogue for the workgroup at row group bx of limb i of
+// key switch r, with its tile in lds (pair_lds_words<S>() words).
 template <int S, int ND>
-__global__ void __launch_bounds__(512)
-    __attribute__((amdgpu_waves_per_eu(ND <= 3 && S >= 7 ? 6 : 1, 8)))
-    ntt_pass_moddown_pair(const uint64_t* __restrict__ y, const ModConst* __restrict__ mc,
-                          const uint64_t* __restrict__ tw_all, uint32_t log_n, uint32_t s_other,
-                          const ModDownEpi e) {
+__device__ __forceinline__ void moddown_pair_body(const uint64_t* __restrict__ y,
+                                                  const ModConst* __restrict__ mc,
+                                                  const uint64_t* __restrict__ tw_all,
+                                                  uint32_t log_n, uint32_t s_other,
+                                                  const ModDownEpi& e, uint32_t bx, uint32_t r,
+                                                  uint32_t i, uint64_t* lds_base) {
   constexpr int RHO = 2, R = 4, TPL = 1 << (S - RHO), LINES = 512 / TPL;
   constexpr int NSP = (S + RHO - 1) / RHO;
   constexpr uint32_t LEN = 1u << S, PITCH = LEN + LEN / 16 + 1;
   static_assert(TPL <= 64 && LINES * TPL == 512 && ND > 0 && ND <= 7, "pair epilogue");
-  __shared__ uint64_t lds[2][LINES * PITCH];
-  const uint32_t n = 1u << log_n, r = blockIdx.y, i = blockIdx.z, tid = threadIdx.x;
+  uint64_t* const lds[2] = {lds_base, lds_base + LINES * PITCH};
+  const uint32_t n = 1u << log_n, tid = threadIdx.x;
   const uint64_t q = mc[i].q, q4 = 4 * q, qneg = mc[i].neg_q, q8neg = mc[i].neg_q8;
   const float rq = mc[i].rq;
   const uint64_t* __restrict__ tw = tw_all + (size_t)i * n * 2;
-  const size_t ps = (size_t)e.nq * n, wg0 = ((size_t)blockIdx.x * LINES) << S;
+  const size_t ps = (size_t)e.nq * n, wg0 = ((size_t)bx * LINES) << S;
   const uint32_t tau = tid % TPL, line = tid / TPL;
-  const uint32_t twbase = (1u << s_other) + blockIdx.x * LINES + line;
+  const uint32_t twbase = (1u << s_other) + bx * LINES + line;
   // Key-product and store positions of this lane: two adjacent pairs in its
   // wavefront's own 64R-word run (the wavefront's rows).
   auto staged = [&](int k) -> uint32_t {
@@ -796,6 +810,17 @@ __global__ void __launch_bounds__(512)
   }
 }
 
+template <int S, int ND>
+__global__ void __launch_bounds__(512)
+    __attribute__((amdgpu_waves_per_eu(ND <= 3 && S >= 7 ? 6 : 1, 8)))
+    ntt_pass_moddown_pair(const uint64_t* __restrict__ y, const ModConst* __restrict__ mc,
+                          const uint64_t* __restrict__ tw_all, uint32_t log_n, uint32_t s_other,
+                          const ModDownEpi e) {
+  __shared__ uint64_t lds[pair_lds_words<S>()];
+  moddown_pair_body<S, ND>(y, mc, tw_all, log_n, s_other, e, blockIdx.x, blockIdx.y, blockIdx.z,
+                           lds);
+}
+
 // First inverse pass of a batched ModDown with both polys of each key
 // switch in one workgroup (the counterpart of ntt_pass_moddown_pair; ND =
 // 1..7 digits, every modulus below 2^60): lane tid forms the P-limb key
@@ -806,24 +831,26 @@ __global__ void __launch_bounds__(512)
 // Up to three digits it fits 64 VGPRs without spills, so four 8-wave
 // workgroups share a CU (LDS allows four; measured 2% faster than three at
 // N=2^16, 24 limbs).
+// Body for the workgroup at row group bx of P limb t of key switch r, with
+// its tile in lds (pair_lds_words<S>() words).
 template <int S, int ND>
-__global__ void __launch_bounds__(512)
-    __attribute__((amdgpu_waves_per_eu(ND <= 3 ? 8 : 1, 8)))
-    ntt_pass_ksk_pair(uint64_t* __restrict__ ext, size_t ps, const ModConst* __restrict__ mc,
-                      const uint64_t* __restrict__ tw_all, uint32_t log_n, uint32_t s_other,
-                      const ModDownEpi e) {
+__device__ __forceinline__ void ksk_pair_body(uint64_t* __restrict__ ext, size_t ps,
+                                              const ModConst* __restrict__ mc,
+                                              const uint64_t* __restrict__ tw_all, uint32_t log_n,
+                                              uint32_t s_other, const ModDownEpi& e, uint32_t bx,
+                                              uint32_t r, uint32_t t, uint64_t* lds_base) {
   constexpr int RHO = 2, R = 4, TPL = 1 << (S - RHO), LINES = 512 / TPL;
   constexpr int NSP = (S + RHO - 1) / RHO;
   constexpr uint32_t LEN = 1u << S, PITCH = LEN + LEN / 16 + 1;
   static_assert(TPL <= 64 && LINES * TPL == 512 && ND > 0 && ND <= 7, "pair ksk pass");
-  __shared__ uint64_t lds[2][LINES * PITCH];
-  const uint32_t n = 1u << log_n, r = blockIdx.y, t = blockIdx.z, tid = threadIdx.x;
+  uint64_t* const lds[2] = {lds_base, lds_base + LINES * PITCH};
+  const uint32_t n = 1u << log_n, tid = threadIdx.x;
   const uint32_t midx = e.L + t;
   const uint64_t q = mc[midx].q, q4 = 4 * q, qneg = mc[midx].neg_q, q4neg = mc[midx].neg_q4;
   const uint64_t* __restrict__ tw = tw_all + (size_t)midx * n * 2;
-  const size_t wg0 = ((size_t)blockIdx.x * LINES) << S;
+  const size_t wg0 = ((size_t)bx * LINES) << S;
   const uint32_t tau = tid % TPL, line = tid / TPL;
-  const uint32_t twbase = (1u << s_other) + blockIdx.x * LINES + line;
+  const uint32_t twbase = (1u << s_other) + bx * LINES + line;
   auto staged = [&](int k) -> uint32_t {
     return (tid >> 6) * (64u * R) + (uint32_t)(k >> 1) * 128u + 2 * (tid & 63) + (k & 1);
   };
@@ -909,6 +936,17 @@ __global__ void __launch_bounds__(512)
       dst[p] = lds[h][lds_idx(p % LINES, p / LINES, PITCH)];
     }
   }
+}
+
+template <int S, int ND>
+__global__ void __launch_bounds__(512)
+    __attribute__((amdgpu_waves_per_eu(ND <= 3 ? 8 : 1, 8)))
+    ntt_pass_ksk_pair(uint64_t* __restrict__ ext, size_t ps, const ModConst* __restrict__ mc,
+                      const uint64_t* __restrict__ tw_all, uint32_t log_n, uint32_t s_other,
+                      const ModDownEpi e) {
+  __shared__ uint64_t lds[pair_lds_words<S>()];
+  ksk_pair_body<S, ND>(ext, ps, mc, tw_all, log_n, s_other, e, blockIdx.x, blockIdx.y, blockIdx.z,
+                       lds);
 }
 
 // ---- Rescale in four launches (ring dimensions 2^13 .. 2^17) ----
@@ -1110,10 +1148,12 @@ struct MidArgs {
 // even first brings X below 8q; values stay below 16q), and the output may
 // reach 16q; otherwise every stage brings X below 4q and the output stays
 // below 8q.
+// Body for (poly, column) tile `tile` with (K + NL) PITCH words of lds.
 template <int S1, int S2, int NW, bool ALT>
-__global__ void __launch_bounds__(64 * NW)
-    k_convert_mid(const MidArgs a, const ModConst* __restrict__ mc,
-                  const uint64_t* __restrict__ tw_inv, const uint64_t* __restrict__ tw_fwd) {
+__device__ __forceinline__ void convert_mid_body(const MidArgs& a, const ModConst* __restrict__ mc,
+                                                 const uint64_t* __restrict__ tw_inv,
+                                                 const uint64_t* __restrict__ tw_fwd,
+                                                 uint32_t tile, uint64_t* lds_dyn) {
   constexpr int M = 1 << S1, TPL = mid_lanes_per_line<S1>(), R = M / TPL;
   constexpr int RHO = R == 4 ? 2 : 3, LPW = 64 / TPL, NL = mid_lines<S1, NW>();
   constexpr int NSP = (S1 + RHO - 1) / RHO;
@@ -1121,13 +1161,6 @@ __global__ void __launch_bounds__(64 * NW)
   constexpr size_t N = (size_t)M << S2;
   constexpr uint32_t M30 = (1u << 30) - 1;
   static_assert(R * TPL == M && (1 << RHO) == R, "column split");
-  extern __shared__ uint64_t lds_dyn[];
-
-  // Tiles in XCD order: workgroup i runs on XCD i % 8, and each XCD takes a
-  // contiguous range of (poly, column) tiles, so neighbouring columns, which
-  // share cache lines of the blocked layout, meet in one L2.
-  const uint32_t per = gridDim.x / 8;
-  const uint32_t tile = (blockIdx.x % 8) * per + blockIdx.x / 8;
   const uint32_t p = tile / N2, col = tile % N2;
   const MidPlan& pl = a.plan[p % a.nplan];
   const uint32_t K = pl.nsrc, nq = pl.ndst;
@@ -1281,6 +1314,19 @@ __global__ void __launch_bounds__(64 * NW)
       }
     }
   }
+}
+
+template <int S1, int S2, int NW, bool ALT>
+__global__ void __launch_bounds__(64 * NW)
+    k_convert_mid(const MidArgs a, const ModConst* __restrict__ mc,
+                  const uint64_t* __restrict__ tw_inv, const uint64_t* __restrict__ tw_fwd) {
+  extern __shared__ uint64_t lds_dyn[];
+  // Tiles in XCD order: workgroup i runs on XCD i % 8, and each XCD takes a
+  // contiguous range of (poly, column) tiles, so neighbouring columns, which
+  // share cache lines of the blocked layout, meet in one L2.
+  const uint32_t per = gridDim.x / 8;
+  const uint32_t tile = (blockIdx.x % 8) * per + blockIdx.x / 8;
+  convert_mid_body<S1, S2, NW, ALT>(a, mc, tw_inv, tw_fwd, tile, lds_dyn);
 }
 
 template <int S, int KIND, bool INV, class Map>

@@ -42,6 +42,7 @@ SIGNATURES = {
     "fhe_context_create": [_u32, _p, _u32, _p, _u32, _u32, _int, _pp],
     "fhe_context_destroy": [_p],
     "fhe_context_info": [_p, _p],
+    "fhe_alloc_count": [_p],
     "fhe_context_moduli": [_p, _p, _p],
     "fhe_context_set_stream": [_p, _p],
     "fhe_sync": [_p],
@@ -140,14 +141,23 @@ def call(name: str, *args) -> None:
     check(getattr(lib, name)(*args))
 
 
-def device_free_bytes() -> int | None:
-    """Free memory of the current HIP device (hipMemGetInfo from the HIP
-    runtime the library links), or None when it cannot be read."""
+def device_free_bytes(device: int | None = None) -> int | None:
+    """Free memory of HIP device `device` (default: the current one;
+    hipMemGetInfo from the HIP runtime the library links, with that device
+    current for the call), or None when it cannot be read."""
     try:
         hip = ctypes.CDLL("libamdhip64.so")
         free, total = ctypes.c_size_t(0), ctypes.c_size_t(0)
-        if hip.hipMemGetInfo(ctypes.byref(free), ctypes.byref(total)) != 0:
-            return None
+        prev = ctypes.c_int(0)
+        if device is not None:
+            if hip.hipGetDevice(ctypes.byref(prev)) != 0 or hip.hipSetDevice(device) != 0:
+                return None
+        try:
+            if hip.hipMemGetInfo(ctypes.byref(free), ctypes.byref(total)) != 0:
+                return None
+        finally:
+            if device is not None:
+                hip.hipSetDevice(prev.value)
         return int(free.value)
     except OSError:
         return None

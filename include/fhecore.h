@@ -70,6 +70,11 @@ int fhe_context_create(uint32_t log_n, const uint64_t *q, uint32_t num_q,
 int fhe_context_destroy(fhe_context *ctx);
 /* log_n, num_q (L), num_p (K), dnum (non-empty digits), alpha (limbs/digit) */
 int fhe_context_info(const fhe_context *ctx, uint32_t *info5);
+/* Allocation requests the library has made in this process (device pool
+ * requests, fresh or reused, and device or pinned-host table and staging
+ * allocations).  No counterpart in the reference: a memory diagnostic, e.g.
+ * to show that a stretch of calls allocated nothing. */
+int fhe_alloc_count(uint64_t *count);
 /* moduli (L+K) and their primitive 2N-th roots psi (L+K). */
 int fhe_context_moduli(const fhe_context *ctx, uint64_t *mods, uint64_t *psi);
 /* Run the context's work on a caller stream (a hipStream_t, e.g. torch's
@@ -187,8 +192,10 @@ int fhe_rotate(fhe_poly *out, const fhe_poly *ct, const fhe_key *key,
  * (roughly N*(dnum_eff*(nq+K) + 3nq + 2K) words, + 2nq*N when out == ct)
  * give FHE_ERR_ARG.  The level's conversion tables must already exist (any
  * allocating key switch at that level builds them), else FHE_ERR_STATE.
- * Calls on one GPU share the array: calls that overlap on one GPU (two
- * host threads, or two streams) race. */
+ * Calls on one GPU share the array and are ordered on it: a call from
+ * another stream (another context, or a caller stream) waits on the GPU for
+ * the previous call's work before its own, and host threads take turns
+ * enqueuing.  The array keeps the last call's contents. */
 int fhe_rotate_noalloc(fhe_poly *out, const fhe_poly *ct, const fhe_key *key,
                        uint32_t galois);
 /* EvalFastRotationPrecompute: ModUp'd digits of c1, in a new poly handle of
