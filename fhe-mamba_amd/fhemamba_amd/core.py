@@ -47,6 +47,7 @@ class Context:
         call("fhe_context_create", log_n, _ptr(qa), len(qa), _ptr(pa), len(p), dnum, device,
              ctypes.byref(h))
         self._h = h
+        self.device = device
         self.set_sampling(sampling, sampling_key)
         info = np.zeros(5, dtype=np.uint32)
         call("fhe_context_info", h, _ptr(info))

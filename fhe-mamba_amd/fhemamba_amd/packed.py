@@ -332,20 +332,22 @@ def monotone_routing(indices, scatter: bool, bits: int = 3):
 
 
 # ----------------------------------------------------------------- evaluator
-def default_pt_cache_bytes() -> int:
-    """Device budget of the evaluator's plaintext cache: 96 GiB, less if
-    the device has under 192 GiB free when the evaluator is built (the
-    rotation and bootstrapping keys, made later, need the rest), and at
-    least 8 GiB.  A Mamba-2-130M-shaped decode at N=2^16 encodes ~53 GiB of
-    in_proj / out_proj diagonals per token; a budget below its working set
-    evicts each diagonal set before its next use (LRU over a cyclic
-    sequence), so every token would encode them again."""
-    from ._lib import device_free_bytes
-    free = device_free_bytes()
+def default_pt_cache_bytes(device: int | None = None) -> int:
+    """Device budget of the evaluator's plaintext cache on `device` (the
+    evaluator's context's GPU): 96 GiB, less if the device has under 192
+    GiB free when the evaluator is built (the rotation and bootstrapping
+    keys, made later, need the rest), and never below an eighth of the free
+    memory, so the budget never exceeds what is free.  A
+    Mamba-2-130M-shaped decode at N=2^16 encodes ~53 GiB of in_proj /
+    out_proj diagonals per token; a budget below its working set evicts each
+    diagonal set before its next use (LRU over a cyclic sequence), so every
+    token would encode them again."""
+    from . import _lib
+    free = _lib.device_free_bytes(device)
     cap = 96 << 30
     if free is None:
         return 48 << 30
-    return int(max(8 << 30, min(cap, free - cap)))
+    return int(max(free // 8, min(cap, free - cap)))
 
 
 class PackedEvaluator:
@@ -378,7 +380,8 @@ class PackedEvaluator:
         self._masks: dict = {}  # host-side replicated-layout masks by matrix key
         self._pt_cache = PlaintextCache(cc.GetRingDimension(),
                                         pt_cache_bytes if pt_cache_bytes is not None
-                                        else default_pt_cache_bytes())
+                                        else default_pt_cache_bytes(
+                                            getattr(getattr(cc, "device", None), "device", None)))
         self.stats = dict(ct_ct=0, ct_pt=0, rotations=0, adds=0, bootstraps=0,
                           logical_refreshes=0, bootstrap_seconds=0.0, keygen_seconds=0.0,
                           rotation_keys=0, evaluated_nodes=0)

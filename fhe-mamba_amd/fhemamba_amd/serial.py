@@ -33,6 +33,7 @@ from __future__ import annotations
 import enum
 import hashlib
 import json
+import os
 import weakref
 import zlib
 
@@ -153,6 +154,14 @@ class _Reader:
         if dtype not in (np.dtype(np.uint64), np.dtype(np.int64)):
             raise SerialError(f"{self.path}: unexpected array type {dtype}")
         shape = tuple(int(d) for d in spec["shape"])
+        # Shapes come from the file: check them against the bytes the file
+        # still holds before allocating anything.
+        if len(shape) > 4 or any(d < 0 for d in shape):
+            raise SerialError(f"{self.path}: bad array shape {shape}")
+        nbytes = int(np.prod(shape, dtype=object)) * dtype.itemsize
+        left = os.fstat(self.f.fileno()).st_size - self.f.tell()
+        if nbytes > left:
+            raise SerialError(f"{self.path}: truncated ({nbytes} array bytes, {left} left)")
         a = np.empty(shape, dtype=dtype)
         got = self.f.readinto(memoryview(a.view(np.uint8).reshape(-1)))
         if got != a.nbytes:

@@ -324,12 +324,20 @@ def test_launcher_reports_bad_arguments_with_exit_code_2():
     assert r.returncode == 2 and "usage" in r.stderr
 
 
-@pytest.mark.parametrize("free_gib, want_gib", [(None, 48), (288, 96), (150, 54), (90, 8)])
-def test_plaintext_cache_budget_follows_free_device_memory(monkeypatch, free_gib, want_gib):
+@pytest.mark.parametrize("free_gib, want", [(None, 48 << 30), (288, 96 << 30),
+                                             (150, 54 << 30), (90, (90 << 30) // 8),
+                                             (4, 512 << 20)])
+def test_plaintext_cache_budget_follows_free_device_memory(monkeypatch, free_gib, want):
     """96 GiB (the 130M-shape decode's projection diagonals, ~53 GiB per
-    token, fit), less when under 192 GiB are free, never below 8 GiB; 48 GiB
-    when the free memory cannot be read."""
+    token, fit), less when under 192 GiB are free, never below an eighth of
+    the free memory (so never above it); 48 GiB when the free memory cannot
+    be read.  The free memory is that of the device asked for."""
     from fhemamba_amd import _lib
-    monkeypatch.setattr(_lib, "device_free_bytes",
-                        lambda: None if free_gib is None else free_gib << 30)
-    assert P.default_pt_cache_bytes() == want_gib << 30
+    seen = []
+
+    def free(device=None):
+        seen.append(device)
+        return None if free_gib is None else free_gib << 30
+    monkeypatch.setattr(_lib, "device_free_bytes", free)
+    assert P.default_pt_cache_bytes(3) == want
+    assert seen == [3]
