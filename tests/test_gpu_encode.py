@@ -9,7 +9,7 @@ pytestmark = pytest.mark.gpu
 F = pytest.importorskip("fhemamba_amd")
 
 
-@pytest.fixture(scope="module", params=[(12, 5, 40), (13, 7, 50), (16, 3, 59)])
+@pytest.fixture(scope="module", params=[(12, 5, 40), (13, 7, 50), (16, 3, 59), (17, 3, 59)])
 def pair(request):
     log_n, depth, sb = request.param
     q, p = O.gen_moduli(log_n, depth, sb, 60, 2)

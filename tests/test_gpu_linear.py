@@ -157,8 +157,40 @@ def test_hoisted_linear_transform_matches_oracle(setup, count, bstep, stride, of
     """fhe_linear_transform_hoisted: the offset folded into the babies'
     shared ModUp and one key per giant step (the giant rotations as one
     batch), bit-exact against the same composition of oracle rotations."""
+    check_hoisted(setup, count, bstep, stride, offset, nulls)
+
+
+@pytest.fixture(scope="module")
+def setup16():
+    q, p = O.gen_moduli(16, 9, 59, 60, 3)
+    ctx, orc = F.Context(16, q, p, 3, sampling="seeded"), O.Ctx(16, q, p, 3)
+    return ctx, orc, orc.secret(22), {}
+
+
+HOISTED16 = [
+    # a CoeffToSlot level-budget group of the N = 2^16 bootstrap: four
+    # radix-2 stages, 31 diagonals on an arithmetic progression of offsets
+    # (stride 2^9 here), baby step 8, four giant steps
+    (31, 8, 512, -15 * 512, ()),
+    # an in_proj-sized projection of the 130M decoder: 110 diagonals, baby
+    # step 10, eleven giant steps (two inner-sum passes of at most eight)
+    (110, 10, 1, 0, (5, 57)),
+]
+
+
+@pytest.mark.parametrize("count,bstep,stride,offset,nulls", HOISTED16)
+def test_hoisted_linear_transform_at_n65536(setup16, count, bstep, stride, offset, nulls):
+    """The hoisted transform (k_mac_giants, the batched giant key switches,
+    k_sum) and its Horner form at N = 2^16 with the giant-step counts of
+    the bootstrap and of the decoder's projections, bit-exact against the
+    oracle composition."""
+    print(f"[linear] N=2^16: {count} diagonals, baby step {bstep}", flush=True)
+    check_hoisted(setup16, count, bstep, stride, offset, nulls)
+
+
+def check_hoisted(setup, count, bstep, stride, offset, nulls):
     ctx, orc, s, _ = setup
-    rng = np.random.default_rng(300 + count + bstep + offset)
+    rng = np.random.default_rng((300 + count + bstep + offset) % 2**32)
     nq = ctx.L - 1
     ct = residues(rng, ctx.q[:nq], (2,), ctx.n)
     pts_host = [None if k in nulls else residues(rng, ctx.q, (), ctx.n)

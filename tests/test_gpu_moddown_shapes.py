@@ -85,6 +85,40 @@ def test_benchmark_shape_rotations():
     assert np.array_equal(got, orc.rotate(low, keys[gal[0]], gal[0]))
 
 
+def test_benchmark_step_matches_oracle():
+    """The benchmark's whole timed step (bench.py run_rotations) at its
+    parameters: the hoisted set {+-2^k, k < 15} of one ciphertext at
+    N = 2^16, L = 24, K = 8, dnum 3 (one ModUp, the 30 rotations as one
+    key-switch batch) and the rescale of the ciphertext; the ModUp digits,
+    every rotation and the rescale equal the oracle word for word (the
+    oracle's rotations on all usable cores)."""
+    import concurrent.futures as cf
+    import os
+    steps = [sg * (1 << k) for k in range(15) for sg in (1, -1)]
+    q, p = O.gen_moduli(16, 23, 59, 60, 3)
+    ctx, orc = F.Context(16, q, p, 3, sampling="seeded"), O.Ctx(16, q, p, 3)
+    assert (ctx.L, ctx.K, ctx.dnum) == (24, 8, 3)
+    s = ctx.keygen_secret(1)
+    gal = [F.galois_element(r, ctx.n) for r in steps]
+    keys = [ctx.keygen_galois(s, g, 1000 + i) for i, g in enumerate(gal)]
+    ct = residues(np.random.default_rng(7), ctx.q, (2,), ctx.n)
+    dct = ctx.upload(ct)
+    digits = ctx.rotation_precompute(dct)
+    outs = ctx.rotate_hoisted(dct, digits, keys, gal)
+    rs = ctx.rescale(dct)
+    print(f"[bench step] GPU done; oracle on {len(steps)} rotations", flush=True)
+    odig = orc.modup(ct[1])
+    assert np.array_equal(digits.numpy(), odig)
+    hkeys = [k.numpy() for k in keys]
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    with cf.ThreadPoolExecutor(threads) as ex:
+        want = list(ex.map(lambda i: orc.rotate_hoisted(ct, odig, hkeys[i], gal[i]),
+                           range(len(steps))))
+    for r, out, w in zip(steps, outs, want):
+        assert np.array_equal(out.numpy(), w), r
+    assert np.array_equal(rs.numpy(), orc.rescale(ct))
+
+
 @pytest.mark.parametrize("log_n,depth,dnum", [(14, 7, 4), (15, 9, 5), (13, 15, 8),
                                                (16, 7, 4), (16, 9, 5), (16, 11, 6),
                                                (16, 13, 7)])
