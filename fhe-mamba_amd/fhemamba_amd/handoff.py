@@ -94,15 +94,18 @@ def _scope(**kw) -> dict:
 
 
 def client_init(payload_dir: str, handoff_dir: str, *, tokens: int = 0,
-                bootstrap_passes: int = 2, seed=None, secret_key_dist=None,
+                bootstrap_passes: int = 2, transient_passes: int | None = None, seed=None,
+                secret_key_dist=None,
                 security: str = "not-set", layers: int = 0, s2c_first: bool = True,
                 ring_dim: int = 0, log=print) -> dict:
     from . import ckks
     from .keyplan import decoder_rotations
-    from .mamba2_decode import _build, _decode_setup, _truncate
+    from .mamba2_decode import _build, _decode_setup, _truncate, default_transient_passes
     paths = HandoffPaths(handoff_dir)
     chain, classical, dist, slots, extra = _decode_setup(payload_dir, security,
                                                          secret_key_dist, ring_dim)
+    if transient_passes is None:
+        transient_passes = default_transient_passes(dist, bootstrap_passes)
     _truncate(chain, layers)
     n_tok = tokens or chain.n_test_tokens
     if n_tok > chain.n_test_tokens:
@@ -133,6 +136,7 @@ def client_init(payload_dir: str, handoff_dir: str, *, tokens: int = 0,
     with open(os.path.join(paths.server, "handoff.json"), "w") as f:
         json.dump({"slots": slots, "s2c_first": bool(s2c_first),
                    "bootstrap_passes": int(bootstrap_passes),
+                   "transient_passes": int(transient_passes),
                    "level_budget": list(LEVEL_BUDGET), "tokens": n_tok,
                    "layers": chain.n_layers}, f)
     for k in range(n_tok):
@@ -181,6 +185,7 @@ def server_eval(payload_dir: str, handoff_dir: str, *, tokens: int = 0, layers: 
         raise ValueError("the server context's batch size differs from the handoff plan")
     keys = ckks.KeyPair(pk, None)
     dec = EncryptedMamba2Decoder(cc, keys, chain, bootstrap_passes=int(plan["bootstrap_passes"]),
+                                 transient_passes=int(plan.get("transient_passes", 1)),
                                  s2c_first=bool(plan["s2c_first"]), log=log)
     setup = time.perf_counter() - t0
     log("server key load done secret_key_loaded=false")

@@ -71,8 +71,9 @@ class LayerCtState:
 
 class EncryptedMamba2Decoder:
     def __init__(self, cc, keys, chain: ChainPayload, *, bootstrap_passes: int = 2,
-                 refresh_ceiling: int | None = None, bounds: dict | None = None, log=None,
-                 s2c_first: bool = False, level_budget=(4, 4)):
+                 transient_passes: int = 1, refresh_ceiling: int | None = None,
+                 bounds: dict | None = None, log=None, s2c_first: bool = False,
+                 level_budget=(4, 4)):
         first = chain.layers[0]
         self.chain, self.cc = chain, cc
         self.slots = cc.GetBatchSize()
@@ -80,6 +81,18 @@ class EncryptedMamba2Decoder:
         self.ev = PackedEvaluator(cc, keys, self.slots, bootstrap_passes=bootstrap_passes,
                                   refresh_ceiling=refresh_ceiling, log=self.log,
                                   s2c_first=s2c_first, level_budget=tuple(level_budget))
+        # Refresh passes by site, the reference decoder's Meta-BTS rule
+        # (should_use_meta_bts, stage1_mamba2_config.cpp:64-81): two-pass
+        # refreshes (bootstrap_passes) for the carried lineages (SSM state,
+        # the projection kept in the conv FIFO), the gated norm's polynomial
+        # input, the residual of the last three layers, the final output and
+        # every refresh inside a scheduled normalization; one pass
+        # (transient_passes) for the other transient values.
+        if transient_passes not in (1, 2):
+            raise ValueError("transient bootstrap passes must be 1 or 2")
+        self.critical_passes = bootstrap_passes
+        self.transient_passes = min(transient_passes, bootstrap_passes)
+        self._critical_residual = set(range(max(0, len(chain.layers) - 3), len(chain.layers)))
         self.bounds = [self._layer_bounds(lay, bounds) for lay in chain.layers]
         self.d, self.di, self.ns = first.d_model, first.d_inner, first.state_size
         self.nh, self.hd, self.kc = first.num_heads, first.head_dim, first.conv_kernel
@@ -124,11 +137,12 @@ class EncryptedMamba2Decoder:
         b.update(override or {})
         return b
 
-    def ready(self, ct, need: int, bound: float, support=None):
+    def ready(self, ct, need: int, bound: float, support=None, critical: bool = False):
         """Refresh ct (masked to `support`) if `need` more levels would pass
-        the ceiling."""
+        the ceiling; `critical` refreshes take the two-pass count."""
         if self.ev._level(ct) + need > self.ev.refresh_ceiling:
-            return self.ev.refresh(ct, bound, support if support is not None else self.slots)
+            return self.ev.refresh(ct, bound, support if support is not None else self.slots,
+                                   self.critical_passes if critical else self.transient_passes)
         return ct
 
     def full_sum(self, ct):
@@ -196,21 +210,22 @@ class EncryptedMamba2Decoder:
         fbound = BOUND_MARGIN * max(a for a, _ in spec.coefficients)
         ubound = BOUND_MARGIN
         n = len(spec.coefficients)
-        v = self.ready(v, 3, vbound)
+        v = self.ready(v, 3, vbound, critical=True)
         u = ev.scale(v, spec.seed * spec.seed)
         y = None
         for i, (a, b) in enumerate(spec.coefficients):
-            u = self.ready(u, 4, ubound)
+            u = self.ready(u, 4, ubound, critical=True)
             f = cc.EvalAdd(ev.scale(u, -b), a)
             if y is None:
                 y = ev.scale(f, spec.seed)
             else:
-                y = ev.mul(self.ready(y, 1, ibound), self.ready(f, 1, fbound))
+                y = ev.mul(self.ready(y, 1, ibound, critical=True),
+                           self.ready(f, 1, fbound, critical=True))
             if i + 1 < n:
-                f = self.ready(f, 2, fbound)
+                f = self.ready(f, 2, fbound, critical=True)
                 u = ev.mul(u, ev.mul(f, f))
-        y = self.ready(y, 3, ibound)
-        v = self.ready(v, 2, vbound)
+        y = self.ready(y, 3, ibound, critical=True)
+        v = self.ready(v, 2, vbound, critical=True)
         t = ev.mul(v, ev.mul(y, y))
         return ev.mul(y, cc.EvalAdd(ev.scale(t, -0.5), 1.5))
 
@@ -297,7 +312,8 @@ class EncryptedMamba2Decoder:
         # matvec runs on the shallow residual (block_norm_w folded in); one
         # refresh of the residual serves the variance, the matvec and the
         # residual add
-        hidden = self.ready(hidden, 4, B["residual"], self._support(0, self.d))
+        res_critical = li in self._critical_residual
+        hidden = self.ready(hidden, 4, B["residual"], self._support(0, self.d), res_critical)
         inv = self.rms_scale(hidden, self.d, lay.eps_block, lay.polys["rms_invsqrt"],
                              B["residual"], B["variance"], B["inv"])
         w_in = t("in_proj_w") * t("block_norm_w")[None, :]
@@ -309,14 +325,14 @@ class EncryptedMamba2Decoder:
         need = max(2, self.cheb_need(lay.polys["gate_silu"]),
                    self.cheb_need(lay.polys["dt_softplus"]) + 2 if lay.joint is None
                    else self.joint_need(lay.joint))
-        proj = self.ready(proj, need, B["proj"], psup)
+        proj = self.ready(proj, need, B["proj"], psup, critical=True)  # kept in the FIFO
         # conv over the FIFO of raw proj ciphertexts (taps on the xBC slots)
         window = list(st.fifo) + [proj]
         xs = self._support(di, cd)
         pad = self.kc - len(window)
         conv = None
         for k, ct in enumerate(window):
-            ct = self.ready(ct, 2, B["proj"], psup)
+            ct = self.ready(ct, 2, B["proj"], psup, critical=True)
             term = ev.plain(ct, self._vec({di: t("conv_w")[:, pad + k]}), True)
             conv = term if conv is None else ev.add(conv, term)
         conv = ev.plain(conv, self._vec({di: t("conv_b")}), False)
@@ -381,11 +397,11 @@ class EncryptedMamba2Decoder:
             write = ev.mul(ev.mul(xg, dg), br)
             if st.ssm is not None:
                 eg = self.ready(decay_groups[g], 2, B["decay"])
-                hg = self.ready(st.ssm[g], 2, B["state"])
+                hg = self.ready(st.ssm[g], 2, B["state"], critical=True)
                 h2 = ev.add(ev.mul(eg, hg), write)
             else:
                 h2 = write
-            h2 = self.ready(h2, 3, B["state"])
+            h2 = self.ready(h2, 3, B["state"], critical=True)
             new_ssm.append(h2)
             cr = self.ready(c_rep, 3, B["act"])
             reads.append(ev.mul(h2, cr))
@@ -411,7 +427,7 @@ class EncryptedMamba2Decoder:
         gated = ev.mul(y, gate)
         # gated norm: out_proj(gated * inv2) = out_proj(gated) * inv2 (one
         # refresh of gated serves the variance and the matvec)
-        gated = self.ready(gated, 4, B["gated"], zs)
+        gated = self.ready(gated, 4, B["gated"], zs, critical=True)
         inv2 = self.rms_scale(gated, di, lay.eps_gated, lay.polys["gated_rms_invsqrt"],
                               B["gated"], B["gated_variance"], B["gated_inv"])
         w_out = t("out_proj_w") * t("gated_norm_w")[None, :]
@@ -419,7 +435,7 @@ class EncryptedMamba2Decoder:
         dsup = self._support(0, self.d)
         out = self.times_scale(ev.linear(gin, w_out, ("out_proj", li)), inv2, B["out_raw"],
                                dsup, B["gated_inv"])
-        hidden = self.ready(hidden, 1, B["residual"], dsup)
+        hidden = self.ready(hidden, 1, B["residual"], dsup, res_critical)
         new_hidden = ev.add(hidden, out)
         fifo = (list(st.fifo) + [proj])[-(self.kc - 1):] if self.kc > 1 else []
         self.stats["layers"] += 1
@@ -446,7 +462,7 @@ class EncryptedMamba2Decoder:
                      f"bootstraps {self.ev.stats['bootstraps']}")
         last = self.chain.layers[-1]
         B = self.bounds[-1]
-        h = self.ready(h, 3, B["out_residual"], self._support(0, self.d))
+        h = self.ready(h, 3, B["out_residual"], self._support(0, self.d), critical=True)
         inv = self.rms_scale(h, self.d, self.chain.final_norm_eps, self.chain.final_invsqrt(),
                              B["out_residual"], B["out_variance"], B["out_inv"])
         final = self.ev.plain(h, self._vec({0: self.chain.final_norm_w}), True)
@@ -519,6 +535,16 @@ def token_loop(dec: EncryptedMamba2Decoder, chain: ChainPayload, n_tok: int, ar=
 SECRET_KEY_DISTS = {"sparse-ternary": "SPARSE_TERNARY", "uniform-ternary": "UNIFORM_TERNARY"}
 
 
+def default_transient_passes(secret_key_dist: str, bootstrap_passes: int) -> int:
+    """Passes of the refreshes outside the precision-critical sites: one
+    with a sparse-ternary secret (a single pass reaches ~2^-19 of the bound
+    at N = 2^16; the 24-layer 130M decode stays within 3e-5 of the
+    polynomial circuit), otherwise as many as the critical ones (a single
+    pass with a uniform-ternary secret reaches ~2^-13 and the classical-128
+    decode would exceed 1e-3)."""
+    return 1 if secret_key_dist == "sparse-ternary" else bootstrap_passes
+
+
 def _decode_setup(payload_dir, security, secret_key_dist, ring_dim, sizes=None):
     from .mamba2_payload import read_chain_payload
     from .packed import CLASSICAL128
@@ -558,7 +584,8 @@ def _build(slots, seed, secret_key_dist, extra):
         ckks.SecretKeyDist, SECRET_KEY_DISTS[secret_key_dist]), **extra)
 
 
-def run_payload(payload_dir: str, *, tokens: int = 0, bootstrap_passes: int = 2, seed=None,
+def run_payload(payload_dir: str, *, tokens: int = 0, bootstrap_passes: int = 2,
+                transient_passes: int | None = None, seed=None,
                 secret_key_dist: str | None = None, security: str = "not-set",
                 layers: int = 0, autoregressive: bool = False, s2c_first: bool = True,
                 ring_dim: int = 0, sizes: dict | None = None, level_budget=(4, 4),
@@ -594,6 +621,8 @@ def run_payload(payload_dir: str, *, tokens: int = 0, bootstrap_passes: int = 2,
     (not-set only; default 2^16) picks a smaller ring for small payloads."""
     chain, classical, secret_key_dist, slots, extra = _decode_setup(
         payload_dir, security, secret_key_dist, ring_dim, sizes)
+    if transient_passes is None:
+        transient_passes = default_transient_passes(secret_key_dist, bootstrap_passes)
     n_layers_total = chain.n_layers
     ar = chain.autoregressive if autoregressive else None
     if autoregressive:
@@ -611,7 +640,8 @@ def run_payload(payload_dir: str, *, tokens: int = 0, bootstrap_passes: int = 2,
     t0 = time.perf_counter()
     cc, keys = _build(slots, seed, secret_key_dist, extra)
     audit = cc.SecurityAudit() if classical else None
-    dec = EncryptedMamba2Decoder(cc, keys, chain, bootstrap_passes=bootstrap_passes, log=log,
+    dec = EncryptedMamba2Decoder(cc, keys, chain, bootstrap_passes=bootstrap_passes,
+                                 transient_passes=transient_passes, log=log,
                                  s2c_first=s2c_first, level_budget=level_budget)
     setup = time.perf_counter() - t0
     loop = token_loop(dec, chain, n_tok, ar, cc.device.sync, log)
@@ -659,6 +689,7 @@ def run_payload(payload_dir: str, *, tokens: int = 0, bootstrap_passes: int = 2,
         "decrypt_seconds": loop["decrypt_seconds"],
         "token0_samples": loop["token0"],
         "level_budget": list(level_budget),
+        "refresh_passes": [dec.critical_passes, dec.transient_passes],
         "multiplicative_depth": len(cc.GetModuli()[0]) - 1,
         "dims": {"d_model": dec.d, "d_inner": dec.di, "num_heads": dec.nh,
                  "head_dim": dec.hd, "state_size": dec.ns, "conv_kernel": dec.kc,
@@ -675,7 +706,12 @@ def main(argv=None) -> int:
     ap.add_argument("payload")
     ap.add_argument("result")
     ap.add_argument("--tokens", type=int, default=0)
-    ap.add_argument("--bootstrap-passes", type=int, default=2, choices=(1, 2))
+    ap.add_argument("--bootstrap-passes", type=int, default=2, choices=(1, 2),
+                    help="passes of the precision-critical refreshes (carried state, FIFO, "
+                         "gated norm input, last residuals, scheduled normalization)")
+    ap.add_argument("--transient-passes", type=int, default=None, choices=(1, 2),
+                    help="passes of the other refreshes (default: 1 with a sparse-ternary "
+                         "secret, else --bootstrap-passes)")
     ap.add_argument("--tolerance", type=float, default=1e-3,
                     help="pass threshold on the error against the polynomial circuit")
     ap.add_argument("--secret-key-dist", default=None, choices=sorted(SECRET_KEY_DISTS),
@@ -705,6 +741,7 @@ def main(argv=None) -> int:
                 report = H.client_init(
                     args.payload, args.handoff_dir, tokens=args.tokens,
                     bootstrap_passes=args.bootstrap_passes,
+                    transient_passes=args.transient_passes,
                     secret_key_dist=args.secret_key_dist, security=args.security,
                     layers=args.layers, s2c_first=not args.ordinary_bootstrap,
                     ring_dim=args.ring_dim)
@@ -723,6 +760,7 @@ def main(argv=None) -> int:
     try:
         report = run_payload(args.payload, tokens=args.tokens,
                              bootstrap_passes=args.bootstrap_passes,
+                             transient_passes=args.transient_passes,
                              secret_key_dist=args.secret_key_dist, security=args.security,
                              layers=args.layers,
                              autoregressive=args.autoregressive_client_loop,

@@ -367,7 +367,12 @@ def run_inline(c: Config, log=print) -> dict:
     n_total = read_chain_payload(c.input_chain).n_layers
     layers = min(c.max_layers, n_total) if c.max_layers > 0 else 0
     t0 = time.perf_counter()
+    # --meta-bts: two-pass refreshes at the precision-critical sites (the
+    # reference's Meta-BTS selection) and the decoder's default elsewhere;
+    # without it every refresh is one bootstrap pass, as the reference's
+    # single EvalBootstrap.
     r = run_payload(c.input_chain, tokens=c.tokens, secret_key_dist=c.secret_key_dist,
+                    bootstrap_passes=2 if c.meta_bts else 1,
                     security=c.security, layers=layers,
                     autoregressive=c.autoregressive_client_loop,
                     ring_dim=c.ring_dim if c.security == "not-set" else 0,
@@ -402,6 +407,8 @@ def run_inline(c: Config, log=print) -> dict:
               "bootstrap_level_budget": r["level_budget"],
               "security_audit": r["security_audit"],
               "refresh_order": "slot-to-coeff-first" if r["s2c_first"] else "ordinary",
+              "refresh_passes": {"critical": r["refresh_passes"][0],
+                                 "transient": r["refresh_passes"][1]},
               "recorded_options": _recorded(c)}
     params["max_layers"] = c.max_layers
     params["fideslib_sync_profile"] = c.fideslib_sync_profile
@@ -484,6 +491,7 @@ def run_role(c: Config, log=print) -> dict:
         raise ValueError("the process roles run depth 44, 59-bit scale, 60-bit first prime")
     if c.process_role == "client-init":
         rep = H.client_init(c.input_chain, c.handoff_dir, tokens=c.tokens,
+                            bootstrap_passes=2 if c.meta_bts else 1,
                             secret_key_dist=c.secret_key_dist, security=c.security,
                             layers=layers,
                             ring_dim=c.ring_dim if c.security == "not-set" else 0)

@@ -514,10 +514,14 @@ class PackedEvaluator:
         return outs
 
     # ------------------------------------------------------------- refresh
-    def refresh(self, ct, bound: float, support):
+    def refresh(self, ct, bound: float, support, passes: int | None = None):
         """Mask ct to its support (a width or a 0/1 slot vector; padding is
         never bootstrapped), scale into [-1, 1] by 1 / bound, bootstrap and
-        scale back."""
+        scale back; `passes` (1 or 2) overrides the evaluator's
+        bootstrap_passes for this refresh."""
+        passes = self.bootstrap_passes if passes is None else passes
+        if passes not in (1, 2):
+            raise ValueError("bootstrap passes must be 1 or 2")
         t0 = time.perf_counter()
         if isinstance(support, (int, np.integer)):
             x = self.mask(ct, int(support)) if support < self.slots else ct
@@ -528,9 +532,8 @@ class PackedEvaluator:
         # for every bound (it goes into EvalMod's integer gain or the last
         # group's constant), at most one bit of the range given up
         bound = 2.0 ** math.ceil(math.log2(max(float(bound), 2.0 ** -30)))
-        out = self.cc.EvalBootstrap(x, self.bootstrap_passes, REFRESH_SCALE_BITS,
-                                    scale=bound)
-        self.stats["bootstraps"] += self.bootstrap_passes
+        out = self.cc.EvalBootstrap(x, passes, REFRESH_SCALE_BITS, scale=bound)
+        self.stats["bootstraps"] += passes
         self.stats["logical_refreshes"] += 1
         self.stats["bootstrap_seconds"] += time.perf_counter() - t0
         return out

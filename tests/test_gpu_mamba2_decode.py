@@ -23,7 +23,9 @@ def test_two_layer_decode_with_carried_state(tmp_path):
     print(f"decode: {report['seconds_per_token']} s/token, errors "
           f"{report['per_token_errors_vs_polynomial']}", flush=True)
     assert report["max_abs_error_vs_polynomial"] < TOL
-    assert report["logical_refreshes"] > 0 and report["bootstraps"] == 2 * report["logical_refreshes"]
+    # two-pass refreshes at the precision-critical sites, one pass elsewhere
+    r, b = report["logical_refreshes"], report["bootstraps"]
+    assert r > 0 and r < b < 2 * r
 
 
 def test_command_line(tmp_path):

@@ -123,6 +123,7 @@ def fake_decode(n_layers, n_tok, errs, selected, expected):
                 "decrypt_seconds": 0.01, "token0_samples": {"decrypted": [0.0],
                                                             "expected": [0.0], "exact": [0.0]},
                 "level_budget": list(kw["level_budget"]), "multiplicative_depth": 44,
+                "refresh_passes": [kw["bootstrap_passes"], 1],
                 "dims": {"d_model": 64, "d_inner": 128, "num_heads": 8, "head_dim": 16,
                          "state_size": 16, "conv_kernel": 4, "conv_dim": 160, "proj_dim": 296,
                          "n_groups": 1, "state_group_count": 1}}
