@@ -457,7 +457,183 @@ def _cpu_threads() -> tuple[int, int]:
     return max(1, min(usable, omp, 16)), nproc
 
 
-def cpu_baseline(budget_s: float = 24.0):
+class OpTally:
+    """Counts the library calls a decode makes, by operation class and limb
+    count, by wrapping the device-context methods (fhemamba_amd.core.Context)
+    for the duration of a `with` block.  Classes:
+      ks      full key switch with its own ModUp (rotate, keyswitch,
+              relinearize, each ciphertext of rotate_many, each Horner or
+              batched giant step of a linear transform);
+      modup   a shared ModUp (rotation_precompute; the babies of a linear
+              transform);
+      hks     a hoisted key switch from shared digits (each key of
+              rotate_hoisted; each rotated baby of a linear transform);
+      rescale, tensor, modraise;
+      pmul    one plaintext or constant product over 2 polys (mul_plain,
+              mul_const, mul_int, each diagonal of a linear transform, each
+              term of linear_wsum);
+      add     one elementwise addition-class op over 2 polys;
+      encode  one encoded vector (per row of encode_many).
+    `snapshot()` returns the counts so far; the decode's per-token counts are
+    differences of snapshots taken before each step."""
+
+    def __init__(self, Context):
+        import collections
+        self.Context = Context
+        self.counts = collections.Counter()
+        self._saved = {}
+
+    def _wrap(self, name, tally):
+        orig = getattr(self.Context, name)
+        self._saved[name] = orig
+
+        def wrapper(ctx, *a, **k):
+            tally(*a, **k)
+            return orig(ctx, *a, **k)
+        setattr(self.Context, name, wrapper)
+
+    def __enter__(self):
+        c = self.counts
+
+        def one(cls, pos=0):
+            return lambda *a, **k: c.update({(cls, a[pos].nlimb): 1})
+
+        def lt(ct, pts, bstep, baby_keys, *rest, giant_keys=None, hoisted=False, **k):
+            n = ct.nlimb
+            count = len(pts)
+            giants = -(-count // bstep)
+            c[("pmul", n)] += sum(p is not None for p in pts)
+            c[("modup", n)] += 1
+            c[("hks", n)] += sum(x is not None for x in baby_keys)
+            c[("ks", n)] += max(0, giants - 1)
+
+        for name in ("add", "sub", "negate", "add_plain", "add_const"):
+            self._wrap(name, one("add"))
+        for name in ("mul_plain", "mul_const", "mul_int"):
+            self._wrap(name, one("pmul"))
+        for name in ("keyswitch", "relinearize", "rotate"):
+            self._wrap(name, one("ks"))
+        self._wrap("rescale", one("rescale"))
+        self._wrap("tensor", one("tensor"))
+        self._wrap("rotation_precompute", one("modup"))
+        self._wrap("mod_raise", lambda a, nlimb, *r, **k: c.update({("modraise", nlimb): 1}))
+        self._wrap("linear_wsum",
+                   lambda terms, w, nlimb, *r, **k: c.update({("pmul", nlimb): len(terms)}))
+        self._wrap("rotate_hoisted",
+                   lambda ct, d, keys, *r, **k: c.update({("hks", ct.nlimb): len(keys)}))
+        self._wrap("rotate_many",
+                   lambda cts, *r, **k: c.update([("ks", x.nlimb) for x in cts]))
+        self._wrap("linear_transform", lambda *a, **k: lt(*a, **k))
+        self._wrap("linear_transform_hoisted", lambda *a, **k: lt(*a, **k))
+        self._wrap("encode", lambda v, slots, scale, nlimb, *r, **k:
+                   c.update({("encode", nlimb): 1}))
+        self._wrap("encode_many", lambda rows, slots, scale, nlimb, *r, **k:
+                   c.update({("encode", nlimb): len(rows)}))
+        return self
+
+    def __exit__(self, *exc):
+        for name, orig in self._saved.items():
+            setattr(self.Context, name, orig)
+        self._saved.clear()
+
+    def snapshot(self):
+        return dict(self.counts)
+
+
+def count_decode_ops(tokens: int = 2):
+    """Library operations of one carried-state token of the 24-layer decode
+    at N = 2^16 (the decode workload's payload and parameters): a separate
+    pass with the tally installed, so the timed decode runs unwrapped."""
+    import tempfile
+    from fhemamba_amd import core
+    from fhemamba_amd import mamba2_decode as D
+    from fhemamba_amd import mamba2_payload as M
+    snaps = []
+    step = D.EncryptedMamba2Decoder.step
+    with tempfile.TemporaryDirectory() as d, OpTally(core.Context) as tally:
+        M.synthetic_chain(d, n_layers=24, n_test_tokens=tokens, seed=13)
+
+        def counted(dec, *a, **k):
+            snaps.append(tally.snapshot())
+            return step(dec, *a, **k)
+        D.EncryptedMamba2Decoder.step = counted
+        try:
+            D.run_payload(d, seed=14, log=lambda m: None)
+        finally:
+            D.EncryptedMamba2Decoder.step = step
+        snaps.append(tally.snapshot())
+    last, prev = snaps[-1], snaps[-2]
+    return {k: v - prev.get(k, 0) for k, v in last.items() if v - prev.get(k, 0)}
+
+
+def cpu_decode_estimate(ops: dict, threads: int, parallel_speedup: float) -> dict:
+    """Seconds per carried-state token of the 24-layer decode on the host
+    CPU, estimated: the token's library operations (count_decode_ops) times
+    the oracle's measured time for each operation class at N = 2^16 on one
+    thread, interpolated linearly in the limb count between the measured
+    levels.  The all-threads figure divides by the oracle's measured
+    limb-parallel speed-up (its batched NTT on `threads` threads), the way a
+    CPU library parallelises these operations over limbs.  An estimate of a
+    port of these algorithms, not a run of OpenFHE."""
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    q, p = O.gen_moduli(LOG_N, 44, SCALE_BITS, FIRST_BITS, DNUM)
+    c = O.Ctx(LOG_N, q, p, DNUM)
+    s = c.secret(1)
+    g = O.galois_elt(1, N)
+    key = c.galois_key(s, g, 5)
+    rng = np.random.default_rng(9)
+    levels = [4, 12, 24, 34, 45]
+    ct_full = np.stack([np.stack([rng.integers(0, qj, N, dtype=np.uint64) for qj in q])
+                        for _ in range(2)])
+    vals = rng.uniform(-1, 1, N // 2)
+
+    def t(fn, reps=1):
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        return (time.perf_counter() - t0) / reps
+
+    table = {k: [] for k in ("ks", "modup", "hks", "rescale", "tensor", "pmul", "add",
+                             "modraise", "encode")}
+    for nq in levels:
+        ct = np.ascontiguousarray(ct_full[:, :nq])
+        dig = c.modup(ct[1])
+        table["ks"].append(t(lambda: c.rotate(ct, key, g)))
+        table["modup"].append(t(lambda: c.modup(ct[1])))
+        table["hks"].append(t(lambda: c.rotate_hoisted(ct, dig, key, g)))
+        table["rescale"].append(t(lambda: c.rescale(ct)))
+        table["tensor"].append(t(lambda: c.tensor(ct, ct), 2))
+        table["pmul"].append(t(lambda: c.mac(ct[None], ct[:1, :, :]), 3))
+        table["add"].append(t(lambda: c.add(ct, ct), 3))
+        table["modraise"].append(t(lambda: (c.ntt_inv_batch(ct[:, :1]),
+                                            c.ntt_fwd_batch(ct, 0))))
+        table["encode"].append(t(lambda: c.encode(vals, N // 2, 2.0**59, nq)))
+
+    def cost(cls, nq):
+        return float(np.interp(nq, levels, table[cls]))
+
+    total, by_class = 0.0, {}
+    for (cls, nq), n in ops.items():
+        sec = n * cost(cls, nq)
+        by_class[cls] = by_class.get(cls, 0.0) + sec
+        total += sec
+    return {
+        "one_thread": total,
+        "all_threads": total / parallel_speedup,
+        "threads": threads,
+        "parallel_speedup": parallel_speedup,
+        "seconds_by_class_one_thread": by_class,
+        "operations_per_token": {cls: sum(n for (k, _), n in ops.items() if k == cls)
+                                 for cls in table},
+        "oracle_seconds_one_thread": {"levels": levels, **table},
+    }
+
+
+def cpu_baseline(budget_s: float = 24.0, decode_ops: dict | None = None):
     """The oracle (this build's scalar C restatement of the same algorithms;
     OpenFHE is not installed on this host) at the benchmark shape on a
     bounded sample:
@@ -531,6 +707,20 @@ def cpu_baseline(budget_s: float = 24.0):
                      budget_s * 0.1, 1)
         return n * ntt_bytes / t / 1e9
 
+    ntt_one, ntt_all = ntt_rate(1), ntt_rate(threads)
+    decode = None
+    if decode_ops:
+        decode = cpu_decode_estimate(decode_ops, threads, ntt_all / ntt_one)
+        decode = {"kind": "port-estimate",
+                  "s_per_token_one_thread": decode["one_thread"],
+                  "s_per_token_all_threads": decode["all_threads"],
+                  "workload": ("one carried-state token of the 24-layer Mamba-2-130M-shaped "
+                               "decode at N=2^16, depth 44 (the mamba2_decode workload): its "
+                               "library operations counted by class and limb count, times the "
+                               "oracle's measured one-thread time of each class at N=2^16 "
+                               "(interpolated in the limb count); all threads: divided by the "
+                               "oracle's measured limb-parallel speed-up"),
+                  **{k: v for k, v in decode.items() if k not in ("one_thread", "all_threads")}}
     return {
         "value": rots / step_all,
         "unit": "rotations/s",
@@ -547,8 +737,9 @@ def cpu_baseline(budget_s: float = 24.0):
         "single_rotations_per_s_one_thread": n2 / t2,
         "modup_s": modup_s,
         "rescale_s": rescale_s,
-        "ntt_gbps": {"one_thread": ntt_rate(1), "all_threads": ntt_rate(threads)},
+        "ntt_gbps": {"one_thread": ntt_one, "all_threads": ntt_all},
         "ntt_sample": "forward NTT of 8 ciphertexts x 24 limbs (60-bit primes) at N=2^16",
+        "decode_s_per_token": decode,
     }
 
 
@@ -651,10 +842,15 @@ def main() -> int:
         log("bootstrap workload")
         out["bootstrap"] = run_bootstrap()
         gc.collect()
+    decode_ops = None
     if not args.skip_decode:
         log("mamba-2 decode workload")
         out["mamba2_decode"] = run_decode()
         gc.collect()
+        if not args.no_cpu_baseline:
+            log("mamba-2 decode operation count (for the CPU estimate)")
+            decode_ops = count_decode_ops()
+            gc.collect()
         log("mamba-2 decode workload, classical-128")
         out["mamba2_decode_classical128"] = run_decode(tokens=3, security="128-classic")
         gc.collect()
@@ -663,7 +859,7 @@ def main() -> int:
         copy_probe(F)
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle)")
-        out["cpu_baseline"] = cpu_baseline()
+        out["cpu_baseline"] = cpu_baseline(decode_ops=decode_ops)
     print(json.dumps(out))
     return 0
 

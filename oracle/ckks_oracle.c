@@ -489,6 +489,20 @@ void orc_mac_batch(const orc_ctx *c, const uint64_t *x, const uint64_t *w,
   }
 }
 
+/* EvalAdd on matching limbs (OpenFHE DCRTPoly operator+, per limb
+ * (a + b) mod q_l): out = a + b over npoly polys of nq limbs each. */
+void orc_add(const orc_ctx *c, const uint64_t *a, const uint64_t *b, uint32_t npoly,
+             uint32_t nq, uint64_t *out) {
+  const size_t n = c->n;
+  for (size_t t = 0; t < (size_t)npoly * nq; ++t) {
+    const uint64_t q = c->mods[t % nq];
+    for (size_t e = 0; e < n; ++e) {
+      const uint64_t s = a[t * n + e] + b[t * n + e];
+      out[t * n + e] = s >= q ? s - q : s;
+    }
+  }
+}
+
 /* ======================================================================
  * Hybrid key switching (OpenFHE KeySwitchHYBRID: EvalKeySwitchPrecomputeCore,
  * EvalFastKeySwitchCoreExt, ApproxModDown)

@@ -94,6 +94,10 @@ void orc_ntt_inv_batch(const orc_ctx *c, uint64_t *data, uint32_t npoly,
 void orc_mac_batch(const orc_ctx *c, const uint64_t *x, const uint64_t *w,
                    uint32_t ncts, uint32_t nq, uint64_t *acc, int nthreads);
 
+/* out = a + b mod q_l on npoly polys of nq limbs ([npoly][nq][N]). */
+void orc_add(const orc_ctx *c, const uint64_t *a, const uint64_t *b, uint32_t npoly,
+             uint32_t nq, uint64_t *out);
+
 /* Hybrid key switching.  A key is [dnum][2][L+K][N] (b then a), evaluation
  * form over Q then P.  Ciphertext polys are evaluation form [nq][N]. */
 uint32_t orc_num_digits(const orc_ctx *c, uint32_t nq);

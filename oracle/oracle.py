@@ -56,6 +56,7 @@ def _load():
         "orc_ntt_fwd_batch": (None, [_p, _p, _u32, _u32, _u32, ctypes.c_int]),
         "orc_ntt_inv_batch": (None, [_p, _p, _u32, _u32, _u32, ctypes.c_int]),
         "orc_mac_batch": (None, [_p, _p, _p, _u32, _u32, _p, ctypes.c_int]),
+        "orc_add": (None, [_p, _p, _p, _u32, _u32, _p]),
         "orc_num_digits": (_u32, [_p, _u32]),
         "orc_modup": (None, [_p, _p, _u32, _p]),
         "orc_ksk_inner": (None, [_p, _p, _u32, _p, _p]),
@@ -208,6 +209,15 @@ class Ctx:
         acc = np.zeros((2, nq, self.n), dtype=np.uint64)
         lib.orc_mac_batch(self.h, ptr(x), ptr(w), ncts, nq, ptr(acc), nthreads)
         return acc
+
+    def add(self, a, b):
+        """a + b mod q_l limb by limb for polys [..., nq, N] (EvalAdd)."""
+        a, b = u64(a), u64(b)
+        nq = a.shape[-2]
+        npoly = int(np.prod(a.shape[:-2])) if a.ndim > 2 else 1
+        out = np.zeros_like(a)
+        lib.orc_add(self.h, ptr(a), ptr(b), npoly, nq, ptr(out))
+        return out
 
     def num_digits(self, nq):
         return int(lib.orc_num_digits(self.h, nq))

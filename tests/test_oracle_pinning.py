@@ -522,3 +522,24 @@ def test_hoisted_rotation_equals_single_rotation(small_scheme):
         g = O.galois_elt(step, c.n)
         key = c.galois_key(s, g, 50 + step)
         assert np.array_equal(c.rotate_hoisted(ct, digits, key, g), c.rotate(ct, key, g))
+
+
+def test_add_matches_big_integer_sum():
+    """orc_add (EvalAdd per limb) against Python integers, including the
+    largest residues (q - 1 + q - 1) and 61-bit moduli where a + b carries
+    past 2^61."""
+    q, p = O.gen_moduli(12, 5, 59, 61, 2)
+    c = O.Ctx(12, q, p, 2)
+    rng = np.random.default_rng(77)
+    a = np.stack([np.stack([rng.integers(0, qj, c.n, dtype=np.uint64) for qj in q])
+                  for _ in range(2)])
+    b = np.stack([np.stack([rng.integers(0, qj, c.n, dtype=np.uint64) for qj in q])
+                  for _ in range(2)])
+    for j, qj in enumerate(q):
+        a[:, j, :4] = qj - 1
+        b[:, j, :4] = [qj - 1, 1, 0, qj - 2]
+    got = c.add(a, b)
+    for k in range(2):
+        for j, qj in enumerate(q):
+            want = [(int(x) + int(y)) % qj for x, y in zip(a[k, j], b[k, j])]
+            assert [int(v) for v in got[k, j]] == want
