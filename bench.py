@@ -45,15 +45,15 @@ HBM_PEAK = 8.0e12  # B/s, MI355X HBM3E
 # hash of the kernel sources they were measured on.  A build from other
 # sources reports traffic as null.
 MEASURED_TRAFFIC = {
-    "csrc_sha16": "692143b00ae15a1d",
+    "csrc_sha16": "20705cbb1efd5396",
     "kernels": {
         # 30-rotation batch launches of the rotation step
-        "ntt_fwd_blocks_moddown": 3_096_557_645 + 756_838_579,
-        "k_moddown_mid": 253_526_144 + 760_009_434,
-        "ntt_inv_blocks_ksk": 776_163_763 + 251_658_240,
+        "ntt_fwd_blocks_moddown": 3_096_408_371 + 754_974_720,
+        "k_moddown_mid": 253_406_899 + 758_562_854,
+        "ntt_inv_blocks_ksk": 776_174_285 + 251_658_240,
         # NTT batch (64 ciphertexts x 2 polys x 24 limbs): one pass, and the MAC
-        "ntt_pass": 1_636_282_086 + 1_610_612_736,
-        "k_mac": 2_416_047_821 + 25_165_824,
+        "ntt_pass": 1_636_266_726 + 1_610_612_736,
+        "k_mac": 2_416_048_102 + 25_165_824,
     },
 }
 
