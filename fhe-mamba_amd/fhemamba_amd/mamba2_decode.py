@@ -82,7 +82,7 @@ class EncryptedMamba2Decoder:
                                   refresh_ceiling=refresh_ceiling, log=self.log,
                                   s2c_first=s2c_first, level_budget=tuple(level_budget))
         # Refresh passes by site, the reference decoder's Meta-BTS rule
-        # (should_use_meta_bts, stage1_mamba2_config.cpp:64-81): two-pass
+        # (should_use_meta_bts, stage1_mamba2_config.cpp:69-86): two-pass
         # refreshes (bootstrap_passes) for the carried lineages (SSM state,
         # the projection kept in the conv FIFO), the gated norm's polynomial
         # input, the residual of the last three layers, the final output and
@@ -364,7 +364,7 @@ class EncryptedMamba2Decoder:
         if max(ev._level(act) + need_act, ev._level(dt) + need_dt) > ev.refresh_ceiling:
             f = 1 << max(0, math.ceil(math.log2(B["act"] / B["dt"])))
             comb = ev.add(act, cc.MultByInteger(dt, f) if f > 1 else dt)
-            comb = ev.refresh(comb, max(B["act"], B["dt"] * f), xs + ds)
+            comb = ev.refresh(comb, max(B["act"], B["dt"] * f), xs + ds, self.transient_passes)
             act = dt = comb
         if lay.joint is None:
             e = self.cheb(ev.plain(dt, self._vec({d0: A / f}), True), dec, ds, dec.squarings)
@@ -386,7 +386,8 @@ class EncryptedMamba2Decoder:
         dt_groups = self.expand_compact(dt_c, 0)
         decay = self.ready(decay, 5, B["decay"], ds)
         if st.ssm is not None and self.decay_policy(ev._level(decay), ev._level(st.ssm[0])):
-            decay = self.ev.refresh(decay, B["decay"], ds)
+            # a transient value (the carried checkpoint is the state)
+            decay = self.ev.refresh(decay, B["decay"], ds, self.transient_passes)
         decay_groups = self.expand_compact(self.spread_heads(decay, d0), 0)
         # state update and readout
         new_ssm, reads = [], []
