@@ -34,7 +34,9 @@ The final hidden goes through RMSNorm with final_norm_w.
 
 Refresh: before each phase every input ciphertext whose level plus the
 phase's level need would pass the ceiling is scaled into [-1, 1] by a
-public bound, bootstrapped (two passes) and scaled back, as the reference's
+public bound, bootstrapped (two passes for the carried and other
+precision-critical values, one for the rest; EncryptedMamba2Decoder's
+constructor lists them) and scaled back, as the reference's
 maybe_bootstrap checkpoints do (:2127-2297).  Bounds are public calibration
 maxima (payload `carried_bounds`, else the defaults below), never values
 read from ciphertexts.
