@@ -588,6 +588,36 @@ int fhe_relinearize(fhe_poly* out, const fhe_poly* ct3, const fhe_key* key) {
   });
 }
 
+int fhe_relinearize_many(fhe_poly* const* outs, const fhe_poly* const* ct3s, uint32_t count,
+                         const fhe_key* key) {
+  return guard([&] {
+    need(outs && ct3s, "null argument");
+    if (count == 0) return;
+    need(ct3s[0] != nullptr, "null tensor");
+    fhe::Context& c = *ct3s[0]->c;
+    const uint32_t nq = ct3s[0]->nlimb;
+    for (uint32_t r = 0; r < count; ++r) {
+      need(ct3s[r] && outs[r], "null handle");
+      same_ctx(outs[r], ct3s[r]);
+      need(ct3s[r]->c == &c && ct3s[r]->npoly == 3 && ct3s[r]->nlimb == nq && nq <= c.L,
+           "relinearize_many needs 3-poly tensors of one context and level");
+      check_key(ct3s[r], key);
+      for (uint32_t s = 0; s < r; ++s) need(outs[s] != outs[r], "outputs must be distinct");
+    }
+    for (uint32_t r = 0; r < count; ++r)
+      for (uint32_t s = 0; s < count; ++s)
+        need(outs[r] != ct3s[s], "an output must not be one of the tensors");
+    std::vector<uint64_t*> dst(count);
+    std::vector<const uint64_t*> src(count);
+    for (uint32_t r = 0; r < count; ++r) {
+      prepare_out(outs[r], 2, nq);
+      dst[r] = outs[r]->data;
+      src[r] = ct3s[r]->data;
+    }
+    fhe::relinearize_many(c, dst.data(), src.data(), nq, key->data, count);
+  });
+}
+
 int fhe_rotate(fhe_poly* out, const fhe_poly* ct, const fhe_key* key, uint32_t galois) {
   return guard([&] {
     same_ctx(out, ct);

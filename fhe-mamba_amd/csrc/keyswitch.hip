@@ -419,28 +419,48 @@ void rotate(Context& c, uint64_t* out, const uint64_t* ct, uint32_t nq, const ui
   keyswitch(c, ct + (size_t)nq * c.n, nq, key, KeySwitchOut{out, ct, nullptr, galois});
 }
 
-void rotate_many(Context& c, uint64_t* const* outs, const uint64_t* const* cts, uint32_t nq,
-                 const uint64_t* const* keys, const uint32_t* galois, uint32_t count) {
+// `count` independent key switches of polys srcs[r] ([nq][N]) with keys[r]
+// into ko[r]: batched ModUps and batched ModDowns, each batch's scratch
+// (digits + ext P limbs + y per key switch) kept under 2 GiB.
+static void keyswitch_many(Context& c, const uint64_t* const* srcs, uint32_t nq,
+                           const uint64_t* const* keys, const KeySwitchOut* ko, uint32_t count) {
   const size_t n = c.n, ne = nq + c.K;
   const uint32_t nd = num_digits(c, nq);
   const size_t ct_words = (size_t)nd * ne * n;
-  // Per rotation: digits + ext (P limbs) + y, kept under 2 GiB per batch.
-  const size_t per_rot = (ct_words + 2 * (size_t)(c.K + nq) * n) * 8;
-  uint32_t batch = (uint32_t)std::max<size_t>(1, (size_t(2) << 30) / per_rot);
+  const size_t per_ks = (ct_words + 2 * (size_t)(c.K + nq) * n) * 8;
+  uint32_t batch = (uint32_t)std::max<size_t>(1, (size_t(2) << 30) / per_ks);
   batch = std::min<uint32_t>(batch, MAX_KS_BATCH);
   for (uint32_t r0 = 0; r0 < count; r0 += batch) {
     const uint32_t b = std::min(batch, count - r0);
     Scratch dig(c, b * ct_words);
-    std::vector<const uint64_t*> c1(b), dg(b);
-    std::vector<KeySwitchOut> ko(b);
-    for (uint32_t r = 0; r < b; ++r) {
-      c1[r] = cts[r0 + r] + (size_t)nq * n;
-      dg[r] = dig.p + r * ct_words;
-      ko[r] = KeySwitchOut{outs[r0 + r], cts[r0 + r], nullptr, galois[r0 + r]};
-    }
-    modup_batch(c, c1.data(), b, nq, dig.p);
-    keyswitch_batch(c, dg.data(), nq, keys + r0, b, ko.data());
+    std::vector<const uint64_t*> dg(b);
+    for (uint32_t r = 0; r < b; ++r) dg[r] = dig.p + r * ct_words;
+    modup_batch(c, srcs + r0, b, nq, dig.p);
+    keyswitch_batch(c, dg.data(), nq, keys + r0, b, ko + r0);
   }
+}
+
+void rotate_many(Context& c, uint64_t* const* outs, const uint64_t* const* cts, uint32_t nq,
+                 const uint64_t* const* keys, const uint32_t* galois, uint32_t count) {
+  std::vector<const uint64_t*> c1(count);
+  std::vector<KeySwitchOut> ko(count);
+  for (uint32_t r = 0; r < count; ++r) {
+    c1[r] = cts[r] + (size_t)nq * c.n;
+    ko[r] = KeySwitchOut{outs[r], cts[r], nullptr, galois[r]};
+  }
+  keyswitch_many(c, c1.data(), nq, keys, ko.data(), count);
+}
+
+void relinearize_many(Context& c, uint64_t* const* outs, const uint64_t* const* ct3s,
+                      uint32_t nq, const uint64_t* key, uint32_t count) {
+  const size_t pl = (size_t)nq * c.n;
+  std::vector<const uint64_t*> d2(count), keys(count, key);
+  std::vector<KeySwitchOut> ko(count);
+  for (uint32_t r = 0; r < count; ++r) {
+    d2[r] = ct3s[r] + 2 * pl;
+    ko[r] = KeySwitchOut{outs[r], ct3s[r], ct3s[r] + pl, 1};
+  }
+  keyswitch_many(c, d2.data(), nq, keys.data(), ko.data(), count);
 }
 
 void linear_transform(Context& c, uint64_t* out, const uint64_t* ct, uint32_t nq,

@@ -108,6 +108,11 @@ void rotate(Context& c, uint64_t* out, const uint64_t* ct, uint32_t nq, const ui
 // batched ModUps and batched ModDowns.  outs[r] must not alias any cts[.].
 void rotate_many(Context& c, uint64_t* const* outs, const uint64_t* const* cts, uint32_t nq,
                  const uint64_t* const* keys, const uint32_t* galois, uint32_t count);
+// Relinearization of `count` tensors ct3s[r] [3][nq][N] by one key:
+// outs[r] = (d0, d1) + KS(d2), batched ModUps and batched ModDowns.
+// outs[r] must not alias any ct3s[.].
+void relinearize_many(Context& c, uint64_t* const* outs, const uint64_t* const* ct3s,
+                      uint32_t nq, const uint64_t* key, uint32_t count);
 // Baby-step giant-step plaintext linear transform of ct [2][nq][N]:
 //   out = sum_{g < G} rot_giant^g( sum_{b < bstep} pts[g*bstep + b] (.) baby_b ),
 // G = ceil(count / bstep), baby_b = ct rotated by baby_keys[b] (all babies

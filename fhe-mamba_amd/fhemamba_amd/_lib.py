@@ -74,6 +74,7 @@ SIGNATURES = {
     "fhe_key_destroy": [_p],
     "fhe_keyswitch": [_p, _p, _p],
     "fhe_relinearize": [_p, _p, _p],
+    "fhe_relinearize_many": [_p, _p, _u32, _p],
     "fhe_rotate": [_p, _p, _p, _u32],
     "fhe_rotate_noalloc": [_p, _p, _p, _u32],
     "fhe_rotation_precompute": [_p, _pp],

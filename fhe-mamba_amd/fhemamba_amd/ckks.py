@@ -654,6 +654,28 @@ class CryptoContext:
     def EvalMult(self, a, b) -> "Ciphertext":  # noqa: N802
         return self._mult(a, b)
 
+    def EvalMultMany(self, pairs) -> list:  # noqa: N802
+        """[EvalMult(a, b) for a, b in pairs] with the ciphertext products
+        of one level relinearized together (fhe_relinearize_many): the
+        same ciphertexts, fewer and larger key-switch launches.  A pair
+        whose operands are one object is a square, as in EvalMult."""
+        out: list = [None] * len(pairs)
+        groups: dict = {}
+        for idx, (a, b) in enumerate(pairs):
+            if not (isinstance(a, Ciphertext) and isinstance(b, Ciphertext)):
+                out[idx] = self._mult(a, b)
+                continue
+            same = a is b
+            a, b = self._align_mult(a, b)
+            t = self._ctx.tensor(a.poly, a.poly if same else b.poly)
+            groups.setdefault(t.nlimb, []).append((idx, t, a, b))
+        key = self._relin_key() if groups else None
+        for items in groups.values():
+            polys = self._ctx.relinearize_many([t for _, t, _, _ in items], key)
+            for (idx, _, a, b), poly in zip(items, polys):
+                out[idx] = self._wrap(poly, a.level, a.deg + b.deg, a.scale * b.scale, a.slots)
+        return out
+
     def EvalMultInPlace(self, a: "Ciphertext", b) -> None:  # noqa: N802
         a._assign(self._mult(a, b))
 

@@ -87,6 +87,27 @@ def cheb_ps_depth(degree: int, baby: int | None = None) -> int:
     return depth(degree)
 
 
+def _mult_many(cc, pairs):
+    """EvalMult of every pair, relinearized together when the context has
+    EvalMultMany (independent products of one circuit step), else one
+    EvalMult each; the same ciphertexts either way."""
+    many = getattr(cc, "EvalMultMany", None)
+    if many is not None and len(pairs) > 1:
+        return many(pairs)
+    return [cc.EvalMult(a, b) for a, b in pairs]
+
+
+def _t_depth(i: int, memo: dict) -> int:
+    if i <= 1:
+        return 0
+    if i not in memo:
+        if i % 2 == 0:
+            memo[i] = _t_depth(i // 2, memo) + 1
+        else:
+            memo[i] = max(_t_depth(i // 2, memo), _t_depth(i // 2 + 1, memo)) + 1
+    return memo[i]
+
+
 class ChebBasis:
     """T_i(u) built on demand from T_1 = u by T_2j = 2 T_j^2 - 1 and
     T_2j+1 = 2 T_j+1 T_j - u, each kept once (series of one input may share
@@ -98,17 +119,49 @@ class ChebBasis:
         self.settle = getattr(cc, "Rescale", None) or (lambda ct: ct)
         self.cache = {1: u}
 
+    @staticmethod
+    def _operands(i: int) -> tuple:
+        return (i // 2, i // 2) if i % 2 == 0 else (i // 2 + 1, i // 2)
+
+    def _finish(self, i: int, product):
+        cc = self.cc
+        self.cache[i] = self.settle(cc.EvalSub(cc.EvalAdd(product, product),
+                                               1.0 if i % 2 == 0 else self.u))
+
     def __call__(self, i: int):
         if i not in self.cache:
-            cc = self.cc
-            if i % 2 == 0:
-                h = self(i // 2)
-                sq = cc.EvalMult(h, h)
-                self.cache[i] = self.settle(cc.EvalSub(cc.EvalAdd(sq, sq), 1.0))
-            else:
-                pr = cc.EvalMult(self(i // 2 + 1), self(i // 2))
-                self.cache[i] = self.settle(cc.EvalSub(cc.EvalAdd(pr, pr), self.u))
+            a, b = self._operands(i)
+            ta = self(a)
+            self._finish(i, self.cc.EvalMult(ta, ta if a == b else self(b)))
         return self.cache[i]
+
+    @staticmethod
+    def build_many(requests) -> None:
+        """For (basis, indices) pairs: every T_i the indices need, by
+        increasing depth, the products of one depth over all the bases
+        multiplied together (_mult_many); each T_i is the value __call__
+        computes."""
+        memo: dict = {}
+        todo = []
+        for basis, indices in requests:
+            need, stack = set(), list(indices)
+            while stack:
+                i = stack.pop()
+                if i <= 1 or i in need or i in basis.cache:
+                    continue
+                need.add(i)
+                stack.extend(basis._operands(i))
+            todo.extend((basis, i) for i in need)
+        if not todo:
+            return
+        for d in range(1, max(_t_depth(i, memo) for _, i in todo) + 1):
+            step = [(b, i) for b, i in todo if _t_depth(i, memo) == d]
+            pairs = []
+            for b, i in step:
+                x, y = b._operands(i)
+                pairs.append((b.cache[x], b.cache[x] if x == y else b.cache[y]))
+            for (b, i), prod in zip(step, _mult_many(step[0][0].cc, pairs)):
+                b._finish(i, prod)
 
 
 def _ps_split(c, n: int, k: int):
@@ -121,47 +174,99 @@ def _ps_split(c, n: int, k: int):
     return rem, quot
 
 
+class _PsNode:
+    """A node of the Paterson-Stockmeyer recursion: a leaf series (degree
+    below the baby size) or the split p = rem + T_k quot."""
+
+    def __init__(self, c: list, m: int):
+        n = len(c) - 1
+        self.value = None
+        if n < m:
+            self.c, self.k, self.rem, self.quot, self.height = c, 0, None, None, 0
+        else:
+            self.k = _giant_split(n, m)
+            rem, quot = _ps_split(c, n, self.k)
+            self.c, self.rem, self.quot = None, _PsNode(rem, m), _PsNode(quot, m)
+            self.height = 1 + max(self.rem.height, self.quot.height)
+
+    def nodes(self):
+        yield self
+        if self.c is None:
+            yield from self.rem.nodes()
+            yield from self.quot.nodes()
+
+
+def chebyshev_ps_many(cc, jobs):
+    """sum_i coeffs[i] T_i(u) by Paterson-Stockmeyer
+    (src/fhemamba/ckks_probes.py:108-155) for every job (u, coeffs, floor,
+    const_ct) of independent inputs, in lockstep: the basis powers of one
+    depth, then the giant-step products of one tree height, of every job
+    are multiplied together (_mult_many).  Each job's result is the one
+    chebyshev_ps gives.  `const_ct(value)` supplies a constant ciphertext
+    when no term of a series survives its coefficient floor."""
+    results = [None] * len(jobs)
+    trees = []
+    for j, (u, coeffs, floor, const_ct) in enumerate(jobs):
+        def constant(value: float, const_ct=const_ct):
+            if const_ct is None:
+                raise ValueError("Chebyshev series has no term above the coefficient floor")
+            return const_ct(value)
+
+        degree = len(coeffs) - 1
+        if degree < 1:
+            results[j] = constant(coeffs[0] if len(coeffs) else 0.0)
+            continue
+        root = _PsNode(list(coeffs), cheb_baby_size(degree))
+        trees.append((j, ChebBasis(cc, u), root, floor, constant))
+    requests = []
+    for _, basis, root, floor, _ in trees:
+        need = set()
+        for node in root.nodes():
+            if node.c is None:
+                need.add(node.k)
+            else:
+                need.update(i for i in range(1, len(node.c)) if abs(node.c[i]) >= floor)
+        requests.append((basis, need))
+    ChebBasis.build_many(requests)
+    # with EvalLinearWSum a leaf's sum of c_i T_i is one weighted sum at the
+    # deepest T_i level instead of products aligned pairwise (same value)
+    wsum = getattr(cc, "EvalLinearWSum", None)
+    splits = []
+    for _, basis, root, floor, constant in trees:
+        for node in root.nodes():
+            if node.c is None:
+                splits.append((basis, node))
+                continue
+            c = node.c
+            idx = [i for i in range(1, len(c)) if abs(c[i]) >= floor]
+            acc = None
+            if idx and wsum is not None:
+                acc = wsum([basis(i) for i in idx], [c[i] for i in idx])
+            else:
+                for i in idx:
+                    term = cc.EvalMult(basis(i), c[i])
+                    acc = term if acc is None else cc.EvalAdd(acc, term)
+            if acc is None:
+                acc = constant(c[0])
+            elif abs(c[0]) >= floor:
+                acc = cc.EvalAdd(acc, c[0])
+            node.value = acc
+    for h in sorted({node.height for _, node in splits}):
+        step = [(basis, node) for basis, node in splits if node.height == h]
+        giants = _mult_many(cc, [(basis(node.k), node.quot.value) for basis, node in step])
+        for (_, node), giant in zip(step, giants):
+            node.value = cc.EvalAdd(node.rem.value, giant)
+    for j, _, root, _, _ in trees:
+        results[j] = root.value
+    return results
+
+
 def chebyshev_ps(cc, u, coeffs: Sequence[float], floor: float = CHEB_COEFF_FLOOR,
                  const_ct=None):
     """sum_i coeffs[i] T_i(u) by Paterson-Stockmeyer
     (src/fhemamba/ckks_probes.py:108-155).  `const_ct(value)` supplies a
     constant ciphertext when no term survives the coefficient floor."""
-    def constant(value: float):
-        if const_ct is None:
-            raise ValueError("Chebyshev series has no term above the coefficient floor")
-        return const_ct(value)
-
-    degree = len(coeffs) - 1
-    if degree < 1:
-        return constant(coeffs[0] if len(coeffs) else 0.0)
-    m = cheb_baby_size(degree)
-    # with EvalLinearWSum a leaf's sum of c_i T_i is one weighted sum at the
-    # deepest T_i level instead of products aligned pairwise (same value)
-    wsum = getattr(cc, "EvalLinearWSum", None)
-    cheb = ChebBasis(cc, u)
-
-    def evaluate(c: list[float]):
-        n = len(c) - 1
-        if n < m:
-            idx = [i for i in range(1, n + 1) if abs(c[i]) >= floor]
-            acc = None
-            if idx and wsum is not None:
-                acc = wsum([cheb(i) for i in idx], [c[i] for i in idx])
-            else:
-                for i in idx:
-                    term = cc.EvalMult(cheb(i), c[i])
-                    acc = term if acc is None else cc.EvalAdd(acc, term)
-            if acc is None:
-                return constant(c[0])
-            if abs(c[0]) >= floor:
-                acc = cc.EvalAdd(acc, c[0])
-            return acc
-        k = _giant_split(n, m)
-        rem, quot = _ps_split(c, n, k)
-        giant = cc.EvalMult(cheb(k), evaluate(quot))
-        return cc.EvalAdd(evaluate(rem), giant)
-
-    return evaluate(list(coeffs))
+    return chebyshev_ps_many(cc, [(u, coeffs, floor, const_ct)])[0]
 
 
 def chebyshev_ps_rows(basis: ChebBasis, rows, baby: int, mul, add, const):

@@ -234,6 +234,16 @@ class Context:
         call("fhe_relinearize", out.handle, ct3.handle, key.handle)
         return out
 
+    def relinearize_many(self, ct3s, key, outs=None):
+        """Relinearize every 3-poly tensor of `ct3s` (one level) in one
+        batched key switch; the same polys as relinearize() of each."""
+        count = len(ct3s)
+        outs = outs if outs is not None else [Poly(self, 2, t.nlimb) for t in ct3s]
+        th = (ctypes.c_void_p * max(count, 1))(*([t.handle.value for t in ct3s] or [None]))
+        oh = (ctypes.c_void_p * max(count, 1))(*([o.handle.value for o in outs] or [None]))
+        call("fhe_relinearize_many", oh, th, count, key.handle)
+        return outs
+
     def rotate(self, ct, key, galois: int, out=None):
         out = self._out(out, 2, ct.nlimb)
         call("fhe_rotate", out.handle, ct.handle, key.handle, galois)

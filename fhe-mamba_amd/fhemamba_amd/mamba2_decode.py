@@ -49,7 +49,7 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
-from .ckks_probes import (ChebBasis, affine, cheb_baby_size, cheb_ps_depth, chebyshev_ps,
+from .ckks_probes import (ChebBasis, affine, cheb_baby_size, cheb_ps_depth, chebyshev_ps_many,
                           chebyshev_ps_rows)
 from .mamba2_payload import ChainPayload, JointGateSpec, LayerPayload, PolySpec
 from .packed import PackedEvaluator, replicated_shape
@@ -158,11 +158,20 @@ class EncryptedMamba2Decoder:
     def cheb(self, x, spec: PolySpec, support: np.ndarray, squarings_scale: int = 0):
         """Chebyshev series of `spec` on the supported slots (domain scaled
         by 2^squarings_scale for the range-reduced exp)."""
-        lo, hi = spec.lo * 2 ** squarings_scale, spec.hi * 2 ** squarings_scale
-        u = self.ev.plain(x, support * (2.0 / (hi - lo)), True)
-        u = self.ev.plain(u, support * (-(lo + hi) / (hi - lo)), False)
-        return chebyshev_ps(self.cc, u, [float(c) for c in spec.coeffs], 1e-14,
-                            lambda v: self.ev.scale(u, 0.0))
+        return self.cheb_many([(x, spec, support, squarings_scale)])[0]
+
+    def cheb_many(self, series):
+        """cheb(x, spec, support, squarings_scale) of every entry of
+        `series` (independent inputs), the series' products of one step
+        relinearized together."""
+        jobs = []
+        for x, spec, support, squarings_scale in series:
+            lo, hi = spec.lo * 2 ** squarings_scale, spec.hi * 2 ** squarings_scale
+            u = self.ev.plain(x, support * (2.0 / (hi - lo)), True)
+            u = self.ev.plain(u, support * (-(lo + hi) / (hi - lo)), False)
+            jobs.append((u, [float(c) for c in spec.coeffs], 1e-14,
+                         lambda v, u=u: self.ev.scale(u, 0.0)))
+        return chebyshev_ps_many(self.cc, jobs)
 
     def cheb_need(self, spec: PolySpec) -> int:
         return 1 + cheb_ps_depth(len(spec.coeffs) - 1) + 1
@@ -339,18 +348,22 @@ class EncryptedMamba2Decoder:
             conv = term if conv is None else ev.add(conv, term)
         conv = ev.plain(conv, self._vec({di: t("conv_b")}), False)
         conv = self.ready(conv, self.cheb_need(lay.polys["conv_silu"]), B["conv"], xs)
-        act = ev.plain(self.cheb(conv, lay.polys["conv_silu"], xs), xs, True,
-                       key=("xbc", di, cd))
-        # gates: SiLU(z), dt, decay
+        # SiLU of the conv output, and the gates SiLU(z) and sqrt-softplus of
+        # dt + dt_bias: independent series, evaluated in lockstep
         zs = self._support(0, di)
-        gate = ev.plain(self.cheb(proj, lay.polys["gate_silu"], zs), zs, True, key=("z", di))
         d0 = di + cd
         ds = self._support(d0, self.nh)
         sp = lay.polys["dt_softplus"]
         dtin = ev.plain(proj, self._vec({d0: t("dt_bias")}), False)
         dec = lay.polys["decay_exp"]
+        series = [(conv, lay.polys["conv_silu"], xs, 0), (proj, lay.polys["gate_silu"], zs, 0)]
         if lay.joint is None:
-            q = self.cheb(dtin, sp, ds)
+            series.append((dtin, sp, ds, 0))
+        values = self.cheb_many(series)
+        act = ev.plain(values[0], xs, True, key=("xbc", di, cd))
+        gate = ev.plain(values[1], zs, True, key=("z", di))
+        if lay.joint is None:
+            q = values[2]
             dt = ev.plain(ev.mul(q, q), ds, True, key=("dt", d0))
             need_dt = self.cheb_need(dec) + dec.squarings + 6
         else:

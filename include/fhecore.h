@@ -178,6 +178,14 @@ int fhe_keyswitch(fhe_poly *out, const fhe_poly *a, const fhe_key *key);
 /* Relinearize a 3-poly tensor (EvalMult(ct, ct) relinearisation,
  * packed_fideslib.cpp:147-149). */
 int fhe_relinearize(fhe_poly *out, const fhe_poly *ct3, const fhe_key *key);
+/* fhe_relinearize of `count` 3-poly tensors of one level at once (ct3s[r]
+ * into outs[r]): the independent EvalMult relinearisations of one step of
+ * the reference's Chebyshev evaluation (the basis powers of one depth and
+ * the giant-step products of one tree height, src/fhemamba/ckks_probes.py:
+ * 108-155) as one batched ModUp and one batched ModDown.  Outputs must be
+ * distinct and none may be one of the tensors. */
+int fhe_relinearize_many(fhe_poly *const *outs, const fhe_poly *const *ct3s, uint32_t count,
+                         const fhe_key *key);
 /* EvalRotate / EvalConjugate: key switch c1, add c0, apply X -> X^galois
  * (packed_fideslib.cpp:207-221, stage1_mamba2_decode_fideslib.cpp:1779-1801,
  *  :2342). */

@@ -11,7 +11,7 @@ import pytest
 from fhemamba_amd import ckks
 from fhemamba_amd.ckks_probes import (CkksPrimitives, affine, build_toy_context, ceil_log2,
                                       cheb_baby_size, cheb_eval64, cheb_ps_depth,
-                                      floor_coeffs)
+                                      chebyshev_ps, chebyshev_ps_many, floor_coeffs)
 
 
 class ArrayBackend:
@@ -72,6 +72,50 @@ def test_chebyshev_matches_numpy(degree):
     np.testing.assert_allclose(he.eval_chebyshev(x, c), cheb_eval64(c, x), rtol=1e-10,
                                atol=1e-10)
     np.testing.assert_array_equal(he.eval_chebyshev(x, [0.0] * 8), np.zeros(37))
+
+
+class LockstepBackend(ArrayBackend):
+    """ArrayBackend with EvalMultMany; counts the ciphertext products and
+    the steps they are issued in (one per EvalMultMany call or lone
+    ciphertext product)."""
+
+    def __init__(self):
+        self.products = self.steps = 0
+
+    def EvalMult(self, left, right):  # noqa: N802
+        if isinstance(right, np.ndarray):
+            self.products += 1
+            self.steps += 1
+        return left * right
+
+    def EvalMultMany(self, pairs):  # noqa: N802
+        self.products += len(pairs)
+        self.steps += 1
+        return [a * b for a, b in pairs]
+
+
+@pytest.mark.parametrize("degrees", [(59,), (96, 64, 64), (3, 31, 119), (0, 8, 15), (59, 59)])
+def test_lockstep_series_equal_one_at_a_time(degrees):
+    """chebyshev_ps_many gives each series exactly what chebyshev_ps gives
+    it alone; in lockstep the products of every series go out in as many
+    steps as the deepest series alone needs."""
+    rng = np.random.default_rng(sum(degrees))
+    xs = [rng.uniform(-0.95, 0.95, 29) for _ in degrees]
+    cs = [floor_coeffs(rng.normal(size=d + 1)) for d in degrees]
+    const = lambda v: np.full(29, v)  # noqa: E731
+    alone = [chebyshev_ps(ArrayBackend(), x, c, 1e-12, const) for x, c in zip(xs, cs)]
+    many = LockstepBackend()
+    got = chebyshev_ps_many(many, [(x, c, 1e-12, const) for x, c in zip(xs, cs)])
+    for a, g, x, c in zip(alone, got, xs, cs):
+        np.testing.assert_array_equal(g, a)
+        np.testing.assert_allclose(g, cheb_eval64(c, x), rtol=1e-9, atol=1e-9)
+    singles = []
+    for x, c in zip(xs, cs):
+        b = LockstepBackend()
+        chebyshev_ps_many(b, [(x, c, 1e-12, const)])
+        singles.append(b)
+    assert many.products == sum(b.products for b in singles)
+    assert many.steps == max(b.steps for b in singles)
 
 
 @pytest.mark.parametrize("degree", [d for d in DEGREES if d >= 1])

@@ -246,3 +246,23 @@ def test_batched_plaintexts_equal_single(env):
             assert np.array_equal(p.poly.numpy(), one.poly.numpy())
             assert (p.level, p.deg, p.scale, p.slots) == (one.level, one.deg, one.scale, one.slots)
     assert cc.MakeCKKSPackedPlaintexts([], 1, 0) == []
+
+
+def test_mult_many_equals_mult(env):
+    """EvalMultMany gives the ciphertexts EvalMult gives, residue for
+    residue: products at two levels (two batched relinearizations), a
+    square (one operand twice), operands of different levels and degrees
+    (aligned as EvalMult aligns them) and a plaintext product."""
+    cc, keys = env
+    a, b = enc(cc, keys, vec(1)), enc(cc, keys, vec(2))
+    c = enc(cc, keys, vec(3), level=2)
+    d = cc.EvalMult(enc(cc, keys, vec(4)), enc(cc, keys, vec(5)))   # degree 2
+    pt = cc.MakeCKKSPackedPlaintext(list(vec(6)))
+    pairs = [(a, b), (a, a), (c, c), (b, c), (d, a), (c, enc(cc, keys, vec(7), level=2)),
+             (a, pt), (b, 0.5)]
+    got = cc.EvalMultMany(pairs)
+    for (x, y), g in zip(pairs, got):
+        want = cc.EvalMult(x, y)
+        assert (g.GetLevel(), g.GetNoiseScaleDeg()) == (want.GetLevel(), want.GetNoiseScaleDeg())
+        assert g.GetScalingFactor() == want.GetScalingFactor()
+        assert np.array_equal(g.poly.numpy(), want.poly.numpy())

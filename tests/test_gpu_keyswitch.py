@@ -9,6 +9,7 @@ from gpu_helpers import residues
 pytestmark = pytest.mark.gpu
 
 F = pytest.importorskip("fhemamba_amd")
+from fhemamba_amd._lib import FheError  # noqa: E402
 
 # (log_n, depth, scale bits, first bits, dnum): config-1-like toy chain and
 # a chain with a partial last digit.
@@ -142,6 +143,30 @@ def test_relinearize_matches_oracle(setup):
     t = orc.tensor(a, b)
     got = ctx.relinearize(ctx.upload(t), ctx.load_key(key)).numpy()
     assert np.array_equal(got, orc.relinearize(t, key))
+
+
+def test_relinearize_many_matches_oracle(setup):
+    """Several tensors of one level in one batched relinearization
+    (fhe_relinearize_many) equal the oracle's relinearization of each, at
+    the top level and one limb lower; an output that is one of the tensors
+    is refused, and so are tensors of two levels in one call."""
+    ctx, orc, s = setup
+    key = orc.relin_key(s, 5)
+    dkey = ctx.load_key(key)
+    rng = np.random.default_rng(19)
+    for nl in (ctx.L, ctx.L - 1):
+        q = ctx.q[:nl]
+        ts = [orc.tensor(residues(rng, q, (2,), ctx.n), residues(rng, q, (2,), ctx.n))
+              for _ in range(5)]
+        got = ctx.relinearize_many([ctx.upload(t) for t in ts], dkey)
+        for r, t in enumerate(ts):
+            assert np.array_equal(got[r].numpy(), orc.relinearize(t, key)), (nl, r)
+    a = ctx.upload(ts[0])
+    with pytest.raises(FheError):
+        ctx.relinearize_many([a, ctx.upload(ts[1])], dkey, outs=[a, ctx.poly(2, ctx.L - 1)])
+    with pytest.raises(FheError):
+        big = orc.tensor(residues(rng, ctx.q, (2,), ctx.n), residues(rng, ctx.q, (2,), ctx.n))
+        ctx.relinearize_many([a, ctx.upload(big)], dkey)
 
 
 def test_rotate_and_relinearize_in_place(setup):
