@@ -511,6 +511,35 @@ int fhe_rescale(fhe_poly* out, const fhe_poly* a) {
   });
 }
 
+int fhe_rescale_many(fhe_poly* const* outs, const fhe_poly* const* as, uint32_t count) {
+  return guard([&] {
+    need(outs && as, "null argument");
+    if (count == 0) return;
+    need(as[0] != nullptr, "null input");
+    fhe::Context& c = *as[0]->c;
+    const uint32_t npoly = as[0]->npoly, nq = as[0]->nlimb;
+    need(nq >= 2 && nq <= c.L, "rescale needs 2..L limbs");
+    for (uint32_t r = 0; r < count; ++r) {
+      need(as[r] && outs[r], "null handle");
+      same_ctx(outs[r], as[r]);
+      need(as[r]->c == &c && as[r]->npoly == npoly && as[r]->nlimb == nq,
+           "rescale_many needs inputs of one context and shape");
+      for (uint32_t s = 0; s < r; ++s) need(outs[s] != outs[r], "outputs must be distinct");
+    }
+    for (uint32_t r = 0; r < count; ++r)
+      for (uint32_t s = 0; s < count; ++s)
+        need(outs[r] != as[s], "an output must not be one of the inputs");
+    std::vector<uint64_t*> dst(count);
+    std::vector<const uint64_t*> src(count);
+    for (uint32_t r = 0; r < count; ++r) {
+      prepare_out(outs[r], npoly, nq - 1);
+      dst[r] = outs[r]->data;
+      src[r] = as[r]->data;
+    }
+    fhe::poly_rescale_many(c, dst.data(), src.data(), count, npoly, nq);
+  });
+}
+
 int fhe_tensor(fhe_poly* out3, const fhe_poly* a, const fhe_poly* b) {
   return guard([&] {
     same_ctx(a, b);

@@ -366,6 +366,11 @@ void moddown_fused(Context& c, uint64_t* ext_p, uint64_t* y, uint32_t npoly, uin
 // Rescale of [npoly][nq][N] into out [npoly][nq-1][N] (out != a) in four
 // launches, for ring dimensions 2^13..2^17.
 void rescale_fused(Context& c, uint64_t* out, const uint64_t* a, uint32_t npoly, uint32_t nq);
+// The same for `count` inputs as[r] into outs[r] (each [npoly][nq][N] into
+// [npoly][nq-1][N], no output aliasing any input): up to 16 inputs share
+// one set of launches.
+void rescale_fused_many(Context& c, uint64_t* const* outs, const uint64_t* const* as,
+                        uint32_t count, uint32_t npoly, uint32_t nq);
 // ModUp of `count` c1 polys (nq limbs each) into digits [count][nd][nq+K][N]
 // in four launches for ring dimensions 2^13..2^17 with every modulus below
 // 2^60: the first inverse pass reading c1 (blocked out), one kernel for the

@@ -1010,14 +1010,24 @@ __global__ void __launch_bounds__(512)
 // The inverse NTT of the last limb reads it from the input (LastLimbLoad);
 // the forward column pass lifts it to modulus i as it loads (LiftLoad:
 // x mod q_i, minus q_l mod q_i in the upper half, the centred lift); the
-// last forward pass stores (a_i - t_i) * q_l^-1 (RescaleStore).
+// last forward pass stores (a_i - t_i) * q_l^-1 (RescaleStore).  One launch
+// set rescales up to RESCALE_MAX inputs of npoly polys each: launch poly y
+// is poly y % npoly of input y / npoly, whose addresses come from a table
+// in the kernel arguments.
+constexpr int RESCALE_MAX = 16;
+struct RescalePtrs {
+  const uint64_t* a[RESCALE_MAX];
+  uint64_t* out[RESCALE_MAX];
+};
 struct LastLimbLoad {
   static constexpr bool kLoad = true;
   static constexpr bool kPair = false;
-  const uint64_t* a;
+  const uint64_t* const* a;  // RESCALE_MAX entries in kernel arguments
+  uint32_t npoly;
   size_t poly_words, last_off;
   __device__ __forceinline__ uint64_t get(size_t g, uint64_t) const {
-    return a[(size_t)blockIdx.y * poly_words + last_off + g];
+    const uint32_t y = blockIdx.y;
+    return a[y / npoly][(size_t)(y % npoly) * poly_words + last_off + g];
   }
   struct Ops2 {};
   __device__ __forceinline__ void fetch2(size_t, Ops2&) const {}
@@ -1044,21 +1054,22 @@ struct LiftLoad {
 struct RescaleStore {
   static constexpr bool kPre = true;
   static constexpr bool kPair = false;
-  const uint64_t* a;
-  uint64_t* out;
+  const uint64_t* const* a;  // RESCALE_MAX entries in kernel arguments
+  uint64_t* const* out;
   const uint64_t* rs;
-  uint32_t n, l, L;
+  uint32_t n, l, L, npoly;
   __device__ __forceinline__ uint64_t pre(size_t s, uint64_t) const {
-    return a[((size_t)blockIdx.y * (l + 1) + blockIdx.z) * n + s];
+    const uint32_t y = blockIdx.y;
+    return a[y / npoly][((size_t)(y % npoly) * (l + 1) + blockIdx.z) * n + s];
   }
   struct Ops2 {};
   __device__ __forceinline__ void fetch2(size_t, Ops2&) const {}
   __device__ __forceinline__ void comb2(const Ops2&, uint64_t, uint64_t&, uint64_t&) const {}
   __device__ __forceinline__ void fin(uint64_t*, size_t s, uint64_t y, uint64_t x,
                                       uint64_t q) const {
-    const uint32_t i = blockIdx.z;
+    const uint32_t i = blockIdx.z, p = blockIdx.y;
     const uint64_t* c = rs + ((size_t)l * L + i) * 4;
-    out[((size_t)blockIdx.y * l + i) * n + s] = shoup(x + q - y, c[1], c[2], q);
+    out[p / npoly][((size_t)(p % npoly) * l + i) * n + s] = shoup(x + q - y, c[1], c[2], q);
   }
 };
 
@@ -1066,10 +1077,10 @@ template <int S>
 __global__ void __launch_bounds__(256)
     ntt_pass_rescale_in(uint64_t* __restrict__ last, const ModConst* __restrict__ mc,
                         const uint64_t* __restrict__ tw_all, uint32_t log_n, uint32_t s_other,
-                        const LastLimbLoad ld, uint32_t l) {
+                        const RescalePtrs ptrs, uint32_t npoly, size_t poly_words, uint32_t l) {
   ntt_body<S, BLOCKS, true, RHO_PLAIN, PlainStore, LastLimbLoad>(
       last, (size_t)1 << log_n, mc, tw_all, log_n, LimbMap::contiguous(l), s_other, 0,
-      PlainStore{}, ld);
+      PlainStore{}, LastLimbLoad{ptrs.a, npoly, poly_words, (size_t)l << log_n});
 }
 
 template <int S>
@@ -1085,9 +1096,12 @@ template <int S>
 __global__ void __launch_bounds__(256)
     ntt_pass_rescale_out(uint64_t* __restrict__ t, size_t poly_stride,
                          const ModConst* __restrict__ mc, const uint64_t* __restrict__ tw_all,
-                         uint32_t log_n, uint32_t s_other, const RescaleStore st) {
+                         uint32_t log_n, uint32_t s_other, const RescalePtrs ptrs,
+                         const uint64_t* __restrict__ rs, uint32_t l, uint32_t L,
+                         uint32_t npoly) {
   ntt_body<S, BLOCKS, false, RHO_PLAIN, RescaleStore>(
-      t, poly_stride, mc, tw_all, log_n, LimbMap::contiguous(0), s_other, 1, st);
+      t, poly_stride, mc, tw_all, log_n, LimbMap::contiguous(0), s_other, 1,
+      RescaleStore{ptrs.a, ptrs.out, rs, 1u << log_n, l, L, npoly});
 }
 
 // ModUp input: limb blockIdx.z of ciphertext blockIdx.y's c1, read from the
@@ -1610,28 +1624,52 @@ void moddown_fused(Context& c, uint64_t* ext_p, uint64_t* y, uint32_t npoly, uin
   (void)s2;
 }
 
+static void rescale_launch(Context& c, uint64_t* const* outs, const uint64_t* const* as,
+                           uint32_t count, uint32_t npoly, uint32_t nq);
+
 void rescale_fused(Context& c, uint64_t* out, const uint64_t* a, uint32_t npoly, uint32_t nq) {
+  rescale_fused_many(c, &out, &a, 1, npoly, nq);
+}
+
+void rescale_fused_many(Context& c, uint64_t* const* outs, const uint64_t* const* as,
+                        uint32_t count, uint32_t npoly, uint32_t nq) {
   if (c.log_n < 13 || c.log_n > 17) throw ArgError("fused rescale needs N = 2^13 .. 2^17");
   if (nq < 2 || npoly == 0 || npoly > 65535) throw ArgError("rescale: bad shape");
-  const uint32_t l = nq - 1, n = c.n;
+  for (uint32_t r0 = 0; r0 < count;) {
+    // inputs of one launch set: at most RESCALE_MAX, and npoly per input
+    const uint32_t b = std::min<uint32_t>({count - r0, (uint32_t)RESCALE_MAX, 65535u / npoly});
+    rescale_launch(c, outs + r0, as + r0, b, npoly, nq);
+    r0 += b;
+  }
+}
+
+// One launch set over `count` <= RESCALE_MAX inputs of npoly polys each.
+static void rescale_launch(Context& c, uint64_t* const* outs, const uint64_t* const* as,
+                           uint32_t count, uint32_t npoly, uint32_t nq) {
+  const uint32_t l = nq - 1, n = c.n, np = count * npoly;
   const uint32_t s1 = (c.log_n + 1) / 2, s2 = c.log_n / 2;
-  Scratch last(c, (size_t)npoly * n), t(c, (size_t)npoly * l * n);
-  const LastLimbLoad in{a, (size_t)nq * n, (size_t)l * n};
+  RescalePtrs ptrs{};
+  for (uint32_t r = 0; r < count; ++r) {
+    ptrs.a[r] = as[r];
+    ptrs.out[r] = outs[r];
+  }
+  Scratch last(c, (size_t)np * n), t(c, (size_t)np * l * n);
   const LiftLoad lift{last.p, c.d_const, c.d_rescale, n, l, c.L, c.mods[l] >> 1};
-  const RescaleStore st{a, out, c.d_rescale, n, l, c.L};
   switch (c.log_n) {
 #define CASE(LN, A, B)                                                                        \
   case LN: {                                                                                  \
     using GB = Geo<B, RHO_PLAIN>;                                                             \
     using GA = Geo<A, RHO_PLAIN>;                                                             \
     const uint32_t tb = (1u << s1) / (256 / GB::TPL), ta = (1u << s2) / (256 / GA::TPL);      \
-    FHE_LAUNCH(c, "ntt_inv_blocks_rescale", (ntt_pass_rescale_in<B>), dim3(tb, npoly, 1),     \
-               dim3(256), 0, last.p, c.d_const, c.d_tw_inv, c.log_n, s1, in, l);              \
-    launch_cols<true>(c, s1, s2, last.p, npoly, n, 1, LimbMap::contiguous(l), true);          \
-    FHE_LAUNCH(c, "ntt_fwd_cols_rescale", (ntt_pass_rescale_lift<A>), dim3(ta, npoly, l),     \
+    FHE_LAUNCH(c, "ntt_inv_blocks_rescale", (ntt_pass_rescale_in<B>), dim3(tb, np, 1),        \
+               dim3(256), 0, last.p, c.d_const, c.d_tw_inv, c.log_n, s1, ptrs, npoly,         \
+               (size_t)nq * n, l);                                                            \
+    launch_cols<true>(c, s1, s2, last.p, np, n, 1, LimbMap::contiguous(l), true);             \
+    FHE_LAUNCH(c, "ntt_fwd_cols_rescale", (ntt_pass_rescale_lift<A>), dim3(ta, np, l),        \
                dim3(256), 0, t.p, (size_t)l * n, c.d_const, c.d_tw_fwd, c.log_n, s2, lift);   \
-    FHE_LAUNCH(c, "ntt_fwd_blocks_rescale", (ntt_pass_rescale_out<B>), dim3(tb, npoly, l),    \
-               dim3(256), 0, t.p, (size_t)l * n, c.d_const, c.d_tw_fwd, c.log_n, s1, st);     \
+    FHE_LAUNCH(c, "ntt_fwd_blocks_rescale", (ntt_pass_rescale_out<B>), dim3(tb, np, l),       \
+               dim3(256), 0, t.p, (size_t)l * n, c.d_const, c.d_tw_fwd, c.log_n, s1, ptrs,    \
+               c.d_rescale, l, c.L, npoly);                                                   \
     return;                                                                                   \
   }
     CASE(13, 7, 6) CASE(14, 7, 7) CASE(15, 8, 7) CASE(16, 8, 8) CASE(17, 9, 8)

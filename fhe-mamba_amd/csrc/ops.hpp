@@ -65,6 +65,10 @@ void poly_mod_raise(Context& c, uint64_t* out, uint32_t nq_out, const uint64_t* 
 // Drop the last limb with centred division (FLEXIBLEAUTO rescale);
 // out is [npoly][nq-1][N].
 void poly_rescale(Context& c, uint64_t* out, const uint64_t* a, uint32_t npoly, uint32_t nq);
+// poly_rescale of `count` inputs of one shape (outs[r] must not alias any
+// as[.]); at N = 2^13..2^17 up to 16 of them share one set of launches.
+void poly_rescale_many(Context& c, uint64_t* const* outs, const uint64_t* const* as,
+                       uint32_t count, uint32_t npoly, uint32_t nq);
 
 // ---- hybrid key switching (keyswitch.hip) ----
 uint32_t num_digits(const Context& c, uint32_t nq);

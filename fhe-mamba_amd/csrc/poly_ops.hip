@@ -558,6 +558,16 @@ void poly_rescale(Context& c, uint64_t* out, const uint64_t* a, uint32_t npoly, 
   FHE_LAUNCH(c, "k_rescale_combine", k_rescale_combine, grid_for(c, l, npoly), dim3(tpb_for(c)), 0, out, a, t.p, c.d_const, c.d_rescale, c.n, l, c.L);
 }
 
+void poly_rescale_many(Context& c, uint64_t* const* outs, const uint64_t* const* as,
+                       uint32_t count, uint32_t npoly, uint32_t nq) {
+  if (nq < 2) throw ArgError("rescale needs at least two limbs");
+  if (c.log_n >= 13 && c.log_n <= 17) {
+    rescale_fused_many(c, outs, as, count, npoly, nq);
+    return;
+  }
+  for (uint32_t r = 0; r < count; ++r) poly_rescale(c, outs[r], as[r], npoly, nq);
+}
+
 
 void poly_mac_giants(Context& c, uint64_t* const* acc, uint32_t ng, const uint64_t* const* x,
                      uint32_t nb, const uint64_t* const* w, uint32_t nq) {

@@ -68,6 +68,7 @@ SIGNATURES = {
     "fhe_add_const": [_p, _p, _p],
     "fhe_mul_int": [_p, _p, _i64],
     "fhe_rescale": [_p, _p],
+    "fhe_rescale_many": [_p, _p, _u32],
     "fhe_tensor": [_p, _p, _p],
     "fhe_key_load": [_p, _p, _pp],
     "fhe_key_download": [_p, _p],

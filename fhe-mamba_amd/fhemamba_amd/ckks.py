@@ -498,6 +498,24 @@ class CryptoContext:
         return self._wrap(self._ctx.rescale(ct.poly), ct.level + 1, ct.deg - 1,
                           ct.scale / q_top, ct.slots)
 
+    def _rescaled_many(self, cts: list) -> list:
+        """[_rescaled(ct) for ct in cts], the ciphertexts of one shape
+        rescaled in shared launches (fhe_rescale_many)."""
+        out: list = [None] * len(cts)
+        groups: dict = {}
+        for idx, ct in enumerate(cts):
+            if ct.poly.nlimb < 2:
+                raise ValueError("no limb left to rescale")
+            groups.setdefault((ct.poly.npoly, ct.poly.nlimb), []).append(idx)
+        for (_, nlimb), idxs in groups.items():
+            q_top = self._ctx.q[nlimb - 1]
+            polys = (self._ctx.rescale_many([cts[i].poly for i in idxs]) if len(idxs) > 1
+                     else [self._ctx.rescale(cts[idxs[0]].poly)])
+            for i, poly in zip(idxs, polys):
+                ct = cts[i]
+                out[i] = self._wrap(poly, ct.level + 1, ct.deg - 1, ct.scale / q_top, ct.slots)
+        return out
+
     def _times_int(self, ct: "Ciphertext", c: int) -> "Ciphertext":
         nq = ct.poly.nlimb
         poly = self._ctx.mul_const(ct.poly, self._const_residues(c, nq))
@@ -661,11 +679,21 @@ class CryptoContext:
         whose operands are one object is a square, as in EvalMult."""
         out: list = [None] * len(pairs)
         groups: dict = {}
+        # the degree-2 operands, rescaled together (each once) as
+        # _align_mult would rescale them one at a time
+        deep = {}
+        for a, b in pairs:
+            if isinstance(a, Ciphertext) and isinstance(b, Ciphertext):
+                for x in (a, b):
+                    if x.deg >= 2:
+                        deep.setdefault(id(x), x)
+        settled = dict(zip(deep, self._rescaled_many(list(deep.values()))))
         for idx, (a, b) in enumerate(pairs):
             if not (isinstance(a, Ciphertext) and isinstance(b, Ciphertext)):
                 out[idx] = self._mult(a, b)
                 continue
             same = a is b
+            a, b = settled.get(id(a), a), settled.get(id(b), b)
             a, b = self._align_mult(a, b)
             t = self._ctx.tensor(a.poly, a.poly if same else b.poly)
             groups.setdefault(t.nlimb, []).append((idx, t, a, b))
@@ -726,6 +754,15 @@ class CryptoContext:
     # ------------------------------------------------------------ levels
     def Rescale(self, a: "Ciphertext") -> "Ciphertext":  # noqa: N802
         return self._rescaled(a) if a.deg >= 2 else a.Clone()
+
+    def RescaleMany(self, cts) -> list:  # noqa: N802
+        """[Rescale(ct) for ct in cts], the rescales of one shape sharing
+        their launches (fhe_rescale_many): the same ciphertexts."""
+        out = [ct if ct.deg >= 2 else ct.Clone() for ct in cts]
+        deep = [i for i, ct in enumerate(cts) if ct.deg >= 2]
+        for i, r in zip(deep, self._rescaled_many([cts[i] for i in deep])):
+            out[i] = r
+        return out
 
     def RescaleInPlace(self, a: "Ciphertext") -> None:  # noqa: N802
         if a.deg >= 2:

@@ -123,10 +123,12 @@ class ChebBasis:
     def _operands(i: int) -> tuple:
         return (i // 2, i // 2) if i % 2 == 0 else (i // 2 + 1, i // 2)
 
-    def _finish(self, i: int, product):
+    def _unsettled(self, i: int, product):
         cc = self.cc
-        self.cache[i] = self.settle(cc.EvalSub(cc.EvalAdd(product, product),
-                                               1.0 if i % 2 == 0 else self.u))
+        return cc.EvalSub(cc.EvalAdd(product, product), 1.0 if i % 2 == 0 else self.u)
+
+    def _finish(self, i: int, product):
+        self.cache[i] = self.settle(self._unsettled(i, product))
 
     def __call__(self, i: int):
         if i not in self.cache:
@@ -139,7 +141,8 @@ class ChebBasis:
     def build_many(requests) -> None:
         """For (basis, indices) pairs: every T_i the indices need, by
         increasing depth, the products of one depth over all the bases
-        multiplied together (_mult_many); each T_i is the value __call__
+        multiplied together (_mult_many) and rescaled together (RescaleMany,
+        where the context has it); each T_i is the value __call__
         computes."""
         memo: dict = {}
         todo = []
@@ -160,8 +163,16 @@ class ChebBasis:
             for b, i in step:
                 x, y = b._operands(i)
                 pairs.append((b.cache[x], b.cache[x] if x == y else b.cache[y]))
-            for (b, i), prod in zip(step, _mult_many(step[0][0].cc, pairs)):
-                b._finish(i, prod)
+            cc = step[0][0].cc
+            many = getattr(cc, "RescaleMany", None)
+            prods = _mult_many(cc, pairs)
+            if many is not None and len(step) > 1:
+                values = many([b._unsettled(i, p) for (b, i), p in zip(step, prods)])
+                for (b, i), v in zip(step, values):
+                    b.cache[i] = v
+            else:
+                for (b, i), p in zip(step, prods):
+                    b._finish(i, p)
 
 
 def _ps_split(c, n: int, k: int):

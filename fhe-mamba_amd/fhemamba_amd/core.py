@@ -219,6 +219,16 @@ class Context:
         call("fhe_rescale", out.handle, a.handle)
         return out
 
+    def rescale_many(self, polys, outs=None):
+        """Rescale every poly set of `polys` (one shape) in shared launches;
+        the same polys as rescale() of each."""
+        count = len(polys)
+        outs = outs if outs is not None else [Poly(self, a.npoly, a.nlimb - 1) for a in polys]
+        ah = (ctypes.c_void_p * max(count, 1))(*([a.handle.value for a in polys] or [None]))
+        oh = (ctypes.c_void_p * max(count, 1))(*([o.handle.value for o in outs] or [None]))
+        call("fhe_rescale_many", oh, ah, count)
+        return outs
+
     def tensor(self, a, b):
         out = Poly(self, 3, a.nlimb)
         call("fhe_tensor", out.handle, a.handle, b.handle)

@@ -149,6 +149,12 @@ int fhe_mul_int(fhe_poly *out, const fhe_poly *a, int64_t c);
 /* RescaleInPlace, FLEXIBLEAUTO (packed_fideslib.cpp:236): drop the last limb
  * with division by its prime and centred rounding. */
 int fhe_rescale(fhe_poly *out, const fhe_poly *a);
+/* fhe_rescale of `count` inputs of one shape at once (as[r] into outs[r]):
+ * the rescales of one step of the reference's Chebyshev evaluation (the
+ * basis powers of one depth before they are multiplied again,
+ * src/fhemamba/ckks_probes.py:108-155) sharing one set of launches.
+ * Outputs must be distinct and none may be one of the inputs. */
+int fhe_rescale_many(fhe_poly *const *outs, const fhe_poly *const *as, uint32_t count);
 /* ModRaise, the first step of EvalBootstrap (packed_fideslib.cpp:235-270,
  * stage1_mamba2_decode_fideslib.cpp:2127): limb 0 (mod q0) of every poly
  * of a, centred, lifted to q_0..q_{nlimb-1}; out is [npoly][nlimb]. */

@@ -252,7 +252,8 @@ def test_mult_many_equals_mult(env):
     """EvalMultMany gives the ciphertexts EvalMult gives, residue for
     residue: products at two levels (two batched relinearizations), a
     square (one operand twice), operands of different levels and degrees
-    (aligned as EvalMult aligns them) and a plaintext product."""
+    (aligned as EvalMult aligns them) and a plaintext product; RescaleMany
+    gives the ciphertexts Rescale gives."""
     cc, keys = env
     a, b = enc(cc, keys, vec(1)), enc(cc, keys, vec(2))
     c = enc(cc, keys, vec(3), level=2)
@@ -263,6 +264,12 @@ def test_mult_many_equals_mult(env):
     got = cc.EvalMultMany(pairs)
     for (x, y), g in zip(pairs, got):
         want = cc.EvalMult(x, y)
+        assert (g.GetLevel(), g.GetNoiseScaleDeg()) == (want.GetLevel(), want.GetNoiseScaleDeg())
+        assert g.GetScalingFactor() == want.GetScalingFactor()
+        assert np.array_equal(g.poly.numpy(), want.poly.numpy())
+    deep = [cc.EvalMult(a, b), cc.EvalMult(c, c), d, cc.EvalMult(b, c)]
+    for g, x in zip(cc.RescaleMany(deep + [a]), deep + [a]):
+        want = cc.Rescale(x)
         assert (g.GetLevel(), g.GetNoiseScaleDeg()) == (want.GetLevel(), want.GetNoiseScaleDeg())
         assert g.GetScalingFactor() == want.GetScalingFactor()
         assert np.array_equal(g.poly.numpy(), want.poly.numpy())

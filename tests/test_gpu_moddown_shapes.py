@@ -12,6 +12,7 @@ from gpu_helpers import residues
 pytestmark = pytest.mark.gpu
 
 F = pytest.importorskip("fhemamba_amd")
+from fhemamba_amd._lib import FheError  # noqa: E402
 
 # (log_n, depth, scale bits, first bits, dnum); N=2^13 is covered by
 # test_gpu_keyswitch.py.
@@ -46,6 +47,25 @@ def test_rescale_shapes(setup):
         for nq in range(2, ctx.L + 1):
             a = residues(rng, ctx.q[:nq], (npoly,), ctx.n)
             assert np.array_equal(ctx.rescale(ctx.upload(a)).numpy(), orc.rescale(a)), nq
+
+
+def test_rescale_many(setup):
+    """Rescale of 19 inputs of one shape in shared launches (16 per launch
+    set, then 3) equals the oracle's rescale of each, for 2-poly and 1-poly
+    inputs; outputs aliasing an input and inputs of two shapes are refused."""
+    ctx, orc, s = setup
+    rng = np.random.default_rng(12)
+    for npoly, nq in ((2, ctx.L), (1, 3)):
+        xs = [residues(rng, ctx.q[:nq], (npoly,), ctx.n) for _ in range(19)]
+        got = ctx.rescale_many([ctx.upload(x) for x in xs])
+        for r, x in enumerate(xs):
+            assert np.array_equal(got[r].numpy(), orc.rescale(x)), (npoly, nq, r)
+    a = ctx.upload(residues(rng, ctx.q[:2], (2,), ctx.n))
+    b = ctx.upload(residues(rng, ctx.q[:3], (2,), ctx.n))
+    with pytest.raises(FheError):
+        ctx.rescale_many([a, b])
+    with pytest.raises(FheError):
+        ctx.rescale_many([a], outs=[a])
 
 
 def test_hoisted_rotations(setup):
