@@ -43,7 +43,7 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
-from .ckks_probes import cheb_ps_depth, chebyshev_ps
+from .ckks_probes import cheb_ps_depth, chebyshev_ps_many
 from .ptcache import PlaintextCache
 from .rotation import bsgs_rotations
 
@@ -395,36 +395,45 @@ class CKKSBootstrapper:
         self.cc.RescaleInPlace(ct)
         return ct
 
-    def _eval_mod(self, v, gain: int = 1):
-        """sin(2 pi u) * gain for v = u / K; the integer gain rides on the
-        last double angle (gain (2 y^2 - 1) = (2 gain) y^2 - gain by an
-        integer product, no level)."""
-        c = chebyshev_ps(self.cc, v, self._coeffs, floor=1e-14)
+    def _squares(self, cs: list) -> list:
+        """EvalSquare of each (one batched relinearization for several)."""
+        many = getattr(self.cc, "EvalMultMany", None)
+        if many is not None and len(cs) > 1:
+            return many([(c, c) for c in cs])
+        return [self.cc.EvalSquare(c) for c in cs]
+
+    def _eval_mod(self, vs: list, gain: int = 1) -> list:
+        """sin(2 pi u) * gain for each v = u / K of `vs` (independent
+        inputs, evaluated in lockstep); the integer gain rides on the last
+        double angle (gain (2 y^2 - 1) = (2 gain) y^2 - gain by an integer
+        product, no level)."""
+        cs = chebyshev_ps_many(self.cc, [(v, self._coeffs, 1e-14, None) for v in vs])
         r = self.cfg.sine.r
         for step in range(r):
-            sq = self.cc.EvalSquare(c)
+            sqs = self._squares(cs)
             if step == r - 1 and gain != 1:
-                c = self.cc.EvalSub(self.cc.MultByInteger(sq, 2 * gain), float(gain))
+                cs = [self.cc.EvalSub(self.cc.MultByInteger(sq, 2 * gain), float(gain))
+                      for sq in sqs]
             else:
-                c = self.cc.EvalSub(self.cc.EvalAdd(sq, sq), 1.0)
+                cs = [self.cc.EvalSub(self.cc.EvalAdd(sq, sq), 1.0) for sq in sqs]
         if r == 0 and gain != 1:
-            c = self.cc.MultByInteger(c, gain)
-        return c
+            cs = [self.cc.MultByInteger(c, gain) for c in cs]
+        return cs
 
-    def _eval_mod_amplitude(self, v, amp: float):
-        """amp sin(2 pi u) for v = u / K and any real amp > 0: the
-        interpolant carries a_0 = amp^(2^-r) and each double angle
-        y <- 2 y^2 - a_(k+1) with a_(k+1) = a_k^2, so y_k = a_k cos(2^k x)
-        and y_r = amp cos(2^r x) with integer products only."""
+    def _eval_mod_amplitude(self, vs: list, amp: float) -> list:
+        """amp sin(2 pi u) for each v = u / K of `vs` (in lockstep) and any
+        real amp > 0: the interpolant carries a_0 = amp^(2^-r) and each
+        double angle y <- 2 y^2 - a_(k+1) with a_(k+1) = a_k^2, so y_k =
+        a_k cos(2^k x) and y_r = amp cos(2^r x) with integer products only."""
         r = self.cfg.sine.r
         a = amp ** (2.0 ** -r)
         # the floor scales with a: the same terms as the unscaled interpolant
-        c = chebyshev_ps(self.cc, v, [a * x for x in self._coeffs], floor=1e-14 * a)
+        coeffs = [a * x for x in self._coeffs]
+        cs = chebyshev_ps_many(self.cc, [(v, coeffs, 1e-14 * a, None) for v in vs])
         for _ in range(r):
             a = a * a
-            sq = self.cc.EvalSquare(c)
-            c = self.cc.EvalSub(self.cc.EvalAdd(sq, sq), a)
-        return c
+            cs = [self.cc.EvalSub(self.cc.EvalAdd(sq, sq), a) for sq in self._squares(cs)]
+        return cs
 
     # --------------------------------------------------------------- bootstrap
     def bootstrap(self, ct, pre: float = 1.0, post: float = 1.0):
@@ -469,8 +478,8 @@ class CKKSBootstrapper:
         # within 2 (times the scale) of the 62-bit encoding limit.
         back = q0 / (2 * math.pi * in_scale) * 2.0 ** c * post
         gain = 1 << max(0, math.ceil(math.log2(max(back, 1.0))) - len(self.s2c))
-        re_m = self._eval_mod(re, gain)                       # gain sin(2 pi u)
-        im_m = self._eval_mod(im, gain)                       #   ~ gain 2 pi P / q0
+        re_m, im_m = self._eval_mod([re, im], gain)           # gain sin(2 pi u)
+                                                              #   ~ gain 2 pi P / q0
         w = cc.EvalAdd(re_m, cc.MultByMonomial(im_m, N // 2))
         return self._transform(w, self.s2c, "s2c", back / gain, power_last=True)
 
@@ -518,13 +527,13 @@ class CKKSBootstrapper:
             # second pass would not see and high-degree polynomials would
             # fold back into the real parts: the result is projected onto
             # its real part, (y + conj(y)) / 2 with the 1/2 in the amplitude
-            out = self._eval_mod_amplitude(cc.EvalAdd(z, zc), amp / 2)
+            out = self._eval_mod_amplitude([cc.EvalAdd(z, zc)], amp / 2)[0]
             cc.RescaleInPlace(out)
             out = cc.EvalAdd(out, cc.EvalConjugate(out))             # pre post Re(m)
         else:
-            out = self._eval_mod_amplitude(cc.EvalAdd(z, zc), amp)
             im = cc.MultByMonomial(cc.EvalSub(z, zc), 3 * N // 2)
-            out = cc.EvalAdd(out, cc.MultByMonomial(self._eval_mod_amplitude(im, amp), N // 2))
+            out, im_m = self._eval_mod_amplitude([cc.EvalAdd(z, zc), im], amp)
+            out = cc.EvalAdd(out, cc.MultByMonomial(im_m, N // 2))
             cc.RescaleInPlace(out)
         return out
 
