@@ -45,15 +45,15 @@ HBM_PEAK = 8.0e12  # B/s, MI355X HBM3E
 # hash of the kernel sources they were measured on.  A build from other
 # sources reports traffic as null.
 MEASURED_TRAFFIC = {
-    "csrc_sha16": "20705cbb1efd5396",
+    "csrc_sha16": "f7e5181e715161d0",
     "kernels": {
         # 30-rotation batch launches of the rotation step
-        "ntt_fwd_blocks_moddown": 3_096_408_371 + 754_974_720,
-        "k_moddown_mid": 253_406_899 + 758_562_854,
-        "ntt_inv_blocks_ksk": 776_174_285 + 251_658_240,
+        "ntt_fwd_blocks_moddown": 3_096_209_792 + 754_974_720,
+        "k_moddown_mid": 253_386_547 + 758_744_205,
+        "ntt_inv_blocks_ksk": 776_270_950 + 251_658_240,
         # NTT batch (64 ciphertexts x 2 polys x 24 limbs): one pass, and the MAC
-        "ntt_pass": 1_636_266_726 + 1_610_612_736,
-        "k_mac": 2_416_048_102 + 25_165_824,
+        "ntt_pass": 1_636_249_088 + 1_610_612_736,
+        "k_mac": 2_416_047_949 + 25_165_824,
     },
 }
 
@@ -462,13 +462,14 @@ class OpTally:
     count, by wrapping the device-context methods (fhemamba_amd.core.Context)
     for the duration of a `with` block.  Classes:
       ks      full key switch with its own ModUp (rotate, keyswitch,
-              relinearize, each ciphertext of rotate_many, each Horner or
-              batched giant step of a linear transform);
+              relinearize, each ciphertext of rotate_many and each tensor of
+              relinearize_many, each Horner or batched giant step of a
+              linear transform);
       modup   a shared ModUp (rotation_precompute; the babies of a linear
               transform);
       hks     a hoisted key switch from shared digits (each key of
               rotate_hoisted; each rotated baby of a linear transform);
-      rescale, tensor, modraise;
+      rescale (each input of rescale_many too), tensor, modraise;
       pmul    one plaintext or constant product over 2 polys (mul_plain,
               mul_const, mul_int, each diagonal of a linear transform, each
               term of linear_wsum);
@@ -523,6 +524,10 @@ class OpTally:
                    lambda ct, d, keys, *r, **k: c.update({("hks", ct.nlimb): len(keys)}))
         self._wrap("rotate_many",
                    lambda cts, *r, **k: c.update([("ks", x.nlimb) for x in cts]))
+        self._wrap("relinearize_many",
+                   lambda ts, *r, **k: c.update([("ks", x.nlimb) for x in ts]))
+        self._wrap("rescale_many",
+                   lambda ps, *r, **k: c.update([("rescale", x.nlimb) for x in ps]))
         self._wrap("linear_transform", lambda *a, **k: lt(*a, **k))
         self._wrap("linear_transform_hoisted", lambda *a, **k: lt(*a, **k))
         self._wrap("encode", lambda v, slots, scale, nlimb, *r, **k:

@@ -24,6 +24,7 @@ class Ctx:
     mul_plain = mul_const = mul_int = _r
     keyswitch = relinearize = rotate = rescale = tensor = rotation_precompute = _r
     mod_raise = linear_wsum = rotate_hoisted = rotate_many = _r
+    relinearize_many = rescale_many = _r
     linear_transform = linear_transform_hoisted = encode = encode_many = _r
 
 
@@ -45,9 +46,11 @@ def test_tally_counts_and_restores():
         c.linear_transform_hoisted(P(20), [1] * 8 + [None] * 2, 4, [None, 1, 2, 3], [1, 5, 25, 125],
                                    giant_keys=[1, 2], giant_galois=[7, 49])
         c.encode_many([[0.0]] * 5, 8, 2.0**40, 3)
+        c.relinearize_many([P(11)] * 3, None)
+        c.rescale_many([P(11)] * 4)
         snap = t.snapshot()
     assert snap == {("add", 10): 2, ("pmul", 7): 1, ("ks", 12): 2, ("rescale", 12): 1,
                     ("hks", 9): 3, ("ks", 8): 2, ("modraise", 30): 1, ("pmul", 5): 4,
                     ("pmul", 20): 8, ("modup", 20): 1, ("hks", 20): 3, ("ks", 20): 2,
-                    ("encode", 3): 5}
+                    ("encode", 3): 5, ("ks", 11): 3, ("rescale", 11): 4}
     assert {k: v for k, v in vars(Ctx).items() if not k.startswith("__")} == originals
