@@ -90,14 +90,15 @@ def test_uniform_ternary_bound():
 def test_secret_bound_and_sparse_plan():
     """K from the secret's Hamming weight: 2N/3 reproduces the uniform
     bound; h = 192 (sparse ternary) gives K = 64, four double angles and a
-    degree-59 cosine, three levels fewer than the uniform plan at N=2^16."""
+    degree-59 cosine, three levels fewer than the uniform plan at N=2^16
+    (K = 512, seven double angles, degree 59)."""
     for ring in (2 ** 12, 2 ** 16):
         assert B.secret_bound(2 * ring / 3) == B.uniform_ternary_bound(ring)
     assert B.secret_bound(192) == 64
     sparse = B.BootstrapConfig.for_ring(2 ** 16, (4, 4), hamming_weight=192).sine
     dense = B.BootstrapConfig.for_ring(2 ** 16, (4, 4)).sine
     assert (sparse.K, sparse.r, sparse.degree) == (64, 4, 59)
-    assert (dense.K, dense.r, dense.degree) == (512, 6, 89)
+    assert (dense.K, dense.r, dense.degree) == (512, 7, 59)
     assert dense.depth() - sparse.depth() == 3
     # a sparse secret's smaller rounding noise (and smaller K) leaves room
     # for a larger scale-down, which shrinks the sine's cubic term

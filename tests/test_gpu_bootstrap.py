@@ -199,7 +199,7 @@ def test_s2c_first_bootstrap(real):
 @pytest.mark.parametrize("s2c_first", [False, True])
 def test_bootstrap_at_ring_2_16(s2c_first):
     """Full packing at N = 2^16 (32768 slots, the decoder's ring) with the
-    uniform-ternary secret (K = 512, degree 89, 6 double angles), both
+    uniform-ternary secret (K = 512, degree 59, 7 double angles), both
     orderings, level budget (4, 4): one pass within 2^-11, two passes
     within 2^-22 (measured about 2^-12.9 and 2^-25)."""
     n = 1 << 16
