@@ -310,6 +310,17 @@ def _bootstrap_once(secret_dist: str, steps: int, warmup: int, s2c_first: bool =
         err = float(np.max(np.abs(np.asarray(pt.GetRealPackedValue()) - x)))
         res[f"{'one' if passes == 1 else 'two'}_pass"] = {
             "ms": sec * 1e3, "max_abs_err": err, "log2_err": float(np.log2(err))}
+    if not s2c_first:
+        # the client's public coefficient bound of its slots (the ordinary
+        # order's EvalMod sees the coefficients): less scale-down
+        from fhemamba_amd.bootstrap import coefficient_bound
+        b = coefficient_bound(x)
+        out = cc.EvalBootstrap(ct, 1, coeff_bound=b)
+        pt = cc.Decrypt(out, keys.secretKey)
+        pt.SetLength(slots)
+        err = float(np.max(np.abs(np.asarray(pt.GetRealPackedValue()) - x)))
+        res["one_pass_coeff_bound"] = {"coeff_bound": b, "max_abs_err": err,
+                                       "log2_err": float(np.log2(err))}
     sine = cc._boot.cfg.sine
     res.update({
         "levels_consumed": cc.GetBootstrapDepth(),

@@ -239,8 +239,33 @@ def secret_bound(hamming_weight: float) -> float:
 NOISE_MODEL_OFFSET_BITS = 4.0
 
 
+def coefficient_bound(values) -> float:
+    """max |m_k| / max |z_j| for the message polynomial m whose n slots are
+    `values`: z_j = m(psi^(5^j)), psi = exp(i pi / 2n), over the subring of
+    degree 2n (a sparse message's coefficients sit at multiples of N / 2n
+    with these values).  m_k = (1 / 2n) sum over odd e of m(psi^e) psi^(-ek),
+    the values at the odd powers being z_j at 5^j and conj(z_j) at -5^j
+    (mod 4n): one FFT of length 2n.  A client that knows its slots computes
+    this before encrypting; every message has it in (0, 1]."""
+    z = np.asarray(values, dtype=np.complex128).ravel()
+    n = len(z)
+    if n < 1 or n & (n - 1):
+        raise ValueError("coefficient_bound needs a power-of-two number of slots")
+    top = float(np.max(np.abs(z)))
+    if top == 0.0:
+        return 1.0
+    m = 2 * n
+    e = np.array([pow(5, j, 2 * m) for j in range(n)])
+    w = np.zeros(2 * m, dtype=np.complex128)
+    w[e] = z
+    w[(-e) % (2 * m)] = np.conj(z)
+    coef = np.exp(-1j * np.pi * np.arange(m) / m) * np.fft.fft(w[1::2]) / m
+    return float(min(1.0, np.max(np.abs(coef.real)) / top))
+
+
 def correction_bits_for(ring_dim: int, sine: SineApprox, in_scale: float, q0: float,
-                        scale: float, slots: int = 0, hamming_weight: float = 0.0) -> int:
+                        scale: float, slots: int = 0, hamming_weight: float = 0.0,
+                        coeff_bound: float = 1.0) -> int:
     """Scale-down c (the message enters ModRaise times 2^-c) balancing the
     two errors of one bootstrap, in message units for a coefficient of size 1:
       * noise: rescale / key-switch rounding of about sqrt(N h / 12) per
@@ -250,9 +275,14 @@ def correction_bits_for(ring_dim: int, sine: SineApprox, in_scale: float, q0: fl
         gain) and q0 / (2 pi in_scale) (the way back), all times 2^c; the
         offset NOISE_MODEL_OFFSET_BITS is measured (N = 2^12 and 2^16,
         59-bit scale, uniform ternary);
-      * the sine's cubic term: (2 pi a)^2 / 6 relative, a = 2^-c in_scale / q0.
-    Equal at 3c = log2((2 pi rho)^2 / 6) - e0, rho = in_scale / q0."""
-    rho = in_scale / q0
+      * the sine's cubic term: (2 pi a)^2 / 6 relative, a = 2^-c b in_scale / q0
+        for coefficients at most b (coeff_bound, 1 by default: a constant
+        slot vector puts its whole mass in one coefficient) times the slot
+        bound.
+    Equal at 3c = log2((2 pi rho)^2 / 6) - e0, rho = b in_scale / q0."""
+    if not 0.0 < coeff_bound <= 1.0:
+        raise ValueError("coeff_bound must lie in (0, 1]")
+    rho = coeff_bound * in_scale / q0
     h = float(hamming_weight) or 2.0 * ring_dim / 3.0
     e0 = (math.log2(math.sqrt(ring_dim * h / 12.0) / scale) + math.log2(sine.K) + sine.r
           + 0.5 * math.log2(slots or ring_dim // 2)
@@ -338,11 +368,12 @@ class CKKSBootstrapper:
         L - 2, less the SlotToCoeff levels under S2C-first."""
         return len(self.cc.GetModuli()[0]) - 2 - (len(self.s2c) if self.s2c_first else 0)
 
-    def correction_bits(self, in_scale: float, q0: float, scale: float) -> int:
+    def correction_bits(self, in_scale: float, q0: float, scale: float,
+                        coeff_bound: float = 1.0) -> int:
         if self.cfg.correction_bits:
             return self.cfg.correction_bits
         return correction_bits_for(self.N, self.cfg.sine, in_scale, q0, scale, self.n,
-                                   self.cfg.hamming_weight)
+                                   self.cfg.hamming_weight, coeff_bound)
 
     # --------------------------------------------------------------- helpers
     def _group_pts(self, which: str, idx: int, plan: GroupPlan, level: int, factor: float):
@@ -436,10 +467,15 @@ class CKKSBootstrapper:
         return cs
 
     # --------------------------------------------------------------- bootstrap
-    def bootstrap(self, ct, pre: float = 1.0, post: float = 1.0):
+    def bootstrap(self, ct, pre: float = 1.0, post: float = 1.0, coeff_bound: float = 1.0):
         """Refresh ct; the slots are multiplied by `pre` on the way in (in
         the scale-down step) and by `post` on the way out (in SlotToCoeff),
-        so a residual pass spends no extra level."""
+        so a residual pass spends no extra level.  `coeff_bound` (the
+        ordinary order only): a public bound b on the message's
+        coefficients relative to its slot bound (coefficient_bound of the
+        slots); EvalMod sees those coefficients, so c is sized for b
+        instead of the worst case 1.  Under S2C-first EvalMod sees the slot
+        values themselves and b has no effect."""
         if self.s2c_first:
             return self._bootstrap_s2c_first(ct, pre, post)
         cc, n, N = self.cc, self.n, self.N
@@ -451,7 +487,7 @@ class CKKSBootstrapper:
             raise ValueError(f"EvalBootstrap needs the input at level <= {L - 2}")
         x.SetLevel(L - 2)
         in_scale = cc.GetScalingFactorReal(L - 1)
-        c = self.correction_bits(in_scale, q0, cc.GetScalingFactorReal(0))
+        c = self.correction_bits(in_scale, q0, cc.GetScalingFactorReal(0), coeff_bound)
         # The product by sf[L-2] / scale(x) makes the rescaled scale
         # sf[L-2]^2 / q1 = sf[L-1] whatever level x came from, so the
         # constants below (and their cached diagonals) depend on pre and

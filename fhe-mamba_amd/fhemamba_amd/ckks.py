@@ -971,19 +971,24 @@ class CryptoContext:
         return self._bootstrapper().input_ceiling()
 
     def EvalBootstrap(self, ct: "Ciphertext", numIterations: int = 1,  # noqa: N802,N803
-                      precision: int = 0, *, scale: float = 1.0) -> "Ciphertext":
+                      precision: int = 0, *, scale: float = 1.0,
+                      coeff_bound: float = 1.0) -> "Ciphertext":
         """Refresh `ct` to level GetBootstrapDepth() (slot values kept to
         bootstrapping precision).  numIterations = 2 runs a second pass on
         the scaled residual of the first (precision = log2 of that scale;
         0 picks 12).  `scale` (an extension of the OpenFHE call) admits
         slots in [-scale, scale]: the division and the multiplication back
         ride on the bootstrap's own scale-down and SlotToCoeff constants,
-        so they cost no level."""
+        so they cost no level.  `coeff_bound` (also an extension; the
+        ordinary order): a public bound on the message's coefficients
+        relative to its slot bound (bootstrap.coefficient_bound of the
+        slots), which lets the first pass scale the message down less; 1,
+        the default, is the worst case."""
         boot = self._bootstrapper()
         scale = float(scale)
         if not scale > 0:
             raise ValueError("bootstrap scale must be positive")
-        out = boot.bootstrap(ct, pre=1.0 / scale, post=scale)
+        out = boot.bootstrap(ct, pre=1.0 / scale, post=scale, coeff_bound=float(coeff_bound))
         if int(numIterations) <= 1:
             return out
         if int(numIterations) != 2:

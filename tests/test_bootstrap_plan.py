@@ -252,6 +252,56 @@ def test_bootstrap_circuit_on_slots(log_n, budget):
     assert err < 1e-5, err
 
 
+def test_coefficient_bound_matches_the_encode_fft():
+    """coefficient_bound against the oracle's encode FFT (the coefficients
+    of the message, as complex pairs): random real and complex slots at
+    full packing and a constant vector (all mass in one coefficient)."""
+    for n in (2, 16, 512, 4096):
+        rng = np.random.default_rng(n)
+        for z in (rng.uniform(-1, 1, n), rng.uniform(-1, 1, n) + 1j * rng.uniform(-1, 1, n),
+                  np.full(n, -0.25)):
+            v = np.asarray(O.fft_special_inv(z))
+            want = max(np.max(np.abs(v.real)), np.max(np.abs(v.imag))) / np.max(np.abs(z))
+            assert B.coefficient_bound(z) == pytest.approx(want, rel=1e-12, abs=1e-15)
+    assert B.coefficient_bound(np.zeros(8)) == 1.0
+    with pytest.raises(ValueError):
+        B.coefficient_bound(np.ones(6))
+
+
+def test_correction_bits_with_a_coefficient_bound():
+    """c falls by (2/3) log2(1/b) for a coefficient bound b (the cubic term
+    is sized for coefficients b times the slot bound); b = 1 is the
+    default's worst case, and b outside (0, 1] is refused."""
+    sine = B.BootstrapConfig.for_ring(2 ** 16).sine
+    args = (2 ** 16, sine, 2.0 ** 59, 2.0 ** 60, 2.0 ** 59)
+    c1 = B.correction_bits_for(*args)
+    assert B.correction_bits_for(*args, coeff_bound=1.0) == c1 == 7
+    assert B.correction_bits_for(*args, coeff_bound=2.0 ** -6) == c1 - 4
+    assert B.correction_bits_for(*args, coeff_bound=2.0 ** -3) == c1 - 2
+    for bad in (0.0, -0.5, 1.5):
+        with pytest.raises(ValueError):
+            B.correction_bits_for(*args, coeff_bound=bad)
+
+
+@pytest.mark.parametrize("log_n,budget", [(10, (3, 3)), (11, (4, 2))])
+def test_bootstrap_circuit_with_a_coefficient_bound(log_n, budget):
+    """Noise-free, the smaller scale-down that a coefficient bound allows
+    keeps the sine's cubic term at the size the worst case has: the same
+    error bound as without it."""
+    cc = SimCC(log_n, L=40)
+    cfg = B.BootstrapConfig.for_ring(1 << log_n, budget)
+    cc.ibound = int(cfg.sine.K) // 2
+    boot = B.CKKSBootstrapper(cc, cfg)
+    n = cc.N // 2
+    rng = np.random.default_rng(log_n + 7)
+    m = rng.uniform(-1, 1, n) + 1j * rng.uniform(-1, 1, n)
+    b = B.coefficient_bound(m)
+    assert boot.correction_bits(2.0 ** 59, cc.q0, 2.0 ** 59, b) <= \
+        boot.correction_bits(2.0 ** 59, cc.q0, 2.0 ** 59) - 2
+    out = boot.bootstrap(SimCt(m, 5), coeff_bound=b)
+    assert np.max(np.abs(out.z - m)) < 1e-5
+
+
 def test_correction_bits_model():
     """c grows with the room the noise leaves: 10 at N = 2^12 and 7 at
     N = 2^16 for a 59-bit scale over a 60-bit q0; 0 at a 50-bit scale."""

@@ -67,6 +67,36 @@ def test_bootstrap_complex_slots_and_lower_input_levels(env):
         assert err < ONE_PASS_TOL, (level, err)
 
 
+def test_bootstrap_with_a_coefficient_bound(env):
+    """A public coefficient bound b (random slots: b ~ 2^-5 at 2048 slots)
+    lets the ordinary order scale the message down ~3 bits less, so the
+    noise, which dominates one pass here, shrinks by about as much; the
+    worst case (a constant vector, b = 1) keeps its precision."""
+    from fhemamba_amd.bootstrap import coefficient_bound
+    cc, keys = env
+    L = len(cc.GetModuli()[0])
+    boot = cc._bootstrapper()
+    rng = np.random.default_rng(11)
+    x = rng.uniform(-1, 1, SLOTS)
+    b = coefficient_bound(x)
+    in_scale, q0 = cc.GetScalingFactorReal(L - 1), float(cc.GetModuli()[0][0])
+    c1 = boot.correction_bits(in_scale, q0, cc.GetScalingFactorReal(0))
+    cb = boot.correction_bits(in_scale, q0, cc.GetScalingFactorReal(0), b)
+    assert c1 - cb >= 2, (c1, cb, b)
+    ct = enc_at(cc, keys, x, L - 2)
+    err1 = np.max(np.abs(dec(cc, keys, cc.EvalBootstrap(ct)) - x))
+    errb = np.max(np.abs(dec(cc, keys, cc.EvalBootstrap(ct, coeff_bound=b)) - x))
+    print(f"one pass: c {c1} -> {cb} (b = 2^{np.log2(b):.1f}): "
+          f"2^{np.log2(err1):.1f} -> 2^{np.log2(errb):.1f}", flush=True)
+    assert errb < err1 / 2
+    const = np.full(SLOTS, 0.75)
+    assert coefficient_bound(const) == 1.0
+    out = cc.EvalBootstrap(enc_at(cc, keys, const, L - 2), coeff_bound=1.0)
+    assert np.max(np.abs(dec(cc, keys, out) - const)) < ONE_PASS_TOL
+    with pytest.raises(ValueError):
+        cc.EvalBootstrap(ct, coeff_bound=0.0)
+
+
 def test_bootstrap_after_a_multiplication(env):
     """A degree-2 input (unrescaled product) is rescaled first."""
     cc, keys = env
