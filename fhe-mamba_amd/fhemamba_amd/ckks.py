@@ -777,6 +777,27 @@ class CryptoContext:
     def LevelReduceInPlace(self, a: "Ciphertext", evalKey=None, levels: int = 1) -> None:  # noqa: N802,N803
         a._assign(self._dropped(a, a.level + int(levels)))
 
+    def AlignToLevel(self, a: "Ciphertext", level: int) -> "Ciphertext":  # noqa: N802
+        """`a` as a degree-1 ciphertext at `level` on that level's standard
+        scale (an extension of the OpenFHE API): rescaled first if degree 2,
+        then, if still shallower, FLEXIBLEAUTO's alignment of a shallower
+        operand (a product by an integer onto the target scale, a rescale
+        and a limb drop, as EvalAdd / EvalMult apply to the shallower of
+        two operands).  Operands met at varying levels reach one level, so
+        plaintexts encoded for it are reused."""
+        x = self._rescaled(a) if a.deg >= 2 else a
+        level = int(level)
+        if not x.level <= level < self.L:
+            raise ValueError(f"cannot align level {x.level} to level {level}")
+        if level == x.level:
+            return x
+        target = self._sf[level]
+        q_top = self._ctx.q[x.poly.nlimb - 1]
+        out = self._rescaled(self._times_int(x, int(round(target * q_top / x.scale))))
+        out = self._dropped(out, level)
+        out.scale = target
+        return out
+
     # ------------------------------------------------------------ rotations
     def EvalRotate(self, a: "Ciphertext", index: int) -> "Ciphertext":  # noqa: N802
         g = galois_element(int(index), self.n)

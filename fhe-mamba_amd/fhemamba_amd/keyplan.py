@@ -117,6 +117,12 @@ class KeyPlanContext:
     def RescaleInPlace(self, ct):  # noqa: N802
         ct._assign(self._settled(ct))
 
+    def AlignToLevel(self, ct, level):  # noqa: N802
+        s = self._settled(ct)
+        if not s.level <= level < self.limbs:
+            raise ValueError(f"cannot align level {s.level} to level {level}")
+        return _SymCt(int(level))
+
     def MakeCKKSPackedPlaintext(self, values, deg=1, level=0, slots=0):  # noqa: N802
         return _SymPlain(int(level), int(deg))
 

@@ -447,7 +447,10 @@ class EncryptedMamba2Decoder:
         inv2 = self.rms_scale(gated, di, lay.eps_gated, lay.polys["gated_rms_invsqrt"],
                               B["gated"], B["gated_variance"], B["gated_inv"])
         w_out = t("out_proj_w") * t("gated_norm_w")[None, :]
-        gin = gated
+        # the carried state deepens gated a level a token: aligned to the
+        # deepest level it can have here, out_proj's diagonals are encoded
+        # once instead of every token
+        gin = ev.at_level(gated, ev.refresh_ceiling - 4)
         dsup = self._support(0, self.d)
         out = self.times_scale(ev.linear(gin, w_out, ("out_proj", li)), inv2, B["out_raw"],
                                dsup, B["gated_inv"])

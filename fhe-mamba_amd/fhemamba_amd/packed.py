@@ -37,6 +37,14 @@ import numpy as np
 from .ptcache import PlaintextCache
 from .rotation import bsgs_rotations
 
+try:
+    from xxhash import xxh3_128_digest as _digest
+except ImportError:  # pragma: no cover - the image ships xxhash
+    import hashlib
+
+    def _digest(buf) -> bytes:
+        return hashlib.blake2b(buf, digest_size=16).digest()
+
 PACKED_MAX_NODES = 1_000_000
 REFRESH_SCALE_BITS = 12          # the reference's 4096 residual scale
 CHEB_COEFF_FLOOR = 1e-14         # packed_fideslib.cpp chebyshev(): |c_i| < 1e-14 skipped
@@ -460,7 +468,16 @@ class PackedEvaluator:
         self.stats["ct_pt"] += 1
         return self.cc.EvalMult(ct, float(c))
 
+    def at_level(self, ct, level: int):
+        """ct on `level`'s standard scale (CryptoContext.AlignToLevel)."""
+        return self.cc.AlignToLevel(ct, level)
+
     def plain(self, ct, values, multiply: bool, key=None):
+        """ct * values (multiply) or ct + values, the plaintext encoded at
+        ct's level.  Plaintexts are cached by `key` (a name for the value
+        set) or, without one, by a 128-bit digest of the values: a decode
+        meets the same constants (affine maps, masks, biases, taps) at the
+        same levels token after token."""
         v = self._pad(values)
         if multiply:
             self.stats["ct_pt"] += 1
@@ -474,15 +491,22 @@ class PackedEvaluator:
                 k = 1 << math.ceil(math.log2(big / 2.0))
                 ct = self.cc.MultByInteger(ct, k)
                 v = v / k
-            ck = None if key is None else (key, ct.GetLevel(), k)
-            pt = self._pt_cache.get(ck) if ck else None
+            ck = (key if key is not None else ("mul", _digest(v.data)), ct.GetLevel(), k)
+            pt = self._pt_cache.get(ck)
             if pt is None:
                 pt = self.cc.MakeCKKSPackedPlaintext(v, 1, ct.GetLevel(), slots=self.slots)
-                if ck:
-                    self._pt_cache.put(ck, pt)
+                self._pt_cache.put(ck, pt)
             return self.cc.EvalMult(ct, pt)
         self.stats["adds"] += 1
-        return self.cc.EvalAdd(ct, self.cc.MakeCKKSPackedPlaintext(v, 1, 0, slots=self.slots))
+        # encoded at ct's level and degree: the plaintext EvalAdd would
+        # otherwise re-encode from a top-level one
+        deg = min(max(int(ct.GetNoiseScaleDeg()), 1), 2)
+        ck = (key if key is not None else ("add", _digest(v.data)), ct.GetLevel(), deg)
+        pt = self._pt_cache.get(ck)
+        if pt is None:
+            pt = self.cc.MakeCKKSPackedPlaintext(v, deg, ct.GetLevel(), slots=self.slots)
+            self._pt_cache.put(ck, pt)
+        return self.cc.EvalAdd(ct, pt)
 
     def mask(self, ct, size: int):
         return self.plain(ct, np.ones(size), True, key=("ones", size))

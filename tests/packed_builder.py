@@ -170,6 +170,12 @@ class SlotContext:
     def _check(self, level):
         assert level <= self.L - 1, f"level {level} beyond the chain"
 
+    def AlignToLevel(self, a, level):  # noqa: N802
+        x = self._rescaled(a)
+        if not x.level <= level < self.L:
+            raise ValueError(f"cannot align level {x.level} to level {level}")
+        return x if level == x.level else SlotCt(x.z, level, 1)
+
     def EvalAdd(self, a, b):  # noqa: N802
         if isinstance(b, SlotCt):
             lv = max(a.level, b.level)

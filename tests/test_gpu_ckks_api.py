@@ -130,6 +130,29 @@ def test_level_and_degree_alignment(env):
     np.testing.assert_allclose(dec(cc, keys, c2), x, atol=TOL)
 
 
+def test_align_to_level(env):
+    """AlignToLevel: a shallower or degree-2 ciphertext reaches the target
+    level on its standard scale with its value kept, and then meets a
+    ciphertext made at that level as EvalAdd's own alignment would; a
+    deeper target than the input is refused."""
+    cc, keys = env
+    x, y = vec(31), vec(32)
+    cx = enc(cc, keys, x)
+    cy = cc.Rescale(cc.EvalMult(enc(cc, keys, y), 1.0))       # level 1
+    for src, want in ((cx, x), (cc.EvalMult(cx, cx), x * x)):
+        out = cc.AlignToLevel(src, 4)
+        assert out.GetLevel() == 4 and out.GetNoiseScaleDeg() == 1
+        assert out.GetScalingFactor() == cc.GetScalingFactorReal(4)
+        np.testing.assert_allclose(dec(cc, keys, out), want, atol=TOL)
+    same = cc.AlignToLevel(cy, 1)
+    assert same.GetLevel() == 1
+    np.testing.assert_allclose(dec(cc, keys, same), y, atol=TOL)
+    deep = cc.AlignToLevel(cx, 3)
+    np.testing.assert_allclose(dec(cc, keys, cc.EvalAdd(deep, cy)), x + y, atol=TOL)
+    with pytest.raises(ValueError):
+        cc.AlignToLevel(deep, 2)
+
+
 def test_in_place_forms(env):
     cc, keys = env
     x, y = vec(10), vec(11)
