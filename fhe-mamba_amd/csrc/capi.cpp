@@ -878,27 +878,39 @@ int fhe_rotate_many(fhe_poly* const* outs, const fhe_poly* const* cts, const fhe
   });
 }
 
-static void linear_transform_checked(fhe_poly* out, const fhe_poly* ct,
-                                     const fhe_poly* const* pts, uint32_t count, uint32_t bstep,
-                                     const fhe_key* const* baby_keys,
+static void linear_transform_checked(fhe_poly* const* outs, const fhe_poly* const* cts,
+                                     uint32_t ncts, const fhe_poly* const* pts, uint32_t count,
+                                     uint32_t bstep, const fhe_key* const* baby_keys,
                                      const uint32_t* baby_galois, const fhe_key* const* giant_keys,
                                      const uint32_t* giant_galois, uint32_t n_giant_keys) {
-  need(ct && pts, "null argument");
-  same_ctx(out, ct);
+  need(outs && cts && pts, "null argument");
+  need(ncts >= 1 && ncts <= 64, "1..64 ciphertexts per linear transform call");
+  const fhe_poly* ct = cts[0];
+  need(ct != nullptr, "null argument");
   fhe::Context& c = *ct->c;
-  need(ct->npoly == 2 && ct->nlimb <= c.L, "linear transform needs a 2-poly ciphertext");
+  const uint32_t nq = ct->nlimb;
+  for (uint32_t i = 0; i < ncts; ++i) {
+    need(cts[i] && outs[i], "null argument");
+    same_ctx(outs[i], cts[i]);
+    need(cts[i]->c == &c, "ciphertexts belong to different contexts");
+    need(cts[i]->npoly == 2 && cts[i]->nlimb <= c.L,
+         "linear transform needs a 2-poly ciphertext");
+    need(cts[i]->nlimb == nq, "ciphertexts of one call must share their limb count");
+    for (uint32_t j = 0; j < i; ++j) need(outs[j] != outs[i], "outputs must be distinct");
+  }
   need(count >= 1 && bstep >= 1 && bstep <= fhe::MAC_TABLE,
        "need count >= 1 and 1 <= bstep <= 64");
-  const uint32_t nq = ct->nlimb, giants = (count + bstep - 1) / bstep;
+  const uint32_t giants = (count + bstep - 1) / bstep;
   std::vector<const uint64_t*> pp(count, nullptr);
   bool any = false;
   for (uint32_t k = 0; k < count; ++k) {
     if (!pts[k]) continue;
     need(pts[k]->c == &c && pts[k]->npoly == 1 && pts[k]->nlimb >= nq,
          "diagonal must be a one-poly plaintext with at least the ciphertext's limbs");
-    // Shaping `out` as a ciphertext would free this diagonal's storage
+    // Shaping an output as a ciphertext would free this diagonal's storage
     // while the transform still reads it.
-    need(pts[k] != out, "the output must not be one of the diagonals");
+    for (uint32_t i = 0; i < ncts; ++i)
+      need(pts[k] != outs[i], "the output must not be one of the diagonals");
     pp[k] = pts[k]->data;
     any = true;
   }
@@ -928,9 +940,18 @@ static void linear_transform_checked(fhe_poly* out, const fhe_poly* ct,
       gg.push_back(giant_galois[g]);
     }
   }
-  prepare_out(out, 2, nq);
-  fhe::linear_transform(c, out->data, ct->data, nq, pp.data(), count, bstep, bk.data(),
-                        bg.data(), gk.data(), gg.data(), giants > 1 ? n_giant_keys : 0);
+  // An output that is some input keeps its storage (same shape); every
+  // input is read before any output is written.
+  std::vector<const uint64_t*> src(ncts);
+  for (uint32_t i = 0; i < ncts; ++i) src[i] = cts[i]->data;
+  std::vector<uint64_t*> dst(ncts);
+  for (uint32_t i = 0; i < ncts; ++i) {
+    prepare_out(outs[i], 2, nq);
+    dst[i] = outs[i]->data;
+  }
+  fhe::linear_transform_many(c, dst.data(), src.data(), ncts, nq, pp.data(), count, bstep,
+                             bk.data(), bg.data(), gk.data(), gg.data(),
+                             giants > 1 ? n_giant_keys : 0);
 }
 
 int fhe_linear_transform(fhe_poly* out, const fhe_poly* ct, const fhe_poly* const* pts,
@@ -947,7 +968,8 @@ int fhe_linear_transform(fhe_poly* out, const fhe_poly* ct, const fhe_poly* cons
       bk[b] = baby_keys[b - 1];
       bg[b] = baby_galois[b - 1];
     }
-    linear_transform_checked(out, ct, pts, count, bstep, bk.data(), bg.data(), &giant_key,
+    need(out && ct, "null argument");
+    linear_transform_checked(&out, &ct, 1, pts, count, bstep, bk.data(), bg.data(), &giant_key,
                              &giant_galois, 1);
   });
 }
@@ -957,9 +979,22 @@ int fhe_linear_transform_hoisted(fhe_poly* out, const fhe_poly* ct, const fhe_po
                                  const uint32_t* baby_galois, const fhe_key* const* giant_keys,
                                  const uint32_t* giant_galois, uint32_t n_giant_keys) {
   return guard([&] {
-    need(baby_keys && baby_galois, "null argument");
-    linear_transform_checked(out, ct, pts, count, bstep, baby_keys, baby_galois, giant_keys,
+    need(baby_keys && baby_galois && out && ct, "null argument");
+    linear_transform_checked(&out, &ct, 1, pts, count, bstep, baby_keys, baby_galois, giant_keys,
                              giant_galois, n_giant_keys);
+  });
+}
+
+int fhe_linear_transform_hoisted_many(fhe_poly* const* outs, const fhe_poly* const* cts,
+                                      uint32_t ncts, const fhe_poly* const* pts, uint32_t count,
+                                      uint32_t bstep, const fhe_key* const* baby_keys,
+                                      const uint32_t* baby_galois,
+                                      const fhe_key* const* giant_keys,
+                                      const uint32_t* giant_galois, uint32_t n_giant_keys) {
+  return guard([&] {
+    need(baby_keys && baby_galois, "null argument");
+    linear_transform_checked(outs, cts, ncts, pts, count, bstep, baby_keys, baby_galois,
+                             giant_keys, giant_galois, n_giant_keys);
   });
 }
 

@@ -468,7 +468,17 @@ void linear_transform(Context& c, uint64_t* out, const uint64_t* ct, uint32_t nq
                       const uint64_t* const* baby_keys, const uint32_t* baby_galois,
                       const uint64_t* const* giant_keys, const uint32_t* giant_galois,
                       uint32_t n_giant_keys) {
+  linear_transform_many(c, &out, &ct, 1, nq, pts, count, bstep, baby_keys, baby_galois,
+                        giant_keys, giant_galois, n_giant_keys);
+}
+
+void linear_transform_many(Context& c, uint64_t* const* outs, const uint64_t* const* cts,
+                           uint32_t ncts, uint32_t nq, const uint64_t* const* pts,
+                           uint32_t count, uint32_t bstep, const uint64_t* const* baby_keys,
+                           const uint32_t* baby_galois, const uint64_t* const* giant_keys,
+                           const uint32_t* giant_galois, uint32_t n_giant_keys) {
   if (count == 0 || bstep == 0) throw ArgError("linear transform: no diagonals");
+  if (ncts == 0) return;
   const size_t n = c.n, ne = nq + c.K, pl = 2 * (size_t)nq * n;
   const uint32_t giants = (count + bstep - 1) / bstep, nb = std::min(bstep, count);
   const bool batched = giants > 1 && n_giant_keys == giants - 1;
@@ -479,102 +489,158 @@ void linear_transform(Context& c, uint64_t* out, const uint64_t* ct, uint32_t nq
   std::vector<uint8_t> used(nb, 0);
   for (uint32_t k = 0; k < count; ++k)
     if (pts[k]) used[k % bstep] = 1;
-  // Babies rot(ct) for the b some diagonal uses, all from one ModUp; baby 0
-  // is ct itself unless baby_keys[0] gives it an offset rotation.
-  std::vector<const uint64_t*> baby(nb, nullptr);
-  Scratch babies(c, std::max<size_t>(1, nb * pl));
-  Scratch dig(c, num_digits(c, nq) * ne * n);
-  std::vector<const uint64_t*> keys;
-  std::vector<KeySwitchOut> outs;
+  const uint32_t nd = num_digits(c, nq);
+  const size_t ct_words = (size_t)nd * ne * n;
+  // Key switches sharing the digits of one ciphertext go out in batches of
+  // at most MAX_KS_BATCH whose ModDown scratch stays under 2 GiB.
+  const size_t per_rot = 2 * (size_t)(c.K + nq) * n * 8;
+  const uint32_t ks_batch =
+      std::min<uint32_t>((uint32_t)std::max<size_t>(1, (size_t(2) << 30) / per_rot), MAX_KS_BATCH);
+  auto switch_all = [&](const std::vector<const uint64_t*>& dg,
+                        const std::vector<const uint64_t*>& keys,
+                        const std::vector<KeySwitchOut>& ko) {
+    const uint32_t total = (uint32_t)ko.size();
+    for (uint32_t r0 = 0; r0 < total; r0 += ks_batch)
+      keyswitch_batch(c, dg.data() + r0, nq, keys.data() + r0, std::min(ks_batch, total - r0),
+                      ko.data() + r0);
+  };
+  // Babies rot(ct_i) for the b some diagonal uses: every ciphertext's c1 in
+  // one batched ModUp, then all (ciphertext, baby) key switches; baby 0 is
+  // ct_i itself unless baby_keys[0] gives it an offset rotation.
+  std::vector<const uint64_t*> baby((size_t)ncts * nb, nullptr);
+  std::vector<uint32_t> ks_b;
   for (uint32_t b = 0; b < nb; ++b) {
     if (b == 0 && !baby_keys[0]) {
-      baby[0] = ct;
+      for (uint32_t i = 0; i < ncts; ++i) baby[(size_t)i * nb] = cts[i];
       continue;
     }
     if (!used[b]) continue;
     if (!baby_keys[b]) throw ArgError("linear transform: baby-step key missing");
-    uint64_t* dst = babies.p + b * pl;
-    baby[b] = dst;
-    keys.push_back(baby_keys[b]);
-    outs.push_back(KeySwitchOut{dst, ct, nullptr, baby_galois[b]});
+    ks_b.push_back(b);
   }
-  if (!keys.empty()) {
-    modup(c, ct + (size_t)nq * n, nq, dig.p);
-    keyswitch_hoisted(c, dig.p, nq, keys.data(), outs.data(), (uint32_t)keys.size());
+  Scratch babies(c, std::max<size_t>(1, (size_t)ncts * ks_b.size() * pl));
+  if (!ks_b.empty()) {
+    Scratch dig(c, (size_t)ncts * ct_words);
+    std::vector<const uint64_t*> c1(ncts), dg, keys;
+    std::vector<KeySwitchOut> ko;
+    for (uint32_t i = 0; i < ncts; ++i) c1[i] = cts[i] + (size_t)nq * n;
+    modup_batch(c, c1.data(), ncts, nq, dig.p);
+    for (uint32_t i = 0; i < ncts; ++i)
+      for (size_t j = 0; j < ks_b.size(); ++j) {
+        const uint32_t b = ks_b[j];
+        uint64_t* dst = babies.p + ((size_t)i * ks_b.size() + j) * pl;
+        baby[(size_t)i * nb + b] = dst;
+        dg.push_back(dig.p + i * ct_words);
+        keys.push_back(baby_keys[b]);
+        ko.push_back(KeySwitchOut{dst, cts[i], nullptr, baby_galois[b]});
+      }
+    switch_all(dg, keys, ko);
   }
   std::vector<const uint64_t*> xs, ws;
-  auto inner = [&](uint32_t g, uint64_t* acc, bool accumulate) {
+  auto inner = [&](uint32_t i, uint32_t g, uint64_t* acc, bool accumulate) {
     xs.clear();
     ws.clear();
     for (uint32_t b = 0; b < bstep; ++b) {
       const uint32_t k = g * bstep + b;
       if (k < count && pts[k]) {
-        xs.push_back(baby[b]);
+        xs.push_back(baby[(size_t)i * nb + b]);
         ws.push_back(pts[k]);
       }
     }
     poly_mac_table(c, acc, xs.data(), ws.data(), (uint32_t)xs.size(), nq, accumulate);
   };
   if (batched) {
-    // Every giant step's inner sum, then their rotations by g giant strides
-    // as one batch of independent key switches, then the sum.
-    Scratch in(c, giants * pl), rot(c, (giants - 1) * pl);
+    // Every giant step's inner sum of every ciphertext, then their
+    // rotations by g giant strides as one set of independent key switches,
+    // then the sums.
+    Scratch in(c, (size_t)ncts * giants * pl), rot(c, (size_t)ncts * (giants - 1) * pl);
     // the babies some diagonal uses (the others were not formed)
     std::vector<uint32_t> bu;
     for (uint32_t b = 0; b < nb; ++b)
       if (baby[b]) bu.push_back(b);
-    if (!bu.empty() && bu.size() <= MACG_MAX_B) {
-      // the inner sums of up to MACG_MAX_G giants per pass over the babies
-      const uint32_t nu = (uint32_t)bu.size();
-      std::vector<const uint64_t*> xs(nu);
-      std::vector<uint64_t*> acc(giants);
-      std::vector<const uint64_t*> w((size_t)giants * nu, nullptr);
-      for (uint32_t j = 0; j < nu; ++j) xs[j] = baby[bu[j]];
-      for (uint32_t g = 0; g < giants; ++g) {
-        acc[g] = in.p + g * pl;
-        for (uint32_t j = 0; j < nu; ++j) {
-          const uint32_t k = g * bstep + bu[j];
-          if (k < count) w[(size_t)g * nu + j] = pts[k];
+    const uint32_t nu = (uint32_t)bu.size();
+    for (uint32_t i = 0; i < ncts; ++i) {
+      uint64_t* in_i = in.p + (size_t)i * giants * pl;
+      if (nu && nu <= MACG_MAX_B) {
+        // the inner sums of up to MACG_MAX_G giants per pass over the babies
+        std::vector<const uint64_t*> xb(nu);
+        std::vector<uint64_t*> acc(giants);
+        std::vector<const uint64_t*> w((size_t)giants * nu, nullptr);
+        for (uint32_t j = 0; j < nu; ++j) xb[j] = baby[(size_t)i * nb + bu[j]];
+        for (uint32_t g = 0; g < giants; ++g) {
+          acc[g] = in_i + g * pl;
+          for (uint32_t j = 0; j < nu; ++j) {
+            const uint32_t k = g * bstep + bu[j];
+            if (k < count) w[(size_t)g * nu + j] = pts[k];
+          }
         }
+        for (uint32_t g0 = 0; g0 < giants; g0 += MACG_MAX_G)
+          poly_mac_giants(c, acc.data() + g0, std::min<uint32_t>(MACG_MAX_G, giants - g0),
+                          xb.data(), nu, w.data() + (size_t)g0 * nu, nq);
+      } else {
+        for (uint32_t g = 0; g < giants; ++g) inner(i, g, in_i + g * pl, false);
       }
-      for (uint32_t g0 = 0; g0 < giants; g0 += MACG_MAX_G)
-        poly_mac_giants(c, acc.data() + g0, std::min<uint32_t>(MACG_MAX_G, giants - g0),
-                        xs.data(), nu, w.data() + (size_t)g0 * nu, nq);
-    } else {
-      for (uint32_t g = 0; g < giants; ++g) inner(g, in.p + g * pl, false);
     }
-    std::vector<uint64_t*> ro(giants - 1);
-    std::vector<const uint64_t*> ri(giants - 1);
-    for (uint32_t g = 1; g < giants; ++g) {
-      ro[g - 1] = rot.p + (g - 1) * pl;
-      ri[g - 1] = in.p + g * pl;
-    }
-    rotate_many(c, ro.data(), ri.data(), nq, giant_keys, giant_galois, giants - 1);
-    if (giants <= SUM_MAX) {
-      std::vector<const uint64_t*> terms(giants);
-      terms[0] = in.p;
-      for (uint32_t g = 1; g < giants; ++g) terms[g] = ro[g - 1];
-      poly_sum(c, out, terms.data(), giants, 2, nq);
-    } else {
-      poly_binary(c, OP_ADD, out, in.p, rot.p, 2, nq);
-      for (uint32_t g = 2; g < giants; ++g) poly_binary(c, OP_ADD, out, out, ro[g - 1], 2, nq);
+    const size_t nr = (size_t)ncts * (giants - 1);
+    std::vector<uint64_t*> ro(nr);
+    std::vector<const uint64_t*> ri(nr), rk(nr);
+    std::vector<uint32_t> rg(nr);
+    for (uint32_t i = 0; i < ncts; ++i)
+      for (uint32_t g = 1; g < giants; ++g) {
+        const size_t r = (size_t)i * (giants - 1) + (g - 1);
+        ro[r] = rot.p + r * pl;
+        ri[r] = in.p + ((size_t)i * giants + g) * pl;
+        rk[r] = giant_keys[g - 1];
+        rg[r] = giant_galois[g - 1];
+      }
+    rotate_many(c, ro.data(), ri.data(), nq, rk.data(), rg.data(), (uint32_t)nr);
+    for (uint32_t i = 0; i < ncts; ++i) {
+      const uint64_t* in_i = in.p + (size_t)i * giants * pl;
+      uint64_t* const* ro_i = ro.data() + (size_t)i * (giants - 1);
+      if (giants <= SUM_MAX) {
+        std::vector<const uint64_t*> terms(giants);
+        terms[0] = in_i;
+        for (uint32_t g = 1; g < giants; ++g) terms[g] = ro_i[g - 1];
+        poly_sum(c, outs[i], terms.data(), giants, 2, nq);
+      } else {
+        poly_binary(c, OP_ADD, outs[i], in_i, ro_i[0], 2, nq);
+        for (uint32_t g = 2; g < giants; ++g)
+          poly_binary(c, OP_ADD, outs[i], outs[i], ro_i[g - 1], 2, nq);
+      }
     }
     return;
   }
-  // Giant steps by Horner's rule: acc = inner_{G-1}; acc = inner_g + rot(acc).
-  Scratch acc0(c, pl), acc1(c, pl);
-  uint64_t* cur = acc0.p;
-  uint64_t* nxt = acc1.p;
-  inner(giants - 1, cur, false);
-  for (int g = (int)giants - 2; g >= 0; --g) {
-    modup(c, cur + (size_t)nq * n, nq, dig.p);
-    const KeySwitchOut ko{nxt, cur, nullptr, giant_galois[0]};
-    keyswitch_batch(c, dig.p, nq, &giant_keys[0], 1, &ko);
-    inner((uint32_t)g, nxt, true);
-    std::swap(cur, nxt);
+  // Giant steps by Horner's rule, every ciphertext in step: acc_i =
+  // inner_{G-1}; acc_i = inner_g + rot(acc_i), the rotations of one step as
+  // one batched ModUp and one set of key switches.
+  Scratch acc(c, 2 * (size_t)ncts * pl);
+  std::vector<uint64_t*> cur(ncts), nxt(ncts);
+  for (uint32_t i = 0; i < ncts; ++i) {
+    cur[i] = acc.p + (2 * (size_t)i) * pl;
+    nxt[i] = acc.p + (2 * (size_t)i + 1) * pl;
+    inner(i, giants - 1, cur[i], false);
   }
-  hip_check(hipMemcpyAsync(out, cur, pl * 8, hipMemcpyDeviceToDevice, c.stream),
-            "linear transform");
+  if (giants > 1) {
+    Scratch dig(c, (size_t)ncts * ct_words);
+    std::vector<const uint64_t*> c1(ncts), dg(ncts), keys(ncts, giant_keys[0]);
+    std::vector<KeySwitchOut> ko(ncts);
+    for (int g = (int)giants - 2; g >= 0; --g) {
+      for (uint32_t i = 0; i < ncts; ++i) {
+        c1[i] = cur[i] + (size_t)nq * n;
+        dg[i] = dig.p + i * ct_words;
+        ko[i] = KeySwitchOut{nxt[i], cur[i], nullptr, giant_galois[0]};
+      }
+      modup_batch(c, c1.data(), ncts, nq, dig.p);
+      switch_all(dg, keys, ko);
+      for (uint32_t i = 0; i < ncts; ++i) {
+        inner(i, (uint32_t)g, nxt[i], true);
+        std::swap(cur[i], nxt[i]);
+      }
+    }
+  }
+  for (uint32_t i = 0; i < ncts; ++i)
+    hip_check(hipMemcpyAsync(outs[i], cur[i], pl * 8, hipMemcpyDeviceToDevice, c.stream),
+              "linear transform");
 }
 
 void automorph(Context& c, uint64_t* out, const uint64_t* in, uint32_t npoly, uint32_t nlimb,

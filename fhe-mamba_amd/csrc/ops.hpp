@@ -131,6 +131,19 @@ void linear_transform(Context& c, uint64_t* out, const uint64_t* ct, uint32_t nq
                       const uint64_t* const* baby_keys, const uint32_t* baby_galois,
                       const uint64_t* const* giant_keys, const uint32_t* giant_galois,
                       uint32_t n_giant_keys);
+// The same transform (diagonals and keys) of ncts ciphertexts cts[i]
+// [2][nq][N] into outs[i], in step: one batched ModUp of every
+// ciphertext's c1 for the babies, their key switches in shared batches, and
+// the giant-step rotations of all of them as one set of key switches (or,
+// by Horner's rule, one batched ModUp and key-switch set per step).  The
+// outputs are those of ncts linear_transform calls; outs[i] are distinct
+// and may alias any cts[j] (every input is read before any output is
+// written).
+void linear_transform_many(Context& c, uint64_t* const* outs, const uint64_t* const* cts,
+                           uint32_t ncts, uint32_t nq, const uint64_t* const* pts,
+                           uint32_t count, uint32_t bstep, const uint64_t* const* baby_keys,
+                           const uint32_t* baby_galois, const uint64_t* const* giant_keys,
+                           const uint32_t* giant_galois, uint32_t n_giant_keys);
 // g^-1 mod 2N for an odd Galois element g < 2N.
 uint32_t galois_inverse(uint32_t g, uint32_t n);
 // Galois permutation X -> X^galois of evaluation-form limbs.

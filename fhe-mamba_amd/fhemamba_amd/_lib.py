@@ -82,6 +82,7 @@ SIGNATURES = {
     "fhe_rotate_hoisted": [_p, _p, _p, _p, _u32, _p],
     "fhe_linear_transform": [_p, _p, _p, _u32, _u32, _p, _p, _p, _u32],
     "fhe_linear_transform_hoisted": [_p, _p, _p, _u32, _u32, _p, _p, _p, _p, _u32],
+    "fhe_linear_transform_hoisted_many": [_p, _p, _u32, _p, _u32, _u32, _p, _p, _p, _p, _u32],
     "fhe_rotate_many": [_p, _p, _p, _p, _u32],
     "fhe_mod_raise": [_p, _p, _u32],
     "fhe_encode": [_p, _p, _p, _u32, _u32, _dbl, _u32, _p],

@@ -426,6 +426,25 @@ class CKKSBootstrapper:
         self.cc.RescaleInPlace(ct)
         return ct
 
+    def _transform_many(self, cts: list, plans: list, which: str, total: float,
+                        power_last: bool = False) -> list:
+        """_transform of every ciphertext of `cts` in step: each group's
+        rescales share their launches and the ciphertexts at one level go
+        through one multi-ciphertext linear transform."""
+        cc = self.cc
+        factors = self.group_factors(total, len(plans), power_last)
+        cts = list(cts)
+        for idx, plan in enumerate(plans):
+            cts = cc.RescaleMany(cts)
+            by_level: dict = {}
+            for ct in cts:
+                by_level.setdefault(ct.GetLevel(), []).append(ct)
+            for level, group in by_level.items():
+                pts = self._group_pts(which, idx, plan, level, factors[idx])
+                cc.LinearTransformManyInPlace(group, plan.rows, plan.bstep, pts, plan.stride,
+                                              plan.offset % self.n)
+        return cc.RescaleMany(cts)
+
     def _squares(self, cs: list) -> list:
         """EvalSquare of each (one batched relinearization for several)."""
         many = getattr(self.cc, "EvalMultMany", None)
@@ -518,6 +537,49 @@ class CKKSBootstrapper:
                                                               #   ~ gain 2 pi P / q0
         w = cc.EvalAdd(re_m, cc.MultByMonomial(im_m, N // 2))
         return self._transform(w, self.s2c, "s2c", back / gain, power_last=True)
+
+    def bootstrap_many(self, cts, pre: float = 1.0, post: float = 1.0) -> list:
+        """bootstrap(ct, pre, post) of every ciphertext of `cts`, in step
+        under S2C-first (each stage's key switches, rescales and EvalMod
+        products of all of them share their launches; the same ciphertexts
+        as one call each); the ordinary order refreshes them in turn."""
+        cts = list(cts)
+        if len(cts) <= 1 or not self.s2c_first:
+            return [self.bootstrap(ct, pre, post) for ct in cts]
+        cc, n, N = self.cc, self.n, self.N
+        L = len(cc.GetModuli()[0])
+        q0 = float(cc.GetModuli()[0][0])
+        top = self.input_ceiling()
+        xs = cc.RescaleMany(cts)
+        for x in xs:
+            if x.GetLevel() > top:
+                raise ValueError(f"S2C-first EvalBootstrap needs the input at level <= {top}")
+            x.SetLevel(top)
+        in_scale = cc.GetScalingFactorReal(L - 1)
+        c = self.correction_bits(in_scale, q0, cc.GetScalingFactorReal(0))
+        amp = q0 / (2 * math.pi * in_scale) * 2.0 ** c * post
+        k = post * q0 / (amp * 2 * math.pi * in_scale)
+        ys = self._transform_many(xs, self.s2c, "s2c_first", k, power_last=True)
+        ys = cc.RescaleMany([cc.EvalMult(y, pre * cc.GetScalingFactorReal(L - 2)
+                                         / y.GetScalingFactor()) for y in ys])
+        for y in ys:
+            y.SetScalingFactor(in_scale)
+        raised = [cc.ModRaise(y) for y in ys]
+        K = self.cfg.sine.K
+        zs = self._transform_many(raised, self.c2s, "c2s",
+                                  raised[0].GetScalingFactor() / (q0 * n * 2 * K))
+        zcs = cc.EvalConjugateMany(zs)
+        if self.real_slots:
+            outs = self._eval_mod_amplitude([cc.EvalAdd(z, zc) for z, zc in zip(zs, zcs)],
+                                            amp / 2)
+            outs = cc.RescaleMany(outs)
+            return [cc.EvalAdd(o, oc) for o, oc in zip(outs, cc.EvalConjugateMany(outs))]
+        m = len(zs)
+        ims = [cc.MultByMonomial(cc.EvalSub(z, zc), 3 * N // 2) for z, zc in zip(zs, zcs)]
+        res = self._eval_mod_amplitude([cc.EvalAdd(z, zc) for z, zc in zip(zs, zcs)] + ims,
+                                       amp)
+        outs = [cc.EvalAdd(res[i], cc.MultByMonomial(res[m + i], N // 2)) for i in range(m)]
+        return cc.RescaleMany(outs)
 
     def _bootstrap_s2c_first(self, ct, pre: float, post: float):
         """SlotToCoeff, scale-down, ModRaise, CoeffToSlot, EvalMod.

@@ -839,6 +839,26 @@ class CryptoContext:
         poly = self._ctx.rotate(a.poly, self._key_for(g), g)
         return self._wrap(poly, a.level, a.deg, a.scale, a.slots)
 
+    def EvalConjugateMany(self, cts: Sequence["Ciphertext"]) -> list:  # noqa: N802
+        """[EvalConjugate(ct) for ct in cts], the conjugations at one level
+        in one batched key switch (fhe_rotate_many): the same ciphertexts."""
+        cts = list(cts)
+        if len(cts) == 1:
+            return [self.EvalConjugate(cts[0])]
+        g = conjugation_element(self.n)
+        key = self._key_for(g)
+        outs: list = [None] * len(cts)
+        by_level: dict = {}
+        for j, c in enumerate(cts):
+            by_level.setdefault(c.level, []).append(j)
+        for idx in by_level.values():
+            polys = self._ctx.rotate_many([cts[j].poly for j in idx], [key] * len(idx),
+                                          [g] * len(idx))
+            for j, p in zip(idx, polys):
+                c = cts[j]
+                outs[j] = self._wrap(p, c.level, c.deg, c.scale, c.slots)
+        return outs
+
     def EvalFastRotationPrecompute(self, a: "Ciphertext") -> "FastRotationPrecompute":  # noqa: N802
         return FastRotationPrecompute(a, self._ctx.rotation_precompute(a.poly))
 
@@ -884,6 +904,17 @@ class CryptoContext:
         steps run as one batch of independent rotations instead of Horner's
         rule; otherwise the offset is one rotation and the giants use the
         bStep*stride key.  All schedules give the same sum."""
+        self.LinearTransformManyInPlace([ct], rowSize, bStep, pts, stride, offset)
+
+    def LinearTransformManyInPlace(self, cts: Sequence["Ciphertext"], rowSize: int,  # noqa: N802,N803
+                                   bStep: int, pts: Sequence, stride: int = 1,  # noqa: N803
+                                   offset: int = 0) -> None:
+        """LinearTransformInPlace of every ciphertext of `cts` with the same
+        diagonals (an extension of the OpenFHE API): ciphertexts that meet
+        at one level share their ModUps and key-switch launches
+        (fhe_linear_transform_hoisted_many); the same results as one call
+        each."""
+        cts = list(cts)
         count, bstep = int(rowSize), int(bStep)
         if len(pts) < count:
             raise ValueError("fewer plaintexts than rowSize")
@@ -898,15 +929,19 @@ class CryptoContext:
         fold = bool(offset) and all(has(offset + b * stride) for b in used)
         batch = giants > 2 and all(has(g * bstep * stride) for g in range(1, giants))
         if offset and not fold:
-            ct._assign(self.EvalRotate(ct, offset))
+            for ct, r in zip(cts, self.EvalRotateMany(cts, offset)):
+                ct._assign(r)
         off = offset if fold else 0
-        if ct.deg >= 2:
-            ct._assign(self._rescaled(ct))
+        deep = [ct for ct in cts if ct.deg >= 2]
+        for ct, r in zip(deep, self._rescaled_many(deep)):
+            ct._assign(r)
         deg, scale = present[0].deg, present[0].scale
         if any(p.deg != deg or abs(p.scale / scale - 1) > 1e-12 for p in present):
             raise ValueError("diagonals must share one scale and degree")
-        if any(p.level > ct.level for p in present):
-            ct._assign(self._dropped(ct, max(p.level for p in present)))
+        plevel = max(p.level for p in present)
+        for ct in cts:
+            if plevel > ct.level:
+                ct._assign(self._dropped(ct, plevel))
         baby_keys, baby_gal = [None] * nb, [1] * nb
         for b in used:
             if b or off:
@@ -914,10 +949,21 @@ class CryptoContext:
                 baby_keys[b], baby_gal[b] = self._key_for(g), g
         steps = range(1, giants) if batch else ([1] if giants > 1 else [])
         gal = [galois_element(g * bstep * stride, self.n) for g in steps]
-        poly = self._ctx.linear_transform_hoisted(
-            ct.poly, [None if p is None else p.poly for p in pts], bstep, baby_keys, baby_gal,
-            [self._key_for(g) for g in gal], gal)
-        ct._assign(self._wrap(poly, ct.level, ct.deg + deg, ct.scale * scale, ct.slots))
+        gkeys = [self._key_for(g) for g in gal]
+        ppolys = [None if p is None else p.poly for p in pts]
+        by_level: dict = {}
+        for ct in cts:
+            by_level.setdefault(ct.level, []).append(ct)
+        for group in by_level.values():
+            if len(group) == 1:
+                polys = [self._ctx.linear_transform_hoisted(
+                    group[0].poly, ppolys, bstep, baby_keys, baby_gal, gkeys, gal)]
+            else:
+                polys = self._ctx.linear_transform_hoisted_many(
+                    [ct.poly for ct in group], ppolys, bstep, baby_keys, baby_gal, gkeys, gal)
+            for ct, poly in zip(group, polys):
+                ct._assign(self._wrap(poly, ct.level, ct.deg + deg, ct.scale * scale,
+                                      ct.slots))
 
     # ------------------------------------------------------------ bootstrapping
     def _monomial(self, power: int, nq: int) -> Poly:
@@ -1018,6 +1064,29 @@ class CryptoContext:
         residual = self.EvalSub(ct, out)
         fix = boot.bootstrap(residual, pre=2.0 ** bits / scale, post=scale * 2.0 ** -bits)
         return self.EvalAdd(out, fix)
+
+    def EvalBootstrapMany(self, cts: Sequence["Ciphertext"], numIterations: int = 1,  # noqa: N802,N803
+                          precision: int = 0, *, scale: float = 1.0) -> list:
+        """[EvalBootstrap(ct, numIterations, precision, scale=scale) for ct
+        in cts] (an extension of the OpenFHE API): under S2C-first the
+        ciphertexts go through every stage in step, sharing their key
+        switches, rescales and EvalMod products; the same ciphertexts as
+        one call each."""
+        boot = self._bootstrapper()
+        scale = float(scale)
+        if not scale > 0:
+            raise ValueError("bootstrap scale must be positive")
+        if int(numIterations) > 2:
+            raise ValueError("numIterations must be 1 or 2")
+        cts = list(cts)
+        outs = boot.bootstrap_many(cts, pre=1.0 / scale, post=scale)
+        if int(numIterations) <= 1:
+            return outs
+        bits = int(precision) or 12
+        residuals = [self.EvalSub(ct, out) for ct, out in zip(cts, outs)]
+        fixes = boot.bootstrap_many(residuals, pre=2.0 ** bits / scale,
+                                    post=scale * 2.0 ** -bits)
+        return [self.EvalAdd(o, f) for o, f in zip(outs, fixes)]
 
 
 class FastRotationPrecompute:

@@ -328,6 +328,30 @@ class Context:
              _ptr(bg), gk, _ptr(gg), ng)
         return out
 
+    def linear_transform_hoisted_many(self, cts, pts, bstep: int, baby_keys, baby_galois,
+                                      giant_keys=(), giant_galois=(), outs=None) -> list:
+        """linear_transform_hoisted of every ciphertext of `cts` (one limb
+        count) with the same diagonals and keys, in shared launches; the
+        same polys as one call per ciphertext."""
+        count, m = len(pts), len(cts)
+        outs = list(outs) if outs is not None else [Poly(self, 2, c.nlimb) for c in cts]
+        ch = (ctypes.c_void_p * m)(*[c.handle.value for c in cts])
+        oh = (ctypes.c_void_p * m)(*[o.handle.value for o in outs])
+        ph = (ctypes.c_void_p * count)(*[p.handle.value if p is not None else None
+                                         for p in pts])
+        nb = max(1, min(bstep, count))
+        bk = (ctypes.c_void_p * nb)(*([k.handle.value if k is not None else None
+                                       for k in baby_keys] + [None] * (nb - len(baby_keys))))
+        bg = np.ones(nb, dtype=np.uint32)
+        bg[: len(baby_galois)] = baby_galois
+        ng = len(giant_keys)
+        gk = (ctypes.c_void_p * max(ng, 1))(*([k.handle.value for k in giant_keys] or [None]))
+        gg = np.ones(max(ng, 1), dtype=np.uint32)
+        gg[:ng] = giant_galois
+        call("fhe_linear_transform_hoisted_many", oh, ch, m, ph, count, bstep, bk, _ptr(bg),
+             gk, _ptr(gg), ng)
+        return outs
+
     # -------------------------------------------------------------- encoding
     def encode(self, values, slots: int, scale: float, nlimb: int, out=None) -> "Poly":
         v = np.asarray(values)

@@ -139,13 +139,31 @@ class EncryptedMamba2Decoder:
         b.update(override or {})
         return b
 
-    def ready(self, ct, need: int, bound: float, support=None, critical: bool = False):
+    def ready(self, ct, need: int, bound: float, support=None, critical: bool = False,
+              passes: int | None = None):
         """Refresh ct (masked to `support`) if `need` more levels would pass
-        the ceiling; `critical` refreshes take the two-pass count."""
+        the ceiling; `critical` refreshes take the two-pass count, `passes`
+        overrides both."""
         if self.ev._level(ct) + need > self.ev.refresh_ceiling:
+            if passes is None:
+                passes = self.critical_passes if critical else self.transient_passes
             return self.ev.refresh(ct, bound, support if support is not None else self.slots,
-                                   self.critical_passes if critical else self.transient_passes)
+                                   passes)
         return ct
+
+    def ready_many(self, cts, need: int, bound: float, support=None, critical: bool = False):
+        """ready() of each ciphertext of `cts` (one bound and support), the
+        ones that need a refresh refreshed together."""
+        ev = self.ev
+        out = list(cts)
+        idx = [i for i, ct in enumerate(out) if ev._level(ct) + need > ev.refresh_ceiling]
+        if idx:
+            fresh = ev.refresh_many([out[i] for i in idx], bound,
+                                    support if support is not None else self.slots,
+                                    self.critical_passes if critical else self.transient_passes)
+            for i, ct in zip(idx, fresh):
+                out[i] = ct
+        return out
 
     def full_sum(self, ct):
         """Every slot gets the sum over all slots (rotate-adds)."""
@@ -255,7 +273,11 @@ class EncryptedMamba2Decoder:
             raise ValueError(f"inverse square root of kind {spec.kind}")
         vh = self.ev.scale(v, -0.5)
         for _ in range(spec.iterations):
-            y = self.ready(y, 3, ibound)
+            # y's refresh is followed by a Newton step, whose map has zero
+            # derivative at the root: a relative error e there leaves
+            # -1.5 e^2, so one pass serves whatever the secret (vh's error
+            # would move the root and keeps the transient count)
+            y = self.ready(y, 3, ibound, passes=1)
             vh = self.ready(vh, 3, vbound)
             t = self.ev.mul(vh, self.ev.mul(y, y))
             y = self.ev.mul(y, self.cc.EvalAdd(t, 1.5))
@@ -404,23 +426,21 @@ class EncryptedMamba2Decoder:
             # a transient value (the carried checkpoint is the state)
             decay = self.ev.refresh(decay, B["decay"], ds, self.transient_passes)
         decay_groups = self.expand_compact(self.spread_heads(decay, d0), 0)
-        # state update and readout
-        new_ssm, reads = [], []
-        for g in range(self.groups):
-            xg = self.ready(x_groups[g], 4, B["act"])
-            dg = self.ready(dt_groups[g], 4, B["dt"])
-            br = self.ready(b_rep, 3, B["act"])
-            write = ev.mul(ev.mul(xg, dg), br)
-            if st.ssm is not None:
-                eg = self.ready(decay_groups[g], 2, B["decay"])
-                hg = self.ready(st.ssm[g], 2, B["state"], critical=True)
-                h2 = ev.add(ev.mul(eg, hg), write)
-            else:
-                h2 = write
-            h2 = self.ready(h2, 3, B["state"], critical=True)
-            new_ssm.append(h2)
-            cr = self.ready(c_rep, 3, B["act"])
-            reads.append(ev.mul(h2, cr))
+        # state update and readout; the groups' state refreshes (they reach
+        # the ceiling together) go through one multi-ciphertext bootstrap
+        xs_g = self.ready_many(x_groups, 4, B["act"])
+        ds_g = self.ready_many(dt_groups, 4, B["dt"])
+        br = self.ready(b_rep, 3, B["act"])
+        writes = [ev.mul(ev.mul(xg, dg), br) for xg, dg in zip(xs_g, ds_g)]
+        if st.ssm is not None:
+            es_g = self.ready_many(decay_groups, 2, B["decay"])
+            hs_g = self.ready_many(st.ssm, 2, B["state"], critical=True)
+            h2s = [ev.add(ev.mul(eg, hg), w) for eg, hg, w in zip(es_g, hs_g, writes)]
+        else:
+            h2s = writes
+        new_ssm = self.ready_many(h2s, 3, B["state"], critical=True)
+        cr = self.ready(c_rep, 3, B["act"])
+        reads = [ev.mul(h2, cr) for h2 in new_ssm]
         k = gb
         while k < self.slots:
             ev._ensure_keys([k])

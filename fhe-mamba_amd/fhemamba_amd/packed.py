@@ -562,6 +562,29 @@ class PackedEvaluator:
         self.stats["bootstrap_seconds"] += time.perf_counter() - t0
         return out
 
+    def refresh_many(self, cts, bound: float, support, passes: int | None = None) -> list:
+        """refresh of every ciphertext of `cts` (one bound and support):
+        through the context's multi-ciphertext bootstrap when it has one
+        (the same ciphertexts, shared launches), else one at a time."""
+        cts = list(cts)
+        many = getattr(self.cc, "EvalBootstrapMany", None)
+        if len(cts) <= 1 or many is None:
+            return [self.refresh(ct, bound, support, passes) for ct in cts]
+        passes = self.bootstrap_passes if passes is None else passes
+        if passes not in (1, 2):
+            raise ValueError("bootstrap passes must be 1 or 2")
+        t0 = time.perf_counter()
+        if isinstance(support, (int, np.integer)):
+            xs = [self.mask(ct, int(support)) if support < self.slots else ct for ct in cts]
+        else:
+            xs = [self.plain(ct, support, True) for ct in cts]
+        bound = 2.0 ** math.ceil(math.log2(max(float(bound), 2.0 ** -30)))
+        outs = many(xs, passes, REFRESH_SCALE_BITS, scale=bound)
+        self.stats["bootstraps"] += passes * len(cts)
+        self.stats["logical_refreshes"] += len(cts)
+        self.stats["bootstrap_seconds"] += time.perf_counter() - t0
+        return outs
+
     # ------------------------------------------------------------- node kinds
     def transform(self, x, masks: dict, key=None):
         """sum over offsets of rot(x, offset) * mask.  Offsets on an

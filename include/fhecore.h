@@ -263,6 +263,25 @@ int fhe_linear_transform_hoisted(fhe_poly *out, const fhe_poly *ct,
                                  const fhe_key *const *giant_keys,
                                  const uint32_t *giant_galois,
                                  uint32_t n_giant_keys);
+/* fhe_linear_transform_hoisted of ncts (1..64) ciphertexts cts[i] of one
+ * limb count with the same diagonals and keys, into outs[i]: the
+ * bootstrap's CoeffToSlot / SlotToCoeff groups of several ciphertexts
+ * refreshed at one point of a circuit (the reference's
+ * LinearTransformInPlace per ciphertext, packed_fideslib.cpp:447-516, run
+ * in each bootstrap of the decoder's state-group refreshes,
+ * stage1_mamba2_decode_fideslib.cpp:3952-3967).  One batched ModUp for every ciphertext's babies, their key
+ * switches in shared batches, the giant-step rotations of all of them as
+ * one set; the same outputs as ncts single calls.  outs must be distinct;
+ * an output may be any of the inputs. */
+int fhe_linear_transform_hoisted_many(fhe_poly *const *outs,
+                                      const fhe_poly *const *cts, uint32_t ncts,
+                                      const fhe_poly *const *pts, uint32_t count,
+                                      uint32_t bstep,
+                                      const fhe_key *const *baby_keys,
+                                      const uint32_t *baby_galois,
+                                      const fhe_key *const *giant_keys,
+                                      const uint32_t *giant_galois,
+                                      uint32_t n_giant_keys);
 
 /* ---- encoding -----------------------------------------------------------
  * MakeCKKSPackedPlaintext (packed_fideslib.cpp:204): special inverse FFT of

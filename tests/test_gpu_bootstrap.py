@@ -226,6 +226,31 @@ def test_s2c_first_bootstrap(real):
         cc.EvalBootstrapSetup([3, 3], [0, 0], SLOTS // 2, s2c_first=True)
 
 
+@pytest.mark.parametrize("real", [False, True])
+def test_bootstrap_many_equals_single(real):
+    """EvalBootstrapMany over three ciphertexts in step (S2C-first: shared
+    linear-transform, conjugation, rescale and EvalMod launches) gives
+    the ciphertexts of one EvalBootstrap each, word for word, for one and
+    two passes; the ordinary order refreshes them in turn."""
+    cc, keys = build_toy_context(ring_dimension=1 << LOG_N, batch=SLOTS, depth=44,
+                                 scale_bits=59, first_mod_bits=60, seed=13)
+    cc.EvalBootstrapSetup([3, 3], [0, 0], SLOTS, s2c_first=True, real_slots=real)
+    cc.EvalBootstrapKeyGen(keys.secretKey, SLOTS)
+    L = len(cc.GetModuli()[0])
+    rng = np.random.default_rng(14)
+    cts = []
+    for i in range(3):
+        z = rng.uniform(-1, 1, SLOTS) + (0 if real else 1j * rng.uniform(-1, 1, SLOTS))
+        cts.append(enc_at(cc, keys, z, L - 5 - (i == 2)))     # one a level deeper
+    for passes in (1, 2):
+        singles = [cc.EvalBootstrap(ct, passes, 15, scale=2.0) for ct in cts]
+        many = cc.EvalBootstrapMany(cts, passes, 15, scale=2.0)
+        for got, want in zip(many, singles):
+            assert got.GetLevel() == want.GetLevel()
+            assert got.GetScalingFactor() == want.GetScalingFactor()
+            assert np.array_equal(got.residues(), want.residues())
+
+
 @pytest.mark.parametrize("s2c_first", [False, True])
 def test_bootstrap_at_ring_2_16(s2c_first):
     """Full packing at N = 2^16 (32768 slots, the decoder's ring) with the

@@ -254,3 +254,75 @@ def test_hoisted_linear_transform_rejects_bad_giant_keys(setup):
                                      [k1[2]] * 3, [k1[0]] * 3)
     with pytest.raises(ValueError):  # no giant key at all
         ctx.linear_transform_hoisted(ct, pts, 3, [None, k1[2], k1[2]], [1, k1[0], k1[0]])
+
+
+MANY = [
+    # (count, bstep, stride, offset, null diagonals)
+    (9, 3, 1, -4, (4,)),
+    (16, 4, 3, 5, (0, 13)),
+    (7, 4, 1, 0, (2,)),
+]
+
+
+@pytest.mark.parametrize("count,bstep,stride,offset,nulls", MANY)
+def test_hoisted_linear_transform_many_equals_single(setup, count, bstep, stride, offset, nulls):
+    """fhe_linear_transform_hoisted_many over three ciphertexts: each output
+    equal to the single entry point's (both giant schedules), the first
+    also to the oracle composition; outputs written over the inputs (each
+    into another input's handle) give the same polys."""
+    ctx, orc, s, _ = setup
+    rng = np.random.default_rng((900 + count * 3 + bstep + offset) % 2**32)
+    nq = ctx.L - 1
+    cts = [residues(rng, ctx.q[:nq], (2,), ctx.n) for _ in range(3)]
+    pts_host = [None if k in nulls else residues(rng, ctx.q, (), ctx.n)
+                for k in range(count)]
+    pts_dev = [None if p is None else ctx.upload(p[None]) for p in pts_host]
+    nb = min(bstep, count)
+    used = {k % bstep for k in range(count) if pts_host[k] is not None}
+    okeys = {b: (_key(setup, offset + b * stride)[:2] if (b or offset) else None)
+             for b in used}
+    bdev = [(_key(setup, offset + b * stride)[2] if b in used and (b or offset) else None)
+            for b in range(nb)]
+    bgal = [(_key(setup, offset + b * stride)[0] if b in used and (b or offset) else 1)
+            for b in range(nb)]
+    giants = -(-count // bstep)
+    gks = [_key(setup, g * bstep * stride) for g in range(1, giants)]
+    schedules = [([k[2] for k in gks], [k[0] for k in gks])]
+    if giants > 2:
+        g1 = _key(setup, bstep * stride)
+        schedules.append(([g1[2]], [g1[0]]))
+    first = None
+    for gk, gg in schedules:
+        singles = [ctx.linear_transform_hoisted(ctx.upload(c), pts_dev, bstep, bdev, bgal,
+                                                gk, gg).numpy() for c in cts]
+        first = singles[0] if first is None else first
+        got = ctx.linear_transform_hoisted_many([ctx.upload(c) for c in cts], pts_dev, bstep,
+                                                bdev, bgal, gk, gg)
+        for g, w in zip(got, singles):
+            assert np.array_equal(g.numpy(), w)
+        dcts = [ctx.upload(c) for c in cts]
+        got = ctx.linear_transform_hoisted_many(dcts, pts_dev, bstep, bdev, bgal, gk, gg,
+                                                outs=dcts[1:] + dcts[:1])
+        for g, w in zip(got, singles):
+            assert np.array_equal(g.numpy(), w)
+    want = oracle_transform_hoisted(orc, ctx.q, cts[0], pts_host, bstep, okeys,
+                                    [k[:2] for k in gks])
+    assert np.array_equal(first, want)
+
+
+def test_linear_transform_many_rejects_bad_arguments(setup):
+    ctx, orc, s, _ = setup
+    rng = np.random.default_rng(6)
+    a = ctx.upload(residues(rng, ctx.q, (2,), ctx.n))
+    b = ctx.upload(residues(rng, ctx.q, (2,), ctx.n))
+    short = ctx.upload(residues(rng, ctx.q[:-1], (2,), ctx.n))
+    pt = ctx.upload(residues(rng, ctx.q, (1,), ctx.n))
+    with pytest.raises(ValueError):  # limb counts differ within the call
+        ctx.linear_transform_hoisted_many([a, short], [pt], 1, [None], [1])
+    o = ctx.upload(residues(rng, ctx.q, (2,), ctx.n))
+    with pytest.raises(ValueError):  # one output for two ciphertexts
+        ctx.linear_transform_hoisted_many([a, b], [pt], 1, [None], [1], outs=[o, o])
+    with pytest.raises(ValueError):  # a diagonal as an output
+        ctx.linear_transform_hoisted_many([a, b], [pt], 1, [None], [1], outs=[o, pt])
+    with pytest.raises(ValueError):  # no ciphertext
+        ctx.linear_transform_hoisted_many([], [pt], 1, [None], [1])

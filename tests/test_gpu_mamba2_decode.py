@@ -28,6 +28,29 @@ def test_two_layer_decode_with_carried_state(tmp_path):
     assert r > 0 and r < b < 2 * r
 
 
+def test_state_groups_refresh_together(tmp_path, monkeypatch):
+    """Two layers decoded over ten tokens: the second layer's carried state
+    deepens a level a token until its six groups reach the refresh ceiling
+    together (the eighth carried token); they are refreshed by one
+    multi-ciphertext bootstrap, and every token stays within the decode
+    tolerance."""
+    from fhemamba_amd import packed
+    sizes = []
+    orig = packed.PackedEvaluator.refresh_many
+
+    def refresh_many(self, cts, *a, **k):
+        sizes.append(len(cts))
+        return orig(self, cts, *a, **k)
+
+    monkeypatch.setattr(packed.PackedEvaluator, "refresh_many", refresh_many)
+    M.synthetic_chain(str(tmp_path), n_layers=2, n_test_tokens=10, seed=15)
+    report = D.run_payload(str(tmp_path), seed=16)
+    print(f"ten-token decode: batched refresh sizes {sizes}, errors "
+          f"{report['per_token_errors_vs_polynomial']}", flush=True)
+    assert max(sizes, default=0) == 6
+    assert report["max_abs_error_vs_polynomial"] < TOL
+
+
 def test_command_line(tmp_path):
     M.synthetic_chain(str(tmp_path / "p"), n_layers=1, n_test_tokens=1, seed=5)
     res = tmp_path / "r.json"
