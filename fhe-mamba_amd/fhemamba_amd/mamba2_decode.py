@@ -526,10 +526,13 @@ def token_loop(dec: EncryptedMamba2Decoder, chain: ChainPayload, n_tok: int, ar=
     """Decode n_tok tokens with carried state: the payload's test embeddings,
     or with `ar` (AutoregressiveAssets) the client-in-loop greedy protocol;
     per token the seconds, the errors of the decrypted final hidden against
-    the polynomial and exact references, and the client's selections."""
+    the polynomial and exact references, the client's selections and the
+    token's window on the monotonic clock (nanoseconds, the clock kernel
+    traces are stamped with on this platform, so a trace can be split by
+    token)."""
     states = dec.initial_states()
     out = dict(seconds=[], errors_poly=[], errors_exact=[], selected=[], client_seconds=0.0,
-               bootstraps=[], decrypt_seconds=0.0, token0={})
+               bootstraps=[], decrypt_seconds=0.0, token0={}, windows_ns=[])
     selected = out["selected"]
     want_poly = ar.expected_poly_final if ar else chain.expected_poly_final
     want_exact = ar.expected_exact_final if ar else chain.expected_final
@@ -543,11 +546,13 @@ def token_loop(dec: EncryptedMamba2Decoder, chain: ChainPayload, n_tok: int, ar=
     for k in range(n_tok):
         sync()
         b0 = dec.ev.stats["bootstraps"]
+        w0 = time.monotonic_ns()
         t = time.perf_counter()
         ct, states = dec.step(ar.input_for(k, selected) if ar else chain.input_embeddings[k],
                               states)
         sync()
         out["seconds"].append(time.perf_counter() - t)
+        out["windows_ns"].append([w0, time.monotonic_ns()])
         out["bootstraps"].append(dec.ev.stats["bootstraps"] - b0)
         t = time.perf_counter()
         got = dec.decrypt(ct)
@@ -725,6 +730,7 @@ def run_payload(payload_dir: str, *, tokens: int = 0, bootstrap_passes: int = 2,
         "n_layers_total": n_layers_total,
         "per_token_errors_vs_exact": errs_exact,
         "per_token_bootstraps": loop["bootstraps"],
+        "token_windows_monotonic_ns": loop["windows_ns"],
         "decrypt_seconds": loop["decrypt_seconds"],
         "token0_samples": loop["token0"],
         "level_budget": list(level_budget),
