@@ -435,7 +435,11 @@ class CKKSBootstrapper:
         factors = self.group_factors(total, len(plans), power_last)
         cts = list(cts)
         for idx, plan in enumerate(plans):
-            cts = cc.RescaleMany(cts)
+            # the degree-2 ones rescaled together (the others are used as
+            # they are, as RescaleInPlace leaves them)
+            deep = [i for i, ct in enumerate(cts) if ct.GetNoiseScaleDeg() >= 2]
+            for i, r in zip(deep, cc.RescaleMany([cts[i] for i in deep])):
+                cts[i] = r
             by_level: dict = {}
             for ct in cts:
                 by_level.setdefault(ct.GetLevel(), []).append(ct)
@@ -538,13 +542,18 @@ class CKKSBootstrapper:
         w = cc.EvalAdd(re_m, cc.MultByMonomial(im_m, N // 2))
         return self._transform(w, self.s2c, "s2c", back / gain, power_last=True)
 
-    def bootstrap_many(self, cts, pre: float = 1.0, post: float = 1.0) -> list:
+    def bootstrap_many(self, cts, pre: float = 1.0, post: float = 1.0,
+                       real_slots: bool | None = None) -> list:
         """bootstrap(ct, pre, post) of every ciphertext of `cts`, in step
         under S2C-first (each stage's key switches, rescales and EvalMod
         products of all of them share their launches; the same ciphertexts
-        as one call each); the ordinary order refreshes them in turn."""
+        as one call each); the ordinary order refreshes them in turn.
+        `real_slots` (S2C-first) overrides the setup's slot mode for this
+        call: False refreshes complex slots (two real ciphertexts packed as
+        a + i b, say) with both EvalMods."""
         cts = list(cts)
-        if len(cts) <= 1 or not self.s2c_first:
+        real = self.real_slots if real_slots is None else bool(real_slots)
+        if not self.s2c_first or (len(cts) <= 1 and real == self.real_slots):
             return [self.bootstrap(ct, pre, post) for ct in cts]
         cc, n, N = self.cc, self.n, self.N
         L = len(cc.GetModuli()[0])
@@ -569,7 +578,7 @@ class CKKSBootstrapper:
         zs = self._transform_many(raised, self.c2s, "c2s",
                                   raised[0].GetScalingFactor() / (q0 * n * 2 * K))
         zcs = cc.EvalConjugateMany(zs)
-        if self.real_slots:
+        if real:
             outs = self._eval_mod_amplitude([cc.EvalAdd(z, zc) for z, zc in zip(zs, zcs)],
                                             amp / 2)
             outs = cc.RescaleMany(outs)

@@ -1066,12 +1066,15 @@ class CryptoContext:
         return self.EvalAdd(out, fix)
 
     def EvalBootstrapMany(self, cts: Sequence["Ciphertext"], numIterations: int = 1,  # noqa: N802,N803
-                          precision: int = 0, *, scale: float = 1.0) -> list:
+                          precision: int = 0, *, scale: float = 1.0,
+                          real_slots: bool | None = None) -> list:
         """[EvalBootstrap(ct, numIterations, precision, scale=scale) for ct
         in cts] (an extension of the OpenFHE API): under S2C-first the
         ciphertexts go through every stage in step, sharing their key
         switches, rescales and EvalMod products; the same ciphertexts as
-        one call each."""
+        one call each.  `real_slots` False (S2C-first) refreshes complex
+        slots whatever the setup's mode, e.g. two real values packed as
+        a + i b."""
         boot = self._bootstrapper()
         scale = float(scale)
         if not scale > 0:
@@ -1079,13 +1082,13 @@ class CryptoContext:
         if int(numIterations) > 2:
             raise ValueError("numIterations must be 1 or 2")
         cts = list(cts)
-        outs = boot.bootstrap_many(cts, pre=1.0 / scale, post=scale)
+        outs = boot.bootstrap_many(cts, pre=1.0 / scale, post=scale, real_slots=real_slots)
         if int(numIterations) <= 1:
             return outs
         bits = int(precision) or 12
         residuals = [self.EvalSub(ct, out) for ct, out in zip(cts, outs)]
         fixes = boot.bootstrap_many(residuals, pre=2.0 ** bits / scale,
-                                    post=scale * 2.0 ** -bits)
+                                    post=scale * 2.0 ** -bits, real_slots=real_slots)
         return [self.EvalAdd(o, f) for o, f in zip(outs, fixes)]
 
 

@@ -563,9 +563,14 @@ class PackedEvaluator:
         return out
 
     def refresh_many(self, cts, bound: float, support, passes: int | None = None) -> list:
-        """refresh of every ciphertext of `cts` (one bound and support):
-        through the context's multi-ciphertext bootstrap when it has one
-        (the same ciphertexts, shared launches), else one at a time."""
+        """refresh of every ciphertext of `cts` (one bound and support)
+        through the context's multi-ciphertext bootstrap when it has one,
+        else one at a time.  Under S2C-first the (real) values go in pairs,
+        as the reference's complex state pairing does (maybe_bootstrap_pair,
+        stage1_mamba2_decode_fideslib.cpp:2298-2330): c = (a + i b) / 2, the
+        1/2 riding on the support mask, one complex-slot bootstrap per pair
+        (both EvalMods; ~1.5 real ones), then a = c + conj(c) and b = -i (c
+        - conj(c)); the pairs' stages in step."""
         cts = list(cts)
         many = getattr(self.cc, "EvalBootstrapMany", None)
         if len(cts) <= 1 or many is None:
@@ -574,13 +579,34 @@ class PackedEvaluator:
         if passes not in (1, 2):
             raise ValueError("bootstrap passes must be 1 or 2")
         t0 = time.perf_counter()
+        pair = self.s2c_first
         if isinstance(support, (int, np.integer)):
-            xs = [self.mask(ct, int(support)) if support < self.slots else ct for ct in cts]
+            if support < self.slots or pair:
+                sup = np.zeros(self.slots)
+                sup[: int(support)] = 1.0
+                xs = [self.plain(ct, sup * (0.5 if pair else 1.0), True) for ct in cts]
+            else:
+                xs = cts
         else:
-            xs = [self.plain(ct, support, True) for ct in cts]
+            xs = [self.plain(ct, np.asarray(support) * (0.5 if pair else 1.0), True)
+                  for ct in cts]
         bound = 2.0 ** math.ceil(math.log2(max(float(bound), 2.0 ** -30)))
-        outs = many(xs, passes, REFRESH_SCALE_BITS, scale=bound)
-        self.stats["bootstraps"] += passes * len(cts)
+        if not pair:
+            outs = many(xs, passes, REFRESH_SCALE_BITS, scale=bound)
+            self.stats["bootstraps"] += passes * len(cts)
+        else:
+            cc, half = self.cc, self.cc.GetRingDimension() // 2
+            packed = [cc.EvalAdd(a, cc.MultByMonomial(b, half)) for a, b in zip(xs[0::2], xs[1::2])]
+            if len(xs) % 2:
+                packed.append(xs[-1])
+            got = many(packed, passes, REFRESH_SCALE_BITS, scale=bound, real_slots=False)
+            conj = cc.EvalConjugateMany(got)
+            outs = []
+            for c, cj in zip(got, conj):
+                outs.append(cc.EvalAdd(c, cj))
+                outs.append(cc.MultByMonomial(cc.EvalSub(c, cj), 3 * half))
+            outs = outs[: len(cts)]
+            self.stats["bootstraps"] += passes * len(packed)
         self.stats["logical_refreshes"] += len(cts)
         self.stats["bootstrap_seconds"] += time.perf_counter() - t0
         return outs

@@ -168,3 +168,27 @@ def test_command_line_s2c_first(tmp_path):
     small.output(small.input(np.ones(4)))
     prog.write_text(small.text())
     assert P.main([str(prog), str(res), str(TOL), str(TOL)] + flags) == 2
+
+
+@pytest.mark.parametrize("count,support", [(3, 256), (4, 100)])
+def test_refresh_many_pairs_complex_slots(count, support):
+    """refresh_many under S2C-first packs the real values in pairs, one
+    complex-slot bootstrap each (the odd one alone), and unpacks them:
+    every value within the two-pass tolerance of one refresh each, masked
+    to the support."""
+    slots = 1 << 11
+    cc, keys = P.build_context(slots, ring_dim=1 << 12, seed=5)
+    ev = P.PackedEvaluator(cc, keys, slots, s2c_first=True, level_budget=(3, 3))
+    rng = np.random.default_rng(count)
+    xs = [rng.uniform(-3, 3, slots) for _ in range(count)]
+    cts = [ev.encrypt(x) for x in xs]
+    b0 = ev.stats["bootstraps"]
+    outs = ev.refresh_many(cts, 4.0, support, passes=2)
+    assert ev.stats["bootstraps"] - b0 == 2 * ((count + 1) // 2)
+    singles = [ev.refresh(ct, 4.0, support, passes=2) for ct in cts]
+    for x, o, s in zip(xs, outs, singles):
+        want = np.where(np.arange(slots) < support, x, 0.0)
+        got, one = ev.decrypt(o, slots), ev.decrypt(s, slots)
+        assert np.max(np.abs(got - want)) < TOL
+        assert np.max(np.abs(one - want)) < TOL
+        assert o.GetLevel() == s.GetLevel()
