@@ -367,9 +367,9 @@ def run_bootstrap(steps: int = 3, warmup: int = 2):
 REF_TOKEN_S = 396.6
 
 
-# carried tokens of one refresh cycle of the carried SSM state in the
-# N=2^16 decode: its level grows by one a token until its six groups are
-# refreshed together, every eighth carried token on this payload
+# carried tokens decoded to cover one refresh cycle of the carried SSM
+# state in the N=2^16 decode: its level grows by one a token until its six
+# groups are refreshed together, every eighth carried token on this payload
 STATE_CYCLE = 8
 
 
@@ -392,10 +392,13 @@ def run_decode(tokens: int = 1 + STATE_CYCLE, security: str = "not-set"):
     with tempfile.TemporaryDirectory() as d:
         M.synthetic_chain(d, n_layers=24, n_test_tokens=tokens, seed=13)
         rep = D.run_payload(d, seed=14, security=security, log=lambda m: None)
-    per = rep["seconds_per_token"]
+    per, passes = rep["seconds_per_token"], rep["per_token_bootstraps"]
     carried = sum(per[1:5]) / len(per[1:5]) if len(per) > 1 else None
-    cycle = (sum(per[1:1 + STATE_CYCLE]) / STATE_CYCLE
-             if len(per) > STATE_CYCLE else None)
+    # the cycle ends at the carried token that refreshes the state groups
+    # (the most bootstrap passes, more than the first carried token's)
+    end = max(range(1, len(per)), key=lambda k: passes[k], default=None)
+    cycle = (sum(per[1:end + 1]) / end
+             if end is not None and passes[end] > passes[1] else None)
     if security == "128-classic":
         a = rep["security_audit"]
         return {
@@ -420,6 +423,7 @@ def run_decode(tokens: int = 1 + STATE_CYCLE, security: str = "not-set"):
         "s_per_token_first": rep["first_token_seconds"],
         "s_per_token_carried": carried,
         "s_per_token_cycle": cycle,
+        "state_refresh_token": (end + 1) if cycle is not None else None,
         "s_per_token_all": rep["seconds_per_token"],
         "bootstrap_passes_per_token": rep["per_token_bootstraps"],
         "max_abs_err_vs_polynomial": rep["max_abs_error_vs_polynomial"],
@@ -433,8 +437,9 @@ def run_decode(tokens: int = 1 + STATE_CYCLE, security: str = "not-set"):
                      "depth 44, sparse-ternary secret (h=192) as the reference decoder's, "
                      "SlotToCoeff-first refreshes (two passes at the precision-critical "
                      "sites); first token from zero state, then carried state; carried: "
-                     "mean of tokens 2-5; cycle: mean of tokens 2-9, one refresh cycle of "
-                     "the carried state (its six groups refreshed in the last)"),
+                     "mean of tokens 2-5; cycle: mean of the carried tokens up to the one "
+                     "that refreshes the state's six groups (state_refresh_token, 1-based), "
+                     "one refresh cycle of the carried state"),
     }
 
 
