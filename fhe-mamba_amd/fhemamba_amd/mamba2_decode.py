@@ -84,12 +84,14 @@ class EncryptedMamba2Decoder:
                                   refresh_ceiling=refresh_ceiling, log=self.log,
                                   s2c_first=s2c_first, level_budget=tuple(level_budget))
         # Refresh passes by site, the reference decoder's Meta-BTS rule
-        # (should_use_meta_bts, stage1_mamba2_config.cpp:69-86): two-pass
-        # refreshes (bootstrap_passes) for the carried lineages (SSM state,
-        # the projection kept in the conv FIFO), the gated norm's polynomial
-        # input, the residual of the last three layers, the final output and
-        # every refresh inside a scheduled normalization; one pass
-        # (transient_passes) for the other transient values.
+        # (should_use_meta_bts, stage1_mamba2_config.cpp:69-86, with
+        # is_carried_checkpoint, stage1_mamba2_decode_fideslib.cpp:218-220):
+        # two-pass refreshes (bootstrap_passes) for the carried lineages
+        # (SSM state, conv-window entries refreshed out of the FIFO), the
+        # gated norm's polynomial input, the residual of the last three
+        # layers, the final output and every refresh inside a scheduled
+        # normalization; one pass (transient_passes) for the other values,
+        # the new projection among them (it enters the FIFO fresh).
         if transient_passes not in (1, 2):
             raise ValueError("transient bootstrap passes must be 1 or 2")
         self.critical_passes = bootstrap_passes
@@ -358,7 +360,7 @@ class EncryptedMamba2Decoder:
         need = max(2, self.cheb_need(lay.polys["gate_silu"]),
                    self.cheb_need(lay.polys["dt_softplus"]) + 2 if lay.joint is None
                    else self.joint_need(lay.joint))
-        proj = self.ready(proj, need, B["proj"], psup, critical=True)  # kept in the FIFO
+        proj = self.ready(proj, need, B["proj"], psup)
         # conv over the FIFO of raw proj ciphertexts (taps on the xBC slots)
         window = list(st.fifo) + [proj]
         xs = self._support(di, cd)
