@@ -99,6 +99,34 @@ def test_decoder_circuit_on_slots_meets_exporter_criterion(chain):
         assert _rel(got, chain.expected_poly_final[k]) < 1e-5, k
 
 
+def test_out_proj_diagonals_encoded_at_one_level(chain, monkeypatch):
+    """The carried state deepens the gated norm's input a level a token;
+    aligned to one level before out_proj, its diagonals are looked up at
+    that level on every token (encoded once), while the slot-level values
+    stay equal to the exporter's polynomial circuit."""
+    from fhemamba_amd import packed
+    from fhemamba_amd.mamba2_decode import EncryptedMamba2Decoder
+    from packed_builder import SlotContext, SlotKeys
+    seen: dict = {}
+    orig = packed.PlaintextCache.get
+
+    def get(self, key):
+        if isinstance(key, tuple) and len(key) == 3 and key[1] == "replicated":
+            seen.setdefault(key[0][0], set()).add(key[2])
+        return orig(self, key)
+
+    monkeypatch.setattr(packed.PlaintextCache, "get", get)
+    dec = EncryptedMamba2Decoder(SlotContext(1024), SlotKeys(), chain)
+    states = dec.initial_states()
+    state_levels = []
+    for k, e in enumerate(chain.input_embeddings):
+        ct, states = dec.step(e, states)
+        state_levels.append(max(s.ssm[0].GetLevel() for s in states if s.ssm))
+        assert _rel(dec.decrypt(ct), chain.expected_poly_final[k]) < 1e-5, k
+    assert len(chain.input_embeddings) >= 2 and len(set(state_levels)) > 1
+    assert seen["out_proj"] == {dec.ev.refresh_ceiling - 4}
+
+
 # ------------------------------------------------------------- variants
 SCHED = os.path.join(os.path.dirname(__file__), "golden", "m2_chain_tiny_sched")
 JOINT = os.path.join(os.path.dirname(__file__), "golden", "m2_chain_tiny_joint")
