@@ -292,6 +292,25 @@ class SlotContext:
         self.bootstraps += passes
         return SlotCt(ct.z, self.boot_depth - getattr(self, "boot_s2c_levels", 0), 1)
 
+    def EvalBootstrapMany(self, cts, passes=1, precision=0, *, scale=1.0,  # noqa: N802
+                          real_slots=None):
+        self.bootstrap_many_calls = getattr(self, "bootstrap_many_calls", []) + [len(cts)]
+        outs = [self.EvalBootstrap(ct, passes, precision, scale=scale) for ct in cts]
+        if real_slots is None or real_slots:
+            for o in outs:
+                o.z = o.z.real.astype(complex)
+        return outs
+
+    def MultByMonomial(self, a, power):  # noqa: N802
+        # X^(N/2) multiplies every slot by i, X^(3N/2) by -i (N = self.n)
+        p = int(power) % (2 * self.n)
+        if p not in (self.n // 2, 3 * self.n // 2):
+            raise NotImplementedError("slot stand-in: only X^(N/2) and X^(3N/2)")
+        return SlotCt(a.z * (1j if p == self.n // 2 else -1j), a.level, a.deg)
+
+    def EvalConjugateMany(self, cts):  # noqa: N802
+        return [SlotCt(np.conj(c.z), c.level, c.deg) for c in cts]
+
 
 class _SlotPlain:
     def __init__(self, z):

@@ -341,3 +341,29 @@ def test_plaintext_cache_budget_follows_free_device_memory(monkeypatch, free_gib
     monkeypatch.setattr(_lib, "device_free_bytes", free)
     assert P.default_pt_cache_bytes(3) == want
     assert seen == [3]
+
+
+@pytest.mark.parametrize("count,support", [(2, 64), (5, 40), (6, None)])
+def test_refresh_many_packs_pairs(count, support):
+    """refresh_many under S2C-first on the slot-level stand-in: the values
+    go in complex pairs, (a + i b) / 2 with the 1/2 on the support mask,
+    one complex-slot bootstrap each (the odd one alone), and come back as
+    the masked values themselves, at the bootstrap's output level; the
+    ordinary order refreshes them one real bootstrap each."""
+    slots = 64
+    rng = np.random.default_rng(count)
+    vals = [rng.uniform(-3, 3, slots) for _ in range(count)]
+    for s2c_first in (True, False):
+        cc = SlotContext(slots)
+        ev = P.PackedEvaluator(cc, SlotKeys(), slots, s2c_first=s2c_first)
+        cts = [ev.encrypt(v) for v in vals]
+        sup = slots if support is None else support
+        outs = ev.refresh_many(cts, 4.0, sup, passes=2)
+        assert len(outs) == count
+        want_calls = [(count + 1) // 2] if s2c_first else [count]
+        assert cc.bootstrap_many_calls == want_calls
+        assert ev.stats["bootstraps"] == 2 * want_calls[0]
+        for v, o in zip(vals, outs):
+            want = np.where(np.arange(slots) < sup, v, 0.0)
+            assert np.allclose(o.z, want, atol=1e-12)
+            assert o.GetLevel() == outs[0].GetLevel()
