@@ -279,6 +279,7 @@ Context::~Context() {
     hipFree(pl->d_qhat_inv);
     hipFree(pl->d_src_scale);
     hipFree(pl->d_qhat_mont);
+    hipFree(pl->d_qhat_mont30);
     hipFree(pl->d_dst_idx);
     hipFree(pl->d_src_idx32);
   }
@@ -306,6 +307,7 @@ ConvPlan* Context::build_plan(const std::vector<uint32_t>& src, const std::vecto
   pl->src_idx = src;
   pl->dst_idx = dst;
   std::vector<uint64_t> qhat_inv(2 * src.size()), qhat_mont(src.size() * dst.size());
+  std::vector<uint64_t> qhat_mont30(src.size() * dst.size());
   std::vector<uint64_t> src_scale(2 * src.size());
   for (size_t a = 0; a < src.size(); ++a) {
     const uint64_t qa = mods[src[a]];
@@ -325,10 +327,13 @@ ConvPlan* Context::build_plan(const std::vector<uint32_t>& src, const std::vecto
         if (b != a) hk = host_mulmod(hk, mods[src[b]] % t, t);
       if (factor) hk = host_mulmod(hk, (*factor)[k] % t, t);
       qhat_mont[a * dst.size() + k] = host_to_mont(hk, t);
+      qhat_mont30[a * dst.size() + k] =
+          host_mulmod(qhat_mont[a * dst.size() + k], (1ull << 30) % t, t);
     }
   }
   pl->d_qhat_inv = upload(qhat_inv);
   pl->d_qhat_mont = upload(qhat_mont);
+  pl->d_qhat_mont30 = upload(qhat_mont30);
   pl->d_src_scale = upload(src_scale);
   pl->d_dst_idx = upload(dst);
   pl->d_src_idx32 = upload(src);

@@ -83,6 +83,7 @@ struct ConvPlan {
   // inverse NTT's scaling folded in, for conversions fused after a transform.
   uint64_t* d_src_scale = nullptr;         // [nsrc][2]
   uint64_t* d_qhat_mont = nullptr;         // [nsrc][ndst]
+  uint64_t* d_qhat_mont30 = nullptr;       // [nsrc][ndst]: qhat_mont * 2^30 mod t_k
   uint32_t* d_dst_idx = nullptr;           // [ndst]
   uint32_t* d_src_idx32 = nullptr;         // [nsrc]
 };

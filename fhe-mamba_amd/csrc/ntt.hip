@@ -1204,6 +1204,7 @@ constexpr int MID_MAXPLAN = 8;
 struct MidPlan {
   const uint64_t* src_scale;  // [nsrc][2]: [Q/q_t]^-1 N^-1 mod q_t (Shoup)
   const uint64_t* qhat_mont;  // [nsrc][ndst], Montgomery form w.r.t. the target
+  const uint64_t* qhat_mont30;  // [nsrc][ndst], qhat_mont * 2^30 mod the target
   uint32_t nsrc, ndst, src_mod0, src_limb0, skip_at, skip_len, qlimbs;
 };
 struct MidArgs {
@@ -1244,6 +1245,7 @@ __device__ __forceinline__ void convert_mid_body(const MidArgs& a, const ModCons
   typedef const uint64_t __attribute__((address_space(4))) cu64;
   cu64* const src_scale = (cu64*)pl.src_scale;
   cu64* const qhat_mont = (cu64*)pl.qhat_mont;
+  cu64* const qhat_mont30 = (cu64*)pl.qhat_mont30;
   uint64_t* const src = lds_dyn;
   uint64_t* const work = lds_dyn + (size_t)K * PITCH;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1315,35 +1317,73 @@ __device__ __forceinline__ void convert_mid_body(const MidArgs& a, const ModCons
     {
       // First forward window (bits S1-RHO .. S1-1): rows thi | v << w | tlo.
       constexpr int w = S1 - RHO;
+      // With w >= 4 the row fields do not interact with the u / 16 padding:
+      // lds_idx(thi | v << w | tlo) = lds_idx(thi | tlo) + v * VSTEP, so one
+      // address register serves a source line's R reads (immediate offsets).
+      static_assert(w >= 4, "padding split");
+      constexpr uint32_t VSTEP = (1u << w) + (1u << (w - 4));
       const uint32_t thi = (tau >> w) << (w + RHO), tlo = tau & ((1u << w) - 1);
-      uint64_t a0[R], a1a[R], a1b[R], a2[R];
+      const uint64_t* const sbase = src + lds_idx(0, thi | tlo, 0);
+      if (K <= 8) {
+        // Up to eight sources: with c = cl + ch 2^30 and c' = c 2^30 mod t
+        // = dl + dh 2^30 (both tables in Montgomery form), v c == vl c + vh c'
+        // (mod t), so b0 = sum vl cl + vh dl and b1 = sum vl ch + vh dh (each
+        // below 2K 2^60 <= 2^64) give T = b0 + b1 2^30 == sum v c with
+        // T >> 64 <= 2^30 < t.
+        uint64_t b0[R], b1[R];
 #pragma unroll
-      for (int v = 0; v < R; ++v) a0[v] = a1a[v] = a1b[v] = a2[v] = 0;
-      for (uint32_t i = 0; i < K; ++i) {
-        const uint64_t cv = qhat_mont[(size_t)i * nq + k];
-        const uint32_t cl = (uint32_t)cv & M30, ch = (uint32_t)(cv >> 30);
-        const uint64_t* sl = src + (size_t)i * PITCH;
+        for (int v = 0; v < R; ++v) b0[v] = b1[v] = 0;
+        for (uint32_t i = 0; i < K; ++i) {
+          const uint64_t cv = qhat_mont[(size_t)i * nq + k];
+          const uint64_t dv = qhat_mont30[(size_t)i * nq + k];
+          const uint32_t cl = (uint32_t)cv & M30, ch = (uint32_t)(cv >> 30);
+          const uint32_t dl = (uint32_t)dv & M30, dh = (uint32_t)(dv >> 30);
+          const uint64_t* sl = sbase + (size_t)i * PITCH;
+#pragma unroll
+          for (int v = 0; v < R; ++v) {
+            const uint64_t sv = sl[v * VSTEP];
+            const uint32_t vl = (uint32_t)sv, vh = (uint32_t)(sv >> 32);
+            b0[v] += (uint64_t)vl * cl + (uint64_t)vh * dl;
+            b1[v] += (uint64_t)vl * ch + (uint64_t)vh * dh;
+          }
+        }
 #pragma unroll
         for (int v = 0; v < R; ++v) {
-          const uint64_t sv = sl[lds_idx(0, thi | ((uint32_t)v << w) | tlo, 0)];
-          const uint32_t vl = (uint32_t)sv, vh = (uint32_t)(sv >> 32);
-          a0[v] += (uint64_t)vl * cl;
-          a1a[v] += (uint64_t)vl * ch;
-          a1b[v] += (uint64_t)vh * cl;
-          a2[v] += (uint64_t)vh * ch;
+          const uint64_t m = b1[v] << 30;
+          const uint64_t lo = b0[v] + m;
+          const uint64_t hh = (b1[v] >> 34) + (lo < m);
+          x[v] = redc_lazy(hh, lo, q, qn);  // (0, 2q)
         }
-      }
+      } else {
+        uint64_t a0[R], a1a[R], a1b[R], a2[R];
 #pragma unroll
-      for (int v = 0; v < R; ++v) {
-        // T = a0 + (a1a + a1b) 2^30 + a2 2^60 < K 2^60 q <= q 2^64.
-        const uint64_t s1 = a1a[v] + a1b[v];
-        const uint64_t c1 = s1 < a1a[v];
-        const uint64_t m1 = s1 << 30, m2 = a2[v] << 60;
-        const uint64_t lo = a0[v] + m1;
-        uint64_t hh = (s1 >> 34) + (c1 << 30) + (a2[v] >> 4) + (lo < m1);
-        const uint64_t lo2 = lo + m2;
-        hh += lo2 < m2;
-        x[v] = redc_lazy(hh, lo2, q, qn);  // (0, 2q)
+        for (int v = 0; v < R; ++v) a0[v] = a1a[v] = a1b[v] = a2[v] = 0;
+        for (uint32_t i = 0; i < K; ++i) {
+          const uint64_t cv = qhat_mont[(size_t)i * nq + k];
+          const uint32_t cl = (uint32_t)cv & M30, ch = (uint32_t)(cv >> 30);
+          const uint64_t* sl = sbase + (size_t)i * PITCH;
+#pragma unroll
+          for (int v = 0; v < R; ++v) {
+            const uint64_t sv = sl[v * VSTEP];
+            const uint32_t vl = (uint32_t)sv, vh = (uint32_t)(sv >> 32);
+            a0[v] += (uint64_t)vl * cl;
+            a1a[v] += (uint64_t)vl * ch;
+            a1b[v] += (uint64_t)vh * cl;
+            a2[v] += (uint64_t)vh * ch;
+          }
+        }
+#pragma unroll
+        for (int v = 0; v < R; ++v) {
+          // T = a0 + (a1a + a1b) 2^30 + a2 2^60 < K 2^60 q <= q 2^64.
+          const uint64_t s1 = a1a[v] + a1b[v];
+          const uint64_t c1 = s1 < a1a[v];
+          const uint64_t m1 = s1 << 30, m2 = a2[v] << 60;
+          const uint64_t lo = a0[v] + m1;
+          uint64_t hh = (s1 >> 34) + (c1 << 30) + (a2[v] >> 4) + (lo < m1);
+          const uint64_t lo2 = lo + m2;
+          hh += lo2 < m2;
+          x[v] = redc_lazy(hh, lo2, q, qn);  // (0, 2q)
+        }
       }
     }
 #pragma unroll
@@ -1557,7 +1597,7 @@ MidPlan mid_plan(const Context& c, const ConvPlan& pl, uint32_t src_mod0, uint32
     if (pl.dst_idx[k] != (pos < qlimbs ? pos : c.L + (pos - qlimbs)))
       throw ArgError("conversion plan target order");
   }
-  return MidPlan{pl.d_src_scale, pl.d_qhat_mont, pl.nsrc, pl.ndst,
+  return MidPlan{pl.d_src_scale, pl.d_qhat_mont, pl.d_qhat_mont30, pl.nsrc, pl.ndst,
                  src_mod0, src_limb0, skip_at, skip_len, qlimbs};
 }
 
