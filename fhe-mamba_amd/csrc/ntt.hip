@@ -1215,6 +1215,48 @@ struct MidArgs {
   uint32_t nplan, L;
 };
 
+// One group of at most eight conversion sources i0 .. i1 - 1 for target k:
+// T_g = t + u 2^64 == sum_i v_i c_ik (mod t_k), from sources held as 30-bit
+// halves (vl, vh) and the Montgomery-form tables c and c' = c 2^30 mod t_k
+// split into 30-bit halves: v c == vl c + vh c', so b0 = sum vl cl + vh dl
+// and b1 = sum vl ch + vh dh (each below 16 2^60 = 2^64) give T_g = b0 +
+// b1 2^30, whose high word u is at most 2^30.
+template <int R, uint32_t VSTEP, uint32_t PITCH, class CU64>
+__device__ __forceinline__ void conv_group(const uint64_t* sbase, CU64* qhat_mont,
+                                           CU64* qhat_mont30, uint32_t nq, uint32_t k,
+                                           uint32_t i0, uint32_t i1, uint64_t (&t)[R],
+                                           uint64_t (&u)[R]) {
+  constexpr uint32_t M30 = (1u << 30) - 1;
+  uint64_t b0[R], b1[R];
+#pragma unroll
+  for (int v = 0; v < R; ++v) b0[v] = b1[v] = 0;
+  for (uint32_t i = i0; i < i1; ++i) {
+    const uint64_t cv = qhat_mont[(size_t)i * nq + k];
+    const uint64_t dv = qhat_mont30[(size_t)i * nq + k];
+    const uint64_t* sl = sbase + (size_t)i * PITCH;
+    uint64_t sv[R];
+#pragma unroll
+    for (int v = 0; v < R; ++v) sv[v] = sl[v * VSTEP];
+    // the constants' and all R elements' reads in flight before the first
+    // product: one wait a source
+    __builtin_amdgcn_sched_barrier(0);
+    const uint32_t cl = (uint32_t)cv & M30, ch = (uint32_t)(cv >> 30);
+    const uint32_t dl = (uint32_t)dv & M30, dh = (uint32_t)(dv >> 30);
+#pragma unroll
+    for (int v = 0; v < R; ++v) {
+      const uint32_t vl = (uint32_t)sv[v], vh = (uint32_t)(sv[v] >> 32);
+      b0[v] += (uint64_t)vl * cl + (uint64_t)vh * dl;
+      b1[v] += (uint64_t)vl * ch + (uint64_t)vh * dh;
+    }
+  }
+#pragma unroll
+  for (int v = 0; v < R; ++v) {
+    const uint64_t m = b1[v] << 30;
+    t[v] = b0[v] + m;
+    u[v] = (b1[v] >> 34) + (t[v] < m);
+  }
+}
+
 // ALT: the forward column stages use the alternating lazy range of the
 // paired ModDown epilogue (a stage whose global index g has logN - 1 - g
 // even first brings X below 8q; values stay below 16q), and the output may
@@ -1324,67 +1366,22 @@ __device__ __forceinline__ void convert_mid_body(const MidArgs& a, const ModCons
       constexpr uint32_t VSTEP = (1u << w) + (1u << (w - 4));
       const uint32_t thi = (tau >> w) << (w + RHO), tlo = tau & ((1u << w) - 1);
       const uint64_t* const sbase = src + lds_idx(0, thi | tlo, 0);
-      if (K <= 8) {
-        // Up to eight sources: with c = cl + ch 2^30 and c' = c 2^30 mod t
-        // = dl + dh 2^30 (both tables in Montgomery form), v c == vl c + vh c'
-        // (mod t), so b0 = sum vl cl + vh dl and b1 = sum vl ch + vh dh (each
-        // below 2K 2^60 <= 2^64) give T = b0 + b1 2^30 == sum v c with
-        // T >> 64 <= 2^30 < t.
-        uint64_t b0[R], b1[R];
-#pragma unroll
-        for (int v = 0; v < R; ++v) b0[v] = b1[v] = 0;
-        for (uint32_t i = 0; i < K; ++i) {
-          const uint64_t cv = qhat_mont[(size_t)i * nq + k];
-          const uint64_t dv = qhat_mont30[(size_t)i * nq + k];
-          const uint32_t cl = (uint32_t)cv & M30, ch = (uint32_t)(cv >> 30);
-          const uint32_t dl = (uint32_t)dv & M30, dh = (uint32_t)(dv >> 30);
-          const uint64_t* sl = sbase + (size_t)i * PITCH;
-#pragma unroll
-          for (int v = 0; v < R; ++v) {
-            const uint64_t sv = sl[v * VSTEP];
-            const uint32_t vl = (uint32_t)sv, vh = (uint32_t)(sv >> 32);
-            b0[v] += (uint64_t)vl * cl + (uint64_t)vh * dl;
-            b1[v] += (uint64_t)vl * ch + (uint64_t)vh * dh;
-          }
-        }
+      // Sources in groups of at most eight (conv_group); the groups' sum T
+      // (K <= 16: T >> 64 < 2^32 < t) takes one Montgomery reduction.
+      uint64_t tl[R], th[R];  // T = tl + th 2^64
+      const uint32_t k1 = K < 8 ? K : 8;
+      conv_group<R, VSTEP, PITCH>(sbase, qhat_mont, qhat_mont30, nq, k, 0, k1, tl, th);
+      if (K > 8) {
+        uint64_t t2[R], u2[R];
+        conv_group<R, VSTEP, PITCH>(sbase, qhat_mont, qhat_mont30, nq, k, 8, K, t2, u2);
 #pragma unroll
         for (int v = 0; v < R; ++v) {
-          const uint64_t m = b1[v] << 30;
-          const uint64_t lo = b0[v] + m;
-          const uint64_t hh = (b1[v] >> 34) + (lo < m);
-          x[v] = redc_lazy(hh, lo, q, qn);  // (0, 2q)
-        }
-      } else {
-        uint64_t a0[R], a1a[R], a1b[R], a2[R];
-#pragma unroll
-        for (int v = 0; v < R; ++v) a0[v] = a1a[v] = a1b[v] = a2[v] = 0;
-        for (uint32_t i = 0; i < K; ++i) {
-          const uint64_t cv = qhat_mont[(size_t)i * nq + k];
-          const uint32_t cl = (uint32_t)cv & M30, ch = (uint32_t)(cv >> 30);
-          const uint64_t* sl = sbase + (size_t)i * PITCH;
-#pragma unroll
-          for (int v = 0; v < R; ++v) {
-            const uint64_t sv = sl[v * VSTEP];
-            const uint32_t vl = (uint32_t)sv, vh = (uint32_t)(sv >> 32);
-            a0[v] += (uint64_t)vl * cl;
-            a1a[v] += (uint64_t)vl * ch;
-            a1b[v] += (uint64_t)vh * cl;
-            a2[v] += (uint64_t)vh * ch;
-          }
-        }
-#pragma unroll
-        for (int v = 0; v < R; ++v) {
-          // T = a0 + (a1a + a1b) 2^30 + a2 2^60 < K 2^60 q <= q 2^64.
-          const uint64_t s1 = a1a[v] + a1b[v];
-          const uint64_t c1 = s1 < a1a[v];
-          const uint64_t m1 = s1 << 30, m2 = a2[v] << 60;
-          const uint64_t lo = a0[v] + m1;
-          uint64_t hh = (s1 >> 34) + (c1 << 30) + (a2[v] >> 4) + (lo < m1);
-          const uint64_t lo2 = lo + m2;
-          hh += lo2 < m2;
-          x[v] = redc_lazy(hh, lo2, q, qn);  // (0, 2q)
+          tl[v] += t2[v];
+          th[v] += u2[v] + (tl[v] < t2[v]);
         }
       }
+#pragma unroll
+      for (int v = 0; v < R; ++v) x[v] = redc_lazy(th[v], tl[v], q, qn);  // (0, 2q)
     }
 #pragma unroll
     for (int sp = 0; sp < NSP; ++sp) {
