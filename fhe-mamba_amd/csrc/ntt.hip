@@ -1572,11 +1572,19 @@ size_t mid_lds_bytes(uint32_t K) {
 
 // Launches with fewer (poly, column) tiles than this use 8-wave workgroups.
 constexpr uint32_t MID_SMALL_TILES = 4096;
+// Launches of at most this many tiles (one ciphertext's ModUp or ModDown)
+// use 16-wave workgroups.
+constexpr uint32_t MID_TINY_TILES = 1024;
 
 template <int S1, int S2, bool ALT = false>
 void launch_mid(Context& c, const char* name, const MidArgs& a, uint32_t npoly,
                 uint32_t max_src) {
   const uint32_t tiles = npoly << S2;
+  if (tiles <= MID_TINY_TILES && mid_lds_bytes<S1, 16>(max_src) <= c.lds_per_block) {
+    FHE_LAUNCH(c, name, (k_convert_mid<S1, S2, 16, ALT>), dim3(tiles), dim3(1024),
+               (mid_lds_bytes<S1, 16>(max_src)), a, c.d_const, c.d_tw_inv, c.d_tw_fwd);
+    return;
+  }
   if (tiles < MID_SMALL_TILES && mid_lds_bytes<S1, 8>(max_src) <= c.lds_per_block) {
     FHE_LAUNCH(c, name, (k_convert_mid<S1, S2, 8, ALT>), dim3(tiles), dim3(512),
                (mid_lds_bytes<S1, 8>(max_src)), a, c.d_const, c.d_tw_inv, c.d_tw_fwd);
