@@ -45,15 +45,15 @@ HBM_PEAK = 8.0e12  # B/s, MI355X HBM3E
 # hash of the kernel sources they were measured on.  A build from other
 # sources reports traffic as null.
 MEASURED_TRAFFIC = {
-    "csrc_sha16": "891213916f290d02",
+    "csrc_sha16": "2b29c5201ab30a84",
     "kernels": {
         # 30-rotation batch launches of the rotation step
-        "ntt_fwd_blocks_moddown": 3_096_645_606 + 754_974_720,
-        "k_moddown_mid": 253_259_008 + 758_866_778,
-        "ntt_inv_blocks_ksk": 776_263_962 + 251_658_240,
+        "ntt_fwd_blocks_moddown": 3_096_788_838 + 754_974_720,
+        "k_moddown_mid": 253_284_736 + 760_415_219,
+        "ntt_inv_blocks_ksk": 776_258_995 + 251_658_240,
         # NTT batch (64 ciphertexts x 2 polys x 24 limbs): one pass, and the MAC
-        "ntt_pass": 1_636_238_669 + 1_610_612_736,
-        "k_mac": 2_416_047_411 + 25_165_824,
+        "ntt_pass": 1_636_304_717 + 1_610_612_736,
+        "k_mac": 2_416_048_077 + 25_165_824,
     },
 }
 

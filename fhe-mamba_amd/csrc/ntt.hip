@@ -865,7 +865,7 @@ __device__ __forceinline__ void moddown_pair_body(const uint64_t* __restrict__ y
 
 template <int S, int ND>
 __global__ void __launch_bounds__(512)
-    __attribute__((amdgpu_waves_per_eu(ND <= 3 && S >= 7 ? 6 : 1, 8)))
+    __attribute__((amdgpu_waves_per_eu(ND <= 3 && S >= 7 ? 6 : ND == 4 && S >= 7 ? 8 : 1, 8)))
     ntt_pass_moddown_pair(const uint64_t* __restrict__ y, const ModConst* __restrict__ mc,
                           const uint64_t* __restrict__ tw_all, uint32_t log_n, uint32_t s_other,
                           const ModDownEpi e) {
@@ -997,7 +997,7 @@ __device__ __forceinline__ void ksk_pair_body(uint64_t* __restrict__ ext, size_t
 
 template <int S, int ND>
 __global__ void __launch_bounds__(512)
-    __attribute__((amdgpu_waves_per_eu(ND <= 3 ? 8 : 1, 8)))
+    __attribute__((amdgpu_waves_per_eu(ND <= 4 ? 8 : 1, 8)))
     ntt_pass_ksk_pair(uint64_t* __restrict__ ext, size_t ps, const ModConst* __restrict__ mc,
                       const uint64_t* __restrict__ tw_all, uint32_t log_n, uint32_t s_other,
                       const ModDownEpi e) {
