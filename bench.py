@@ -45,15 +45,15 @@ HBM_PEAK = 8.0e12  # B/s, MI355X HBM3E
 # hash of the kernel sources they were measured on.  A build from other
 # sources reports traffic as null.
 MEASURED_TRAFFIC = {
-    "csrc_sha16": "2b29c5201ab30a84",
+    "csrc_sha16": "6ad08020f8f65fc1",
     "kernels": {
         # 30-rotation batch launches of the rotation step
-        "ntt_fwd_blocks_moddown": 3_096_788_838 + 754_974_720,
-        "k_moddown_mid": 253_284_736 + 760_415_219,
-        "ntt_inv_blocks_ksk": 776_258_995 + 251_658_240,
+        "ntt_fwd_blocks_moddown": 3_096_902_938 + 754_974_720,
+        "k_moddown_mid": 253_253_914 + 758_124_698,
+        "ntt_inv_blocks_ksk": 776_259_507 + 251_658_240,
         # NTT batch (64 ciphertexts x 2 polys x 24 limbs): one pass, and the MAC
-        "ntt_pass": 1_636_304_717 + 1_610_612_736,
-        "k_mac": 2_416_048_077 + 25_165_824,
+        "ntt_pass": 1_636_265_370 + 1_610_612_736,
+        "k_mac": 2_416_048_000 + 25_165_824,
     },
 }
 

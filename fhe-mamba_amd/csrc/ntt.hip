@@ -1007,6 +1007,9 @@ __global__ void __launch_bounds__(512)
 }
 
 // ---- Rescale in four launches (ring dimensions 2^13 .. 2^17) ----
+// The three rescale passes run radix 8 (RHO_EPILOGUE: eight lines of 2^S
+// words, 17 KB of LDS and ~60 VGPRs per 256-lane workgroup), so one
+// ciphertext's launch fits the chip in one round of workgroups.
 // The inverse NTT of the last limb reads it from the input (LastLimbLoad);
 // the forward column pass lifts it to modulus i as it loads (LiftLoad:
 // x mod q_i, minus q_l mod q_i in the upper half, the centred lift); the
@@ -1078,7 +1081,7 @@ __global__ void __launch_bounds__(256)
     ntt_pass_rescale_in(uint64_t* __restrict__ last, const ModConst* __restrict__ mc,
                         const uint64_t* __restrict__ tw_all, uint32_t log_n, uint32_t s_other,
                         const RescalePtrs ptrs, uint32_t npoly, size_t poly_words, uint32_t l) {
-  ntt_body<S, BLOCKS, true, RHO_PLAIN, PlainStore, LastLimbLoad>(
+  ntt_body<S, BLOCKS, true, RHO_EPILOGUE, PlainStore, LastLimbLoad>(
       last, (size_t)1 << log_n, mc, tw_all, log_n, LimbMap::contiguous(l), s_other, 0,
       PlainStore{}, LastLimbLoad{ptrs.a, npoly, poly_words, (size_t)l << log_n});
 }
@@ -1088,7 +1091,7 @@ __global__ void __launch_bounds__(256)
     ntt_pass_rescale_lift(uint64_t* __restrict__ t, size_t poly_stride,
                           const ModConst* __restrict__ mc, const uint64_t* __restrict__ tw_all,
                           uint32_t log_n, uint32_t s_other, const LiftLoad ld) {
-  ntt_body<S, COLS, false, RHO_PLAIN, PlainStore, LiftLoad>(
+  ntt_body<S, COLS, false, RHO_EPILOGUE, PlainStore, LiftLoad>(
       t, poly_stride, mc, tw_all, log_n, LimbMap::contiguous(0), s_other, 0, PlainStore{}, ld);
 }
 
@@ -1099,7 +1102,7 @@ __global__ void __launch_bounds__(256)
                          uint32_t log_n, uint32_t s_other, const RescalePtrs ptrs,
                          const uint64_t* __restrict__ rs, uint32_t l, uint32_t L,
                          uint32_t npoly) {
-  ntt_body<S, BLOCKS, false, RHO_PLAIN, RescaleStore>(
+  ntt_body<S, BLOCKS, false, RHO_EPILOGUE, RescaleStore>(
       t, poly_stride, mc, tw_all, log_n, LimbMap::contiguous(0), s_other, 1,
       RescaleStore{ptrs.a, ptrs.out, rs, 1u << log_n, l, L, npoly});
 }
@@ -1703,8 +1706,8 @@ static void rescale_launch(Context& c, uint64_t* const* outs, const uint64_t* co
   switch (c.log_n) {
 #define CASE(LN, A, B)                                                                        \
   case LN: {                                                                                  \
-    using GB = Geo<B, RHO_PLAIN>;                                                             \
-    using GA = Geo<A, RHO_PLAIN>;                                                             \
+    using GB = Geo<B, RHO_EPILOGUE>;                                                          \
+    using GA = Geo<A, RHO_EPILOGUE>;                                                          \
     const uint32_t tb = (1u << s1) / (256 / GB::TPL), ta = (1u << s2) / (256 / GA::TPL);      \
     FHE_LAUNCH(c, "ntt_inv_blocks_rescale", (ntt_pass_rescale_in<B>), dim3(tb, np, 1),        \
                dim3(256), 0, last.p, c.d_const, c.d_tw_inv, c.log_n, s1, ptrs, npoly,         \
