@@ -45,15 +45,15 @@ HBM_PEAK = 8.0e12  # B/s, MI355X HBM3E
 # hash of the kernel sources they were measured on.  A build from other
 # sources reports traffic as null.
 MEASURED_TRAFFIC = {
-    "csrc_sha16": "6ad08020f8f65fc1",
+    "csrc_sha16": "d4c33860f0b17125",
     "kernels": {
         # 30-rotation batch launches of the rotation step
-        "ntt_fwd_blocks_moddown": 3_096_902_938 + 754_974_720,
-        "k_moddown_mid": 253_253_914 + 758_124_698,
-        "ntt_inv_blocks_ksk": 776_259_507 + 251_658_240,
+        "ntt_fwd_blocks_moddown": 3_096_629_069 + 754_974_720,
+        "k_moddown_mid": 253_267_354 + 758_981_414,
+        "ntt_inv_blocks_ksk": 776_270_925 + 251_658_240,
         # NTT batch (64 ciphertexts x 2 polys x 24 limbs): one pass, and the MAC
-        "ntt_pass": 1_636_265_370 + 1_610_612_736,
-        "k_mac": 2_416_048_000 + 25_165_824,
+        "ntt_pass": 1_636_261_914 + 1_610_612_736,
+        "k_mac": 2_416_047_309 + 25_165_824,
     },
 }
 
@@ -954,7 +954,7 @@ def step_kernel_bytes(L: int, K: int, R: int) -> dict:
         "k_moddown_mid": R * (2 * K + 2 * L),
         "ntt_fwd_blocks_moddown": DNUM * L + L + R * (2 * L + DNUM * 2 * L + 2 * L),
         "ntt_inv_blocks_rescale": 4,
-        "ntt_inv_cols": 4,
+        "ntt_inv_cols_rescale": 4,
         "ntt_fwd_cols_rescale": 2 + 2 * (L - 1),
         "ntt_fwd_blocks_rescale": 6 * (L - 1),
     }.items()}

@@ -1007,7 +1007,7 @@ __global__ void __launch_bounds__(512)
 }
 
 // ---- Rescale in four launches (ring dimensions 2^13 .. 2^17) ----
-// The three rescale passes run radix 8 (RHO_EPILOGUE: eight lines of 2^S
+// The rescale's passes run radix 8 (RHO_EPILOGUE: eight lines of 2^S
 // words, 17 KB of LDS and ~60 VGPRs per 256-lane workgroup), so one
 // ciphertext's launch fits the chip in one round of workgroups.
 // The inverse NTT of the last limb reads it from the input (LastLimbLoad);
@@ -1105,6 +1105,17 @@ __global__ void __launch_bounds__(256)
   ntt_body<S, BLOCKS, false, RHO_EPILOGUE, RescaleStore>(
       t, poly_stride, mc, tw_all, log_n, LimbMap::contiguous(0), s_other, 1,
       RescaleStore{ptrs.a, ptrs.out, rs, 1u << log_n, l, L, npoly});
+}
+
+// The rescale's inverse column pass over the last limb (radix 8, as the
+// other rescale passes): launch poly y's single limb, modulus l.
+template <int S>
+__global__ void __launch_bounds__(256)
+    ntt_pass_rescale_cols(uint64_t* __restrict__ data, size_t poly_stride,
+                          const ModConst* __restrict__ mc, const uint64_t* __restrict__ tw_all,
+                          uint32_t log_n, uint32_t s_other, uint32_t l) {
+  ntt_body<S, COLS, true, RHO_EPILOGUE, PlainStore, PlainLoad, LimbMap>(
+      data, poly_stride, mc, tw_all, log_n, LimbMap::contiguous(l), s_other, 1, PlainStore{});
 }
 
 // ModUp input: limb blockIdx.z of ciphertext blockIdx.y's c1, read from the
@@ -1712,7 +1723,8 @@ static void rescale_launch(Context& c, uint64_t* const* outs, const uint64_t* co
     FHE_LAUNCH(c, "ntt_inv_blocks_rescale", (ntt_pass_rescale_in<B>), dim3(tb, np, 1),        \
                dim3(256), 0, last.p, c.d_const, c.d_tw_inv, c.log_n, s1, ptrs, npoly,         \
                (size_t)nq * n, l);                                                            \
-    launch_cols<true>(c, s1, s2, last.p, np, n, 1, LimbMap::contiguous(l), true);             \
+    FHE_LAUNCH(c, "ntt_inv_cols_rescale", (ntt_pass_rescale_cols<A>), dim3(ta, np, 1),      \
+               dim3(256), 0, last.p, (size_t)n, c.d_const, c.d_tw_inv, c.log_n, s2, l);   \
     FHE_LAUNCH(c, "ntt_fwd_cols_rescale", (ntt_pass_rescale_lift<A>), dim3(ta, np, l),        \
                dim3(256), 0, t.p, (size_t)l * n, c.d_const, c.d_tw_fwd, c.log_n, s2, lift);   \
     FHE_LAUNCH(c, "ntt_fwd_blocks_rescale", (ntt_pass_rescale_out<B>), dim3(tb, np, l),       \
