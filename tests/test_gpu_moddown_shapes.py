@@ -214,3 +214,36 @@ def test_classical128_chain_key_switch():
         for out, k, g in zip(outs, gkeys, gal):
             assert np.array_equal(out.numpy(), orc.rotate(ct, k, g)), (nq, g)
     ctx.close()
+
+
+def test_decode_chain_conversion_groups():
+    """The decode's N=2^16 chain (45 Q + 15 P primes, dnum 3), whose
+    conversions have 15 sources (two groups of at most eight), word for word
+    against the oracle in each middle-kernel launch shape: a relinearisation
+    key switch (one ciphertext: 16-wave workgroups), 3 hoisted rotations
+    (8-wave) and 9 (4-wave), at 45 limbs and at 20 (ModUp digits of 15 and 5
+    sources)."""
+    q, p = O.gen_moduli(16, 44, 59, 60, 3)
+    print(f"[decode chain] N=2^16 Q={len(q)} P={len(p)} dnum=3", flush=True)
+    ctx, orc = F.Context(16, q, p, 3, sampling="seeded"), O.Ctx(16, q, p, 3)
+    assert (ctx.L, ctx.K, ctx.dnum) == (45, 15, 3)
+    s = orc.secret(31)
+    rng = np.random.default_rng(32)
+    key = orc.relin_key(s, 33)
+    dkey = ctx.load_key(key)
+    gal = [O.galois_elt(r, ctx.n) for r in (1, -2, 4, 8, -16, 32, 64, -128, 256)]
+    gkeys = [orc.galois_key(s, g, 40 + i) for i, g in enumerate(gal)]
+    dgk = [ctx.load_key(k) for k in gkeys]
+    for nq, counts in ((45, (3,)), (20, (3, 9))):
+        a = residues(rng, ctx.q[:nq], (1,), ctx.n)
+        assert np.array_equal(ctx.keyswitch(ctx.upload(a), dkey).numpy(),
+                              orc.keyswitch(a[0], key)), nq
+        ct = residues(rng, ctx.q[:nq], (2,), ctx.n)
+        want = [orc.rotate(ct, k, g) for k, g in zip(gkeys[:max(counts)], gal)]
+        dct = ctx.upload(ct)
+        pre = ctx.rotation_precompute(dct)
+        for m in counts:
+            outs = ctx.rotate_hoisted(dct, pre, dgk[:m], gal[:m])
+            for i, out in enumerate(outs):
+                assert np.array_equal(out.numpy(), want[i]), (nq, m, i)
+    ctx.close()
