@@ -186,7 +186,7 @@ def test_full_batch_small_ring():
 def test_classical128_chain_key_switch():
     """The reference's audited classical-128 chain (N=2^17, 45 Q + 12 P
     primes, four digits: the golden OpenFHE chain) at the full level and at
-    31 limbs: relinearisation key switch and two hoisted rotations, word for
+    31 limbs: relinearisation key switch and hoisted rotations, word for
     word against the oracle (the fused middle kernel holds the 12 source
     lines of a column in up to 160 KB of LDS per workgroup)."""
     import json
@@ -201,18 +201,23 @@ def test_classical128_chain_key_switch():
     rng = np.random.default_rng(18)
     key = orc.relin_key(s, 19)
     dkey = ctx.load_key(key)
-    gal = [O.galois_elt(r, ctx.n) for r in (1, -8)]
+    gal = [O.galois_elt(r, ctx.n) for r in (1, -8, 2, 4, -16, 32, 64, -128, 256)]
     gkeys = [orc.galois_key(s, g, 60 + i) for i, g in enumerate(gal)]
     dgk = [ctx.load_key(k) for k in gkeys]
-    for nq in (45, 31):
+    # 2 rotations: one 16-wave middle-kernel launch; at 31 limbs also 3
+    # (8-wave) and 9 (4-wave), the 12 sources in two groups each time
+    for nq, counts in ((45, (2,)), (31, (2, 3, 9))):
         a = residues(rng, ctx.q[:nq], (1,), ctx.n)
         assert np.array_equal(ctx.keyswitch(ctx.upload(a), dkey).numpy(),
                               orc.keyswitch(a[0], key)), nq
         ct = residues(rng, ctx.q[:nq], (2,), ctx.n)
+        want = [orc.rotate(ct, k, g) for k, g in zip(gkeys[:max(counts)], gal)]
         dct = ctx.upload(ct)
-        outs = ctx.rotate_hoisted(dct, ctx.rotation_precompute(dct), dgk, gal)
-        for out, k, g in zip(outs, gkeys, gal):
-            assert np.array_equal(out.numpy(), orc.rotate(ct, k, g)), (nq, g)
+        pre = ctx.rotation_precompute(dct)
+        for m in counts:
+            outs = ctx.rotate_hoisted(dct, pre, dgk[:m], gal[:m])
+            for i, out in enumerate(outs):
+                assert np.array_equal(out.numpy(), want[i]), (nq, m, i)
     ctx.close()
 
 
